@@ -1,0 +1,248 @@
+/*
+ * tl_hip.h -- C ABI of tl_hip, the MI355X (gfx950) backend for TL's quantized
+ * LLM-inference hot path.
+ *
+ * Conventions (the reference's FFI conventions, crates/tl_runtime/src/device_ffi.rs):
+ *   - Tensor-returning calls return a NEW handle (reference count 1) owned by the caller;
+ *     input handles are borrowed (ffi_helpers.rs:43-66).  Release with tl_hip_tensor_release.
+ *   - On failure a call returns NULL (or a non-zero status) and records a thread-local
+ *     message readable with tl_hip_last_error() -- the LAST_ERROR + sentinel convention of
+ *     device_ffi.rs:22-80, 106-113.  Nothing aborts or panics.
+ *   - Status codes mirror tl_backend::BackendError (crates/tl_backend/src/error.rs:7-17).
+ *   - All device work is ordered on one HIP stream per process (tl_hip_stream); calls that
+ *     return data to the host synchronise that stream.
+ * Every entry point names the reference interface it replaces.
+ */
+#ifndef TL_HIP_H
+#define TL_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define TL_HIP_MAX_RANK 8
+
+/* status codes: 0 = ok, else BackendError variant (error.rs:7-17) */
+#define TL_HIP_OK 0
+#define TL_HIP_ERR_SHAPE 1     /* ShapeMismatch */
+#define TL_HIP_ERR_DEVICE 2    /* DeviceError */
+#define TL_HIP_ERR_ALLOC 3     /* AllocationError */
+#define TL_HIP_ERR_NULL 4      /* NullPointerError */
+#define TL_HIP_ERR_INTERNAL 5  /* InternalError */
+#define TL_HIP_ERR_INDEX 6     /* IndexOutOfBounds */
+#define TL_HIP_ERR_TYPE 7      /* TypeMismatch */
+#define TL_HIP_ERR_ARG 8       /* ArgumentError */
+
+/* element types of device tensors (tl_backend DType subset, dtype.rs:5-30) */
+#define TL_HIP_F32 0
+#define TL_HIP_F16 1
+
+/* GGML type ids accepted for quantized weights (quantized.rs:10-22; gguf.rs:157-168) */
+#define TL_HIP_GGML_F32 0
+#define TL_HIP_GGML_F16 1
+#define TL_HIP_GGML_Q4_0 2
+#define TL_HIP_GGML_Q8_0 8
+
+typedef struct tl_hip_tensor tl_hip_tensor;   /* GpuTensor (tl_backend tensor.rs:7-55) */
+typedef struct tl_hip_qtensor tl_hip_qtensor; /* QTensor + gpu_raw_cache (quantized.rs:29-40) */
+typedef struct tl_hip_llama tl_hip_llama;     /* decoder state of chatbot.tl (see below) */
+
+/* ---------------------------------------------------------------- runtime -------- */
+/* Last error of the calling thread (device_ffi.rs:22-80 LAST_ERROR); "" when none. */
+const char* tl_hip_last_error(void);
+int tl_hip_last_status(void);
+void tl_hip_clear_error(void);
+/* Selects the device and creates the library stream.  Optional: every other call
+ * initialises device 0 on first use (the reference's global device, tl_cuda device.rs:19-86). */
+int tl_hip_init(int device);
+int tl_hip_device_count(void);
+/* Library stream as a hipStream_t (GpuStream, tl_backend stream.rs:12-31). */
+void* tl_hip_stream(void);
+/* Redirects library work to a caller stream (NULL restores the library stream). */
+int tl_hip_set_stream(void* hip_stream);
+int tl_hip_synchronize(void);
+/* Device-memory plumbing for C callers and tests. */
+void* tl_hip_malloc(size_t bytes);
+int tl_hip_free(void* p);
+int tl_hip_memcpy_h2d(void* dst, const void* src, size_t bytes);
+int tl_hip_memcpy_d2h(void* dst, const void* src, size_t bytes);
+int tl_hip_memcpy_d2d(void* dst, const void* src, size_t bytes);
+/* hipEvent timing on the library stream. */
+void* tl_hip_event_create(void);
+int tl_hip_event_record(void* ev);
+int tl_hip_event_elapsed_ms(void* start, void* stop, float* ms);
+int tl_hip_event_destroy(void* ev);
+
+/* ---------------------------------------------------------------- tensors -------- */
+/* IDevice::tensor_new (crates/tl_backend/src/device.rs:21-26): f32 host data -> device. */
+tl_hip_tensor* tl_hip_tensor_new(const float* host, const int64_t* shape, int rank);
+/* tensor_new for f16 payloads given as raw IEEE binary16 bits (KV-cache / f16 inputs). */
+tl_hip_tensor* tl_hip_tensor_new_f16(const uint16_t* host, const int64_t* shape, int rank);
+/* IDevice::tensor_zeros (device.rs:34-39). */
+tl_hip_tensor* tl_hip_tensor_zeros(const int64_t* shape, int rank, int dtype);
+/* IDevice::tensor_release / tensor_acquire (device.rs:213-214; ffi_helpers.rs:49-66). */
+int tl_hip_tensor_release(tl_hip_tensor* t);
+tl_hip_tensor* tl_hip_tensor_acquire(tl_hip_tensor* t);
+/* IDevice::tensor_to_vec_f32 (device.rs:83): copies numel f32 values (f16 is widened). */
+int tl_hip_tensor_to_host(const tl_hip_tensor* t, float* out, int64_t numel);
+int tl_hip_tensor_rank(const tl_hip_tensor* t);
+int tl_hip_tensor_shape(const tl_hip_tensor* t, int64_t* shape_out);
+int64_t tl_hip_tensor_numel(const tl_hip_tensor* t);
+int tl_hip_tensor_dtype(const tl_hip_tensor* t);
+/* IDevice::tensor_data (device.rs:224): the device pointer. */
+void* tl_hip_tensor_data(const tl_hip_tensor* t);
+/* IDevice::tensor_reshape_new (device.rs:367-371): a new handle with the new shape
+ * (data copied on device). */
+tl_hip_tensor* tl_hip_tensor_reshape(const tl_hip_tensor* t, const int64_t* shape, int rank);
+
+/* ------------------------------------------------------- quantized weights -------- */
+/* Upload of one GGUF tensor: gguf.rs:129-189 hands over the raw block bytes with the
+ * row-major shape [n, k]; QTensor::dequantize_to_tensor's size checks apply
+ * (quantized.rs:182-260).  Q4_0 and Q8_0 are repacked once into the device residency
+ * format (the gpu_raw_cache of system.rs:316-331); F16/F32 are rejected (TypeMismatch). */
+tl_hip_qtensor* tl_hip_qtensor_new(int ggml_type, const uint8_t* data, size_t nbytes,
+                                   const int64_t* shape, int rank);
+int tl_hip_qtensor_release(tl_hip_qtensor* q);
+/* QTensor::dequantize_to_tensor (quantized.rs:117-165): f32 [n, k] on the device. */
+tl_hip_tensor* tl_hip_qtensor_dequantize(const tl_hip_qtensor* q);
+/* tl_qtensor_matmul (crates/tl_runtime/src/system.rs:180-382): y = x . W^T with x
+ * [..., k] f32 and W [n, k] quantized; y is [..., n].  Fused dequant + product; m <= 4
+ * rows take the matvec kernel, larger m the tiled GEMM. */
+tl_hip_tensor* tl_hip_qtensor_matmul(const tl_hip_tensor* x, const tl_hip_qtensor* q);
+/* Same with the f16-MFMA prefill GEMM for m > 4 (dequant -> f16 LDS tiles -> MFMA,
+ * f32 accumulate); tolerance class "f16 path". */
+tl_hip_tensor* tl_hip_qtensor_matmul_f16(const tl_hip_tensor* x, const tl_hip_qtensor* q);
+
+/* ---------------------------------------------------------------- raw launchers --- */
+/* Kernel ABI in the style of launch_mul_mv_q4_k_kernel (crates/tl_cuda/src/cuda_kernels/
+ * autograd.cu:2904-2924): device pointers + dims + stream, returns a status.  `w` is a
+ * quantized weight handle (its residency buffers); x is [m, k] f32, y is [m, n] f32.
+ * stream NULL = library stream. */
+int tl_hip_launch_quant_matvec(const tl_hip_qtensor* w, const float* x, float* y, int64_t m,
+                               void* stream);
+int tl_hip_launch_quant_gemm(const tl_hip_qtensor* w, const float* x, float* y, int64_t m,
+                             int use_f16_mfma, void* stream);
+
+/* ------------------------------------------------------------ tensor operators --- */
+/* IDevice::tensor_matmul (device.rs:258; tl_cpu tensor.rs:1248-1313): [.., m, k] x
+ * [.., k, n] (b batched only when its rank > 2) or 1-D operands. */
+tl_hip_tensor* tl_hip_tensor_matmul(const tl_hip_tensor* a, const tl_hip_tensor* b);
+/* IDevice::tensor_transpose_2d (device.rs:513; tensor.rs:902-941) */
+tl_hip_tensor* tl_hip_tensor_transpose_2d(const tl_hip_tensor* a);
+/* IDevice::tensor_transpose (device.rs:378-383; tensor.rs:902-941) */
+tl_hip_tensor* tl_hip_tensor_transpose(const tl_hip_tensor* a, int64_t dim0, int64_t dim1);
+/* IDevice::tensor_rms_norm (device.rs:428-433; tl_cpu ffi.rs:2444-2486):
+ * (x / sqrt(mean(x^2) + eps)) * w over the last dim; w may be NULL. */
+tl_hip_tensor* tl_hip_tensor_rms_norm(const tl_hip_tensor* x, const tl_hip_tensor* w, float eps);
+/* IDevice::tensor_rope_new_cos / _sin (device.rs:434-445; ffi.rs:2589-2629): table
+ * [seq_len, dim] with each pair's value duplicated. */
+tl_hip_tensor* tl_hip_tensor_rope_new_cos(int64_t dim, int64_t seq_len, float base);
+tl_hip_tensor* tl_hip_tensor_rope_new_sin(int64_t dim, int64_t seq_len, float base);
+/* IDevice::tensor_apply_rope (device.rs:446-451; ffi.rs:2631-2686): interleaved pairs,
+ * every vector rotated by the first row of the given tables. */
+tl_hip_tensor* tl_hip_tensor_apply_rope(const tl_hip_tensor* x, const tl_hip_tensor* cos_t,
+                                        const tl_hip_tensor* sin_t);
+/* Position-aware variant (no reference counterpart on tl_cpu; the tl_cuda kernel's
+ * per-token rows, autograd.cu:1196-1227, with tl_cpu's interleaved pairs): vector v of
+ * token t = v / vectors_per_token uses table row pos0 + t. */
+tl_hip_tensor* tl_hip_tensor_apply_rope_pos(const tl_hip_tensor* x, const tl_hip_tensor* cos_t,
+                                            const tl_hip_tensor* sin_t, int64_t pos0,
+                                            int64_t vectors_per_token);
+/* IDevice::tensor_silu (device.rs:310; ffi.rs:2097-2113) */
+tl_hip_tensor* tl_hip_tensor_silu(const tl_hip_tensor* x);
+/* IDevice::tensor_add / tensor_mul / tensor_sub / tensor_div (device.rs:253-256;
+ * tensor.rs:549-621), numpy broadcasting. */
+tl_hip_tensor* tl_hip_tensor_add(const tl_hip_tensor* a, const tl_hip_tensor* b);
+tl_hip_tensor* tl_hip_tensor_mul(const tl_hip_tensor* a, const tl_hip_tensor* b);
+tl_hip_tensor* tl_hip_tensor_sub(const tl_hip_tensor* a, const tl_hip_tensor* b);
+tl_hip_tensor* tl_hip_tensor_div(const tl_hip_tensor* a, const tl_hip_tensor* b);
+/* IDevice::tensor_scale (device.rs:285; ffi.rs:2083-2094) */
+tl_hip_tensor* tl_hip_tensor_scale(const tl_hip_tensor* x, float s);
+/* IDevice::tensor_softmax (device.rs:317; tensor.rs:1065-1092), negative dim allowed */
+tl_hip_tensor* tl_hip_tensor_softmax(const tl_hip_tensor* x, int64_t dim);
+/* IDevice::tensor_new_causal_mask (device.rs:53; ffi.rs:3184-3196) */
+tl_hip_tensor* tl_hip_tensor_new_causal_mask(int64_t size);
+/* IDevice::tensor_narrow (device.rs:391-397; tensor.rs:989-1015) */
+tl_hip_tensor* tl_hip_tensor_narrow(const tl_hip_tensor* x, int64_t dim, int64_t start,
+                                    int64_t len);
+/* IDevice::tensor_cat (device.rs:398; tensor.rs:1021-1063), two operands */
+tl_hip_tensor* tl_hip_tensor_cat(const tl_hip_tensor* a, const tl_hip_tensor* b, int64_t dim);
+/* IDevice::tensor_repeat_interleave (device.rs:409-414; tensor.rs:1178-1200) */
+tl_hip_tensor* tl_hip_tensor_repeat_interleave(const tl_hip_tensor* x, int64_t repeats,
+                                               int64_t dim);
+/* IDevice::tensor_embedding (device.rs:418-425; tensor.rs:1094-1112): ids hold f32 token
+ * ids; an id outside [0, vocab) is IndexOutOfBounds. */
+tl_hip_tensor* tl_hip_tensor_embedding(const tl_hip_tensor* weight, const tl_hip_tensor* ids);
+/* IDevice::tensor_sample (device.rs:349; tensor.rs:1626-1680), greedy branch only:
+ * temp <= 0 returns [1] holding the argmax (last index among equal maxima); temp > 0 is
+ * ArgumentError (stochastic top-p sampling is not provided). */
+tl_hip_tensor* tl_hip_tensor_sample(const tl_hip_tensor* logits, float temp, float top_p);
+/* argmax over all elements (tensor.rs:841-846), last index among equal maxima. */
+int64_t tl_hip_tensor_argmax_all(const tl_hip_tensor* x);
+/* IDevice::tensor_repetition_penalty (device.rs:194-199; tl_cpu device_impl.rs:967-1001) */
+tl_hip_tensor* tl_hip_tensor_repetition_penalty(const tl_hip_tensor* logits,
+                                                const tl_hip_tensor* tokens, double penalty);
+
+/* GpuFusedOps (crates/tl_backend/src/fused_ops.rs:15-57; tl_cpu fused_ops.rs:15-85) */
+tl_hip_tensor* tl_hip_fused_silu_mul(const tl_hip_tensor* gate, const tl_hip_tensor* up);
+tl_hip_tensor* tl_hip_fused_rms_norm(const tl_hip_tensor* x, const tl_hip_tensor* w, float eps);
+tl_hip_tensor* tl_hip_fused_add_rms_norm(const tl_hip_tensor* x, const tl_hip_tensor* residual,
+                                         const tl_hip_tensor* w, float eps);
+
+/* Single-query decode attention over an f16 KV cache: the chatbot's
+ * transpose/cat_4d/repeat_interleave/matmul_4d/scale/softmax/matmul_4d chain
+ * (examples/apps/tinyllama/chatbot.tl:63-87) for sl = 1, in one fused split-L kernel pair.
+ *   q [B, Hq, D] f32;  k, v [B, Hkv, Lmax, D] f16 with the first L rows valid;
+ *   out [B, Hq, D] f32;  query head h reads KV head h / (Hq / Hkv). */
+tl_hip_tensor* tl_hip_attention_decode(const tl_hip_tensor* q, const tl_hip_tensor* k,
+                                       const tl_hip_tensor* v, int64_t L, float scale);
+
+/* ------------------------------------------------------ Llama decoder driver ----- */
+/* The model composition of examples/apps/tinyllama/chatbot.tl:1-226 (Linear / RMSNorm /
+ * MLP / Attention / Block and the decode loop), run on the device with a persistent f16 KV
+ * cache in place of cat_4d + KVCache.update (system.rs:387-600).  Weight slots: which =
+ * 0 attn_q, 1 attn_k, 2 attn_v, 3 attn_output, 4 ffn_gate, 5 ffn_up, 6 ffn_down; layer -1
+ * is the LM head ("output.weight"); norms: which 0 attn_norm, 1 ffn_norm, layer -1
+ * output_norm. */
+tl_hip_llama* tl_hip_llama_new(int n_layers, int d_model, int n_heads, int n_kv_heads,
+                               int ffn_dim, int vocab, float eps, float rope_theta,
+                               int max_seq);
+int tl_hip_llama_free(tl_hip_llama* m);
+int tl_hip_llama_set_linear(tl_hip_llama* m, int layer, int which, int ggml_type,
+                            const uint8_t* data, size_t nbytes);
+int tl_hip_llama_set_norm(tl_hip_llama* m, int layer, int which, const float* w);
+int tl_hip_llama_set_embedding(tl_hip_llama* m, const float* table);
+/* KV-cache element type (kv_f16: 0 = f32, the tl_cpu cache; 1 = f16) and RoPE position rule
+ * (rope_per_token: 0 = tl_cpu's, every token of a call rotated by the table row of the call's
+ * start position, chatbot.tl:56-61 + ffi.rs:2655-2681; 1 = token t at start + t).  Resets the
+ * cache. */
+int tl_hip_llama_configure(tl_hip_llama* m, int kv_f16, int rope_per_token);
+/* KVCache::new / free (system.rs:387-454): empties the cache. */
+int tl_hip_llama_reset(tl_hip_llama* m);
+/* Number of cached positions (the chatbot's start_pos for the next call). */
+int64_t tl_hip_llama_position(const tl_hip_llama* m);
+/* One pass of the decode-loop body (chatbot.tl:174-187) over n new token ids at the
+ * current cache position; writes the last row's logits [vocab] to logits_out (host,
+ * may be NULL). prefill_f16 selects the f16-MFMA GEMM for the n > 4 linears. */
+int tl_hip_llama_forward(tl_hip_llama* m, const int32_t* ids, int n, float* logits_out,
+                         int prefill_f16);
+/* Greedy choice from the logits of the last forward call, on the device:
+ * repetition_penalty(history, p) (device_impl.rs:967-1001) then sample(temp <= 0) = argmax
+ * (tensor.rs:1633-1637); returns the token id or -1 on error. */
+int32_t tl_hip_llama_sample_greedy(tl_hip_llama* m, double repetition_penalty,
+                                   const int32_t* history, int n_history);
+/* Greedy decode of n_steps tokens after the cached context (chatbot.tl:188-222 with
+ * sample(temp <= 0) = argmax): first token id `first`, generated ids to out_ids (host).
+ * repetition_penalty 1.0 disables the penalty; history holds the prior ids (host). With
+ * use_graph != 0 each step is a captured hipGraph replay. */
+int tl_hip_llama_generate(tl_hip_llama* m, int32_t first, int n_steps, int32_t* out_ids,
+                          double repetition_penalty, const int32_t* history, int n_history,
+                          int use_graph);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* TL_HIP_H */

@@ -1,0 +1,247 @@
+"""GPU parity: every HIP kernel on the path against the CPU oracle on the same seeded inputs,
+called through the C ABI (tl_amd binds libtl_hip.so with ctypes).
+
+max-rel-err = max_i |a_i - b_i| / max(max_j |b_j|, 1e-30); bounds from the north star:
+bit-exact for dequant, 1e-4 for f32 paths, 1e-2 for f16 paths."""
+import json
+import os
+
+import numpy as np
+import pytest
+
+import oracle
+from tl_amd import GGML_Q4_0, GGML_Q8_0, BackendError, QTensor
+from tl_amd.quant import random_q4_0_blocks, random_q8_0_blocks
+
+pytestmark = pytest.mark.gpu
+HERE = os.path.dirname(os.path.abspath(__file__))
+F32_TOL, F16_TOL = 1e-4, 1e-2
+
+
+def max_rel(a, b):
+    a = np.asarray(a, np.float64)
+    b = np.asarray(b, np.float64)
+    assert a.shape == b.shape, (a.shape, b.shape)
+    return float(np.max(np.abs(a - b)) / max(np.max(np.abs(b)), 1e-30)) if b.size else 0.0
+
+
+def blocks(t, rng, n, k):
+    return random_q4_0_blocks(rng, n, k) if t == GGML_Q4_0 else random_q8_0_blocks(rng, n, k)
+
+
+# ------------------------------------------------------------------ dequant (bit-exact)
+def test_dequant_golden_blocks(dev):
+    with open(os.path.join(HERE, "golden", "q_blocks.json")) as f:
+        cases = json.load(f)["cases"]
+    for c in cases:
+        t = GGML_Q4_0 if c["type"] == "Q4_0" else GGML_Q8_0
+        got = dev.qtensor_dequantize(QTensor(t, bytes.fromhex(c["hex"]), (1, 32))).to_numpy().reshape(-1)
+        assert list(got.view(np.uint32)) == c["f32_bits"], c["name"]
+
+
+@pytest.mark.parametrize("t", [GGML_Q4_0, GGML_Q8_0])
+@pytest.mark.parametrize("nk", [(4096, 4096), (11008, 4096), (64, 11008)])
+def test_dequant_bit_exact(dev, t, nk):
+    n, k = nk
+    rng = np.random.default_rng(0x71510000 + n + k + t)
+    raw = blocks(t, rng, n, k)
+    got = dev.qtensor_dequantize(QTensor(t, raw, (n, k))).to_numpy()
+    ref = oracle.dequantize(t, raw, n * k).reshape(n, k)
+    assert np.array_equal(got.view(np.uint32), ref.view(np.uint32))
+
+
+# ------------------------------------------------------------------ quantized linear
+@pytest.mark.parametrize("t", [GGML_Q4_0, GGML_Q8_0])
+@pytest.mark.parametrize("nk", [(4096, 4096), (11008, 4096), (4096, 11008), (2560, 2048), (256, 2048),
+                                (5632, 2048), (2048, 5632), (32, 32), (100, 96)])
+@pytest.mark.parametrize("m", [1, 2, 4])
+def test_quant_matvec(dev, t, nk, m):
+    n, k = nk
+    rng = np.random.default_rng(0x71510000 + 7 * n + k + m + t)
+    raw = blocks(t, rng, n, k)
+    x = rng.standard_normal((m, k)).astype(np.float32)
+    y = dev.tl_qtensor_matmul(dev.tensor_new(x), QTensor(t, raw, (n, k))).to_numpy()
+    ref = oracle.qtensor_matmul(x, raw, t, n)
+    assert max_rel(y, ref) <= F32_TOL
+
+
+@pytest.mark.parametrize("t", [GGML_Q4_0, GGML_Q8_0])
+@pytest.mark.parametrize("m", [5, 16, 128, 512])
+@pytest.mark.parametrize("nk", [(4096, 4096), (11008, 4096), (4096, 11008)])
+def test_quant_gemm_f32_and_f16(dev, t, m, nk):
+    n, k = nk
+    if m == 512 and n * k > 4096 * 4096:
+        n = 1024  # keep the CPU oracle to seconds: the row band of the same kernel
+    rng = np.random.default_rng(0x71520000 + m + n + t)
+    raw = blocks(t, rng, n, k)
+    x = rng.standard_normal((m, k)).astype(np.float32)
+    q = QTensor(t, raw, (n, k))
+    xt = dev.tensor_new(x)
+    ref = oracle.qtensor_matmul(x, raw, t, n)
+    y32 = dev.tl_qtensor_matmul(xt, q).to_numpy()
+    assert max_rel(y32, ref) <= F32_TOL
+    y16 = dev.tl_qtensor_matmul_f16(xt, q).to_numpy()
+    assert max_rel(y16, ref) <= F16_TOL
+
+
+def test_qtensor_matmul_shapes_and_errors(dev):
+    rng = np.random.default_rng(5)
+    raw = random_q4_0_blocks(rng, 64, 128)
+    q = QTensor(GGML_Q4_0, raw, (64, 128))
+    x3 = rng.standard_normal((2, 3, 128)).astype(np.float32)  # leading dims are kept
+    y = dev.tl_qtensor_matmul(dev.tensor_new(x3), q)
+    assert y.shape == (2, 3, 64)
+    np.testing.assert_allclose(y.to_numpy().reshape(6, 64), oracle.qtensor_matmul(x3.reshape(6, 128), raw, 2, 64),
+                               rtol=1e-4, atol=1e-5)
+    with pytest.raises(BackendError) as e:
+        dev.tl_qtensor_matmul(dev.tensor_new(np.zeros((2, 96), np.float32)), q)
+    assert e.value.variant == "ShapeMismatch"
+
+
+# ------------------------------------------------------------------ fused row ops (config 1)
+def test_rms_norm(dev):
+    rng = np.random.default_rng(0x71510001)
+    x = rng.standard_normal((512, 4096)).astype(np.float32)
+    w = rng.uniform(0.5, 1.5, 4096).astype(np.float32)
+    got = dev.tensor_rms_norm(dev.tensor_new(x), dev.tensor_new(w), 1e-5).to_numpy()
+    assert max_rel(got, oracle.rms_norm(x, w, 1e-5)) <= F32_TOL
+    x2 = rng.standard_normal((3, 2050)).astype(np.float32)  # odd width: generic kernel
+    assert max_rel(dev.tensor_rms_norm(dev.tensor_new(x2), None, 1e-5).to_numpy(),
+                   oracle.rms_norm(x2, None, 1e-5)) <= F32_TOL
+    r = rng.standard_normal((512, 4096)).astype(np.float32)
+    xt, rt, wt = dev.tensor_new(x), dev.tensor_new(r), dev.tensor_new(w)
+    assert max_rel(dev.fused_rms_norm(xt, wt, 1e-5).to_numpy(), oracle.fused_rms_norm(x, w, 1e-5)) <= F32_TOL
+    assert max_rel(dev.fused_add_rms_norm(xt, rt, wt, 1e-5).to_numpy(),
+                   oracle.fused_add_rms_norm(x, r, w, 1e-5)) <= F32_TOL
+
+
+def test_rope(dev):
+    rng = np.random.default_rng(0x71510001)
+    x = rng.standard_normal((512, 32, 128)).astype(np.float32)
+    cos_d, sin_d = dev.tensor_rope_new_cos(128, 512, 10000.0), dev.tensor_rope_new_sin(128, 512, 10000.0)
+    cos_h, sin_h = oracle.rope_table(512, 128, 10000.0), oracle.rope_table(512, 128, 10000.0, sin=True)
+    assert max_rel(cos_d.to_numpy(), cos_h) <= 1e-5 and max_rel(sin_d.to_numpy(), sin_h) <= 1e-5
+    xt = dev.tensor_new(x)
+    # tl_cpu semantics: the (narrowed) table's first row for every vector
+    for start in (0, 7, 300):
+        cs = dev.tensor_narrow(cos_d, 0, start, 5)
+        ss = dev.tensor_narrow(sin_d, 0, start, 5)
+        got = dev.tensor_apply_rope(xt, cs, ss).to_numpy()
+        assert max_rel(got, oracle.apply_rope(x, cos_h[start:start + 5], sin_h[start:start + 5])) <= F32_TOL
+    # position-aware: token t rotated by row t, equal to per-token tl_cpu calls
+    got = dev.tensor_apply_rope_pos(xt, cos_d, sin_d, 0, 32).to_numpy()
+    ref = np.stack([oracle.apply_rope(x[t], cos_h[t:t + 1], sin_h[t:t + 1]) for t in range(512)])
+    assert max_rel(got, ref) <= F32_TOL
+
+
+def test_swiglu(dev):
+    rng = np.random.default_rng(0x71510001)
+    g = rng.standard_normal((512, 11008)).astype(np.float32)
+    u = rng.standard_normal((512, 11008)).astype(np.float32)
+    gt, ut = dev.tensor_new(g), dev.tensor_new(u)
+    unfused = dev.tensor_mul(dev.tensor_silu(gt), ut).to_numpy()
+    ref = oracle.binop("mul", oracle.silu(g), u)
+    assert max_rel(unfused, ref) <= F32_TOL
+    assert max_rel(dev.fused_silu_mul(gt, ut).to_numpy(), oracle.fused_silu_mul(g, u)) <= F32_TOL
+
+
+def test_softmax(dev):
+    rng = np.random.default_rng(0x71510001)
+    x = (rng.standard_normal((512, 32000)) * 3).astype(np.float32)
+    got = dev.tensor_softmax(dev.tensor_new(x), -1).to_numpy()
+    assert max_rel(got, oracle.softmax(x, -1)) <= F32_TOL
+    np.testing.assert_allclose(got.sum(-1), 1.0, rtol=1e-4)
+    y = (rng.standard_normal((4, 33, 6)) * 3).astype(np.float32)  # middle axis, odd size
+    assert max_rel(dev.tensor_softmax(dev.tensor_new(y), 1).to_numpy(), oracle.softmax(y, 1)) <= F32_TOL
+
+
+# ------------------------------------------------------------------ decode attention (config 3)
+@pytest.mark.parametrize("L", [512, 2048, 8192])
+@pytest.mark.parametrize("B", [1, 8])
+def test_attention_decode_f16_kv(dev, L, B):
+    rng = np.random.default_rng(0x71530000 + L + B)
+    hq, hkv, d = 32, 8, 128
+    q = rng.standard_normal((B, hq, d)).astype(np.float16)
+    k = rng.standard_normal((B, hkv, L, d)).astype(np.float16)
+    v = rng.standard_normal((B, hkv, L, d)).astype(np.float16)
+    got = dev.attention_decode(dev.tensor_new(q.astype(np.float32)), dev.tensor_new_f16(k),
+                               dev.tensor_new_f16(v), L, 1.0 / np.sqrt(128.0)).to_numpy()
+    bsel = range(B) if L * B <= 4096 else [0, B - 1]  # oracle time: check first and last batch
+    for b in bsel:
+        ref = oracle.attention(q[b][None].astype(np.float32), k[b].astype(np.float32), v[b].astype(np.float32),
+                               np.float32(1.0 / np.sqrt(128.0)), False).reshape(hq, d)
+        assert max_rel(got[b], ref) <= F32_TOL
+
+
+def test_attention_decode_partial_length_and_f32_cache(dev):
+    rng = np.random.default_rng(17)
+    q = rng.standard_normal((2, 32, 64)).astype(np.float32)
+    k = rng.standard_normal((2, 4, 300, 64)).astype(np.float32)
+    v = rng.standard_normal((2, 4, 300, 64)).astype(np.float32)
+    got = dev.attention_decode(dev.tensor_new(q), dev.tensor_new(k), dev.tensor_new(v), 129, 0.125).to_numpy()
+    for b in range(2):
+        ref = oracle.attention(q[b][None], k[b, :, :129], v[b, :, :129], 0.125, False).reshape(32, 64)
+        assert max_rel(got[b], ref) <= F32_TOL
+    assert max_rel(dev.attention_decode(dev.tensor_new(q), dev.tensor_new(k), dev.tensor_new(v), 1, 0.125)
+                   .to_numpy()[0], np.repeat(k[0, :, 0][None] * 0 + v[0, :, 0][None], 8, 0).reshape(32, 64)
+                   .reshape(32, 64)) <= 1e-6  # L = 1: the output is V
+
+
+# ------------------------------------------------------------------ glue ops
+def test_glue_ops(dev):
+    rng = np.random.default_rng(21)
+    x = rng.standard_normal((1, 5, 4, 16)).astype(np.float32)
+    xt = dev.tensor_new(x)
+    assert np.array_equal(dev.tensor_transpose(xt, 1, 2).to_numpy(), oracle.transpose(x, 1, 2))
+    assert np.array_equal(dev.tensor_repeat_interleave(xt, 8, 2).to_numpy(), oracle.repeat_interleave(x, 8, 2))
+    y = rng.standard_normal((1, 3, 4, 16)).astype(np.float32)
+    assert np.array_equal(dev.tensor_cat(xt, dev.tensor_new(y), 1).to_numpy(), oracle.cat(x, y, 1))
+    assert np.array_equal(dev.tensor_narrow(xt, 1, 2, 3).to_numpy(), oracle.narrow(x, 1, 2, 3))
+    a2 = rng.standard_normal((300, 77)).astype(np.float32)
+    assert np.array_equal(dev.tensor_transpose_2d(dev.tensor_new(a2)).to_numpy(), a2.T)
+    assert np.array_equal(dev.tensor_new_causal_mask(6).to_numpy(), oracle.causal_mask(6))
+    assert np.array_equal(dev.tensor_scale(xt, 0.125).to_numpy(), oracle.scale(x, 0.125))
+    b = rng.standard_normal(16).astype(np.float32)
+    bt = dev.tensor_new(b)
+    for op, fn in (("add", dev.tensor_add), ("mul", dev.tensor_mul), ("sub", dev.tensor_sub), ("div", dev.tensor_div)):
+        assert np.array_equal(fn(xt, bt).to_numpy(), oracle.binop(op, x, b)), op
+    with pytest.raises(BackendError) as e:
+        dev.tensor_add(xt, dev.tensor_new(np.ones(3, np.float32)))
+    assert e.value.variant == "ShapeMismatch"
+
+
+def test_matmul_batched(dev):
+    rng = np.random.default_rng(22)
+    a = rng.standard_normal((1, 32, 7, 64)).astype(np.float32)
+    b = rng.standard_normal((1, 32, 64, 130)).astype(np.float32)
+    got = dev.tensor_matmul(dev.tensor_new(a), dev.tensor_new(b)).to_numpy()
+    assert max_rel(got, oracle.matmul(a, b)) <= F32_TOL
+    b2 = rng.standard_normal((64, 5)).astype(np.float32)
+    assert max_rel(dev.tensor_matmul(dev.tensor_new(a), dev.tensor_new(b2)).to_numpy(), oracle.matmul(a, b2)) <= F32_TOL
+    v = rng.standard_normal(64).astype(np.float32)
+    got = dev.tensor_matmul(dev.tensor_new(a[0, 0]), dev.tensor_new(v))
+    assert got.shape == (7,)
+    assert max_rel(got.to_numpy(), oracle.matmul(a[0, 0], v)) <= F32_TOL
+
+
+def test_embedding_argmax_penalty(dev):
+    rng = np.random.default_rng(23)
+    table = rng.standard_normal((1000, 64)).astype(np.float32)
+    ids = np.array([3, 999, 0, 3], np.float32)
+    tt = dev.tensor_new(table)
+    assert np.array_equal(dev.tensor_embedding(tt, dev.tensor_new(ids)).to_numpy(), oracle.embedding(table, ids))
+    with pytest.raises(BackendError) as e:
+        dev.tensor_embedding(tt, dev.tensor_new(np.array([1000], np.float32)))
+    assert e.value.variant == "IndexOutOfBounds"
+    for arr in ([1, 5, 3, 5, 2], [7, 7, 7], [5, np.nan, 3], [1, 9, np.nan], list(rng.standard_normal(32000))):
+        a = np.array(arr, np.float32)
+        assert dev.tensor_argmax_all(dev.tensor_new(a)) == oracle.argmax_last(a)
+    ties = np.zeros(32000, np.float32)
+    ties[[5, 17000, 31999 - 3]] = 2.0
+    assert dev.tensor_argmax_all(dev.tensor_new(ties)) == 31996
+    s = dev.tensor_sample(dev.tensor_new(ties), 0.0, 0.9).to_numpy()
+    assert s.shape == (1,) and s[0] == 31996.0
+    lg = rng.standard_normal((2, 500)).astype(np.float32)
+    tok = np.array([3, 3, 499, 17, -1], np.float32)
+    got = dev.tensor_repetition_penalty(dev.tensor_new(lg), dev.tensor_new(tok), 1.1).to_numpy()
+    assert np.array_equal(got, oracle.repetition_penalty(lg, tok, 1.1))

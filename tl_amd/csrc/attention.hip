@@ -1,0 +1,340 @@
+// Single-query decode attention with grouped KV heads over a KV cache (f16 or f32),
+// split along the cached length (flash-decoding) so one token at batch 1 still fills the
+// GPU.  Replaces the chatbot's transpose / cat_4d / repeat_interleave / matmul_4d / scale /
+// softmax / matmul_4d chain (examples/apps/tinyllama/chatbot.tl:63-87) for sl = 1: K and V
+// are read once, in place, and the Hq/Hkv query heads of a group share every K/V row that
+// is loaded (no repeat_interleave copy).
+//
+// Pass 1 (k_attn_partial): workgroup = (split, kv head, batch), 4 wavefronts.  Eight lanes
+// share one cache row (each owns D/8 consecutive dims), so a wavefront covers 8 positions
+// per load instruction.  Scores of the chunk go to LDS, then each head's chunk max / exp-sum
+// is formed and the exp-weighted V rows are accumulated.  Pass 2 (k_attn_combine) merges
+// the per-split (max, sum, o) triples.  All arithmetic is f32.
+#include "internal.h"
+
+namespace tlhip {
+
+template <typename KVT>
+struct KVLoad;
+
+template <>
+struct KVLoad<__half> {
+    // DL consecutive f16 -> f32
+    template <int DL>
+    __device__ static void load(const __half* p, float* out) {
+        static_assert(DL % 8 == 0, "f16 rows are read 16 bytes at a time");
+#pragma unroll
+        for (int i = 0; i < DL / 8; i++) {
+            uint4 w = reinterpret_cast<const uint4*>(p)[i];
+            const uint32_t u[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                __half2 h2 = *reinterpret_cast<const __half2*>(&u[j]);
+                float2 f = __half22float2(h2);
+                out[8 * i + 2 * j] = f.x;
+                out[8 * i + 2 * j + 1] = f.y;
+            }
+        }
+    }
+};
+
+template <>
+struct KVLoad<float> {
+    template <int DL>
+    __device__ static void load(const float* p, float* out) {
+#pragma unroll
+        for (int i = 0; i < DL / 4; i++) {
+            float4 v = reinterpret_cast<const float4*>(p)[i];
+            out[4 * i] = v.x;
+            out[4 * i + 1] = v.y;
+            out[4 * i + 2] = v.z;
+            out[4 * i + 3] = v.w;
+        }
+    }
+};
+
+constexpr int ATT_MAX_CHUNK = 1024;
+
+// Cached length of batch item b: (len_dev ? *len_dev + len_add : L) + b * len_step.
+// Decode uses len_step 0; a causal prefill of n queries over one shared cache
+// (kv_bstride 0) uses len_step 1, so query i sees positions 0 .. base + i.
+struct AttnLen {
+    int64_t L;
+    const int32_t* len_dev;
+    int len_add, len_step;
+    __device__ int64_t of(int b) const {
+        return (len_dev ? (int64_t)(*len_dev) + len_add : L) + (int64_t)b * len_step;
+    }
+};
+
+template <int D, int G, typename KVT>
+__global__ __launch_bounds__(256) void k_attn_partial(const float* __restrict__ q,
+                                                      const KVT* __restrict__ kc,
+                                                      const KVT* __restrict__ vc,
+                                                      float* __restrict__ ws, int hkv,
+                                                      int64_t lmax, int64_t kv_bstride,
+                                                      AttnLen len, int chunk, int nsplit,
+                                                      float scale) {
+    constexpr int DL = D / 8;  // dims per lane
+    __shared__ float sc[G][ATT_MAX_CHUNK];
+    __shared__ float stat[G][2];
+    __shared__ float part[4][G][D];
+    const int split = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int grp = lane >> 3, sub = lane & 7;
+    int64_t L = len.of(b);
+    if (L > lmax) L = lmax;
+    const int64_t p0 = (int64_t)split * chunk;
+    const int64_t p1 = p0 + chunk < L ? p0 + chunk : (L > p0 ? L : p0);
+    const int hq = hkv * G;
+    const KVT* kb = kc + (int64_t)b * kv_bstride + (int64_t)h * lmax * D;
+    const KVT* vb = vc + (int64_t)b * kv_bstride + (int64_t)h * lmax * D;
+
+    // q slices of the group's heads for this lane's dims
+    float qv[G][DL];
+#pragma unroll
+    for (int g = 0; g < G; g++) {
+        const float* qp = q + ((int64_t)b * hq + h * G + g) * D + sub * DL;
+#pragma unroll
+        for (int i = 0; i < DL; i += 4) {
+            float4 t = *reinterpret_cast<const float4*>(qp + i);
+            qv[g][i] = t.x;
+            qv[g][i + 1] = t.y;
+            qv[g][i + 2] = t.z;
+            qv[g][i + 3] = t.w;
+        }
+    }
+    // ---- scores
+    for (int64_t base = p0; base < p1; base += 32) {
+        int64_t p = base + wave * 8 + grp;
+        int64_t pc = p < p1 ? p : p1 - 1;  // clamp: loads stay in bounds
+        float kv[DL];
+        KVLoad<KVT>::template load<DL>(kb + pc * D + sub * DL, kv);
+#pragma unroll
+        for (int g = 0; g < G; g++) {
+            float s = 0.f;
+#pragma unroll
+            for (int i = 0; i < DL; i++) s = fmaf(qv[g][i], kv[i], s);
+            s += __shfl_xor(s, 1, 64);
+            s += __shfl_xor(s, 2, 64);
+            s += __shfl_xor(s, 4, 64);
+            if (sub == 0 && p < p1) sc[g][p - p0] = s * scale;
+        }
+    }
+    __syncthreads();
+    // ---- per-head chunk max and exp-sum (wave w handles heads w, w+4, ...)
+    const int cn = (int)(p1 - p0);
+    for (int g = wave; g < G; g += 4) {
+        float mx = -INFINITY;
+        for (int i = lane; i < cn; i += 64) mx = fmaxf(mx, sc[g][i]);
+#pragma unroll
+        for (int off = 32; off >= 1; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off, 64));
+        float sum = 0.f;
+        for (int i = lane; i < cn; i += 64) {
+            float e = cn > 0 ? expf(sc[g][i] - mx) : 0.f;
+            sc[g][i] = e;
+            sum += e;
+        }
+#pragma unroll
+        for (int off = 32; off >= 1; off >>= 1) sum += __shfl_xor(sum, off, 64);
+        if (lane == 0) {
+            stat[g][0] = mx;
+            stat[g][1] = sum;
+        }
+    }
+    __syncthreads();
+    // ---- exp-weighted V
+    float o[G][DL];
+#pragma unroll
+    for (int g = 0; g < G; g++)
+#pragma unroll
+        for (int i = 0; i < DL; i++) o[g][i] = 0.f;
+    for (int64_t base = p0; base < p1; base += 32) {
+        int64_t p = base + wave * 8 + grp;
+        if (p < p1) {
+            float vv[DL];
+            KVLoad<KVT>::template load<DL>(vb + p * D + sub * DL, vv);
+#pragma unroll
+            for (int g = 0; g < G; g++) {
+                float e = sc[g][p - p0];
+#pragma unroll
+                for (int i = 0; i < DL; i++) o[g][i] = fmaf(e, vv[i], o[g][i]);
+            }
+        }
+    }
+    // reduce over the 8 position groups of the wavefront (lane bits 3..5)
+#pragma unroll
+    for (int g = 0; g < G; g++)
+#pragma unroll
+        for (int i = 0; i < DL; i++) {
+            float v = o[g][i];
+            v += __shfl_xor(v, 8, 64);
+            v += __shfl_xor(v, 16, 64);
+            v += __shfl_xor(v, 32, 64);
+            o[g][i] = v;
+        }
+    if (grp == 0) {
+#pragma unroll
+        for (int g = 0; g < G; g++)
+#pragma unroll
+            for (int i = 0; i < DL; i++) part[wave][g][sub * DL + i] = o[g][i];
+    }
+    __syncthreads();
+    // workspace record per (b, h, split, g): o[D], max, sum
+    float* wr = ws + ((((int64_t)b * hkv + h) * nsplit + split) * G) * (D + 2);
+    for (int idx = threadIdx.x; idx < G * D; idx += 256) {
+        int g = idx / D, d = idx % D;
+        float s = part[0][g][d] + part[1][g][d] + part[2][g][d] + part[3][g][d];
+        wr[g * (D + 2) + d] = s;
+    }
+    if (threadIdx.x < G) {
+        wr[threadIdx.x * (D + 2) + D] = stat[threadIdx.x][0];
+        wr[threadIdx.x * (D + 2) + D + 1] = stat[threadIdx.x][1];
+    }
+}
+
+// out[b, hq, d] = sum_s o_s[d] e^(m_s - M) / sum_s l_s e^(m_s - M)
+template <int D, int G>
+__global__ void k_attn_combine(const float* __restrict__ ws, float* __restrict__ out, int hkv,
+                               int nsplit) {
+    const int hq_idx = blockIdx.x, b = blockIdx.y;  // query head, batch
+    const int h = hq_idx / G, g = hq_idx % G;
+    const int d = threadIdx.x;
+    const float* base = ws + (((int64_t)b * hkv + h) * nsplit * G + g) * (D + 2);
+    const int64_t stride = (int64_t)G * (D + 2);
+    float M = -INFINITY;
+    for (int s = 0; s < nsplit; s++) M = fmaxf(M, base[s * stride + D]);
+    float num = 0.f, den = 0.f;
+    for (int s = 0; s < nsplit; s++) {
+        const float* r = base + s * stride;
+        float l = r[D + 1];
+        if (l == 0.f) continue;  // split with no positions
+        float f = expf(r[D] - M);
+        num = fmaf(r[d], f, num);
+        den = fmaf(l, f, den);
+    }
+    out[((int64_t)b * hkv * G + hq_idx) * D + d] = num / den;
+}
+
+template <int D, int G, typename KVT>
+static int attn_run(const float* q, const KVT* k, const KVT* v, float* out, float* ws, int B,
+                    int hkv, int64_t lmax, int64_t kv_bstride, AttnLen len, int chunk,
+                    int nsplit, float scale, hipStream_t s) {
+    k_attn_partial<D, G, KVT><<<dim3(nsplit, hkv, B), 256, 0, s>>>(q, k, v, ws, hkv, lmax,
+                                                                  kv_bstride, len, chunk,
+                                                                  nsplit, scale);
+    k_attn_combine<D, G><<<dim3(hkv * G, B), D, 0, s>>>(ws, out, hkv, nsplit);
+    hipError_t e = hipGetLastError();
+    return e == hipSuccess ? TL_HIP_OK : hip_fail(e, "attention launch");
+}
+
+// Split plan: about 1024 workgroups over (B x Hkv x splits), chunks a multiple of 32 and at
+// most ATT_MAX_CHUNK positions.
+void attn_plan(int B, int hkv, int64_t L, int* chunk, int* nsplit) {
+    int64_t pairs = (int64_t)B * hkv;
+    int64_t want = (1024 + pairs - 1) / pairs;
+    int64_t c = (L + want - 1) / want;
+    if (c < 64) c = 64;
+    c = (c + 31) / 32 * 32;
+    if (c > ATT_MAX_CHUNK) c = ATT_MAX_CHUNK;
+    *chunk = (int)c;
+    *nsplit = (int)((L + c - 1) / c);
+}
+
+size_t attn_workspace_floats(int B, int hkv, int G, int D, int nsplit) {
+    return (size_t)B * hkv * nsplit * G * (D + 2);
+}
+
+template <typename KVT>
+static int attn_dispatch(const float* q, const KVT* k, const KVT* v, float* out, float* ws,
+                         int B, int hq, int hkv, int D, int64_t lmax, int64_t kv_bstride,
+                         AttnLen len, int chunk, int nsplit, float scale, hipStream_t s) {
+    const int G = hq / hkv;
+#define TLH_ATT(DD, GG)                                                                      \
+    if (D == DD && G == GG)                                                                  \
+        return attn_run<DD, GG, KVT>(q, k, v, out, ws, B, hkv, lmax, kv_bstride, len, chunk, \
+                                     nsplit, scale, s);
+    TLH_ATT(128, 1) TLH_ATT(128, 2) TLH_ATT(128, 4) TLH_ATT(128, 8)
+    TLH_ATT(64, 1) TLH_ATT(64, 2) TLH_ATT(64, 4) TLH_ATT(64, 8)
+#undef TLH_ATT
+    set_error(TL_HIP_ERR_ARG, "ArgumentError: attention supports head_dim 64/128 and 1, 2, 4 or 8 "
+              "query heads per KV head (got D=%d, group %d)", D, G);
+    return TL_HIP_ERR_ARG;
+}
+
+int launch_attention(const float* q, const void* k, const void* v, int kv_dtype, float* out,
+                     float* ws, int B, int hq, int hkv, int D, int64_t lmax, int64_t kv_bstride,
+                     int64_t L, const int32_t* len_dev, int len_add, int len_step, int chunk,
+                     int nsplit, float scale, hipStream_t s) {
+    AttnLen len{L, len_dev, len_add, len_step};
+    if (kv_dtype == TL_HIP_F16)
+        return attn_dispatch<__half>(q, (const __half*)k, (const __half*)v, out, ws, B, hq, hkv, D,
+                                     lmax, kv_bstride, len, chunk, nsplit, scale, s);
+    return attn_dispatch<float>(q, (const float*)k, (const float*)v, out, ws, B, hq, hkv, D, lmax,
+                                kv_bstride, len, chunk, nsplit, scale, s);
+}
+
+}  // namespace tlhip
+
+using namespace tlhip;
+
+extern "C" tl_hip_tensor* tl_hip_attention_decode(const tl_hip_tensor* qh, const tl_hip_tensor* kh,
+                                                  const tl_hip_tensor* vh, int64_t L, float scale) {
+    if (!qh || !kh || !vh) {
+        set_error(TL_HIP_ERR_NULL, "NullPointerError: q, k or v");
+        return nullptr;
+    }
+    if (!state()) return nullptr;
+    const Tensor* q = reinterpret_cast<const Tensor*>(qh);
+    const Tensor* k = reinterpret_cast<const Tensor*>(kh);
+    const Tensor* v = reinterpret_cast<const Tensor*>(vh);
+    if (q->dtype != TL_HIP_F32 || k->dtype != v->dtype) {
+        set_error(TL_HIP_ERR_TYPE, "TypeMismatch: q must be f32 and k, v of one dtype");
+        return nullptr;
+    }
+    if (q->rank != 3 || k->rank != 4 || v->rank != 4) {
+        set_error(TL_HIP_ERR_SHAPE, "ShapeMismatch: q [B,Hq,D], k/v [B,Hkv,Lmax,D] expected");
+        return nullptr;
+    }
+    const int64_t B = q->shape[0], hq = q->shape[1], D = q->shape[2];
+    const int64_t hkv = k->shape[1], lmax = k->shape[2];
+    for (int i = 0; i < 4; i++)
+        if (k->shape[i] != v->shape[i]) {
+            set_error(TL_HIP_ERR_SHAPE, "ShapeMismatch: k and v shapes differ");
+            return nullptr;
+        }
+    if (k->shape[0] != B || k->shape[3] != D || hkv <= 0 || hq % hkv != 0) {
+        set_error(TL_HIP_ERR_SHAPE, "ShapeMismatch: q [%lld,%lld,%lld] vs kv [%lld,%lld,%lld,%lld]",
+                  (long long)B, (long long)hq, (long long)D, (long long)k->shape[0], (long long)hkv,
+                  (long long)lmax, (long long)k->shape[3]);
+        return nullptr;
+    }
+    if (L < 1 || L > lmax) {
+        set_error(TL_HIP_ERR_ARG, "ArgumentError: cached length %lld outside 1..%lld", (long long)L,
+                  (long long)lmax);
+        return nullptr;
+    }
+    if (B > 65535 || hkv > 65535) {
+        set_error(TL_HIP_ERR_ARG, "ArgumentError: batch or head count too large");
+        return nullptr;
+    }
+    int chunk, nsplit;
+    attn_plan((int)B, (int)hkv, L, &chunk, &nsplit);
+    int64_t oshape[3] = {B, hq, D};
+    Tensor* o = tensor_alloc(oshape, 3);
+    if (!o) return nullptr;
+    float* ws = (float*)dev_alloc(attn_workspace_floats((int)B, (int)hkv, (int)(hq / hkv), (int)D, nsplit) * 4);
+    if (!ws) {
+        tensor_drop(o);
+        return nullptr;
+    }
+    int rc = launch_attention(q->f32(), k->data, v->data, k->dtype, o->f32(), ws, (int)B, (int)hq,
+                              (int)hkv, (int)D, lmax, hkv * lmax * D, L, nullptr, 0, 0, chunk, nsplit,
+                              scale, cur_stream());
+    dev_free(ws);  // stream-ordered: reused only by later work on the same stream
+    if (rc != TL_HIP_OK) {
+        tensor_drop(o);
+        return nullptr;
+    }
+    return H(o);
+}

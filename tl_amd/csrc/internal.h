@@ -1,0 +1,110 @@
+// Internal declarations shared by the tl_hip translation units (not part of the C ABI).
+#pragma once
+#include <hip/hip_runtime.h>
+#include <hip/hip_fp16.h>
+#include <stdint.h>
+#include <stddef.h>
+#include <atomic>
+#include <string>
+
+#include "../../include/tl_hip.h"
+
+namespace tlhip {
+
+// ---- errors: thread-local last error, mirroring the reference's TLS LAST_ERROR
+// (crates/tl_runtime/src/device_ffi.rs:22-80) ---------------------------------------
+void set_error(int status, const char* fmt, ...) __attribute__((format(printf, 2, 3)));
+void clear_error();
+int hip_fail(hipError_t e, const char* what);  // records a DeviceError, returns status
+
+#define TLH_CHECK_HIP(expr)                                  \
+    do {                                                     \
+        hipError_t _e = (expr);                              \
+        if (_e != hipSuccess) return ::tlhip::hip_fail(_e, #expr); \
+    } while (0)
+
+// ---- device state -----------------------------------------------------------------
+struct DeviceState {
+    int device = -1;
+    hipStream_t stream = nullptr;
+    int num_cus = 0;
+    int num_xcds = 8;
+};
+DeviceState* state();      // initialises device 0 on first use; nullptr on failure
+hipStream_t cur_stream();  // library stream (or the override set by tl_hip_set_stream)
+
+// ---- stream-ordered caching allocator --------------------------------------------
+// Every library kernel runs on one stream, so a block freed after its last use on that
+// stream can be handed to the next request without a device synchronisation.
+void* dev_alloc(size_t bytes);  // nullptr + AllocationError on failure
+void dev_free(void* p);
+
+// ---- tensors ---------------------------------------------------------------------
+struct Tensor {
+    void* data = nullptr;  // device memory
+    int64_t shape[TL_HIP_MAX_RANK] = {0};
+    int rank = 0;
+    int64_t numel = 0;
+    int dtype = TL_HIP_F32;
+    bool owns = true;
+    std::atomic<int> refs{1};
+    float* f32() const { return static_cast<float*>(data); }
+};
+Tensor* tensor_alloc(const int64_t* shape, int rank, int dtype = TL_HIP_F32);
+inline Tensor* T(tl_hip_tensor* h) { return reinterpret_cast<Tensor*>(h); }
+inline tl_hip_tensor* H(Tensor* t) { return reinterpret_cast<tl_hip_tensor*>(t); }
+void tensor_drop(Tensor* t);
+size_t dtype_size(int dtype);
+
+// ---- quantized weights (device residency of a GGUF Q4_0 / Q8_0 tensor) ------------
+// Struct-of-arrays repack of the 18-byte (Q4_0) / 34-byte (Q8_0) GGUF blocks:
+//   qs: [n][nb][16 | 32] bytes, 16-byte aligned (one dwordx4 / two per block)
+//   d : [n][nb] f16 scales
+// Same byte count as the GGUF stream; rows of one block column are contiguous.
+struct QWeight {
+    int ggml_type = 0;
+    int64_t n = 0, k = 0, nb = 0;  // rows, cols, blocks per row
+    uint8_t* qs = nullptr;
+    __half* d = nullptr;
+    int64_t shape[TL_HIP_MAX_RANK] = {0};
+    int rank = 0;
+    std::atomic<int> refs{1};
+};
+inline QWeight* Q(tl_hip_qtensor* h) { return reinterpret_cast<QWeight*>(h); }
+
+// kernel entry points shared across translation units (all on the given stream)
+int launch_quant_matvec(const QWeight* w, const float* x, float* y, int64_t m, hipStream_t s,
+                        const float* residual);
+int launch_quant_gemm(const QWeight* w, const float* x, float* y, int64_t m, hipStream_t s,
+                      int mode);
+int launch_matmul_f32(const float* a, const float* b, float* c, int64_t batch, int64_t m,
+                      int64_t k, int64_t n, int64_t a_bstride, int64_t b_bstride,
+                      hipStream_t s);
+
+int launch_rmsnorm(const float* x, const float* r, const float* w, float* out, int64_t rows,
+                   int64_t n, float eps, int mode, hipStream_t s);
+int launch_swiglu(const float* g, const float* u, float* o, int64_t n, int mode, hipStream_t s);
+int launch_softmax(const float* x, float* out, int64_t outer, int64_t as, int64_t inner,
+                   hipStream_t s);
+int launch_argmax(const float* x, int64_t n, int32_t* out_idx, hipStream_t s);
+int launch_rep_penalty(const float* x, const uint8_t* seen, float* o, int64_t rows,
+                       int64_t vocab, float p, hipStream_t s);
+int launch_embedding(const float* table, const int32_t* ids, float* o, int64_t n, int64_t dim,
+                     hipStream_t s);
+int launch_apply_rope(const float* x, const float* ct, const float* st, float* out,
+                      int64_t total, int64_t hd, int64_t cos_len, int64_t sin_len, int64_t row0,
+                      int64_t vpt, hipStream_t s);
+int launch_rope_table(float* out, int64_t seq_len, int64_t dim, float base, int is_sin,
+                      hipStream_t s);
+// Attention over a [B?, Hkv, lmax, D] cache (kv_bstride elements between batch items, 0 =
+// shared).  Cached length of item b = (len_dev ? *len_dev + len_add : L) + b * len_step.
+int launch_attention(const float* q, const void* k, const void* v, int kv_dtype, float* out,
+                     float* ws, int B, int hq, int hkv, int D, int64_t lmax, int64_t kv_bstride,
+                     int64_t L, const int32_t* len_dev, int len_add, int len_step, int chunk,
+                     int nsplit, float scale, hipStream_t s);
+void attn_plan(int B, int hkv, int64_t L, int* chunk, int* nsplit);
+size_t attn_workspace_floats(int B, int hkv, int G, int D, int nsplit);
+
+inline int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
+
+}  // namespace tlhip

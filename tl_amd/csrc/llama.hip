@@ -1,0 +1,653 @@
+// Llama decoder driver: the model composition of examples/apps/tinyllama/chatbot.tl
+// (Linear / RMSNorm / MLP / Attention / Block, lines 1-112, and the decode loop, 174-222)
+// executed on the device.
+//
+// Differences in form (not in arithmetic) from the chatbot's op-by-op execution:
+//  * q/k/v and gate/up weights are concatenated row-wise at load, so each projection pair /
+//    triple is one matvec (every output row is the same dot product);
+//  * the residual adds x + o-proj(x) and x + down(x) are fused into the matvec epilogue;
+//  * RoPE, the KV-cache append and the q transpose are one kernel writing into a persistent
+//    per-layer cache [Hkv, max_seq, head_dim] (instead of cat_4d + KVCache.update,
+//    chatbot.tl:63-69), and attention reads the cache in place with GQA (no
+//    repeat_interleave copy);
+//  * the LM head runs on the last row only (the chatbot narrows to it, chatbot.tl:189);
+//  * the cache position lives in device memory, so a decode step has no host
+//    dependency and is captured once as a hipGraph and replayed.
+#include "internal.h"
+
+#include <cstring>
+#include <vector>
+
+namespace tlhip {
+
+// token embedding of one or more ids (tensor.rs:1094-1112); ids were range-checked on the
+// host or produced by argmax (< vocab).
+__global__ void k_embed(const float* __restrict__ emb, const int32_t* __restrict__ ids,
+                        float* __restrict__ x, int n, int64_t dim) {
+    int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (t >= n * dim) return;
+    int64_t i = t / dim, j = t % dim;
+    x[t] = emb[(int64_t)ids[i] * dim + j];
+}
+
+// RoPE (interleaved pairs, ffi.rs:2655-2681) on q and k of n tokens, q re-laid out as
+// [n, H, hd] (already its layout) and k, v appended to the cache at position pos + t.
+// Rotation row: pos (tl_cpu: the narrowed table's first row) or pos + t (per-token).
+template <typename KVT>
+__global__ void k_rope_kv(const float* __restrict__ qkv, float* __restrict__ qout,
+                          KVT* __restrict__ kc, KVT* __restrict__ vc,
+                          const float* __restrict__ ct, const float* __restrict__ st,
+                          const int32_t* __restrict__ pos_dev, int n, int H, int KV, int hd,
+                          int64_t max_seq, int per_token) {
+    const int row = H * hd + 2 * KV * hd;
+    const int pairs = (H + KV) * hd / 2;  // rotated pairs per token
+    const int vals = KV * hd;             // copied v values per token
+    int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    const int per_tok = pairs + vals;
+    if (t >= (int64_t)n * per_tok) return;
+    const int tok = (int)(t / per_tok);
+    const int e = (int)(t % per_tok);
+    const int64_t pos = (int64_t)(*pos_dev);
+    const int64_t cpos = pos + tok;  // cache slot
+    const float* src = qkv + (int64_t)tok * row;
+    if (e < pairs) {
+        const int64_t trow = per_token ? pos + tok : pos;
+        const int idx = 2 * e;  // element index within q|k
+        const int i = idx % hd;  // pair start within the head vector
+        float c = ct[trow * hd + i], s = st[trow * hd + i];
+        float x0 = src[idx], x1 = src[idx + 1];
+        float r0 = x0 * c - x1 * s;
+        float r1 = x0 * s + x1 * c;
+        if (idx < H * hd) {
+            qout[(int64_t)tok * H * hd + idx] = r0;
+            qout[(int64_t)tok * H * hd + idx + 1] = r1;
+        } else {
+            int kidx = idx - H * hd;
+            int kh = kidx / hd;
+            KVT* dst = kc + ((int64_t)kh * max_seq + cpos) * hd + i;
+            dst[0] = (KVT)r0;
+            dst[1] = (KVT)r1;
+        }
+    } else {
+        int vidx = e - pairs;
+        int vh = vidx / hd, d = vidx % hd;
+        vc[((int64_t)vh * max_seq + cpos) * hd + d] = (KVT)src[H * hd + KV * hd + vidx];
+    }
+}
+
+// SwiGLU on the concatenated gate|up rows: a[r, j] = silu(gu[r, j]) * gu[r, F + j]
+// (silu of ffi.rs:2097-2113 then mul, chatbot.tl:33-38)
+__global__ void k_swiglu_rows(const float* __restrict__ gu, float* __restrict__ a, int n,
+                              int64_t F) {
+    int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (t >= n * F) return;
+    int64_t r = t / F, j = t % F;
+    float g = gu[r * 2 * F + j], u = gu[r * 2 * F + F + j];
+    a[t] = (g * (1.0f / (1.0f + expf(-g)))) * u;
+}
+
+__global__ void k_add_inplace(float* __restrict__ x, const float* __restrict__ t, int64_t n) {
+    int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) x[i] = x[i] + t[i];
+}
+
+__global__ void k_advance(int32_t* pos, int n) {
+    if (threadIdx.x == 0 && blockIdx.x == 0) *pos += n;
+}
+
+// end of a decode step: record the sampled id, mark it for the repetition penalty,
+// advance the step counter
+__global__ void k_step_end(const int32_t* __restrict__ tok, int32_t* __restrict__ out_ids,
+                           int32_t* __restrict__ step, uint8_t* __restrict__ seen, int max_out) {
+    if (threadIdx.x == 0 && blockIdx.x == 0) {
+        int s = *step;
+        if (s < max_out) out_ids[s] = *tok;
+        if (seen) seen[*tok] = 1;
+        *step = s + 1;
+    }
+}
+
+struct Llama {
+    int nl, D, H, KV, hd, F, V, max_seq;
+    float eps, theta;
+    int kv_f16 = 0, rope_per_token = 0;
+    std::vector<QWeight*> wqkv, wo, wgu, wdown;
+    QWeight* lm = nullptr;
+    // host staging of q/k/v and gate/up until all parts of a layer are present
+    std::vector<std::vector<uint8_t>> stage;  // [nl * 5]: q k v gate up
+    std::vector<int> stage_type;
+    std::vector<float*> attn_norm, ffn_norm;
+    float* out_norm = nullptr;
+    float* emb = nullptr;
+    float *cos_t = nullptr, *sin_t = nullptr;
+    std::vector<void*> kc, vc;
+    // activations for up to max_tok tokens per call
+    int64_t max_tok = 0;
+    float *x = nullptr, *h = nullptr, *qkv = nullptr, *q = nullptr, *ao = nullptr, *t = nullptr,
+          *gu = nullptr, *act = nullptr, *logits = nullptr, *plogits = nullptr, *ws = nullptr;
+    size_t ws_floats = 0;
+    int32_t *ids = nullptr, *pos = nullptr, *tok = nullptr, *step = nullptr, *out_ids = nullptr;
+    uint8_t* seen = nullptr;
+    int max_out = 0;
+    int64_t host_pos = 0;
+    hipGraphExec_t graph = nullptr;
+    int graph_key[3] = {-1, -1, -1};  // (penalty on, kv_f16, rope_per_token) it was built for
+};
+
+static Llama* L_(tl_hip_llama* h) { return reinterpret_cast<Llama*>(h); }
+
+static void free_graph(Llama* m) {
+    if (m->graph) {
+        (void)hipGraphExecDestroy(m->graph);
+        m->graph = nullptr;
+    }
+}
+
+static int alloc_kv(Llama* m) {
+    for (void* p : m->kc) dev_free(p);
+    for (void* p : m->vc) dev_free(p);
+    m->kc.assign(m->nl, nullptr);
+    m->vc.assign(m->nl, nullptr);
+    size_t bytes = (size_t)m->KV * m->max_seq * m->hd * (m->kv_f16 ? 2 : 4);
+    for (int l = 0; l < m->nl; l++) {
+        m->kc[l] = dev_alloc(bytes);
+        m->vc[l] = dev_alloc(bytes);
+        if (!m->kc[l] || !m->vc[l]) return TL_HIP_ERR_ALLOC;
+        TLH_CHECK_HIP(hipMemsetAsync(m->kc[l], 0, bytes, cur_stream()));
+        TLH_CHECK_HIP(hipMemsetAsync(m->vc[l], 0, bytes, cur_stream()));
+    }
+    return TL_HIP_OK;
+}
+
+static int ensure_tokens(Llama* m, int64_t n) {
+    if (n <= m->max_tok) return TL_HIP_OK;
+    float** bufs[] = {&m->x, &m->h, &m->qkv, &m->q, &m->ao, &m->t, &m->gu, &m->act};
+    for (float** b : bufs) {
+        dev_free(*b);
+        *b = nullptr;
+    }
+    dev_free(m->ids);
+    dev_free(m->ws);
+    const int64_t qkv_w = m->D + 2 * (int64_t)m->KV * m->hd;
+    m->x = (float*)dev_alloc(n * m->D * 4);
+    m->h = (float*)dev_alloc(n * m->D * 4);
+    m->qkv = (float*)dev_alloc(n * qkv_w * 4);
+    m->q = (float*)dev_alloc(n * m->D * 4);
+    m->ao = (float*)dev_alloc(n * m->D * 4);
+    m->t = (float*)dev_alloc(n * m->D * 4);
+    m->gu = (float*)dev_alloc(n * 2 * (int64_t)m->F * 4);
+    m->act = (float*)dev_alloc(n * (int64_t)m->F * 4);
+    m->ids = (int32_t*)dev_alloc(n * 4);
+    // attention workspace: B = n queries, 64-position chunks over max_seq
+    int nsplit = (int)cdiv(m->max_seq, 64);
+    m->ws_floats = attn_workspace_floats((int)n, m->KV, m->H / m->KV, m->hd, nsplit);
+    m->ws = (float*)dev_alloc(m->ws_floats * 4);
+    for (float** b : bufs)
+        if (!*b) return TL_HIP_ERR_ALLOC;
+    if (!m->ids || !m->ws) return TL_HIP_ERR_ALLOC;
+    m->max_tok = n;
+    free_graph(m);  // captured pointers changed
+    return TL_HIP_OK;
+}
+
+static int try_merge(Llama* m, int layer) {
+    auto& S = m->stage;
+    const int base = layer * 5;
+    if (!S[base].empty() && !S[base + 1].empty() && !S[base + 2].empty()) {
+        int ty = m->stage_type[base];
+        if (m->stage_type[base + 1] != ty || m->stage_type[base + 2] != ty) {
+            set_error(TL_HIP_ERR_TYPE, "TypeMismatch: q/k/v of layer %d differ in ggml type", layer);
+            return TL_HIP_ERR_TYPE;
+        }
+        std::vector<uint8_t> cat;
+        for (int i = 0; i < 3; i++) cat.insert(cat.end(), S[base + i].begin(), S[base + i].end());
+        int64_t shape[2] = {m->D + 2 * (int64_t)m->KV * m->hd, m->D};
+        tl_hip_qtensor* q = tl_hip_qtensor_new(ty, cat.data(), cat.size(), shape, 2);
+        if (!q) return tl_hip_last_status();
+        if (m->wqkv[layer]) tl_hip_qtensor_release(reinterpret_cast<tl_hip_qtensor*>(m->wqkv[layer]));
+        m->wqkv[layer] = Q(q);
+        for (int i = 0; i < 3; i++) std::vector<uint8_t>().swap(S[base + i]);
+    }
+    if (!S[base + 3].empty() && !S[base + 4].empty()) {
+        int ty = m->stage_type[base + 3];
+        if (m->stage_type[base + 4] != ty) {
+            set_error(TL_HIP_ERR_TYPE, "TypeMismatch: gate/up of layer %d differ in ggml type", layer);
+            return TL_HIP_ERR_TYPE;
+        }
+        std::vector<uint8_t> cat(S[base + 3]);
+        cat.insert(cat.end(), S[base + 4].begin(), S[base + 4].end());
+        int64_t shape[2] = {2 * (int64_t)m->F, m->D};
+        tl_hip_qtensor* q = tl_hip_qtensor_new(ty, cat.data(), cat.size(), shape, 2);
+        if (!q) return tl_hip_last_status();
+        if (m->wgu[layer]) tl_hip_qtensor_release(reinterpret_cast<tl_hip_qtensor*>(m->wgu[layer]));
+        m->wgu[layer] = Q(q);
+        for (int i = 3; i < 5; i++) std::vector<uint8_t>().swap(S[base + i]);
+    }
+    return TL_HIP_OK;
+}
+
+// y[n, N] = x[n, K] . W^T (+ residual); matvec for n <= 4, GEMM otherwise
+static int linear(const QWeight* w, const float* x, float* y, int64_t n, const float* res,
+                  float* tmp, int f16, hipStream_t s) {
+    if (n <= 4) return launch_quant_matvec(w, x, y, n, s, res);
+    if (!res) return launch_quant_gemm(w, x, y, n, s, f16);
+    int rc = launch_quant_gemm(w, x, tmp, n, s, f16);
+    if (rc) return rc;
+    k_add_inplace<<<cdiv(n * w->n, 256), 256, 0, s>>>(y, tmp, n * w->n);
+    return TL_HIP_OK;
+}
+
+static int check_ready(Llama* m) {
+    for (int l = 0; l < m->nl; l++)
+        if (!m->wqkv[l] || !m->wo[l] || !m->wgu[l] || !m->wdown[l] || !m->attn_norm[l] || !m->ffn_norm[l]) {
+            set_error(TL_HIP_ERR_ARG, "ArgumentError: layer %d is missing weights", l);
+            return TL_HIP_ERR_ARG;
+        }
+    if (!m->lm || !m->out_norm || !m->emb) {
+        set_error(TL_HIP_ERR_ARG, "ArgumentError: LM head, output norm or embedding missing");
+        return TL_HIP_ERR_ARG;
+    }
+    return TL_HIP_OK;
+}
+
+// Enqueues one forward over n tokens whose ids are already in m->ids (device); leaves the
+// last row's logits in m->logits and advances the device position by n.
+static int enqueue_forward(Llama* m, int n, int f16, hipStream_t s) {
+    const int64_t D = m->D, hd = m->hd;
+    const int64_t qkv_w = D + 2 * (int64_t)m->KV * hd;
+    int rc;
+    k_embed<<<cdiv(n * D, 256), 256, 0, s>>>(m->emb, m->ids, m->x, n, D);
+    const int G = m->H / m->KV;
+    const int nsplit = (int)cdiv(m->max_seq, 64);
+    for (int l = 0; l < m->nl; l++) {
+        if ((rc = launch_rmsnorm(m->x, nullptr, m->attn_norm[l], m->h, n, D, m->eps, 0, s))) return rc;
+        if ((rc = linear(m->wqkv[l], m->h, m->qkv, n, nullptr, nullptr, f16, s))) return rc;
+        int64_t work = (int64_t)n * ((m->H + m->KV) * hd / 2 + m->KV * hd);
+        if (m->kv_f16)
+            k_rope_kv<__half><<<cdiv(work, 256), 256, 0, s>>>(m->qkv, m->q, (__half*)m->kc[l], (__half*)m->vc[l],
+                                                             m->cos_t, m->sin_t, m->pos, n, m->H, m->KV, (int)hd,
+                                                             m->max_seq, m->rope_per_token);
+        else
+            k_rope_kv<float><<<cdiv(work, 256), 256, 0, s>>>(m->qkv, m->q, (float*)m->kc[l], (float*)m->vc[l],
+                                                            m->cos_t, m->sin_t, m->pos, n, m->H, m->KV, (int)hd,
+                                                            m->max_seq, m->rope_per_token);
+        // query i (absolute position pos + i) attends cache positions 0 .. pos + i
+        if ((rc = launch_attention(m->q, m->kc[l], m->vc[l], m->kv_f16 ? TL_HIP_F16 : TL_HIP_F32, m->ao,
+                                   m->ws, n, m->H, m->KV, (int)hd, m->max_seq, 0, 0, m->pos, 1, 1, 64,
+                                   nsplit, 1.0f / sqrtf((float)hd), s)))
+            return rc;
+        (void)G;
+        if ((rc = linear(m->wo[l], m->ao, m->x, n, m->x, m->t, f16, s))) return rc;
+        if ((rc = launch_rmsnorm(m->x, nullptr, m->ffn_norm[l], m->h, n, D, m->eps, 0, s))) return rc;
+        if ((rc = linear(m->wgu[l], m->h, m->gu, n, nullptr, nullptr, f16, s))) return rc;
+        k_swiglu_rows<<<cdiv(n * (int64_t)m->F, 256), 256, 0, s>>>(m->gu, m->act, n, m->F);
+        if ((rc = linear(m->wdown[l], m->act, m->x, n, m->x, m->t, f16, s))) return rc;
+    }
+    (void)qkv_w;
+    k_advance<<<1, 64, 0, s>>>(m->pos, n);
+    if ((rc = launch_rmsnorm(m->x + (int64_t)(n - 1) * D, nullptr, m->out_norm, m->h, 1, D, m->eps, 0, s))) return rc;
+    if ((rc = launch_quant_matvec(m->lm, m->h, m->logits, 1, s, nullptr))) return rc;
+    hipError_t e = hipGetLastError();
+    return e == hipSuccess ? TL_HIP_OK : hip_fail(e, "forward launch");
+}
+
+// one greedy decode step from the token in m->tok (device)
+static int enqueue_step(Llama* m, float penalty, hipStream_t s) {
+    hipError_t e = hipMemcpyAsync(m->ids, m->tok, 4, hipMemcpyDeviceToDevice, s);
+    if (e != hipSuccess) return hip_fail(e, "token copy");
+    int rc = enqueue_forward(m, 1, 0, s);
+    if (rc) return rc;
+    const float* lg = m->logits;
+    if (penalty != 1.0f) {
+        if ((rc = launch_rep_penalty(m->logits, m->seen, m->plogits, 1, m->V, penalty, s))) return rc;
+        lg = m->plogits;
+    }
+    if ((rc = launch_argmax(lg, m->V, m->tok, s))) return rc;
+    k_step_end<<<1, 64, 0, s>>>(m->tok, m->out_ids, m->step, penalty != 1.0f ? m->seen : nullptr, m->max_out);
+    e = hipGetLastError();
+    return e == hipSuccess ? TL_HIP_OK : hip_fail(e, "step launch");
+}
+
+}  // namespace tlhip
+
+using namespace tlhip;
+
+extern "C" {
+
+tl_hip_llama* tl_hip_llama_new(int n_layers, int d_model, int n_heads, int n_kv_heads, int ffn_dim,
+                               int vocab, float eps, float rope_theta, int max_seq) {
+    if (!state()) return nullptr;
+    if (n_layers <= 0 || d_model <= 0 || n_heads <= 0 || n_kv_heads <= 0 || ffn_dim <= 0 || vocab <= 0 ||
+        max_seq <= 0 || d_model % n_heads || n_heads % n_kv_heads || (d_model / n_heads) % 2 ||
+        d_model % 32 || ffn_dim % 32) {
+        set_error(TL_HIP_ERR_ARG, "ArgumentError: invalid decoder configuration");
+        return nullptr;
+    }
+    Llama* m = new Llama();
+    m->nl = n_layers;
+    m->D = d_model;
+    m->H = n_heads;
+    m->KV = n_kv_heads;
+    m->hd = d_model / n_heads;
+    m->F = ffn_dim;
+    m->V = vocab;
+    m->max_seq = max_seq;
+    m->eps = eps;
+    m->theta = rope_theta;
+    m->wqkv.assign(n_layers, nullptr);
+    m->wo.assign(n_layers, nullptr);
+    m->wgu.assign(n_layers, nullptr);
+    m->wdown.assign(n_layers, nullptr);
+    m->stage.assign((size_t)n_layers * 5, {});
+    m->stage_type.assign((size_t)n_layers * 5, -1);
+    m->attn_norm.assign(n_layers, nullptr);
+    m->ffn_norm.assign(n_layers, nullptr);
+    hipStream_t s = cur_stream();
+    // chatbot.tl:151-152: rope_new_cos(head_dim, table_len, theta) -> [table_len, head_dim]
+    m->cos_t = (float*)dev_alloc((size_t)max_seq * m->hd * 4);
+    m->sin_t = (float*)dev_alloc((size_t)max_seq * m->hd * 4);
+    m->logits = (float*)dev_alloc((size_t)vocab * 4);
+    m->plogits = (float*)dev_alloc((size_t)vocab * 4);
+    m->pos = (int32_t*)dev_alloc(4);
+    m->tok = (int32_t*)dev_alloc(4);
+    m->step = (int32_t*)dev_alloc(4);
+    m->seen = (uint8_t*)dev_alloc(vocab);
+    int rc = (m->cos_t && m->sin_t && m->logits && m->plogits && m->pos && m->tok && m->step && m->seen)
+                 ? TL_HIP_OK : TL_HIP_ERR_ALLOC;
+    if (rc == TL_HIP_OK) rc = launch_rope_table(m->cos_t, max_seq, m->hd, rope_theta, 0, s);
+    if (rc == TL_HIP_OK) rc = launch_rope_table(m->sin_t, max_seq, m->hd, rope_theta, 1, s);
+    if (rc == TL_HIP_OK) rc = alloc_kv(m);
+    if (rc == TL_HIP_OK) rc = ensure_tokens(m, 1);
+    if (rc == TL_HIP_OK) rc = tl_hip_llama_reset(reinterpret_cast<tl_hip_llama*>(m));
+    if (rc != TL_HIP_OK) {
+        tl_hip_llama_free(reinterpret_cast<tl_hip_llama*>(m));
+        return nullptr;
+    }
+    return reinterpret_cast<tl_hip_llama*>(m);
+}
+
+int tl_hip_llama_free(tl_hip_llama* h) {
+    if (!h) return TL_HIP_OK;
+    Llama* m = L_(h);
+    (void)hipStreamSynchronize(cur_stream());
+    free_graph(m);
+    auto rel = [](QWeight* w) {
+        if (w) tl_hip_qtensor_release(reinterpret_cast<tl_hip_qtensor*>(w));
+    };
+    for (int l = 0; l < m->nl; l++) {
+        rel(m->wqkv[l]);
+        rel(m->wo[l]);
+        rel(m->wgu[l]);
+        rel(m->wdown[l]);
+        dev_free(m->attn_norm[l]);
+        dev_free(m->ffn_norm[l]);
+    }
+    rel(m->lm);
+    for (void* p : m->kc) dev_free(p);
+    for (void* p : m->vc) dev_free(p);
+    void* bufs[] = {m->out_norm, m->emb, m->cos_t, m->sin_t, m->x, m->h, m->qkv, m->q, m->ao, m->t, m->gu,
+                    m->act, m->logits, m->plogits, m->ws, m->ids, m->pos, m->tok, m->step, m->out_ids, m->seen};
+    for (void* p : bufs) dev_free(p);
+    delete m;
+    return TL_HIP_OK;
+}
+
+int tl_hip_llama_set_linear(tl_hip_llama* h, int layer, int which, int ggml_type, const uint8_t* data,
+                            size_t nbytes) {
+    if (!h || !data) {
+        set_error(TL_HIP_ERR_NULL, "NullPointerError: model or data");
+        return TL_HIP_ERR_NULL;
+    }
+    Llama* m = L_(h);
+    if (layer < -1 || layer >= m->nl || (layer >= 0 && (which < 0 || which > 6))) {
+        set_error(TL_HIP_ERR_ARG, "ArgumentError: weight slot (%d, %d)", layer, which);
+        return TL_HIP_ERR_ARG;
+    }
+    free_graph(m);
+    const int64_t D = m->D, KVd = (int64_t)m->KV * m->hd, F = m->F;
+    if (layer == -1 || which == 3 || which == 6) {
+        int64_t shape[2];
+        if (layer == -1) { shape[0] = m->V; shape[1] = D; }
+        else if (which == 3) { shape[0] = D; shape[1] = D; }
+        else { shape[0] = D; shape[1] = F; }
+        tl_hip_qtensor* q = tl_hip_qtensor_new(ggml_type, data, nbytes, shape, 2);
+        if (!q) return tl_hip_last_status();
+        QWeight** slot = layer == -1 ? &m->lm : (which == 3 ? &m->wo[layer] : &m->wdown[layer]);
+        if (*slot) tl_hip_qtensor_release(reinterpret_cast<tl_hip_qtensor*>(*slot));
+        *slot = Q(q);
+        return TL_HIP_OK;
+    }
+    // q k v gate up: validate the part, stage it, and merge once a group is complete
+    int part = which <= 2 ? which : which - 1;  // 0 q, 1 k, 2 v, 3 gate, 4 up
+    int64_t rows = which == 0 ? D : (which <= 2 ? KVd : F);
+    int64_t numel = rows * D;
+    size_t want = (size_t)(numel / 32) * (ggml_type == TL_HIP_GGML_Q4_0 ? 18 : 34);
+    if (ggml_type != TL_HIP_GGML_Q4_0 && ggml_type != TL_HIP_GGML_Q8_0) {
+        set_error(TL_HIP_ERR_TYPE, "TypeMismatch: ggml type %d has no device residency", ggml_type);
+        return TL_HIP_ERR_TYPE;
+    }
+    if (nbytes != want) {
+        set_error(TL_HIP_ERR_ARG, "ArgumentError: Data size mismatch: expected %zu, got %zu", want, nbytes);
+        return TL_HIP_ERR_ARG;
+    }
+    m->stage[layer * 5 + part].assign(data, data + nbytes);
+    m->stage_type[layer * 5 + part] = ggml_type;
+    return try_merge(m, layer);
+}
+
+int tl_hip_llama_set_norm(tl_hip_llama* h, int layer, int which, const float* w) {
+    if (!h || !w) {
+        set_error(TL_HIP_ERR_NULL, "NullPointerError: model or weight");
+        return TL_HIP_ERR_NULL;
+    }
+    Llama* m = L_(h);
+    if (layer < -1 || layer >= m->nl || (layer >= 0 && which != 0 && which != 1)) {
+        set_error(TL_HIP_ERR_ARG, "ArgumentError: norm slot (%d, %d)", layer, which);
+        return TL_HIP_ERR_ARG;
+    }
+    float** slot = layer == -1 ? &m->out_norm : (which == 0 ? &m->attn_norm[layer] : &m->ffn_norm[layer]);
+    if (!*slot) {
+        *slot = (float*)dev_alloc((size_t)m->D * 4);
+        if (!*slot) return TL_HIP_ERR_ALLOC;
+        free_graph(m);
+    }
+    TLH_CHECK_HIP(hipMemcpyAsync(*slot, w, (size_t)m->D * 4, hipMemcpyHostToDevice, cur_stream()));
+    TLH_CHECK_HIP(hipStreamSynchronize(cur_stream()));
+    return TL_HIP_OK;
+}
+
+int tl_hip_llama_set_embedding(tl_hip_llama* h, const float* table) {
+    if (!h || !table) {
+        set_error(TL_HIP_ERR_NULL, "NullPointerError: model or table");
+        return TL_HIP_ERR_NULL;
+    }
+    Llama* m = L_(h);
+    size_t bytes = (size_t)m->V * m->D * 4;
+    if (!m->emb) {
+        m->emb = (float*)dev_alloc(bytes);
+        if (!m->emb) return TL_HIP_ERR_ALLOC;
+        free_graph(m);
+    }
+    TLH_CHECK_HIP(hipMemcpyAsync(m->emb, table, bytes, hipMemcpyHostToDevice, cur_stream()));
+    TLH_CHECK_HIP(hipStreamSynchronize(cur_stream()));
+    return TL_HIP_OK;
+}
+
+int tl_hip_llama_configure(tl_hip_llama* h, int kv_f16, int rope_per_token) {
+    if (!h) {
+        set_error(TL_HIP_ERR_NULL, "NullPointerError: model");
+        return TL_HIP_ERR_NULL;
+    }
+    Llama* m = L_(h);
+    free_graph(m);
+    m->rope_per_token = rope_per_token ? 1 : 0;
+    if ((kv_f16 ? 1 : 0) != m->kv_f16) {
+        m->kv_f16 = kv_f16 ? 1 : 0;
+        int rc = alloc_kv(m);
+        if (rc) return rc;
+    }
+    return tl_hip_llama_reset(h);
+}
+
+int tl_hip_llama_reset(tl_hip_llama* h) {
+    if (!h) {
+        set_error(TL_HIP_ERR_NULL, "NullPointerError: model");
+        return TL_HIP_ERR_NULL;
+    }
+    Llama* m = L_(h);
+    TLH_CHECK_HIP(hipMemsetAsync(m->pos, 0, 4, cur_stream()));
+    TLH_CHECK_HIP(hipStreamSynchronize(cur_stream()));
+    m->host_pos = 0;
+    return TL_HIP_OK;
+}
+
+int64_t tl_hip_llama_position(const tl_hip_llama* h) {
+    if (!h) {
+        set_error(TL_HIP_ERR_NULL, "NullPointerError: model");
+        return -1;
+    }
+    return reinterpret_cast<const Llama*>(h)->host_pos;
+}
+
+int tl_hip_llama_forward(tl_hip_llama* h, const int32_t* ids, int n, float* logits_out, int prefill_f16) {
+    if (!h || !ids) {
+        set_error(TL_HIP_ERR_NULL, "NullPointerError: model or ids");
+        return TL_HIP_ERR_NULL;
+    }
+    Llama* m = L_(h);
+    int rc = check_ready(m);
+    if (rc) return rc;
+    if (n <= 0 || m->host_pos + n > m->max_seq) {
+        set_error(TL_HIP_ERR_ARG, "ArgumentError: %d tokens at position %lld exceed max_seq %d", n,
+                  (long long)m->host_pos, m->max_seq);
+        return TL_HIP_ERR_ARG;
+    }
+    for (int i = 0; i < n; i++)
+        if (ids[i] < 0 || ids[i] >= m->V) {
+            set_error(TL_HIP_ERR_INDEX, "IndexOutOfBounds: Embedding index %d out of range for vocab size %d",
+                      ids[i], m->V);
+            return TL_HIP_ERR_INDEX;
+        }
+    if ((rc = ensure_tokens(m, n))) return rc;
+    hipStream_t s = cur_stream();
+    TLH_CHECK_HIP(hipMemcpyAsync(m->ids, ids, (size_t)n * 4, hipMemcpyHostToDevice, s));
+    if ((rc = enqueue_forward(m, n, prefill_f16, s))) return rc;
+    m->host_pos += n;
+    if (logits_out)
+        TLH_CHECK_HIP(hipMemcpyAsync(logits_out, m->logits, (size_t)m->V * 4, hipMemcpyDeviceToHost, s));
+    TLH_CHECK_HIP(hipStreamSynchronize(s));
+    return TL_HIP_OK;
+}
+
+int32_t tl_hip_llama_sample_greedy(tl_hip_llama* h, double repetition_penalty, const int32_t* history,
+                                   int n_history) {
+    if (!h) {
+        set_error(TL_HIP_ERR_NULL, "NullPointerError: model");
+        return -1;
+    }
+    Llama* m = L_(h);
+    if (repetition_penalty <= 0.0) {
+        set_error(TL_HIP_ERR_ARG, "ArgumentError: repetition penalty must be positive");
+        return -1;
+    }
+    hipStream_t s = cur_stream();
+    const float pen = (float)repetition_penalty;
+    const float* lg = m->logits;
+    if (pen != 1.0f) {
+        std::vector<uint8_t> seen(m->V, 0);
+        for (int i = 0; i < n_history; i++)
+            if (history && history[i] >= 0 && history[i] < m->V) seen[history[i]] = 1;
+        if (hipMemcpyAsync(m->seen, seen.data(), m->V, hipMemcpyHostToDevice, s) != hipSuccess ||
+            launch_rep_penalty(m->logits, m->seen, m->plogits, 1, m->V, pen, s) != TL_HIP_OK) {
+            hip_fail(hipGetLastError(), "repetition penalty");
+            return -1;
+        }
+        lg = m->plogits;
+    }
+    if (launch_argmax(lg, m->V, m->tok, s) != TL_HIP_OK) return -1;
+    int32_t id = -1;
+    hipError_t e = hipMemcpyAsync(&id, m->tok, 4, hipMemcpyDeviceToHost, s);
+    if (e == hipSuccess) e = hipStreamSynchronize(s);
+    if (e != hipSuccess) {
+        hip_fail(e, "sample readback");
+        return -1;
+    }
+    return id;
+}
+
+int tl_hip_llama_generate(tl_hip_llama* h, int32_t first, int n_steps, int32_t* out_ids,
+                          double repetition_penalty, const int32_t* history, int n_history, int use_graph) {
+    if (!h || !out_ids) {
+        set_error(TL_HIP_ERR_NULL, "NullPointerError: model or output");
+        return TL_HIP_ERR_NULL;
+    }
+    Llama* m = L_(h);
+    int rc = check_ready(m);
+    if (rc) return rc;
+    if (n_steps <= 0) return TL_HIP_OK;
+    if (m->host_pos + n_steps > m->max_seq) {
+        set_error(TL_HIP_ERR_ARG, "ArgumentError: %d steps at position %lld exceed max_seq %d", n_steps,
+                  (long long)m->host_pos, m->max_seq);
+        return TL_HIP_ERR_ARG;
+    }
+    if (first < 0 || first >= m->V) {
+        set_error(TL_HIP_ERR_INDEX, "IndexOutOfBounds: token %d out of range for vocab size %d", first, m->V);
+        return TL_HIP_ERR_INDEX;
+    }
+    if (repetition_penalty <= 0.0) {
+        set_error(TL_HIP_ERR_ARG, "ArgumentError: repetition penalty must be positive");
+        return TL_HIP_ERR_ARG;
+    }
+    hipStream_t s = cur_stream();
+    if ((rc = ensure_tokens(m, 1))) return rc;
+    if (n_steps > m->max_out) {
+        free_graph(m);
+        dev_free(m->out_ids);
+        m->out_ids = (int32_t*)dev_alloc((size_t)n_steps * 4);
+        if (!m->out_ids) return TL_HIP_ERR_ALLOC;
+        m->max_out = n_steps;
+    }
+    const float pen = (float)repetition_penalty;
+    if (pen != 1.0f) {
+        // the ids the penalty sees: history plus the token being fed (chatbot.tl:188, 221)
+        std::vector<uint8_t> seen(m->V, 0);
+        for (int i = 0; i < n_history; i++)
+            if (history && history[i] >= 0 && history[i] < m->V) seen[history[i]] = 1;
+        seen[first] = 1;
+        TLH_CHECK_HIP(hipMemcpyAsync(m->seen, seen.data(), m->V, hipMemcpyHostToDevice, s));
+        TLH_CHECK_HIP(hipStreamSynchronize(s));
+    }
+    int32_t zero = 0;
+    TLH_CHECK_HIP(hipMemcpyAsync(m->tok, &first, 4, hipMemcpyHostToDevice, s));
+    TLH_CHECK_HIP(hipMemcpyAsync(m->step, &zero, 4, hipMemcpyHostToDevice, s));
+    TLH_CHECK_HIP(hipStreamSynchronize(s));
+    if (use_graph) {
+        const int key[3] = {pen != 1.0f, m->kv_f16, m->rope_per_token};
+        if (m->graph && std::memcmp(key, m->graph_key, sizeof(key)) != 0) free_graph(m);
+        if (!m->graph) {
+            hipGraph_t g;
+            TLH_CHECK_HIP(hipStreamBeginCapture(s, hipStreamCaptureModeThreadLocal));
+            rc = enqueue_step(m, pen, s);
+            hipError_t e = hipStreamEndCapture(s, &g);
+            if (rc) return rc;
+            if (e != hipSuccess) return hip_fail(e, "hipStreamEndCapture");
+            e = hipGraphInstantiate(&m->graph, g, nullptr, nullptr, 0);
+            (void)hipGraphDestroy(g);
+            if (e != hipSuccess) {
+                m->graph = nullptr;
+                return hip_fail(e, "hipGraphInstantiate");
+            }
+            std::memcpy(m->graph_key, key, sizeof(key));
+        }
+        for (int i = 0; i < n_steps; i++) TLH_CHECK_HIP(hipGraphLaunch(m->graph, s));
+    } else {
+        for (int i = 0; i < n_steps; i++)
+            if ((rc = enqueue_step(m, pen, s))) return rc;
+    }
+    TLH_CHECK_HIP(hipMemcpyAsync(out_ids, m->out_ids, (size_t)n_steps * 4, hipMemcpyDeviceToHost, s));
+    TLH_CHECK_HIP(hipStreamSynchronize(s));
+    m->host_pos += n_steps;
+    return TL_HIP_OK;
+}
+
+}  // extern "C"

@@ -1,0 +1,1105 @@
+// Memory-bound row and element operators of the decode/prefill path, single pass where
+// the reference makes several: RMSNorm (+weight), RoPE tables and application, SiLU /
+// SwiGLU, row softmax, broadcast binary ops, scale, and the data-movement glue of the
+// chatbot's attention (narrow / cat / repeat_interleave / transpose), embedding gather,
+// greedy argmax and repetition penalty.  f32 math throughout.
+#include "internal.h"
+
+#include <cmath>
+#include <cstring>
+#include <vector>
+
+namespace tlhip {
+
+__device__ __forceinline__ float warp_sum(float v) {
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off, 64);
+    return v;
+}
+__device__ __forceinline__ float warp_max(float v) {
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, 64));
+    return v;
+}
+
+// block-wide sum; every thread receives the result.  `red` holds >= blockDim/64 floats.
+__device__ __forceinline__ float block_sum(float v, float* red) {
+    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, nw = blockDim.x >> 6;
+    v = warp_sum(v);
+    __syncthreads();
+    if (lane == 0) red[w] = v;
+    __syncthreads();
+    float s = 0.f;
+    for (int i = 0; i < nw; i++) s += red[i];
+    return s;
+}
+__device__ __forceinline__ float block_max(float v, float* red) {
+    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, nw = blockDim.x >> 6;
+    v = warp_max(v);
+    __syncthreads();
+    if (lane == 0) red[w] = v;
+    __syncthreads();
+    float s = -INFINITY;
+    for (int i = 0; i < nw; i++) s = fmaxf(s, red[i]);
+    return s;
+}
+
+// ------------------------------------------------------------------ RMSNorm ---------
+// One workgroup per row; the row is held in registers (V float4 per thread) so x is read
+// once.  mode 0: (x / sqrt(ms + eps)) * w     (tl_cpu ffi.rs:2444-2486 + mul_impl)
+//      mode 1: x * (1 / sqrt(ms + eps)) * w   (fused_rms_norm, fused_ops.rs:37-57)
+// With a residual r the row is x + r first (fused_add_rms_norm, fused_ops.rs:59-85).
+template <int V>
+__global__ __launch_bounds__(256) void k_rmsnorm(const float* __restrict__ x,
+                                                 const float* __restrict__ r,
+                                                 const float* __restrict__ w,
+                                                 float* __restrict__ out, int64_t n, float eps,
+                                                 int mode) {
+    __shared__ float red[4];
+    const int64_t row = blockIdx.x;
+    const float4* xr = reinterpret_cast<const float4*>(x + row * n);
+    const float4* rr = r ? reinterpret_cast<const float4*>(r + row * n) : nullptr;
+    const int64_t n4 = n >> 2;
+    float4 v[V];
+    float ss = 0.f;
+#pragma unroll
+    for (int i = 0; i < V; i++) {
+        int64_t j = threadIdx.x + (int64_t)i * 256;
+        v[i] = make_float4(0.f, 0.f, 0.f, 0.f);
+        if (j < n4) {
+            v[i] = xr[j];
+            if (rr) {
+                float4 q = rr[j];
+                v[i].x = v[i].x + q.x;
+                v[i].y = v[i].y + q.y;
+                v[i].z = v[i].z + q.z;
+                v[i].w = v[i].w + q.w;
+            }
+        }
+        ss += v[i].x * v[i].x + v[i].y * v[i].y + v[i].z * v[i].z + v[i].w * v[i].w;
+    }
+    ss = block_sum(ss, red);
+    const float ms = ss / (float)n;
+    const float rms = sqrtf(ms + eps);
+    const float rcp = 1.0f / rms;
+    float4* o = reinterpret_cast<float4*>(out + row * n);
+    const float4* w4 = reinterpret_cast<const float4*>(w);
+#pragma unroll
+    for (int i = 0; i < V; i++) {
+        int64_t j = threadIdx.x + (int64_t)i * 256;
+        if (j >= n4) continue;
+        float4 a = v[i], ww = w4 ? w4[j] : make_float4(1.f, 1.f, 1.f, 1.f), res;
+        if (mode == 0) {
+            res.x = a.x / rms; res.y = a.y / rms; res.z = a.z / rms; res.w = a.w / rms;
+            if (w4) { res.x = res.x * ww.x; res.y = res.y * ww.y; res.z = res.z * ww.z; res.w = res.w * ww.w; }
+        } else {
+            res.x = a.x * rcp * ww.x; res.y = a.y * rcp * ww.y;
+            res.z = a.z * rcp * ww.z; res.w = a.w * rcp * ww.w;
+        }
+        o[j] = res;
+    }
+}
+
+// generic RMSNorm for rows not divisible by 4 or longer than 8192: two reads of the row
+__global__ __launch_bounds__(256) void k_rmsnorm_generic(const float* __restrict__ x,
+                                                         const float* __restrict__ r,
+                                                         const float* __restrict__ w,
+                                                         float* __restrict__ out, int64_t n,
+                                                         float eps, int mode) {
+    __shared__ float red[4];
+    const int64_t row = blockIdx.x;
+    const float* xr = x + row * n;
+    const float* rr = r ? r + row * n : nullptr;
+    float ss = 0.f;
+    for (int64_t j = threadIdx.x; j < n; j += 256) {
+        float a = rr ? xr[j] + rr[j] : xr[j];
+        ss += a * a;
+    }
+    ss = block_sum(ss, red);
+    const float rms = sqrtf(ss / (float)n + eps), rcp = 1.0f / rms;
+    for (int64_t j = threadIdx.x; j < n; j += 256) {
+        float a = rr ? xr[j] + rr[j] : xr[j];
+        float res;
+        if (mode == 0) {
+            res = a / rms;
+            if (w) res = res * w[j];
+        } else {
+            res = a * rcp * (w ? w[j] : 1.f);
+        }
+        out[row * n + j] = res;
+    }
+}
+
+int launch_rmsnorm(const float* x, const float* r, const float* w, float* out, int64_t rows,
+                   int64_t n, float eps, int mode, hipStream_t s) {
+    if (rows <= 0 || n <= 0) return TL_HIP_OK;
+    const bool vec = (n % 4 == 0) && ((uintptr_t)x % 16 == 0) && ((uintptr_t)out % 16 == 0) &&
+                     (!r || (uintptr_t)r % 16 == 0) && (!w || (uintptr_t)w % 16 == 0);
+    const int64_t per = cdiv(n / 4, 256);
+    if (vec && per <= 1)
+        k_rmsnorm<1><<<rows, 256, 0, s>>>(x, r, w, out, n, eps, mode);
+    else if (vec && per <= 2)
+        k_rmsnorm<2><<<rows, 256, 0, s>>>(x, r, w, out, n, eps, mode);
+    else if (vec && per <= 4)
+        k_rmsnorm<4><<<rows, 256, 0, s>>>(x, r, w, out, n, eps, mode);
+    else if (vec && per <= 8)
+        k_rmsnorm<8><<<rows, 256, 0, s>>>(x, r, w, out, n, eps, mode);
+    else
+        k_rmsnorm_generic<<<rows, 256, 0, s>>>(x, r, w, out, n, eps, mode);
+    hipError_t e = hipGetLastError();
+    return e == hipSuccess ? TL_HIP_OK : hip_fail(e, "rmsnorm launch");
+}
+
+// -------------------------------------------------------------------- RoPE ----------
+// Tables of tl_cpu_tensor_rope_new_cos/_sin (ffi.rs:2589-2629): [seq_len, dim], entries
+// 2i and 2i+1 hold cos/sin(pos * 1/base^(2i/dim)).
+__global__ void k_rope_table(float* __restrict__ out, int64_t seq_len, int64_t dim, float base,
+                             int is_sin) {
+    int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    int64_t half = dim / 2;
+    if (t >= seq_len * half) return;
+    int64_t pos = t / half, i = t % half;
+    float freq = 1.0f / powf(base, 2.0f * (float)i / (float)dim);
+    float a = (float)pos * freq;
+    float v = is_sin ? sinf(a) : cosf(a);
+    out[pos * dim + 2 * i] = v;
+    out[pos * dim + 2 * i + 1] = v;
+}
+
+// apply_rope (ffi.rs:2631-2686): interleaved pairs (i, i+1) of each head_dim vector.
+// Table row: row0 for every vector (tl_cpu semantics, vpt == 0), or row0 + v / vpt.
+// Entries past the table's end read as cos 1, sin 0.
+__global__ void k_apply_rope(const float* __restrict__ x, const float* __restrict__ ct,
+                             const float* __restrict__ st, float* __restrict__ out,
+                             int64_t npairs, int64_t hd, int64_t cos_len, int64_t sin_len,
+                             int64_t row0, int64_t vpt) {
+    int64_t p = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (p >= npairs) return;
+    int64_t hp = hd / 2;
+    int64_t v = p / hp, i = 2 * (p % hp);
+    int64_t row = vpt > 0 ? row0 + v / vpt : row0;
+    int64_t ti = row * hd + i;
+    float c = ti < cos_len ? ct[ti] : 1.0f;
+    float s = ti < sin_len ? st[ti] : 0.0f;
+    float2 a = reinterpret_cast<const float2*>(x)[p];
+    float2 r;
+    r.x = a.x * c - a.y * s;
+    r.y = a.x * s + a.y * c;
+    reinterpret_cast<float2*>(out)[p] = r;
+}
+
+// --------------------------------------------------------------- elementwise --------
+// op: 0 add, 1 mul, 2 sub, 3 div  (tensor.rs:549-621)
+__device__ __forceinline__ float binop(int op, float a, float b) {
+    switch (op) {
+        case 0: return a + b;
+        case 1: return a * b;
+        case 2: return a - b;
+        default: return a / b;
+    }
+}
+
+struct BStrides {
+    int64_t out_stride[TL_HIP_MAX_RANK];
+    int64_t a_stride[TL_HIP_MAX_RANK];
+    int64_t b_stride[TL_HIP_MAX_RANK];
+    int nd;
+};
+
+__global__ void k_binop_same(const float* __restrict__ a, const float* __restrict__ b,
+                             float* __restrict__ o, int64_t n, int op) {
+    int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) o[i] = binop(op, a[i], b[i]);
+}
+
+__global__ void k_binop_bcast(const float* __restrict__ a, const float* __restrict__ b,
+                              float* __restrict__ o, int64_t n, int op, BStrides st) {
+    int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= n) return;
+    int64_t rem = i, ai = 0, bi = 0;
+    for (int d = 0; d < st.nd; d++) {
+        int64_t c = rem / st.out_stride[d];
+        rem -= c * st.out_stride[d];
+        ai += c * st.a_stride[d];
+        bi += c * st.b_stride[d];
+    }
+    o[i] = binop(op, a[ai], b[bi]);
+}
+
+__global__ void k_scale(const float* __restrict__ x, float* __restrict__ o, int64_t n, float s) {
+    int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) o[i] = x[i] * s;
+}
+
+// silu (ffi.rs:2097-2113): x * (1 / (1 + exp(-x)))
+__global__ void k_silu(const float* __restrict__ x, float* __restrict__ o, int64_t n) {
+    int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) {
+        float v = x[i];
+        o[i] = v * (1.0f / (1.0f + expf(-v)));
+    }
+}
+
+// SwiGLU.  mode 0: silu(g) * u with the silu of ffi.rs:2102 then mul (chatbot.tl:33-38);
+// mode 1: (g / (1 + exp(-g))) * u (fused_silu_mul, tl_cpu fused_ops.rs:15-35).
+__global__ void k_swiglu(const float* __restrict__ g, const float* __restrict__ u,
+                         float* __restrict__ o, int64_t n, int mode) {
+    int64_t i4 = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i4 * 4 + 3 < n) {
+        float4 a = reinterpret_cast<const float4*>(g)[i4];
+        float4 b = reinterpret_cast<const float4*>(u)[i4];
+        float4 r;
+        if (mode == 0) {
+            r.x = (a.x * (1.0f / (1.0f + expf(-a.x)))) * b.x;
+            r.y = (a.y * (1.0f / (1.0f + expf(-a.y)))) * b.y;
+            r.z = (a.z * (1.0f / (1.0f + expf(-a.z)))) * b.z;
+            r.w = (a.w * (1.0f / (1.0f + expf(-a.w)))) * b.w;
+        } else {
+            r.x = (a.x / (1.0f + expf(-a.x))) * b.x;
+            r.y = (a.y / (1.0f + expf(-a.y))) * b.y;
+            r.z = (a.z / (1.0f + expf(-a.z))) * b.z;
+            r.w = (a.w / (1.0f + expf(-a.w))) * b.w;
+        }
+        reinterpret_cast<float4*>(o)[i4] = r;
+    } else {
+        for (int64_t i = i4 * 4; i < n; i++) {
+            float a = g[i];
+            o[i] = mode == 0 ? (a * (1.0f / (1.0f + expf(-a)))) * u[i] : (a / (1.0f + expf(-a))) * u[i];
+        }
+    }
+}
+
+int launch_swiglu(const float* g, const float* u, float* o, int64_t n, int mode, hipStream_t s) {
+    if (n <= 0) return TL_HIP_OK;
+    if (((uintptr_t)g | (uintptr_t)u | (uintptr_t)o) % 16 != 0) {
+        set_error(TL_HIP_ERR_ARG, "ArgumentError: swiglu operands must be 16-byte aligned");
+        return TL_HIP_ERR_ARG;
+    }
+    k_swiglu<<<cdiv(cdiv(n, 4), 256), 256, 0, s>>>(g, u, o, n, mode);
+    hipError_t e = hipGetLastError();
+    return e == hipSuccess ? TL_HIP_OK : hip_fail(e, "swiglu launch");
+}
+
+// ------------------------------------------------------------------ softmax ---------
+// Row softmax over the last dim (tensor.rs:1065-1092): max, e = exp(x - max), sum, e / sum.
+// One workgroup of 512 threads per row with the row in registers (V float4 per thread),
+// so x is read once and written once.
+template <int V>
+__global__ __launch_bounds__(512) void k_softmax_row(const float* __restrict__ x,
+                                                     float* __restrict__ out, int64_t n) {
+    __shared__ float red[8];
+    const int64_t row = blockIdx.x;
+    const float4* xr = reinterpret_cast<const float4*>(x + row * n);
+    const int64_t n4 = n >> 2;
+    float4 v[V];
+    float mx = -INFINITY;
+#pragma unroll
+    for (int i = 0; i < V; i++) {
+        int64_t j = threadIdx.x + (int64_t)i * 512;
+        v[i] = j < n4 ? xr[j] : make_float4(-INFINITY, -INFINITY, -INFINITY, -INFINITY);
+        mx = fmaxf(mx, fmaxf(fmaxf(v[i].x, v[i].y), fmaxf(v[i].z, v[i].w)));
+    }
+    mx = block_max(mx, red);
+    float sum = 0.f;
+#pragma unroll
+    for (int i = 0; i < V; i++) {
+        int64_t j = threadIdx.x + (int64_t)i * 512;
+        if (j < n4) {
+            v[i].x = expf(v[i].x - mx);
+            v[i].y = expf(v[i].y - mx);
+            v[i].z = expf(v[i].z - mx);
+            v[i].w = expf(v[i].w - mx);
+            sum += (v[i].x + v[i].y) + (v[i].z + v[i].w);
+        }
+    }
+    sum = block_sum(sum, red);
+    float4* o = reinterpret_cast<float4*>(out + row * n);
+#pragma unroll
+    for (int i = 0; i < V; i++) {
+        int64_t j = threadIdx.x + (int64_t)i * 512;
+        if (j < n4) {
+            float4 r;
+            r.x = v[i].x / sum;
+            r.y = v[i].y / sum;
+            r.z = v[i].z / sum;
+            r.w = v[i].w / sum;
+            o[j] = r;
+        }
+    }
+}
+
+// strided softmax for any axis / size: one thread per (outer, inner) column, three passes
+__global__ void k_softmax_strided(const float* __restrict__ x, float* __restrict__ out,
+                                  int64_t outer, int64_t as, int64_t inner) {
+    int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (t >= outer * inner) return;
+    int64_t i = t / inner, kk = t % inner;
+    const float* xp = x + i * as * inner + kk;
+    float* op = out + i * as * inner + kk;
+    float mx = -INFINITY;
+    for (int64_t j = 0; j < as; j++) {
+        float v = xp[j * inner];
+        if (v > mx) mx = v;
+    }
+    float sum = 0.f;
+    for (int64_t j = 0; j < as; j++) {
+        float e = expf(xp[j * inner] - mx);
+        op[j * inner] = e;
+        sum += e;
+    }
+    for (int64_t j = 0; j < as; j++) op[j * inner] = op[j * inner] / sum;
+}
+
+int launch_softmax(const float* x, float* out, int64_t outer, int64_t as, int64_t inner,
+                   hipStream_t s) {
+    if (outer * as * inner == 0) return TL_HIP_OK;
+    const bool vec = inner == 1 && as % 4 == 0 && (uintptr_t)x % 16 == 0 && (uintptr_t)out % 16 == 0;
+    const int64_t per = cdiv(as / 4, 512);
+    if (vec && per <= 2)
+        k_softmax_row<2><<<outer, 512, 0, s>>>(x, out, as);
+    else if (vec && per <= 4)
+        k_softmax_row<4><<<outer, 512, 0, s>>>(x, out, as);
+    else if (vec && per <= 8)
+        k_softmax_row<8><<<outer, 512, 0, s>>>(x, out, as);
+    else if (vec && per <= 16)
+        k_softmax_row<16><<<outer, 512, 0, s>>>(x, out, as);
+    else
+        k_softmax_strided<<<cdiv(outer * inner, 256), 256, 0, s>>>(x, out, outer, as, inner);
+    hipError_t e = hipGetLastError();
+    return e == hipSuccess ? TL_HIP_OK : hip_fail(e, "softmax launch");
+}
+
+// ------------------------------------------------------------ data movement ---------
+// out[i, j, r, k] = x[i, j, k] for r < repeats (repeat_interleave, tensor.rs:1178-1200)
+__global__ void k_repeat_interleave(const float* __restrict__ x, float* __restrict__ o,
+                                    int64_t total, int64_t as, int64_t inner, int64_t rep) {
+    int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (t >= total) return;
+    int64_t kk = t % inner;
+    int64_t rest = t / inner;
+    int64_t jr = rest % (as * rep);
+    int64_t i = rest / (as * rep);
+    o[t] = x[(i * as + jr / rep) * inner + kk];
+}
+
+// generic slab copy: out[i, off + j, k] = x[i, j, k] -- narrow (tensor.rs:989-1015) and
+// cat (tensor.rs:1021-1063) are built from it.
+__global__ void k_slab_copy(const float* __restrict__ x, float* __restrict__ o, int64_t outer,
+                            int64_t in_as, int64_t in_start, int64_t len, int64_t out_as,
+                            int64_t out_start, int64_t inner) {
+    int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (t >= outer * len * inner) return;
+    int64_t kk = t % inner;
+    int64_t j = (t / inner) % len;
+    int64_t i = t / (inner * len);
+    o[(i * out_as + out_start + j) * inner + kk] = x[(i * in_as + in_start + j) * inner + kk];
+}
+
+struct TStrides {
+    int64_t out_stride[TL_HIP_MAX_RANK];  // strides of the output index space
+    int64_t in_stride[TL_HIP_MAX_RANK];   // input stride for each output dim
+    int nd;
+};
+
+__global__ void k_permute(const float* __restrict__ x, float* __restrict__ o, int64_t n,
+                          TStrides st) {
+    int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (t >= n) return;
+    int64_t rem = t, src = 0;
+    for (int d = 0; d < st.nd; d++) {
+        int64_t c = rem / st.out_stride[d];
+        rem -= c * st.out_stride[d];
+        src += c * st.in_stride[d];
+    }
+    o[t] = x[src];
+}
+
+// 2-D transpose through a 32 x 33 LDS tile (coalesced reads and writes)
+__global__ void k_transpose2d(const float* __restrict__ a, float* __restrict__ o, int64_t rows,
+                              int64_t cols) {
+    __shared__ float tile[32][33];
+    int64_t bx = (int64_t)blockIdx.x * 32, by = (int64_t)blockIdx.y * 32;
+    int tx = threadIdx.x & 31, ty = threadIdx.x >> 5;  // 256 threads: 32 x 8
+    for (int j = ty; j < 32; j += 8) {
+        int64_t r = by + j, c = bx + tx;
+        if (r < rows && c < cols) tile[j][tx] = a[r * cols + c];
+    }
+    __syncthreads();
+    for (int j = ty; j < 32; j += 8) {
+        int64_t r = bx + j, c = by + tx;  // output [cols, rows]
+        if (r < cols && c < rows) o[r * rows + c] = tile[tx][j];
+    }
+}
+
+__global__ void k_causal_mask(float* __restrict__ o, int64_t size) {
+    int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (t >= size * size) return;
+    int64_t i = t / size, j = t % size;
+    o[t] = j > i ? -INFINITY : 0.0f;
+}
+
+__global__ void k_embedding(const float* __restrict__ table, const int32_t* __restrict__ ids,
+                            float* __restrict__ o, int64_t n, int64_t dim) {
+    int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (t >= n * dim) return;
+    int64_t i = t / dim, j = t % dim;
+    o[t] = table[(int64_t)ids[i] * dim + j];
+}
+
+// ------------------------------------------------------------------- argmax ---------
+// Greedy choice (tensor.rs:1633-1637, 841-846): the left fold keeps the running best only
+// when it compares strictly greater, so the last of equal maxima wins.  For NaN-free input
+// that is the associative (max value, last index) reduction done here; if any NaN is
+// present the fold is not associative and thread 0 replays it sequentially.
+__global__ __launch_bounds__(1024) void k_argmax(const float* __restrict__ x, int64_t n,
+                                                 int32_t* __restrict__ out_idx) {
+    __shared__ float sv[16];
+    __shared__ int64_t si[16];
+    __shared__ int has_nan;
+    if (threadIdx.x == 0) has_nan = 0;
+    __syncthreads();
+    float bv = -INFINITY;
+    int64_t bi = -1;
+    int nan_seen = 0;
+    for (int64_t i = threadIdx.x; i < n; i += blockDim.x) {
+        float v = x[i];
+        if (v != v) nan_seen = 1;
+        if (bi < 0 || !(bv > v)) {  // later index wins ties (i increases per thread)
+            bv = v;
+            bi = i;
+        }
+    }
+    if (nan_seen) has_nan = 1;
+    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) {
+        float ov = __shfl_xor(bv, off, 64);
+        int64_t oi = __shfl_xor(bi, off, 64);
+        // keep the pair a fold would keep: larger value, ties -> larger index
+        bool take = oi >= 0 && (bi < 0 || ov > bv || (ov == bv && oi > bi));
+        if (take) {
+            bv = ov;
+            bi = oi;
+        }
+    }
+    if (lane == 0) {
+        sv[w] = bv;
+        si[w] = bi;
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        float fv = sv[0];
+        int64_t fi = si[0];
+        for (int i = 1; i < (int)(blockDim.x >> 6); i++) {
+            if (si[i] >= 0 && (fi < 0 || sv[i] > fv || (sv[i] == fv && si[i] > fi))) {
+                fv = sv[i];
+                fi = si[i];
+            }
+        }
+        if (has_nan) {
+            fi = 0;
+            for (int64_t i = 1; i < n; i++)
+                if (!(x[fi] > x[i])) fi = i;
+        }
+        *out_idx = (int32_t)(fi < 0 ? 0 : fi);
+    }
+}
+
+int launch_argmax(const float* x, int64_t n, int32_t* out_idx, hipStream_t s) {
+    k_argmax<<<1, 1024, 0, s>>>(x, n, out_idx);
+    hipError_t e = hipGetLastError();
+    return e == hipSuccess ? TL_HIP_OK : hip_fail(e, "argmax launch");
+}
+
+// repetition penalty (device_impl.rs:967-1001): entries flagged in `seen` get v / p when
+// v > 0, else v * p, in every row.
+__global__ void k_rep_penalty(const float* __restrict__ x, const uint8_t* __restrict__ seen,
+                              float* __restrict__ o, int64_t rows, int64_t vocab, float p) {
+    int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (t >= rows * vocab) return;
+    float v = x[t];
+    if (seen[t % vocab]) v = v > 0.0f ? v / p : v * p;
+    o[t] = v;
+}
+
+int launch_rep_penalty(const float* x, const uint8_t* seen, float* o, int64_t rows,
+                       int64_t vocab, float p, hipStream_t s) {
+    k_rep_penalty<<<cdiv(rows * vocab, 256), 256, 0, s>>>(x, seen, o, rows, vocab, p);
+    hipError_t e = hipGetLastError();
+    return e == hipSuccess ? TL_HIP_OK : hip_fail(e, "repetition penalty launch");
+}
+
+int launch_embedding(const float* table, const int32_t* ids, float* o, int64_t n, int64_t dim,
+                     hipStream_t s) {
+    if (n * dim == 0) return TL_HIP_OK;
+    k_embedding<<<cdiv(n * dim, 256), 256, 0, s>>>(table, ids, o, n, dim);
+    hipError_t e = hipGetLastError();
+    return e == hipSuccess ? TL_HIP_OK : hip_fail(e, "embedding launch");
+}
+
+int launch_apply_rope(const float* x, const float* ct, const float* st, float* out,
+                      int64_t total, int64_t hd, int64_t cos_len, int64_t sin_len, int64_t row0,
+                      int64_t vpt, hipStream_t s) {
+    if (total == 0 || hd == 0) return TL_HIP_OK;
+    int64_t np = total / 2;
+    k_apply_rope<<<cdiv(np, 256), 256, 0, s>>>(x, ct, st, out, np, hd, cos_len, sin_len, row0, vpt);
+    hipError_t e = hipGetLastError();
+    return e == hipSuccess ? TL_HIP_OK : hip_fail(e, "apply_rope launch");
+}
+
+int launch_rope_table(float* out, int64_t seq_len, int64_t dim, float base, int is_sin,
+                      hipStream_t s) {
+    int64_t n = seq_len * (dim / 2);
+    if (n == 0) return TL_HIP_OK;
+    k_rope_table<<<cdiv(n, 256), 256, 0, s>>>(out, seq_len, dim, base, is_sin);
+    hipError_t e = hipGetLastError();
+    return e == hipSuccess ? TL_HIP_OK : hip_fail(e, "rope table launch");
+}
+
+}  // namespace tlhip
+
+// =============================================================== C ABI wrappers ======
+using namespace tlhip;
+
+static const Tensor* CT(const tl_hip_tensor* h) { return reinterpret_cast<const Tensor*>(h); }
+
+static bool need(const tl_hip_tensor* a, const char* what) {
+    if (!a) {
+        set_error(TL_HIP_ERR_NULL, "NullPointerError: %s", what);
+        return false;
+    }
+    if (CT(a)->dtype != TL_HIP_F32) {
+        set_error(TL_HIP_ERR_TYPE, "TypeMismatch: %s must be f32", what);
+        return false;
+    }
+    return state() != nullptr;
+}
+
+static tl_hip_tensor* finish(Tensor* o, int rc) {
+    if (rc != TL_HIP_OK) {
+        tensor_drop(o);
+        return nullptr;
+    }
+    return H(o);
+}
+
+static int last_launch(const char* what) {
+    hipError_t e = hipGetLastError();
+    return e == hipSuccess ? TL_HIP_OK : hip_fail(e, what);
+}
+
+extern "C" {
+
+tl_hip_tensor* tl_hip_tensor_rms_norm(const tl_hip_tensor* x, const tl_hip_tensor* w, float eps) {
+    if (!need(x, "input")) return nullptr;
+    const Tensor* t = CT(x);
+    int64_t n = t->rank ? t->shape[t->rank - 1] : 1;
+    if (w) {
+        // the weight is applied by a broadcast mul (tensor.rs:549-609); only a trailing
+        // [n] (or [1, n]) weight broadcasts against every row
+        if (CT(w)->dtype != TL_HIP_F32 || CT(w)->numel != n) {
+            set_error(TL_HIP_ERR_SHAPE, "ShapeMismatch: rms_norm weight has %lld elements, last dim is %lld",
+                      (long long)CT(w)->numel, (long long)n);
+            return nullptr;
+        }
+    }
+    Tensor* o = tensor_alloc(t->shape, t->rank);
+    if (!o) return nullptr;
+    int64_t rows = n ? t->numel / n : 0;
+    return finish(o, launch_rmsnorm(t->f32(), nullptr, w ? CT(w)->f32() : nullptr, o->f32(), rows,
+                                    n, eps, 0, cur_stream()));
+}
+
+tl_hip_tensor* tl_hip_fused_rms_norm(const tl_hip_tensor* x, const tl_hip_tensor* w, float eps) {
+    if (!need(x, "input") || !need(w, "weight")) return nullptr;
+    const Tensor* t = CT(x);
+    int64_t n = t->rank ? t->shape[t->rank - 1] : 1;
+    if (CT(w)->numel < n) {
+        set_error(TL_HIP_ERR_SHAPE, "ShapeMismatch: fused_rms_norm weight shorter than last dim");
+        return nullptr;
+    }
+    Tensor* o = tensor_alloc(t->shape, t->rank);
+    if (!o) return nullptr;
+    return finish(o, launch_rmsnorm(t->f32(), nullptr, CT(w)->f32(), o->f32(), n ? t->numel / n : 0,
+                                    n, eps, 1, cur_stream()));
+}
+
+tl_hip_tensor* tl_hip_fused_add_rms_norm(const tl_hip_tensor* x, const tl_hip_tensor* r,
+                                         const tl_hip_tensor* w, float eps) {
+    if (!need(x, "input") || !need(r, "residual") || !need(w, "weight")) return nullptr;
+    const Tensor* t = CT(x);
+    if (CT(r)->numel != t->numel) {
+        set_error(TL_HIP_ERR_SHAPE, "ShapeMismatch: fused_add_rms_norm: shape mismatch");
+        return nullptr;
+    }
+    int64_t n = t->rank ? t->shape[t->rank - 1] : 1;
+    if (CT(w)->numel < n) {
+        set_error(TL_HIP_ERR_SHAPE, "ShapeMismatch: fused_add_rms_norm weight shorter than last dim");
+        return nullptr;
+    }
+    Tensor* o = tensor_alloc(t->shape, t->rank);
+    if (!o) return nullptr;
+    return finish(o, launch_rmsnorm(t->f32(), CT(r)->f32(), CT(w)->f32(), o->f32(),
+                                    n ? t->numel / n : 0, n, eps, 1, cur_stream()));
+}
+
+static tl_hip_tensor* rope_table(int64_t dim, int64_t seq_len, float base, int is_sin) {
+    if (!state()) return nullptr;
+    if (dim < 0 || seq_len < 0) {
+        set_error(TL_HIP_ERR_ARG, "ArgumentError: negative rope table size");
+        return nullptr;
+    }
+    int64_t shape[2] = {seq_len, dim};
+    Tensor* o = tensor_alloc(shape, 2);
+    if (!o) return nullptr;
+    if (dim % 2 && o->numel) (void)hipMemsetAsync(o->data, 0, o->numel * 4, cur_stream());
+    return finish(o, launch_rope_table(o->f32(), seq_len, dim, base, is_sin, cur_stream()));
+}
+
+tl_hip_tensor* tl_hip_tensor_rope_new_cos(int64_t dim, int64_t seq_len, float base) {
+    return rope_table(dim, seq_len, base, 0);
+}
+
+tl_hip_tensor* tl_hip_tensor_rope_new_sin(int64_t dim, int64_t seq_len, float base) {
+    return rope_table(dim, seq_len, base, 1);
+}
+
+static tl_hip_tensor* rope(const tl_hip_tensor* x, const tl_hip_tensor* c, const tl_hip_tensor* s,
+                           int64_t row0, int64_t vpt) {
+    if (!need(x, "input") || !need(c, "cos table") || !need(s, "sin table")) return nullptr;
+    const Tensor* t = CT(x);
+    int64_t hd = t->rank ? t->shape[t->rank - 1] : 0;
+    if (hd % 2) {
+        set_error(TL_HIP_ERR_SHAPE, "ShapeMismatch: apply_rope needs an even head_dim, got %lld",
+                  (long long)hd);
+        return nullptr;
+    }
+    if (row0 < 0 || vpt < 0) {
+        set_error(TL_HIP_ERR_ARG, "ArgumentError: negative position");
+        return nullptr;
+    }
+    Tensor* o = tensor_alloc(t->shape, t->rank);
+    if (!o) return nullptr;
+    return finish(o, launch_apply_rope(t->f32(), CT(c)->f32(), CT(s)->f32(), o->f32(), t->numel, hd,
+                                       CT(c)->numel, CT(s)->numel, row0, vpt, cur_stream()));
+}
+
+tl_hip_tensor* tl_hip_tensor_apply_rope(const tl_hip_tensor* x, const tl_hip_tensor* c,
+                                        const tl_hip_tensor* s) {
+    return rope(x, c, s, 0, 0);
+}
+
+tl_hip_tensor* tl_hip_tensor_apply_rope_pos(const tl_hip_tensor* x, const tl_hip_tensor* c,
+                                            const tl_hip_tensor* s, int64_t pos0, int64_t vpt) {
+    if (vpt <= 0) {
+        set_error(TL_HIP_ERR_ARG, "ArgumentError: vectors_per_token must be positive");
+        return nullptr;
+    }
+    return rope(x, c, s, pos0, vpt);
+}
+
+tl_hip_tensor* tl_hip_tensor_silu(const tl_hip_tensor* x) {
+    if (!need(x, "input")) return nullptr;
+    const Tensor* t = CT(x);
+    Tensor* o = tensor_alloc(t->shape, t->rank);
+    if (!o) return nullptr;
+    if (t->numel) k_silu<<<cdiv(t->numel, 256), 256, 0, cur_stream()>>>(t->f32(), o->f32(), t->numel);
+    return finish(o, last_launch("silu launch"));
+}
+
+tl_hip_tensor* tl_hip_fused_silu_mul(const tl_hip_tensor* g, const tl_hip_tensor* u) {
+    if (!need(g, "gate") || !need(u, "up")) return nullptr;
+    if (CT(g)->numel != CT(u)->numel) {
+        set_error(TL_HIP_ERR_SHAPE, "ShapeMismatch: fused_silu_mul: shape mismatch");
+        return nullptr;
+    }
+    const Tensor* t = CT(g);
+    Tensor* o = tensor_alloc(t->shape, t->rank);
+    if (!o) return nullptr;
+    return finish(o, launch_swiglu(t->f32(), CT(u)->f32(), o->f32(), t->numel, 1, cur_stream()));
+}
+
+static tl_hip_tensor* binary(const tl_hip_tensor* ah, const tl_hip_tensor* bh, int op) {
+    if (!need(ah, "lhs") || !need(bh, "rhs")) return nullptr;
+    const Tensor* a = CT(ah);
+    const Tensor* b = CT(bh);
+    if (a->numel == 0 || b->numel == 0) {  // tensor.rs:550-559: empty -> shape [0]
+        int64_t z = 0;
+        return H(tensor_alloc(&z, 1));
+    }
+    int nd = a->rank > b->rank ? a->rank : b->rank;
+    int64_t as[TL_HIP_MAX_RANK], bs[TL_HIP_MAX_RANK], os[TL_HIP_MAX_RANK];
+    for (int d = 0; d < nd; d++) {
+        as[d] = d < nd - a->rank ? 1 : a->shape[d - (nd - a->rank)];
+        bs[d] = d < nd - b->rank ? 1 : b->shape[d - (nd - b->rank)];
+        if (as[d] != bs[d] && as[d] != 1 && bs[d] != 1) {
+            set_error(TL_HIP_ERR_SHAPE,
+                      "ShapeMismatch: Operands could not be broadcast together (dim %d: %lld vs %lld)",
+                      d, (long long)as[d], (long long)bs[d]);
+            return nullptr;
+        }
+        os[d] = as[d] > bs[d] ? as[d] : bs[d];
+    }
+    Tensor* o = tensor_alloc(os, nd);
+    if (!o) return nullptr;
+    hipStream_t s = cur_stream();
+    if (a->numel == o->numel && b->numel == o->numel) {
+        k_binop_same<<<cdiv(o->numel, 256), 256, 0, s>>>(a->f32(), b->f32(), o->f32(), o->numel, op);
+    } else {
+        BStrides st;
+        st.nd = nd;
+        int64_t so = 1, sa = 1, sb = 1;
+        for (int d = nd - 1; d >= 0; d--) {
+            st.out_stride[d] = so;
+            st.a_stride[d] = as[d] == 1 ? 0 : sa;
+            st.b_stride[d] = bs[d] == 1 ? 0 : sb;
+            so *= os[d];
+            sa *= as[d];
+            sb *= bs[d];
+        }
+        k_binop_bcast<<<cdiv(o->numel, 256), 256, 0, s>>>(a->f32(), b->f32(), o->f32(), o->numel, op, st);
+    }
+    return finish(o, last_launch("binop launch"));
+}
+
+tl_hip_tensor* tl_hip_tensor_add(const tl_hip_tensor* a, const tl_hip_tensor* b) { return binary(a, b, 0); }
+tl_hip_tensor* tl_hip_tensor_mul(const tl_hip_tensor* a, const tl_hip_tensor* b) { return binary(a, b, 1); }
+tl_hip_tensor* tl_hip_tensor_sub(const tl_hip_tensor* a, const tl_hip_tensor* b) { return binary(a, b, 2); }
+tl_hip_tensor* tl_hip_tensor_div(const tl_hip_tensor* a, const tl_hip_tensor* b) { return binary(a, b, 3); }
+
+tl_hip_tensor* tl_hip_tensor_scale(const tl_hip_tensor* x, float s) {
+    if (!need(x, "input")) return nullptr;
+    const Tensor* t = CT(x);
+    Tensor* o = tensor_alloc(t->shape, t->rank);
+    if (!o) return nullptr;
+    if (t->numel) k_scale<<<cdiv(t->numel, 256), 256, 0, cur_stream()>>>(t->f32(), o->f32(), t->numel, s);
+    return finish(o, last_launch("scale launch"));
+}
+
+tl_hip_tensor* tl_hip_tensor_softmax(const tl_hip_tensor* x, int64_t dim) {
+    if (!need(x, "input")) return nullptr;
+    const Tensor* t = CT(x);
+    int64_t ax = dim < 0 ? dim + t->rank : dim;
+    if (ax < 0 || ax >= t->rank) {
+        set_error(TL_HIP_ERR_SHAPE, "ShapeMismatch: softmax dim %lld out of range for rank %d",
+                  (long long)dim, t->rank);
+        return nullptr;
+    }
+    int64_t outer = 1, inner = 1;
+    for (int d = 0; d < ax; d++) outer *= t->shape[d];
+    for (int d = ax + 1; d < t->rank; d++) inner *= t->shape[d];
+    Tensor* o = tensor_alloc(t->shape, t->rank);
+    if (!o) return nullptr;
+    return finish(o, launch_softmax(t->f32(), o->f32(), outer, t->shape[ax], inner, cur_stream()));
+}
+
+tl_hip_tensor* tl_hip_tensor_new_causal_mask(int64_t size) {
+    if (!state()) return nullptr;
+    if (size < 0) {
+        set_error(TL_HIP_ERR_ARG, "ArgumentError: negative mask size");
+        return nullptr;
+    }
+    int64_t shape[2] = {size, size};
+    Tensor* o = tensor_alloc(shape, 2);
+    if (!o) return nullptr;
+    if (size) k_causal_mask<<<cdiv(size * size, 256), 256, 0, cur_stream()>>>(o->f32(), size);
+    return finish(o, last_launch("causal mask launch"));
+}
+
+tl_hip_tensor* tl_hip_tensor_narrow(const tl_hip_tensor* x, int64_t dim, int64_t start, int64_t len) {
+    if (!need(x, "input")) return nullptr;
+    const Tensor* t = CT(x);
+    if (dim < 0 || dim >= t->rank) {
+        set_error(TL_HIP_ERR_SHAPE, "ShapeMismatch: Slice axis %lld out of bounds for tensor of rank %d",
+                  (long long)dim, t->rank);
+        return nullptr;
+    }
+    if (start < 0 || len < 0 || start + len > t->shape[dim]) {
+        set_error(TL_HIP_ERR_SHAPE, "ShapeMismatch: Slice range %lld:%lld out of bounds for axis %lld of size %lld",
+                  (long long)start, (long long)(start + len), (long long)dim, (long long)t->shape[dim]);
+        return nullptr;
+    }
+    int64_t shape[TL_HIP_MAX_RANK];
+    for (int d = 0; d < t->rank; d++) shape[d] = t->shape[d];
+    shape[dim] = len;
+    Tensor* o = tensor_alloc(shape, t->rank);
+    if (!o) return nullptr;
+    int64_t outer = 1, inner = 1;
+    for (int d = 0; d < dim; d++) outer *= t->shape[d];
+    for (int d = dim + 1; d < t->rank; d++) inner *= t->shape[d];
+    if (o->numel)
+        k_slab_copy<<<cdiv(o->numel, 256), 256, 0, cur_stream()>>>(t->f32(), o->f32(), outer, t->shape[dim],
+                                                                    start, len, len, 0, inner);
+    return finish(o, last_launch("narrow launch"));
+}
+
+tl_hip_tensor* tl_hip_tensor_cat(const tl_hip_tensor* ah, const tl_hip_tensor* bh, int64_t dim) {
+    if (!need(ah, "lhs") || !need(bh, "rhs")) return nullptr;
+    const Tensor* a = CT(ah);
+    const Tensor* b = CT(bh);
+    if (dim < 0 || dim >= a->rank) {
+        set_error(TL_HIP_ERR_SHAPE, "ShapeMismatch: Cat axis %lld out of bounds", (long long)dim);
+        return nullptr;
+    }
+    if (b->rank != a->rank) {
+        set_error(TL_HIP_ERR_SHAPE, "ShapeMismatch: Tensor 1 has different rank");
+        return nullptr;
+    }
+    for (int d = 0; d < a->rank; d++)
+        if (d != dim && a->shape[d] != b->shape[d]) {
+            set_error(TL_HIP_ERR_SHAPE, "ShapeMismatch: Tensor 1 has mismatching shape at dim %d (expected %lld, got %lld)",
+                      d, (long long)a->shape[d], (long long)b->shape[d]);
+            return nullptr;
+        }
+    int64_t shape[TL_HIP_MAX_RANK];
+    for (int d = 0; d < a->rank; d++) shape[d] = a->shape[d];
+    shape[dim] = a->shape[dim] + b->shape[dim];
+    Tensor* o = tensor_alloc(shape, a->rank);
+    if (!o) return nullptr;
+    int64_t outer = 1, inner = 1;
+    for (int d = 0; d < dim; d++) outer *= a->shape[d];
+    for (int d = dim + 1; d < a->rank; d++) inner *= a->shape[d];
+    hipStream_t s = cur_stream();
+    if (a->numel)
+        k_slab_copy<<<cdiv(a->numel, 256), 256, 0, s>>>(a->f32(), o->f32(), outer, a->shape[dim], 0,
+                                                       a->shape[dim], shape[dim], 0, inner);
+    if (b->numel)
+        k_slab_copy<<<cdiv(b->numel, 256), 256, 0, s>>>(b->f32(), o->f32(), outer, b->shape[dim], 0,
+                                                       b->shape[dim], shape[dim], a->shape[dim], inner);
+    return finish(o, last_launch("cat launch"));
+}
+
+tl_hip_tensor* tl_hip_tensor_repeat_interleave(const tl_hip_tensor* x, int64_t repeats, int64_t dim) {
+    if (!need(x, "input")) return nullptr;
+    const Tensor* t = CT(x);
+    if (dim < 0 || dim >= t->rank) {
+        set_error(TL_HIP_ERR_SHAPE, "ShapeMismatch: Axis %lld out of bounds for repeat_interleave (rank %d)",
+                  (long long)dim, t->rank);
+        return nullptr;
+    }
+    if (repeats < 0) {
+        set_error(TL_HIP_ERR_ARG, "ArgumentError: negative repeats");
+        return nullptr;
+    }
+    int64_t shape[TL_HIP_MAX_RANK];
+    for (int d = 0; d < t->rank; d++) shape[d] = t->shape[d];
+    shape[dim] *= repeats;
+    Tensor* o = tensor_alloc(shape, t->rank);
+    if (!o) return nullptr;
+    int64_t inner = 1;
+    for (int d = dim + 1; d < t->rank; d++) inner *= t->shape[d];
+    if (o->numel)
+        k_repeat_interleave<<<cdiv(o->numel, 256), 256, 0, cur_stream()>>>(t->f32(), o->f32(), o->numel,
+                                                                           t->shape[dim], inner, repeats);
+    return finish(o, last_launch("repeat_interleave launch"));
+}
+
+tl_hip_tensor* tl_hip_tensor_transpose(const tl_hip_tensor* x, int64_t d0, int64_t d1) {
+    if (!need(x, "input")) return nullptr;
+    const Tensor* t = CT(x);
+    if (t->rank < 2) return tl_hip_tensor_reshape(x, t->shape, t->rank);  // tensor.rs:903-905
+    if (d0 < 0 || d1 < 0 || d0 >= t->rank || d1 >= t->rank) {
+        set_error(TL_HIP_ERR_SHAPE, "ShapeMismatch: Transpose dims %lld and %lld are out of bounds for tensor of rank %d",
+                  (long long)d0, (long long)d1, t->rank);
+        return nullptr;
+    }
+    int64_t shape[TL_HIP_MAX_RANK], in_stride[TL_HIP_MAX_RANK];
+    int64_t st = 1;
+    for (int d = t->rank - 1; d >= 0; d--) {
+        in_stride[d] = st;
+        st *= t->shape[d];
+    }
+    for (int d = 0; d < t->rank; d++) shape[d] = t->shape[d];
+    shape[d0] = t->shape[d1];
+    shape[d1] = t->shape[d0];
+    Tensor* o = tensor_alloc(shape, t->rank);
+    if (!o) return nullptr;
+    TStrides ts;
+    ts.nd = t->rank;
+    int64_t so = 1;
+    for (int d = t->rank - 1; d >= 0; d--) {
+        ts.out_stride[d] = so;
+        so *= shape[d];
+        int src_dim = d == d0 ? (int)d1 : (d == d1 ? (int)d0 : d);
+        ts.in_stride[d] = in_stride[src_dim];
+    }
+    if (o->numel) k_permute<<<cdiv(o->numel, 256), 256, 0, cur_stream()>>>(t->f32(), o->f32(), o->numel, ts);
+    return finish(o, last_launch("transpose launch"));
+}
+
+tl_hip_tensor* tl_hip_tensor_transpose_2d(const tl_hip_tensor* x) {
+    if (!need(x, "input")) return nullptr;
+    const Tensor* t = CT(x);
+    if (t->rank != 2) {
+        set_error(TL_HIP_ERR_SHAPE, "ShapeMismatch: transpose_2d needs a 2-D tensor, got rank %d", t->rank);
+        return nullptr;
+    }
+    int64_t shape[2] = {t->shape[1], t->shape[0]};
+    Tensor* o = tensor_alloc(shape, 2);
+    if (!o) return nullptr;
+    if (o->numel) {
+        dim3 grid((unsigned)cdiv(t->shape[1], 32), (unsigned)cdiv(t->shape[0], 32));
+        k_transpose2d<<<grid, 256, 0, cur_stream()>>>(t->f32(), o->f32(), t->shape[0], t->shape[1]);
+    }
+    return finish(o, last_launch("transpose_2d launch"));
+}
+
+tl_hip_tensor* tl_hip_tensor_matmul(const tl_hip_tensor* ah, const tl_hip_tensor* bh) {
+    if (!need(ah, "lhs") || !need(bh, "rhs")) return nullptr;
+    const Tensor* a = CT(ah);
+    const Tensor* b = CT(bh);
+    if (a->rank < 1 || b->rank < 1) {
+        set_error(TL_HIP_ERR_SHAPE, "ShapeMismatch: Matmul requires at least 1D tensors");
+        return nullptr;
+    }
+    int64_t m = a->rank >= 2 ? a->shape[a->rank - 2] : 1, k = a->shape[a->rank - 1];
+    int64_t k2 = b->rank >= 2 ? b->shape[b->rank - 2] : b->shape[0];
+    int64_t n = b->rank >= 2 ? b->shape[b->rank - 1] : 1;
+    if (k != k2) {
+        set_error(TL_HIP_ERR_SHAPE, "ShapeMismatch: Matmul shape mismatch (inner dims %lld vs %lld)",
+                  (long long)k, (long long)k2);
+        return nullptr;
+    }
+    int64_t batch = 1;
+    for (int d = 0; d < a->rank - 2; d++) batch *= a->shape[d];
+    int64_t b_batched = b->rank > 2;
+    if (b_batched && b->numel != batch * k * n) {
+        // matmul_impl indexes B batch b at b * k * n (tensor.rs:1285-1288)
+        set_error(TL_HIP_ERR_SHAPE, "ShapeMismatch: batched rhs holds %lld elements, lhs batch needs %lld",
+                  (long long)b->numel, (long long)(batch * k * n));
+        return nullptr;
+    }
+    int64_t shape[TL_HIP_MAX_RANK];
+    int r = 0;
+    for (int d = 0; d < a->rank - 2; d++) shape[r++] = a->shape[d];
+    shape[r++] = m;
+    if (b->rank >= 2) shape[r++] = n;
+    Tensor* o = tensor_alloc(shape, r);
+    if (!o) return nullptr;
+    if (k == 0) {
+        if (o->numel) (void)hipMemsetAsync(o->data, 0, o->numel * 4, cur_stream());
+        return H(o);
+    }
+    return finish(o, launch_matmul_f32(a->f32(), b->f32(), o->f32(), batch, m, k, n, m * k,
+                                       b_batched ? k * n : 0, cur_stream()));
+}
+
+tl_hip_tensor* tl_hip_tensor_embedding(const tl_hip_tensor* wh, const tl_hip_tensor* ih) {
+    if (!need(wh, "weight") || !need(ih, "indices")) return nullptr;
+    const Tensor* w = CT(wh);
+    const Tensor* ids = CT(ih);
+    int64_t vocab = w->rank ? w->shape[0] : 0;
+    int64_t dim = w->rank > 1 ? w->shape[1] : 1;
+    std::vector<float> hid(ids->numel);
+    if (tl_hip_tensor_to_host(ih, hid.data(), ids->numel) != TL_HIP_OK) return nullptr;
+    std::vector<int32_t> iid(ids->numel);
+    for (int64_t i = 0; i < ids->numel; i++) {
+        float f = hid[i];
+        // `as i64` truncates toward zero, saturating (NaN -> 0)
+        int64_t id = f != f ? 0 : (f >= 9.2e18f ? INT64_MAX : (f <= -9.2e18f ? INT64_MIN : (int64_t)f));
+        if (id < 0 || id >= vocab) {
+            set_error(TL_HIP_ERR_INDEX, "IndexOutOfBounds: Embedding index %lld out of range for vocab size %lld",
+                      (long long)id, (long long)vocab);
+            return nullptr;
+        }
+        iid[i] = (int32_t)id;
+    }
+    int64_t shape[TL_HIP_MAX_RANK];
+    if (ids->rank + 1 > TL_HIP_MAX_RANK) {
+        set_error(TL_HIP_ERR_ARG, "ArgumentError: indices rank too large");
+        return nullptr;
+    }
+    for (int d = 0; d < ids->rank; d++) shape[d] = ids->shape[d];
+    shape[ids->rank] = dim;
+    Tensor* o = tensor_alloc(shape, ids->rank + 1);
+    if (!o) return nullptr;
+    if (o->numel == 0) return H(o);
+    int32_t* dids = (int32_t*)dev_alloc(iid.size() * 4);
+    if (!dids) {
+        tensor_drop(o);
+        return nullptr;
+    }
+    hipStream_t s = cur_stream();
+    hipError_t e = hipMemcpyAsync(dids, iid.data(), iid.size() * 4, hipMemcpyHostToDevice, s);
+    int rc = e == hipSuccess ? launch_embedding(w->f32(), dids, o->f32(), ids->numel, dim, s)
+                             : hip_fail(e, "hipMemcpyAsync(ids)");
+    if (rc == TL_HIP_OK) {
+        e = hipStreamSynchronize(s);  // iid (host) must outlive the copy
+        if (e != hipSuccess) rc = hip_fail(e, "hipStreamSynchronize");
+    }
+    dev_free(dids);
+    return finish(o, rc);
+}
+
+int64_t tl_hip_tensor_argmax_all(const tl_hip_tensor* x) {
+    if (!need(x, "input")) return -1;
+    const Tensor* t = CT(x);
+    if (t->numel == 0) return 0;  // unwrap_or(0), tensor.rs:845
+    int32_t* d = (int32_t*)dev_alloc(4);
+    if (!d) return -1;
+    hipStream_t s = cur_stream();
+    int32_t h = 0;
+    int rc = launch_argmax(t->f32(), t->numel, d, s);
+    if (rc == TL_HIP_OK) {
+        hipError_t e = hipMemcpyAsync(&h, d, 4, hipMemcpyDeviceToHost, s);
+        if (e == hipSuccess) e = hipStreamSynchronize(s);
+        if (e != hipSuccess) rc = hip_fail(e, "argmax readback");
+    }
+    dev_free(d);
+    return rc == TL_HIP_OK ? (int64_t)h : -1;
+}
+
+tl_hip_tensor* tl_hip_tensor_sample(const tl_hip_tensor* x, float temp, float top_p) {
+    (void)top_p;
+    if (!need(x, "logits")) return nullptr;
+    if (CT(x)->numel == 0) {
+        set_error(TL_HIP_ERR_INTERNAL, "InternalError: Empty tensor for sampling");
+        return nullptr;
+    }
+    if (temp > 0.0f) {
+        set_error(TL_HIP_ERR_ARG, "ArgumentError: only greedy sampling (temp <= 0) is provided");
+        return nullptr;
+    }
+    int64_t idx = tl_hip_tensor_argmax_all(x);
+    if (idx < 0) return nullptr;
+    float v = (float)idx;
+    int64_t one = 1;
+    return tl_hip_tensor_new(&v, &one, 1);
+}
+
+tl_hip_tensor* tl_hip_tensor_repetition_penalty(const tl_hip_tensor* lh, const tl_hip_tensor* th,
+                                                double penalty) {
+    if (!need(lh, "logits") || !need(th, "tokens")) return nullptr;
+    const Tensor* l = CT(lh);
+    const Tensor* tk = CT(th);
+    int64_t vocab = l->rank ? l->shape[l->rank - 1] : 1;
+    int64_t rows = vocab ? l->numel / vocab : 0;
+    std::vector<float> tok(tk->numel);
+    if (tk->numel && tl_hip_tensor_to_host(th, tok.data(), tk->numel) != TL_HIP_OK) return nullptr;
+    std::vector<uint8_t> seen(vocab ? vocab : 1, 0);
+    for (float f : tok) {
+        // `as usize` saturates: NaN and negatives give 0
+        uint64_t id = !(f >= 0.0f) ? 0 : (f >= 1.8e19f ? UINT64_MAX : (uint64_t)f);
+        if (id < (uint64_t)vocab) seen[id] = 1;
+    }
+    Tensor* o = tensor_alloc(l->shape, l->rank);
+    if (!o) return nullptr;
+    if (l->numel == 0) return H(o);
+    uint8_t* dseen = (uint8_t*)dev_alloc(seen.size());
+    if (!dseen) {
+        tensor_drop(o);
+        return nullptr;
+    }
+    hipStream_t s = cur_stream();
+    hipError_t e = hipMemcpyAsync(dseen, seen.data(), seen.size(), hipMemcpyHostToDevice, s);
+    int rc = e == hipSuccess ? launch_rep_penalty(l->f32(), dseen, o->f32(), rows, vocab, (float)penalty, s)
+                             : hip_fail(e, "hipMemcpyAsync(seen)");
+    if (rc == TL_HIP_OK) {
+        e = hipStreamSynchronize(s);
+        if (e != hipSuccess) rc = hip_fail(e, "hipStreamSynchronize");
+    }
+    dev_free(dseen);
+    return finish(o, rc);
+}
+
+}  // extern "C"
