@@ -159,9 +159,14 @@ __global__ void k_rope_table(float* __restrict__ out, int64_t seq_len, int64_t d
     int64_t half = dim / 2;
     if (t >= seq_len * half) return;
     int64_t pos = t / half, i = t % half;
-    float freq = 1.0f / powf(base, 2.0f * (float)i / (float)dim);
+    // f32 operation sequence of ffi.rs:2598-2601; pow / cos / sin are evaluated in double and
+    // rounded once, i.e. correctly rounded f32 results (what the host libm returns for all
+    // but rare halfway cases) -- the angle pos * freq amplifies any ulp difference in freq
+    float e = 2.0f * (float)i / (float)dim;
+    float r = (float)pow((double)base, (double)e);
+    float freq = 1.0f / r;
     float a = (float)pos * freq;
-    float v = is_sin ? sinf(a) : cosf(a);
+    float v = is_sin ? (float)sin((double)a) : (float)cos((double)a);
     out[pos * dim + 2 * i] = v;
     out[pos * dim + 2 * i + 1] = v;
 }
