@@ -54,6 +54,9 @@ def bench_matvec(dev, launches=340, copies=34):
             raise RuntimeError(lib.tl_hip_last_error())
     dev.synchronize()
     e0, e1 = lib.tl_hip_event_create(), lib.tl_hip_event_create()
+    # the stall keeps the GPU busy while the host enqueues every timed launch, so the events
+    # measure back-to-back GPU execution, not the host's launch rate
+    lib.tl_hip_stall(20000)
     lib.tl_hip_event_record(e0)
     for i in range(launches):
         lib.tl_hip_launch_quant_matvec(hs[i % copies], C.c_void_p(x.data_ptr), C.c_void_p(y.data_ptr), 1, stream)
@@ -118,6 +121,7 @@ def main():
     ap.add_argument("--prompt", type=int, default=512)
     ap.add_argument("--kv", choices=["f16", "f32"], default="f16")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-graph", action="store_true", help="eager launches instead of hipGraph replay")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU: this build has no multi-GPU path (every box has one GPU); "
@@ -151,11 +155,11 @@ def main():
     prefill_s = time.perf_counter() - t0
     first = model.sample_greedy(1.0, prompt)
     log(f"[bench] prefill {args.prompt} tokens: {prefill_s * 1e3:.1f} ms")
-    warm = model.generate(first, args.warmup, use_graph=True) if args.warmup else np.array([first])
+    warm = model.generate(first, args.warmup, use_graph=not args.no_graph) if args.warmup else np.array([first])
     nxt = int(warm[-1]) if args.warmup else first
     dev.synchronize()
     t0 = time.perf_counter()
-    model.generate(nxt, args.steps, use_graph=True)  # ends with a stream synchronize
+    model.generate(nxt, args.steps, use_graph=not args.no_graph)  # ends with a stream synchronize
     dev.synchronize()
     decode_s = time.perf_counter() - t0
     tok_s = args.steps / decode_s

@@ -75,6 +75,10 @@ void* tl_hip_event_create(void);
 int tl_hip_event_record(void* ev);
 int tl_hip_event_elapsed_ms(void* start, void* stop, float* ms);
 int tl_hip_event_destroy(void* ev);
+/* Enqueues a one-wavefront kernel that idles for `us` microseconds (at most 100000) on the
+ * library stream, so that work enqueued behind it is timed back-to-back on the GPU rather
+ * than at the host's launch rate.  Timing plumbing; no reference counterpart. */
+int tl_hip_stall(uint32_t us);
 
 /* ---------------------------------------------------------------- tensors -------- */
 /* IDevice::tensor_new (crates/tl_backend/src/device.rs:21-26): f32 host data -> device. */

@@ -35,6 +35,7 @@ PROTOS = {
     "tl_hip_event_record": (i32, [P]),
     "tl_hip_event_elapsed_ms": (i32, [P, P, f32p]),
     "tl_hip_event_destroy": (i32, [P]),
+    "tl_hip_stall": (i32, [C.c_uint32]),
     "tl_hip_tensor_new": (P, [f32p, i64p, i32]),
     "tl_hip_tensor_new_f16": (P, [u16p, i64p, i32]),
     "tl_hip_tensor_zeros": (P, [i64p, i32, i32]),

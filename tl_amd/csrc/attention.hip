@@ -1,15 +1,19 @@
 // Single-query decode attention with grouped KV heads over a KV cache (f16 or f32),
-// split along the cached length (flash-decoding) so one token at batch 1 still fills the
-// GPU.  Replaces the chatbot's transpose / cat_4d / repeat_interleave / matmul_4d / scale /
-// softmax / matmul_4d chain (examples/apps/tinyllama/chatbot.tl:63-87) for sl = 1: K and V
-// are read once, in place, and the Hq/Hkv query heads of a group share every K/V row that
-// is loaded (no repeat_interleave copy).
+// split along the cached length (flash-decoding) so one token at batch 1 still spreads over
+// many CUs.  Replaces the chatbot's transpose / cat_4d / repeat_interleave / matmul_4d /
+// scale / softmax / matmul_4d chain (examples/apps/tinyllama/chatbot.tl:63-87): K and V are
+// read once, in place, and the Hq/Hkv query heads of a group share every K/V row loaded
+// (no repeat_interleave copy).
 //
-// Pass 1 (k_attn_partial): workgroup = (split, kv head, batch), 4 wavefronts.  Eight lanes
-// share one cache row (each owns D/8 consecutive dims), so a wavefront covers 8 positions
-// per load instruction.  Scores of the chunk go to LDS, then each head's chunk max / exp-sum
-// is formed and the exp-weighted V rows are accumulated.  Pass 2 (k_attn_combine) merges
-// the per-split (max, sum, o) triples.  All arithmetic is f32.
+// One kernel: workgroup = (split, kv head, batch item), 4 wavefronts.  Eight lanes share a
+// cache row (each owns D/8 consecutive dims), so a wavefront covers 8 positions per load
+// instruction and a workgroup 32.  The K and V rows of the first two 32-position steps are
+// requested at kernel start, so the chunk's memory latency overlaps the q load and the
+// score pass.  Scores go to LDS, each head's chunk max and exp-sum are formed, the
+// exp-weighted V rows are accumulated, and the (o, max, sum) record is written.  The last
+// workgroup of a (batch, kv head) to finish -- an arrival counter, no waiting -- merges the
+// records: out = sum_s o_s e^(m_s - M) / sum_s l_s e^(m_s - M).  A single split writes its
+// result directly.  All arithmetic is f32.
 #include "internal.h"
 
 namespace tlhip {
@@ -19,7 +23,6 @@ struct KVLoad;
 
 template <>
 struct KVLoad<__half> {
-    // DL consecutive f16 -> f32
     template <int DL>
     __device__ static void load(const __half* p, float* out) {
         static_assert(DL % 8 == 0, "f16 rows are read 16 bytes at a time");
@@ -54,6 +57,7 @@ struct KVLoad<float> {
 };
 
 constexpr int ATT_MAX_CHUNK = 1024;
+constexpr int ATT_PF = 2;  // 32-position steps whose K/V rows are requested up front
 
 // Cached length of batch item b: (len_dev ? *len_dev + len_add : L) + b * len_step.
 // Decode uses len_step 0; a causal prefill of n queries over one shared cache
@@ -67,168 +71,201 @@ struct AttnLen {
     }
 };
 
+struct AttnArgs {
+    const float* q;  // [B, Hq, D]
+    const void* k;   // [B?, Hkv, lmax, D]
+    const void* v;
+    float* out;      // [B, Hq, D]
+    float* ws;       // [B, Hkv, nsplit, G, D + 2]
+    int32_t* counter;  // [B, Hkv], zero between launches
+    int hkv;
+    int64_t lmax, kv_bstride;
+    AttnLen len;
+    int chunk, nsplit;
+    float scale;
+};
+
 template <int D, int G, typename KVT>
-__global__ __launch_bounds__(256) void k_attn_partial(const float* __restrict__ q,
-                                                      const KVT* __restrict__ kc,
-                                                      const KVT* __restrict__ vc,
-                                                      float* __restrict__ ws, int hkv,
-                                                      int64_t lmax, int64_t kv_bstride,
-                                                      AttnLen len, int chunk, int nsplit,
-                                                      float scale) {
+__global__ __launch_bounds__(256) void k_attn(AttnArgs a) {
     constexpr int DL = D / 8;  // dims per lane
     __shared__ float sc[G][ATT_MAX_CHUNK];
     __shared__ float stat[G][2];
     __shared__ float part[4][G][D];
+    __shared__ int s_last;
     const int split = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int grp = lane >> 3, sub = lane & 7;
-    int64_t L = len.of(b);
-    if (L > lmax) L = lmax;
-    const int64_t p0 = (int64_t)split * chunk;
-    const int64_t p1 = p0 + chunk < L ? p0 + chunk : (L > p0 ? L : p0);
-    const int hq = hkv * G;
-    const KVT* kb = kc + (int64_t)b * kv_bstride + (int64_t)h * lmax * D;
-    const KVT* vb = vc + (int64_t)b * kv_bstride + (int64_t)h * lmax * D;
+    int64_t L = a.len.of(b);
+    if (L > a.lmax) L = a.lmax;
+    const int64_t p0 = (int64_t)split * a.chunk;
+    const int64_t p1 = p0 + a.chunk < L ? p0 + a.chunk : (L > p0 ? L : p0);
+    const int hq = a.hkv * G;
+    const KVT* kb = reinterpret_cast<const KVT*>(a.k) + (int64_t)b * a.kv_bstride + (int64_t)h * a.lmax * D;
+    const KVT* vb = reinterpret_cast<const KVT*>(a.v) + (int64_t)b * a.kv_bstride + (int64_t)h * a.lmax * D;
+    const int64_t rec0 = (((int64_t)b * a.hkv + h) * a.nsplit) * G * (D + 2);
 
-    // q slices of the group's heads for this lane's dims
-    float qv[G][DL];
+    if (p0 < p1) {
+        // K / V rows of the first steps, then q
+        float kpre[ATT_PF][DL], vpre[ATT_PF][DL];
 #pragma unroll
-    for (int g = 0; g < G; g++) {
-        const float* qp = q + ((int64_t)b * hq + h * G + g) * D + sub * DL;
-#pragma unroll
-        for (int i = 0; i < DL; i += 4) {
-            float4 t = *reinterpret_cast<const float4*>(qp + i);
-            qv[g][i] = t.x;
-            qv[g][i + 1] = t.y;
-            qv[g][i + 2] = t.z;
-            qv[g][i + 3] = t.w;
+        for (int it = 0; it < ATT_PF; it++) {
+            int64_t p = p0 + it * 32 + wave * 8 + grp;
+            int64_t pc = p < p1 ? p : p1 - 1;
+            KVLoad<KVT>::template load<DL>(kb + pc * D + sub * DL, kpre[it]);
+            KVLoad<KVT>::template load<DL>(vb + pc * D + sub * DL, vpre[it]);
         }
-    }
-    // ---- scores
-    for (int64_t base = p0; base < p1; base += 32) {
-        int64_t p = base + wave * 8 + grp;
-        int64_t pc = p < p1 ? p : p1 - 1;  // clamp: loads stay in bounds
-        float kv[DL];
-        KVLoad<KVT>::template load<DL>(kb + pc * D + sub * DL, kv);
+        float qv[G][DL];
 #pragma unroll
         for (int g = 0; g < G; g++) {
-            float s = 0.f;
+            const float* qp = a.q + ((int64_t)b * hq + h * G + g) * D + sub * DL;
 #pragma unroll
-            for (int i = 0; i < DL; i++) s = fmaf(qv[g][i], kv[i], s);
-            s += __shfl_xor(s, 1, 64);
-            s += __shfl_xor(s, 2, 64);
-            s += __shfl_xor(s, 4, 64);
-            if (sub == 0 && p < p1) sc[g][p - p0] = s * scale;
-        }
-    }
-    __syncthreads();
-    // ---- per-head chunk max and exp-sum (wave w handles heads w, w+4, ...)
-    const int cn = (int)(p1 - p0);
-    for (int g = wave; g < G; g += 4) {
-        float mx = -INFINITY;
-        for (int i = lane; i < cn; i += 64) mx = fmaxf(mx, sc[g][i]);
-#pragma unroll
-        for (int off = 32; off >= 1; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off, 64));
-        float sum = 0.f;
-        for (int i = lane; i < cn; i += 64) {
-            float e = cn > 0 ? expf(sc[g][i] - mx) : 0.f;
-            sc[g][i] = e;
-            sum += e;
-        }
-#pragma unroll
-        for (int off = 32; off >= 1; off >>= 1) sum += __shfl_xor(sum, off, 64);
-        if (lane == 0) {
-            stat[g][0] = mx;
-            stat[g][1] = sum;
-        }
-    }
-    __syncthreads();
-    // ---- exp-weighted V
-    float o[G][DL];
-#pragma unroll
-    for (int g = 0; g < G; g++)
-#pragma unroll
-        for (int i = 0; i < DL; i++) o[g][i] = 0.f;
-    for (int64_t base = p0; base < p1; base += 32) {
-        int64_t p = base + wave * 8 + grp;
-        if (p < p1) {
-            float vv[DL];
-            KVLoad<KVT>::template load<DL>(vb + p * D + sub * DL, vv);
-#pragma unroll
-            for (int g = 0; g < G; g++) {
-                float e = sc[g][p - p0];
-#pragma unroll
-                for (int i = 0; i < DL; i++) o[g][i] = fmaf(e, vv[i], o[g][i]);
+            for (int i = 0; i < DL; i += 4) {
+                float4 t = *reinterpret_cast<const float4*>(qp + i);
+                qv[g][i] = t.x;
+                qv[g][i + 1] = t.y;
+                qv[g][i + 2] = t.z;
+                qv[g][i + 3] = t.w;
             }
         }
-    }
-    // reduce over the 8 position groups of the wavefront (lane bits 3..5)
+        auto scores = [&](int64_t base, const float* kv) {
+            const int64_t p = base + wave * 8 + grp;
 #pragma unroll
-    for (int g = 0; g < G; g++)
+            for (int g = 0; g < G; g++) {
+                float s = 0.f;
 #pragma unroll
-        for (int i = 0; i < DL; i++) {
-            float v = o[g][i];
-            v += __shfl_xor(v, 8, 64);
-            v += __shfl_xor(v, 16, 64);
-            v += __shfl_xor(v, 32, 64);
-            o[g][i] = v;
+                for (int i = 0; i < DL; i++) s = fmaf(qv[g][i], kv[i], s);
+                s += __shfl_xor(s, 1, 64);
+                s += __shfl_xor(s, 2, 64);
+                s += __shfl_xor(s, 4, 64);
+                if (sub == 0 && p < p1) sc[g][p - p0] = s * a.scale;
+            }
+        };
+#pragma unroll
+        for (int it = 0; it < ATT_PF; it++)
+            if (p0 + it * 32 < p1) scores(p0 + it * 32, kpre[it]);
+        for (int64_t base = p0 + ATT_PF * 32; base < p1; base += 32) {
+            int64_t p = base + wave * 8 + grp;
+            int64_t pc = p < p1 ? p : p1 - 1;
+            float kv[DL];
+            KVLoad<KVT>::template load<DL>(kb + pc * D + sub * DL, kv);
+            scores(base, kv);
         }
-    if (grp == 0) {
+        __syncthreads();
+        // per-head chunk max and exp-sum (wavefront w handles heads w, w + 4)
+        const int cn = (int)(p1 - p0);
+        for (int g = wave; g < G; g += 4) {
+            float mx = -INFINITY;
+            for (int i = lane; i < cn; i += 64) mx = fmaxf(mx, sc[g][i]);
+#pragma unroll
+            for (int off = 32; off >= 1; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off, 64));
+            float sum = 0.f;
+            for (int i = lane; i < cn; i += 64) {
+                float e = expf(sc[g][i] - mx);
+                sc[g][i] = e;
+                sum += e;
+            }
+#pragma unroll
+            for (int off = 32; off >= 1; off >>= 1) sum += __shfl_xor(sum, off, 64);
+            if (lane == 0) {
+                stat[g][0] = mx;
+                stat[g][1] = sum;
+            }
+        }
+        __syncthreads();
+        // exp-weighted V
+        float o[G][DL];
 #pragma unroll
         for (int g = 0; g < G; g++)
 #pragma unroll
-            for (int i = 0; i < DL; i++) part[wave][g][sub * DL + i] = o[g][i];
+            for (int i = 0; i < DL; i++) o[g][i] = 0.f;
+        auto accum = [&](int64_t base, const float* vv) {
+            const int64_t p = base + wave * 8 + grp;
+            if (p < p1) {
+#pragma unroll
+                for (int g = 0; g < G; g++) {
+                    const float e = sc[g][p - p0];
+#pragma unroll
+                    for (int i = 0; i < DL; i++) o[g][i] = fmaf(e, vv[i], o[g][i]);
+                }
+            }
+        };
+#pragma unroll
+        for (int it = 0; it < ATT_PF; it++)
+            if (p0 + it * 32 < p1) accum(p0 + it * 32, vpre[it]);
+        for (int64_t base = p0 + ATT_PF * 32; base < p1; base += 32) {
+            int64_t p = base + wave * 8 + grp;
+            float vv[DL];
+            if (p < p1) KVLoad<KVT>::template load<DL>(vb + p * D + sub * DL, vv);
+            accum(base, vv);
+        }
+        // reduce over the 8 position groups of the wavefront (lane bits 3..5)
+#pragma unroll
+        for (int g = 0; g < G; g++)
+#pragma unroll
+            for (int i = 0; i < DL; i++) {
+                float v = o[g][i];
+                v += __shfl_xor(v, 8, 64);
+                v += __shfl_xor(v, 16, 64);
+                v += __shfl_xor(v, 32, 64);
+                o[g][i] = v;
+            }
+        if (grp == 0) {
+#pragma unroll
+            for (int g = 0; g < G; g++)
+#pragma unroll
+                for (int i = 0; i < DL; i++) part[wave][g][sub * DL + i] = o[g][i];
+        }
+        __syncthreads();
+        if (a.nsplit == 1) {  // the only split: normalise and store
+            for (int idx = tid; idx < G * D; idx += 256) {
+                const int g = idx / D, d = idx % D;
+                const float s = (part[0][g][d] + part[1][g][d]) + (part[2][g][d] + part[3][g][d]);
+                a.out[((int64_t)b * hq + h * G + g) * D + d] = s / stat[g][1];
+            }
+            return;
+        }
+        float* wr = a.ws + rec0 + (int64_t)split * G * (D + 2);
+        for (int idx = tid; idx < G * D; idx += 256) {
+            const int g = idx / D, d = idx % D;
+            wr[g * (D + 2) + d] = (part[0][g][d] + part[1][g][d]) + (part[2][g][d] + part[3][g][d]);
+        }
+        if (tid < G) {
+            wr[tid * (D + 2) + D] = stat[tid][0];
+            wr[tid * (D + 2) + D + 1] = stat[tid][1];
+        }
+    } else if (a.nsplit == 1) {
+        return;  // (L == 0 is rejected on the host)
+    }
+    // arrival: the last workgroup of this (batch, kv head) merges the records
+    __syncthreads();
+    if (tid == 0) {
+        __threadfence();  // this workgroup's record is visible device-wide before it is counted
+        const int prev = atomicAdd(a.counter + (int64_t)b * a.hkv + h, 1);
+        s_last = prev == a.nsplit - 1;
     }
     __syncthreads();
-    // workspace record per (b, h, split, g): o[D], max, sum
-    float* wr = ws + ((((int64_t)b * hkv + h) * nsplit + split) * G) * (D + 2);
-    for (int idx = threadIdx.x; idx < G * D; idx += 256) {
-        int g = idx / D, d = idx % D;
-        float s = part[0][g][d] + part[1][g][d] + part[2][g][d] + part[3][g][d];
-        wr[g * (D + 2) + d] = s;
+    if (!s_last) return;
+    __threadfence();  // acquire: observe the other workgroups' records
+    const int nact = (int)((L + a.chunk - 1) / a.chunk);
+    for (int idx = tid; idx < G * D; idx += 256) {
+        const int g = idx / D, d = idx % D;
+        const float* r = a.ws + rec0 + (int64_t)g * (D + 2);
+        const int64_t stride = (int64_t)G * (D + 2);
+        float M = -INFINITY;
+        for (int s = 0; s < nact; s++) M = fmaxf(M, __builtin_nontemporal_load(r + s * stride + D));
+        float num = 0.f, den = 0.f;
+        for (int s = 0; s < nact; s++) {
+            const float* rs = r + s * stride;
+            const float f = expf(__builtin_nontemporal_load(rs + D) - M);
+            num = fmaf(__builtin_nontemporal_load(rs + d), f, num);
+            den = fmaf(__builtin_nontemporal_load(rs + D + 1), f, den);
+        }
+        a.out[((int64_t)b * hq + h * G + g) * D + d] = num / den;
     }
-    if (threadIdx.x < G) {
-        wr[threadIdx.x * (D + 2) + D] = stat[threadIdx.x][0];
-        wr[threadIdx.x * (D + 2) + D + 1] = stat[threadIdx.x][1];
-    }
+    if (tid == 0) a.counter[(int64_t)b * a.hkv + h] = 0;  // ready for the next launch
 }
 
-// out[b, hq, d] = sum_s o_s[d] e^(m_s - M) / sum_s l_s e^(m_s - M)
-template <int D, int G>
-__global__ void k_attn_combine(const float* __restrict__ ws, float* __restrict__ out, int hkv,
-                               int nsplit) {
-    const int hq_idx = blockIdx.x, b = blockIdx.y;  // query head, batch
-    const int h = hq_idx / G, g = hq_idx % G;
-    const int d = threadIdx.x;
-    const float* base = ws + (((int64_t)b * hkv + h) * nsplit * G + g) * (D + 2);
-    const int64_t stride = (int64_t)G * (D + 2);
-    float M = -INFINITY;
-    for (int s = 0; s < nsplit; s++) M = fmaxf(M, base[s * stride + D]);
-    float num = 0.f, den = 0.f;
-    for (int s = 0; s < nsplit; s++) {
-        const float* r = base + s * stride;
-        float l = r[D + 1];
-        if (l == 0.f) continue;  // split with no positions
-        float f = expf(r[D] - M);
-        num = fmaf(r[d], f, num);
-        den = fmaf(l, f, den);
-    }
-    out[((int64_t)b * hkv * G + hq_idx) * D + d] = num / den;
-}
-
-template <int D, int G, typename KVT>
-static int attn_run(const float* q, const KVT* k, const KVT* v, float* out, float* ws, int B,
-                    int hkv, int64_t lmax, int64_t kv_bstride, AttnLen len, int chunk,
-                    int nsplit, float scale, hipStream_t s) {
-    k_attn_partial<D, G, KVT><<<dim3(nsplit, hkv, B), 256, 0, s>>>(q, k, v, ws, hkv, lmax,
-                                                                  kv_bstride, len, chunk,
-                                                                  nsplit, scale);
-    k_attn_combine<D, G><<<dim3(hkv * G, B), D, 0, s>>>(ws, out, hkv, nsplit);
-    hipError_t e = hipGetLastError();
-    return e == hipSuccess ? TL_HIP_OK : hip_fail(e, "attention launch");
-}
-
-// Split plan: about 1024 workgroups over (B x Hkv x splits), chunks a multiple of 32 and at
+// Split plan: about 1024 workgroups over (B x Hkv x splits); chunks a multiple of 32 and at
 // most ATT_MAX_CHUNK positions.
 void attn_plan(int B, int hkv, int64_t L, int* chunk, int* nsplit) {
     int64_t pairs = (int64_t)B * hkv;
@@ -246,14 +283,15 @@ size_t attn_workspace_floats(int B, int hkv, int G, int D, int nsplit) {
 }
 
 template <typename KVT>
-static int attn_dispatch(const float* q, const KVT* k, const KVT* v, float* out, float* ws,
-                         int B, int hq, int hkv, int D, int64_t lmax, int64_t kv_bstride,
-                         AttnLen len, int chunk, int nsplit, float scale, hipStream_t s) {
-    const int G = hq / hkv;
-#define TLH_ATT(DD, GG)                                                                      \
-    if (D == DD && G == GG)                                                                  \
-        return attn_run<DD, GG, KVT>(q, k, v, out, ws, B, hkv, lmax, kv_bstride, len, chunk, \
-                                     nsplit, scale, s);
+static int attn_dispatch(const AttnArgs& a, int B, int hq, int D, hipStream_t s) {
+    const int G = hq / a.hkv;
+    dim3 grid(a.nsplit, a.hkv, B);
+#define TLH_ATT(DD, GG)                                  \
+    if (D == DD && G == GG) {                            \
+        k_attn<DD, GG, KVT><<<grid, 256, 0, s>>>(a);     \
+        hipError_t e = hipGetLastError();                \
+        return e == hipSuccess ? TL_HIP_OK : hip_fail(e, "attention launch"); \
+    }
     TLH_ATT(128, 1) TLH_ATT(128, 2) TLH_ATT(128, 4) TLH_ATT(128, 8)
     TLH_ATT(64, 1) TLH_ATT(64, 2) TLH_ATT(64, 4) TLH_ATT(64, 8)
 #undef TLH_ATT
@@ -263,15 +301,17 @@ static int attn_dispatch(const float* q, const KVT* k, const KVT* v, float* out,
 }
 
 int launch_attention(const float* q, const void* k, const void* v, int kv_dtype, float* out,
-                     float* ws, int B, int hq, int hkv, int D, int64_t lmax, int64_t kv_bstride,
-                     int64_t L, const int32_t* len_dev, int len_add, int len_step, int chunk,
-                     int nsplit, float scale, hipStream_t s) {
-    AttnLen len{L, len_dev, len_add, len_step};
-    if (kv_dtype == TL_HIP_F16)
-        return attn_dispatch<__half>(q, (const __half*)k, (const __half*)v, out, ws, B, hq, hkv, D,
-                                     lmax, kv_bstride, len, chunk, nsplit, scale, s);
-    return attn_dispatch<float>(q, (const float*)k, (const float*)v, out, ws, B, hq, hkv, D, lmax,
-                                kv_bstride, len, chunk, nsplit, scale, s);
+                     float* ws, int32_t* counter, int B, int hq, int hkv, int D, int64_t lmax,
+                     int64_t kv_bstride, int64_t L, const int32_t* len_dev, int len_add,
+                     int len_step, int chunk, int nsplit, float scale, hipStream_t s) {
+    if (chunk > ATT_MAX_CHUNK || chunk % 32) {
+        set_error(TL_HIP_ERR_ARG, "ArgumentError: attention chunk %d", chunk);
+        return TL_HIP_ERR_ARG;
+    }
+    AttnArgs a{q, k, v, out, ws, counter, hkv, lmax, kv_bstride, AttnLen{L, len_dev, len_add, len_step},
+               chunk, nsplit, scale};
+    if (kv_dtype == TL_HIP_F16) return attn_dispatch<__half>(a, B, hq, D, s);
+    return attn_dispatch<float>(a, B, hq, D, s);
 }
 
 }  // namespace tlhip
@@ -323,15 +363,19 @@ extern "C" tl_hip_tensor* tl_hip_attention_decode(const tl_hip_tensor* qh, const
     int64_t oshape[3] = {B, hq, D};
     Tensor* o = tensor_alloc(oshape, 3);
     if (!o) return nullptr;
+    hipStream_t s = cur_stream();
     float* ws = (float*)dev_alloc(attn_workspace_floats((int)B, (int)hkv, (int)(hq / hkv), (int)D, nsplit) * 4);
-    if (!ws) {
-        tensor_drop(o);
-        return nullptr;
+    int32_t* cnt = (int32_t*)dev_alloc((size_t)B * hkv * 4);
+    int rc = ws && cnt ? TL_HIP_OK : TL_HIP_ERR_ALLOC;
+    if (rc == TL_HIP_OK) {
+        hipError_t e = hipMemsetAsync(cnt, 0, (size_t)B * hkv * 4, s);
+        rc = e == hipSuccess ? TL_HIP_OK : hip_fail(e, "hipMemsetAsync(counters)");
     }
-    int rc = launch_attention(q->f32(), k->data, v->data, k->dtype, o->f32(), ws, (int)B, (int)hq,
-                              (int)hkv, (int)D, lmax, hkv * lmax * D, L, nullptr, 0, 0, chunk, nsplit,
-                              scale, cur_stream());
+    if (rc == TL_HIP_OK)
+        rc = launch_attention(q->f32(), k->data, v->data, k->dtype, o->f32(), ws, cnt, (int)B, (int)hq, (int)hkv,
+                              (int)D, lmax, hkv * lmax * D, L, nullptr, 0, 0, chunk, nsplit, scale, s);
     dev_free(ws);  // stream-ordered: reused only by later work on the same stream
+    dev_free(cnt);
     if (rc != TL_HIP_OK) {
         tensor_drop(o);
         return nullptr;

@@ -72,6 +72,51 @@ struct QWeight {
 };
 inline QWeight* Q(tl_hip_qtensor* h) { return reinterpret_cast<QWeight*>(h); }
 
+// ---- fused decode matvec (matvec.hip) ---------------------------------------------
+enum { EPI_PLAIN = 0, EPI_RES = 1, EPI_GLU = 2, EPI_ROPE_KV = 3, EPI_ARGMAX = 4 };
+
+struct MvArgs {
+    const uint8_t* qs;
+    const __half* d;
+    int64_t n, k, nb;
+    const float* x;           // [m, k]; with EMBED the embedding table [vocab, k]
+    const int32_t* embed_id;  // EMBED: token id (device)
+    float* x_out;             // EMBED: gathered row written here (workgroup 0)
+    const float* norm_w;      // NORM weight [k]
+    float eps;
+    float* y;                 // output
+    const float* res;         // EPI_RES residual (may alias y)
+    // EPI_ROPE_KV
+    const int32_t* pos;
+    const float* cos_t;
+    const float* sin_t;
+    float* q_out;
+    void* kc;
+    void* vc;
+    int q_rows, kv_rows, hd, kv_f16;
+    int64_t max_seq;
+    // EPI_ARGMAX
+    float* plogits;       // penalised logits
+    const uint8_t* seen;  // repetition-penalty mask (nullptr = no penalty)
+    uint8_t* seen_out;    // mask updated with the chosen token
+    float penalty;
+    float* part_v;        // per-workgroup best value
+    int32_t* part_i;      // per-workgroup best index
+    int32_t* part_nan;    // per-workgroup NaN flag
+    int32_t* counter;     // arrival counter (zero between launches)
+    int32_t* tok_out;
+    int32_t* out_ids;
+    int32_t* step;
+    int32_t* pos_inc;     // position advanced by one (decode step end)
+    int max_out;
+};
+struct QWeight;
+// One fused matvec launch over weight w (m = 1 or 2 activation rows); weight fields of `a`
+// are filled from w.
+int launch_mv(const QWeight* w, MvArgs a, int m, int epi, bool norm, bool embed, hipStream_t s);
+// workgroups (= argmax partial slots) of a matvec over n rows
+int mv_partials(int64_t n);
+
 // kernel entry points shared across translation units (all on the given stream)
 int launch_quant_matvec(const QWeight* w, const float* x, float* y, int64_t m, hipStream_t s,
                         const float* residual);
@@ -98,10 +143,11 @@ int launch_rope_table(float* out, int64_t seq_len, int64_t dim, float base, int 
                       hipStream_t s);
 // Attention over a [B?, Hkv, lmax, D] cache (kv_bstride elements between batch items, 0 =
 // shared).  Cached length of item b = (len_dev ? *len_dev + len_add : L) + b * len_step.
+// `counter` holds B * hkv ints that are zero before the launch (and zero again after it).
 int launch_attention(const float* q, const void* k, const void* v, int kv_dtype, float* out,
-                     float* ws, int B, int hq, int hkv, int D, int64_t lmax, int64_t kv_bstride,
-                     int64_t L, const int32_t* len_dev, int len_add, int len_step, int chunk,
-                     int nsplit, float scale, hipStream_t s);
+                     float* ws, int32_t* counter, int B, int hq, int hkv, int D, int64_t lmax,
+                     int64_t kv_bstride, int64_t L, const int32_t* len_dev, int len_add,
+                     int len_step, int chunk, int nsplit, float scale, hipStream_t s);
 void attn_plan(int B, int hkv, int64_t L, int* chunk, int* nsplit);
 size_t attn_workspace_floats(int B, int hkv, int G, int D, int nsplit);
 

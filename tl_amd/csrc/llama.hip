@@ -75,15 +75,14 @@ __global__ void k_rope_kv(const float* __restrict__ qkv, float* __restrict__ qou
     }
 }
 
-// SwiGLU on the concatenated gate|up rows: a[r, j] = silu(gu[r, j]) * gu[r, F + j]
+// SwiGLU on the interleaved gate/up rows: a[r, j] = silu(gu[r, 2j]) * gu[r, 2j + 1]
 // (silu of ffi.rs:2097-2113 then mul, chatbot.tl:33-38)
 __global__ void k_swiglu_rows(const float* __restrict__ gu, float* __restrict__ a, int n,
                               int64_t F) {
     int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
     if (t >= n * F) return;
-    int64_t r = t / F, j = t % F;
-    float g = gu[r * 2 * F + j], u = gu[r * 2 * F + F + j];
-    a[t] = (g * (1.0f / (1.0f + expf(-g)))) * u;
+    float2 p = reinterpret_cast<const float2*>(gu)[t];
+    a[t] = (p.x * (1.0f / (1.0f + expf(-p.x)))) * p.y;
 }
 
 __global__ void k_add_inplace(float* __restrict__ x, const float* __restrict__ t, int64_t n) {
@@ -128,6 +127,10 @@ struct Llama {
     size_t ws_floats = 0;
     int32_t *ids = nullptr, *pos = nullptr, *tok = nullptr, *step = nullptr, *out_ids = nullptr;
     uint8_t* seen = nullptr;
+    int32_t* att_cnt = nullptr;  // attention arrival counters [max_tok * KV]
+    // greedy-argmax partials of the LM-head matvec (one per workgroup) and its counter
+    float* am_v = nullptr;
+    int32_t *am_i = nullptr, *am_nan = nullptr, *am_cnt = nullptr;
     int max_out = 0;
     int64_t host_pos = 0;
     hipGraphExec_t graph = nullptr;
@@ -168,6 +171,7 @@ static int ensure_tokens(Llama* m, int64_t n) {
     }
     dev_free(m->ids);
     dev_free(m->ws);
+    dev_free(m->att_cnt);
     const int64_t qkv_w = m->D + 2 * (int64_t)m->KV * m->hd;
     m->x = (float*)dev_alloc(n * m->D * 4);
     m->h = (float*)dev_alloc(n * m->D * 4);
@@ -182,9 +186,11 @@ static int ensure_tokens(Llama* m, int64_t n) {
     int nsplit = (int)cdiv(m->max_seq, 64);
     m->ws_floats = attn_workspace_floats((int)n, m->KV, m->H / m->KV, m->hd, nsplit);
     m->ws = (float*)dev_alloc(m->ws_floats * 4);
+    m->att_cnt = (int32_t*)dev_alloc((size_t)n * m->KV * 4);
     for (float** b : bufs)
         if (!*b) return TL_HIP_ERR_ALLOC;
-    if (!m->ids || !m->ws) return TL_HIP_ERR_ALLOC;
+    if (!m->ids || !m->ws || !m->att_cnt) return TL_HIP_ERR_ALLOC;
+    TLH_CHECK_HIP(hipMemsetAsync(m->att_cnt, 0, (size_t)n * m->KV * 4, cur_stream()));
     m->max_tok = n;
     free_graph(m);  // captured pointers changed
     return TL_HIP_OK;
@@ -214,8 +220,14 @@ static int try_merge(Llama* m, int layer) {
             set_error(TL_HIP_ERR_TYPE, "TypeMismatch: gate/up of layer %d differ in ggml type", layer);
             return TL_HIP_ERR_TYPE;
         }
-        std::vector<uint8_t> cat(S[base + 3]);
-        cat.insert(cat.end(), S[base + 4].begin(), S[base + 4].end());
+        // rows interleaved (gate_0, up_0, gate_1, up_1, ...): the SwiGLU epilogue of the
+        // matvec then sees both halves of an output in one workgroup
+        const size_t row_bytes = (size_t)(m->D / 32) * (ty == TL_HIP_GGML_Q4_0 ? 18 : 34);
+        std::vector<uint8_t> cat(S[base + 3].size() * 2);
+        for (int64_t i = 0; i < m->F; i++) {
+            std::memcpy(cat.data() + (2 * i) * row_bytes, S[base + 3].data() + i * row_bytes, row_bytes);
+            std::memcpy(cat.data() + (2 * i + 1) * row_bytes, S[base + 4].data() + i * row_bytes, row_bytes);
+        }
         int64_t shape[2] = {2 * (int64_t)m->F, m->D};
         tl_hip_qtensor* q = tl_hip_qtensor_new(ty, cat.data(), cat.size(), shape, 2);
         if (!q) return tl_hip_last_status();
@@ -273,8 +285,8 @@ static int enqueue_forward(Llama* m, int n, int f16, hipStream_t s) {
                                                             m->max_seq, m->rope_per_token);
         // query i (absolute position pos + i) attends cache positions 0 .. pos + i
         if ((rc = launch_attention(m->q, m->kc[l], m->vc[l], m->kv_f16 ? TL_HIP_F16 : TL_HIP_F32, m->ao,
-                                   m->ws, n, m->H, m->KV, (int)hd, m->max_seq, 0, 0, m->pos, 1, 1, 64,
-                                   nsplit, 1.0f / sqrtf((float)hd), s)))
+                                   m->ws, m->att_cnt, n, m->H, m->KV, (int)hd, m->max_seq, 0, 0, m->pos, 1, 1,
+                                   64, nsplit, 1.0f / sqrtf((float)hd), s)))
             return rc;
         (void)G;
         if ((rc = linear(m->wo[l], m->ao, m->x, n, m->x, m->t, f16, s))) return rc;
@@ -291,21 +303,80 @@ static int enqueue_forward(Llama* m, int n, int f16, hipStream_t s) {
     return e == hipSuccess ? TL_HIP_OK : hip_fail(e, "forward launch");
 }
 
-// one greedy decode step from the token in m->tok (device)
+// One greedy decode step from the token in m->tok (device), five kernels per layer:
+//   [embed (layer 0) +] RMSNorm + q|k|v matvec + RoPE + KV append   (EPI_ROPE_KV)
+//   attention over the cache (split-L, in-kernel merge)
+//   o-proj matvec + residual                                         (EPI_RES)
+//   RMSNorm + gate/up matvec + SwiGLU                                (EPI_GLU)
+//   down matvec + residual                                           (EPI_RES)
+// and one more for the output RMSNorm + LM head + penalty + argmax + step bookkeeping.
 static int enqueue_step(Llama* m, float penalty, hipStream_t s) {
-    hipError_t e = hipMemcpyAsync(m->ids, m->tok, 4, hipMemcpyDeviceToDevice, s);
-    if (e != hipSuccess) return hip_fail(e, "token copy");
-    int rc = enqueue_forward(m, 1, 0, s);
-    if (rc) return rc;
-    const float* lg = m->logits;
-    if (penalty != 1.0f) {
-        if ((rc = launch_rep_penalty(m->logits, m->seen, m->plogits, 1, m->V, penalty, s))) return rc;
-        lg = m->plogits;
+    const int64_t hd = m->hd;
+    const int nsplit = (int)cdiv(m->max_seq, 64);
+    int rc;
+    for (int l = 0; l < m->nl; l++) {
+        MvArgs a = {};
+        a.eps = m->eps;
+        if (l == 0) {  // the token's embedding row, also stored as the residual stream
+            a.x = m->emb;
+            a.embed_id = m->tok;
+            a.x_out = m->x;
+        } else {
+            a.x = m->x;
+        }
+        a.norm_w = m->attn_norm[l];
+        a.pos = m->pos;
+        a.cos_t = m->cos_t;
+        a.sin_t = m->sin_t;
+        a.q_out = m->q;
+        a.kc = m->kc[l];
+        a.vc = m->vc[l];
+        a.q_rows = m->D;
+        a.kv_rows = m->KV * (int)hd;
+        a.hd = (int)hd;
+        a.kv_f16 = m->kv_f16;
+        a.max_seq = m->max_seq;
+        if ((rc = launch_mv(m->wqkv[l], a, 1, EPI_ROPE_KV, true, l == 0, s))) return rc;
+        if ((rc = launch_attention(m->q, m->kc[l], m->vc[l], m->kv_f16 ? TL_HIP_F16 : TL_HIP_F32, m->ao, m->ws,
+                                   m->att_cnt, 1, m->H, m->KV, (int)hd, m->max_seq, 0, 0, m->pos, 1, 0, 64,
+                                   nsplit, 1.0f / sqrtf((float)hd), s)))
+            return rc;
+        MvArgs o = {};
+        o.x = m->ao;
+        o.y = m->x;
+        o.res = m->x;
+        if ((rc = launch_mv(m->wo[l], o, 1, EPI_RES, false, false, s))) return rc;
+        MvArgs g = {};
+        g.x = m->x;
+        g.norm_w = m->ffn_norm[l];
+        g.eps = m->eps;
+        g.y = m->act;
+        if ((rc = launch_mv(m->wgu[l], g, 1, EPI_GLU, true, false, s))) return rc;
+        MvArgs d = {};
+        d.x = m->act;
+        d.y = m->x;
+        d.res = m->x;
+        if ((rc = launch_mv(m->wdown[l], d, 1, EPI_RES, false, false, s))) return rc;
     }
-    if ((rc = launch_argmax(lg, m->V, m->tok, s))) return rc;
-    k_step_end<<<1, 64, 0, s>>>(m->tok, m->out_ids, m->step, penalty != 1.0f ? m->seen : nullptr, m->max_out);
-    e = hipGetLastError();
-    return e == hipSuccess ? TL_HIP_OK : hip_fail(e, "step launch");
+    MvArgs h = {};
+    h.x = m->x;
+    h.norm_w = m->out_norm;
+    h.eps = m->eps;
+    h.y = m->logits;
+    h.plogits = m->plogits;
+    h.seen = penalty != 1.0f ? m->seen : nullptr;
+    h.seen_out = penalty != 1.0f ? m->seen : nullptr;
+    h.penalty = penalty;
+    h.part_v = m->am_v;
+    h.part_i = m->am_i;
+    h.part_nan = m->am_nan;
+    h.counter = m->am_cnt;
+    h.tok_out = m->tok;
+    h.out_ids = m->out_ids;
+    h.step = m->step;
+    h.pos_inc = m->pos;
+    h.max_out = m->max_out;
+    return launch_mv(m->lm, h, 1, EPI_ARGMAX, true, false, s);
 }
 
 }  // namespace tlhip
@@ -352,8 +423,15 @@ tl_hip_llama* tl_hip_llama_new(int n_layers, int d_model, int n_heads, int n_kv_
     m->tok = (int32_t*)dev_alloc(4);
     m->step = (int32_t*)dev_alloc(4);
     m->seen = (uint8_t*)dev_alloc(vocab);
-    int rc = (m->cos_t && m->sin_t && m->logits && m->plogits && m->pos && m->tok && m->step && m->seen)
+    const int parts = mv_partials(vocab);
+    m->am_v = (float*)dev_alloc((size_t)parts * 4);
+    m->am_i = (int32_t*)dev_alloc((size_t)parts * 4);
+    m->am_nan = (int32_t*)dev_alloc((size_t)parts * 4);
+    m->am_cnt = (int32_t*)dev_alloc(4);
+    int rc = (m->cos_t && m->sin_t && m->logits && m->plogits && m->pos && m->tok && m->step && m->seen &&
+              m->am_v && m->am_i && m->am_nan && m->am_cnt)
                  ? TL_HIP_OK : TL_HIP_ERR_ALLOC;
+    if (rc == TL_HIP_OK && hipMemsetAsync(m->am_cnt, 0, 4, s) != hipSuccess) rc = hip_fail(hipGetLastError(), "memset");
     if (rc == TL_HIP_OK) rc = launch_rope_table(m->cos_t, max_seq, m->hd, rope_theta, 0, s);
     if (rc == TL_HIP_OK) rc = launch_rope_table(m->sin_t, max_seq, m->hd, rope_theta, 1, s);
     if (rc == TL_HIP_OK) rc = alloc_kv(m);
@@ -386,7 +464,8 @@ int tl_hip_llama_free(tl_hip_llama* h) {
     for (void* p : m->kc) dev_free(p);
     for (void* p : m->vc) dev_free(p);
     void* bufs[] = {m->out_norm, m->emb, m->cos_t, m->sin_t, m->x, m->h, m->qkv, m->q, m->ao, m->t, m->gu,
-                    m->act, m->logits, m->plogits, m->ws, m->ids, m->pos, m->tok, m->step, m->out_ids, m->seen};
+                    m->act, m->logits, m->plogits, m->ws, m->ids, m->pos, m->tok, m->step, m->out_ids, m->seen,
+                    m->att_cnt, m->am_v, m->am_i, m->am_nan, m->am_cnt};
     for (void* p : bufs) dev_free(p);
     delete m;
     return TL_HIP_OK;

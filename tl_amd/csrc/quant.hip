@@ -1,5 +1,5 @@
 // Quantized weights: GGUF Q4_0 / Q8_0 upload + repack, dequantisation, and the fused
-// dequant x matvec used for decode (m <= 4 activation rows).
+// entry points of the quantized linear (matvec kernels: matvec.hip, GEMM: gemm.hip).
 //
 // Residency format (built once at upload, the role of QTensor::gpu_raw_cache,
 // crates/tl_runtime/src/system.rs:316-331):  the 18-byte (Q4_0) / 34-byte (Q8_0) GGUF blocks
@@ -75,179 +75,6 @@ __global__ void k_dequant_q8_0(const uint8_t* __restrict__ qs, const __half* __r
     v.z = s * (float)(int8_t)((w >> 16) & 0xFF);
     v.w = s * (float)(int8_t)(w >> 24);
     reinterpret_cast<float4*>(out + b * 32)[c] = v;
-}
-
-// ---------------------------------------------------------------- matvec -----------
-// y[m, n] = sum_k x[m, k] * W[n, k] (+ residual[m, n]) for m <= 4.
-//
-// Mapping: a workgroup is 4 wavefronts; wavefront w owns R consecutive rows; lane l walks
-// blocks l, l+64, ... of those rows, so one load instruction covers 64 consecutive 16-byte
-// quant blocks of a row.  Per block the lane forms
-//     sum_j x_j * W_j = d * (sum_j x_j * q_j - 8 * sum_j x_j)          (Q4_0)
-//     sum_j x_j * W_j = d * (sum_j x_j * u_j - 128 * sum_j x_j), u = q ^ 0x80   (Q8_0)
-// with q_j / u_j converted from bytes (v_cvt_f32_ubyteN), so the inner loop is one
-// conversion and one FMA per weight.  The 64 lane partials of a row are reduced across
-// the wavefront at the end.  Accumulation is f32 throughout.
-__device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off, 64);
-    return v;
-}
-
-__device__ __forceinline__ float dot_nib4(uint32_t q, const float* x) {
-    // q holds 4 bytes each in 0..255 (already masked to one nibble or shifted)
-    float s = x[0] * (float)(q & 0xFF);
-    s = fmaf(x[1], (float)((q >> 8) & 0xFF), s);
-    s = fmaf(x[2], (float)((q >> 16) & 0xFF), s);
-    s = fmaf(x[3], (float)(q >> 24), s);
-    return s;
-}
-
-template <int QT>  // 2 = Q4_0, 8 = Q8_0
-struct QTraits;
-template <>
-struct QTraits<2> {
-    static constexpr int QB = 16;
-};
-template <>
-struct QTraits<8> {
-    static constexpr int QB = 32;
-};
-
-template <int QT, int R, int M, bool RES>
-__global__ __launch_bounds__(256) void k_matvec(const uint8_t* __restrict__ qs,
-                                                const __half* __restrict__ dsc,
-                                                const float* __restrict__ x,
-                                                float* __restrict__ y,
-                                                const float* __restrict__ res, int64_t n,
-                                                int64_t k, int64_t nb) {
-    constexpr int QB = QTraits<QT>::QB;
-    const int lane = threadIdx.x & 63;
-    const int64_t row0 = ((int64_t)blockIdx.x * 4 + (threadIdx.x >> 6)) * R;
-    if (row0 >= n) return;  // uniform per wavefront
-    float acc[M][R];
-#pragma unroll
-    for (int m = 0; m < M; m++)
-#pragma unroll
-        for (int r = 0; r < R; r++) acc[m][r] = 0.f;
-
-    for (int64_t b = lane; b < nb; b += 64) {
-        uint4 w[R][QB / 16];
-        float d[R];
-#pragma unroll
-        for (int r = 0; r < R; r++) {
-            int64_t row = row0 + r < n ? row0 + r : n - 1;  // clamp: loads stay in bounds
-            const uint4* p = reinterpret_cast<const uint4*>(qs + (row * nb + b) * QB);
-#pragma unroll
-            for (int i = 0; i < QB / 16; i++) w[r][i] = p[i];
-            d[r] = __half2float(dsc[row * nb + b]);
-        }
-#pragma unroll
-        for (int m = 0; m < M; m++) {
-            float xv[32];
-            const float4* xp = reinterpret_cast<const float4*>(x + m * k + b * 32);
-#pragma unroll
-            for (int i = 0; i < 8; i++) {
-                float4 t = xp[i];
-                xv[4 * i] = t.x;
-                xv[4 * i + 1] = t.y;
-                xv[4 * i + 2] = t.z;
-                xv[4 * i + 3] = t.w;
-            }
-            float sx0 = 0.f, sx1 = 0.f;
-#pragma unroll
-            for (int j = 0; j < 16; j++) {
-                sx0 += xv[j];
-                sx1 += xv[16 + j];
-            }
-            const float sx = sx0 + sx1;
-#pragma unroll
-            for (int r = 0; r < R; r++) {
-                float s0 = 0.f, s1 = 0.f;
-                if constexpr (QT == 2) {
-                    const uint32_t q[4] = {w[r][0].x, w[r][0].y, w[r][0].z, w[r][0].w};
-#pragma unroll
-                    for (int c = 0; c < 4; c++) {
-                        s0 += dot_nib4(q[c] & 0x0F0F0F0Fu, xv + 4 * c);
-                        s1 += dot_nib4((q[c] >> 4) & 0x0F0F0F0Fu, xv + 16 + 4 * c);
-                    }
-                    acc[m][r] = fmaf(d[r], (s0 + s1) - 8.f * sx, acc[m][r]);
-                } else {
-                    const uint32_t q[8] = {w[r][0].x, w[r][0].y, w[r][0].z, w[r][0].w,
-                                           w[r][1].x, w[r][1].y, w[r][1].z, w[r][1].w};
-#pragma unroll
-                    for (int c = 0; c < 4; c++) {
-                        s0 += dot_nib4(q[c] ^ 0x80808080u, xv + 4 * c);
-                        s1 += dot_nib4(q[4 + c] ^ 0x80808080u, xv + 16 + 4 * c);
-                    }
-                    acc[m][r] = fmaf(d[r], (s0 + s1) - 128.f * sx, acc[m][r]);
-                }
-            }
-        }
-    }
-#pragma unroll
-    for (int m = 0; m < M; m++)
-#pragma unroll
-        for (int r = 0; r < R; r++) {
-            float v = wave_sum(acc[m][r]);
-            int64_t row = row0 + r;
-            if (lane == 0 && row < n) {
-                if (RES) v = res[m * n + row] + v;
-                y[m * n + row] = v;
-            }
-        }
-}
-
-template <int QT, int R, int M>
-static void launch_mv(const QWeight* w, const float* x, float* y, const float* res,
-                      hipStream_t s) {
-    dim3 grid((unsigned)cdiv(w->n, 4 * R));
-    if (res)
-        k_matvec<QT, R, M, true><<<grid, 256, 0, s>>>(w->qs, w->d, x, y, res, w->n, w->k, w->nb);
-    else
-        k_matvec<QT, R, M, false><<<grid, 256, 0, s>>>(w->qs, w->d, x, y, res, w->n, w->k, w->nb);
-}
-
-template <int QT, int M>
-static void launch_mv_r(const QWeight* w, const float* x, float* y, const float* res,
-                        hipStream_t s) {
-    if (w->n <= 2048)
-        launch_mv<QT, 1, M>(w, x, y, res, s);
-    else if (w->n <= 8192)
-        launch_mv<QT, 2, M>(w, x, y, res, s);
-    else
-        launch_mv<QT, 4, M>(w, x, y, res, s);
-}
-
-template <int QT>
-static void launch_mv_m(const QWeight* w, const float* x, float* y, int64_t m,
-                        const float* res, hipStream_t s) {
-    switch (m) {
-        case 1: launch_mv_r<QT, 1>(w, x, y, res, s); break;
-        case 2: launch_mv_r<QT, 2>(w, x, y, res, s); break;
-        case 3: launch_mv_r<QT, 3>(w, x, y, res, s); break;
-        default: launch_mv_r<QT, 4>(w, x, y, res, s); break;
-    }
-}
-
-int launch_quant_matvec(const QWeight* w, const float* x, float* y, int64_t m, hipStream_t s,
-                        const float* residual) {
-    if (m < 1 || m > 4) {
-        set_error(TL_HIP_ERR_ARG, "ArgumentError: matvec supports 1..4 rows, got %lld",
-                  (long long)m);
-        return TL_HIP_ERR_ARG;
-    }
-    if ((reinterpret_cast<uintptr_t>(x) & 15) != 0) {
-        set_error(TL_HIP_ERR_ARG, "ArgumentError: x must be 16-byte aligned");
-        return TL_HIP_ERR_ARG;
-    }
-    if (w->ggml_type == TL_HIP_GGML_Q4_0)
-        launch_mv_m<2>(w, x, y, m, residual, s);
-    else
-        launch_mv_m<8>(w, x, y, m, residual, s);
-    hipError_t e = hipGetLastError();
-    if (e != hipSuccess) return hip_fail(e, "matvec launch");
-    return TL_HIP_OK;
 }
 
 }  // namespace tlhip

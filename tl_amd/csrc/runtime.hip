@@ -298,6 +298,27 @@ int tl_hip_event_elapsed_ms(void* a, void* b, float* ms) {
     return TL_HIP_OK;
 }
 
+// One wavefront that sleeps for `us` microseconds of the 100 MHz constant clock
+// (s_memrealtime); the loop also stops after a fixed number of iterations, so it always ends.
+__global__ void k_stall(uint64_t ticks) {
+    const uint64_t t0 = __builtin_amdgcn_s_memrealtime();
+    for (int i = 0; i < (1 << 22); i++) {
+        if (__builtin_amdgcn_s_memrealtime() - t0 >= ticks) break;
+        __builtin_amdgcn_s_sleep(32);
+    }
+}
+
+int tl_hip_stall(uint32_t us) {
+    if (!state()) return tls_status;
+    if (us > 100000) {
+        set_error(TL_HIP_ERR_ARG, "ArgumentError: stall of %u us exceeds 100 ms", us);
+        return TL_HIP_ERR_ARG;
+    }
+    k_stall<<<1, 64, 0, cur_stream()>>>((uint64_t)us * 100);
+    TLH_CHECK_HIP(hipGetLastError());
+    return TL_HIP_OK;
+}
+
 int tl_hip_event_destroy(void* ev) {
     if (!ev) return TL_HIP_OK;
     TLH_CHECK_HIP(hipEventDestroy((hipEvent_t)ev));
