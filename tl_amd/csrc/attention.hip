@@ -5,15 +5,15 @@
 // read once, in place, and the Hq/Hkv query heads of a group share every K/V row loaded
 // (no repeat_interleave copy).
 //
-// One kernel: workgroup = (split, kv head, batch item), 4 wavefronts.  Eight lanes share a
+// Pass 1: workgroup = (split, kv head, batch item), 4 wavefronts.  Eight lanes share a
 // cache row (each owns D/8 consecutive dims), so a wavefront covers 8 positions per load
 // instruction and a workgroup 32.  The K and V rows of the first two 32-position steps are
 // requested at kernel start, so the chunk's memory latency overlaps the q load and the
 // score pass.  Scores go to LDS, each head's chunk max and exp-sum are formed, the
-// exp-weighted V rows are accumulated, and the (o, max, sum) record is written.  The last
-// workgroup of a (batch, kv head) to finish -- an arrival counter, no waiting -- merges the
-// records: out = sum_s o_s e^(m_s - M) / sum_s l_s e^(m_s - M).  A single split writes its
-// result directly.  All arithmetic is f32.
+// exp-weighted V rows are accumulated, and the (o, max, sum) record is written.  A second
+// small kernel merges the records of a (batch, kv head):
+// out = sum_s o_s e^(m_s - M) / sum_s l_s e^(m_s - M).  A single split writes its result
+// directly.  All arithmetic is f32.
 #include "internal.h"
 
 namespace tlhip {
@@ -57,6 +57,7 @@ struct KVLoad<float> {
 };
 
 constexpr int ATT_MAX_CHUNK = 1024;
+constexpr int ATT_MAX_SPLITS = 256;
 constexpr int ATT_PF = 2;  // 32-position steps whose K/V rows are requested up front
 
 // Cached length of batch item b: (len_dev ? *len_dev + len_add : L) + b * len_step.
@@ -77,7 +78,6 @@ struct AttnArgs {
     const void* v;
     float* out;      // [B, Hq, D]
     float* ws;       // [B, Hkv, nsplit, G, D + 2]
-    int32_t* counter;  // [B, Hkv], zero between launches
     int hkv;
     int64_t lmax, kv_bstride;
     AttnLen len;
@@ -91,7 +91,6 @@ __global__ __launch_bounds__(256) void k_attn(AttnArgs a) {
     __shared__ float sc[G][ATT_MAX_CHUNK];
     __shared__ float stat[G][2];
     __shared__ float part[4][G][D];
-    __shared__ int s_last;
     const int split = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int grp = lane >> 3, sub = lane & 7;
@@ -233,36 +232,52 @@ __global__ __launch_bounds__(256) void k_attn(AttnArgs a) {
             wr[tid * (D + 2) + D] = stat[tid][0];
             wr[tid * (D + 2) + D + 1] = stat[tid][1];
         }
-    } else if (a.nsplit == 1) {
-        return;  // (L == 0 is rejected on the host)
     }
-    // arrival: the last workgroup of this (batch, kv head) merges the records
-    __syncthreads();
-    if (tid == 0) {
-        __threadfence();  // this workgroup's record is visible device-wide before it is counted
-        const int prev = atomicAdd(a.counter + (int64_t)b * a.hkv + h, 1);
-        s_last = prev == a.nsplit - 1;
-    }
-    __syncthreads();
-    if (!s_last) return;
-    __threadfence();  // acquire: observe the other workgroups' records
+}
+
+// Merge of the split records of one (batch, kv head): the (max, sum) pairs of the active
+// splits are read in parallel into LDS, then each output element sums its o_s in split order.
+template <int D, int G>
+__global__ __launch_bounds__(256) void k_attn_merge(AttnArgs a) {
+    __shared__ float sm[G][ATT_MAX_SPLITS], sf[G][ATT_MAX_SPLITS], sden[G];
+    const int h = blockIdx.x, b = blockIdx.y, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    int64_t L = a.len.of(b);
+    if (L > a.lmax) L = a.lmax;
     const int nact = (int)((L + a.chunk - 1) / a.chunk);
+    const int64_t stride = (int64_t)G * (D + 2);
+    const float* base = a.ws + (((int64_t)b * a.hkv + h) * a.nsplit) * stride;
+    for (int idx = tid; idx < G * nact; idx += 256) {
+        const int g = idx / nact, s = idx % nact;
+        sm[g][s] = base[s * stride + g * (D + 2) + D];
+        sf[g][s] = base[s * stride + g * (D + 2) + D + 1];
+    }
+    __syncthreads();
+    // per head: M = max_s m_s, weights f_s = e^(m_s - M), den = sum_s l_s f_s
+    for (int g = wave; g < G; g += 4) {
+        float M = -INFINITY;
+        for (int s = lane; s < nact; s += 64) M = fmaxf(M, sm[g][s]);
+#pragma unroll
+        for (int off = 32; off >= 1; off >>= 1) M = fmaxf(M, __shfl_xor(M, off, 64));
+        float den = 0.f;
+        for (int s = lane; s < nact; s += 64) {
+            const float f = expf(sm[g][s] - M);
+            den = fmaf(sf[g][s], f, den);
+            sm[g][s] = f;
+        }
+#pragma unroll
+        for (int off = 32; off >= 1; off >>= 1) den += __shfl_xor(den, off, 64);
+        if (lane == 0) sden[g] = den;
+    }
+    __syncthreads();
+    const int hq = a.hkv * G;
     for (int idx = tid; idx < G * D; idx += 256) {
         const int g = idx / D, d = idx % D;
-        const float* r = a.ws + rec0 + (int64_t)g * (D + 2);
-        const int64_t stride = (int64_t)G * (D + 2);
-        float M = -INFINITY;
-        for (int s = 0; s < nact; s++) M = fmaxf(M, __builtin_nontemporal_load(r + s * stride + D));
-        float num = 0.f, den = 0.f;
-        for (int s = 0; s < nact; s++) {
-            const float* rs = r + s * stride;
-            const float f = expf(__builtin_nontemporal_load(rs + D) - M);
-            num = fmaf(__builtin_nontemporal_load(rs + d), f, num);
-            den = fmaf(__builtin_nontemporal_load(rs + D + 1), f, den);
-        }
-        a.out[((int64_t)b * hq + h * G + g) * D + d] = num / den;
+        const float* r = base + g * (D + 2) + d;
+        float num = 0.f;
+#pragma unroll 4
+        for (int s = 0; s < nact; s++) num = fmaf(r[s * stride], sm[g][s], num);
+        a.out[((int64_t)b * hq + h * G + g) * D + d] = num / sden[g];
     }
-    if (tid == 0) a.counter[(int64_t)b * a.hkv + h] = 0;  // ready for the next launch
 }
 
 // Split plan: about 1024 workgroups over (B x Hkv x splits); chunks a multiple of 32 and at
@@ -276,6 +291,10 @@ void attn_plan(int B, int hkv, int64_t L, int* chunk, int* nsplit) {
     if (c > ATT_MAX_CHUNK) c = ATT_MAX_CHUNK;
     *chunk = (int)c;
     *nsplit = (int)((L + c - 1) / c);
+    while (*nsplit > ATT_MAX_SPLITS) {  // very long caches: widen the chunk
+        c += 32;
+        *nsplit = (int)((L + c - 1) / c);
+    }
 }
 
 size_t attn_workspace_floats(int B, int hkv, int G, int D, int nsplit) {
@@ -286,11 +305,12 @@ template <typename KVT>
 static int attn_dispatch(const AttnArgs& a, int B, int hq, int D, hipStream_t s) {
     const int G = hq / a.hkv;
     dim3 grid(a.nsplit, a.hkv, B);
-#define TLH_ATT(DD, GG)                                  \
-    if (D == DD && G == GG) {                            \
-        k_attn<DD, GG, KVT><<<grid, 256, 0, s>>>(a);     \
-        hipError_t e = hipGetLastError();                \
-        return e == hipSuccess ? TL_HIP_OK : hip_fail(e, "attention launch"); \
+#define TLH_ATT(DD, GG)                                                          \
+    if (D == DD && G == GG) {                                                    \
+        k_attn<DD, GG, KVT><<<grid, 256, 0, s>>>(a);                             \
+        if (a.nsplit > 1) k_attn_merge<DD, GG><<<dim3(a.hkv, B), 256, 0, s>>>(a); \
+        hipError_t e = hipGetLastError();                                        \
+        return e == hipSuccess ? TL_HIP_OK : hip_fail(e, "attention launch");    \
     }
     TLH_ATT(128, 1) TLH_ATT(128, 2) TLH_ATT(128, 4) TLH_ATT(128, 8)
     TLH_ATT(64, 1) TLH_ATT(64, 2) TLH_ATT(64, 4) TLH_ATT(64, 8)
@@ -301,14 +321,18 @@ static int attn_dispatch(const AttnArgs& a, int B, int hq, int D, hipStream_t s)
 }
 
 int launch_attention(const float* q, const void* k, const void* v, int kv_dtype, float* out,
-                     float* ws, int32_t* counter, int B, int hq, int hkv, int D, int64_t lmax,
+                     float* ws, int B, int hq, int hkv, int D, int64_t lmax,
                      int64_t kv_bstride, int64_t L, const int32_t* len_dev, int len_add,
                      int len_step, int chunk, int nsplit, float scale, hipStream_t s) {
     if (chunk > ATT_MAX_CHUNK || chunk % 32) {
         set_error(TL_HIP_ERR_ARG, "ArgumentError: attention chunk %d", chunk);
         return TL_HIP_ERR_ARG;
     }
-    AttnArgs a{q, k, v, out, ws, counter, hkv, lmax, kv_bstride, AttnLen{L, len_dev, len_add, len_step},
+    if (nsplit > ATT_MAX_SPLITS) {
+        set_error(TL_HIP_ERR_ARG, "ArgumentError: %d attention splits exceed %d", nsplit, ATT_MAX_SPLITS);
+        return TL_HIP_ERR_ARG;
+    }
+    AttnArgs a{q, k, v, out, ws, hkv, lmax, kv_bstride, AttnLen{L, len_dev, len_add, len_step},
                chunk, nsplit, scale};
     if (kv_dtype == TL_HIP_F16) return attn_dispatch<__half>(a, B, hq, D, s);
     return attn_dispatch<float>(a, B, hq, D, s);
@@ -365,17 +389,11 @@ extern "C" tl_hip_tensor* tl_hip_attention_decode(const tl_hip_tensor* qh, const
     if (!o) return nullptr;
     hipStream_t s = cur_stream();
     float* ws = (float*)dev_alloc(attn_workspace_floats((int)B, (int)hkv, (int)(hq / hkv), (int)D, nsplit) * 4);
-    int32_t* cnt = (int32_t*)dev_alloc((size_t)B * hkv * 4);
-    int rc = ws && cnt ? TL_HIP_OK : TL_HIP_ERR_ALLOC;
-    if (rc == TL_HIP_OK) {
-        hipError_t e = hipMemsetAsync(cnt, 0, (size_t)B * hkv * 4, s);
-        rc = e == hipSuccess ? TL_HIP_OK : hip_fail(e, "hipMemsetAsync(counters)");
-    }
+    int rc = ws ? TL_HIP_OK : TL_HIP_ERR_ALLOC;
     if (rc == TL_HIP_OK)
-        rc = launch_attention(q->f32(), k->data, v->data, k->dtype, o->f32(), ws, cnt, (int)B, (int)hq, (int)hkv,
+        rc = launch_attention(q->f32(), k->data, v->data, k->dtype, o->f32(), ws, (int)B, (int)hq, (int)hkv,
                               (int)D, lmax, hkv * lmax * D, L, nullptr, 0, 0, chunk, nsplit, scale, s);
     dev_free(ws);  // stream-ordered: reused only by later work on the same stream
-    dev_free(cnt);
     if (rc != TL_HIP_OK) {
         tensor_drop(o);
         return nullptr;

@@ -103,7 +103,6 @@ struct MvArgs {
     float* part_v;        // per-workgroup best value
     int32_t* part_i;      // per-workgroup best index
     int32_t* part_nan;    // per-workgroup NaN flag
-    int32_t* counter;     // arrival counter (zero between launches)
     int32_t* tok_out;
     int32_t* out_ids;
     int32_t* step;
@@ -143,9 +142,8 @@ int launch_rope_table(float* out, int64_t seq_len, int64_t dim, float base, int 
                       hipStream_t s);
 // Attention over a [B?, Hkv, lmax, D] cache (kv_bstride elements between batch items, 0 =
 // shared).  Cached length of item b = (len_dev ? *len_dev + len_add : L) + b * len_step.
-// `counter` holds B * hkv ints that are zero before the launch (and zero again after it).
 int launch_attention(const float* q, const void* k, const void* v, int kv_dtype, float* out,
-                     float* ws, int32_t* counter, int B, int hq, int hkv, int D, int64_t lmax,
+                     float* ws, int B, int hq, int hkv, int D, int64_t lmax,
                      int64_t kv_bstride, int64_t L, const int32_t* len_dev, int len_add,
                      int len_step, int chunk, int nsplit, float scale, hipStream_t s);
 void attn_plan(int B, int hkv, int64_t L, int* chunk, int* nsplit);

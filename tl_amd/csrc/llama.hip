@@ -94,18 +94,6 @@ __global__ void k_advance(int32_t* pos, int n) {
     if (threadIdx.x == 0 && blockIdx.x == 0) *pos += n;
 }
 
-// end of a decode step: record the sampled id, mark it for the repetition penalty,
-// advance the step counter
-__global__ void k_step_end(const int32_t* __restrict__ tok, int32_t* __restrict__ out_ids,
-                           int32_t* __restrict__ step, uint8_t* __restrict__ seen, int max_out) {
-    if (threadIdx.x == 0 && blockIdx.x == 0) {
-        int s = *step;
-        if (s < max_out) out_ids[s] = *tok;
-        if (seen) seen[*tok] = 1;
-        *step = s + 1;
-    }
-}
-
 struct Llama {
     int nl, D, H, KV, hd, F, V, max_seq;
     float eps, theta;
@@ -127,10 +115,9 @@ struct Llama {
     size_t ws_floats = 0;
     int32_t *ids = nullptr, *pos = nullptr, *tok = nullptr, *step = nullptr, *out_ids = nullptr;
     uint8_t* seen = nullptr;
-    int32_t* att_cnt = nullptr;  // attention arrival counters [max_tok * KV]
-    // greedy-argmax partials of the LM-head matvec (one per workgroup) and its counter
+    // greedy-argmax candidates of the LM-head matvec (one per workgroup)
     float* am_v = nullptr;
-    int32_t *am_i = nullptr, *am_nan = nullptr, *am_cnt = nullptr;
+    int32_t *am_i = nullptr, *am_nan = nullptr;
     int max_out = 0;
     int64_t host_pos = 0;
     hipGraphExec_t graph = nullptr;
@@ -171,7 +158,6 @@ static int ensure_tokens(Llama* m, int64_t n) {
     }
     dev_free(m->ids);
     dev_free(m->ws);
-    dev_free(m->att_cnt);
     const int64_t qkv_w = m->D + 2 * (int64_t)m->KV * m->hd;
     m->x = (float*)dev_alloc(n * m->D * 4);
     m->h = (float*)dev_alloc(n * m->D * 4);
@@ -186,11 +172,9 @@ static int ensure_tokens(Llama* m, int64_t n) {
     int nsplit = (int)cdiv(m->max_seq, 64);
     m->ws_floats = attn_workspace_floats((int)n, m->KV, m->H / m->KV, m->hd, nsplit);
     m->ws = (float*)dev_alloc(m->ws_floats * 4);
-    m->att_cnt = (int32_t*)dev_alloc((size_t)n * m->KV * 4);
     for (float** b : bufs)
         if (!*b) return TL_HIP_ERR_ALLOC;
-    if (!m->ids || !m->ws || !m->att_cnt) return TL_HIP_ERR_ALLOC;
-    TLH_CHECK_HIP(hipMemsetAsync(m->att_cnt, 0, (size_t)n * m->KV * 4, cur_stream()));
+    if (!m->ids || !m->ws) return TL_HIP_ERR_ALLOC;
     m->max_tok = n;
     free_graph(m);  // captured pointers changed
     return TL_HIP_OK;
@@ -270,7 +254,8 @@ static int enqueue_forward(Llama* m, int n, int f16, hipStream_t s) {
     int rc;
     k_embed<<<cdiv(n * D, 256), 256, 0, s>>>(m->emb, m->ids, m->x, n, D);
     const int G = m->H / m->KV;
-    const int nsplit = (int)cdiv(m->max_seq, 64);
+    // splits of 64 positions up to the longest length of this call (host-known here)
+    const int nsplit = (int)cdiv(m->host_pos + n, 64);
     for (int l = 0; l < m->nl; l++) {
         if ((rc = launch_rmsnorm(m->x, nullptr, m->attn_norm[l], m->h, n, D, m->eps, 0, s))) return rc;
         if ((rc = linear(m->wqkv[l], m->h, m->qkv, n, nullptr, nullptr, f16, s))) return rc;
@@ -285,7 +270,7 @@ static int enqueue_forward(Llama* m, int n, int f16, hipStream_t s) {
                                                             m->max_seq, m->rope_per_token);
         // query i (absolute position pos + i) attends cache positions 0 .. pos + i
         if ((rc = launch_attention(m->q, m->kc[l], m->vc[l], m->kv_f16 ? TL_HIP_F16 : TL_HIP_F32, m->ao,
-                                   m->ws, m->att_cnt, n, m->H, m->KV, (int)hd, m->max_seq, 0, 0, m->pos, 1, 1,
+                                   m->ws, n, m->H, m->KV, (int)hd, m->max_seq, 0, 0, m->pos, 1, 1,
                                    64, nsplit, 1.0f / sqrtf((float)hd), s)))
             return rc;
         (void)G;
@@ -338,7 +323,7 @@ static int enqueue_step(Llama* m, float penalty, hipStream_t s) {
         a.max_seq = m->max_seq;
         if ((rc = launch_mv(m->wqkv[l], a, 1, EPI_ROPE_KV, true, l == 0, s))) return rc;
         if ((rc = launch_attention(m->q, m->kc[l], m->vc[l], m->kv_f16 ? TL_HIP_F16 : TL_HIP_F32, m->ao, m->ws,
-                                   m->att_cnt, 1, m->H, m->KV, (int)hd, m->max_seq, 0, 0, m->pos, 1, 0, 64,
+                                   1, m->H, m->KV, (int)hd, m->max_seq, 0, 0, m->pos, 1, 0, 64,
                                    nsplit, 1.0f / sqrtf((float)hd), s)))
             return rc;
         MvArgs o = {};
@@ -370,7 +355,6 @@ static int enqueue_step(Llama* m, float penalty, hipStream_t s) {
     h.part_v = m->am_v;
     h.part_i = m->am_i;
     h.part_nan = m->am_nan;
-    h.counter = m->am_cnt;
     h.tok_out = m->tok;
     h.out_ids = m->out_ids;
     h.step = m->step;
@@ -427,11 +411,9 @@ tl_hip_llama* tl_hip_llama_new(int n_layers, int d_model, int n_heads, int n_kv_
     m->am_v = (float*)dev_alloc((size_t)parts * 4);
     m->am_i = (int32_t*)dev_alloc((size_t)parts * 4);
     m->am_nan = (int32_t*)dev_alloc((size_t)parts * 4);
-    m->am_cnt = (int32_t*)dev_alloc(4);
     int rc = (m->cos_t && m->sin_t && m->logits && m->plogits && m->pos && m->tok && m->step && m->seen &&
-              m->am_v && m->am_i && m->am_nan && m->am_cnt)
+              m->am_v && m->am_i && m->am_nan)
                  ? TL_HIP_OK : TL_HIP_ERR_ALLOC;
-    if (rc == TL_HIP_OK && hipMemsetAsync(m->am_cnt, 0, 4, s) != hipSuccess) rc = hip_fail(hipGetLastError(), "memset");
     if (rc == TL_HIP_OK) rc = launch_rope_table(m->cos_t, max_seq, m->hd, rope_theta, 0, s);
     if (rc == TL_HIP_OK) rc = launch_rope_table(m->sin_t, max_seq, m->hd, rope_theta, 1, s);
     if (rc == TL_HIP_OK) rc = alloc_kv(m);
@@ -465,7 +447,7 @@ int tl_hip_llama_free(tl_hip_llama* h) {
     for (void* p : m->vc) dev_free(p);
     void* bufs[] = {m->out_norm, m->emb, m->cos_t, m->sin_t, m->x, m->h, m->qkv, m->q, m->ao, m->t, m->gu,
                     m->act, m->logits, m->plogits, m->ws, m->ids, m->pos, m->tok, m->step, m->out_ids, m->seen,
-                    m->att_cnt, m->am_v, m->am_i, m->am_nan, m->am_cnt};
+                    m->am_v, m->am_i, m->am_nan};
     for (void* p : bufs) dev_free(p);
     delete m;
     return TL_HIP_OK;

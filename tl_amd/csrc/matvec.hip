@@ -23,9 +23,9 @@
 //                         device position (ffi.rs:2655-2681), q written out, k and v appended
 //                         to the KV cache at that position (chatbot.tl:56-69)
 //             EPI_ARGMAX  logits written, optional repetition penalty (device_impl.rs:967-1001),
-//                         greedy token (last maximum, tensor.rs:1633-1637) reduced across
-//                         workgroups by the last one to finish; it also advances the decode
-//                         position and records the token.
+//                         per-workgroup greedy candidates; a one-workgroup kernel reduces
+//                         them (last maximum, tensor.rs:1633-1637), records the token and
+//                         advances the decode position.
 #include "internal.h"
 
 namespace tlhip {
@@ -262,7 +262,6 @@ __global__ __launch_bounds__(256) void k_mv(MvArgs a) {
             }
         }
     } else if constexpr (EPI == EPI_ARGMAX) {
-        __shared__ int s_last;
         // logits, penalised logits, then this workgroup's greedy candidate (the left fold of
         // tensor.rs:1633-1637 over its rows: keep the best only when strictly greater)
         if (tid < 4 * R) {
@@ -291,69 +290,67 @@ __global__ __launch_bounds__(256) void k_mv(MvArgs a) {
             a.part_v[blockIdx.x] = bv;
             a.part_i[blockIdx.x] = (int32_t)(wg_row0 + bi);
             a.part_nan[blockIdx.x] = nan;
-            __threadfence();  // partials visible device-wide before this workgroup is counted
-            const int prev = atomicAdd(a.counter, 1);
-            s_last = prev == (int)gridDim.x - 1;
         }
-        __syncthreads();
-        if (!s_last) return;
-        __threadfence();  // acquire: observe every other workgroup's partials
-        // the last workgroup: fold the partials in workgroup order (NaN-free case: the
-        // (greater value, then larger index) reduction equals the left fold)
-        const int nwg = gridDim.x;
-        float bv = -INFINITY;
-        int bi = -1, nan = 0;
-        for (int i = tid; i < nwg; i += 256) {
-            const float v = __builtin_nontemporal_load(a.part_v + i);
-            const int ix = __builtin_nontemporal_load(a.part_i + i);
-            nan |= __builtin_nontemporal_load(a.part_nan + i);
-            if (bi < 0 || !(bv > v)) {
-                bv = v;
-                bi = ix;
-            }
+    }
+}
+
+// Greedy token from the per-workgroup candidates of an EPI_ARGMAX matvec (one workgroup):
+// the candidates are folded in workgroup order; for NaN-free input the (greater value, then
+// larger index) reduction equals the left fold of tensor.rs:1633-1637, otherwise thread 0
+// replays that fold over the penalised logits.  Then the decode-step bookkeeping: token
+// recorded, penalty mask updated, position advanced.
+__global__ __launch_bounds__(256) void k_argmax_finish(MvArgs a, int nwg) {
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    float bv = -INFINITY;
+    int bi = -1, nan = 0;
+    for (int i = tid; i < nwg; i += 256) {
+        const float v = a.part_v[i];
+        const int ix = a.part_i[i];
+        nan |= a.part_nan[i];
+        if (bi < 0 || !(bv > v)) {
+            bv = v;
+            bi = ix;
         }
+    }
 #pragma unroll
-        for (int off = 32; off >= 1; off >>= 1) {
-            const float ov = __shfl_xor(bv, off, 64);
-            const int oi = __shfl_xor(bi, off, 64);
-            if (oi >= 0 && (bi < 0 || ov > bv || (ov == bv && oi > bi))) {
-                bv = ov;
-                bi = oi;
-            }
-            nan |= __shfl_xor(nan, off, 64);
+    for (int off = 32; off >= 1; off >>= 1) {
+        const float ov = __shfl_xor(bv, off, 64);
+        const int oi = __shfl_xor(bi, off, 64);
+        if (oi >= 0 && (bi < 0 || ov > bv || (ov == bv && oi > bi))) {
+            bv = ov;
+            bi = oi;
         }
-        __shared__ float fv[4];
-        __shared__ int fi[4], fn[4];
-        if (lane == 0) {
-            fv[wave] = bv;
-            fi[wave] = bi;
-            fn[wave] = nan;
+        nan |= __shfl_xor(nan, off, 64);
+    }
+    __shared__ float fv[4];
+    __shared__ int fi[4], fn[4];
+    if (lane == 0) {
+        fv[wave] = bv;
+        fi[wave] = bi;
+        fn[wave] = nan;
+    }
+    __syncthreads();
+    if (tid == 0) {
+        for (int i = 1; i < 4; i++) {
+            if (fi[i] >= 0 && (bi < 0 || fv[i] > bv || (fv[i] == bv && fi[i] > bi))) {
+                bv = fv[i];
+                bi = fi[i];
+            }
+            nan |= fn[i];
         }
-        __syncthreads();
-        if (tid == 0) {
-            for (int i = 1; i < 4; i++) {
-                if (fi[i] >= 0 && (bi < 0 || fv[i] > bv || (fv[i] == bv && fi[i] > bi))) {
-                    bv = fv[i];
-                    bi = fi[i];
-                }
-                nan |= fn[i];
-            }
-            if (nan) {  // non-associative case: replay the sequential fold
-                bi = 0;
-                for (int64_t i = 1; i < n; i++)
-                    if (!(__builtin_nontemporal_load(a.plogits + bi) > __builtin_nontemporal_load(a.plogits + i)))
-                        bi = (int)i;
-            }
-            *a.tok_out = bi;
-            if (a.out_ids) {
-                const int s = *a.step;
-                if (s < a.max_out) a.out_ids[s] = bi;
-                *a.step = s + 1;
-            }
-            if (a.seen_out) a.seen_out[bi] = 1;
-            if (a.pos_inc) *a.pos_inc += 1;
-            *a.counter = 0;  // ready for the next launch
+        if (nan) {  // non-associative case: replay the sequential fold
+            bi = 0;
+            for (int64_t i = 1; i < a.n; i++)
+                if (!(a.plogits[bi] > a.plogits[i])) bi = (int)i;
         }
+        *a.tok_out = bi;
+        if (a.out_ids) {
+            const int s = *a.step;
+            if (s < a.max_out) a.out_ids[s] = bi;
+            *a.step = s + 1;
+        }
+        if (a.seen_out) a.seen_out[bi] = 1;
+        if (a.pos_inc) *a.pos_inc += 1;
     }
 }
 
@@ -376,6 +373,7 @@ static int run(const MvArgs& a, hipStream_t s) {
     }
     const unsigned grid = (unsigned)cdiv(a.n, 4 * R);
     kern<<<grid, 256, lds, s>>>(a);
+    if constexpr (EPI == EPI_ARGMAX) k_argmax_finish<<<1, 256, 0, s>>>(a, (int)grid);
     hipError_t e = hipGetLastError();
     return e == hipSuccess ? TL_HIP_OK : hip_fail(e, "matvec launch");
 }
