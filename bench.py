@@ -122,6 +122,8 @@ def main():
     ap.add_argument("--kv", choices=["f16", "f32"], default="f16")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-graph", action="store_true", help="eager launches instead of hipGraph replay")
+    ap.add_argument("--matvec-only", action="store_true",
+                    help="only the 4096x4096 matvec timing plus a 64 MiB device copy (counter runs)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU: this build has no multi-GPU path (every box has one GPU); "
@@ -140,6 +142,18 @@ def main():
     avg_s = bench_matvec(dev)
     achieved = MATVEC_BYTES / avg_s / 1e9
     log(f"[bench] matvec avg {avg_s * 1e6:.2f} us -> {achieved:.0f} GB/s")
+    if args.matvec_only:
+        # reference dispatch for the FETCH_SIZE / WRITE_SIZE scale: a device copy of 64 MiB
+        import ctypes as C
+        nbytes = 64 << 20
+        src, dst = dev.lib.tl_hip_malloc(nbytes), dev.lib.tl_hip_malloc(nbytes)
+        dev.lib.tl_hip_memcpy_d2d(C.c_void_p(dst), C.c_void_p(src), nbytes)
+        dev.synchronize()
+        dev.lib.tl_hip_free(C.c_void_p(src))
+        dev.lib.tl_hip_free(C.c_void_p(dst))
+        print(json.dumps({"matvec_avg_us": round(avg_s * 1e6, 3), "matvec_gbs": round(achieved, 1),
+                          "copy_bytes": nbytes}), flush=True)
+        return
 
     log("[bench] generating synthetic TinyLlama-shape Q4_0 weights ...")
     t0 = time.time()

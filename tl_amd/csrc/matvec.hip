@@ -51,9 +51,20 @@ __device__ __forceinline__ float dot4b(uint32_t q, const float* x) {
     return s;
 }
 
+template <int CTRL>
+__device__ __forceinline__ float dpp_mov(float v) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), CTRL, 0xF, 0xF, true));
+}
+// Sum over the 64 lanes of a wavefront: DPP within rows of 16 (quad_perm 1-0-3-2 and
+// 2-3-0-1, half-row and row mirrors -- VALU ops, no LDS traffic), then two cross-row
+// exchanges through ds_bpermute.  Every lane receives the total.
 __device__ __forceinline__ float wsum(float v) {
-#pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off, 64);
+    v += dpp_mov<0xB1>(v);
+    v += dpp_mov<0x4E>(v);
+    v += dpp_mov<0x141>(v);
+    v += dpp_mov<0x140>(v);
+    v += __shfl_xor(v, 16, 64);
+    v += __shfl_xor(v, 32, 64);
     return v;
 }
 
