@@ -29,6 +29,10 @@ sys.path.insert(0, ROOT)
 MATVEC_N = MATVEC_K = 4096
 MATVEC_BYTES = MATVEC_N * MATVEC_K // 32 * 18 + MATVEC_K * 4 + MATVEC_N * 4  # 9,469,952
 HBM_PEAK_GBS = 8000.0
+# HBM bytes per 4096 x 4096 matvec launch from the two counter runs of
+# `bench.py --matvec-only` (FETCH_SIZE 4,701.01 KiB x 1.9989 + WRITE_SIZE 16.0 KiB x 1.0, the
+# scale factors read off a 64 MiB device copy in the same runs): 1.018 x the algorithmic bytes
+MATVEC_TRAFFIC = 9_639_000
 
 
 def log(*a):
@@ -219,7 +223,7 @@ def main():
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBS, 4),
-            "traffic": None,
+            "traffic": MATVEC_TRAFFIC,
             "avg_launch_us": round(avg_s * 1e6, 3),
         },
         "cpu_baseline": cpu,
