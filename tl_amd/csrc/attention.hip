@@ -280,6 +280,406 @@ __global__ __launch_bounds__(256) void k_attn_merge(AttnArgs a) {
     }
 }
 
+// ------------------------------------------------------------------------------------------
+// Decode form for 4 or 8 query heads per KV head: splits of 64 positions, no cross-lane
+// reductions in the inner loops.
+//   scores: lane = position; the lane reads its whole K row (D/8 16-byte loads) and takes
+//           the dot products with the q rows of its wavefront's heads (LDS broadcast reads);
+//   softmax over the 64 positions of the split: one wavefront max and sum per head;
+//   P.V:    lane = (dim group dg = lane / 8, slot = lane % 8): positions slot, slot+8, ...,
+//           D/8 dims each; the 8 slots are summed with DPP at the end.
+// Wavefront w owns heads w*G/4 .. (w+1)*G/4 - 1.  Splits past the cached length exit at once.
+// With FUSED, the last active split of a (batch, kv head) to finish -- an arrival counter,
+// no waiting -- merges the records, so a decode step needs one launch; otherwise
+// k_attn_merge does it.
+template <int CTRL>
+__device__ __forceinline__ float dpp_f(float v) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), CTRL, 0xF, 0xF, true));
+}
+__device__ __forceinline__ float sum8_dpp(float v) {  // over aligned groups of 8 lanes
+    v += dpp_f<0xB1>(v);   // quad_perm [1,0,3,2]
+    v += dpp_f<0x4E>(v);   // quad_perm [2,3,0,1]
+    v += dpp_f<0x141>(v);  // row_half_mirror
+    return v;
+}
+__device__ __forceinline__ float wave_max64(float v) {
+    v = fmaxf(v, dpp_f<0xB1>(v));
+    v = fmaxf(v, dpp_f<0x4E>(v));
+    v = fmaxf(v, dpp_f<0x141>(v));
+    v = fmaxf(v, dpp_f<0x140>(v));
+    v = fmaxf(v, __shfl_xor(v, 16, 64));
+    v = fmaxf(v, __shfl_xor(v, 32, 64));
+    return v;
+}
+__device__ __forceinline__ float wave_sum64(float v) {
+    v += dpp_f<0xB1>(v);
+    v += dpp_f<0x4E>(v);
+    v += dpp_f<0x141>(v);
+    v += dpp_f<0x140>(v);
+    v += __shfl_xor(v, 16, 64);
+    v += __shfl_xor(v, 32, 64);
+    return v;
+}
+
+template <typename KVT>
+__device__ __forceinline__ void cvt8(const uint4& w, float* f);
+template <>
+__device__ __forceinline__ void cvt8<__half>(const uint4& w, float* f) {
+    const uint32_t u[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+        const float2 t = __half22float2(*reinterpret_cast<const __half2*>(&u[j]));
+        f[2 * j] = t.x;
+        f[2 * j + 1] = t.y;
+    }
+}
+
+constexpr int DEC_C = 64;           // positions per split in the decode form
+constexpr int DEC_MAX_FUSED = 32;   // splits the in-kernel merge handles (2048 positions)
+
+template <int D, int G, bool FUSED>
+__global__ __launch_bounds__(256) void k_attn_dec(AttnArgs a, int32_t* counter) {
+    using KVT = __half;
+    constexpr int HPW = G / 4;   // heads per wavefront
+    constexpr int DL = D / 8;    // dims per lane in P.V
+    constexpr int KC = D / 8;    // 16-byte chunks of a K row
+    __shared__ __attribute__((aligned(16))) float qsh[G][D];
+    __shared__ float P[G][DEC_C];
+    __shared__ float stat[G][2];
+    __shared__ int s_last;
+    const int split = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    int64_t L = a.len.of(b);
+    if (L > a.lmax) L = a.lmax;
+    const int64_t p0 = (int64_t)split * DEC_C;
+    if (p0 >= L) return;  // inactive split (uniform per workgroup)
+    const int nact = (int)((L + DEC_C - 1) / DEC_C);
+    const int hq = a.hkv * G;
+    const KVT* kb = reinterpret_cast<const KVT*>(a.k) + (int64_t)b * a.kv_bstride + (int64_t)h * a.lmax * D;
+    const KVT* vb = reinterpret_cast<const KVT*>(a.v) + (int64_t)b * a.kv_bstride + (int64_t)h * a.lmax * D;
+
+    // K row of this lane's position and the V slices of its P.V positions, requested first
+    const int64_t pk = p0 + lane;
+    const bool kvalid = pk < L;
+    const int64_t pkc = kvalid ? pk : L - 1;
+    uint4 kraw[KC];
+#pragma unroll
+    for (int c = 0; c < KC; c++) kraw[c] = reinterpret_cast<const uint4*>(kb + pkc * D)[c];
+    const int slot = lane & 7, dg = lane >> 3;
+    uint4 vraw[8][DL / 8];
+#pragma unroll
+    for (int j = 0; j < 8; j++) {
+        int64_t pv = p0 + slot + 8 * j;
+        pv = pv < L ? pv : L - 1;
+#pragma unroll
+        for (int c = 0; c < DL / 8; c++) vraw[j][c] = reinterpret_cast<const uint4*>(vb + pv * D + dg * DL)[c];
+    }
+    // q rows of this wavefront's heads -> LDS
+    const float* qg = a.q + ((int64_t)b * hq + h * G + wave * HPW) * D;
+    for (int i = lane; i < HPW * D / 4; i += 64)
+        *reinterpret_cast<float4*>(&qsh[wave * HPW][0] + 4 * i) = reinterpret_cast<const float4*>(qg)[i];
+    __syncthreads();
+
+    // scores of this lane's position for the wavefront's heads
+    float s[HPW];
+#pragma unroll
+    for (int hh = 0; hh < HPW; hh++) s[hh] = 0.f;
+#pragma unroll
+    for (int c = 0; c < KC; c++) {
+        float kf[8];
+        cvt8<KVT>(kraw[c], kf);
+#pragma unroll
+        for (int hh = 0; hh < HPW; hh++) {
+            const float4 q0 = *reinterpret_cast<const float4*>(&qsh[wave * HPW + hh][8 * c]);
+            const float4 q1 = *reinterpret_cast<const float4*>(&qsh[wave * HPW + hh][8 * c + 4]);
+            float t = s[hh];
+            t = fmaf(q0.x, kf[0], t);
+            t = fmaf(q0.y, kf[1], t);
+            t = fmaf(q0.z, kf[2], t);
+            t = fmaf(q0.w, kf[3], t);
+            t = fmaf(q1.x, kf[4], t);
+            t = fmaf(q1.y, kf[5], t);
+            t = fmaf(q1.z, kf[6], t);
+            t = fmaf(q1.w, kf[7], t);
+            s[hh] = t;
+        }
+    }
+    // softmax over the split's positions, per head
+    float mh[HPW], lh[HPW];
+#pragma unroll
+    for (int hh = 0; hh < HPW; hh++) {
+        const float sc = kvalid ? s[hh] * a.scale : -INFINITY;
+        const float m = wave_max64(sc);
+        const float e = kvalid ? expf(sc - m) : 0.f;
+        mh[hh] = m;
+        lh[hh] = wave_sum64(e);
+        P[wave * HPW + hh][lane] = e;
+    }
+    __syncthreads();
+    // P.V over the split: lane (dg, slot) takes positions slot + 8j
+    float o[HPW][DL];
+#pragma unroll
+    for (int hh = 0; hh < HPW; hh++)
+#pragma unroll
+        for (int i = 0; i < DL; i++) o[hh][i] = 0.f;
+#pragma unroll
+    for (int j = 0; j < 8; j++) {
+        float vf[DL];
+#pragma unroll
+        for (int c = 0; c < DL / 8; c++) cvt8<KVT>(vraw[j][c], vf + 8 * c);
+#pragma unroll
+        for (int hh = 0; hh < HPW; hh++) {
+            const float e = P[wave * HPW + hh][slot + 8 * j];
+#pragma unroll
+            for (int i = 0; i < DL; i++) o[hh][i] = fmaf(e, vf[i], o[hh][i]);
+        }
+    }
+#pragma unroll
+    for (int hh = 0; hh < HPW; hh++)
+#pragma unroll
+        for (int i = 0; i < DL; i++) o[hh][i] = sum8_dpp(o[hh][i]);
+
+    // a single split normalises and stores directly (with FUSED: a single active split)
+    if (FUSED ? nact == 1 : a.nsplit == 1) {
+        if (slot == 0) {
+#pragma unroll
+            for (int hh = 0; hh < HPW; hh++)
+#pragma unroll
+                for (int i = 0; i < DL; i++)
+                    a.out[((int64_t)b * hq + h * G + wave * HPW + hh) * D + dg * DL + i] = o[hh][i] / lh[hh];
+        }
+        return;
+    }
+    const int64_t rec0 = (((int64_t)b * a.hkv + h) * a.nsplit) * G * (D + 2);
+    float* wr = a.ws + rec0 + (int64_t)split * G * (D + 2);
+    if (slot == 0) {
+#pragma unroll
+        for (int hh = 0; hh < HPW; hh++)
+#pragma unroll
+            for (int i = 0; i < DL; i++) wr[(wave * HPW + hh) * (D + 2) + dg * DL + i] = o[hh][i];
+    }
+    if (lane == 0) {
+#pragma unroll
+        for (int hh = 0; hh < HPW; hh++) {
+            wr[(wave * HPW + hh) * (D + 2) + D] = mh[hh];
+            wr[(wave * HPW + hh) * (D + 2) + D + 1] = lh[hh];
+        }
+    }
+    if constexpr (!FUSED) return;
+    __syncthreads();
+    if (tid == 0) {
+        __threadfence();  // this split's record is visible device-wide before it is counted
+        const int prev = atomicAdd(counter + (int64_t)b * a.hkv + h, 1);
+        s_last = prev == nact - 1;
+    }
+    __syncthreads();
+    if (!s_last) return;
+    __threadfence();  // acquire: observe the other splits' records
+    // merge: every load is issued before any is consumed (one memory round trip)
+    constexpr int OPT = G * D / 256;  // outputs per thread
+    __shared__ float sm[G][DEC_MAX_FUSED], sf[G][DEC_MAX_FUSED], sden[G];
+    const int64_t stride = (int64_t)G * (D + 2);
+    const float* r0 = a.ws + rec0;
+    float ov[OPT][DEC_MAX_FUSED];
+#pragma unroll
+    for (int u = 0; u < OPT; u++) {
+        const int idx = tid + u * 256, g = idx / D, d = idx % D;
+#pragma unroll
+        for (int sp = 0; sp < DEC_MAX_FUSED; sp++)
+            if (sp < nact) ov[u][sp] = r0[sp * stride + g * (D + 2) + d];
+    }
+    for (int idx = tid; idx < G * nact; idx += 256) {
+        const int g = idx / nact, sp = idx % nact;
+        sm[g][sp] = r0[sp * stride + g * (D + 2) + D];
+        sf[g][sp] = r0[sp * stride + g * (D + 2) + D + 1];
+    }
+    __syncthreads();
+    for (int g = wave; g < G; g += 4) {  // per head: M, weights e^(m_s - M), denominator
+        const float mv = lane < nact ? sm[g][lane] : -INFINITY;
+        const float M = wave_max64(mv);
+        const float f = lane < nact ? expf(mv - M) : 0.f;
+        const float den = wave_sum64(lane < nact ? sf[g][lane] * f : 0.f);
+        if (lane < nact) sm[g][lane] = f;
+        if (lane == 0) sden[g] = den;
+    }
+    __syncthreads();
+#pragma unroll
+    for (int u = 0; u < OPT; u++) {
+        const int idx = tid + u * 256, g = idx / D, d = idx % D;
+        float num = 0.f;
+#pragma unroll
+        for (int sp = 0; sp < DEC_MAX_FUSED; sp++)
+            if (sp < nact) num = fmaf(ov[u][sp], sm[g][sp], num);
+        a.out[((int64_t)b * hq + h * G + g) * D + d] = num / sden[g];
+    }
+    if (tid == 0) counter[(int64_t)b * a.hkv + h] = 0;  // ready for the next launch
+}
+
+// ------------------------------------------------------------------------------------------
+// Short-cache decode form: one workgroup per (query head, batch item) over all cached
+// positions, so no cross-workgroup merge exists.  The KV head's rows are read by the
+// Hq/Hkv workgroups of its group (the re-reads hit L2 / MALL); for caches of a few thousand
+// positions that costs less than a merge pass.  Eight wavefronts take 64-position chunks in
+// turn (lane = position for the scores, q held in registers -- it is uniform), keep an
+// online softmax (running max m, sum l, rescaled accumulators), and compute P.V with
+// lane = (dim group, slot); the next chunk's K and V rows are requested before the current
+// chunk is consumed.  The eight (m, l, o) states are merged through LDS.
+constexpr int QH_WAVES = 8;
+
+template <typename KVT, int N>
+__device__ __forceinline__ void load_row16(const KVT* p, uint4 (&r)[N]) {
+#pragma unroll
+    for (int c = 0; c < N; c++) r[c] = reinterpret_cast<const uint4*>(p)[c];
+}
+
+template <typename KVT>
+__device__ __forceinline__ void cvt_chunk(const uint4& w, float* f);  // 16 bytes -> floats
+template <>
+__device__ __forceinline__ void cvt_chunk<__half>(const uint4& w, float* f) {
+    cvt8<__half>(w, f);
+}
+template <>
+__device__ __forceinline__ void cvt_chunk<float>(const uint4& w, float* f) {
+    f[0] = __uint_as_float(w.x);
+    f[1] = __uint_as_float(w.y);
+    f[2] = __uint_as_float(w.z);
+    f[3] = __uint_as_float(w.w);
+}
+
+template <int D, typename KVT>
+__global__ __launch_bounds__(64 * QH_WAVES) void k_attn_qh(AttnArgs a, int G) {
+    constexpr int C = 64;
+    constexpr int EPC = 16 / sizeof(KVT);  // elements per 16-byte chunk
+    constexpr int KC = D / EPC;            // chunks of a K row
+    constexpr int DL = D / 8;              // dims per lane in P.V
+    constexpr int VC = DL / EPC;           // chunks of a lane's V slice
+    __shared__ float P[QH_WAVES][C];
+    __shared__ float wm[QH_WAVES], wl[QH_WAVES];
+    __shared__ float wo[QH_WAVES][D];
+    const int qh = blockIdx.x, b = blockIdx.y;
+    const int h = qh / G;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int slot = lane & 7, dg = lane >> 3;
+    int64_t L = a.len.of(b);
+    if (L > a.lmax) L = a.lmax;
+    const int hq = a.hkv * G;
+    const KVT* kb = reinterpret_cast<const KVT*>(a.k) + (int64_t)b * a.kv_bstride + (int64_t)h * a.lmax * D;
+    const KVT* vb = reinterpret_cast<const KVT*>(a.v) + (int64_t)b * a.kv_bstride + (int64_t)h * a.lmax * D;
+    const float* qp = a.q + ((int64_t)b * hq + qh) * D;
+
+    auto issue = [&](int64_t c0, uint4 (&kr)[KC], uint4 (&vr)[8][VC]) {
+        const int64_t p = c0 + lane < L ? c0 + lane : L - 1;
+        load_row16<KVT, KC>(kb + p * D, kr);
+#pragma unroll
+        for (int j = 0; j < 8; j++) {
+            const int64_t pv = c0 + slot + 8 * j < L ? c0 + slot + 8 * j : L - 1;
+            load_row16<KVT, VC>(vb + pv * D + dg * DL, vr[j]);
+        }
+    };
+    uint4 kr[KC], vr[8][VC];
+    int64_t c0 = (int64_t)wave * C;
+    if (c0 < L) issue(c0, kr, vr);
+    float qv[D];  // uniform: scalar loads
+#pragma unroll
+    for (int i = 0; i < D; i++) qv[i] = qp[i];
+
+    float m = -INFINITY, l = 0.f, o[DL];
+#pragma unroll
+    for (int i = 0; i < DL; i++) o[i] = 0.f;
+    for (; c0 < L; c0 += (int64_t)QH_WAVES * C) {
+        uint4 nkr[KC], nvr[8][VC];
+        const int64_t n0 = c0 + (int64_t)QH_WAVES * C;
+        if (n0 < L) issue(n0, nkr, nvr);
+        // score of this lane's position
+        float s = 0.f;
+#pragma unroll
+        for (int c = 0; c < KC; c++) {
+            float kf[EPC];
+            cvt_chunk<KVT>(kr[c], kf);
+#pragma unroll
+            for (int e = 0; e < EPC; e++) s = fmaf(qv[c * EPC + e], kf[e], s);
+        }
+        const bool valid = c0 + lane < L;
+        s = valid ? s * a.scale : -INFINITY;
+        const float mn = fmaxf(m, wave_max64(s));
+        const float e = valid ? expf(s - mn) : 0.f;
+        const float alpha = expf(m - mn);
+        l = l * alpha + wave_sum64(e);
+        m = mn;
+        P[wave][lane] = e;
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+#pragma unroll
+        for (int i = 0; i < DL; i++) o[i] *= alpha;
+#pragma unroll
+        for (int j = 0; j < 8; j++) {
+            const float pj = P[wave][slot + 8 * j];
+            float vf[DL];
+#pragma unroll
+            for (int c = 0; c < VC; c++) cvt_chunk<KVT>(vr[j][c], vf + c * EPC);
+#pragma unroll
+            for (int i = 0; i < DL; i++) o[i] = fmaf(pj, vf[i], o[i]);
+        }
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+        if (n0 < L) {
+#pragma unroll
+            for (int c = 0; c < KC; c++) kr[c] = nkr[c];
+#pragma unroll
+            for (int j = 0; j < 8; j++)
+#pragma unroll
+                for (int c = 0; c < VC; c++) vr[j][c] = nvr[j][c];
+        }
+    }
+#pragma unroll
+    for (int i = 0; i < DL; i++) o[i] = sum8_dpp(o[i]);
+    if (slot == 0) {
+#pragma unroll
+        for (int i = 0; i < DL; i++) wo[wave][dg * DL + i] = o[i];
+    }
+    if (lane == 0) {
+        wm[wave] = m;
+        wl[wave] = l;
+    }
+    __syncthreads();
+    for (int d = tid; d < D; d += 64 * QH_WAVES) {
+        float M = -INFINITY;
+#pragma unroll
+        for (int w = 0; w < QH_WAVES; w++) M = fmaxf(M, wm[w]);
+        float num = 0.f, den = 0.f;
+#pragma unroll
+        for (int w = 0; w < QH_WAVES; w++) {
+            const float f = wl[w] > 0.f ? expf(wm[w] - M) : 0.f;  // idle wavefronts add nothing
+            num = fmaf(wo[w][d], f, num);
+            den = fmaf(wl[w], f, den);
+        }
+        a.out[((int64_t)b * hq + qh) * D + d] = num / den;
+    }
+}
+
+// Short-cache form; returns TL_HIP_ERR_ARG (no launch) for head dims it does not cover.
+int launch_attention_qh(const float* q, const void* k, const void* v, int kv_dtype, float* out,
+                        int B, int hq, int hkv, int D, int64_t lmax, int64_t kv_bstride, int64_t L,
+                        const int32_t* len_dev, int len_add, int len_step, float scale, hipStream_t s) {
+    AttnArgs a{q, k, v, out, nullptr, hkv, lmax, kv_bstride, AttnLen{L, len_dev, len_add, len_step}, 64, 1,
+               scale};
+    const int G = hq / hkv;
+    dim3 grid(hq, B);
+    const unsigned th = 64 * QH_WAVES;
+    if (D == 64 && kv_dtype == TL_HIP_F16) k_attn_qh<64, __half><<<grid, th, 0, s>>>(a, G);
+    else if (D == 128 && kv_dtype == TL_HIP_F16) k_attn_qh<128, __half><<<grid, th, 0, s>>>(a, G);
+    else if (D == 64) k_attn_qh<64, float><<<grid, th, 0, s>>>(a, G);
+    else if (D == 128) k_attn_qh<128, float><<<grid, th, 0, s>>>(a, G);
+    else {
+        set_error(TL_HIP_ERR_ARG, "ArgumentError: short-cache attention needs head_dim 64 or 128");
+        return TL_HIP_ERR_ARG;
+    }
+    hipError_t e = hipGetLastError();
+    return e == hipSuccess ? TL_HIP_OK : hip_fail(e, "attention launch");
+}
+
 // Split plan: about 1024 workgroups over (B x Hkv x splits); chunks a multiple of 32 and at
 // most ATT_MAX_CHUNK positions.
 void attn_plan(int B, int hkv, int64_t L, int* chunk, int* nsplit) {
@@ -318,6 +718,43 @@ static int attn_dispatch(const AttnArgs& a, int B, int hq, int D, hipStream_t s)
     set_error(TL_HIP_ERR_ARG, "ArgumentError: attention supports head_dim 64/128 and 1, 2, 4 or 8 "
               "query heads per KV head (got D=%d, group %d)", D, G);
     return TL_HIP_ERR_ARG;
+}
+
+// Decode form (f16 cache, D in {64, 128}, 4 or 8 query heads per KV head, 64-position
+// splits).  counter != nullptr: in-kernel merge (B * hkv zeroed ints); else k_attn_merge.
+// Returns TL_HIP_ERR_ARG (no launch) for shapes the form does not cover.
+int launch_attention_dec(const float* q, const void* k, const void* v, float* out, float* ws,
+                         int32_t* counter, int B, int hq, int hkv, int D, int64_t lmax,
+                         int64_t kv_bstride, int64_t L, const int32_t* len_dev, int len_add,
+                         int len_step, int nsplit, float scale, hipStream_t s) {
+    const int G = hq / hkv;
+    if (nsplit > ATT_MAX_SPLITS) {
+        set_error(TL_HIP_ERR_ARG, "ArgumentError: %d attention splits exceed %d", nsplit, ATT_MAX_SPLITS);
+        return TL_HIP_ERR_ARG;
+    }
+    AttnArgs a{q, k, v, out, ws, hkv, lmax, kv_bstride, AttnLen{L, len_dev, len_add, len_step},
+               DEC_C, nsplit, scale};
+    dim3 grid(nsplit, hkv, B);
+#define TLH_DEC(DD, GG)                                                                            \
+    if (D == DD && G == GG) {                                                                      \
+        if (counter && nsplit <= DEC_MAX_FUSED) {                                                  \
+            k_attn_dec<DD, GG, true><<<grid, 256, 0, s>>>(a, counter);                             \
+        } else {                                                                                   \
+            k_attn_dec<DD, GG, false><<<grid, 256, 0, s>>>(a, nullptr);                            \
+            if (nsplit > 1) k_attn_merge<DD, GG><<<dim3(hkv, B), 256, 0, s>>>(a);                   \
+        }                                                                                          \
+        hipError_t e = hipGetLastError();                                                          \
+        return e == hipSuccess ? TL_HIP_OK : hip_fail(e, "attention launch");                      \
+    }
+    TLH_DEC(64, 4) TLH_DEC(64, 8) TLH_DEC(128, 4) TLH_DEC(128, 8)
+#undef TLH_DEC
+    set_error(TL_HIP_ERR_ARG, "ArgumentError: decode attention form needs D 64/128 and 4 or 8 heads per KV head");
+    return TL_HIP_ERR_ARG;
+}
+
+bool attention_dec_supported(int kv_dtype, int hq, int hkv, int D) {
+    const int G = hkv > 0 ? hq / hkv : 0;
+    return kv_dtype == TL_HIP_F16 && (D == 64 || D == 128) && (G == 4 || G == 8) && hq == G * hkv;
 }
 
 int launch_attention(const float* q, const void* k, const void* v, int kv_dtype, float* out,
@@ -382,15 +819,26 @@ extern "C" tl_hip_tensor* tl_hip_attention_decode(const tl_hip_tensor* qh, const
         set_error(TL_HIP_ERR_ARG, "ArgumentError: batch or head count too large");
         return nullptr;
     }
+    const bool dec = attention_dec_supported(k->dtype, (int)hq, (int)hkv, (int)D);
     int chunk, nsplit;
     attn_plan((int)B, (int)hkv, L, &chunk, &nsplit);
+    if (dec) {
+        chunk = DEC_C;
+        nsplit = (int)cdiv(L, DEC_C);
+    }
     int64_t oshape[3] = {B, hq, D};
     Tensor* o = tensor_alloc(oshape, 3);
     if (!o) return nullptr;
     hipStream_t s = cur_stream();
     float* ws = (float*)dev_alloc(attn_workspace_floats((int)B, (int)hkv, (int)(hq / hkv), (int)D, nsplit) * 4);
     int rc = ws ? TL_HIP_OK : TL_HIP_ERR_ALLOC;
-    if (rc == TL_HIP_OK)
+    if (rc == TL_HIP_OK && L <= 1024 && (D == 64 || D == 128))
+        rc = launch_attention_qh(q->f32(), k->data, v->data, k->dtype, o->f32(), (int)B, (int)hq, (int)hkv, (int)D,
+                                 lmax, hkv * lmax * D, L, nullptr, 0, 0, scale, s);
+    else if (rc == TL_HIP_OK && dec)
+        rc = launch_attention_dec(q->f32(), k->data, v->data, o->f32(), ws, nullptr, (int)B, (int)hq, (int)hkv,
+                                  (int)D, lmax, hkv * lmax * D, L, nullptr, 0, 0, nsplit, scale, s);
+    else if (rc == TL_HIP_OK)
         rc = launch_attention(q->f32(), k->data, v->data, k->dtype, o->f32(), ws, (int)B, (int)hq, (int)hkv,
                               (int)D, lmax, hkv * lmax * D, L, nullptr, 0, 0, chunk, nsplit, scale, s);
     dev_free(ws);  // stream-ordered: reused only by later work on the same stream

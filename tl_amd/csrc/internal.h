@@ -146,6 +146,17 @@ int launch_attention(const float* q, const void* k, const void* v, int kv_dtype,
                      float* ws, int B, int hq, int hkv, int D, int64_t lmax,
                      int64_t kv_bstride, int64_t L, const int32_t* len_dev, int len_add,
                      int len_step, int chunk, int nsplit, float scale, hipStream_t s);
+// Decode form (f16 cache, D 64/128, 4 or 8 query heads per KV head, 64-position splits);
+// counter (B * hkv ints, zero between launches) selects the in-kernel merge.
+int launch_attention_dec(const float* q, const void* k, const void* v, float* out, float* ws,
+                         int32_t* counter, int B, int hq, int hkv, int D, int64_t lmax,
+                         int64_t kv_bstride, int64_t L, const int32_t* len_dev, int len_add,
+                         int len_step, int nsplit, float scale, hipStream_t s);
+bool attention_dec_supported(int kv_dtype, int hq, int hkv, int D);
+// Short-cache form: one workgroup per (query head, batch item), D 64 or 128, f16 or f32 cache.
+int launch_attention_qh(const float* q, const void* k, const void* v, int kv_dtype, float* out,
+                        int B, int hq, int hkv, int D, int64_t lmax, int64_t kv_bstride, int64_t L,
+                        const int32_t* len_dev, int len_add, int len_step, float scale, hipStream_t s);
 void attn_plan(int B, int hkv, int64_t L, int* chunk, int* nsplit);
 size_t attn_workspace_floats(int B, int hkv, int G, int D, int nsplit);
 
