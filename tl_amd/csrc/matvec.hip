@@ -1,19 +1,31 @@
 // Fused dequant x matvec for decode: y[m, n] = sum_k x[m, k] * W[n, k] with W resident as
 // Q4_0 / Q8_0 (qs[n][nb][16|32], d[n][nb] f16), m in {1, 2} per launch.
 //
-// Layout of the work: a workgroup is 4 wavefronts and owns 4R consecutive rows (R per
-// wavefront).  Lane l of a wavefront walks blocks l, l+64, ... of its R rows, so a load
-// instruction covers 64 consecutive 16-byte quant blocks of one row (1 KiB contiguous).
-// The activation row(s) are staged once per workgroup in LDS (coalesced 16-byte loads, block
-// stride padded to 36 floats so the lanes of a ds_read_b128 hit distinct banks) and reused
-// by all 4R rows: the weight stream is the only HBM traffic of the main loop.  The quant
-// loads of the next block column are issued before the current one is consumed.
+// Decode matvecs are small (2 - 40 MB of weights, a few microseconds each), so the kernel is
+// built for memory-level parallelism: every thread issues all of its loads before it does
+// any arithmetic, and the whole matrix is in flight within the first few hundred cycles.
 //
-// Per block the lane forms d * (sum_j x_j q_j - 8 sum_j x_j) (Q4_0; Q8_0 uses q ^ 0x80 and
+// Layout of the work: a workgroup owns RW consecutive rows and S row subsets of TC threads
+// (TC = the block count nb rounded up to wavefronts, at most 256).  Thread (s, t) owns block
+// columns t, t + TC, ... (BT per pass) of the RW / S rows s, s + S, ...:
+//   * one load instruction covers TC consecutive 16-byte quant blocks of one row;
+//   * the thread's activation blocks (32 floats each) are loaded once, straight into
+//     registers, and reused for its rows -- no LDS staging and no barrier before the math;
+//   * the K dimension is split across the wavefronts of a subset.  Row sums are formed by a
+//     transpose-reduce inside each wavefront (each exchange step halves the number of
+//     values a lane carries: N - 1 exchanges for N values instead of 6 per value) and one
+//     LDS pass across the wavefronts.
+//   * residual, RoPE table entries and penalty flags for the epilogue are requested right
+//     after the weight loads, so no memory round trip is left after the reduction.
+//
+// Per block the thread forms d * (sum_j x_j q_j - 8 sum_j x_j) (Q4_0; Q8_0 uses q ^ 0x80 and
 // 128), one byte->float conversion and one FMA per weight, f32 throughout.
 //
 // Prologue options:  NORM  x := (x / sqrt(mean(x^2) + eps)) * w   (the RMSNorm that precedes
-//                          every projection in the chatbot, ffi.rs:2444-2486 + mul_impl)
+//                          every projection in the chatbot, ffi.rs:2444-2486 + mul_impl),
+//                          applied as (sum_j W_j x_j w_j) / sqrt(mean(x^2) + eps): the
+//                          squares are summed alongside the dot products and the division
+//                          is done once per row after the reduction
 //                    EMBED x := embedding row of the token id held in device memory
 //                          (tensor.rs:1094-1112), also written out as the residual stream
 // Epilogues:  EPI_PLAIN   y = v
@@ -30,8 +42,6 @@
 
 namespace tlhip {
 
-constexpr int XPAD = 36;  // floats per staged 32-float block
-
 template <int QT>
 struct QB_;
 template <>
@@ -43,255 +53,394 @@ struct QB_<TL_HIP_GGML_Q8_0> {
     static constexpr int v = 32;
 };
 
-__device__ __forceinline__ float dot4b(uint32_t q, const float* x) {
-    float s = x[0] * (float)(q & 0xFF);
-    s = fmaf(x[1], (float)((q >> 8) & 0xFF), s);
-    s = fmaf(x[2], (float)((q >> 16) & 0xFF), s);
-    s = fmaf(x[3], (float)(q >> 24), s);
-    return s;
+// acc + sum_j x[j] * byte_j(q): one v_cvt_f32_ubyteN and one FMA per byte.  The empty asm
+// hides which bits of q are known to be zero (after a nibble mask); otherwise the byte
+// extraction is narrowed to a 4-bit field extract plus a ubyte0 conversion per byte.
+__device__ __forceinline__ float fma4b(uint32_t q, const float* x, float acc) {
+    asm("" : "+v"(q));
+    acc = fmaf(x[0], (float)(q & 0xFF), acc);
+    acc = fmaf(x[1], (float)((q >> 8) & 0xFF), acc);
+    acc = fmaf(x[2], (float)((q >> 16) & 0xFF), acc);
+    acc = fmaf(x[3], (float)(q >> 24), acc);
+    return acc;
 }
 
 template <int CTRL>
 __device__ __forceinline__ float dpp_mov(float v) {
     return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), CTRL, 0xF, 0xF, true));
 }
-// Sum over the 64 lanes of a wavefront: DPP within rows of 16 (quad_perm 1-0-3-2 and
-// 2-3-0-1, half-row and row mirrors -- VALU ops, no LDS traffic), then two cross-row
-// exchanges through ds_bpermute.  Every lane receives the total.
-__device__ __forceinline__ float wsum(float v) {
-    v += dpp_mov<0xB1>(v);
-    v += dpp_mov<0x4E>(v);
-    v += dpp_mov<0x141>(v);
-    v += dpp_mov<0x140>(v);
-    v += __shfl_xor(v, 16, 64);
-    v += __shfl_xor(v, 32, 64);
-    return v;
+
+// Lane exchange used by the reductions.  Each form is an involution that flips lane bit OFF
+// within the group of lanes agreeing on the higher bits: ds_bpermute xor for 32 and 16, the
+// DPP row mirror (xor 15), half-row mirror (xor 7) and quad permutations (xor 2, xor 1)
+// below -- VALU ops, no LDS traffic.
+template <int OFF>
+__device__ __forceinline__ float xchg(float v) {
+    if constexpr (OFF >= 16) return __shfl_xor(v, OFF, 64);
+    else if constexpr (OFF == 8) return dpp_mov<0x140>(v);
+    else if constexpr (OFF == 4) return dpp_mov<0x141>(v);
+    else if constexpr (OFF == 2) return dpp_mov<0x4E>(v);
+    else return dpp_mov<0xB1>(v);
 }
 
-template <int QT, int R>
-__device__ __forceinline__ void load_rows(const MvArgs& a, int64_t row0, int64_t b,
-                                          uint4 (&w)[R][QB_<QT>::v / 16], float (&dd)[R]) {
-    constexpr int QB = QB_<QT>::v;
+template <int OFF>
+__device__ __forceinline__ float fold(float t) {
+    t += xchg<OFF>(t);
+    if constexpr (OFF > 1) return fold<OFF / 2>(t);
+    else return t;
+}
+
+// Sum over the 64 lanes of a wavefront; every lane receives the total.
+__device__ __forceinline__ float wsum(float v) { return fold<32>(v); }
+
+// Transpose-reduce of N values per lane (N a power of two, 2..64): after the call lane l
+// holds, in v[0], the wavefront sum of value l / (64 / N).  Step OFF exchanges half of the
+// values with the partner across lane bit OFF and keeps the half selected by that bit.
+template <int OFF, int H, int N>
+__device__ __forceinline__ void halve(float (&v)[N], int lane) {
+    const bool up = (lane & OFF) != 0;
 #pragma unroll
-    for (int r = 0; r < R; r++) {
-        int64_t row = row0 + r < a.n ? row0 + r : a.n - 1;  // clamp: loads stay in bounds
-        const uint4* p = reinterpret_cast<const uint4*>(a.qs + (row * a.nb + b) * QB);
-#pragma unroll
-        for (int i = 0; i < QB / 16; i++) w[r][i] = p[i];
-        dd[r] = __half2float(a.d[row * a.nb + b]);
+    for (int i = 0; i < H; i++) {
+        const float send = up ? v[i] : v[i + H];
+        const float keep = up ? v[i + H] : v[i];
+        v[i] = keep + xchg<OFF>(send);
+    }
+    if constexpr (H > 1) halve<OFF / 2, H / 2, N>(v, lane);
+}
+
+template <int N>
+__device__ __forceinline__ float xreduce(float (&v)[N], int lane) {
+    if constexpr (N == 1) {
+        return fold<32>(v[0]);
+    } else {
+        halve<32, N / 2, N>(v, lane);
+        constexpr int G = 64 / N;  // lanes that share a value index
+        if constexpr (G > 1) return fold<G / 2>(v[0]);
+        else return v[0];
     }
 }
 
-template <int QT, int R, int M, int EPI, bool NORM, bool EMBED>
-__global__ __launch_bounds__(256) void k_mv(MvArgs a) {
-    constexpr int QB = QB_<QT>::v;
-    extern __shared__ float xs[];  // [M][nb][XPAD]
-    __shared__ float ys[M][4 * R];
-    __shared__ float red[M][4];
+constexpr int MV_MAX_RW = 32;  // rows per workgroup
+constexpr int XPAD = 36;       // floats per staged 32-float block: lane-per-block LDS reads hit distinct banks
+constexpr int XR = 8;          // float4 per thread staged ahead of the weight loads
+
+// Launch shape: S = 1 << s_shift row subsets of tc threads each (tc a multiple of 64 and,
+// when S > 1, a power of two 1 << tc_shift).
+struct MvShape {
+    int tc, tc_shift, s_shift;
+};
+
+// Thread (sub, tcol) owns block columns tcol + tc * (i + BT * pass) of rows
+// row0 + sub + S * j, j < RWT.  Rows per workgroup RW = S * RWT.  Offsets are 32-bit
+// (checked at launch: the quant array is below 2 GiB).
+template <int QT, int BT, int RWT, int M, int EPI, bool NORM, bool EMBED>
+__global__ __launch_bounds__(256) void k_mv(MvArgs a, MvShape sh) {
+    constexpr int QB = QB_<QT>::v, QW = QB / 16;  // 16-byte loads per block
+    constexpr int N = M * RWT;
+    constexpr int RWT_SHIFT = RWT == 1 ? 0 : RWT == 2 ? 1 : RWT == 4 ? 2 : RWT == 8 ? 3 : 4;
+    static_assert(N <= 64 && (N & (N - 1)) == 0 && (1 << RWT_SHIFT) == RWT, "RWT, M * RWT: powers of two");
+    extern __shared__ float xs[];  // [M][nb][XPAD] staged activations (x * norm weight with NORM)
+    __shared__ float red[4][N];
+    __shared__ float ys[M][MV_MAX_RW];
+    __shared__ float ssq[4][M];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int64_t nb = a.nb, k = a.k, n = a.n;
-    const int64_t wg_row0 = (int64_t)blockIdx.x * 4 * R;
-    const int64_t row0 = wg_row0 + wave * R;
+    const int TC = sh.tc, S = 1 << sh.s_shift, RW = RWT << sh.s_shift, rw_shift = RWT_SHIFT + sh.s_shift;
+    const int tcol = sh.s_shift ? (tid & (TC - 1)) : tid;
+    const int sub = sh.s_shift ? (tid >> sh.tc_shift) : 0;
+    const int wps = TC >> 6;  // wavefronts per row subset
+    const uint32_t nb = (uint32_t)a.nb, k = (uint32_t)a.k, n = (uint32_t)a.n;
+    const uint32_t row0 = blockIdx.x * (uint32_t)RW;
+    const uint32_t my_row0 = row0 + sub;
 
-    // (1) first block column of quant data in flight before x is staged
-    uint4 w[R][QB / 16];
-    float dd[R];
-    if (lane < nb) load_rows<QT, R>(a, row0, lane, w, dd);
-
-    // (2) stage x (optionally gathered and normalised) into LDS
-    const int64_t k4 = k >> 2;
-    const float* xsrc = EMBED ? a.x + (int64_t)(*a.embed_id) * k : a.x;
-#pragma unroll
-    for (int m = 0; m < M; m++) {
-        const float4* xm = reinterpret_cast<const float4*>(xsrc + m * k);
-        if constexpr (NORM) {
-            float ss = 0.f;
-            for (int64_t e = tid; e < k4; e += 256) {
-                float4 v = xm[e];
-                ss += v.x * v.x + v.y * v.y + v.z * v.z + v.w * v.w;
-            }
-            ss = wsum(ss);
-            if (lane == 0) red[m][wave] = ss;
-        }
-    }
-    if constexpr (NORM) __syncthreads();
-#pragma unroll
-    for (int m = 0; m < M; m++) {
-        const float4* xm = reinterpret_cast<const float4*>(xsrc + m * k);
-        float rms = 1.f;
-        if constexpr (NORM) {
-            float ss = (red[m][0] + red[m][1]) + (red[m][2] + red[m][3]);
-            rms = sqrtf(ss / (float)k + a.eps);
-        }
-        for (int64_t e = tid; e < k4; e += 256) {
-            float4 v = xm[e];
-            if constexpr (EMBED) {
-                if (blockIdx.x == 0 && a.x_out) reinterpret_cast<float4*>(a.x_out + m * k)[e] = v;
-            }
-            if constexpr (NORM) {
-                float4 g = reinterpret_cast<const float4*>(a.norm_w)[e];
-                v.x = (v.x / rms) * g.x;
-                v.y = (v.y / rms) * g.y;
-                v.z = (v.z / rms) * g.z;
-                v.w = (v.w / rms) * g.w;
-            }
-            const int64_t b = e >> 3, c = e & 7;
-            *reinterpret_cast<float4*>(xs + (m * nb + b) * XPAD + c * 4) = v;
-        }
-    }
-    __syncthreads();
-
-    // (3) main loop over this lane's block columns
-    float acc[M][R];
+    // epilogue operands, requested right after the first loads
+    float pre_res = 0.f, pre_c = 0.f, pre_s = 0.f;
+    uint32_t pre_pos = 0;
+    int pre_seen = 0;
+    float acc[M][RWT];
 #pragma unroll
     for (int m = 0; m < M; m++)
 #pragma unroll
-        for (int r = 0; r < R; r++) acc[m][r] = 0.f;
-    for (int64_t b = lane; b < nb; b += 64) {
-        uint4 wn[R][QB / 16];
-        float dn[R];
-        const bool more = b + 64 < nb;
-        if (more) load_rows<QT, R>(a, row0, b + 64, wn, dn);
+        for (int r = 0; r < RWT; r++) acc[m][r] = 0.f;
+
+    for (uint32_t base = 0; base < nb; base += (uint32_t)(BT * TC)) {
+        uint32_t bc[BT];
+        bool valid[BT];
 #pragma unroll
-        for (int m = 0; m < M; m++) {
-            float xv[32];
-            const float* xb = xs + (m * nb + b) * XPAD;
+        for (int i = 0; i < BT; i++) {
+            const uint32_t b = base + (uint32_t)(tcol + i * TC);
+            valid[i] = b < nb;
+            bc[i] = valid[i] ? b : nb - 1;  // past the end: read the last column, scale 0
+        }
+        uint4 w[BT][RWT][QW];
+        float dd[BT][RWT];
+        auto load_w = [&]() {
 #pragma unroll
-            for (int i = 0; i < 8; i++) {
-                float4 t = *reinterpret_cast<const float4*>(xb + 4 * i);
-                xv[4 * i] = t.x;
-                xv[4 * i + 1] = t.y;
-                xv[4 * i + 2] = t.z;
-                xv[4 * i + 3] = t.w;
+            for (int i = 0; i < BT; i++) {
+#pragma unroll
+                for (int r = 0; r < RWT; r++) {
+                    uint32_t row = my_row0 + (uint32_t)(S * r);
+                    row = row < n ? row : n - 1;
+                    const uint32_t blk = __umul24(row, nb) + bc[i];
+                    const uint4* p = reinterpret_cast<const uint4*>(a.qs + (size_t)blk * QB);
+#pragma unroll
+                    for (int c = 0; c < QW; c++) w[i][r][c] = p[c];
+                    const float dv = __half2float(a.d[blk]);
+                    dd[i][r] = valid[i] ? dv : 0.f;
+                }
             }
-            float sx0 = 0.f, sx1 = 0.f;
+        };
+
+        if (base == 0) {
+            // (1) the activations (all passes) are staged once per workgroup in LDS with
+            // coalesced loads -- a lane reading its own 128-byte block straight from memory
+            // would touch 64 cache lines per load instruction.  The first XR float4 per
+            // thread are requested before the weights of the first pass, the stores follow
+            // them, so the weight stream is in flight while the staging completes.
+            const float* xsrc = EMBED ? a.x + (size_t)(*a.embed_id) * k : a.x;
+            const uint32_t k4 = k >> 2, nthr = blockDim.x;
+            float s2[M];
+            float4 xr[M][XR], gr[NORM ? XR : 1];
 #pragma unroll
-            for (int j = 0; j < 16; j++) {
-                sx0 += xv[j];
-                sx1 += xv[16 + j];
+            for (int m = 0; m < M; m++) {
+                s2[m] = 0.f;
+#pragma unroll
+                for (int j = 0; j < XR; j++) {
+                    const uint32_t e = tid + j * nthr;
+                    if (e < k4) xr[m][j] = reinterpret_cast<const float4*>(xsrc + m * k)[e];
+                }
             }
-            const float sx = sx0 + sx1;
+            if constexpr (NORM) {
 #pragma unroll
-            for (int r = 0; r < R; r++) {
-                float s0 = 0.f, s1 = 0.f;
+                for (int j = 0; j < XR; j++) {
+                    const uint32_t e = tid + j * nthr;
+                    if (e < k4) gr[j] = reinterpret_cast<const float4*>(a.norm_w)[e];
+                }
+            }
+            load_w();
+            auto stage = [&](int m, uint32_t e, float4 v, float4 g) {
+                if constexpr (EMBED) {
+                    if (blockIdx.x == 0 && a.x_out) reinterpret_cast<float4*>(a.x_out)[e] = v;
+                }
+                if constexpr (NORM) {
+                    s2[m] = fmaf(v.x, v.x, fmaf(v.y, v.y, fmaf(v.z, v.z, fmaf(v.w, v.w, s2[m]))));
+                    v.x *= g.x;
+                    v.y *= g.y;
+                    v.z *= g.z;
+                    v.w *= g.w;
+                }
+                *reinterpret_cast<float4*>(xs + (m * nb + (e >> 3)) * XPAD + (e & 7) * 4) = v;
+            };
+#pragma unroll
+            for (int m = 0; m < M; m++) {
+#pragma unroll
+                for (int j = 0; j < XR; j++) {
+                    const uint32_t e = tid + j * nthr;
+                    if (e < k4) stage(m, e, xr[m][j], NORM ? gr[j] : xr[m][j]);
+                }
+                for (uint32_t e = tid + XR * nthr; e < k4; e += nthr) {  // long rows only
+                    const float4 v = reinterpret_cast<const float4*>(xsrc + m * k)[e];
+                    stage(m, e, v, NORM ? reinterpret_cast<const float4*>(a.norm_w)[e] : v);
+                }
+            }
+            if constexpr (NORM) {
+#pragma unroll
+                for (int m = 0; m < M; m++) {
+                    const float ss = wsum(s2[m]);
+                    if (lane == 0) ssq[wave][m] = ss;
+                }
+            }
+            if constexpr (EPI == EPI_RES) {
+                if (tid < M * RW && row0 + (tid & (RW - 1)) < n)
+                    pre_res = a.res[(tid >> rw_shift) * n + row0 + (tid & (RW - 1))];
+            } else if constexpr (EPI == EPI_ROPE_KV) {
+                pre_pos = (uint32_t)*a.pos;
+                const uint32_t r0 = row0 + 2 * tid;
+                if (tid < RW / 2 && r0 < n && r0 < (uint32_t)(a.q_rows + a.kv_rows)) {
+                    const uint32_t i = (r0 < (uint32_t)a.q_rows ? r0 : r0 - a.q_rows) % (uint32_t)a.hd;
+                    pre_c = a.cos_t[pre_pos * a.hd + i];
+                    pre_s = a.sin_t[pre_pos * a.hd + i];
+                }
+            } else if constexpr (EPI == EPI_ARGMAX) {
+                if (a.seen && tid < RW && row0 + tid < n) pre_seen = a.seen[row0 + tid];
+            }
+            __syncthreads();
+        } else {
+            load_w();
+        }
+
+        // (3) block dot products
+#pragma unroll
+        for (int i = 0; i < BT; i++) {
+            float xv[M][1][32];  // this thread's block of the staged activations
+#pragma unroll
+            for (int m = 0; m < M; m++) {
+                const float* xb = xs + (m * nb + bc[i]) * XPAD;
+#pragma unroll
+                for (int c = 0; c < 8; c++) {
+                    const float4 t = *reinterpret_cast<const float4*>(xb + 4 * c);
+                    xv[m][0][4 * c] = t.x;
+                    xv[m][0][4 * c + 1] = t.y;
+                    xv[m][0][4 * c + 2] = t.z;
+                    xv[m][0][4 * c + 3] = t.w;
+                }
+            }
+            float sx[M];
+#pragma unroll
+            for (int m = 0; m < M; m++) {
+                float sx0 = 0.f, sx1 = 0.f;
+#pragma unroll
+                for (int j = 0; j < 16; j++) {
+                    sx0 += xv[m][0][j];
+                    sx1 += xv[m][0][16 + j];
+                }
+                sx[m] = sx0 + sx1;
+            }
+            // row outer, activation row inner: each quant word is unpacked once.  Q4_0 high
+            // nibbles are taken in place (16 q, one AND) and the factor 1/16 applied to their
+            // sum, which is exact.
+#pragma unroll
+            for (int r = 0; r < RWT; r++) {
+                float s0[M], s1[M];
+#pragma unroll
+                for (int m = 0; m < M; m++) s0[m] = s1[m] = 0.f;
                 if constexpr (QT == TL_HIP_GGML_Q4_0) {
-                    const uint32_t q[4] = {w[r][0].x, w[r][0].y, w[r][0].z, w[r][0].w};
+                    const uint32_t q[4] = {w[i][r][0].x, w[i][r][0].y, w[i][r][0].z, w[i][r][0].w};
 #pragma unroll
                     for (int c = 0; c < 4; c++) {
-                        s0 += dot4b(q[c] & 0x0F0F0F0Fu, xv + 4 * c);
-                        s1 += dot4b((q[c] >> 4) & 0x0F0F0F0Fu, xv + 16 + 4 * c);
+                        const uint32_t lo = q[c] & 0x0F0F0F0Fu, hi = q[c] & 0xF0F0F0F0u;
+#pragma unroll
+                        for (int m = 0; m < M; m++) {
+                            s0[m] = fma4b(lo, xv[m][0] + 4 * c, s0[m]);
+                            s1[m] = fma4b(hi, xv[m][0] + 16 + 4 * c, s1[m]);
+                        }
                     }
-                    acc[m][r] = fmaf(dd[r], (s0 + s1) - 8.f * sx, acc[m][r]);
+#pragma unroll
+                    for (int m = 0; m < M; m++)
+                        acc[m][r] = fmaf(dd[i][r], fmaf(s1[m], 0.0625f, s0[m]) - 8.f * sx[m], acc[m][r]);
                 } else {
-                    const uint32_t q[8] = {w[r][0].x, w[r][0].y, w[r][0].z, w[r][0].w,
-                                           w[r][1].x, w[r][1].y, w[r][1].z, w[r][1].w};
+                    const uint32_t q[8] = {w[i][r][0].x, w[i][r][0].y, w[i][r][0].z, w[i][r][0].w,
+                                           w[i][r][1].x, w[i][r][1].y, w[i][r][1].z, w[i][r][1].w};
 #pragma unroll
                     for (int c = 0; c < 4; c++) {
-                        s0 += dot4b(q[c] ^ 0x80808080u, xv + 4 * c);
-                        s1 += dot4b(q[4 + c] ^ 0x80808080u, xv + 16 + 4 * c);
+                        const uint32_t lo = q[c] ^ 0x80808080u, hi = q[4 + c] ^ 0x80808080u;
+#pragma unroll
+                        for (int m = 0; m < M; m++) {
+                            s0[m] = fma4b(lo, xv[m][0] + 4 * c, s0[m]);
+                            s1[m] = fma4b(hi, xv[m][0] + 16 + 4 * c, s1[m]);
+                        }
                     }
-                    acc[m][r] = fmaf(dd[r], (s0 + s1) - 128.f * sx, acc[m][r]);
+#pragma unroll
+                    for (int m = 0; m < M; m++)
+                        acc[m][r] = fmaf(dd[i][r], (s0[m] + s1[m]) - 128.f * sx[m], acc[m][r]);
                 }
             }
         }
-        if (more) {
-#pragma unroll
-            for (int r = 0; r < R; r++) {
-#pragma unroll
-                for (int i = 0; i < QB / 16; i++) w[r][i] = wn[r][i];
-                dd[r] = dn[r];
-            }
-        }
     }
 
-    // (4) lane partials -> row sums in LDS
+    // (4) thread partials -> row sums: transpose-reduce per wavefront, then across wavefronts
+    {
+        float v[N];
 #pragma unroll
-    for (int m = 0; m < M; m++)
+        for (int m = 0; m < M; m++)
 #pragma unroll
-        for (int r = 0; r < R; r++) {
-            float v = wsum(acc[m][r]);
-            if (lane == 0) ys[m][wave * R + r] = v;
+            for (int r = 0; r < RWT; r++) v[m * RWT + r] = acc[m][r];
+        const float t = xreduce<N>(v, lane);
+        constexpr int G = 64 / N;
+        if ((lane & (G - 1)) == 0) red[wave][lane / G] = t;
+        __syncthreads();
+        if (tid < M * RW) {  // value (m, j) of subset s is row s + S * j
+            const int m = tid >> rw_shift, rl = tid & (RW - 1), s = rl & (S - 1), j = rl >> sh.s_shift;
+            float acc_s = 0.f;
+            for (int q = s * wps; q < (s + 1) * wps; q++) acc_s += red[q][m * RWT + j];
+            if constexpr (NORM) {
+                float ss = 0.f;
+                for (int q = 0; q < (int)(blockDim.x >> 6); q++) ss += ssq[q][m];
+                acc_s = acc_s / sqrtf(ss / (float)k + a.eps);
+            }
+            ys[m][rl] = acc_s;
         }
-    __syncthreads();
+        __syncthreads();
+    }
 
     // (5) epilogue
     if constexpr (EPI == EPI_PLAIN || EPI == EPI_RES) {
-        for (int t = tid; t < M * 4 * R; t += 256) {
-            const int m = t / (4 * R), rl = t % (4 * R);
-            const int64_t row = wg_row0 + rl;
+        if (tid < M * RW) {
+            const int m = tid >> rw_shift, rl = tid & (RW - 1);
+            const uint32_t row = row0 + rl;
             if (row < n) {
                 float v = ys[m][rl];
-                if constexpr (EPI == EPI_RES) v = a.res[m * n + row] + v;
+                if constexpr (EPI == EPI_RES) v = pre_res + v;
                 a.y[m * n + row] = v;
             }
         }
     } else if constexpr (EPI == EPI_GLU) {
-        const int64_t half_n = n / 2;
-        for (int t = tid; t < M * 2 * R; t += 256) {
-            const int m = t / (2 * R), p = t % (2 * R);
-            const int64_t i = wg_row0 / 2 + p;
+        const uint32_t half_n = n / 2;
+        if (tid < M * (RW / 2)) {
+            const int m = tid >> (rw_shift - 1), p = tid & (RW / 2 - 1);
+            const uint32_t i = row0 / 2 + p;
             if (i < half_n) {
                 const float g = ys[m][2 * p], u = ys[m][2 * p + 1];
                 a.y[m * half_n + i] = (g * (1.0f / (1.0f + expf(-g)))) * u;
             }
         }
     } else if constexpr (EPI == EPI_ROPE_KV) {
-        const int64_t pos = *a.pos;
-        for (int t = tid; t < 2 * R; t += 256) {
-            const int64_t r0 = wg_row0 + 2 * t;
-            if (r0 >= n) continue;
-            const float v0 = ys[0][2 * t], v1 = ys[0][2 * t + 1];
-            if (r0 < a.q_rows + a.kv_rows) {
-                const bool isq = r0 < a.q_rows;
-                const int64_t rr = isq ? r0 : r0 - a.q_rows;
-                const int64_t i = rr % a.hd;
-                const float c = a.cos_t[pos * a.hd + i], s = a.sin_t[pos * a.hd + i];
-                const float o0 = v0 * c - v1 * s, o1 = v0 * s + v1 * c;
-                if (isq) {
-                    a.q_out[r0] = o0;
-                    a.q_out[r0 + 1] = o1;
+        const int64_t pos = pre_pos;
+        if (tid < RW / 2) {
+            const int64_t r0 = row0 + 2 * tid;
+            if (r0 < n) {
+                const float v0 = ys[0][2 * tid], v1 = ys[0][2 * tid + 1];
+                if (r0 < a.q_rows + a.kv_rows) {
+                    const bool isq = r0 < a.q_rows;
+                    const int64_t rr = isq ? r0 : r0 - a.q_rows;
+                    const int64_t i = rr % a.hd;
+                    const float c = pre_c, s = pre_s;
+                    const float o0 = v0 * c - v1 * s, o1 = v0 * s + v1 * c;
+                    if (isq) {
+                        a.q_out[r0] = o0;
+                        a.q_out[r0 + 1] = o1;
+                    } else {
+                        const int64_t off = ((rr / a.hd) * a.max_seq + pos) * a.hd + i;
+                        if (a.kv_f16) {
+                            reinterpret_cast<__half*>(a.kc)[off] = __float2half(o0);
+                            reinterpret_cast<__half*>(a.kc)[off + 1] = __float2half(o1);
+                        } else {
+                            reinterpret_cast<float*>(a.kc)[off] = o0;
+                            reinterpret_cast<float*>(a.kc)[off + 1] = o1;
+                        }
+                    }
                 } else {
+                    const int64_t rr = r0 - a.q_rows - a.kv_rows, i = rr % a.hd;
                     const int64_t off = ((rr / a.hd) * a.max_seq + pos) * a.hd + i;
                     if (a.kv_f16) {
-                        reinterpret_cast<__half*>(a.kc)[off] = __float2half(o0);
-                        reinterpret_cast<__half*>(a.kc)[off + 1] = __float2half(o1);
+                        reinterpret_cast<__half*>(a.vc)[off] = __float2half(v0);
+                        reinterpret_cast<__half*>(a.vc)[off + 1] = __float2half(v1);
                     } else {
-                        reinterpret_cast<float*>(a.kc)[off] = o0;
-                        reinterpret_cast<float*>(a.kc)[off + 1] = o1;
+                        reinterpret_cast<float*>(a.vc)[off] = v0;
+                        reinterpret_cast<float*>(a.vc)[off + 1] = v1;
                     }
-                }
-            } else {
-                const int64_t rr = r0 - a.q_rows - a.kv_rows, i = rr % a.hd;
-                const int64_t off = ((rr / a.hd) * a.max_seq + pos) * a.hd + i;
-                if (a.kv_f16) {
-                    reinterpret_cast<__half*>(a.vc)[off] = __float2half(v0);
-                    reinterpret_cast<__half*>(a.vc)[off + 1] = __float2half(v1);
-                } else {
-                    reinterpret_cast<float*>(a.vc)[off] = v0;
-                    reinterpret_cast<float*>(a.vc)[off + 1] = v1;
                 }
             }
         }
     } else if constexpr (EPI == EPI_ARGMAX) {
         // logits, penalised logits, then this workgroup's greedy candidate (the left fold of
         // tensor.rs:1633-1637 over its rows: keep the best only when strictly greater)
-        if (tid < 4 * R) {
-            const int64_t row = wg_row0 + tid;
+        if (tid < RW) {
+            const uint32_t row = row0 + tid;
             if (row < n) {
                 float v = ys[0][tid];
                 a.y[row] = v;
-                if (a.seen && a.seen[row]) v = v > 0.0f ? v / a.penalty : v * a.penalty;
+                if (pre_seen) v = v > 0.0f ? v / a.penalty : v * a.penalty;
                 a.plogits[row] = v;
                 ys[0][tid] = v;
             }
         }
         __syncthreads();
         if (tid == 0) {
-            int cnt = (int)((n - wg_row0) < 4 * R ? (n - wg_row0) : 4 * R);
+            const int cnt = (int)((n - row0) < (uint32_t)RW ? (n - row0) : (uint32_t)RW);
             float bv = ys[0][0];
             int bi = 0, nan = bv != bv;
             for (int i = 1; i < cnt; i++) {
-                float v = ys[0][i];
+                const float v = ys[0][i];
                 nan |= v != v;
                 if (!(bv > v)) {
                     bv = v;
@@ -299,7 +448,7 @@ __global__ __launch_bounds__(256) void k_mv(MvArgs a) {
                 }
             }
             a.part_v[blockIdx.x] = bv;
-            a.part_i[blockIdx.x] = (int32_t)(wg_row0 + bi);
+            a.part_i[blockIdx.x] = (int32_t)(row0 + bi);
             a.part_nan[blockIdx.x] = nan;
         }
     }
@@ -366,57 +515,86 @@ __global__ __launch_bounds__(256) void k_argmax_finish(MvArgs a, int nwg) {
 }
 
 // ---------------------------------------------------------------- dispatch --------------
-static int pick_r(int64_t n) {
-    // about 512 - 1024 workgroups of 4R rows
-    if (n >= 4 * 8 * 1024) return 8;
-    if (n >= 4 * 4 * 1024) return 4;
-    if (n >= 4 * 2 * 512) return 2;
-    return 1;
+// TC = nb rounded up to wavefronts (at most 256) threads per row subset, BT block columns
+// per thread and pass (2 once nb > 256), S row subsets (four wavefronts per workgroup when
+// TC is one or two wavefronts), RWT rows per thread: the smallest of 2, 4, 8 that keeps the
+// grid at <= 720 workgroups (about three per CU), with at most 64 quant VGPRs per thread.
+// (Measured on MI355X over the decode shapes: fewer, fuller workgroups lose to this because
+// the per-thread block math then serialises on fewer SIMDs; many more lose to the repeated
+// activation loads.)
+struct MvPlan {
+    int TC, S, BT, RWT;
+    int64_t grid;
+    MvShape shape() const {
+        int tc_shift = 0, s_shift = 0;
+        while ((1 << tc_shift) < TC) tc_shift++;
+        while ((1 << s_shift) < S) s_shift++;
+        return MvShape{TC, tc_shift, s_shift};
+    }
+};
+constexpr int MV_MIN_RW = 2;
+
+static MvPlan mv_plan(int64_t n, int64_t nb, int qt) {
+    MvPlan p;
+    p.TC = (int)(nb >= 256 ? 256 : cdiv(nb, 64) * 64);
+    p.BT = nb > 256 ? 2 : 1;
+    p.S = p.TC <= 128 ? 256 / p.TC : 1;  // TC of 64 or 128: a power of two
+    const int qw = qt == TL_HIP_GGML_Q8_0 ? 2 : 1;
+    int rwt = 2;
+    while (rwt < 8 && cdiv(n, (int64_t)p.S * rwt) > 720) rwt *= 2;
+    while (rwt > 2 && rwt * p.BT * qw > 16) rwt /= 2;
+    p.RWT = rwt;
+    p.grid = cdiv(n, (int64_t)p.S * rwt);
+    return p;
 }
 
-template <int QT, int R, int M, int EPI, bool NORM, bool EMBED>
-static int run(const MvArgs& a, hipStream_t s) {
-    const size_t lds = (size_t)M * a.nb * XPAD * 4;
-    auto kern = k_mv<QT, R, M, EPI, NORM, EMBED>;
+template <int QT, int BT, int RWT, int M, int EPI, bool NORM, bool EMBED>
+static int run(const MvArgs& a, const MvPlan& p, hipStream_t s) {
+    const size_t lds = (size_t)M * a.nb * XPAD * sizeof(float);
+    auto kern = k_mv<QT, BT, RWT, M, EPI, NORM, EMBED>;
     if (lds > 64 * 1024) {
         hipError_t e = hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
         if (e != hipSuccess) return hip_fail(e, "hipFuncSetAttribute(LDS)");
     }
-    const unsigned grid = (unsigned)cdiv(a.n, 4 * R);
-    kern<<<grid, 256, lds, s>>>(a);
-    if constexpr (EPI == EPI_ARGMAX) k_argmax_finish<<<1, 256, 0, s>>>(a, (int)grid);
+    kern<<<(unsigned)p.grid, p.S * p.TC, lds, s>>>(a, p.shape());
+    if constexpr (EPI == EPI_ARGMAX) k_argmax_finish<<<1, 256, 0, s>>>(a, (int)p.grid);
     hipError_t e = hipGetLastError();
     return e == hipSuccess ? TL_HIP_OK : hip_fail(e, "matvec launch");
 }
 
+// (BT, RWT) combinations the plan can produce: Q4_0 (1, 8|4|2), (2, 8|4|2);
+// Q8_0 (1, 8|4|2), (2, 4|2).
 template <int QT, int M, int EPI, bool NORM, bool EMBED>
-static int run_r(const MvArgs& a, int R, hipStream_t s) {
-    switch (R) {
-        case 8: return run<QT, 8, M, EPI, NORM, EMBED>(a, s);
-        case 4: return run<QT, 4, M, EPI, NORM, EMBED>(a, s);
-        case 2: return run<QT, 2, M, EPI, NORM, EMBED>(a, s);
-        default: return run<QT, 1, M, EPI, NORM, EMBED>(a, s);
+static int run_p(const MvArgs& a, const MvPlan& p, hipStream_t s) {
+    if (p.BT == 1) {
+        if (p.RWT == 8) return run<QT, 1, 8, M, EPI, NORM, EMBED>(a, p, s);
+        if (p.RWT == 4) return run<QT, 1, 4, M, EPI, NORM, EMBED>(a, p, s);
+        return run<QT, 1, 2, M, EPI, NORM, EMBED>(a, p, s);
     }
+    if constexpr (QT == TL_HIP_GGML_Q4_0)
+        if (p.RWT == 8) return run<QT, 2, 8, M, EPI, NORM, EMBED>(a, p, s);
+    if (p.RWT == 4) return run<QT, 2, 4, M, EPI, NORM, EMBED>(a, p, s);
+    return run<QT, 2, 2, M, EPI, NORM, EMBED>(a, p, s);
 }
 
 template <int QT>
-static int run_t(const MvArgs& a, int m, int epi, bool norm, bool embed, int R, hipStream_t s) {
+static int run_t(const MvArgs& a, int m, int epi, bool norm, bool embed, const MvPlan& p, hipStream_t s) {
     if (m == 2) {
-        if (epi == EPI_RES) return run_r<QT, 2, EPI_RES, false, false>(a, R, s);
-        return run_r<QT, 2, EPI_PLAIN, false, false>(a, R, s);
+        if (epi == EPI_RES) return run_p<QT, 2, EPI_RES, false, false>(a, p, s);
+        return run_p<QT, 2, EPI_PLAIN, false, false>(a, p, s);
     }
     switch (epi) {
-        case EPI_RES: return run_r<QT, 1, EPI_RES, false, false>(a, R, s);
+        case EPI_RES: return run_p<QT, 1, EPI_RES, false, false>(a, p, s);
         case EPI_GLU:
-            return norm ? run_r<QT, 1, EPI_GLU, true, false>(a, R, s) : run_r<QT, 1, EPI_GLU, false, false>(a, R, s);
+            return norm ? run_p<QT, 1, EPI_GLU, true, false>(a, p, s) : run_p<QT, 1, EPI_GLU, false, false>(a, p, s);
         case EPI_ROPE_KV:
-            if (embed) return run_r<QT, 1, EPI_ROPE_KV, true, true>(a, R, s);
-            return norm ? run_r<QT, 1, EPI_ROPE_KV, true, false>(a, R, s)
-                        : run_r<QT, 1, EPI_ROPE_KV, false, false>(a, R, s);
+            if (embed) return run_p<QT, 1, EPI_ROPE_KV, true, true>(a, p, s);
+            return norm ? run_p<QT, 1, EPI_ROPE_KV, true, false>(a, p, s)
+                        : run_p<QT, 1, EPI_ROPE_KV, false, false>(a, p, s);
         case EPI_ARGMAX:
-            return norm ? run_r<QT, 1, EPI_ARGMAX, true, false>(a, R, s) : run_r<QT, 1, EPI_ARGMAX, false, false>(a, R, s);
+            return norm ? run_p<QT, 1, EPI_ARGMAX, true, false>(a, p, s) : run_p<QT, 1, EPI_ARGMAX, false, false>(a, p, s);
         default:
-            return norm ? run_r<QT, 1, EPI_PLAIN, true, false>(a, R, s) : run_r<QT, 1, EPI_PLAIN, false, false>(a, R, s);
+            return norm ? run_p<QT, 1, EPI_PLAIN, true, false>(a, p, s) : run_p<QT, 1, EPI_PLAIN, false, false>(a, p, s);
     }
 }
 
@@ -436,20 +614,30 @@ int launch_mv(const QWeight* w, MvArgs a, int m, int epi, bool norm, bool embed,
         set_error(TL_HIP_ERR_ARG, "ArgumentError: x and the norm weight must be 16-byte aligned");
         return TL_HIP_ERR_ARG;
     }
-    if ((size_t)m * a.nb * XPAD * 4 > 160 * 1024) {
+    if (a.n < 1 || a.nb < 1) {
+        set_error(TL_HIP_ERR_SHAPE, "ShapeMismatch: empty matvec weight");
+        return TL_HIP_ERR_SHAPE;
+    }
+    if ((uint64_t)a.n * a.nb * (w->ggml_type == TL_HIP_GGML_Q8_0 ? 32 : 16) >= (1ull << 31)) {
+        set_error(TL_HIP_ERR_ARG, "ArgumentError: quant weight of %lld x %lld exceeds the 2 GiB decode matvec limit",
+                  (long long)a.n, (long long)a.k);
+        return TL_HIP_ERR_ARG;
+    }
+    const MvPlan p = mv_plan(a.n, a.nb, w->ggml_type);
+    if ((size_t)m * a.nb * XPAD * sizeof(float) > 150 * 1024) {
         set_error(TL_HIP_ERR_ARG, "ArgumentError: k = %lld too large for the LDS-staged matvec", (long long)a.k);
         return TL_HIP_ERR_ARG;
     }
-    int R = pick_r(a.n);
     if ((epi == EPI_GLU || epi == EPI_ROPE_KV) && (a.n % 2)) {
         set_error(TL_HIP_ERR_SHAPE, "ShapeMismatch: paired epilogue needs an even row count");
         return TL_HIP_ERR_SHAPE;
     }
-    if (w->ggml_type == TL_HIP_GGML_Q4_0) return run_t<TL_HIP_GGML_Q4_0>(a, m, epi, norm, embed, R, s);
-    return run_t<TL_HIP_GGML_Q8_0>(a, m, epi, norm, embed, R, s);
+    if (w->ggml_type == TL_HIP_GGML_Q4_0) return run_t<TL_HIP_GGML_Q4_0>(a, m, epi, norm, embed, p, s);
+    return run_t<TL_HIP_GGML_Q8_0>(a, m, epi, norm, embed, p, s);
 }
 
-int mv_partials(int64_t n) { return (int)cdiv(n, 4 * pick_r(n)); }
+// Upper bound on the workgroups (= argmax partial slots) of a matvec over n rows.
+int mv_partials(int64_t n) { return (int)cdiv(n, MV_MIN_RW); }
 
 int launch_quant_matvec(const QWeight* w, const float* x, float* y, int64_t m, hipStream_t s,
                         const float* residual) {
