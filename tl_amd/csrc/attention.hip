@@ -515,51 +515,56 @@ __global__ __launch_bounds__(256) void k_attn_dec(AttnArgs a, int32_t* counter) 
     if (tid == 0) counter[(int64_t)b * a.hkv + h] = 0;  // ready for the next launch
 }
 
-// ------------------------------------------------------------------------------------------
-// Short-cache decode form: one workgroup per (query head, batch item) over all cached
-// positions, so no cross-workgroup merge exists.  The KV head's rows are read by the
-// Hq/Hkv workgroups of its group (the re-reads hit L2 / MALL); for caches of a few thousand
-// positions that costs less than a merge pass.  Eight wavefronts take 64-position chunks in
-// turn (lane = position for the scores, q held in registers -- it is uniform), keep an
-// online softmax (running max m, sum l, rescaled accumulators), and compute P.V with
-// lane = (dim group, slot); the next chunk's K and V rows are requested before the current
-// chunk is consumed.  The eight (m, l, o) states are merged through LDS.
-constexpr int QH_WAVES = 8;
-
-template <typename KVT, int N>
-__device__ __forceinline__ void load_row16(const KVT* p, uint4 (&r)[N]) {
-#pragma unroll
-    for (int c = 0; c < N; c++) r[c] = reinterpret_cast<const uint4*>(p)[c];
+// ---- short-cache form: one workgroup per (query head, batch item) ------------------------
+// W wavefronts each take 64 consecutive positions per round (W * 64 per round, one round
+// for the decode lengths it is used for).  K rows are read coalesced: LPR consecutive lanes
+// share a row (16 bytes each), so one load instruction covers 64 / LPR whole rows; the score
+// of a position is the LPR-lane sum of the partial dot products.  V rows are read by lane
+// (dim group dg = lane / 8, position slot = lane % 8), eight full rows per instruction.
+// Scores pass to the P.V lanes through LDS.  Softmax is online across rounds; the
+// wavefronts' (max, sum, o) records are merged through LDS at the end.  All arithmetic f32.
+template <int LPR>
+__device__ __forceinline__ float row_sum(float v) {  // over aligned groups of LPR lanes
+    static_assert(LPR == 8 || LPR == 16 || LPR == 32, "row width");
+    v += dpp_f<0xB1>(v);   // xor 1
+    v += dpp_f<0x4E>(v);   // xor 2
+    v += dpp_f<0x141>(v);  // half-row mirror: the other four of the eight
+    if constexpr (LPR >= 16) v += dpp_f<0x140>(v);  // row mirror: the other eight of sixteen
+    if constexpr (LPR >= 32) v += __shfl_xor(v, 16, 64);
+    return v;
 }
 
 template <typename KVT>
-__device__ __forceinline__ void cvt_chunk(const uint4& w, float* f);  // 16 bytes -> floats
+__device__ __forceinline__ void cvt16(const uint4& w, float* f);  // 16 bytes -> floats
 template <>
-__device__ __forceinline__ void cvt_chunk<__half>(const uint4& w, float* f) {
+__device__ __forceinline__ void cvt16<__half>(const uint4& w, float* f) {
     cvt8<__half>(w, f);
 }
 template <>
-__device__ __forceinline__ void cvt_chunk<float>(const uint4& w, float* f) {
+__device__ __forceinline__ void cvt16<float>(const uint4& w, float* f) {
     f[0] = __uint_as_float(w.x);
     f[1] = __uint_as_float(w.y);
     f[2] = __uint_as_float(w.z);
     f[3] = __uint_as_float(w.w);
 }
 
-template <int D, typename KVT>
-__global__ __launch_bounds__(64 * QH_WAVES) void k_attn_qh(AttnArgs a, int G) {
-    constexpr int C = 64;
-    constexpr int EPC = 16 / sizeof(KVT);  // elements per 16-byte chunk
-    constexpr int KC = D / EPC;            // chunks of a K row
+template <int D, typename KVT, int W>
+__global__ __launch_bounds__(64 * W) void k_attn_qh(AttnArgs a, int G) {
+    constexpr int C = 64;                  // positions per wavefront and round
+    constexpr int EPC = 16 / sizeof(KVT);  // elements per 16-byte load
+    constexpr int LPR = D / EPC;           // lanes per K row
+    constexpr int PPI = 64 / LPR;          // K rows per load instruction
+    constexpr int NI = C / PPI;            // K load instructions per round
     constexpr int DL = D / 8;              // dims per lane in P.V
-    constexpr int VC = DL / EPC;           // chunks of a lane's V slice
-    __shared__ float P[QH_WAVES][C];
-    __shared__ float wm[QH_WAVES], wl[QH_WAVES];
-    __shared__ float wo[QH_WAVES][D];
+    constexpr int VC = DL / EPC;           // 16-byte loads of a lane's V slice
+    __shared__ float P[W][C];
+    __shared__ float wm[W], wl[W];
+    __shared__ float wo[W][D];
     const int qh = blockIdx.x, b = blockIdx.y;
     const int h = qh / G;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int slot = lane & 7, dg = lane >> 3;
+    const int kl = lane % LPR, kr = lane / LPR;  // K: slice and row within an instruction
+    const int slot = lane & 7, dg = lane >> 3;   // V: position slot and dim group
     int64_t L = a.len.of(b);
     if (L > a.lmax) L = a.lmax;
     const int hq = a.hkv * G;
@@ -567,46 +572,61 @@ __global__ __launch_bounds__(64 * QH_WAVES) void k_attn_qh(AttnArgs a, int G) {
     const KVT* vb = reinterpret_cast<const KVT*>(a.v) + (int64_t)b * a.kv_bstride + (int64_t)h * a.lmax * D;
     const float* qp = a.q + ((int64_t)b * hq + qh) * D;
 
-    auto issue = [&](int64_t c0, uint4 (&kr)[KC], uint4 (&vr)[8][VC]) {
-        const int64_t p = c0 + lane < L ? c0 + lane : L - 1;
-        load_row16<KVT, KC>(kb + p * D, kr);
+    float qv[EPC];  // this lane's slice of q
 #pragma unroll
-        for (int j = 0; j < 8; j++) {
-            const int64_t pv = c0 + slot + 8 * j < L ? c0 + slot + 8 * j : L - 1;
-            load_row16<KVT, VC>(vb + pv * D + dg * DL, vr[j]);
-        }
-    };
-    uint4 kr[KC], vr[8][VC];
-    int64_t c0 = (int64_t)wave * C;
-    if (c0 < L) issue(c0, kr, vr);
-    float qv[D];  // uniform: scalar loads
-#pragma unroll
-    for (int i = 0; i < D; i++) qv[i] = qp[i];
-
+    for (int e = 0; e < EPC; e += 4) {
+        const float4 t = *reinterpret_cast<const float4*>(qp + kl * EPC + e);
+        qv[e] = t.x;
+        qv[e + 1] = t.y;
+        qv[e + 2] = t.z;
+        qv[e + 3] = t.w;
+    }
     float m = -INFINITY, l = 0.f, o[DL];
 #pragma unroll
     for (int i = 0; i < DL; i++) o[i] = 0.f;
-    for (; c0 < L; c0 += (int64_t)QH_WAVES * C) {
-        uint4 nkr[KC], nvr[8][VC];
-        const int64_t n0 = c0 + (int64_t)QH_WAVES * C;
-        if (n0 < L) issue(n0, nkr, nvr);
-        // score of this lane's position
-        float s = 0.f;
+
+    for (int64_t base = (int64_t)wave * C; base < L; base += (int64_t)W * C) {
+        uint4 kraw[NI], vraw[8][VC];
 #pragma unroll
-        for (int c = 0; c < KC; c++) {
-            float kf[EPC];
-            cvt_chunk<KVT>(kr[c], kf);
-#pragma unroll
-            for (int e = 0; e < EPC; e++) s = fmaf(qv[c * EPC + e], kf[e], s);
+        for (int c = 0; c < NI; c++) {
+            int64_t p = base + c * PPI + kr;
+            p = p < L ? p : L - 1;
+            kraw[c] = *reinterpret_cast<const uint4*>(kb + p * D + kl * EPC);
         }
-        const bool valid = c0 + lane < L;
-        s = valid ? s * a.scale : -INFINITY;
-        const float mn = fmaxf(m, wave_max64(s));
-        const float e = valid ? expf(s - mn) : 0.f;
+#pragma unroll
+        for (int j = 0; j < 8; j++) {
+            int64_t p = base + slot + 8 * j;
+            p = p < L ? p : L - 1;
+#pragma unroll
+            for (int c = 0; c < VC; c++) vraw[j][c] = reinterpret_cast<const uint4*>(vb + p * D + dg * DL)[c];
+        }
+        // scores: position base + c * PPI + kr lives in register s[c] of its LPR lanes
+        float s[NI], mx = -INFINITY;
+#pragma unroll
+        for (int c = 0; c < NI; c++) {
+            float kf[EPC];
+            cvt16<KVT>(kraw[c], kf);
+            float t = 0.f;
+#pragma unroll
+            for (int e = 0; e < EPC; e++) t = fmaf(qv[e], kf[e], t);
+            t = row_sum<LPR>(t);
+            s[c] = base + c * PPI + kr < L ? t * a.scale : -INFINITY;
+            mx = fmaxf(mx, s[c]);
+        }
+        const float mn = fmaxf(m, wave_max64(mx));
+        float es = 0.f;
+#pragma unroll
+        for (int c = 0; c < NI; c++) {
+            s[c] = expf(s[c] - mn);  // 0 for positions past the end
+            es += s[c];
+        }
         const float alpha = expf(m - mn);
-        l = l * alpha + wave_sum64(e);
+        l = l * alpha + wave_sum64(kl == 0 ? es : 0.f);
         m = mn;
-        P[wave][lane] = e;
+        if (kl == 0) {
+#pragma unroll
+            for (int c = 0; c < NI; c++) P[wave][c * PPI + kr] = s[c];
+        }
         __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
         __builtin_amdgcn_wave_barrier();
         __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
@@ -617,21 +637,13 @@ __global__ __launch_bounds__(64 * QH_WAVES) void k_attn_qh(AttnArgs a, int G) {
             const float pj = P[wave][slot + 8 * j];
             float vf[DL];
 #pragma unroll
-            for (int c = 0; c < VC; c++) cvt_chunk<KVT>(vr[j][c], vf + c * EPC);
+            for (int c = 0; c < VC; c++) cvt16<KVT>(vraw[j][c], vf + c * EPC);
 #pragma unroll
             for (int i = 0; i < DL; i++) o[i] = fmaf(pj, vf[i], o[i]);
         }
         __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
         __builtin_amdgcn_wave_barrier();
         __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-        if (n0 < L) {
-#pragma unroll
-            for (int c = 0; c < KC; c++) kr[c] = nkr[c];
-#pragma unroll
-            for (int j = 0; j < 8; j++)
-#pragma unroll
-                for (int c = 0; c < VC; c++) vr[j][c] = nvr[j][c];
-        }
     }
 #pragma unroll
     for (int i = 0; i < DL; i++) o[i] = sum8_dpp(o[i]);
@@ -644,13 +656,13 @@ __global__ __launch_bounds__(64 * QH_WAVES) void k_attn_qh(AttnArgs a, int G) {
         wl[wave] = l;
     }
     __syncthreads();
-    for (int d = tid; d < D; d += 64 * QH_WAVES) {
+    for (int d = tid; d < D; d += 64 * W) {
         float M = -INFINITY;
 #pragma unroll
-        for (int w = 0; w < QH_WAVES; w++) M = fmaxf(M, wm[w]);
+        for (int w = 0; w < W; w++) M = fmaxf(M, wm[w]);
         float num = 0.f, den = 0.f;
 #pragma unroll
-        for (int w = 0; w < QH_WAVES; w++) {
+        for (int w = 0; w < W; w++) {
             const float f = wl[w] > 0.f ? expf(wm[w] - M) : 0.f;  // idle wavefronts add nothing
             num = fmaf(wo[w][d], f, num);
             den = fmaf(wl[w], f, den);
@@ -659,7 +671,11 @@ __global__ __launch_bounds__(64 * QH_WAVES) void k_attn_qh(AttnArgs a, int G) {
     }
 }
 
-// Short-cache form; returns TL_HIP_ERR_ARG (no launch) for head dims it does not cover.
+bool attention_qh_supported(int kv_dtype, int D) {
+    return (kv_dtype == TL_HIP_F16 && (D == 64 || D == 128)) || (kv_dtype == TL_HIP_F32 && D == 64);
+}
+
+// Short-cache form; returns TL_HIP_ERR_ARG (no launch) for shapes it does not cover.
 int launch_attention_qh(const float* q, const void* k, const void* v, int kv_dtype, float* out,
                         int B, int hq, int hkv, int D, int64_t lmax, int64_t kv_bstride, int64_t L,
                         const int32_t* len_dev, int len_add, int len_step, float scale, hipStream_t s) {
@@ -667,13 +683,11 @@ int launch_attention_qh(const float* q, const void* k, const void* v, int kv_dty
                scale};
     const int G = hq / hkv;
     dim3 grid(hq, B);
-    const unsigned th = 64 * QH_WAVES;
-    if (D == 64 && kv_dtype == TL_HIP_F16) k_attn_qh<64, __half><<<grid, th, 0, s>>>(a, G);
-    else if (D == 128 && kv_dtype == TL_HIP_F16) k_attn_qh<128, __half><<<grid, th, 0, s>>>(a, G);
-    else if (D == 64) k_attn_qh<64, float><<<grid, th, 0, s>>>(a, G);
-    else if (D == 128) k_attn_qh<128, float><<<grid, th, 0, s>>>(a, G);
+    if (D == 64 && kv_dtype == TL_HIP_F16) k_attn_qh<64, __half, 16><<<grid, 64 * 16, 0, s>>>(a, G);
+    else if (D == 128 && kv_dtype == TL_HIP_F16) k_attn_qh<128, __half, 8><<<grid, 64 * 8, 0, s>>>(a, G);
+    else if (D == 64 && kv_dtype == TL_HIP_F32) k_attn_qh<64, float, 8><<<grid, 64 * 8, 0, s>>>(a, G);
     else {
-        set_error(TL_HIP_ERR_ARG, "ArgumentError: short-cache attention needs head_dim 64 or 128");
+        set_error(TL_HIP_ERR_ARG, "ArgumentError: short-cache attention covers head_dim 64 / 128 (f16 cache) and 64 (f32)");
         return TL_HIP_ERR_ARG;
     }
     hipError_t e = hipGetLastError();
@@ -832,7 +846,7 @@ extern "C" tl_hip_tensor* tl_hip_attention_decode(const tl_hip_tensor* qh, const
     hipStream_t s = cur_stream();
     float* ws = (float*)dev_alloc(attn_workspace_floats((int)B, (int)hkv, (int)(hq / hkv), (int)D, nsplit) * 4);
     int rc = ws ? TL_HIP_OK : TL_HIP_ERR_ALLOC;
-    if (rc == TL_HIP_OK && L <= 1024 && (D == 64 || D == 128))
+    if (rc == TL_HIP_OK && L <= 1024 && attention_qh_supported(k->dtype, (int)D))
         rc = launch_attention_qh(q->f32(), k->data, v->data, k->dtype, o->f32(), (int)B, (int)hq, (int)hkv, (int)D,
                                  lmax, hkv * lmax * D, L, nullptr, 0, 0, scale, s);
     else if (rc == TL_HIP_OK && dec)

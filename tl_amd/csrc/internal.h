@@ -153,7 +153,8 @@ int launch_attention_dec(const float* q, const void* k, const void* v, float* ou
                          int64_t kv_bstride, int64_t L, const int32_t* len_dev, int len_add,
                          int len_step, int nsplit, float scale, hipStream_t s);
 bool attention_dec_supported(int kv_dtype, int hq, int hkv, int D);
-// Short-cache form: one workgroup per (query head, batch item), D 64 or 128, f16 or f32 cache.
+// Short-cache form: one workgroup per (query head, batch item); shapes: attention_qh_supported.
+bool attention_qh_supported(int kv_dtype, int D);
 int launch_attention_qh(const float* q, const void* k, const void* v, int kv_dtype, float* out,
                         int B, int hq, int hkv, int D, int64_t lmax, int64_t kv_bstride, int64_t L,
                         const int32_t* len_dev, int len_add, int len_step, float scale, hipStream_t s);

@@ -327,7 +327,7 @@ static int enqueue_step(Llama* m, float penalty, hipStream_t s) {
         a.kv_f16 = m->kv_f16;
         a.max_seq = m->max_seq;
         if ((rc = launch_mv(m->wqkv[l], a, 1, EPI_ROPE_KV, true, l == 0, s))) return rc;
-        if (m->max_seq <= 4096 && (hd == 64 || hd == 128))  // short caches: no merge pass
+        if (m->max_seq <= 4096 && attention_qh_supported(m->kv_f16 ? TL_HIP_F16 : TL_HIP_F32, (int)hd))
             rc = launch_attention_qh(m->q, m->kc[l], m->vc[l], m->kv_f16 ? TL_HIP_F16 : TL_HIP_F32, m->ao, 1, m->H,
                                      m->KV, (int)hd, m->max_seq, 0, 0, m->pos, 1, 0, 1.0f / sqrtf((float)hd), s);
         else if (attention_dec_supported(m->kv_f16 ? TL_HIP_F16 : TL_HIP_F32, m->H, m->KV, (int)hd))
