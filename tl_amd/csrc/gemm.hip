@@ -106,89 +106,269 @@ __global__ __launch_bounds__(256) void k_qgemm_f32(const uint8_t* __restrict__ q
 }
 
 // ------------------------------------------------------- f16 MFMA quantized GEMM ----
-// Tile BM (x rows) x BN (weight rows) x 64 (two quant blocks); 4 wavefronts in a 2x2
-// grid, each computing (BM/2) x (BN/2) with 16x16x32 MFMAs.  LDS rows are padded to 72
-// halves (144 B) so the 16 lanes that read one operand column hit distinct bank groups.
-// Operand layout of v_mfma_f32_16x16x32_f16: lane l supplies A[l % 16][8*(l/16) .. +7]
-// and B[8*(l/16) .. +7][l % 16]; it receives C[4*(l/16) .. +3][l % 16].
-constexpr int M_LD = 72;
+// Y[m, n] = sum_k X[m, k] W[n, k] with v_mfma_f32_16x16x32_f16 and f32 accumulation.
+// Operand layout: lane l supplies A[l % 16][8*(l/16) .. +7] and B[8*(l/16) .. +7][l % 16]
+// and receives C[4*(l/16) .. +3][l % 16].
+//
+// X is first converted to f16 once (k_x_to_f16q), with every 32-element block stored in the
+// k order of the MFMA operands below.  Workgroup tile BM (x rows) x BN (weight rows), 4
+// wavefronts in a 2 x 2 grid, each owning (BM/2) x (BN/2).  One iteration covers 128 k =
+// 4 quant blocks with 4 MFMAs per 16 x 16 output tile; in MFMA t, lane group g (lanes
+// 16g .. 16g+15) supplies block kb+g's values held in word t of its quant data.
+//   * X rows, W quant chunks and W scales reach LDS by global_load_lds (no VGPR staging),
+//     double-buffered, with the next iteration's loads in flight during the MFMAs;
+//   * each lane turns its W word t into the f16 operand of MFMA t in registers (Q4_0: fp8
+//     reinterpretation of the nibble bytes, Q8_0: the 0x6400 magic), times the block scale
+//     d with one f16 rounding (the f16 path's rounding);
+//   * the A operand is one ds_read_b128 per 16 x 32 tile.
+// Measured on MI355X: an iteration moves 37 KB per workgroup from L2 at ~456-cycle latency,
+// which bounds this tile at roughly a quarter of the MFMA peak for M = 512 problems.
+typedef _Float16 half2v __attribute__((ext_vector_type(2)));
+constexpr int Q_KR = 4;     // quant blocks per iteration
+
+template <int QT>
+struct QWords;
+template <>
+struct QWords<TL_HIP_GGML_Q4_0> {
+    static constexpr int BYTES = 16;
+    // f16 operand of MFMA t from the block's 16 bytes: word t = bytes 4t .. 4t+3, i.e.
+    // elements 4t..4t+3 (low nibbles) and 16+4t..16+4t+3 (high nibbles), in that order.
+    // A byte holding one nibble q is, read as an OCP fp8 E4M3 value, exactly q * 2^-9, so
+    // v_cvt_scalef32_pk_f16_fp8 with scale 2^9 turns two such bytes into the f16 pair (q, q')
+    // (the instruction applies only the exponent of its scale, hence the separate d); then
+    // fma(q, d, -8 d) = (q - 8) d with one rounding (-8 d is exact).
+    __device__ static half8 operand(const uint4& raw, int t, half2v d2, half2v m8d2) {
+        const uint32_t w = t == 0 ? raw.x : t == 1 ? raw.y : t == 2 ? raw.z : raw.w;
+        const uint32_t lo = w & 0x0F0F0F0Fu, hi = (w >> 4) & 0x0F0F0F0Fu;
+        const half2v p0 = __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(lo, 512.0f, false);
+        const half2v p1 = __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(lo, 512.0f, true);
+        const half2v p2 = __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(hi, 512.0f, false);
+        const half2v p3 = __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(hi, 512.0f, true);
+        const half2v v0 = __builtin_elementwise_fma(p0, d2, m8d2), v1 = __builtin_elementwise_fma(p1, d2, m8d2);
+        const half2v v2 = __builtin_elementwise_fma(p2, d2, m8d2), v3 = __builtin_elementwise_fma(p3, d2, m8d2);
+        return half8{v0.x, v0.y, v1.x, v1.y, v2.x, v2.y, v3.x, v3.y};
+    }
+};
+template <>
+struct QWords<TL_HIP_GGML_Q8_0> {
+    static constexpr int BYTES = 32;
+    // words 2t, 2t+1 = elements 8t .. 8t+7 as pairs (8t, 8t+2) (8t+1, 8t+3) (8t+4, 8t+6)
+    // (8t+5, 8t+7); (q ^ 0x80) | 0x6400 is 1024 + q + 128
+    __device__ static half8 operand(const uint4 (&raw)[2], int t, half2v d2, half2v) {
+        const uint32_t src[8] = {raw[0].x, raw[0].y, raw[0].z, raw[0].w, raw[1].x, raw[1].y, raw[1].z, raw[1].w};
+        const half2v off = {(_Float16)-1152.0f, (_Float16)-1152.0f};
+        half8 r;
+#pragma unroll
+        for (int h = 0; h < 2; h++) {
+            const uint32_t w = src[2 * t + h] ^ 0x80808080u;
+#pragma unroll
+            for (int p = 0; p < 2; p++) {
+                const uint32_t bits = ((w >> (8 * p)) & 0x00FF00FFu) | 0x64006400u;
+                const half2v v = (__builtin_bit_cast(half2v, bits) + off) * d2;
+                r[4 * h + 2 * p] = v.x;
+                r[4 * h + 2 * p + 1] = v.y;
+            }
+        }
+        return r;
+    }
+};
+
+template <int QT>
+struct QRaw {
+    uint4 v[QWords<QT>::BYTES / 16];
+};
+
+// X f32 [m, k] -> f16 [m, k] with every 32-element block stored in the k-slot order of the
+// MFMA operands above: unit (row, block, word t) = 8 halves, one 16-byte store.
+template <int QT>
+__global__ __launch_bounds__(256) void k_x_to_f16q(const float* __restrict__ x, _Float16* __restrict__ x16,
+                                                   int64_t units) {
+    const int64_t u = (int64_t)blockIdx.x * 256 + threadIdx.x;  // = row * nb * 4 + block * 4 + t
+    if (u >= units) return;
+    const int t = (int)(u & 3);
+    const float4* p = reinterpret_cast<const float4*>(x + (u >> 2) * 32);
+    const float4 e = p[QT == TL_HIP_GGML_Q4_0 ? t : 2 * t], f = p[QT == TL_HIP_GGML_Q4_0 ? t + 4 : 2 * t + 1];
+    half8 h;
+    if constexpr (QT == TL_HIP_GGML_Q4_0) {  // slots: e0 e1 e2 e3 f0 f1 f2 f3
+        h[0] = (_Float16)e.x; h[1] = (_Float16)e.y; h[2] = (_Float16)e.z; h[3] = (_Float16)e.w;
+        h[4] = (_Float16)f.x; h[5] = (_Float16)f.y; h[6] = (_Float16)f.z; h[7] = (_Float16)f.w;
+    } else {  // slots: e0 e2 e1 e3 f0 f2 f1 f3
+        h[0] = (_Float16)e.x; h[1] = (_Float16)e.z; h[2] = (_Float16)e.y; h[3] = (_Float16)e.w;
+        h[4] = (_Float16)f.x; h[5] = (_Float16)f.z; h[6] = (_Float16)f.y; h[7] = (_Float16)f.w;
+    }
+    reinterpret_cast<half8*>(x16)[u] = h;
+}
+
+// global_load_lds: each lane's SIZE bytes from src land at lds + lane * SIZE (one 64-lane
+// instruction writes 64 consecutive elements).  The builtin exists only in the device pass.
+__device__ __forceinline__ void lds_dma16(const void* src, void* lds) {
+#if defined(__HIP_DEVICE_COMPILE__)
+    __builtin_amdgcn_global_load_lds(src, lds, 16, 0, 0);
+#endif
+}
+__device__ __forceinline__ void lds_dma4(const void* src, void* lds) {
+#if defined(__HIP_DEVICE_COMPILE__)
+    __builtin_amdgcn_global_load_lds(src, lds, 4, 0, 0);
+#endif
+}
 
 template <int QT, int BM, int BN>
-__global__ __launch_bounds__(256) void k_qgemm_mfma(const uint8_t* __restrict__ qs,
-                                                    const __half* __restrict__ dsc,
-                                                    const float* __restrict__ x,
-                                                    float* __restrict__ y, int64_t m,
-                                                    int64_t n, int64_t k, int64_t nb) {
-    __shared__ __attribute__((aligned(16))) _Float16 As[BM * M_LD];
-    __shared__ __attribute__((aligned(16))) _Float16 Bs[BN * M_LD];
-    constexpr int TM = BM / 32, TN = BN / 32;  // 16x16 tiles per wave in m / n
-    const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
-    const int wm = wave >> 1, wn = wave & 1;
-    const int64_t m0 = (int64_t)blockIdx.y * BM, n0 = (int64_t)blockIdx.x * BN;
+__global__ __launch_bounds__(256, 2) void k_qgemm_mfma(const uint8_t* __restrict__ qs,
+                                                       const __half* __restrict__ dsc,
+                                                       const _Float16* __restrict__ x16,
+                                                       float* __restrict__ y, int64_t m,
+                                                       int64_t n, int64_t k, int64_t nb, int mt) {
+    constexpr int TM = BM / 32, TN = BN / 32;  // 16 x 16 tiles per wavefront
+    constexpr int QB = QWords<QT>::BYTES;
+    constexpr int QC = QB / 16;                // 16-byte chunks per quant block
+    constexpr int CPR = Q_KR * QC;             // W chunks per row and iteration
+    constexpr int RSH = CPR == 4 ? 2 : 1;      // W chunk swizzle: + (row >> RSH)
+    constexpr int XI = BM * 16 / 256;          // X chunks per thread per iteration
+    constexpr int WI = BN * CPR / 256;         // W chunks per thread per iteration
+    constexpr int DI = BN * Q_KR / 256;        // scales per thread per iteration
+    constexpr int NS = 2;                      // pipeline stages (LDS: X + W per stage)
+    constexpr int GI = XI + WI + DI;           // DMA instructions per thread per stage
+    static_assert(XI >= 1 && WI >= 1 && DI >= 1 && (NS - 2) * GI <= 63, "tile");
+    // Every operand reaches LDS through global_load_lds (a wavefront's instruction writes 64
+    // consecutive LDS elements, one per lane), so no load in the main loop writes a VGPR and
+    // the pipeline is governed by one counted wait per iteration.
+    //  * X: two stages.  Row r's 16-byte chunk c (= block * 4 + word) sits at c ^ (r & 15).
+    //  * W: three stages of BN rows x CPR chunks, chunk c of row r at (c + (r >> RSH)) mod
+    //    CPR, and BN x 4 scales.  Both swizzles make the 16 lanes that read one operand
+    //    column hit 16 distinct 16-byte bank groups.
+    __shared__ __attribute__((aligned(16))) _Float16 Xs[NS][BM * 128];
+    __shared__ __attribute__((aligned(16))) uint8_t Wq[NS][BN * CPR * 16];
+    __shared__ __attribute__((aligned(16))) uint32_t Wd[NS][BN * Q_KR];  // aligned word holding the scale
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int wm = wave >> 1, wn = wave & 1, col = lane & 15, g = lane >> 4;
+    // Tile of this workgroup.  Workgroups are dispatched to the 8 XCDs round-robin (id % 8);
+    // with mt (M tiles) dividing 8, XCD x takes only M tile x % mt, so each XCD's L2 holds one
+    // X row band while the weight stream passes through; mt = 0 selects the plain mapping.
+    int64_t mtile, ntile;
+    if (mt > 0) {
+        const int xcd = blockIdx.x & 7, l = blockIdx.x >> 3, rep = 8 / mt;
+        mtile = xcd % mt;
+        ntile = (int64_t)l * rep + xcd / mt;
+    } else {
+        const int64_t nt = (n + BN - 1) / BN;
+        mtile = blockIdx.x / nt;
+        ntile = blockIdx.x % nt;
+    }
+    const int64_t m0 = mtile * BM, n0 = ntile * BN;
+
     floatx4 acc[TM][TN];
 #pragma unroll
     for (int i = 0; i < TM; i++)
 #pragma unroll
         for (int j = 0; j < TN; j++) acc[i][j] = floatx4{0.f, 0.f, 0.f, 0.f};
 
-    for (int64_t kb = 0; kb < nb; kb += 2) {
-        // ---- stage X: BM rows x 64 floats (16 float4 per row) -> f16
-        constexpr int XV = BM * 16 / 256;
+    // Per-lane source offsets (bytes) are fixed for the whole K loop; an iteration adds one
+    // uniform advance, so each DMA issue is a scalar base plus a VGPR offset.  K is a multiple
+    // of 128 (checked at launch): no block past nb is ever addressed.
+    uint32_t xoff[XI], woff[WI], doff[DI];
 #pragma unroll
-        for (int i = 0; i < XV; i++) {
-            int idx = t + i * 256;
-            int r = idx >> 4, c4 = idx & 15;
-            float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
-            int64_t kc = kb * 32 + c4 * 4;
-            if (m0 + r < m && kc < k) v = *reinterpret_cast<const float4*>(x + (m0 + r) * k + kc);
-            _Float16* dst = As + r * M_LD + c4 * 4;
-            dst[0] = (_Float16)v.x;
-            dst[1] = (_Float16)v.y;
-            dst[2] = (_Float16)v.z;
-            dst[3] = (_Float16)v.w;
+    for (int u = 0; u < XI; u++) {
+        const int slot = (wave * XI + u) * 64 + lane, r = slot >> 4, c = (slot & 15) ^ (r & 15);
+        const int64_t row = m0 + r < m ? m0 + r : m - 1;  // rows past m feed outputs that are not stored
+        xoff[u] = (uint32_t)((row * k + (c >> 2) * 32 + (c & 3) * 8) * 2);
+    }
+#pragma unroll
+    for (int u = 0; u < WI; u++) {
+        const int slot = (wave * WI + u) * 64 + lane, r = slot / CPR, c = (slot % CPR - (r >> RSH)) & (CPR - 1);
+        const int64_t row = n0 + r < n ? n0 + r : n - 1;
+        woff[u] = (uint32_t)((row * nb + c / QC) * QB + (c % QC) * 16);
+    }
+#pragma unroll
+    for (int u = 0; u < DI; u++) {  // the 4-byte word that holds scale (row, block)
+        const int slot = (wave * DI + u) * 64 + lane;
+        const int64_t row = n0 + (slot >> 2) < n ? n0 + (slot >> 2) : n - 1;
+        doff[u] = (uint32_t)(((row * nb + (slot & 3)) >> 1) * 4);
+    }
+    auto issue_x = [&](int64_t kb, int st) {
+        const char* src = reinterpret_cast<const char*>(x16) + kb * 64;  // 32 halves per block
+#pragma unroll
+        for (int u = 0; u < XI; u++) lds_dma16(src + xoff[u], &Xs[st][(wave * XI + u) * 64 * 8]);
+    };
+    auto issue_w = [&](int64_t kb, int st) {
+        const char* src = reinterpret_cast<const char*>(qs) + kb * QB;
+#pragma unroll
+        for (int u = 0; u < WI; u++) lds_dma16(src + woff[u], &Wq[st][(wave * WI + u) * 64 * 16]);
+        const char* dsrc = reinterpret_cast<const char*>(dsc) + kb * 2;  // kb even: whole words
+#pragma unroll
+        for (int u = 0; u < DI; u++) lds_dma4(dsrc + doff[u], &Wd[st][(wave * DI + u) * 64]);
+    };
+    uint32_t dpar[TN];  // which half of its word holds this lane's scale (kb is even)
+#pragma unroll
+    for (int j = 0; j < TN; j++) {
+        const int r = wn * (BN / 2) + 16 * j + col;
+        const int64_t row = n0 + r < n ? n0 + r : n - 1;
+        dpar[j] = (uint32_t)((row * nb + g) & 1) * 16;
+    }
+    auto compute = [&](int xst, int wst, int64_t kb) {
+        QRaw<QT> wr[TN];
+        half2v d2[TN], m8d2[TN];
+#pragma unroll
+        for (int j = 0; j < TN; j++) {
+            const int r = wn * (BN / 2) + 16 * j + col;
+#pragma unroll
+            for (int h = 0; h < QC; h++)
+                wr[j].v[h] = *reinterpret_cast<const uint4*>(&Wq[wst][(r * CPR + ((g * QC + h + (r >> RSH)) & (CPR - 1))) * 16]);
+            const uint32_t b = (Wd[wst][r * Q_KR + g] >> dpar[j]) & 0xFFFFu;
+            d2[j] = __builtin_bit_cast(half2v, b | (b << 16));
+            m8d2[j] = d2[j] * half2v{(_Float16)-8.0f, (_Float16)-8.0f};
         }
-        // ---- stage W: BN rows x 2 blocks, dequantised then rounded to f16
-        for (int idx = t; idx < BN * 2; idx += 256) {
-            int r = idx >> 1, bsel = idx & 1;
-            int64_t row = n0 + r < n ? n0 + r : n - 1;
-            _Float16* dst = Bs + r * M_LD + bsel * 32;
-            if (kb + bsel < nb) {
-                float v[32];
-                dequant_block<QT>(qs, dsc, row * nb + kb + bsel, v);
+        const _Float16* xs = Xs[xst];
 #pragma unroll
-                for (int j = 0; j < 32; j++) dst[j] = (_Float16)v[j];
-            } else {
+        for (int t = 0; t < 4; t++) {
+            half8 a[TM];
 #pragma unroll
-                for (int j = 0; j < 32; j++) dst[j] = (_Float16)0.f;
+            for (int i = 0; i < TM; i++)
+                a[i] = *reinterpret_cast<const half8*>(xs + (wm * (BM / 2) + 16 * i + col) * 128 + ((g * 4 + t) ^ col) * 8);
+#pragma unroll
+            for (int j = 0; j < TN; j++) {
+                half8 bop;
+                if constexpr (QT == TL_HIP_GGML_Q4_0) bop = QWords<QT>::operand(wr[j].v[0], t, d2[j], m8d2[j]);
+                else bop = QWords<QT>::operand(wr[j].v, t, d2[j], m8d2[j]);
+#pragma unroll
+                for (int i = 0; i < TM; i++) acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[i], bop, acc[i][j], 0, 0, 0);
             }
         }
+    };
+
+    // NS-stage pipeline: stage it % NS holds X and W of iteration it.  Groups 0 .. NS-2 are
+    // issued up front; iteration it waits until its own group has landed (loads retire in
+    // issue order, so at most the groups of it+1 .. it+NS-2 may still be outstanding, GI
+    // instructions each), the barrier makes every wavefront's chunks visible and frees the
+    // stage iteration it-1 read, and group it+NS-1 goes into that stage.
+    const int64_t iters = nb / Q_KR;
+    for (int64_t i0 = 0; i0 < NS - 1 && i0 < iters; i0++) {
+        issue_x(i0 * Q_KR, (int)i0);
+        issue_w(i0 * Q_KR, (int)i0);
+    }
+    for (int64_t it = 0; it < iters; it++) {
+        const int64_t after = iters - 1 - it < NS - 2 ? iters - 1 - it : NS - 2;  // groups issued after it
+        if (after == 2) __builtin_amdgcn_s_waitcnt(0xF70 | (2 * GI & 15) | ((2 * GI >> 4) << 14));
+        else if (after == 1) __builtin_amdgcn_s_waitcnt(0xF70 | (GI & 15) | ((GI >> 4) << 14));
+        else __builtin_amdgcn_s_waitcnt(0xF70);  // vmcnt(0); the encodings carry no lgkm / exp wait
         __syncthreads();
-#pragma unroll
-        for (int ks = 0; ks < 2; ks++) {
-            half8 a[TM], b[TN];
-            const int kcol = ks * 32 + (lane >> 4) * 8;
-#pragma unroll
-            for (int i = 0; i < TM; i++)
-                a[i] = *reinterpret_cast<const half8*>(As + (wm * (BM / 2) + i * 16 + (lane & 15)) * M_LD + kcol);
-#pragma unroll
-            for (int j = 0; j < TN; j++)
-                b[j] = *reinterpret_cast<const half8*>(Bs + (wn * (BN / 2) + j * 16 + (lane & 15)) * M_LD + kcol);
-#pragma unroll
-            for (int i = 0; i < TM; i++)
-#pragma unroll
-                for (int j = 0; j < TN; j++)
-                    acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[i], b[j], acc[i][j], 0, 0, 0);
+        __builtin_amdgcn_sched_barrier(0);
+        if (it + NS - 1 < iters) {
+            const int st = (int)((it + NS - 1) % NS);
+            issue_x((it + NS - 1) * Q_KR, st);
+            issue_w((it + NS - 1) * Q_KR, st);
         }
-        __syncthreads();
+        __builtin_amdgcn_sched_barrier(0);
+        const int cur = (int)(it % NS);
+        compute(cur, cur, it * Q_KR);
     }
 #pragma unroll
     for (int i = 0; i < TM; i++)
 #pragma unroll
         for (int j = 0; j < TN; j++) {
-            int64_t c = n0 + wn * (BN / 2) + j * 16 + (lane & 15);
+            const int64_t c = n0 + wn * (BN / 2) + 16 * j + col;
 #pragma unroll
             for (int e = 0; e < 4; e++) {
-                int64_t r = m0 + wm * (BM / 2) + i * 16 + (lane >> 4) * 4 + e;
+                const int64_t r = m0 + wm * (BM / 2) + 16 * i + 4 * g + e;
                 if (r < m && c < n) y[r * n + c] = acc[i][j][e];
             }
         }
@@ -202,6 +382,7 @@ int launch_quant_gemm(const QWeight* w, const float* x, float* y, int64_t m, hip
         return TL_HIP_ERR_ARG;
     }
     const bool q4 = w->ggml_type == TL_HIP_GGML_Q4_0;
+    if (mode != 0 && w->nb % Q_KR != 0) mode = 0;  // the MFMA pipeline takes K in steps of 128
     if (mode == 0) {
         dim3 grid((unsigned)cdiv(w->n, F_BN), (unsigned)cdiv(m, F_BM));
         if (q4)
@@ -209,12 +390,22 @@ int launch_quant_gemm(const QWeight* w, const float* x, float* y, int64_t m, hip
         else
             k_qgemm_f32<TL_HIP_GGML_Q8_0><<<grid, 256, 0, s>>>(w->qs, w->d, x, y, m, w->n, w->k, w->nb);
     } else {
+        // X -> f16 in the operand k order (a workspace of m * k halves), then the MFMA GEMM
+        _Float16* x16 = static_cast<_Float16*>(dev_alloc((size_t)m * w->k * sizeof(_Float16)));
+        if (!x16) return TL_HIP_ERR_ALLOC;
+        const int64_t units = m * w->nb * 4;
         constexpr int BM = 128, BN = 64;
-        dim3 grid((unsigned)cdiv(w->n, BN), (unsigned)cdiv(m, BM));
-        if (q4)
-            k_qgemm_mfma<TL_HIP_GGML_Q4_0, BM, BN><<<grid, 256, 0, s>>>(w->qs, w->d, x, y, m, w->n, w->k, w->nb);
-        else
-            k_qgemm_mfma<TL_HIP_GGML_Q8_0, BM, BN><<<grid, 256, 0, s>>>(w->qs, w->d, x, y, m, w->n, w->k, w->nb);
+        const int64_t mtn = cdiv(m, BM), ntn = cdiv(w->n, BN), tiles = mtn * ntn;
+        // XCD-local M tiles when mt divides 8 and the grid fills the XCDs evenly
+        const int mt = (8 % mtn == 0 && tiles % 8 == 0) ? (int)mtn : 0;
+        if (q4) {
+            k_x_to_f16q<TL_HIP_GGML_Q4_0><<<(unsigned)cdiv(units, 256), 256, 0, s>>>(x, x16, units);
+            k_qgemm_mfma<TL_HIP_GGML_Q4_0, BM, BN><<<(unsigned)tiles, 256, 0, s>>>(w->qs, w->d, x16, y, m, w->n, w->k, w->nb, mt);
+        } else {
+            k_x_to_f16q<TL_HIP_GGML_Q8_0><<<(unsigned)cdiv(units, 256), 256, 0, s>>>(x, x16, units);
+            k_qgemm_mfma<TL_HIP_GGML_Q8_0, BM, BN><<<(unsigned)tiles, 256, 0, s>>>(w->qs, w->d, x16, y, m, w->n, w->k, w->nb, mt);
+        }
+        dev_free(x16);
     }
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return hip_fail(e, "quant gemm launch");

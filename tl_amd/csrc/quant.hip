@@ -144,7 +144,7 @@ tl_hip_qtensor* tl_hip_qtensor_new(int ggml_type, const uint8_t* data, size_t nb
     w->shape[0] = n;
     w->shape[1] = k;
     w->qs = (uint8_t*)dev_alloc(nblocks * QB);
-    w->d = (__half*)dev_alloc(nblocks * 2);
+    w->d = (__half*)dev_alloc(nblocks * 2 + 4);  // + 4: the prefill GEMM reads scales as aligned words
     uint8_t* raw = (uint8_t*)dev_alloc(nbytes);
     if (!w->qs || !w->d || !raw) {
         dev_free(w->qs);
