@@ -75,6 +75,94 @@ def bench_matvec(dev, launches=340, copies=34):
     return avg_s
 
 
+MFMA_F16_PEAK_TFLOPS = 2500.0
+GEMM_SHAPES = [(4096, 4096), (11008, 4096), (4096, 11008)]  # configs[2] (N, K), M = 512
+ATTN_CASES = [(512, 1), (2048, 1), (8192, 1), (512, 8), (2048, 8), (8192, 8)]  # configs[3] (L, B)
+
+
+def _timed(dev, launch, reps):
+    """Average seconds per call of launch(i) over reps back-to-back calls on the library
+    stream (a stall kernel covers the host's enqueue time)."""
+    import ctypes as C
+    lib = dev.lib
+    for i in range(3):
+        launch(i)
+    dev.synchronize()
+    e0, e1 = lib.tl_hip_event_create(), lib.tl_hip_event_create()
+    lib.tl_hip_stall(20000)
+    lib.tl_hip_event_record(e0)
+    for i in range(reps):
+        launch(i)
+    lib.tl_hip_event_record(e1)
+    ms = C.c_float()
+    lib.tl_hip_event_elapsed_ms(e0, e1, C.byref(ms))
+    lib.tl_hip_event_destroy(e0)
+    lib.tl_hip_event_destroy(e1)
+    return ms.value / 1e3 / reps
+
+
+def bench_gemm(dev, m=512, reps=20):
+    """Quantized prefill GEMM on the f16 MFMA path (tl_hip_launch_quant_gemm, mode 1: the
+    f32 -> f16 operand conversion + the MFMA kernel) at the configs[2] shapes."""
+    import ctypes as C
+
+    from tl_amd import GGML_Q4_0, GGML_Q8_0, QTensor
+    from tl_amd.quant import random_q4_0_blocks, random_q8_0_blocks
+
+    lib = dev.lib
+    rows = []
+    for t, gen, name in ((GGML_Q4_0, random_q4_0_blocks, "Q4_0"), (GGML_Q8_0, random_q8_0_blocks, "Q8_0")):
+        for n, k in GEMM_SHAPES:
+            rng = np.random.default_rng(0x71520000 + n + k)
+            q = QTensor(t, gen(rng, n, k), (n, k))
+            h = q.upload(lib)
+            x = dev.tensor_new(rng.standard_normal((m, k)).astype(np.float32))
+            y = dev.tensor_zeros((m, n))
+            stream = lib.tl_hip_stream()
+
+            def launch(i):
+                if lib.tl_hip_launch_quant_gemm(h, C.c_void_p(x.data_ptr), C.c_void_p(y.data_ptr), m, 1, stream):
+                    raise RuntimeError(lib.tl_hip_last_error())
+            sec = _timed(dev, launch, reps)
+            tflops = 2.0 * m * n * k / sec / 1e12
+            rows.append({"type": name, "m": m, "n": n, "k": k, "us": round(sec * 1e6, 2),
+                         "tflops": round(tflops, 1), "frac": round(tflops / MFMA_F16_PEAK_TFLOPS, 4)})
+            log(f"[bench] prefill GEMM {name} M={m} N={n} K={k}: {sec * 1e6:.1f} us, {tflops:.0f} TFLOP/s "
+                f"({100 * tflops / MFMA_F16_PEAK_TFLOPS:.1f}% of dense f16 MFMA peak)")
+            q.release()
+    return rows
+
+
+def bench_attention(dev, reps=20, hq=32, hkv=8, d=128, min_bytes=300 << 20):
+    """Decode attention over an f16 KV cache at the configs[3] cases, rotating KV copies so
+    that at least 300 MB are touched (the 256 MB Infinity Cache cannot hold them)."""
+    rows = []
+    for L, B in ATTN_CASES:
+        rng = np.random.default_rng(0x71530000 + L + B)
+        kv_bytes = 2 * B * hkv * L * d * 2
+        copies = max(1, min(64, -(-min_bytes // kv_bytes)))
+        q = dev.tensor_new(rng.standard_normal((B, hq, d)).astype(np.float32))
+        kvs = []
+        for _ in range(copies):
+            kh = rng.standard_normal((B, hkv, L, d)).astype(np.float16)
+            kvs.append((dev.tensor_new_f16(kh), dev.tensor_new_f16(kh[..., ::-1].copy())))
+
+        def launch(i):
+            k, v = kvs[i % copies]
+            dev.attention_decode(q, k, v, L, 1.0 / np.sqrt(d)).release()
+        sec = _timed(dev, launch, max(reps, copies))
+        algo = kv_bytes + B * hq * d * 4 * 2
+        gbs = algo / sec / 1e9
+        rows.append({"L": L, "B": B, "us": round(sec * 1e6, 2), "gbs": round(gbs, 1),
+                     "frac": round(gbs / HBM_PEAK_GBS, 4)})
+        log(f"[bench] decode attention L={L} B={B}: {sec * 1e6:.1f} us, {gbs:.0f} GB/s")
+        for k, v in kvs:
+            k.release()
+            v.release()
+        q.release()
+    return rows
+
+
 def cpu_baseline(cfg, L):
     """Faithful tl_cpu decode cost for one token at cache length L: per layer the seven
     linears as matmul_impl over the cached transposed f32 weights (system.rs:193-222,
@@ -126,6 +214,7 @@ def main():
     ap.add_argument("--kv", choices=["f16", "f32"], default="f16")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-graph", action="store_true", help="eager launches instead of hipGraph replay")
+    ap.add_argument("--no-extra", action="store_true", help="skip the prefill GEMM and attention legs")
     ap.add_argument("--matvec-only", action="store_true",
                     help="only the 4096x4096 matvec timing plus a 64 MiB device copy (counter runs)")
     args = ap.parse_args()
@@ -158,6 +247,11 @@ def main():
         print(json.dumps({"matvec_avg_us": round(avg_s * 1e6, 3), "matvec_gbs": round(achieved, 1),
                           "copy_bytes": nbytes}), flush=True)
         return
+
+    gemm = attn = None
+    if not args.no_extra:
+        gemm = bench_gemm(dev)
+        attn = bench_attention(dev)
 
     log("[bench] generating synthetic TinyLlama-shape Q4_0 weights ...")
     t0 = time.time()
@@ -227,6 +321,10 @@ def main():
             "avg_launch_us": round(avg_s * 1e6, 3),
         },
         "cpu_baseline": cpu,
+        "prefill_gemm": {"path": "f16 MFMA (v_mfma_f32_16x16x32_f16), f32 accumulate", "unit": "TFLOP/s",
+                         "peak": MFMA_F16_PEAK_TFLOPS, "shapes": gemm},
+        "decode_attention": {"kv": "f16", "hq": 32, "hkv": 8, "head_dim": 128, "unit": "GB/s",
+                             "peak": HBM_PEAK_GBS, "cases": attn},
     }
     print(json.dumps(out), flush=True)
 
