@@ -30,9 +30,9 @@ MATVEC_N = MATVEC_K = 4096
 MATVEC_BYTES = MATVEC_N * MATVEC_K // 32 * 18 + MATVEC_K * 4 + MATVEC_N * 4  # 9,469,952
 HBM_PEAK_GBS = 8000.0
 # HBM bytes per 4096 x 4096 matvec launch from the two counter runs of
-# `bench.py --matvec-only` (FETCH_SIZE 4,701.01 KiB x 1.9989 + WRITE_SIZE 16.0 KiB x 1.0, the
-# scale factors read off a 64 MiB device copy in the same runs): 1.018 x the algorithmic bytes
-MATVEC_TRAFFIC = 9_639_000
+# `bench.py --matvec-only` (FETCH_SIZE 4,713.04 KiB x 1.99895 + WRITE_SIZE 16.0 KiB x 1.0, the
+# scale factors read off a 64 MiB device copy in the same runs): 1.020 x the algorithmic bytes
+MATVEC_TRAFFIC = 9_663_629
 
 
 def log(*a):
@@ -215,6 +215,7 @@ def main():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-graph", action="store_true", help="eager launches instead of hipGraph replay")
     ap.add_argument("--no-extra", action="store_true", help="skip the prefill GEMM and attention legs")
+    ap.add_argument("--gemm-only", action="store_true", help="only the prefill GEMM leg (counter runs)")
     ap.add_argument("--matvec-only", action="store_true",
                     help="only the 4096x4096 matvec timing plus a 64 MiB device copy (counter runs)")
     args = ap.parse_args()
@@ -230,6 +231,10 @@ def main():
     cfg = LlamaConfig.tinyllama(max_seq=2048)
     if args.prompt + args.warmup + args.steps > cfg.max_seq:
         sys.exit("prompt + warmup + steps exceed the 2048-position cache")
+
+    if args.gemm_only:
+        print(json.dumps({"prefill_gemm": bench_gemm(dev)}), flush=True)
+        return
 
     log("[bench] Q4_0 4096x4096 matvec roofline ...")
     avg_s = bench_matvec(dev)
