@@ -45,6 +45,8 @@ extern "C" {
 #define TL_HIP_GGML_F16 1
 #define TL_HIP_GGML_Q4_0 2
 #define TL_HIP_GGML_Q8_0 8
+#define TL_HIP_GGML_Q4_K 12
+#define TL_HIP_GGML_Q6_K 14
 
 typedef struct tl_hip_tensor tl_hip_tensor;   /* GpuTensor (tl_backend tensor.rs:7-55) */
 typedef struct tl_hip_qtensor tl_hip_qtensor; /* QTensor + gpu_raw_cache (quantized.rs:29-40) */
@@ -105,19 +107,23 @@ tl_hip_tensor* tl_hip_tensor_reshape(const tl_hip_tensor* t, const int64_t* shap
 /* ------------------------------------------------------- quantized weights -------- */
 /* Upload of one GGUF tensor: gguf.rs:129-189 hands over the raw block bytes with the
  * row-major shape [n, k]; QTensor::dequantize_to_tensor's size checks apply
- * (quantized.rs:182-260).  Q4_0 and Q8_0 are repacked once into the device residency
- * format (the gpu_raw_cache of system.rs:316-331); F16/F32 are rejected (TypeMismatch). */
+ * (quantized.rs:182-260 for Q4_0 / Q8_0, 268-400 for Q6_K / Q4_K; rows must hold whole
+ * blocks: k % 32, k % 256 for the K-quants).  The blocks are repacked once into the device
+ * residency format (the gpu_raw_cache of system.rs:316-331, which the reference keeps for
+ * Q4_K / Q6_K); F16/F32 are rejected (TypeMismatch). */
 tl_hip_qtensor* tl_hip_qtensor_new(int ggml_type, const uint8_t* data, size_t nbytes,
                                    const int64_t* shape, int rank);
 int tl_hip_qtensor_release(tl_hip_qtensor* q);
 /* QTensor::dequantize_to_tensor (quantized.rs:117-165): f32 [n, k] on the device. */
 tl_hip_tensor* tl_hip_qtensor_dequantize(const tl_hip_qtensor* q);
 /* tl_qtensor_matmul (crates/tl_runtime/src/system.rs:180-382): y = x . W^T with x
- * [..., k] f32 and W [n, k] quantized; y is [..., n].  Fused dequant + product; m <= 4
- * rows take the matvec kernel, larger m the tiled GEMM. */
+ * [..., k] f32 and W [n, k] quantized; y is [..., n].  Fused dequant + product for all four
+ * types (the reference fuses Q4_K / Q6_K on its GPU backends, cuda_mul_mv_q4_k /
+ * cuda_mul_mv_q6_k at device_ffi.rs:1803-1833); m <= 4 rows take the matvec kernel, larger
+ * m the tiled GEMM. */
 tl_hip_tensor* tl_hip_qtensor_matmul(const tl_hip_tensor* x, const tl_hip_qtensor* q);
 /* Same with the f16-MFMA prefill GEMM for m > 4 (dequant -> f16 LDS tiles -> MFMA,
- * f32 accumulate); tolerance class "f16 path". */
+ * f32 accumulate); tolerance class "f16 path".  Q4_K / Q6_K weights take the f32 GEMM. */
 tl_hip_tensor* tl_hip_qtensor_matmul_f16(const tl_hip_tensor* x, const tl_hip_qtensor* q);
 
 /* ---------------------------------------------------------------- raw launchers --- */

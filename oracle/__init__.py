@@ -23,6 +23,8 @@ _PROTOS = {
     "tlo_dequantize_f16": (_int, [_u8p, _i64, _f32p]),
     "tlo_dequantize_q4_0": (_int, [_u8p, _i64, _i64, _f32p]),
     "tlo_dequantize_q8_0": (_int, [_u8p, _i64, _i64, _f32p]),
+    "tlo_dequantize_q4_k": (_int, [_u8p, _i64, _i64, _f32p]),
+    "tlo_dequantize_q6_k": (_int, [_u8p, _i64, _i64, _f32p]),
     "tlo_transpose_2d": (None, [_f32p, _i64, _i64, _f32p]),
     "tlo_transpose": (_int, [_f32p, _i64p, _int, _int, _int, _f32p]),
     "tlo_matmul": (_int, [_f32p, _i64p, _int, _f32p, _i64p, _int, _f32p]),
@@ -109,6 +111,10 @@ def dequantize(ggml_type, data, numel):
         rc = lib().tlo_dequantize_q4_0(d.ctypes.data_as(_u8p), d.size, numel, _p(out))
     elif ggml_type == 8:
         rc = lib().tlo_dequantize_q8_0(d.ctypes.data_as(_u8p), d.size, numel, _p(out))
+    elif ggml_type == 12:
+        rc = lib().tlo_dequantize_q4_k(d.ctypes.data_as(_u8p), d.size, numel, _p(out))
+    elif ggml_type == 14:
+        rc = lib().tlo_dequantize_q6_k(d.ctypes.data_as(_u8p), d.size, numel, _p(out))
     elif ggml_type == 1:
         rc = lib().tlo_dequantize_f16(d.ctypes.data_as(_u8p), d.size, _p(out))
     else:
@@ -310,7 +316,7 @@ class Llama:
 
     def load(self, tensors, ggml_type=2):
         cfg = self.cfg
-        from tl_amd.llama import SLOTS  # shapes only (host-side naming)
+        from tl_amd.llama import SLOTS, linear_type  # shapes and type plan only (host-side naming)
         for kind, layer, which, payload in tensors:
             if kind == "embedding":
                 p = _f(payload)
@@ -319,9 +325,11 @@ class Llama:
                 p = _f(payload)
                 _rc(lib().tlo_llama_set_norm(self.h, layer, which, _p(p)), "set_norm")
             else:
-                n, k = cfg.linear_shape(SLOTS[which] if layer >= 0 else "output")
+                name = SLOTS[which] if layer >= 0 else "output"
+                n, k = cfg.linear_shape(name)
                 p = np.ascontiguousarray(payload, dtype=np.uint8)
-                _rc(lib().tlo_llama_set_linear(self.h, layer, which, p.ctypes.data_as(_u8p), p.size, ggml_type, n, k),
+                t = linear_type(ggml_type, cfg, layer, name)
+                _rc(lib().tlo_llama_set_linear(self.h, layer, which, p.ctypes.data_as(_u8p), p.size, t, n, k),
                     "set_linear")
 
     def reset(self):

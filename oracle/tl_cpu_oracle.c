@@ -16,6 +16,10 @@
  *   tlo_f16_to_f32          all 65536 bit patterns vs numpy float16 (IEEE binary16)
  *   tlo_dequantize_q4_0/q8_0 hand-built golden blocks (tests/golden/q_blocks.json) and
  *                           the closed form d*(q-8) / d*q (exact in f32)
+ *   tlo_dequantize_q4_k/q6_k golden super-blocks (tests/golden/k_blocks.json) built by
+ *                           packing chosen (scale, min, q) values with llama.cpp's
+ *                           published block encoders; expected values come from the chosen
+ *                           values, not from the decoder
  *   tlo_matmul              reference KAT [[58,64],[139,154]] (tl_cpu tests
  *                           cpu_tensor_tests.rs:488-497) + float64 brute force
  *   tlo_rms_norm            closed form of tl_cuda nn_llm_test.rs:123-132
@@ -107,6 +111,89 @@ int tlo_dequantize_q8_0(const uint8_t* data, int64_t nbytes, int64_t numel, floa
         p += 2;
         for (int j = 0; j < 32; j++) out[b * 32 + j] = d * (float)(int8_t)p[j];
         p += 32;
+    }
+    return TLO_OK;
+}
+
+/* QTensor::get_scale_min_k4 (crates/tl_runtime/src/quantized.rs:405-415): 6-bit scale and
+ * min of sub-block j (0..7) from the 12 packed bytes of a Q4_K block. */
+static void tlo_scale_min_k4(int j, const uint8_t* s, uint8_t* sc, uint8_t* m) {
+    if (j < 4) {
+        *sc = s[j] & 63;
+        *m = s[j + 4] & 63;
+    } else {
+        *sc = (uint8_t)((s[j + 4] & 0xF) | ((s[j - 4] >> 6) << 4));
+        *m = (uint8_t)((s[j + 4] >> 4) | ((s[j] >> 6) << 4));
+    }
+}
+
+/* QTensor::dequantize_q4_k (crates/tl_runtime/src/quantized.rs:337-400).  Block of 256
+ * weights, 144 bytes: f16 d, f16 dmin, 12 packed scale/min bytes, 128 quant bytes.  Group g
+ * (64 weights) uses quant bytes 32g..32g+31: low nibble of byte l -> weight 64g + l with
+ * sub-block 2g's (scale, min), high nibble -> weight 64g + 32 + l with sub-block 2g+1's.
+ * Value (d * sc) * q - dmin * m, each product rounded to f32 (all three are exact). */
+int tlo_dequantize_q4_k(const uint8_t* data, int64_t nbytes, int64_t numel, float* out) {
+    if (numel % 256 != 0) return TLO_ERR_SHAPE;      /* quantized.rs:342-344 */
+    int64_t nblocks = numel / 256;
+    if (nbytes != nblocks * 144) return TLO_ERR_SIZE; /* quantized.rs:347-352 */
+    for (int64_t b = 0; b < nblocks; b++) {
+        const uint8_t* p = data + b * 144;
+        float d = tlo_f16_to_f32((uint16_t)(p[0] | (p[1] << 8)));
+        float dmin = tlo_f16_to_f32((uint16_t)(p[2] | (p[3] << 8)));
+        const uint8_t* scales = p + 4;
+        const uint8_t* q = p + 16;
+        float* y = out + b * 256;
+        int is = 0;
+        for (int j = 0; j < 256; j += 64) {
+            uint8_t sc1, m1, sc2, m2;
+            tlo_scale_min_k4(is, scales, &sc1, &m1);
+            tlo_scale_min_k4(is + 1, scales, &sc2, &m2);
+            float d1 = d * (float)sc1, min1 = dmin * (float)m1;
+            float d2 = d * (float)sc2, min2 = dmin * (float)m2;
+            for (int l = 0; l < 32; l++) y[j + l] = d1 * (float)(q[l] & 0xF) - min1;
+            for (int l = 0; l < 32; l++) y[j + 32 + l] = d2 * (float)(q[l] >> 4) - min2;
+            q += 32;
+            is += 2;
+        }
+    }
+    return TLO_OK;
+}
+
+/* QTensor::dequantize_q6_k (crates/tl_runtime/src/quantized.rs:268-329).  Block of 256
+ * weights, 210 bytes: ql[128] (low 4 bits), qh[64] (high 2 bits), 16 int8 sub-block scales,
+ * f16 d at bytes 208-209.  Per 128-weight half (ql += 64, qh += 32, scales += 8), l < 32:
+ *   weight l      = ql[l] & 15      | (qh[l] >> 0 & 3) << 4, scale[l/16]
+ *   weight l + 32 = ql[l + 32] & 15 | (qh[l] >> 2 & 3) << 4, scale[l/16 + 2]
+ *   weight l + 64 = ql[l] >> 4      | (qh[l] >> 4 & 3) << 4, scale[l/16 + 4]
+ *   weight l + 96 = ql[l + 32] >> 4 | (qh[l] >> 6 & 3) << 4, scale[l/16 + 6]
+ * value (d * scale) * (q - 32), evaluated left to right as `d * sc as f32 * q as f32`. */
+int tlo_dequantize_q6_k(const uint8_t* data, int64_t nbytes, int64_t numel, float* out) {
+    if (numel % 256 != 0) return TLO_ERR_SHAPE;      /* quantized.rs:273-275 */
+    int64_t nblocks = numel / 256;
+    if (nbytes != nblocks * 210) return TLO_ERR_SIZE; /* quantized.rs:278-283 */
+    for (int64_t b = 0; b < nblocks; b++) {
+        const uint8_t* p = data + b * 210;
+        float d = tlo_f16_to_f32((uint16_t)(p[208] | (p[209] << 8)));
+        const uint8_t* ql = p;
+        const uint8_t* qh = p + 128;
+        const uint8_t* sc = p + 192;
+        for (int half = 0; half < 2; half++) {
+            float* y = out + b * 256 + half * 128;
+            for (int l = 0; l < 32; l++) {
+                int is = l / 16;
+                int q1 = (int)((ql[l] & 0xF) | (((qh[l] >> 0) & 3) << 4)) - 32;
+                int q2 = (int)((ql[l + 32] & 0xF) | (((qh[l] >> 2) & 3) << 4)) - 32;
+                int q3 = (int)((ql[l] >> 4) | (((qh[l] >> 4) & 3) << 4)) - 32;
+                int q4 = (int)((ql[l + 32] >> 4) | (((qh[l] >> 6) & 3) << 4)) - 32;
+                y[l + 0] = d * (float)(int8_t)sc[is + 0] * (float)q1;
+                y[l + 32] = d * (float)(int8_t)sc[is + 2] * (float)q2;
+                y[l + 64] = d * (float)(int8_t)sc[is + 4] * (float)q3;
+                y[l + 96] = d * (float)(int8_t)sc[is + 6] * (float)q4;
+            }
+            ql += 64;
+            qh += 32;
+            sc += 8;
+        }
     }
     return TLO_OK;
 }
@@ -204,7 +291,7 @@ void tlo_matmul_fast(const float* A, const float* B, float* C, int64_t m, int64_
 /* tl_qtensor_matmul, TL_DEVICE=cpu branch (crates/tl_runtime/src/system.rs:193-222):
  * dequantize W [n,k] (quantized.rs:117-141), transpose to [k,n] (tensor.rs:902-941), then
  * matmul_impl x[m,k] . W^T (tensor.rs:1248-1313).  ggml_type: 2 = Q4_0, 8 = Q8_0,
- * 1 = F16, 0 = F32 (GGML type ids).  `fast` selects tlo_matmul_fast (bit-identical). */
+ * 12 = Q4_K, 14 = Q6_K, 1 = F16, 0 = F32 (GGML type ids).  `fast` selects tlo_matmul_fast (bit-identical). */
 int tlo_qtensor_matmul(const float* x, int64_t m, int64_t k, const uint8_t* wdata,
                        int64_t wbytes, int ggml_type, int64_t n, float* y, int fast) {
     float* w = (float*)malloc(sizeof(float) * (size_t)(n * k));
@@ -213,6 +300,8 @@ int tlo_qtensor_matmul(const float* x, int64_t m, int64_t k, const uint8_t* wdat
     int rc;
     if (ggml_type == 2) rc = tlo_dequantize_q4_0(wdata, wbytes, n * k, w);
     else if (ggml_type == 8) rc = tlo_dequantize_q8_0(wdata, wbytes, n * k, w);
+    else if (ggml_type == 12) rc = tlo_dequantize_q4_k(wdata, wbytes, n * k, w);
+    else if (ggml_type == 14) rc = tlo_dequantize_q6_k(wdata, wbytes, n * k, w);
     else if (ggml_type == 1) rc = wbytes == n * k * 2 ? tlo_dequantize_f16(wdata, wbytes, w) : TLO_ERR_SIZE;
     else if (ggml_type == 0) { rc = wbytes == n * k * 4 ? TLO_OK : TLO_ERR_SIZE; if (!rc) memcpy(w, wdata, (size_t)wbytes); }
     else rc = TLO_ERR_ARG;

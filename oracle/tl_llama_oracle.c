@@ -22,6 +22,8 @@
 
 int tlo_dequantize_q4_0(const uint8_t* data, int64_t nbytes, int64_t numel, float* out);
 int tlo_dequantize_q8_0(const uint8_t* data, int64_t nbytes, int64_t numel, float* out);
+int tlo_dequantize_q4_k(const uint8_t* data, int64_t nbytes, int64_t numel, float* out);
+int tlo_dequantize_q6_k(const uint8_t* data, int64_t nbytes, int64_t numel, float* out);
 void tlo_transpose_2d(const float* a, int64_t rows, int64_t cols, float* out);
 void tlo_matmul_fast(const float* A, const float* B, float* C, int64_t m, int64_t k, int64_t n);
 void tlo_rms_norm(const float* x, int64_t rows, int64_t n, const float* w, float eps, float* out);
@@ -146,8 +148,11 @@ int tlo_llama_set_linear(tlo_llama* m, int layer, int which, const uint8_t* data
     tlo_linear* L = layer < 0 ? &m->lm_head : &m->lin[layer * 7 + which];
     float* w = (float*)malloc(sizeof(float) * (size_t)(n * k));
     if (!w) return -1;
-    int rc = ggml_type == 2 ? tlo_dequantize_q4_0(data, nbytes, n * k, w)
-                            : tlo_dequantize_q8_0(data, nbytes, n * k, w);
+    int rc = ggml_type == 2    ? tlo_dequantize_q4_0(data, nbytes, n * k, w)
+             : ggml_type == 8  ? tlo_dequantize_q8_0(data, nbytes, n * k, w)
+             : ggml_type == 12 ? tlo_dequantize_q4_k(data, nbytes, n * k, w)
+             : ggml_type == 14 ? tlo_dequantize_q6_k(data, nbytes, n * k, w)
+                               : -1;
     if (rc) { free(w); return rc; }
     lin_free(L);
     L->wt = (float*)malloc(sizeof(float) * (size_t)(n * k));

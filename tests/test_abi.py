@@ -52,9 +52,18 @@ def test_qtensor_validation_errors_before_device_use():
     assert not lib.tl_hip_qtensor_new(2, p, data.nbytes, bad, 2)
     st, msg = _err(lib)
     assert st == 1 and "multiple of 32" in msg
-    # types without a device residency
+    # types without a device residency (13 = Q5_K, 3 = Q4_1)
+    for t in (13, 3, 0, 1):
+        assert not lib.tl_hip_qtensor_new(t, p, data.nbytes, shape, 2)
+        assert _err(lib)[0] == 7
+    # K-quants: whole 256-weight blocks per row (quantized.rs:342-344) and 144 bytes each
     assert not lib.tl_hip_qtensor_new(12, p, data.nbytes, shape, 2)
-    assert _err(lib)[0] == 7
+    st, msg = _err(lib)
+    assert st == 1 and "multiple of 256 for Q4_K" in msg
+    sh256 = (C.c_int64 * 2)(1, 256)
+    assert not lib.tl_hip_qtensor_new(14, p, 209, sh256, 2)
+    st, msg = _err(lib)
+    assert st == 8 and "Data size mismatch for Q6_K: expected 210" in msg
     # a 2-D QTensor is required (system.rs:228)
     assert not lib.tl_hip_qtensor_new(2, p, data.nbytes, shape, 1)
     assert _err(lib)[0] == 1

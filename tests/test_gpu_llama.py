@@ -109,3 +109,34 @@ def test_tinyllama_greedy_golden():
     agree = int(np.argmax(np.array(list(got16) + [-1]) != np.array(gold["tokens"] + [-2])))
     print(f"f16 KV / f16 prefill: first {agree} of {len(gold['tokens'])} tokens agree")
     assert list(got16) == gold["tokens"]
+
+
+def _mixed_plan(cfg, layer, which):
+    # every grouping case of the loader: q | k | v in three runs, gate and up of different types
+    return {"attn_q": 14, "attn_k": 12, "attn_v": 14, "ffn_gate": 14, "ffn_up": 12}.get(which, 12)
+
+
+@pytest.mark.parametrize("plan", ["Q4_K_M", "mixed"])
+def test_kquant_model_logits_and_tokens(plan):
+    """K-quant weights through the whole decoder: llama.cpp's Q4_K_M mixture (Q4_K with Q6_K
+    attn_v / ffn_down in some layers and the LM head) and a plan with q/k/v and gate/up of
+    different types.  f32 logits within 1e-4 and identical greedy tokens, graph and eager."""
+    cfg = LlamaConfig(4, 256, 4, 2, 512, 1000, max_seq=128)
+    gt = "Q4_K_M" if plan == "Q4_K_M" else _mixed_plan
+    tensors = list(synthetic_weights(cfg, 31, ggml_type=gt))
+    gpu = HipLlama(cfg)
+    gpu.load(tensors, ggml_type=gt)
+    cpu = oracle.Llama(cfg)
+    cpu.load(tensors, ggml_type=gt)
+    try:
+        prompt = synthetic_prompt(cfg, 31, 19)
+        cpu.reset()
+        for chunk in (prompt, [7], [998]):
+            err = max_rel(gpu.forward(chunk), cpu.forward(chunk))
+            assert err <= 1e-4, f"logits max-rel-err {err:.2e} after {len(chunk)} tokens"
+        for use_graph in (True, False):
+            got = greedy_generate(gpu, prompt, 16, use_graph=use_graph)
+            assert list(got) == list(cpu.greedy(prompt, 16))
+    finally:
+        gpu.close()
+        cpu.close()

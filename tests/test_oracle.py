@@ -47,6 +47,32 @@ def test_dequant_errors():
         oracle.dequantize(8, bytes(33), 32)
 
 
+def _k_golden():
+    with open(os.path.join(HERE, "golden", "k_blocks.json")) as f:
+        return json.load(f)["cases"]
+
+
+@pytest.mark.parametrize("case", _k_golden(), ids=lambda c: f"{c['type']}:{c['name']}")
+def test_dequant_k_golden_blocks(case):
+    # blocks packed from chosen values by llama.cpp's encoders; expected values from those
+    # values, so a wrong nibble, high-bit or scale index in the decoder fails here
+    t = 12 if case["type"] == "Q4_K" else 14
+    got = oracle.dequantize(t, bytes.fromhex(case["hex"]), 256)
+    assert list(got.view(np.uint32)) == case["f32_bits"]
+
+
+def test_dequant_k_errors():
+    # quantized.rs:273-283 (Q6_K), 342-352 (Q4_K): numel % 256 and byte-count checks
+    with pytest.raises(oracle.OracleError):
+        oracle.dequantize(12, bytes(144), 255)
+    with pytest.raises(oracle.OracleError):
+        oracle.dequantize(12, bytes(143), 256)
+    with pytest.raises(oracle.OracleError):
+        oracle.dequantize(14, bytes(210), 128)
+    with pytest.raises(oracle.OracleError):
+        oracle.dequantize(14, bytes(211), 256)
+
+
 def test_q4_layout_low_then_high_nibble():
     # a block whose byte 0 = 0x1F: element 0 = d*(0xF-8) = 7, element 16 = d*(1-8) = -7
     blk = bytes([0x00, 0x3C, 0x1F] + [0x88] * 15)

@@ -1,7 +1,7 @@
 // Dense contractions: the quantized prefill GEMM (Y = X . W^T, W Q4_0 / Q8_0 resident) in
 // two precisions, and the plain f32 batched matmul behind tensor_matmul / matmul_4d.
 //
-//  * k_qgemm_f32   exact dequant (d * (q - 8) in f32) into LDS, f32 FMA accumulate.
+//  * k_qgemm_f32   exact dequant (all four types) into LDS, f32 FMA accumulate.
 //                  The "f32 path": max-rel-err 1e-4 class against tl_cpu.
 //  * k_qgemm_mfma  dequant -> f16 LDS tiles -> v_mfma_f32_16x16x32_f16, f32 accumulate.
 //                  The "f16 path": 1e-2 class.  X is rounded to f16 while it is staged.
@@ -14,14 +14,22 @@ namespace tlhip {
 typedef _Float16 half8 __attribute__((ext_vector_type(8)));
 typedef float floatx4 __attribute__((ext_vector_type(4)));
 
-// Dequantise the 32 weights of one block into v[32] (f32, exact).
+// Residency buffers of a quantized weight (layout at struct QWeight).
+struct QView {
+    const uint8_t* qs;
+    const __half* d;
+    const uint8_t* hdr;
+    const uint8_t* qh;
+    const int8_t* sc;
+};
+
+// Dequantise the 32 weights of unit blk into v[32] (f32, bit-identical to the reference's
+// dequantizers: Q4_0 d * (q - 8), Q8_0 d * q, Q4_K (d sc) q - dmin m, Q6_K (d sc) (q - 32)).
 template <int QT>
-__device__ __forceinline__ void dequant_block(const uint8_t* __restrict__ qs,
-                                              const __half* __restrict__ dsc, int64_t blk,
-                                              float* v) {
-    float d = __half2float(dsc[blk]);
+__device__ __forceinline__ void dequant_block(const QView& qv, int64_t blk, float* v) {
     if constexpr (QT == TL_HIP_GGML_Q4_0) {
-        uint4 w = *reinterpret_cast<const uint4*>(qs + blk * 16);
+        const float d = __half2float(qv.d[blk]);
+        uint4 w = *reinterpret_cast<const uint4*>(qv.qs + blk * 16);
         const uint32_t q[4] = {w.x, w.y, w.z, w.w};
 #pragma unroll
         for (int c = 0; c < 4; c++)
@@ -31,14 +39,54 @@ __device__ __forceinline__ void dequant_block(const uint8_t* __restrict__ qs,
                 v[4 * c + i] = d * (float)((int)(byte & 0xF) - 8);
                 v[16 + 4 * c + i] = d * (float)((int)(byte >> 4) - 8);
             }
-    } else {
-        const uint4* p = reinterpret_cast<const uint4*>(qs + blk * 32);
+    } else if constexpr (QT == TL_HIP_GGML_Q8_0) {
+        const float d = __half2float(qv.d[blk]);
+        const uint4* p = reinterpret_cast<const uint4*>(qv.qs + blk * 32);
         uint4 w0 = p[0], w1 = p[1];
         const uint32_t q[8] = {w0.x, w0.y, w0.z, w0.w, w1.x, w1.y, w1.z, w1.w};
 #pragma unroll
         for (int c = 0; c < 8; c++)
 #pragma unroll
             for (int i = 0; i < 4; i++) v[4 * c + i] = d * (float)(int8_t)((q[c] >> (8 * i)) & 0xFF);
+    } else if constexpr (QT == TL_HIP_GGML_Q4_K) {
+        const uint4 hd = reinterpret_cast<const uint4*>(qv.hdr)[blk >> 3];
+        const int j = (int)(blk & 7), sh = 8 * (j & 3);
+        uint32_t sc, mn;
+        if (j < 4) {
+            sc = (hd.y >> sh) & 63;
+            mn = (hd.z >> sh) & 63;
+        } else {
+            const uint32_t lo = hd.w >> sh;
+            sc = (lo & 0xF) | (((hd.y >> sh) >> 2) & 0x30);
+            mn = ((lo >> 4) & 0xF) | (((hd.z >> sh) >> 2) & 0x30);
+        }
+        const float d1 = __half2float(__ushort_as_half((uint16_t)(hd.x & 0xFFFF))) * (float)sc;
+        const float m1 = __half2float(__ushort_as_half((uint16_t)(hd.x >> 16))) * (float)mn;
+        uint4 w = *reinterpret_cast<const uint4*>(qv.qs + blk * 16);
+        const uint32_t q[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+        for (int c = 0; c < 4; c++)
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                uint32_t byte = (q[c] >> (8 * i)) & 0xFF;
+                v[4 * c + i] = d1 * (float)(byte & 0xF) - m1;
+                v[16 + 4 * c + i] = d1 * (float)(byte >> 4) - m1;
+            }
+    } else {
+        const float d = __half2float(qv.d[blk >> 3]);
+        const float e0 = d * (float)qv.sc[2 * blk], e1 = d * (float)qv.sc[2 * blk + 1];
+        uint4 w = *reinterpret_cast<const uint4*>(qv.qs + blk * 16);
+        const uint2 h = reinterpret_cast<const uint2*>(qv.qh)[blk];
+        const uint32_t q[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+        for (int c = 0; c < 4; c++)
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                uint32_t byte = (q[c] >> (8 * i)) & 0xFF;
+                const uint32_t h0 = (h.x >> (8 * i + 2 * c)) & 3, h1 = (h.y >> (8 * i + 2 * c)) & 3;
+                v[4 * c + i] = e0 * (float)((int)((byte & 0xF) | (h0 << 4)) - 32);
+                v[16 + 4 * c + i] = e1 * (float)((int)((byte >> 4) | (h1 << 4)) - 32);
+            }
     }
 }
 
@@ -48,9 +96,7 @@ __device__ __forceinline__ void dequant_block(const uint8_t* __restrict__ qs,
 constexpr int F_BM = 64, F_BN = 64, F_BK = 32;
 
 template <int QT>
-__global__ __launch_bounds__(256) void k_qgemm_f32(const uint8_t* __restrict__ qs,
-                                                   const __half* __restrict__ dsc,
-                                                   const float* __restrict__ x,
+__global__ __launch_bounds__(256) void k_qgemm_f32(QView qv, const float* __restrict__ x,
                                                    float* __restrict__ y, int64_t m, int64_t n,
                                                    int64_t k, int64_t nb) {
     __shared__ __attribute__((aligned(16))) float Xs[F_BK][F_BM + 4];
@@ -76,7 +122,7 @@ __global__ __launch_bounds__(256) void k_qgemm_f32(const uint8_t* __restrict__ q
         if (t < 64) {
             float v[32];
             int64_t row = n0 + t < n ? n0 + t : n - 1;
-            dequant_block<QT>(qs, dsc, row * nb + kb, v);
+            dequant_block<QT>(qv, row * nb + kb, v);
 #pragma unroll
             for (int j = 0; j < 32; j++) Ws[j][t] = v[j];
         }
@@ -383,12 +429,16 @@ int launch_quant_gemm(const QWeight* w, const float* x, float* y, int64_t m, hip
     }
     const bool q4 = w->ggml_type == TL_HIP_GGML_Q4_0;
     if (mode != 0 && w->nb % Q_KR != 0) mode = 0;  // the MFMA pipeline takes K in steps of 128
+    if (w->ggml_type == TL_HIP_GGML_Q4_K || w->ggml_type == TL_HIP_GGML_Q6_K) mode = 0;
     if (mode == 0) {
         dim3 grid((unsigned)cdiv(w->n, F_BN), (unsigned)cdiv(m, F_BM));
-        if (q4)
-            k_qgemm_f32<TL_HIP_GGML_Q4_0><<<grid, 256, 0, s>>>(w->qs, w->d, x, y, m, w->n, w->k, w->nb);
-        else
-            k_qgemm_f32<TL_HIP_GGML_Q8_0><<<grid, 256, 0, s>>>(w->qs, w->d, x, y, m, w->n, w->k, w->nb);
+        const QView qv{w->qs, w->d, w->hdr, w->qh, w->sc};
+        switch (w->ggml_type) {
+            case TL_HIP_GGML_Q4_0: k_qgemm_f32<TL_HIP_GGML_Q4_0><<<grid, 256, 0, s>>>(qv, x, y, m, w->n, w->k, w->nb); break;
+            case TL_HIP_GGML_Q8_0: k_qgemm_f32<TL_HIP_GGML_Q8_0><<<grid, 256, 0, s>>>(qv, x, y, m, w->n, w->k, w->nb); break;
+            case TL_HIP_GGML_Q4_K: k_qgemm_f32<TL_HIP_GGML_Q4_K><<<grid, 256, 0, s>>>(qv, x, y, m, w->n, w->k, w->nb); break;
+            default: k_qgemm_f32<TL_HIP_GGML_Q6_K><<<grid, 256, 0, s>>>(qv, x, y, m, w->n, w->k, w->nb); break;
+        }
     } else {
         // X -> f16 in the operand k order (a workspace of m * k halves), then the MFMA GEMM
         _Float16* x16 = static_cast<_Float16*>(dev_alloc((size_t)m * w->k * sizeof(_Float16)));

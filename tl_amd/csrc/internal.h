@@ -56,16 +56,29 @@ inline tl_hip_tensor* H(Tensor* t) { return reinterpret_cast<tl_hip_tensor*>(t);
 void tensor_drop(Tensor* t);
 size_t dtype_size(int dtype);
 
-// ---- quantized weights (device residency of a GGUF Q4_0 / Q8_0 tensor) ------------
-// Struct-of-arrays repack of the 18-byte (Q4_0) / 34-byte (Q8_0) GGUF blocks:
-//   qs: [n][nb][16 | 32] bytes, 16-byte aligned (one dwordx4 / two per block)
-//   d : [n][nb] f16 scales
-// Same byte count as the GGUF stream; rows of one block column are contiguous.
+// ---- quantized weights (device residency of a GGUF tensor) -------------------------
+// Struct-of-arrays repack of the GGUF blocks, organised in 32-weight units (nb units per
+// row) so that every type offers one 16-byte quant load per unit:
+//   Q4_0  qs [n][nb][16]  GGUF nibble order (byte j: weight j | weight j + 16 << 4)
+//         d  [n][nb]      f16 scale
+//   Q8_0  qs [n][nb][32]  int8, d [n][nb] f16
+//   Q4_K  qs [n][nb][16]  the unit's 32 nibbles in Q4_0 order (unit = one sub-block)
+//         hdr[n][nb/8][16] the super-block header as stored: f16 d, f16 dmin, 12 packed
+//                          6-bit (scale, min) pairs
+//   Q6_K  qs [n][nb][16]  low 4 bits in Q4_0 order
+//         qh [n][nb][8]   high 2 bits: word 0 byte b bits 2t..2t+1 = weight b + 4t,
+//                         word 1 the same for weights 16 + b + 4t
+//         sc [n][nb][2]   the int8 scales of the unit's two 16-weight sub-blocks
+//         d  [n][nb/8]    f16 super-block scale
+// Byte counts equal the GGUF stream's (18 / 34 / 144 / 210 bytes per 32 / 32 / 256 / 256).
 struct QWeight {
     int ggml_type = 0;
-    int64_t n = 0, k = 0, nb = 0;  // rows, cols, blocks per row
+    int64_t n = 0, k = 0, nb = 0;  // rows, cols, 32-weight units per row
     uint8_t* qs = nullptr;
     __half* d = nullptr;
+    uint8_t* hdr = nullptr;  // Q4_K
+    uint8_t* qh = nullptr;   // Q6_K
+    int8_t* sc = nullptr;    // Q6_K
     int64_t shape[TL_HIP_MAX_RANK] = {0};
     int rank = 0;
     std::atomic<int> refs{1};
@@ -78,6 +91,9 @@ enum { EPI_PLAIN = 0, EPI_RES = 1, EPI_GLU = 2, EPI_ROPE_KV = 3, EPI_ARGMAX = 4 
 struct MvArgs {
     const uint8_t* qs;
     const __half* d;
+    const uint8_t* hdr;
+    const uint8_t* qh;
+    const int8_t* sc;
     int64_t n, k, nb;
     const float* x;           // [m, k]; with EMBED the embedding table [vocab, k]
     const int32_t* embed_id;  // EMBED: token id (device)
@@ -95,6 +111,7 @@ struct MvArgs {
     void* vc;
     int q_rows, kv_rows, hd, kv_f16;
     int64_t max_seq;
+    int64_t row_off;  // rows of this weight start at row_off of the q | k | v projection
     // EPI_ARGMAX
     float* plogits;       // penalised logits
     const uint8_t* seen;  // repetition-penalty mask (nullptr = no penalty)
@@ -162,5 +179,18 @@ void attn_plan(int B, int hkv, int64_t L, int* chunk, int* nsplit);
 size_t attn_workspace_floats(int B, int hkv, int G, int D, int nsplit);
 
 inline int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
+
+// GGUF block geometry of the quantized types: weights and bytes per block (0 = unsupported).
+inline int ggml_block_elems(int t) {
+    return t == TL_HIP_GGML_Q4_0 || t == TL_HIP_GGML_Q8_0 ? 32 : t == TL_HIP_GGML_Q4_K || t == TL_HIP_GGML_Q6_K ? 256 : 0;
+}
+inline int ggml_block_bytes(int t) {
+    return t == TL_HIP_GGML_Q4_0 ? 18 : t == TL_HIP_GGML_Q8_0 ? 34 : t == TL_HIP_GGML_Q4_K ? 144 : t == TL_HIP_GGML_Q6_K ? 210 : 0;
+}
+inline const char* ggml_type_name(int t) {
+    return t == TL_HIP_GGML_Q4_0 ? "Q4_0" : t == TL_HIP_GGML_Q8_0 ? "Q8_0" : t == TL_HIP_GGML_Q4_K ? "Q4_K" : t == TL_HIP_GGML_Q6_K ? "Q6_K" : "?";
+}
+// bytes of one row of k weights in the GGUF stream
+inline size_t ggml_row_bytes(int t, int64_t k) { return (size_t)(k / ggml_block_elems(t)) * ggml_block_bytes(t); }
 
 }  // namespace tlhip

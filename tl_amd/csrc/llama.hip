@@ -4,7 +4,10 @@
 //
 // Differences in form (not in arithmetic) from the chatbot's op-by-op execution:
 //  * q/k/v and gate/up weights are concatenated row-wise at load, so each projection pair /
-//    triple is one matvec (every output row is the same dot product);
+//    triple is one matvec (every output row is the same dot product).  Parts stored in
+//    different GGUF types (llama.cpp's Q4_K_M files keep some attn_v / ffn_down tensors in
+//    Q6_K) form one segment per run of equal type: the q|k|v segments share the RoPE + KV
+//    epilogue through their row offset, separate gate / up run as two matvecs + SwiGLU;
 //  * the residual adds x + o-proj(x) and x + down(x) are fused into the matvec epilogue;
 //  * RoPE, the KV-cache append and the q transpose are one kernel writing into a persistent
 //    per-layer cache [Hkv, max_seq, head_dim] (instead of cat_4d + KVCache.update,
@@ -15,6 +18,7 @@
 //    dependency and is captured once as a hipGraph and replayed.
 #include "internal.h"
 
+#include <algorithm>
 #include <cstring>
 #include <vector>
 
@@ -94,11 +98,19 @@ __global__ void k_advance(int32_t* pos, int n) {
     if (threadIdx.x == 0 && blockIdx.x == 0) *pos += n;
 }
 
+// A run of q|k|v rows stored in one type: rows [row_off, row_off + w->n) of the projection.
+struct Seg {
+    QWeight* w;
+    int64_t row_off;
+};
+
 struct Llama {
     int nl, D, H, KV, hd, F, V, max_seq;
     float eps, theta;
     int kv_f16 = 0, rope_per_token = 0;
-    std::vector<QWeight*> wqkv, wo, wgu, wdown;
+    std::vector<std::vector<Seg>> qkv_segs;
+    std::vector<QWeight*> wo, wgu, wdown;
+    std::vector<QWeight*> wg, wu;  // gate / up when their types differ (wgu is then null)
     QWeight* lm = nullptr;
     // host staging of q/k/v and gate/up until all parts of a layer are present
     std::vector<std::vector<uint8_t>> stage;  // [nl * 5]: q k v gate up
@@ -166,7 +178,7 @@ static int ensure_tokens(Llama* m, int64_t n) {
     m->q = (float*)dev_alloc(n * m->D * 4);
     m->ao = (float*)dev_alloc(n * m->D * 4);
     m->t = (float*)dev_alloc(n * m->D * 4);
-    m->gu = (float*)dev_alloc(n * 2 * (int64_t)m->F * 4);
+    m->gu = (float*)dev_alloc(n * std::max(2 * (int64_t)m->F, qkv_w) * 4);  // also the q|k|v segment staging
     m->act = (float*)dev_alloc(n * (int64_t)m->F * 4);
     m->ids = (int32_t*)dev_alloc(n * 4);
     // attention workspace: B = n queries, 64-position chunks over max_seq
@@ -181,43 +193,73 @@ static int ensure_tokens(Llama* m, int64_t n) {
     return TL_HIP_OK;
 }
 
+static void release_w(QWeight* w) {
+    if (w) tl_hip_qtensor_release(reinterpret_cast<tl_hip_qtensor*>(w));
+}
+
 static int try_merge(Llama* m, int layer) {
     auto& S = m->stage;
     const int base = layer * 5;
     if (!S[base].empty() && !S[base + 1].empty() && !S[base + 2].empty()) {
-        int ty = m->stage_type[base];
-        if (m->stage_type[base + 1] != ty || m->stage_type[base + 2] != ty) {
-            set_error(TL_HIP_ERR_TYPE, "TypeMismatch: q/k/v of layer %d differ in ggml type", layer);
-            return TL_HIP_ERR_TYPE;
+        // q | k | v in runs of equal type, each run one row-concatenated weight
+        const int64_t rows[3] = {m->D, (int64_t)m->KV * m->hd, (int64_t)m->KV * m->hd};
+        std::vector<Seg> segs;
+        int64_t off = 0;
+        for (int i = 0; i < 3;) {
+            const int ty = m->stage_type[base + i];
+            int j = i;
+            std::vector<uint8_t> cat;
+            int64_t nrows = 0;
+            while (j < 3 && m->stage_type[base + j] == ty) {
+                cat.insert(cat.end(), S[base + j].begin(), S[base + j].end());
+                nrows += rows[j];
+                j++;
+            }
+            int64_t shape[2] = {nrows, m->D};
+            tl_hip_qtensor* q = tl_hip_qtensor_new(ty, cat.data(), cat.size(), shape, 2);
+            if (!q) {
+                for (auto& sg : segs) release_w(sg.w);
+                return tl_hip_last_status();
+            }
+            segs.push_back(Seg{Q(q), off});
+            off += nrows;
+            i = j;
         }
-        std::vector<uint8_t> cat;
-        for (int i = 0; i < 3; i++) cat.insert(cat.end(), S[base + i].begin(), S[base + i].end());
-        int64_t shape[2] = {m->D + 2 * (int64_t)m->KV * m->hd, m->D};
-        tl_hip_qtensor* q = tl_hip_qtensor_new(ty, cat.data(), cat.size(), shape, 2);
-        if (!q) return tl_hip_last_status();
-        if (m->wqkv[layer]) tl_hip_qtensor_release(reinterpret_cast<tl_hip_qtensor*>(m->wqkv[layer]));
-        m->wqkv[layer] = Q(q);
+        for (auto& sg : m->qkv_segs[layer]) release_w(sg.w);
+        m->qkv_segs[layer] = segs;
         for (int i = 0; i < 3; i++) std::vector<uint8_t>().swap(S[base + i]);
     }
     if (!S[base + 3].empty() && !S[base + 4].empty()) {
-        int ty = m->stage_type[base + 3];
-        if (m->stage_type[base + 4] != ty) {
-            set_error(TL_HIP_ERR_TYPE, "TypeMismatch: gate/up of layer %d differ in ggml type", layer);
-            return TL_HIP_ERR_TYPE;
+        const int ty = m->stage_type[base + 3], tu = m->stage_type[base + 4];
+        release_w(m->wgu[layer]);
+        release_w(m->wg[layer]);
+        release_w(m->wu[layer]);
+        m->wgu[layer] = m->wg[layer] = m->wu[layer] = nullptr;
+        if (ty == tu) {
+            // rows interleaved (gate_0, up_0, gate_1, up_1, ...): the SwiGLU epilogue of the
+            // matvec then sees both halves of an output in one workgroup
+            const size_t row_bytes = ggml_row_bytes(ty, m->D);
+            std::vector<uint8_t> cat(S[base + 3].size() * 2);
+            for (int64_t i = 0; i < m->F; i++) {
+                std::memcpy(cat.data() + (2 * i) * row_bytes, S[base + 3].data() + i * row_bytes, row_bytes);
+                std::memcpy(cat.data() + (2 * i + 1) * row_bytes, S[base + 4].data() + i * row_bytes, row_bytes);
+            }
+            int64_t shape[2] = {2 * (int64_t)m->F, m->D};
+            tl_hip_qtensor* q = tl_hip_qtensor_new(ty, cat.data(), cat.size(), shape, 2);
+            if (!q) return tl_hip_last_status();
+            m->wgu[layer] = Q(q);
+        } else {
+            int64_t shape[2] = {(int64_t)m->F, m->D};
+            tl_hip_qtensor* g = tl_hip_qtensor_new(ty, S[base + 3].data(), S[base + 3].size(), shape, 2);
+            if (!g) return tl_hip_last_status();
+            tl_hip_qtensor* u = tl_hip_qtensor_new(tu, S[base + 4].data(), S[base + 4].size(), shape, 2);
+            if (!u) {
+                tl_hip_qtensor_release(g);
+                return tl_hip_last_status();
+            }
+            m->wg[layer] = Q(g);
+            m->wu[layer] = Q(u);
         }
-        // rows interleaved (gate_0, up_0, gate_1, up_1, ...): the SwiGLU epilogue of the
-        // matvec then sees both halves of an output in one workgroup
-        const size_t row_bytes = (size_t)(m->D / 32) * (ty == TL_HIP_GGML_Q4_0 ? 18 : 34);
-        std::vector<uint8_t> cat(S[base + 3].size() * 2);
-        for (int64_t i = 0; i < m->F; i++) {
-            std::memcpy(cat.data() + (2 * i) * row_bytes, S[base + 3].data() + i * row_bytes, row_bytes);
-            std::memcpy(cat.data() + (2 * i + 1) * row_bytes, S[base + 4].data() + i * row_bytes, row_bytes);
-        }
-        int64_t shape[2] = {2 * (int64_t)m->F, m->D};
-        tl_hip_qtensor* q = tl_hip_qtensor_new(ty, cat.data(), cat.size(), shape, 2);
-        if (!q) return tl_hip_last_status();
-        if (m->wgu[layer]) tl_hip_qtensor_release(reinterpret_cast<tl_hip_qtensor*>(m->wgu[layer]));
-        m->wgu[layer] = Q(q);
         for (int i = 3; i < 5; i++) std::vector<uint8_t>().swap(S[base + i]);
     }
     return TL_HIP_OK;
@@ -236,7 +278,8 @@ static int linear(const QWeight* w, const float* x, float* y, int64_t n, const f
 
 static int check_ready(Llama* m) {
     for (int l = 0; l < m->nl; l++)
-        if (!m->wqkv[l] || !m->wo[l] || !m->wgu[l] || !m->wdown[l] || !m->attn_norm[l] || !m->ffn_norm[l]) {
+        if (m->qkv_segs[l].empty() || !m->wo[l] || !(m->wgu[l] || (m->wg[l] && m->wu[l])) || !m->wdown[l] ||
+            !m->attn_norm[l] || !m->ffn_norm[l]) {
             set_error(TL_HIP_ERR_ARG, "ArgumentError: layer %d is missing weights", l);
             return TL_HIP_ERR_ARG;
         }
@@ -259,7 +302,15 @@ static int enqueue_forward(Llama* m, int n, int f16, hipStream_t s) {
     const int nsplit = (int)cdiv(m->host_pos + n, 64);
     for (int l = 0; l < m->nl; l++) {
         if ((rc = launch_rmsnorm(m->x, nullptr, m->attn_norm[l], m->h, n, D, m->eps, 0, s))) return rc;
-        if ((rc = linear(m->wqkv[l], m->h, m->qkv, n, nullptr, nullptr, f16, s))) return rc;
+        if (m->qkv_segs[l].size() == 1) {
+            if ((rc = linear(m->qkv_segs[l][0].w, m->h, m->qkv, n, nullptr, nullptr, f16, s))) return rc;
+        } else {
+            for (const Seg& sg : m->qkv_segs[l]) {  // each segment's columns of the [n, qkv_w] rows
+                if ((rc = linear(sg.w, m->h, m->gu, n, nullptr, nullptr, f16, s))) return rc;
+                TLH_CHECK_HIP(hipMemcpy2DAsync(m->qkv + sg.row_off, qkv_w * 4, m->gu, sg.w->n * 4, sg.w->n * 4, n,
+                                               hipMemcpyDeviceToDevice, s));
+            }
+        }
         int64_t work = (int64_t)n * ((m->H + m->KV) * hd / 2 + m->KV * hd);
         if (m->kv_f16)
             k_rope_kv<__half><<<cdiv(work, 256), 256, 0, s>>>(m->qkv, m->q, (__half*)m->kc[l], (__half*)m->vc[l],
@@ -281,11 +332,17 @@ static int enqueue_forward(Llama* m, int n, int f16, hipStream_t s) {
         (void)G;
         if ((rc = linear(m->wo[l], m->ao, m->x, n, m->x, m->t, f16, s))) return rc;
         if ((rc = launch_rmsnorm(m->x, nullptr, m->ffn_norm[l], m->h, n, D, m->eps, 0, s))) return rc;
-        if ((rc = linear(m->wgu[l], m->h, m->gu, n, nullptr, nullptr, f16, s))) return rc;
-        k_swiglu_rows<<<cdiv(n * (int64_t)m->F, 256), 256, 0, s>>>(m->gu, m->act, n, m->F);
+        if (m->wgu[l]) {
+            if ((rc = linear(m->wgu[l], m->h, m->gu, n, nullptr, nullptr, f16, s))) return rc;
+            k_swiglu_rows<<<cdiv(n * (int64_t)m->F, 256), 256, 0, s>>>(m->gu, m->act, n, m->F);
+        } else {
+            float* up = m->gu + (int64_t)n * m->F;
+            if ((rc = linear(m->wg[l], m->h, m->gu, n, nullptr, nullptr, f16, s))) return rc;
+            if ((rc = linear(m->wu[l], m->h, up, n, nullptr, nullptr, f16, s))) return rc;
+            if ((rc = launch_swiglu(m->gu, up, m->act, (int64_t)n * m->F, 0, s))) return rc;
+        }
         if ((rc = linear(m->wdown[l], m->act, m->x, n, m->x, m->t, f16, s))) return rc;
     }
-    (void)qkv_w;
     k_advance<<<1, 64, 0, s>>>(m->pos, n);
     if ((rc = launch_rmsnorm(m->x + (int64_t)(n - 1) * D, nullptr, m->out_norm, m->h, 1, D, m->eps, 0, s))) return rc;
     if ((rc = launch_quant_matvec(m->lm, m->h, m->logits, 1, s, nullptr))) return rc;
@@ -326,7 +383,10 @@ static int enqueue_step(Llama* m, float penalty, hipStream_t s) {
         a.hd = (int)hd;
         a.kv_f16 = m->kv_f16;
         a.max_seq = m->max_seq;
-        if ((rc = launch_mv(m->wqkv[l], a, 1, EPI_ROPE_KV, true, l == 0, s))) return rc;
+        for (const Seg& sg : m->qkv_segs[l]) {
+            a.row_off = sg.row_off;
+            if ((rc = launch_mv(sg.w, a, 1, EPI_ROPE_KV, true, l == 0, s))) return rc;
+        }
         if (m->max_seq <= 4096 && attention_qh_supported(m->kv_f16 ? TL_HIP_F16 : TL_HIP_F32, (int)hd))
             rc = launch_attention_qh(m->q, m->kc[l], m->vc[l], m->kv_f16 ? TL_HIP_F16 : TL_HIP_F32, m->ao, 1, m->H,
                                      m->KV, (int)hd, m->max_seq, 0, 0, m->pos, 1, 0, 1.0f / sqrtf((float)hd), s);
@@ -347,8 +407,16 @@ static int enqueue_step(Llama* m, float penalty, hipStream_t s) {
         g.x = m->x;
         g.norm_w = m->ffn_norm[l];
         g.eps = m->eps;
-        g.y = m->act;
-        if ((rc = launch_mv(m->wgu[l], g, 1, EPI_GLU, true, false, s))) return rc;
+        if (m->wgu[l]) {
+            g.y = m->act;
+            if ((rc = launch_mv(m->wgu[l], g, 1, EPI_GLU, true, false, s))) return rc;
+        } else {
+            g.y = m->gu;
+            if ((rc = launch_mv(m->wg[l], g, 1, EPI_PLAIN, true, false, s))) return rc;
+            g.y = m->gu + m->F;
+            if ((rc = launch_mv(m->wu[l], g, 1, EPI_PLAIN, true, false, s))) return rc;
+            if ((rc = launch_swiglu(m->gu, m->gu + m->F, m->act, m->F, 0, s))) return rc;
+        }
         MvArgs d = {};
         d.x = m->act;
         d.y = m->x;
@@ -401,9 +469,11 @@ tl_hip_llama* tl_hip_llama_new(int n_layers, int d_model, int n_heads, int n_kv_
     m->max_seq = max_seq;
     m->eps = eps;
     m->theta = rope_theta;
-    m->wqkv.assign(n_layers, nullptr);
+    m->qkv_segs.assign(n_layers, {});
     m->wo.assign(n_layers, nullptr);
     m->wgu.assign(n_layers, nullptr);
+    m->wg.assign(n_layers, nullptr);
+    m->wu.assign(n_layers, nullptr);
     m->wdown.assign(n_layers, nullptr);
     m->stage.assign((size_t)n_layers * 5, {});
     m->stage_type.assign((size_t)n_layers * 5, -1);
@@ -450,9 +520,11 @@ int tl_hip_llama_free(tl_hip_llama* h) {
         if (w) tl_hip_qtensor_release(reinterpret_cast<tl_hip_qtensor*>(w));
     };
     for (int l = 0; l < m->nl; l++) {
-        rel(m->wqkv[l]);
+        for (auto& sg : m->qkv_segs[l]) rel(sg.w);
         rel(m->wo[l]);
         rel(m->wgu[l]);
+        rel(m->wg[l]);
+        rel(m->wu[l]);
         rel(m->wdown[l]);
         dev_free(m->attn_norm[l]);
         dev_free(m->ffn_norm[l]);
@@ -497,11 +569,17 @@ int tl_hip_llama_set_linear(tl_hip_llama* h, int layer, int which, int ggml_type
     int part = which <= 2 ? which : which - 1;  // 0 q, 1 k, 2 v, 3 gate, 4 up
     int64_t rows = which == 0 ? D : (which <= 2 ? KVd : F);
     int64_t numel = rows * D;
-    size_t want = (size_t)(numel / 32) * (ggml_type == TL_HIP_GGML_Q4_0 ? 18 : 34);
-    if (ggml_type != TL_HIP_GGML_Q4_0 && ggml_type != TL_HIP_GGML_Q8_0) {
+    if (!ggml_block_elems(ggml_type)) {
         set_error(TL_HIP_ERR_TYPE, "TypeMismatch: ggml type %d has no device residency", ggml_type);
         return TL_HIP_ERR_TYPE;
     }
+    if (D % ggml_block_elems(ggml_type)) {
+        set_error(TL_HIP_ERR_SHAPE, "ShapeMismatch: rows of %lld do not hold whole %s blocks", (long long)D,
+                  ggml_type_name(ggml_type));
+        return TL_HIP_ERR_SHAPE;
+    }
+    const size_t want = (size_t)rows * ggml_row_bytes(ggml_type, D);
+    (void)numel;
     if (nbytes != want) {
         set_error(TL_HIP_ERR_ARG, "ArgumentError: Data size mismatch: expected %zu, got %zu", want, nbytes);
         return TL_HIP_ERR_ARG;

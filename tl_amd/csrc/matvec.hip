@@ -1,5 +1,6 @@
 // Fused dequant x matvec for decode: y[m, n] = sum_k x[m, k] * W[n, k] with W resident as
-// Q4_0 / Q8_0 (qs[n][nb][16|32], d[n][nb] f16), m in {1, 2} per launch.
+// Q4_0 / Q8_0 / Q4_K / Q6_K in 32-weight units (qs[n][nb][16|32] plus per-type scale data,
+// layout at struct QWeight), m in {1, 2} per launch.
 //
 // Decode matvecs are small (2 - 40 MB of weights, a few microseconds each), so the kernel is
 // built for memory-level parallelism: every thread issues all of its loads before it does
@@ -18,8 +19,12 @@
 //   * residual, RoPE table entries and penalty flags for the epilogue are requested right
 //     after the weight loads, so no memory round trip is left after the reduction.
 //
-// Per block the thread forms d * (sum_j x_j q_j - 8 sum_j x_j) (Q4_0; Q8_0 uses q ^ 0x80 and
-// 128), one byte->float conversion and one FMA per weight, f32 throughout.
+// Per unit the thread forms d * (sum_j x_j q_j - 8 sum_j x_j) (Q4_0; Q8_0 uses q ^ 0x80 and
+// 128), one byte->float conversion and one FMA per weight, f32 throughout.  The K-quants use
+// the same dot products with their own scale terms: Q4_K (d sc) sum x q - (dmin m) sum x
+// with (sc, m) decoded from the super-block header; Q6_K rebuilds each 6-bit value as one
+// byte (low nibble | high bits << 4) and forms sum over its two 16-weight halves of
+// (d sc_h) (sum x q - 32 sum x).
 //
 // Prologue options:  NORM  x := (x / sqrt(mean(x^2) + eps)) * w   (the RMSNorm that precedes
 //                          every projection in the chatbot, ffi.rs:2444-2486 + mul_impl),
@@ -31,9 +36,10 @@
 // Epilogues:  EPI_PLAIN   y = v
 //             EPI_RES     y = residual + v             (chatbot.tl:109, 111)
 //             EPI_GLU     rows (2i, 2i+1) = (gate_i, up_i): y_i = silu(g) * u (chatbot.tl:33-38)
-//             EPI_ROPE_KV rows of [q | k | v]: q, k pairs rotated by the table row of the
-//                         device position (ffi.rs:2655-2681), q written out, k and v appended
-//                         to the KV cache at that position (chatbot.tl:56-69)
+//             EPI_ROPE_KV rows of [q | k | v] (this weight's rows start at row_off of it):
+//                         q, k pairs rotated by the table row of the device position
+//                         (ffi.rs:2655-2681), q written out, k and v appended to the KV cache
+//                         at that position (chatbot.tl:56-69)
 //             EPI_ARGMAX  logits written, optional repetition penalty (device_impl.rs:967-1001),
 //                         per-workgroup greedy candidates; a one-workgroup kernel reduces
 //                         them (last maximum, tensor.rs:1633-1637), records the token and
@@ -52,6 +58,31 @@ template <>
 struct QB_<TL_HIP_GGML_Q8_0> {
     static constexpr int v = 32;
 };
+template <>
+struct QB_<TL_HIP_GGML_Q4_K> {
+    static constexpr int v = 16;
+};
+template <>
+struct QB_<TL_HIP_GGML_Q6_K> {
+    static constexpr int v = 16;
+};
+
+// Q4_K (scale, min) of sub-block j from a super-block header held as four words (f16 d |
+// f16 dmin, then the 12 packed bytes), QTensor::get_scale_min_k4 (quantized.rs:405-415).
+__device__ __forceinline__ void k4_sm(const uint4& hd, int j, float* du, float* mu) {
+    const int sh = 8 * (j & 3);
+    uint32_t sc, mn;
+    if (j < 4) {
+        sc = (hd.y >> sh) & 63;
+        mn = (hd.z >> sh) & 63;
+    } else {
+        const uint32_t lo = hd.w >> sh;
+        sc = (lo & 0xF) | (((hd.y >> sh) >> 2) & 0x30);
+        mn = ((lo >> 4) & 0xF) | (((hd.z >> sh) >> 2) & 0x30);
+    }
+    *du = __half2float(__ushort_as_half((uint16_t)(hd.x & 0xFFFF))) * (float)sc;
+    *mu = __half2float(__ushort_as_half((uint16_t)(hd.x >> 16))) * (float)mn;
+}
 
 // acc + sum_j x[j] * byte_j(q): one v_cvt_f32_ubyteN and one FMA per byte.  The empty asm
 // hides which bits of q are known to be zero (after a nibble mask); otherwise the byte
@@ -171,8 +202,12 @@ __global__ __launch_bounds__(256) void k_mv(MvArgs a, MvShape sh) {
             valid[i] = b < nb;
             bc[i] = valid[i] ? b : nb - 1;  // past the end: read the last column, scale 0
         }
+        constexpr bool K4 = QT == TL_HIP_GGML_Q4_K, K6 = QT == TL_HIP_GGML_Q6_K;
         uint4 w[BT][RWT][QW];
-        float dd[BT][RWT];
+        float dd[BT][RWT];                  // Q4_0 / Q8_0 / Q6_K (super-block) scale
+        uint4 kh[BT][K4 ? RWT : 1];         // Q4_K super-block header
+        uint2 h6[BT][K6 ? RWT : 1];         // Q6_K high bits
+        uint32_t s6[BT][K6 ? RWT : 1];      // Q6_K scale pair
         auto load_w = [&]() {
 #pragma unroll
             for (int i = 0; i < BT; i++) {
@@ -184,8 +219,17 @@ __global__ __launch_bounds__(256) void k_mv(MvArgs a, MvShape sh) {
                     const uint4* p = reinterpret_cast<const uint4*>(a.qs + (size_t)blk * QB);
 #pragma unroll
                     for (int c = 0; c < QW; c++) w[i][r][c] = p[c];
-                    const float dv = __half2float(a.d[blk]);
-                    dd[i][r] = valid[i] ? dv : 0.f;
+                    if constexpr (K4) {
+                        kh[i][r] = reinterpret_cast<const uint4*>(a.hdr)[blk >> 3];
+                    } else if constexpr (K6) {
+                        h6[i][r] = reinterpret_cast<const uint2*>(a.qh)[blk];
+                        s6[i][r] = reinterpret_cast<const uint16_t*>(a.sc)[blk];
+                        const float dv = __half2float(a.d[blk >> 3]);
+                        dd[i][r] = valid[i] ? dv : 0.f;
+                    } else {
+                        const float dv = __half2float(a.d[blk]);
+                        dd[i][r] = valid[i] ? dv : 0.f;
+                    }
                 }
             }
         };
@@ -254,8 +298,8 @@ __global__ __launch_bounds__(256) void k_mv(MvArgs a, MvShape sh) {
                     pre_res = a.res[(tid >> rw_shift) * n + row0 + (tid & (RW - 1))];
             } else if constexpr (EPI == EPI_ROPE_KV) {
                 pre_pos = (uint32_t)*a.pos;
-                const uint32_t r0 = row0 + 2 * tid;
-                if (tid < RW / 2 && r0 < n && r0 < (uint32_t)(a.q_rows + a.kv_rows)) {
+                const uint32_t r0 = row0 + 2 * tid + (uint32_t)a.row_off;
+                if (tid < RW / 2 && row0 + 2 * tid < n && r0 < (uint32_t)(a.q_rows + a.kv_rows)) {
                     const uint32_t i = (r0 < (uint32_t)a.q_rows ? r0 : r0 - a.q_rows) % (uint32_t)a.hd;
                     pre_c = a.cos_t[pre_pos * a.hd + i];
                     pre_s = a.sin_t[pre_pos * a.hd + i];
@@ -284,7 +328,7 @@ __global__ __launch_bounds__(256) void k_mv(MvArgs a, MvShape sh) {
                     xv[m][0][4 * c + 3] = t.w;
                 }
             }
-            float sx[M];
+            float sx[M], sxl[M], sxh[M];
 #pragma unroll
             for (int m = 0; m < M; m++) {
                 float sx0 = 0.f, sx1 = 0.f;
@@ -293,6 +337,8 @@ __global__ __launch_bounds__(256) void k_mv(MvArgs a, MvShape sh) {
                     sx0 += xv[m][0][j];
                     sx1 += xv[m][0][16 + j];
                 }
+                sxl[m] = sx0;
+                sxh[m] = sx1;
                 sx[m] = sx0 + sx1;
             }
             // row outer, activation row inner: each quant word is unpacked once.  Q4_0 high
@@ -303,7 +349,7 @@ __global__ __launch_bounds__(256) void k_mv(MvArgs a, MvShape sh) {
                 float s0[M], s1[M];
 #pragma unroll
                 for (int m = 0; m < M; m++) s0[m] = s1[m] = 0.f;
-                if constexpr (QT == TL_HIP_GGML_Q4_0) {
+                if constexpr (QT == TL_HIP_GGML_Q4_0 || QT == TL_HIP_GGML_Q4_K) {
                     const uint32_t q[4] = {w[i][r][0].x, w[i][r][0].y, w[i][r][0].z, w[i][r][0].w};
 #pragma unroll
                     for (int c = 0; c < 4; c++) {
@@ -314,9 +360,39 @@ __global__ __launch_bounds__(256) void k_mv(MvArgs a, MvShape sh) {
                             s1[m] = fma4b(hi, xv[m][0] + 16 + 4 * c, s1[m]);
                         }
                     }
+                    if constexpr (QT == TL_HIP_GGML_Q4_0) {
+#pragma unroll
+                        for (int m = 0; m < M; m++)
+                            acc[m][r] = fmaf(dd[i][r], fmaf(s1[m], 0.0625f, s0[m]) - 8.f * sx[m], acc[m][r]);
+                    } else {
+                        // unit = sub-block bc & 7: du * sum x q - mu * sum x
+                        float du, mu;
+                        k4_sm(kh[i][r], (int)(bc[i] & 7), &du, &mu);
+                        du = valid[i] ? du : 0.f;
+                        mu = valid[i] ? mu : 0.f;
+#pragma unroll
+                        for (int m = 0; m < M; m++)
+                            acc[m][r] = fmaf(du, fmaf(s1[m], 0.0625f, s0[m]), fmaf(-mu, sx[m], acc[m][r]));
+                    }
+                } else if constexpr (QT == TL_HIP_GGML_Q6_K) {
+                    // 6-bit values rebuilt per byte: low nibble | high 2 bits << 4
+                    const uint32_t q[4] = {w[i][r][0].x, w[i][r][0].y, w[i][r][0].z, w[i][r][0].w};
+                    const uint32_t H0 = h6[i][r].x, H1 = h6[i][r].y;
+#pragma unroll
+                    for (int c = 0; c < 4; c++) {
+                        const uint32_t lo = (q[c] & 0x0F0F0F0Fu) | (((H0 >> (2 * c)) & 0x03030303u) << 4);
+                        const uint32_t hi = ((q[c] >> 4) & 0x0F0F0F0Fu) | (((H1 >> (2 * c)) & 0x03030303u) << 4);
+#pragma unroll
+                        for (int m = 0; m < M; m++) {
+                            s0[m] = fma4b(lo, xv[m][0] + 4 * c, s0[m]);
+                            s1[m] = fma4b(hi, xv[m][0] + 16 + 4 * c, s1[m]);
+                        }
+                    }
+                    const float e0 = dd[i][r] * (float)(int8_t)(s6[i][r] & 0xFF);
+                    const float e1 = dd[i][r] * (float)(int8_t)(s6[i][r] >> 8);
 #pragma unroll
                     for (int m = 0; m < M; m++)
-                        acc[m][r] = fmaf(dd[i][r], fmaf(s1[m], 0.0625f, s0[m]) - 8.f * sx[m], acc[m][r]);
+                        acc[m][r] = fmaf(e0, fmaf(-32.f, sxl[m], s0[m]), fmaf(e1, fmaf(-32.f, sxh[m], s1[m]), acc[m][r]));
                 } else {
                     const uint32_t q[8] = {w[i][r][0].x, w[i][r][0].y, w[i][r][0].z, w[i][r][0].w,
                                            w[i][r][1].x, w[i][r][1].y, w[i][r][1].z, w[i][r][1].w};
@@ -386,8 +462,8 @@ __global__ __launch_bounds__(256) void k_mv(MvArgs a, MvShape sh) {
     } else if constexpr (EPI == EPI_ROPE_KV) {
         const int64_t pos = pre_pos;
         if (tid < RW / 2) {
-            const int64_t r0 = row0 + 2 * tid;
-            if (r0 < n) {
+            const int64_t r0 = row0 + 2 * tid + a.row_off;  // row of the q | k | v projection
+            if (row0 + 2 * tid < n) {
                 const float v0 = ys[0][2 * tid], v1 = ys[0][2 * tid + 1];
                 if (r0 < a.q_rows + a.kv_rows) {
                     const bool isq = r0 < a.q_rows;
@@ -539,7 +615,7 @@ static MvPlan mv_plan(int64_t n, int64_t nb, int qt) {
     p.TC = (int)(nb >= 256 ? 256 : cdiv(nb, 64) * 64);
     p.BT = nb > 256 ? 2 : 1;
     p.S = p.TC <= 128 ? 256 / p.TC : 1;  // TC of 64 or 128: a power of two
-    const int qw = qt == TL_HIP_GGML_Q8_0 ? 2 : 1;
+    const int qw = qt == TL_HIP_GGML_Q4_0 ? 1 : 2;  // 16-byte loads per unit incl. scale data
     int rwt = 2;
     while (rwt < 8 && cdiv(n, (int64_t)p.S * rwt) > 720) rwt *= 2;
     while (rwt > 2 && rwt * p.BT * qw > 16) rwt /= 2;
@@ -603,6 +679,9 @@ static int run_t(const MvArgs& a, int m, int epi, bool norm, bool embed, const M
 int launch_mv(const QWeight* w, MvArgs a, int m, int epi, bool norm, bool embed, hipStream_t s) {
     a.qs = w->qs;
     a.d = w->d;
+    a.hdr = w->hdr;
+    a.qh = w->qh;
+    a.sc = w->sc;
     a.n = w->n;
     a.k = w->k;
     a.nb = w->nb;
@@ -632,8 +711,12 @@ int launch_mv(const QWeight* w, MvArgs a, int m, int epi, bool norm, bool embed,
         set_error(TL_HIP_ERR_SHAPE, "ShapeMismatch: paired epilogue needs an even row count");
         return TL_HIP_ERR_SHAPE;
     }
-    if (w->ggml_type == TL_HIP_GGML_Q4_0) return run_t<TL_HIP_GGML_Q4_0>(a, m, epi, norm, embed, p, s);
-    return run_t<TL_HIP_GGML_Q8_0>(a, m, epi, norm, embed, p, s);
+    switch (w->ggml_type) {
+        case TL_HIP_GGML_Q4_0: return run_t<TL_HIP_GGML_Q4_0>(a, m, epi, norm, embed, p, s);
+        case TL_HIP_GGML_Q8_0: return run_t<TL_HIP_GGML_Q8_0>(a, m, epi, norm, embed, p, s);
+        case TL_HIP_GGML_Q4_K: return run_t<TL_HIP_GGML_Q4_K>(a, m, epi, norm, embed, p, s);
+        default: return run_t<TL_HIP_GGML_Q6_K>(a, m, epi, norm, embed, p, s);
+    }
 }
 
 // Upper bound on the workgroups (= argmax partial slots) of a matvec over n rows.

@@ -13,7 +13,7 @@ import numpy as np
 
 from . import _lib
 
-GGML_F32, GGML_F16, GGML_Q4_0, GGML_Q8_0 = 0, 1, 2, 8
+GGML_F32, GGML_F16, GGML_Q4_0, GGML_Q8_0, GGML_Q4_K, GGML_Q6_K = 0, 1, 2, 8, 12, 14
 F32, F16 = 0, 1
 
 _VARIANTS = {
