@@ -27,7 +27,7 @@ ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, ROOT)
 
 MATVEC_N = MATVEC_K = 4096
-MATVEC_BYTES = MATVEC_N * MATVEC_K // 32 * 18 + MATVEC_K * 4 + MATVEC_N * 4  # 9,469,952
+MATVEC_BYTES = MATVEC_N * MATVEC_K // 32 * 18 + MATVEC_K * 4 + MATVEC_N * 4  # 9,469,952 (Q4_0)
 HBM_PEAK_GBS = 8000.0
 # HBM bytes per 4096 x 4096 matvec launch from the two counter runs of
 # `bench.py --matvec-only` (FETCH_SIZE 4,713.04 KiB x 1.99895 + WRITE_SIZE 16.0 KiB x 1.0, the
@@ -39,16 +39,27 @@ def log(*a):
     print(*a, file=sys.stderr, flush=True)
 
 
-def bench_matvec(dev, launches=340, copies=34):
+def matvec_bytes(t, n=MATVEC_N, k=MATVEC_K):
+    """Algorithmic bytes of one m = 1 matvec: the GGUF blocks + x + y (f32)."""
+    per = {2: (32, 18), 8: (32, 34), 12: (256, 144), 14: (256, 210)}[t]
+    return n * k // per[0] * per[1] + k * 4 + n * 4
+
+
+def bench_matvec(dev, t=2, launches=340, min_bytes=320 << 20):
+    """Average seconds of one 4096 x 4096 matvec (m = 1) of GGML type t, launched back to back
+    over enough resident weight copies (>= 320 MB) that the 256 MB Infinity Cache cannot
+    serve them."""
     import ctypes as C
 
-    from tl_amd import GGML_Q4_0, QTensor
-    from tl_amd.quant import random_q4_0_blocks
+    from tl_amd import QTensor
+    from tl_amd.quant import random_q4_0_blocks, random_q4_k_blocks, random_q6_k_blocks, random_q8_0_blocks
 
+    gen = {2: random_q4_0_blocks, 8: random_q8_0_blocks, 12: random_q4_k_blocks, 14: random_q6_k_blocks}[t]
     lib = dev.lib
     rng = np.random.default_rng(0x71510000)
-    raw = random_q4_0_blocks(rng, MATVEC_N, MATVEC_K)
-    ws = [QTensor(GGML_Q4_0, raw, (MATVEC_N, MATVEC_K)) for _ in range(copies)]
+    raw = gen(rng, MATVEC_N, MATVEC_K)
+    copies = -(-min_bytes // raw.nbytes)
+    ws = [QTensor(t, raw, (MATVEC_N, MATVEC_K)) for _ in range(copies)]
     hs = [w.upload(lib) for w in ws]
     x = dev.tensor_new(rng.standard_normal((1, MATVEC_K)).astype(np.float32))
     y = dev.tensor_zeros((1, MATVEC_N))
@@ -73,6 +84,18 @@ def bench_matvec(dev, launches=340, copies=34):
     for w in ws:
         w.release()
     return avg_s
+
+
+def bench_quant_matvec(dev):
+    """The 4096 x 4096 m = 1 matvec in every resident type (GB/s of algorithmic bytes)."""
+    rows = []
+    for t, name in ((2, "Q4_0"), (8, "Q8_0"), (12, "Q4_K"), (14, "Q6_K")):
+        sec = bench_matvec(dev, t)
+        gbs = matvec_bytes(t) / sec / 1e9
+        rows.append({"type": name, "bytes": matvec_bytes(t), "us": round(sec * 1e6, 3), "gbs": round(gbs, 1),
+                     "frac": round(gbs / HBM_PEAK_GBS, 4)})
+        log(f"[bench] matvec {name} 4096x4096: {sec * 1e6:.2f} us, {gbs:.0f} GB/s")
+    return rows
 
 
 MFMA_F16_PEAK_TFLOPS = 2500.0
@@ -205,6 +228,40 @@ def cpu_baseline(cfg, L):
     return tok_s, t_layer, t_head
 
 
+def bench_decode(dev, cfg, ggml_type, args, steps=None):
+    """Prefill of the prompt, then warm-up and timed greedy decode tokens (hipGraph replay
+    unless --no-graph); returns (tok/s, decode seconds, prefill seconds)."""
+    from tl_amd.llama import HipLlama, synthetic_prompt, synthetic_weights
+
+    steps = steps or args.steps
+    log(f"[bench] generating synthetic TinyLlama-shape {ggml_type if isinstance(ggml_type, str) else 'Q4_0'} "
+        f"weights ...")
+    t0 = time.time()
+    model = HipLlama(cfg, kv_f16=(args.kv == "f16"))
+    model.load(synthetic_weights(cfg, 1234, ggml_type=ggml_type), ggml_type=ggml_type)
+    log(f"[bench] weights resident ({time.time() - t0:.1f} s)")
+    prompt = synthetic_prompt(cfg, 1234, args.prompt)
+    model.reset()
+    dev.synchronize()
+    t0 = time.perf_counter()
+    model.forward(prompt, prefill_f16=True, want_logits=False)
+    dev.synchronize()
+    prefill_s = time.perf_counter() - t0
+    first = model.sample_greedy(1.0, prompt)
+    log(f"[bench] prefill {args.prompt} tokens: {prefill_s * 1e3:.1f} ms")
+    warm = model.generate(first, args.warmup, use_graph=not args.no_graph) if args.warmup else np.array([first])
+    nxt = int(warm[-1]) if args.warmup else first
+    dev.synchronize()
+    t0 = time.perf_counter()
+    model.generate(nxt, steps, use_graph=not args.no_graph)  # ends with a stream synchronize
+    dev.synchronize()
+    decode_s = time.perf_counter() - t0
+    tok_s = steps / decode_s
+    log(f"[bench] decode {steps} tokens: {decode_s * 1e3:.1f} ms -> {tok_s:.1f} tok/s")
+    model.close()
+    return tok_s, decode_s, prefill_s
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -216,6 +273,7 @@ def main():
     ap.add_argument("--no-graph", action="store_true", help="eager launches instead of hipGraph replay")
     ap.add_argument("--no-extra", action="store_true", help="skip the prefill GEMM and attention legs")
     ap.add_argument("--gemm-only", action="store_true", help="only the prefill GEMM leg (counter runs)")
+    ap.add_argument("--kquant-only", action="store_true", help="only the per-type matvec and Q4_K_M decode legs")
     ap.add_argument("--matvec-only", action="store_true",
                     help="only the 4096x4096 matvec timing plus a 64 MiB device copy (counter runs)")
     args = ap.parse_args()
@@ -225,7 +283,7 @@ def main():
         sys.exit(2)
 
     from tl_amd import HipDevice
-    from tl_amd.llama import HipLlama, LlamaConfig, synthetic_prompt, synthetic_weights
+    from tl_amd.llama import LlamaConfig
 
     dev = HipDevice(0)
     cfg = LlamaConfig.tinyllama(max_seq=2048)
@@ -234,6 +292,12 @@ def main():
 
     if args.gemm_only:
         print(json.dumps({"prefill_gemm": bench_gemm(dev)}), flush=True)
+        return
+    if args.kquant_only:
+        print(json.dumps({"quant_matvec": bench_quant_matvec(dev)}), flush=True)
+        tok_s, decode_s, prefill_s = bench_decode(dev, cfg, "Q4_K_M", args, steps=64)
+        print(json.dumps({"q4_k_m_decode_tok_s": round(tok_s, 2), "prefill_ms": round(prefill_s * 1e3, 2)}),
+              flush=True)
         return
 
     log("[bench] Q4_0 4096x4096 matvec roofline ...")
@@ -253,35 +317,20 @@ def main():
                           "copy_bytes": nbytes}), flush=True)
         return
 
-    gemm = attn = None
+    gemm = attn = qmv = None
     if not args.no_extra:
+        qmv = bench_quant_matvec(dev)
         gemm = bench_gemm(dev)
         attn = bench_attention(dev)
 
-    log("[bench] generating synthetic TinyLlama-shape Q4_0 weights ...")
-    t0 = time.time()
-    model = HipLlama(cfg, kv_f16=(args.kv == "f16"))
-    model.load(synthetic_weights(cfg, 1234))
-    log(f"[bench] weights resident ({time.time() - t0:.1f} s)")
-    prompt = synthetic_prompt(cfg, 1234, args.prompt)
-
-    model.reset()
-    dev.synchronize()
-    t0 = time.perf_counter()
-    model.forward(prompt, prefill_f16=True, want_logits=False)
-    prefill_s = time.perf_counter() - t0
-    first = model.sample_greedy(1.0, prompt)
-    log(f"[bench] prefill {args.prompt} tokens: {prefill_s * 1e3:.1f} ms")
-    warm = model.generate(first, args.warmup, use_graph=not args.no_graph) if args.warmup else np.array([first])
-    nxt = int(warm[-1]) if args.warmup else first
-    dev.synchronize()
-    t0 = time.perf_counter()
-    model.generate(nxt, args.steps, use_graph=not args.no_graph)  # ends with a stream synchronize
-    dev.synchronize()
-    decode_s = time.perf_counter() - t0
-    tok_s = args.steps / decode_s
-    log(f"[bench] decode {args.steps} tokens: {decode_s * 1e3:.1f} ms -> {tok_s:.1f} tok/s")
-    model.close()
+    tok_s, decode_s, prefill_s = bench_decode(dev, cfg, 2, args)
+    kq = None
+    if not args.no_extra:
+        kq_tok_s, kq_decode_s, kq_prefill_s = bench_decode(dev, cfg, "Q4_K_M", args, steps=64)
+        kq = {"workload": "same decoder with llama.cpp's Q4_K_M type mixture (Q4_K; Q6_K for the LM head and "
+                          "attn_v / ffn_down of 11 of 22 layers)", "value": round(kq_tok_s, 2), "unit": "tok/s",
+              "steps": 64, "ms_per_step": round(kq_decode_s * 1e3 / 64, 4), "prefill_ms": round(kq_prefill_s * 1e3, 2),
+              "prefill_path": "f32 GEMM (K-quant weights)"}
 
     cpu = None
     if not args.no_cpu_baseline:
@@ -330,6 +379,8 @@ def main():
                          "peak": MFMA_F16_PEAK_TFLOPS, "shapes": gemm},
         "decode_attention": {"kv": "f16", "hq": 32, "hkv": 8, "head_dim": 128, "unit": "GB/s",
                              "peak": HBM_PEAK_GBS, "cases": attn},
+        "quant_matvec": {"shape": "4096x4096, m=1", "unit": "GB/s", "peak": HBM_PEAK_GBS, "types": qmv},
+        "q4_k_m_decode": kq,
     }
     print(json.dumps(out), flush=True)
 
