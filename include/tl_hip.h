@@ -126,6 +126,37 @@ tl_hip_tensor* tl_hip_qtensor_matmul(const tl_hip_tensor* x, const tl_hip_qtenso
  * f32 accumulate); tolerance class "f16 path".  Q4_K / Q6_K weights take the f32 GEMM. */
 tl_hip_tensor* tl_hip_qtensor_matmul_f16(const tl_hip_tensor* x, const tl_hip_qtensor* q);
 
+/* ---------------------------------------------------------------- GGUF files ----- */
+/* The tensor map of a GGUF file (OpaqueTensorMap of tensor_map.rs, filled by tl_gguf_load). */
+typedef struct tl_hip_gguf tl_hip_gguf;
+/* tl_gguf_load (crates/tl_runtime/src/gguf.rs:34-196): maps the file and reads the GGUF v2 / v3
+ * header ("GGUF" or byte-swapped "FUGG"), metadata and tensor table; data start = end of the
+ * tensor table rounded up to general.alignment (default 32).  Shapes as gguf.rs:129-136
+ * (trailing 1s trimmed, reversed to row-major); tensors of types outside F32, F16, Q4_0,
+ * Q4_1, Q5_0, Q5_1, Q8_0, Q8_1, Q4_K, Q6_K or with data past the end of the file are skipped
+ * (gguf.rs:157-182).  NULL + ArgumentError when the file cannot be opened or decoded. */
+tl_hip_gguf* tl_hip_gguf_open(const char* path);
+/* tl_tensor_map_free (tensor_map.rs:68-77): also drops the map's references to the weight
+ * residencies handed out by tl_hip_gguf_get_quantized. */
+int tl_hip_gguf_close(tl_hip_gguf* g);
+int64_t tl_hip_gguf_tensor_count(const tl_hip_gguf* g);
+const char* tl_hip_gguf_tensor_name(const tl_hip_gguf* g, int64_t i);
+/* ggml type, row-major shape (up to TL_HIP_MAX_RANK entries), rank and data bytes of a tensor. */
+int tl_hip_gguf_tensor_info(const tl_hip_gguf* g, const char* name, int* ggml_type, int64_t* shape,
+                            int* rank, uint64_t* nbytes);
+/* The tensor's bytes inside the mapped file (valid until tl_hip_gguf_close). */
+const uint8_t* tl_hip_gguf_tensor_data(const tl_hip_gguf* g, const char* name, uint64_t* nbytes);
+/* Metadata (GGUF key/value section): numeric values as double, strings as text. */
+int tl_hip_gguf_meta_f64(const tl_hip_gguf* g, const char* key, double* out);
+const char* tl_hip_gguf_meta_str(const tl_hip_gguf* g, const char* key);
+/* tl_tensor_map_get_quantized (tensor_map.rs:279-301): the quantized weight handle; its
+ * device residency is built from the mapped bytes on the first request and shared by later
+ * ones (each call returns one more reference, released with tl_hip_qtensor_release). */
+tl_hip_qtensor* tl_hip_gguf_get_quantized(tl_hip_gguf* g, const char* name);
+/* tl_tensor_map_get (tensor_map.rs:110-150): an f32 device tensor -- F32 data as stored, F16
+ * converted (quantized.rs:167-180), quantized types dequantized (quantized.rs:117-165). */
+tl_hip_tensor* tl_hip_gguf_get(tl_hip_gguf* g, const char* name);
+
 /* ---------------------------------------------------------------- raw launchers --- */
 /* Kernel ABI in the style of launch_mul_mv_q4_k_kernel (crates/tl_cuda/src/cuda_kernels/
  * autograd.cu:2904-2924): device pointers + dims + stream, returns a status.  `w` is a
@@ -225,6 +256,12 @@ int tl_hip_llama_set_linear(tl_hip_llama* m, int layer, int which, int ggml_type
                             const uint8_t* data, size_t nbytes);
 int tl_hip_llama_set_norm(tl_hip_llama* m, int layer, int which, const float* w);
 int tl_hip_llama_set_embedding(tl_hip_llama* m, const float* table);
+/* Every weight of the decoder from a GGUF tensor map under the names chatbot.tl reads
+ * (Block::from_map / Attention / MLP / RMSNorm::new, chatbot.tl:10-26, 44-47, 94-99, and
+ * token_embd / output_norm / output, 153-155): blk.{i}.attn_{q,k,v,output}.weight,
+ * blk.{i}.ffn_{gate,up,down}.weight, blk.{i}.{attn,ffn}_norm.weight.  Shapes are checked
+ * against the decoder's configuration. */
+int tl_hip_llama_load_gguf(tl_hip_llama* m, tl_hip_gguf* g);
 /* KV-cache element type (kv_f16: 0 = f32, the tl_cpu cache; 1 = f16) and RoPE position rule
  * (rope_per_token: 0 = tl_cpu's, every token of a call rotated by the table row of the call's
  * start position, chatbot.tl:56-61 + ffi.rs:2655-2681; 1 = token t at start + t).  Resets the

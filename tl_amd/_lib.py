@@ -53,6 +53,18 @@ PROTOS = {
     "tl_hip_qtensor_dequantize": (P, [P]),
     "tl_hip_qtensor_matmul": (P, [P, P]),
     "tl_hip_qtensor_matmul_f16": (P, [P, P]),
+    "tl_hip_gguf_open": (P, [C.c_char_p]),
+    "tl_hip_gguf_close": (i32, [P]),
+    "tl_hip_gguf_tensor_count": (i64, [P]),
+    "tl_hip_gguf_tensor_name": (C.c_char_p, [P, i64]),
+    "tl_hip_gguf_tensor_info": (i32, [P, C.c_char_p, C.POINTER(i32), i64p, C.POINTER(i32),
+                                      C.POINTER(C.c_uint64)]),
+    "tl_hip_gguf_tensor_data": (P, [P, C.c_char_p, C.POINTER(C.c_uint64)]),
+    "tl_hip_gguf_meta_f64": (i32, [P, C.c_char_p, C.POINTER(f64)]),
+    "tl_hip_gguf_meta_str": (C.c_char_p, [P, C.c_char_p]),
+    "tl_hip_gguf_get_quantized": (P, [P, C.c_char_p]),
+    "tl_hip_gguf_get": (P, [P, C.c_char_p]),
+    "tl_hip_llama_load_gguf": (i32, [P, P]),
     "tl_hip_launch_quant_matvec": (i32, [P, P, P, i64, P]),
     "tl_hip_launch_quant_gemm": (i32, [P, P, P, i64, i32, P]),
     "tl_hip_tensor_matmul": (P, [P, P]),

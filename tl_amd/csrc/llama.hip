@@ -627,6 +627,87 @@ int tl_hip_llama_set_embedding(tl_hip_llama* h, const float* table) {
     return TL_HIP_OK;
 }
 
+// One GGUF tensor as a host f32 vector of the expected shape (norms are tiny).
+static int gguf_f32(tl_hip_gguf* g, const char* name, int64_t n, std::vector<float>* out) {
+    tl_hip_tensor* t = tl_hip_gguf_get(g, name);
+    if (!t) return tl_hip_last_status();
+    int rc = TL_HIP_OK;
+    if (tl_hip_tensor_numel(t) != n) {
+        set_error(TL_HIP_ERR_SHAPE, "ShapeMismatch: '%s' has %lld elements, expected %lld", name,
+                  (long long)tl_hip_tensor_numel(t), (long long)n);
+        rc = TL_HIP_ERR_SHAPE;
+    } else {
+        out->resize((size_t)n);
+        rc = tl_hip_tensor_to_host(t, out->data(), n);
+    }
+    tl_hip_tensor_release(t);
+    return rc;
+}
+
+int tl_hip_llama_load_gguf(tl_hip_llama* h, tl_hip_gguf* g) {
+    if (!h || !g) {
+        set_error(TL_HIP_ERR_NULL, "NullPointerError: model or gguf");
+        return TL_HIP_ERR_NULL;
+    }
+    Llama* m = L_(h);
+    static const char* kLin[7] = {"attn_q", "attn_k", "attn_v", "attn_output", "ffn_gate", "ffn_up", "ffn_down"};
+    const int64_t D = m->D, KVd = (int64_t)m->KV * m->hd, F = m->F;
+    const int64_t want[7][2] = {{D, D}, {KVd, D}, {KVd, D}, {D, D}, {F, D}, {F, D}, {D, F}};
+    char name[160];
+    auto linear = [&](int layer, int which, const char* nm, int64_t n, int64_t k) -> int {
+        int type = 0, rank = 0;
+        int64_t shape[TL_HIP_MAX_RANK];
+        uint64_t nbytes = 0;
+        if (tl_hip_gguf_tensor_info(g, nm, &type, shape, &rank, &nbytes)) return tl_hip_last_status();
+        if (rank != 2 || shape[0] != n || shape[1] != k) {
+            set_error(TL_HIP_ERR_SHAPE, "ShapeMismatch: '%s' is not [%lld, %lld]", nm, (long long)n, (long long)k);
+            return TL_HIP_ERR_SHAPE;
+        }
+        const uint8_t* data = tl_hip_gguf_tensor_data(g, nm, &nbytes);
+        if (!data) return tl_hip_last_status();
+        return tl_hip_llama_set_linear(h, layer, which, type, data, (size_t)nbytes);
+    };
+    std::vector<float> v;
+    int rc;
+    for (int l = 0; l < m->nl; l++) {
+        for (int w = 0; w < 7; w++) {
+            snprintf(name, sizeof(name), "blk.%d.%s.weight", l, kLin[w]);
+            if ((rc = linear(l, w, name, want[w][0], want[w][1]))) return rc;
+        }
+        for (int w = 0; w < 2; w++) {
+            snprintf(name, sizeof(name), "blk.%d.%s_norm.weight", l, w == 0 ? "attn" : "ffn");
+            if ((rc = gguf_f32(g, name, D, &v))) return rc;
+            if ((rc = tl_hip_llama_set_norm(h, l, w, v.data()))) return rc;
+        }
+    }
+    if ((rc = gguf_f32(g, "output_norm.weight", D, &v))) return rc;
+    if ((rc = tl_hip_llama_set_norm(h, -1, 0, v.data()))) return rc;
+    if ((rc = linear(-1, 0, "output.weight", m->V, D))) return rc;
+    // token_embd.weight: the f32 table (dequantized on the device when stored quantized)
+    tl_hip_tensor* e = tl_hip_gguf_get(g, "token_embd.weight");
+    if (!e) return tl_hip_last_status();
+    const Tensor* et = reinterpret_cast<const Tensor*>(e);
+    if (et->rank != 2 || et->shape[0] != m->V || et->shape[1] != D) {
+        tl_hip_tensor_release(e);
+        set_error(TL_HIP_ERR_SHAPE, "ShapeMismatch: token_embd.weight is not [%d, %lld]", m->V, (long long)D);
+        return TL_HIP_ERR_SHAPE;
+    }
+    const size_t bytes = (size_t)m->V * D * 4;
+    if (!m->emb) {
+        m->emb = (float*)dev_alloc(bytes);
+        if (!m->emb) {
+            tl_hip_tensor_release(e);
+            return TL_HIP_ERR_ALLOC;
+        }
+        free_graph(m);
+    }
+    hipError_t err = hipMemcpyAsync(m->emb, et->data, bytes, hipMemcpyDeviceToDevice, cur_stream());
+    if (err == hipSuccess) err = hipStreamSynchronize(cur_stream());
+    tl_hip_tensor_release(e);
+    if (err != hipSuccess) return hip_fail(err, "embedding copy");
+    return TL_HIP_OK;
+}
+
 int tl_hip_llama_configure(tl_hip_llama* h, int kv_f16, int rope_per_token) {
     if (!h) {
         set_error(TL_HIP_ERR_NULL, "NullPointerError: model");
