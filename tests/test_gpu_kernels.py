@@ -180,6 +180,23 @@ def test_attention_decode_f16_kv(dev, L, B):
         assert_rel(got[b], ref, F32_TOL)
 
 
+@pytest.mark.parametrize("d,hq,hkv,lmax,L,B", [(64, 32, 4, 2000, 1500, 2), (128, 32, 4, 1100, 1031, 1),
+                                               (64, 16, 4, 1400, 1025, 3), (128, 64, 8, 4096, 4096, 1)])
+def test_attention_grouped_split_lengths(dev, d, hq, hkv, lmax, L, B):
+    # caches longer than 1024 positions take the grouped-query split kernel: lengths that end
+    # inside a 128-position split, 4 and 8 query heads per KV head, head_dim 64 and 128
+    rng = np.random.default_rng(0x71570000 + L + d + B)
+    q = rng.standard_normal((B, hq, d)).astype(np.float32)
+    k = rng.standard_normal((B, hkv, lmax, d)).astype(np.float16)
+    v = rng.standard_normal((B, hkv, lmax, d)).astype(np.float16)
+    got = dev.attention_decode(dev.tensor_new(q), dev.tensor_new_f16(k), dev.tensor_new_f16(v), L,
+                               1.0 / np.sqrt(d)).to_numpy()
+    for b in range(B):
+        ref = oracle.attention(q[b][None], k[b, :, :L].astype(np.float32), v[b, :, :L].astype(np.float32),
+                               np.float32(1.0 / np.sqrt(d)), False).reshape(hq, d)
+        assert_rel(got[b], ref, F32_TOL)
+
+
 def test_attention_decode_partial_length_and_f32_cache(dev):
     rng = np.random.default_rng(17)
     q = rng.standard_normal((2, 32, 64)).astype(np.float32)

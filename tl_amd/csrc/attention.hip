@@ -1,19 +1,17 @@
-// Single-query decode attention with grouped KV heads over a KV cache (f16 or f32),
-// split along the cached length (flash-decoding) so one token at batch 1 still spreads over
-// many CUs.  Replaces the chatbot's transpose / cat_4d / repeat_interleave / matmul_4d /
-// scale / softmax / matmul_4d chain (examples/apps/tinyllama/chatbot.tl:63-87): K and V are
-// read once, in place, and the Hq/Hkv query heads of a group share every K/V row loaded
-// (no repeat_interleave copy).
-//
-// Pass 1: workgroup = (split, kv head, batch item), 4 wavefronts.  Eight lanes share a
-// cache row (each owns D/8 consecutive dims), so a wavefront covers 8 positions per load
-// instruction and a workgroup 32.  The K and V rows of the first two 32-position steps are
-// requested at kernel start, so the chunk's memory latency overlaps the q load and the
-// score pass.  Scores go to LDS, each head's chunk max and exp-sum are formed, the
-// exp-weighted V rows are accumulated, and the (o, max, sum) record is written.  A second
-// small kernel merges the records of a (batch, kv head):
-// out = sum_s o_s e^(m_s - M) / sum_s l_s e^(m_s - M).  A single split writes its result
-// directly.  All arithmetic is f32.
+// Single-query decode attention with grouped KV heads over a KV cache (f16 or f32), the
+// replacement of the chatbot's transpose / cat_4d / repeat_interleave / matmul_4d / scale /
+// softmax / matmul_4d chain (examples/apps/tinyllama/chatbot.tl:63-87): K and V are read in
+// place, and the Hq/Hkv query heads of a group share every K/V row loaded (no
+// repeat_interleave copy).  A causal prefill of n queries over one shared cache is the same
+// computation with per-query lengths (AttnLen.len_step = 1).  Three forms, all f32 arithmetic:
+//   * k_attn_qh  short caches (decode of the chatbot's model): one workgroup per query head;
+//   * k_attn_gq  f16 caches, 4 or 8 query heads per KV head, head_dim 64 / 128: one workgroup
+//                per (split of 128 or 64 positions, KV head, query), every row read once for
+//                all heads of the group, then k_attn_merge_gq (flash-decoding);
+//   * k_attn     the general form (f32 caches, other group sizes), split the same way, then
+//                k_attn_merge.
+// A split's record is (o, max, sum); the merge forms
+// out = sum_s o_s e^(m_s - M) / sum_s l_s e^(m_s - M); a single split writes its result.
 #include "internal.h"
 
 namespace tlhip {
@@ -280,18 +278,7 @@ __global__ __launch_bounds__(256) void k_attn_merge(AttnArgs a) {
     }
 }
 
-// ------------------------------------------------------------------------------------------
-// Decode form for 4 or 8 query heads per KV head: splits of 64 positions, no cross-lane
-// reductions in the inner loops.
-//   scores: lane = position; the lane reads its whole K row (D/8 16-byte loads) and takes
-//           the dot products with the q rows of its wavefront's heads (LDS broadcast reads);
-//   softmax over the 64 positions of the split: one wavefront max and sum per head;
-//   P.V:    lane = (dim group dg = lane / 8, slot = lane % 8): positions slot, slot+8, ...,
-//           D/8 dims each; the 8 slots are summed with DPP at the end.
-// Wavefront w owns heads w*G/4 .. (w+1)*G/4 - 1.  Splits past the cached length exit at once.
-// With FUSED, the last active split of a (batch, kv head) to finish -- an arrival counter,
-// no waiting -- merges the records, so a decode step needs one launch; otherwise
-// k_attn_merge does it.
+// ---- shared helpers ---------------------------------------------------------------------
 template <int CTRL>
 __device__ __forceinline__ float dpp_f(float v) {
     return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), CTRL, 0xF, 0xF, true));
@@ -334,185 +321,186 @@ __device__ __forceinline__ void cvt8<__half>(const uint4& w, float* f) {
     }
 }
 
-constexpr int DEC_C = 64;           // positions per split in the decode form
-constexpr int DEC_MAX_FUSED = 32;   // splits the in-kernel merge handles (2048 positions)
+// ---- grouped-query split form: one workgroup per (split of 128 positions, kv head, item) --
+// Every K / V row of the split is read exactly once (coalesced: D/8 consecutive lanes share a
+// row, 16 bytes each) and serves all G query heads of its KV head -- no per-head re-reads.
+// The rows of a wavefront's 32 positions are requested at kernel start.
+//   scores: lane (row r, slice kl) forms the partial dot products of its 8 dims with the G
+//           q vectors for each of its rows; one transpose-reduce over the D/8 lanes of a row
+//           leaves N / (D/8) finished scores per lane, which go to LDS;
+//   softmax over the split's 128 positions per head (one wavefront per head);
+//   P.V:    the same lanes accumulate p_g * v for their rows and all heads, then a second
+//           transpose-reduce over the rows of the wavefront and an LDS sum over the four
+//           wavefronts give the split's (o, max, sum) record; k_attn_merge combines splits
+//           (a single split writes the output directly).
+template <int OFF>
+__device__ __forceinline__ float xchg_lo(float v) {  // partner across lane bit OFF within 16 lanes
+    if constexpr (OFF == 8) return dpp_f<0x140>(v);      // row mirror (15 - i)
+    else if constexpr (OFF == 4) return dpp_f<0x141>(v); // half-row mirror (7 - i)
+    else if constexpr (OFF == 2) return dpp_f<0x4E>(v);  // quad_perm [2,3,0,1]
+    else return dpp_f<0xB1>(v);                          // quad_perm [1,0,3,2]
+}
+template <int OFF>
+__device__ __forceinline__ float xchg_hi(float v) {  // exact xor of lane bit OFF (OFF >= 8)
+    if constexpr (OFF == 8) return dpp_f<0x128>(v);  // row_ror:8 = xor 8 within 16 lanes
+    else return __shfl_xor(v, OFF, 64);
+}
 
-template <int D, int G, bool FUSED>
-__global__ __launch_bounds__(256) void k_attn_dec(AttnArgs a, int32_t* counter) {
-    using KVT = __half;
-    constexpr int HPW = G / 4;   // heads per wavefront
-    constexpr int DL = D / 8;    // dims per lane in P.V
-    constexpr int KC = D / 8;    // 16-byte chunks of a K row
-    __shared__ __attribute__((aligned(16))) float qsh[G][D];
-    __shared__ float P[G][DEC_C];
+// Transpose-reduce of N values over the lanes that differ in lane bits LO .. OFF (powers of
+// two, the first call's OFF the highest): each step sends half of the values across one bit
+// and keeps the half its own bit selects.  Afterwards value j of the lane whose bits
+// LO .. OFF read r holds the group sum of original value j + r * N / (2 OFF / LO).  Partners
+// below 16 lanes apart may also differ in lower bits (the DPP mirrors): every lane of a
+// group holds the same value indices when they exchange, so only the stepped bit matters.
+template <int OFF, int LO, int H, int N, bool HIGH>
+__device__ __forceinline__ void tr_halve(float (&v)[N], int lane) {
+    const bool up = (lane & OFF) != 0;
+#pragma unroll
+    for (int i = 0; i < H; i++) {
+        const float send = up ? v[i] : v[i + H];
+        const float keep = up ? v[i + H] : v[i];
+        if constexpr (HIGH) v[i] = keep + xchg_hi<OFF>(send);
+        else v[i] = keep + xchg_lo<OFF>(send);
+    }
+    if constexpr (OFF > LO) tr_halve<OFF / 2, LO, H / 2, N, HIGH>(v, lane);
+}
+
+template <int D, int G, int PW>  // PW positions per wavefront, 4 PW per workgroup (split)
+__global__ __launch_bounds__(256) void k_attn_gq(AttnArgs a) {
+    constexpr int GQ_PW = PW, GQ_CH = 4 * PW;
+    constexpr int LPR = D / 8;          // lanes per row (16 bytes of f16 each)
+    constexpr int RPI = 64 / LPR;       // rows per load instruction
+    constexpr int NI = GQ_PW / RPI;     // load instructions per wavefront (K and V each)
+    constexpr int NS = NI * G;          // partial scores per lane
+    constexpr int NSL = NS / LPR;       // finished scores per lane
+    constexpr int NO = G * 8;           // output partials per lane
+    constexpr int NOL = NO / RPI;       // output sums per lane after the row reduction
+    static_assert(NS % LPR == 0 && NO % RPI == 0, "shape");
+    __shared__ float S[G][GQ_CH];
     __shared__ float stat[G][2];
-    __shared__ int s_last;
+    __shared__ float part[4][G][D];
     const int split = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int kl = lane % LPR, kr = lane / LPR;
     int64_t L = a.len.of(b);
     if (L > a.lmax) L = a.lmax;
-    const int64_t p0 = (int64_t)split * DEC_C;
+    const int64_t p0 = (int64_t)split * GQ_CH;
     if (p0 >= L) return;  // inactive split (uniform per workgroup)
-    const int nact = (int)((L + DEC_C - 1) / DEC_C);
     const int hq = a.hkv * G;
-    const KVT* kb = reinterpret_cast<const KVT*>(a.k) + (int64_t)b * a.kv_bstride + (int64_t)h * a.lmax * D;
-    const KVT* vb = reinterpret_cast<const KVT*>(a.v) + (int64_t)b * a.kv_bstride + (int64_t)h * a.lmax * D;
+    const __half* kb = reinterpret_cast<const __half*>(a.k) + (int64_t)b * a.kv_bstride + (int64_t)h * a.lmax * D;
+    const __half* vb = reinterpret_cast<const __half*>(a.v) + (int64_t)b * a.kv_bstride + (int64_t)h * a.lmax * D;
 
-    // K row of this lane's position and the V slices of its P.V positions, requested first
-    const int64_t pk = p0 + lane;
-    const bool kvalid = pk < L;
-    const int64_t pkc = kvalid ? pk : L - 1;
-    uint4 kraw[KC];
+    uint4 kraw[NI], vraw[NI];
+    const int64_t pw = p0 + wave * GQ_PW + kr;  // this lane's row of instruction 0
 #pragma unroll
-    for (int c = 0; c < KC; c++) kraw[c] = reinterpret_cast<const uint4*>(kb + pkc * D)[c];
-    const int slot = lane & 7, dg = lane >> 3;
-    uint4 vraw[8][DL / 8];
-#pragma unroll
-    for (int j = 0; j < 8; j++) {
-        int64_t pv = p0 + slot + 8 * j;
-        pv = pv < L ? pv : L - 1;
-#pragma unroll
-        for (int c = 0; c < DL / 8; c++) vraw[j][c] = reinterpret_cast<const uint4*>(vb + pv * D + dg * DL)[c];
+    for (int i = 0; i < NI; i++) {
+        int64_t p = pw + i * RPI;
+        p = p < L ? p : L - 1;
+        kraw[i] = *reinterpret_cast<const uint4*>(kb + p * D + kl * 8);
     }
-    // q rows of this wavefront's heads -> LDS
-    const float* qg = a.q + ((int64_t)b * hq + h * G + wave * HPW) * D;
-    for (int i = lane; i < HPW * D / 4; i += 64)
-        *reinterpret_cast<float4*>(&qsh[wave * HPW][0] + 4 * i) = reinterpret_cast<const float4*>(qg)[i];
-    __syncthreads();
+#pragma unroll
+    for (int i = 0; i < NI; i++) {
+        int64_t p = pw + i * RPI;
+        p = p < L ? p : L - 1;
+        vraw[i] = *reinterpret_cast<const uint4*>(vb + p * D + kl * 8);
+    }
+    float q[G][8];
+#pragma unroll
+    for (int g = 0; g < G; g++) {
+        const float* qp = a.q + ((int64_t)b * hq + h * G + g) * D + kl * 8;
+        const float4 t0 = reinterpret_cast<const float4*>(qp)[0], t1 = reinterpret_cast<const float4*>(qp)[1];
+        q[g][0] = t0.x; q[g][1] = t0.y; q[g][2] = t0.z; q[g][3] = t0.w;
+        q[g][4] = t1.x; q[g][5] = t1.y; q[g][6] = t1.z; q[g][7] = t1.w;
+    }
 
-    // scores of this lane's position for the wavefront's heads
-    float s[HPW];
+    // scores
+    {
+        float sc[NS];
 #pragma unroll
-    for (int hh = 0; hh < HPW; hh++) s[hh] = 0.f;
+        for (int i = 0; i < NI; i++) {
+            float kf[8];
+            cvt8<__half>(kraw[i], kf);
 #pragma unroll
-    for (int c = 0; c < KC; c++) {
-        float kf[8];
-        cvt8<KVT>(kraw[c], kf);
+            for (int g = 0; g < G; g++) {
+                float t = 0.f;
 #pragma unroll
-        for (int hh = 0; hh < HPW; hh++) {
-            const float4 q0 = *reinterpret_cast<const float4*>(&qsh[wave * HPW + hh][8 * c]);
-            const float4 q1 = *reinterpret_cast<const float4*>(&qsh[wave * HPW + hh][8 * c + 4]);
-            float t = s[hh];
-            t = fmaf(q0.x, kf[0], t);
-            t = fmaf(q0.y, kf[1], t);
-            t = fmaf(q0.z, kf[2], t);
-            t = fmaf(q0.w, kf[3], t);
-            t = fmaf(q1.x, kf[4], t);
-            t = fmaf(q1.y, kf[5], t);
-            t = fmaf(q1.z, kf[6], t);
-            t = fmaf(q1.w, kf[7], t);
-            s[hh] = t;
+                for (int e = 0; e < 8; e++) t = fmaf(q[g][e], kf[e], t);
+                sc[i * G + g] = t;
+            }
+        }
+        tr_halve<LPR / 2, 1, NS / 2, NS, false>(sc, lane);
+#pragma unroll
+        for (int j = 0; j < NSL; j++) {
+            const int f = kl * NSL + j, i = f / G, g = f % G;
+            const int pl = wave * GQ_PW + i * RPI + kr;  // position within the split
+            S[g][pl] = p0 + pl < L ? sc[j] * a.scale : -INFINITY;
         }
     }
-    // softmax over the split's positions, per head
-    float mh[HPW], lh[HPW];
-#pragma unroll
-    for (int hh = 0; hh < HPW; hh++) {
-        const float sc = kvalid ? s[hh] * a.scale : -INFINITY;
-        const float m = wave_max64(sc);
-        const float e = kvalid ? expf(sc - m) : 0.f;
-        mh[hh] = m;
-        lh[hh] = wave_sum64(e);
-        P[wave * HPW + hh][lane] = e;
-    }
     __syncthreads();
-    // P.V over the split: lane (dg, slot) takes positions slot + 8j
-    float o[HPW][DL];
+    // softmax statistics of the split, one wavefront per head
+    for (int g = wave; g < G; g += 4) {
+        constexpr int PL = GQ_CH / 64;  // positions per lane
+        float sv[PL], mx = -INFINITY;
 #pragma unroll
-    for (int hh = 0; hh < HPW; hh++)
+        for (int u = 0; u < PL; u++) {
+            sv[u] = S[g][lane + 64 * u];
+            mx = fmaxf(mx, sv[u]);
+        }
+        const float m = wave_max64(mx);  // position p0 is always valid: m is finite
+        float es = 0.f;
 #pragma unroll
-        for (int i = 0; i < DL; i++) o[hh][i] = 0.f;
-#pragma unroll
-    for (int j = 0; j < 8; j++) {
-        float vf[DL];
-#pragma unroll
-        for (int c = 0; c < DL / 8; c++) cvt8<KVT>(vraw[j][c], vf + 8 * c);
-#pragma unroll
-        for (int hh = 0; hh < HPW; hh++) {
-            const float e = P[wave * HPW + hh][slot + 8 * j];
-#pragma unroll
-            for (int i = 0; i < DL; i++) o[hh][i] = fmaf(e, vf[i], o[hh][i]);
+        for (int u = 0; u < PL; u++) {
+            sv[u] = expf(sv[u] - m);
+            S[g][lane + 64 * u] = sv[u];
+            es += sv[u];
+        }
+        const float l = wave_sum64(es);
+        if (lane == 0) {
+            stat[g][0] = m;
+            stat[g][1] = l;
         }
     }
+    __syncthreads();
+    // P.V for this lane's rows and all heads
+    float o[NO];
 #pragma unroll
-    for (int hh = 0; hh < HPW; hh++)
+    for (int j = 0; j < NO; j++) o[j] = 0.f;
 #pragma unroll
-        for (int i = 0; i < DL; i++) o[hh][i] = sum8_dpp(o[hh][i]);
-
-    // a single split normalises and stores directly (with FUSED: a single active split)
-    if (FUSED ? nact == 1 : a.nsplit == 1) {
-        if (slot == 0) {
+    for (int i = 0; i < NI; i++) {
+        float vf[8];
+        cvt8<__half>(vraw[i], vf);
+        const int pl = wave * GQ_PW + i * RPI + kr;
 #pragma unroll
-            for (int hh = 0; hh < HPW; hh++)
+        for (int g = 0; g < G; g++) {
+            const float e = S[g][pl];
 #pragma unroll
-                for (int i = 0; i < DL; i++)
-                    a.out[((int64_t)b * hq + h * G + wave * HPW + hh) * D + dg * DL + i] = o[hh][i] / lh[hh];
+            for (int d = 0; d < 8; d++) o[g * 8 + d] = fmaf(e, vf[d], o[g * 8 + d]);
+        }
+    }
+    tr_halve<32, LPR, NO / 2, NO, true>(o, lane);
+#pragma unroll
+    for (int j = 0; j < NOL; j++) {
+        const int f = kr * NOL + j, g = f / 8, d = f % 8;
+        part[wave][g][kl * 8 + d] = o[j];
+    }
+    __syncthreads();
+    if (a.nsplit == 1) {
+        for (int idx = tid; idx < G * D; idx += 256) {
+            const int g = idx / D, d = idx % D;
+            const float v = (part[0][g][d] + part[1][g][d]) + (part[2][g][d] + part[3][g][d]);
+            a.out[((int64_t)b * hq + h * G + g) * D + d] = v / stat[g][1];
         }
         return;
     }
-    const int64_t rec0 = (((int64_t)b * a.hkv + h) * a.nsplit) * G * (D + 2);
-    float* wr = a.ws + rec0 + (int64_t)split * G * (D + 2);
-    if (slot == 0) {
-#pragma unroll
-        for (int hh = 0; hh < HPW; hh++)
-#pragma unroll
-            for (int i = 0; i < DL; i++) wr[(wave * HPW + hh) * (D + 2) + dg * DL + i] = o[hh][i];
+    float* wr = a.ws + (((int64_t)b * a.hkv + h) * a.nsplit + split) * G * (D + 2);
+    for (int idx = tid; idx < G * D; idx += 256) {
+        const int g = idx / D, d = idx % D;
+        wr[g * (D + 2) + d] = (part[0][g][d] + part[1][g][d]) + (part[2][g][d] + part[3][g][d]);
     }
-    if (lane == 0) {
-#pragma unroll
-        for (int hh = 0; hh < HPW; hh++) {
-            wr[(wave * HPW + hh) * (D + 2) + D] = mh[hh];
-            wr[(wave * HPW + hh) * (D + 2) + D + 1] = lh[hh];
-        }
+    if (tid < G) {
+        wr[tid * (D + 2) + D] = stat[tid][0];
+        wr[tid * (D + 2) + D + 1] = stat[tid][1];
     }
-    if constexpr (!FUSED) return;
-    __syncthreads();
-    if (tid == 0) {
-        __threadfence();  // this split's record is visible device-wide before it is counted
-        const int prev = atomicAdd(counter + (int64_t)b * a.hkv + h, 1);
-        s_last = prev == nact - 1;
-    }
-    __syncthreads();
-    if (!s_last) return;
-    __threadfence();  // acquire: observe the other splits' records
-    // merge: every load is issued before any is consumed (one memory round trip)
-    constexpr int OPT = G * D / 256;  // outputs per thread
-    __shared__ float sm[G][DEC_MAX_FUSED], sf[G][DEC_MAX_FUSED], sden[G];
-    const int64_t stride = (int64_t)G * (D + 2);
-    const float* r0 = a.ws + rec0;
-    float ov[OPT][DEC_MAX_FUSED];
-#pragma unroll
-    for (int u = 0; u < OPT; u++) {
-        const int idx = tid + u * 256, g = idx / D, d = idx % D;
-#pragma unroll
-        for (int sp = 0; sp < DEC_MAX_FUSED; sp++)
-            if (sp < nact) ov[u][sp] = r0[sp * stride + g * (D + 2) + d];
-    }
-    for (int idx = tid; idx < G * nact; idx += 256) {
-        const int g = idx / nact, sp = idx % nact;
-        sm[g][sp] = r0[sp * stride + g * (D + 2) + D];
-        sf[g][sp] = r0[sp * stride + g * (D + 2) + D + 1];
-    }
-    __syncthreads();
-    for (int g = wave; g < G; g += 4) {  // per head: M, weights e^(m_s - M), denominator
-        const float mv = lane < nact ? sm[g][lane] : -INFINITY;
-        const float M = wave_max64(mv);
-        const float f = lane < nact ? expf(mv - M) : 0.f;
-        const float den = wave_sum64(lane < nact ? sf[g][lane] * f : 0.f);
-        if (lane < nact) sm[g][lane] = f;
-        if (lane == 0) sden[g] = den;
-    }
-    __syncthreads();
-#pragma unroll
-    for (int u = 0; u < OPT; u++) {
-        const int idx = tid + u * 256, g = idx / D, d = idx % D;
-        float num = 0.f;
-#pragma unroll
-        for (int sp = 0; sp < DEC_MAX_FUSED; sp++)
-            if (sp < nact) num = fmaf(ov[u][sp], sm[g][sp], num);
-        a.out[((int64_t)b * hq + h * G + g) * D + d] = num / sden[g];
-    }
-    if (tid == 0) counter[(int64_t)b * a.hkv + h] = 0;  // ready for the next launch
 }
 
 // ---- short-cache form: one workgroup per (query head, batch item) ------------------------
@@ -734,39 +722,132 @@ static int attn_dispatch(const AttnArgs& a, int B, int hq, int D, hipStream_t s)
     return TL_HIP_ERR_ARG;
 }
 
-// Decode form (f16 cache, D in {64, 128}, 4 or 8 query heads per KV head, 64-position
-// splits).  counter != nullptr: in-kernel merge (B * hkv zeroed ints); else k_attn_merge.
-// Returns TL_HIP_ERR_ARG (no launch) for shapes the form does not cover.
-int launch_attention_dec(const float* q, const void* k, const void* v, float* out, float* ws,
-                         int32_t* counter, int B, int hq, int hkv, int D, int64_t lmax,
-                         int64_t kv_bstride, int64_t L, const int32_t* len_dev, int len_add,
-                         int len_step, int nsplit, float scale, hipStream_t s) {
+// Merge of the split records of one (batch, kv head, query head): 256 threads = D/4 float4
+// columns x (1024 / D) split groups.  Every thread requests the o, max and sum entries of its
+// splits at once (one memory round trip), the global max and the sums over split groups go
+// through LDS.  out = sum_s o_s e^(m_s - M) / sum_s l_s e^(m_s - M).
+template <int D, int G>
+__global__ __launch_bounds__(256) void k_attn_merge_gq(AttnArgs a) {
+    constexpr int NC = D / 4, NG = 256 / NC;  // float4 columns, split groups
+    constexpr int U = 8;                       // splits per thread held in registers
+    __shared__ float4 acc[NG][NC];
+    __shared__ float smax[NG], sden[NG];
+    const int h = blockIdx.x, b = blockIdx.y, g = blockIdx.z, tid = threadIdx.x;
+    const int col = tid % NC, grp = tid / NC;
+    int64_t L = a.len.of(b);
+    if (L > a.lmax) L = a.lmax;
+    const int nact = (int)((L + a.chunk - 1) / a.chunk);
+    const int64_t stride = (int64_t)G * (D + 2);
+    const float* base = a.ws + (((int64_t)b * a.hkv + h) * a.nsplit) * stride + g * (D + 2);
+    float M = -INFINITY;
+    float4 num = make_float4(0.f, 0.f, 0.f, 0.f);
+    float den = 0.f;
+    // this thread's splits: grp, grp + NG, ... in passes of U (one pass up to U * NG splits)
+    for (int s0 = grp; s0 < nact; s0 += U * NG) {
+        float4 ov[U];
+        float mv[U], lv[U];
+#pragma unroll
+        for (int u = 0; u < U; u++) {
+            const int sp = s0 + u * NG;
+            if (sp < nact) {
+                ov[u] = *reinterpret_cast<const float4*>(base + sp * stride + 4 * col);
+                mv[u] = base[sp * stride + D];
+                lv[u] = base[sp * stride + D + 1];
+            } else {
+                ov[u] = make_float4(0.f, 0.f, 0.f, 0.f);
+                mv[u] = -INFINITY;
+                lv[u] = 0.f;
+            }
+        }
+        float mp = M;
+#pragma unroll
+        for (int u = 0; u < U; u++) mp = fmaxf(mp, mv[u]);
+        const float r = M == -INFINITY ? 0.f : expf(M - mp);  // rescale the earlier passes
+        num.x *= r;
+        num.y *= r;
+        num.z *= r;
+        num.w *= r;
+        den *= r;
+#pragma unroll
+        for (int u = 0; u < U; u++) {
+            const float w = mv[u] == -INFINITY ? 0.f : expf(mv[u] - mp);
+            num.x = fmaf(ov[u].x, w, num.x);
+            num.y = fmaf(ov[u].y, w, num.y);
+            num.z = fmaf(ov[u].z, w, num.z);
+            num.w = fmaf(ov[u].w, w, num.w);
+            den = fmaf(lv[u], w, den);
+        }
+        M = mp;
+    }
+    if (col == 0) smax[grp] = M;
+    __syncthreads();
+    float Mall = -INFINITY;
+#pragma unroll
+    for (int q = 0; q < NG; q++) Mall = fmaxf(Mall, smax[q]);
+    const float r = M == -INFINITY ? 0.f : expf(M - Mall);  // groups without splits add nothing
+    acc[grp][col] = make_float4(num.x * r, num.y * r, num.z * r, num.w * r);
+    if (col == 0) sden[grp] = den * r;
+    __syncthreads();
+    if (grp == 0) {
+        float4 t = acc[0][col];
+        float dd = sden[0];
+#pragma unroll
+        for (int q = 1; q < NG; q++) {
+            const float4 v = acc[q][col];
+            t.x += v.x;
+            t.y += v.y;
+            t.z += v.z;
+            t.w += v.w;
+            dd += sden[q];
+        }
+        const float rd = 1.0f / dd;
+        const int hq = a.hkv * G;
+        float4* o = reinterpret_cast<float4*>(a.out + ((int64_t)b * hq + h * G + g) * D) + col;
+        *o = make_float4(t.x * rd, t.y * rd, t.z * rd, t.w * rd);
+    }
+}
+
+// Grouped-query split form + merge; shapes as attention_gq_supported.  nsplit = splits of
+// 128 positions the grid covers (attention_gq_splits of the longest length); ws holds
+// 2 * nsplit records, since the launch halves the split size when the grid would be small.
+int launch_attention_gq(const float* q, const void* k, const void* v, float* out, float* ws, int B, int hq,
+                        int hkv, int D, int64_t lmax, int64_t kv_bstride, int64_t L, const int32_t* len_dev,
+                        int len_add, int len_step, int nsplit, float scale, hipStream_t s) {
     const int G = hq / hkv;
+    if (nsplit < 1 || nsplit > ATT_MAX_SPLITS) {
+        set_error(TL_HIP_ERR_ARG, "ArgumentError: %d attention splits outside 1..%d", nsplit, ATT_MAX_SPLITS);
+        return TL_HIP_ERR_ARG;
+    }
+    // 32 positions per wavefront, or 16 when that leaves fewer than ~2 workgroups per CU
+    const int pw = (int64_t)B * hkv * nsplit >= 512 ? 32 : 16;
+    if (pw == 16) nsplit *= 2;
     if (nsplit > ATT_MAX_SPLITS) {
         set_error(TL_HIP_ERR_ARG, "ArgumentError: %d attention splits exceed %d", nsplit, ATT_MAX_SPLITS);
         return TL_HIP_ERR_ARG;
     }
-    AttnArgs a{q, k, v, out, ws, hkv, lmax, kv_bstride, AttnLen{L, len_dev, len_add, len_step},
-               DEC_C, nsplit, scale};
+    AttnArgs a{q, k, v, out, ws, hkv, lmax, kv_bstride, AttnLen{L, len_dev, len_add, len_step}, 4 * pw, nsplit,
+               scale};
     dim3 grid(nsplit, hkv, B);
-#define TLH_DEC(DD, GG)                                                                            \
-    if (D == DD && G == GG) {                                                                      \
-        if (counter && nsplit <= DEC_MAX_FUSED) {                                                  \
-            k_attn_dec<DD, GG, true><<<grid, 256, 0, s>>>(a, counter);                             \
-        } else {                                                                                   \
-            k_attn_dec<DD, GG, false><<<grid, 256, 0, s>>>(a, nullptr);                            \
-            if (nsplit > 1) k_attn_merge<DD, GG><<<dim3(hkv, B), 256, 0, s>>>(a);                   \
-        }                                                                                          \
-        hipError_t e = hipGetLastError();                                                          \
-        return e == hipSuccess ? TL_HIP_OK : hip_fail(e, "attention launch");                      \
+#define TLH_GQ(DD, GG)                                                                   \
+    if (D == DD && G == GG) {                                                            \
+        if (pw == 32) k_attn_gq<DD, GG, 32><<<grid, 256, 0, s>>>(a);                     \
+        else k_attn_gq<DD, GG, 16><<<grid, 256, 0, s>>>(a);                              \
+        if (nsplit > 1) k_attn_merge_gq<DD, GG><<<dim3(hkv, B, GG), 256, 0, s>>>(a);     \
+        hipError_t e = hipGetLastError();                                                \
+        return e == hipSuccess ? TL_HIP_OK : hip_fail(e, "attention launch");            \
     }
-    TLH_DEC(64, 4) TLH_DEC(64, 8) TLH_DEC(128, 4) TLH_DEC(128, 8)
-#undef TLH_DEC
-    set_error(TL_HIP_ERR_ARG, "ArgumentError: decode attention form needs D 64/128 and 4 or 8 heads per KV head");
+    TLH_GQ(64, 4) TLH_GQ(64, 8) TLH_GQ(128, 4) TLH_GQ(128, 8)
+#undef TLH_GQ
+    set_error(TL_HIP_ERR_ARG, "ArgumentError: grouped-query attention covers head_dim 64 / 128 with 4 or 8 "
+              "query heads per KV head (got D=%d, group %d)", D, G);
     return TL_HIP_ERR_ARG;
 }
 
-bool attention_dec_supported(int kv_dtype, int hq, int hkv, int D) {
+// Splits of 128 positions covering L; the launch may halve the split size (the workspace
+// must then hold twice as many records: attn_workspace_floats(..., 2 * nsplit)).
+int attention_gq_splits(int64_t L) { return (int)cdiv(L, 128); }
+
+bool attention_gq_supported(int kv_dtype, int hq, int hkv, int D) {
     const int G = hkv > 0 ? hq / hkv : 0;
     return kv_dtype == TL_HIP_F16 && (D == 64 || D == 128) && (G == 4 || G == 8) && hq == G * hkv;
 }
@@ -833,25 +914,25 @@ extern "C" tl_hip_tensor* tl_hip_attention_decode(const tl_hip_tensor* qh, const
         set_error(TL_HIP_ERR_ARG, "ArgumentError: batch or head count too large");
         return nullptr;
     }
-    const bool dec = attention_dec_supported(k->dtype, (int)hq, (int)hkv, (int)D);
+    const bool dec = attention_gq_supported(k->dtype, (int)hq, (int)hkv, (int)D);
     int chunk, nsplit;
     attn_plan((int)B, (int)hkv, L, &chunk, &nsplit);
     if (dec) {
-        chunk = DEC_C;
-        nsplit = (int)cdiv(L, DEC_C);
+        chunk = 128;
+        nsplit = attention_gq_splits(L);
     }
     int64_t oshape[3] = {B, hq, D};
     Tensor* o = tensor_alloc(oshape, 3);
     if (!o) return nullptr;
     hipStream_t s = cur_stream();
-    float* ws = (float*)dev_alloc(attn_workspace_floats((int)B, (int)hkv, (int)(hq / hkv), (int)D, nsplit) * 4);
+    float* ws = (float*)dev_alloc(attn_workspace_floats((int)B, (int)hkv, (int)(hq / hkv), (int)D, 2 * nsplit) * 4);
     int rc = ws ? TL_HIP_OK : TL_HIP_ERR_ALLOC;
     if (rc == TL_HIP_OK && L <= 1024 && attention_qh_supported(k->dtype, (int)D))
         rc = launch_attention_qh(q->f32(), k->data, v->data, k->dtype, o->f32(), (int)B, (int)hq, (int)hkv, (int)D,
                                  lmax, hkv * lmax * D, L, nullptr, 0, 0, scale, s);
     else if (rc == TL_HIP_OK && dec)
-        rc = launch_attention_dec(q->f32(), k->data, v->data, o->f32(), ws, nullptr, (int)B, (int)hq, (int)hkv,
-                                  (int)D, lmax, hkv * lmax * D, L, nullptr, 0, 0, nsplit, scale, s);
+        rc = launch_attention_gq(q->f32(), k->data, v->data, o->f32(), ws, (int)B, (int)hq, (int)hkv, (int)D, lmax,
+                                 hkv * lmax * D, L, nullptr, 0, 0, nsplit, scale, s);
     else if (rc == TL_HIP_OK)
         rc = launch_attention(q->f32(), k->data, v->data, k->dtype, o->f32(), ws, (int)B, (int)hq, (int)hkv,
                               (int)D, lmax, hkv * lmax * D, L, nullptr, 0, 0, chunk, nsplit, scale, s);

@@ -163,13 +163,15 @@ int launch_attention(const float* q, const void* k, const void* v, int kv_dtype,
                      float* ws, int B, int hq, int hkv, int D, int64_t lmax,
                      int64_t kv_bstride, int64_t L, const int32_t* len_dev, int len_add,
                      int len_step, int chunk, int nsplit, float scale, hipStream_t s);
-// Decode form (f16 cache, D 64/128, 4 or 8 query heads per KV head, 64-position splits);
-// counter (B * hkv ints, zero between launches) selects the in-kernel merge.
-int launch_attention_dec(const float* q, const void* k, const void* v, float* out, float* ws,
-                         int32_t* counter, int B, int hq, int hkv, int D, int64_t lmax,
-                         int64_t kv_bstride, int64_t L, const int32_t* len_dev, int len_add,
-                         int len_step, int nsplit, float scale, hipStream_t s);
-bool attention_dec_supported(int kv_dtype, int hq, int hkv, int D);
+// Shapes of the grouped-query split form: f16 cache, D 64 / 128, 4 or 8 query heads per KV head.
+bool attention_gq_supported(int kv_dtype, int hq, int hkv, int D);
+// Grouped-query split form (shapes of attention_gq_supported): one workgroup per split of
+// 128 (or 64) positions, KV head and batch item, then the split merge; nsplit =
+// attention_gq_splits of the longest length, ws sized for 2 * nsplit records.
+int launch_attention_gq(const float* q, const void* k, const void* v, float* out, float* ws, int B, int hq,
+                        int hkv, int D, int64_t lmax, int64_t kv_bstride, int64_t L, const int32_t* len_dev,
+                        int len_add, int len_step, int nsplit, float scale, hipStream_t s);
+int attention_gq_splits(int64_t L);
 // Short-cache form: one workgroup per (query head, batch item); shapes: attention_qh_supported.
 bool attention_qh_supported(int kv_dtype, int D);
 int launch_attention_qh(const float* q, const void* k, const void* v, int kv_dtype, float* out,

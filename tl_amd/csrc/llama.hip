@@ -130,7 +130,6 @@ struct Llama {
     // greedy-argmax candidates of the LM-head matvec (one per workgroup)
     float* am_v = nullptr;
     int32_t *am_i = nullptr, *am_nan = nullptr;
-    int32_t* att_cnt = nullptr;  // decode attention arrival counters [KV], zero between steps
     int max_out = 0;
     int64_t host_pos = 0;
     hipGraphExec_t graph = nullptr;
@@ -181,8 +180,9 @@ static int ensure_tokens(Llama* m, int64_t n) {
     m->gu = (float*)dev_alloc(n * std::max(2 * (int64_t)m->F, qkv_w) * 4);  // also the q|k|v segment staging
     m->act = (float*)dev_alloc(n * (int64_t)m->F * 4);
     m->ids = (int32_t*)dev_alloc(n * 4);
-    // attention workspace: B = n queries, 64-position chunks over max_seq
-    int nsplit = (int)cdiv(m->max_seq, 64);
+    // attention workspace: B = n queries, splits of 64 positions over max_seq (the grouped-query
+    // kernel's smallest split; 128-position splits use half of it)
+    int nsplit = 2 * (int)cdiv(m->max_seq, 128);
     m->ws_floats = attn_workspace_floats((int)n, m->KV, m->H / m->KV, m->hd, nsplit);
     m->ws = (float*)dev_alloc(m->ws_floats * 4);
     for (float** b : bufs)
@@ -321,9 +321,10 @@ static int enqueue_forward(Llama* m, int n, int f16, hipStream_t s) {
                                                             m->cos_t, m->sin_t, m->pos, n, m->H, m->KV, (int)hd,
                                                             m->max_seq, m->rope_per_token);
         // query i (absolute position pos + i) attends cache positions 0 .. pos + i
-        if (attention_dec_supported(m->kv_f16 ? TL_HIP_F16 : TL_HIP_F32, m->H, m->KV, (int)hd))
-            rc = launch_attention_dec(m->q, m->kc[l], m->vc[l], m->ao, m->ws, nullptr, n, m->H, m->KV, (int)hd,
-                                      m->max_seq, 0, 0, m->pos, 1, 1, nsplit, 1.0f / sqrtf((float)hd), s);
+        if (attention_gq_supported(m->kv_f16 ? TL_HIP_F16 : TL_HIP_F32, m->H, m->KV, (int)hd))
+            rc = launch_attention_gq(m->q, m->kc[l], m->vc[l], m->ao, m->ws, n, m->H, m->KV, (int)hd, m->max_seq, 0,
+                                     0, m->pos, 1, 1, attention_gq_splits(m->host_pos + n),
+                                     1.0f / sqrtf((float)hd), s);
         else
             rc = launch_attention(m->q, m->kc[l], m->vc[l], m->kv_f16 ? TL_HIP_F16 : TL_HIP_F32, m->ao, m->ws, n,
                                   m->H, m->KV, (int)hd, m->max_seq, 0, 0, m->pos, 1, 1, 64, nsplit,
@@ -390,9 +391,9 @@ static int enqueue_step(Llama* m, float penalty, hipStream_t s) {
         if (m->max_seq <= 4096 && attention_qh_supported(m->kv_f16 ? TL_HIP_F16 : TL_HIP_F32, (int)hd))
             rc = launch_attention_qh(m->q, m->kc[l], m->vc[l], m->kv_f16 ? TL_HIP_F16 : TL_HIP_F32, m->ao, 1, m->H,
                                      m->KV, (int)hd, m->max_seq, 0, 0, m->pos, 1, 0, 1.0f / sqrtf((float)hd), s);
-        else if (attention_dec_supported(m->kv_f16 ? TL_HIP_F16 : TL_HIP_F32, m->H, m->KV, (int)hd))
-            rc = launch_attention_dec(m->q, m->kc[l], m->vc[l], m->ao, m->ws, m->att_cnt, 1, m->H, m->KV, (int)hd,
-                                      m->max_seq, 0, 0, m->pos, 1, 0, nsplit, 1.0f / sqrtf((float)hd), s);
+        else if (attention_gq_supported(m->kv_f16 ? TL_HIP_F16 : TL_HIP_F32, m->H, m->KV, (int)hd))
+            rc = launch_attention_gq(m->q, m->kc[l], m->vc[l], m->ao, m->ws, 1, m->H, m->KV, (int)hd, m->max_seq, 0,
+                                     0, m->pos, 1, 0, attention_gq_splits(m->max_seq), 1.0f / sqrtf((float)hd), s);
         else
             rc = launch_attention(m->q, m->kc[l], m->vc[l], m->kv_f16 ? TL_HIP_F16 : TL_HIP_F32, m->ao, m->ws, 1,
                                   m->H, m->KV, (int)hd, m->max_seq, 0, 0, m->pos, 1, 0, 64, nsplit,
@@ -493,12 +494,9 @@ tl_hip_llama* tl_hip_llama_new(int n_layers, int d_model, int n_heads, int n_kv_
     m->am_v = (float*)dev_alloc((size_t)parts * 4);
     m->am_i = (int32_t*)dev_alloc((size_t)parts * 4);
     m->am_nan = (int32_t*)dev_alloc((size_t)parts * 4);
-    m->att_cnt = (int32_t*)dev_alloc((size_t)n_kv_heads * 4);
     int rc = (m->cos_t && m->sin_t && m->logits && m->plogits && m->pos && m->tok && m->step && m->seen &&
-              m->am_v && m->am_i && m->am_nan && m->att_cnt)
+              m->am_v && m->am_i && m->am_nan)
                  ? TL_HIP_OK : TL_HIP_ERR_ALLOC;
-    if (rc == TL_HIP_OK && hipMemsetAsync(m->att_cnt, 0, (size_t)n_kv_heads * 4, s) != hipSuccess)
-        rc = hip_fail(hipGetLastError(), "hipMemsetAsync(counters)");
     if (rc == TL_HIP_OK) rc = launch_rope_table(m->cos_t, max_seq, m->hd, rope_theta, 0, s);
     if (rc == TL_HIP_OK) rc = launch_rope_table(m->sin_t, max_seq, m->hd, rope_theta, 1, s);
     if (rc == TL_HIP_OK) rc = alloc_kv(m);
@@ -534,7 +532,7 @@ int tl_hip_llama_free(tl_hip_llama* h) {
     for (void* p : m->vc) dev_free(p);
     void* bufs[] = {m->out_norm, m->emb, m->cos_t, m->sin_t, m->x, m->h, m->qkv, m->q, m->ao, m->t, m->gu,
                     m->act, m->logits, m->plogits, m->ws, m->ids, m->pos, m->tok, m->step, m->out_ids, m->seen,
-                    m->am_v, m->am_i, m->am_nan, m->att_cnt};
+                    m->am_v, m->am_i, m->am_nan};
     for (void* p : bufs) dev_free(p);
     delete m;
     return TL_HIP_OK;
