@@ -157,18 +157,22 @@ __global__ __launch_bounds__(256) void k_qgemm_f32(QView qv, const float* __rest
 // and receives C[4*(l/16) .. +3][l % 16].
 //
 // X is first converted to f16 once (k_x_to_f16q), with every 32-element block stored in the
-// k order of the MFMA operands below.  Workgroup tile BM (x rows) x BN (weight rows), 4
-// wavefronts in a 2 x 2 grid, each owning (BM/2) x (BN/2).  One iteration covers 128 k =
-// 4 quant blocks with 4 MFMAs per 16 x 16 output tile; in MFMA t, lane group g (lanes
-// 16g .. 16g+15) supplies block kb+g's values held in word t of its quant data.
+// k order of the MFMA operands below.  Workgroup tile BM (x rows) x BN (weight rows), eight
+// wavefronts: four (BM/2) x (BN/2) output sub-tiles in a 2 x 2 grid, each held by two
+// wavefronts that split an iteration's k-steps and add their sums once at the end (two
+// wavefronts per SIMD: with one, the MFMA and LDS latencies of a single instruction stream
+// stay exposed).  One iteration covers 128 k = 4 quant blocks with 4 MFMAs per 16 x 16
+// output tile; in MFMA t, lane group g (lanes 16g .. 16g+15) supplies block kb+g's values
+// held in word t of its quant data.
 //   * X rows, W quant chunks and W scales reach LDS by global_load_lds (no VGPR staging),
 //     double-buffered, with the next iteration's loads in flight during the MFMAs;
 //   * each lane turns its W word t into the f16 operand of MFMA t in registers (Q4_0: fp8
 //     reinterpretation of the nibble bytes, Q8_0: the 0x6400 magic), times the block scale
 //     d with one f16 rounding (the f16 path's rounding);
 //   * the A operand is one ds_read_b128 per 16 x 32 tile.
-// Measured on MI355X: an iteration moves 37 KB per workgroup from L2 at ~456-cycle latency,
-// which bounds this tile at roughly a quarter of the MFMA peak for M = 512 problems.
+// Measured on MI355X (M = 512): the loads alone take about 60 % of the kernel time (an
+// iteration moves 37 KB per workgroup from L2), the MFMA work alone about 50 %; larger
+// tiles (64 x 128, 128 x 128) and 16-accumulator wavefronts measured slower.
 typedef _Float16 half2v __attribute__((ext_vector_type(2)));
 constexpr int Q_KR = 4;     // quant blocks per iteration
 
@@ -258,49 +262,33 @@ __device__ __forceinline__ void lds_dma4(const void* src, void* lds) {
 #endif
 }
 
-template <int QT, int BM, int BN>
-__global__ __launch_bounds__(256, 2) void k_qgemm_mfma(const uint8_t* __restrict__ qs,
-                                                       const __half* __restrict__ dsc,
-                                                       const _Float16* __restrict__ x16,
-                                                       float* __restrict__ y, int64_t m,
-                                                       int64_t n, int64_t k, int64_t nb, int mt) {
+template <int QT, int BM, int BN, int NS>  // NS pipeline stages (LDS: X + W per stage)
+__global__ __launch_bounds__(512) void k_qgemm_mfma(const uint8_t* __restrict__ qs, const __half* __restrict__ dsc,
+                                                    const _Float16* __restrict__ x16, float* __restrict__ y,
+                                                    int64_t m, int64_t n, int64_t k, int64_t nb) {
     constexpr int TM = BM / 32, TN = BN / 32;  // 16 x 16 tiles per wavefront
     constexpr int QB = QWords<QT>::BYTES;
     constexpr int QC = QB / 16;                // 16-byte chunks per quant block
     constexpr int CPR = Q_KR * QC;             // W chunks per row and iteration
     constexpr int RSH = CPR == 4 ? 2 : 1;      // W chunk swizzle: + (row >> RSH)
-    constexpr int XI = BM * 16 / 256;          // X chunks per thread per iteration
-    constexpr int WI = BN * CPR / 256;         // W chunks per thread per iteration
-    constexpr int DI = BN * Q_KR / 256;        // scales per thread per iteration
-    constexpr int NS = 2;                      // pipeline stages (LDS: X + W per stage)
-    constexpr int GI = XI + WI + DI;           // DMA instructions per thread per stage
-    static_assert(XI >= 1 && WI >= 1 && DI >= 1 && (NS - 2) * GI <= 63, "tile");
+    constexpr int XI = BM * 16 / 512;          // X chunks per thread per iteration
+    constexpr int WW = BN * CPR / 64;          // wavefronts that issue one W DMA instruction
+    constexpr int DW = BN * Q_KR / 64;         // wavefronts that issue one scale DMA instruction
+    static_assert(XI >= 1 && WW <= 8 && DW <= 8, "tile");
     // Every operand reaches LDS through global_load_lds (a wavefront's instruction writes 64
-    // consecutive LDS elements, one per lane), so no load in the main loop writes a VGPR and
-    // the pipeline is governed by one counted wait per iteration.
-    //  * X: two stages.  Row r's 16-byte chunk c (= block * 4 + word) sits at c ^ (r & 15).
-    //  * W: three stages of BN rows x CPR chunks, chunk c of row r at (c + (r >> RSH)) mod
-    //    CPR, and BN x 4 scales.  Both swizzles make the 16 lanes that read one operand
-    //    column hit 16 distinct 16-byte bank groups.
+    // consecutive LDS elements, one per lane), so no load in the main loop writes a VGPR.
+    //  * X: row r's 16-byte chunk c (= block * 4 + word) sits at c ^ (r & 15);
+    //  * W: BN rows x CPR chunks, chunk c of row r at (c + (r >> RSH)) mod CPR, and BN x 4
+    //    scales.  Both swizzles make the 16 lanes that read one operand column hit 16
+    //    distinct 16-byte bank groups.
     __shared__ __attribute__((aligned(16))) _Float16 Xs[NS][BM * 128];
     __shared__ __attribute__((aligned(16))) uint8_t Wq[NS][BN * CPR * 16];
     __shared__ __attribute__((aligned(16))) uint32_t Wd[NS][BN * Q_KR];  // aligned word holding the scale
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int wm = wave >> 1, wn = wave & 1, col = lane & 15, g = lane >> 4;
-    // Tile of this workgroup.  Workgroups are dispatched to the 8 XCDs round-robin (id % 8);
-    // with mt (M tiles) dividing 8, XCD x takes only M tile x % mt, so each XCD's L2 holds one
-    // X row band while the weight stream passes through; mt = 0 selects the plain mapping.
-    int64_t mtile, ntile;
-    if (mt > 0) {
-        const int xcd = blockIdx.x & 7, l = blockIdx.x >> 3, rep = 8 / mt;
-        mtile = xcd % mt;
-        ntile = (int64_t)l * rep + xcd / mt;
-    } else {
-        const int64_t nt = (n + BN - 1) / BN;
-        mtile = blockIdx.x / nt;
-        ntile = blockIdx.x % nt;
-    }
-    const int64_t m0 = mtile * BM, n0 = ntile * BN;
+    const int sub = wave & 3, kh = wave >> 2;  // output sub-tile, k half
+    const int wm = sub >> 1, wn = sub & 1, col = lane & 15, g = lane >> 4;
+    const int64_t nt = (n + BN - 1) / BN;
+    const int64_t m0 = (blockIdx.x / nt) * BM, n0 = (blockIdx.x % nt) * BN;
 
     floatx4 acc[TM][TN];
 #pragma unroll
@@ -309,39 +297,31 @@ __global__ __launch_bounds__(256, 2) void k_qgemm_mfma(const uint8_t* __restrict
         for (int j = 0; j < TN; j++) acc[i][j] = floatx4{0.f, 0.f, 0.f, 0.f};
 
     // Per-lane source offsets (bytes) are fixed for the whole K loop; an iteration adds one
-    // uniform advance, so each DMA issue is a scalar base plus a VGPR offset.  K is a multiple
-    // of 128 (checked at launch): no block past nb is ever addressed.
-    uint32_t xoff[XI], woff[WI], doff[DI];
+    // uniform advance.  K is a multiple of 128 (checked at launch): no block past nb is read.
+    uint32_t xoff[XI], woff = 0, doff = 0;
 #pragma unroll
     for (int u = 0; u < XI; u++) {
         const int slot = (wave * XI + u) * 64 + lane, r = slot >> 4, c = (slot & 15) ^ (r & 15);
         const int64_t row = m0 + r < m ? m0 + r : m - 1;  // rows past m feed outputs that are not stored
         xoff[u] = (uint32_t)((row * k + (c >> 2) * 32 + (c & 3) * 8) * 2);
     }
-#pragma unroll
-    for (int u = 0; u < WI; u++) {
-        const int slot = (wave * WI + u) * 64 + lane, r = slot / CPR, c = (slot % CPR - (r >> RSH)) & (CPR - 1);
+    if (wave < WW) {
+        const int slot = wave * 64 + lane, r = slot / CPR, c = (slot % CPR - (r >> RSH)) & (CPR - 1);
         const int64_t row = n0 + r < n ? n0 + r : n - 1;
-        woff[u] = (uint32_t)((row * nb + c / QC) * QB + (c % QC) * 16);
+        woff = (uint32_t)((row * nb + c / QC) * QB + (c % QC) * 16);
     }
-#pragma unroll
-    for (int u = 0; u < DI; u++) {  // the 4-byte word that holds scale (row, block)
-        const int slot = (wave * DI + u) * 64 + lane;
+    if (wave >= 8 - DW) {  // the 4-byte word that holds scale (row, block)
+        const int slot = (wave - (8 - DW)) * 64 + lane;
         const int64_t row = n0 + (slot >> 2) < n ? n0 + (slot >> 2) : n - 1;
-        doff[u] = (uint32_t)(((row * nb + (slot & 3)) >> 1) * 4);
+        doff = (uint32_t)(((row * nb + (slot & 3)) >> 1) * 4);
     }
-    auto issue_x = [&](int64_t kb, int st) {
+    auto issue = [&](int64_t kb, int st) {
         const char* src = reinterpret_cast<const char*>(x16) + kb * 64;  // 32 halves per block
 #pragma unroll
         for (int u = 0; u < XI; u++) lds_dma16(src + xoff[u], &Xs[st][(wave * XI + u) * 64 * 8]);
-    };
-    auto issue_w = [&](int64_t kb, int st) {
-        const char* src = reinterpret_cast<const char*>(qs) + kb * QB;
-#pragma unroll
-        for (int u = 0; u < WI; u++) lds_dma16(src + woff[u], &Wq[st][(wave * WI + u) * 64 * 16]);
-        const char* dsrc = reinterpret_cast<const char*>(dsc) + kb * 2;  // kb even: whole words
-#pragma unroll
-        for (int u = 0; u < DI; u++) lds_dma4(dsrc + doff[u], &Wd[st][(wave * DI + u) * 64]);
+        if (wave < WW) lds_dma16(reinterpret_cast<const char*>(qs) + kb * QB + woff, &Wq[st][wave * 64 * 16]);
+        if (wave >= 8 - DW)  // kb even: whole words
+            lds_dma4(reinterpret_cast<const char*>(dsc) + kb * 2 + doff, &Wd[st][(wave - (8 - DW)) * 64]);
     };
     uint32_t dpar[TN];  // which half of its word holds this lane's scale (kb is even)
 #pragma unroll
@@ -350,75 +330,89 @@ __global__ __launch_bounds__(256, 2) void k_qgemm_mfma(const uint8_t* __restrict
         const int64_t row = n0 + r < n ? n0 + r : n - 1;
         dpar[j] = (uint32_t)((row * nb + g) & 1) * 16;
     }
-    auto compute = [&](int xst, int wst, int64_t kb) {
+    // This wavefront's half of the iteration: k-steps t = 2 kh, 2 kh + 1.  Every LDS read
+    // (W quants, scale words, A fragments) is issued before the first use.
+    auto compute = [&](int st) {
         QRaw<QT> wr[TN];
-        half2v d2[TN], m8d2[TN];
+        uint32_t dw[TN];
 #pragma unroll
         for (int j = 0; j < TN; j++) {
             const int r = wn * (BN / 2) + 16 * j + col;
 #pragma unroll
             for (int h = 0; h < QC; h++)
-                wr[j].v[h] = *reinterpret_cast<const uint4*>(&Wq[wst][(r * CPR + ((g * QC + h + (r >> RSH)) & (CPR - 1))) * 16]);
-            const uint32_t b = (Wd[wst][r * Q_KR + g] >> dpar[j]) & 0xFFFFu;
+                wr[j].v[h] = *reinterpret_cast<const uint4*>(&Wq[st][(r * CPR + ((g * QC + h + (r >> RSH)) & (CPR - 1))) * 16]);
+            dw[j] = Wd[st][r * Q_KR + g];
+        }
+        const _Float16* xs = Xs[st];
+        half8 a[2][TM];
+#pragma unroll
+        for (int tt = 0; tt < 2; tt++)
+#pragma unroll
+            for (int i = 0; i < TM; i++)
+                a[tt][i] = *reinterpret_cast<const half8*>(xs + (wm * (BM / 2) + 16 * i + col) * 128 + ((g * 4 + 2 * kh + tt) ^ col) * 8);
+        __builtin_amdgcn_sched_barrier(0);
+        half2v d2[TN], m8d2[TN];
+#pragma unroll
+        for (int j = 0; j < TN; j++) {
+            const uint32_t b = (dw[j] >> dpar[j]) & 0xFFFFu;
             d2[j] = __builtin_bit_cast(half2v, b | (b << 16));
             m8d2[j] = d2[j] * half2v{(_Float16)-8.0f, (_Float16)-8.0f};
         }
-        const _Float16* xs = Xs[xst];
 #pragma unroll
-        for (int t = 0; t < 4; t++) {
-            half8 a[TM];
-#pragma unroll
-            for (int i = 0; i < TM; i++)
-                a[i] = *reinterpret_cast<const half8*>(xs + (wm * (BM / 2) + 16 * i + col) * 128 + ((g * 4 + t) ^ col) * 8);
+        for (int tt = 0; tt < 2; tt++) {
+            const int t = 2 * kh + tt;
 #pragma unroll
             for (int j = 0; j < TN; j++) {
                 half8 bop;
                 if constexpr (QT == TL_HIP_GGML_Q4_0) bop = QWords<QT>::operand(wr[j].v[0], t, d2[j], m8d2[j]);
                 else bop = QWords<QT>::operand(wr[j].v, t, d2[j], m8d2[j]);
 #pragma unroll
-                for (int i = 0; i < TM; i++) acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[i], bop, acc[i][j], 0, 0, 0);
+                for (int i = 0; i < TM; i++) acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[tt][i], bop, acc[i][j], 0, 0, 0);
             }
         }
     };
 
-    // NS-stage pipeline: stage it % NS holds X and W of iteration it.  Groups 0 .. NS-2 are
-    // issued up front; iteration it waits until its own group has landed (loads retire in
-    // issue order, so at most the groups of it+1 .. it+NS-2 may still be outstanding, GI
-    // instructions each), the barrier makes every wavefront's chunks visible and frees the
-    // stage iteration it-1 read, and group it+NS-1 goes into that stage.
+    // Stage it % NS holds X and W of iteration it; the loads of it + 1 .. it + NS - 1 are in
+    // flight while it computes.  The barrier after the wait makes every wavefront's chunks
+    // visible and frees the stage iteration it - 1 read.
     const int64_t iters = nb / Q_KR;
-    for (int64_t i0 = 0; i0 < NS - 1 && i0 < iters; i0++) {
-        issue_x(i0 * Q_KR, (int)i0);
-        issue_w(i0 * Q_KR, (int)i0);
-    }
+    for (int64_t i0 = 0; i0 < NS - 1 && i0 < iters; i0++) issue(i0 * Q_KR, (int)i0);
     for (int64_t it = 0; it < iters; it++) {
-        const int64_t after = iters - 1 - it < NS - 2 ? iters - 1 - it : NS - 2;  // groups issued after it
-        if (after == 2) __builtin_amdgcn_s_waitcnt(0xF70 | (2 * GI & 15) | ((2 * GI >> 4) << 14));
-        else if (after == 1) __builtin_amdgcn_s_waitcnt(0xF70 | (GI & 15) | ((GI >> 4) << 14));
-        else __builtin_amdgcn_s_waitcnt(0xF70);  // vmcnt(0); the encodings carry no lgkm / exp wait
+        __builtin_amdgcn_s_waitcnt(0xF70);  // vmcnt(0); the encoding carries no lgkm / exp wait
         __syncthreads();
         __builtin_amdgcn_sched_barrier(0);
-        if (it + NS - 1 < iters) {
-            const int st = (int)((it + NS - 1) % NS);
-            issue_x((it + NS - 1) * Q_KR, st);
-            issue_w((it + NS - 1) * Q_KR, st);
-        }
+        if (it + NS - 1 < iters) issue((it + NS - 1) * Q_KR, (int)((it + NS - 1) % NS));
         __builtin_amdgcn_sched_barrier(0);
-        const int cur = (int)(it % NS);
-        compute(cur, cur, it * Q_KR);
+        compute((int)(it % NS));
     }
+    // the k half kh = 1 hands its sums to kh = 0 through the (now free) X stages
+    static_assert(4 * TM * TN * 256 * 4 <= NS * BM * 128 * 2, "reduction space");
+    __syncthreads();
+    float* red = reinterpret_cast<float*>(&Xs[0][0]);
+    if (kh == 1) {
 #pragma unroll
-    for (int i = 0; i < TM; i++)
+        for (int i = 0; i < TM; i++)
 #pragma unroll
-        for (int j = 0; j < TN; j++) {
-            const int64_t c = n0 + wn * (BN / 2) + 16 * j + col;
+            for (int j = 0; j < TN; j++)
+                *reinterpret_cast<floatx4*>(red + ((sub * TM + i) * TN + j) * 256 + lane * 4) = acc[i][j];
+    }
+    __syncthreads();
+    if (kh == 0) {
 #pragma unroll
-            for (int e = 0; e < 4; e++) {
-                const int64_t r = m0 + wm * (BM / 2) + 16 * i + 4 * g + e;
-                if (r < m && c < n) y[r * n + c] = acc[i][j][e];
+        for (int i = 0; i < TM; i++)
+#pragma unroll
+            for (int j = 0; j < TN; j++) {
+                const floatx4 o = *reinterpret_cast<const floatx4*>(red + ((sub * TM + i) * TN + j) * 256 + lane * 4);
+                const int64_t c = n0 + wn * (BN / 2) + 16 * j + col;
+#pragma unroll
+                for (int e = 0; e < 4; e++) {
+                    const int64_t r = m0 + wm * (BM / 2) + 16 * i + 4 * g + e;
+                    if (r < m && c < n) y[r * n + c] = acc[i][j][e] + o[e];
+                }
             }
-        }
+    }
 }
+
 
 int launch_quant_gemm(const QWeight* w, const float* x, float* y, int64_t m, hipStream_t s,
                       int mode) {
@@ -445,15 +439,13 @@ int launch_quant_gemm(const QWeight* w, const float* x, float* y, int64_t m, hip
         if (!x16) return TL_HIP_ERR_ALLOC;
         const int64_t units = m * w->nb * 4;
         constexpr int BM = 128, BN = 64;
-        const int64_t mtn = cdiv(m, BM), ntn = cdiv(w->n, BN), tiles = mtn * ntn;
-        // XCD-local M tiles when mt divides 8 and the grid fills the XCDs evenly
-        const int mt = (8 % mtn == 0 && tiles % 8 == 0) ? (int)mtn : 0;
+        const int64_t tiles = cdiv(m, BM) * cdiv(w->n, BN);
         if (q4) {
             k_x_to_f16q<TL_HIP_GGML_Q4_0><<<(unsigned)cdiv(units, 256), 256, 0, s>>>(x, x16, units);
-            k_qgemm_mfma<TL_HIP_GGML_Q4_0, BM, BN><<<(unsigned)tiles, 256, 0, s>>>(w->qs, w->d, x16, y, m, w->n, w->k, w->nb, mt);
+            k_qgemm_mfma<TL_HIP_GGML_Q4_0, BM, BN, 2><<<(unsigned)tiles, 512, 0, s>>>(w->qs, w->d, x16, y, m, w->n, w->k, w->nb);
         } else {
             k_x_to_f16q<TL_HIP_GGML_Q8_0><<<(unsigned)cdiv(units, 256), 256, 0, s>>>(x, x16, units);
-            k_qgemm_mfma<TL_HIP_GGML_Q8_0, BM, BN><<<(unsigned)tiles, 256, 0, s>>>(w->qs, w->d, x16, y, m, w->n, w->k, w->nb, mt);
+            k_qgemm_mfma<TL_HIP_GGML_Q8_0, BM, BN, 2><<<(unsigned)tiles, 512, 0, s>>>(w->qs, w->d, x16, y, m, w->n, w->k, w->nb);
         }
         dev_free(x16);
     }
