@@ -330,7 +330,7 @@ def main():
         kq = {"workload": "same decoder with llama.cpp's Q4_K_M type mixture (Q4_K; Q6_K for the LM head and "
                           "attn_v / ffn_down of 11 of 22 layers)", "value": round(kq_tok_s, 2), "unit": "tok/s",
               "steps": 64, "ms_per_step": round(kq_decode_s * 1e3 / 64, 4), "prefill_ms": round(kq_prefill_s * 1e3, 2),
-              "prefill_path": "f32 GEMM (K-quant weights)"}
+              "prefill_path": "f16 MFMA GEMM, K-quant weights dequantized to f16 operand order per call"}
 
     cpu = None
     if not args.no_cpu_baseline:

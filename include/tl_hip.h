@@ -123,7 +123,8 @@ tl_hip_tensor* tl_hip_qtensor_dequantize(const tl_hip_qtensor* q);
  * m the tiled GEMM. */
 tl_hip_tensor* tl_hip_qtensor_matmul(const tl_hip_tensor* x, const tl_hip_qtensor* q);
 /* Same with the f16-MFMA prefill GEMM for m > 4 (dequant -> f16 LDS tiles -> MFMA,
- * f32 accumulate); tolerance class "f16 path".  Q4_K / Q6_K weights take the f32 GEMM. */
+ * f32 accumulate); tolerance class "f16 path".  Q4_K / Q6_K weights are first dequantized
+ * into an f16 workspace in the MFMA operand order. */
 tl_hip_tensor* tl_hip_qtensor_matmul_f16(const tl_hip_tensor* x, const tl_hip_qtensor* q);
 
 /* ---------------------------------------------------------------- GGUF files ----- */

@@ -2,8 +2,8 @@
 linear against the CPU oracle (quantized.rs:268-415 restated in oracle/), through the C ABI.
 
 max-rel-err = max_i |a_i - b_i| / max(max_j |b_j|, 1e-30); dequant bit-exact, the quantized
-linear 1e-4 (f32 accumulation; K-quant weights take the f32 GEMM for m > 4 on both entry
-points, so the f16 entry point is held to 1e-4 too)."""
+linear 1e-4 on the f32 paths and 1e-2 on the f16-MFMA prefill path (weights dequantized to
+f16 operand order, X rounded to f16)."""
 import json
 import os
 
@@ -16,7 +16,7 @@ from tl_amd.quant import random_q4_k_blocks, random_q6_k_blocks
 
 pytestmark = pytest.mark.gpu
 HERE = os.path.dirname(os.path.abspath(__file__))
-F32_TOL = 1e-4
+F32_TOL, F16_TOL = 1e-4, 1e-2
 
 
 def max_rel(a, b):
@@ -72,7 +72,7 @@ def test_kquant_matvec(dev, t, nk, m):
 
 @pytest.mark.parametrize("t", [GGML_Q4_K, GGML_Q6_K])
 @pytest.mark.parametrize("m", [5, 16, 128])
-@pytest.mark.parametrize("nk", [(4096, 4096), (1024, 11008), (300, 768)])
+@pytest.mark.parametrize("nk", [(4096, 4096), (1024, 11008), (300, 768), (2048, 5632)])
 def test_kquant_gemm(dev, t, m, nk):
     n, k = nk
     rng = np.random.default_rng(0x71560000 + m + n + t)
@@ -82,7 +82,7 @@ def test_kquant_gemm(dev, t, m, nk):
     xt = dev.tensor_new(x)
     ref = oracle.qtensor_matmul(x, raw, t, n)
     assert_rel(dev.tl_qtensor_matmul(xt, q).to_numpy(), ref, F32_TOL)
-    assert_rel(dev.tl_qtensor_matmul_f16(xt, q).to_numpy(), ref, F32_TOL)
+    assert_rel(dev.tl_qtensor_matmul_f16(xt, q).to_numpy(), ref, F16_TOL)
 
 
 def test_kquant_upload_errors(dev):

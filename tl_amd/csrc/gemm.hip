@@ -223,9 +223,11 @@ struct QWords<TL_HIP_GGML_Q8_0> {
     }
 };
 
-template <int QT>
-struct QRaw {
-    uint4 v[QWords<QT>::BYTES / 16];
+// f16 weights already in the operand order (k_dequant_f16q): block = 4 words of 8 halves,
+// word t is the operand of MFMA t as stored.
+template <>
+struct QWords<TL_HIP_GGML_F16> {
+    static constexpr int BYTES = 64;
 };
 
 // X f32 [m, k] -> f16 [m, k] with every 32-element block stored in the k-slot order of the
@@ -249,6 +251,29 @@ __global__ __launch_bounds__(256) void k_x_to_f16q(const float* __restrict__ x, 
     reinterpret_cast<half8*>(x16)[u] = h;
 }
 
+// Weights of any resident type -> f16 [n, k] in the Q4_0 operand order (unit (row, block,
+// word t) = the 8 halves of elements 4t..4t+3 and 16+4t..16+4t+3), for the MFMA GEMM of the
+// types without an in-register operand builder (Q4_K, Q6_K).  One thread per 32-weight unit;
+// each value is the exact f32 dequantization rounded once to f16.
+template <int QT>
+__global__ __launch_bounds__(256) void k_dequant_f16q(QView qv, _Float16* __restrict__ w16, int64_t units) {
+    const int64_t u = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (u >= units) return;
+    float v[32];
+    dequant_block<QT>(qv, u, v);
+    half8* o = reinterpret_cast<half8*>(w16) + u * 4;
+#pragma unroll
+    for (int t = 0; t < 4; t++) {
+        half8 h;
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+            h[e] = (_Float16)v[4 * t + e];
+            h[4 + e] = (_Float16)v[16 + 4 * t + e];
+        }
+        o[t] = h;
+    }
+}
+
 // global_load_lds: each lane's SIZE bytes from src land at lds + lane * SIZE (one 64-lane
 // instruction writes 64 consecutive elements).  The builtin exists only in the device pass.
 __device__ __forceinline__ void lds_dma16(const void* src, void* lds) {
@@ -270,11 +295,14 @@ __global__ __launch_bounds__(512) void k_qgemm_mfma(const uint8_t* __restrict__ 
     constexpr int QB = QWords<QT>::BYTES;
     constexpr int QC = QB / 16;                // 16-byte chunks per quant block
     constexpr int CPR = Q_KR * QC;             // W chunks per row and iteration
-    constexpr int RSH = CPR == 4 ? 2 : 1;      // W chunk swizzle: + (row >> RSH)
+    constexpr int RSH = CPR == 4 ? 2 : CPR == 8 ? 1 : 0;  // W chunk swizzle: + (row >> RSH)
+    constexpr bool SCALED = QT != TL_HIP_GGML_F16;   // quant blocks carry an f16 scale
     constexpr int XI = BM * 16 / 512;          // X chunks per thread per iteration
-    constexpr int WW = BN * CPR / 64;          // wavefronts that issue one W DMA instruction
-    constexpr int DW = BN * Q_KR / 64;         // wavefronts that issue one scale DMA instruction
-    static_assert(XI >= 1 && WW <= 8 && DW <= 8, "tile");
+    constexpr int WCH = BN * CPR;              // W chunks per iteration
+    constexpr int WPT = WCH >= 512 ? WCH / 512 : 1;  // W DMA instructions per issuing wavefront
+    constexpr int WW = WCH >= 512 ? 8 : WCH / 64;    // wavefronts that issue W DMA
+    constexpr int DW = SCALED ? BN * Q_KR / 64 : 0;  // wavefronts that issue one scale DMA instruction
+    static_assert(XI >= 1 && WW >= 1 && WW * WPT * 64 == WCH && DW <= 8, "tile");
     // Every operand reaches LDS through global_load_lds (a wavefront's instruction writes 64
     // consecutive LDS elements, one per lane), so no load in the main loop writes a VGPR.
     //  * X: row r's 16-byte chunk c (= block * 4 + word) sits at c ^ (r & 15);
@@ -283,7 +311,7 @@ __global__ __launch_bounds__(512) void k_qgemm_mfma(const uint8_t* __restrict__ 
     //    distinct 16-byte bank groups.
     __shared__ __attribute__((aligned(16))) _Float16 Xs[NS][BM * 128];
     __shared__ __attribute__((aligned(16))) uint8_t Wq[NS][BN * CPR * 16];
-    __shared__ __attribute__((aligned(16))) uint32_t Wd[NS][BN * Q_KR];  // aligned word holding the scale
+    __shared__ __attribute__((aligned(16))) uint32_t Wd[NS][SCALED ? BN * Q_KR : 1];  // aligned word holding the scale
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int sub = wave & 3, kh = wave >> 2;  // output sub-tile, k half
     const int wm = sub >> 1, wn = sub & 1, col = lane & 15, g = lane >> 4;
@@ -298,7 +326,7 @@ __global__ __launch_bounds__(512) void k_qgemm_mfma(const uint8_t* __restrict__ 
 
     // Per-lane source offsets (bytes) are fixed for the whole K loop; an iteration adds one
     // uniform advance.  K is a multiple of 128 (checked at launch): no block past nb is read.
-    uint32_t xoff[XI], woff = 0, doff = 0;
+    uint32_t xoff[XI], woff[WPT] = {}, doff = 0;
 #pragma unroll
     for (int u = 0; u < XI; u++) {
         const int slot = (wave * XI + u) * 64 + lane, r = slot >> 4, c = (slot & 15) ^ (r & 15);
@@ -306,11 +334,14 @@ __global__ __launch_bounds__(512) void k_qgemm_mfma(const uint8_t* __restrict__ 
         xoff[u] = (uint32_t)((row * k + (c >> 2) * 32 + (c & 3) * 8) * 2);
     }
     if (wave < WW) {
-        const int slot = wave * 64 + lane, r = slot / CPR, c = (slot % CPR - (r >> RSH)) & (CPR - 1);
-        const int64_t row = n0 + r < n ? n0 + r : n - 1;
-        woff = (uint32_t)((row * nb + c / QC) * QB + (c % QC) * 16);
+#pragma unroll
+        for (int u = 0; u < WPT; u++) {
+            const int slot = (wave * WPT + u) * 64 + lane, r = slot / CPR, c = (slot % CPR - (r >> RSH)) & (CPR - 1);
+            const int64_t row = n0 + r < n ? n0 + r : n - 1;
+            woff[u] = (uint32_t)((row * nb + c / QC) * QB + (c % QC) * 16);
+        }
     }
-    if (wave >= 8 - DW) {  // the 4-byte word that holds scale (row, block)
+    if (DW > 0 && wave >= 8 - DW) {  // the 4-byte word that holds scale (row, block)
         const int slot = (wave - (8 - DW)) * 64 + lane;
         const int64_t row = n0 + (slot >> 2) < n ? n0 + (slot >> 2) : n - 1;
         doff = (uint32_t)(((row * nb + (slot & 3)) >> 1) * 4);
@@ -319,8 +350,12 @@ __global__ __launch_bounds__(512) void k_qgemm_mfma(const uint8_t* __restrict__ 
         const char* src = reinterpret_cast<const char*>(x16) + kb * 64;  // 32 halves per block
 #pragma unroll
         for (int u = 0; u < XI; u++) lds_dma16(src + xoff[u], &Xs[st][(wave * XI + u) * 64 * 8]);
-        if (wave < WW) lds_dma16(reinterpret_cast<const char*>(qs) + kb * QB + woff, &Wq[st][wave * 64 * 16]);
-        if (wave >= 8 - DW)  // kb even: whole words
+        if (wave < WW) {
+#pragma unroll
+            for (int u = 0; u < WPT; u++)
+                lds_dma16(reinterpret_cast<const char*>(qs) + kb * QB + woff[u], &Wq[st][(wave * WPT + u) * 64 * 16]);
+        }
+        if (DW > 0 && wave >= 8 - DW)  // kb even: whole words
             lds_dma4(reinterpret_cast<const char*>(dsc) + kb * 2 + doff, &Wd[st][(wave - (8 - DW)) * 64]);
     };
     uint32_t dpar[TN];  // which half of its word holds this lane's scale (kb is even)
@@ -333,15 +368,20 @@ __global__ __launch_bounds__(512) void k_qgemm_mfma(const uint8_t* __restrict__ 
     // This wavefront's half of the iteration: k-steps t = 2 kh, 2 kh + 1.  Every LDS read
     // (W quants, scale words, A fragments) is issued before the first use.
     auto compute = [&](int st) {
-        QRaw<QT> wr[TN];
+        // quant data of the wavefront's rows: the whole block (scaled types), or the two
+        // operand words of its k-steps (f16 weights)
+        constexpr int NW = SCALED ? QC : 2;
+        uint4 wr[TN][NW];
         uint32_t dw[TN];
 #pragma unroll
         for (int j = 0; j < TN; j++) {
             const int r = wn * (BN / 2) + 16 * j + col;
 #pragma unroll
-            for (int h = 0; h < QC; h++)
-                wr[j].v[h] = *reinterpret_cast<const uint4*>(&Wq[st][(r * CPR + ((g * QC + h + (r >> RSH)) & (CPR - 1))) * 16]);
-            dw[j] = Wd[st][r * Q_KR + g];
+            for (int h = 0; h < NW; h++) {
+                const int c = SCALED ? g * QC + h : g * QC + 2 * kh + h;
+                wr[j][h] = *reinterpret_cast<const uint4*>(&Wq[st][(r * CPR + ((c + (r >> RSH)) & (CPR - 1))) * 16]);
+            }
+            if constexpr (SCALED) dw[j] = Wd[st][r * Q_KR + g];
         }
         const _Float16* xs = Xs[st];
         half8 a[2][TM];
@@ -354,9 +394,11 @@ __global__ __launch_bounds__(512) void k_qgemm_mfma(const uint8_t* __restrict__ 
         half2v d2[TN], m8d2[TN];
 #pragma unroll
         for (int j = 0; j < TN; j++) {
-            const uint32_t b = (dw[j] >> dpar[j]) & 0xFFFFu;
-            d2[j] = __builtin_bit_cast(half2v, b | (b << 16));
-            m8d2[j] = d2[j] * half2v{(_Float16)-8.0f, (_Float16)-8.0f};
+            if constexpr (SCALED) {
+                const uint32_t b = (dw[j] >> dpar[j]) & 0xFFFFu;
+                d2[j] = __builtin_bit_cast(half2v, b | (b << 16));
+                m8d2[j] = d2[j] * half2v{(_Float16)-8.0f, (_Float16)-8.0f};
+            }
         }
 #pragma unroll
         for (int tt = 0; tt < 2; tt++) {
@@ -364,8 +406,9 @@ __global__ __launch_bounds__(512) void k_qgemm_mfma(const uint8_t* __restrict__ 
 #pragma unroll
             for (int j = 0; j < TN; j++) {
                 half8 bop;
-                if constexpr (QT == TL_HIP_GGML_Q4_0) bop = QWords<QT>::operand(wr[j].v[0], t, d2[j], m8d2[j]);
-                else bop = QWords<QT>::operand(wr[j].v, t, d2[j], m8d2[j]);
+                if constexpr (QT == TL_HIP_GGML_Q4_0) bop = QWords<QT>::operand(wr[j][0], t, d2[j], m8d2[j]);
+                else if constexpr (QT == TL_HIP_GGML_Q8_0) bop = QWords<QT>::operand(wr[j], t, d2[j], m8d2[j]);
+                else bop = __builtin_bit_cast(half8, wr[j][tt]);
 #pragma unroll
                 for (int i = 0; i < TM; i++) acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[tt][i], bop, acc[i][j], 0, 0, 0);
             }
@@ -423,7 +466,7 @@ int launch_quant_gemm(const QWeight* w, const float* x, float* y, int64_t m, hip
     }
     const bool q4 = w->ggml_type == TL_HIP_GGML_Q4_0;
     if (mode != 0 && w->nb % Q_KR != 0) mode = 0;  // the MFMA pipeline takes K in steps of 128
-    if (w->ggml_type == TL_HIP_GGML_Q4_K || w->ggml_type == TL_HIP_GGML_Q6_K) mode = 0;
+
     if (mode == 0) {
         dim3 grid((unsigned)cdiv(w->n, F_BN), (unsigned)cdiv(m, F_BM));
         const QView qv{w->qs, w->d, w->hdr, w->qh, w->sc};
@@ -440,7 +483,25 @@ int launch_quant_gemm(const QWeight* w, const float* x, float* y, int64_t m, hip
         const int64_t units = m * w->nb * 4;
         constexpr int BM = 128, BN = 64;
         const int64_t tiles = cdiv(m, BM) * cdiv(w->n, BN);
-        if (q4) {
+        if (w->ggml_type == TL_HIP_GGML_Q4_K || w->ggml_type == TL_HIP_GGML_Q6_K) {
+            // K-quants: dequantize once into f16 operand order (n * k halves), then the same
+            // MFMA pipeline with the weights read as stored
+            _Float16* w16 = static_cast<_Float16*>(dev_alloc((size_t)w->n * w->k * sizeof(_Float16)));
+            if (!w16) {
+                dev_free(x16);
+                return TL_HIP_ERR_ALLOC;
+            }
+            const QView qv{w->qs, w->d, w->hdr, w->qh, w->sc};
+            const int64_t wunits = w->n * w->nb;
+            if (w->ggml_type == TL_HIP_GGML_Q4_K)
+                k_dequant_f16q<TL_HIP_GGML_Q4_K><<<(unsigned)cdiv(wunits, 256), 256, 0, s>>>(qv, w16, wunits);
+            else
+                k_dequant_f16q<TL_HIP_GGML_Q6_K><<<(unsigned)cdiv(wunits, 256), 256, 0, s>>>(qv, w16, wunits);
+            k_x_to_f16q<TL_HIP_GGML_Q4_0><<<(unsigned)cdiv(units, 256), 256, 0, s>>>(x, x16, units);
+            k_qgemm_mfma<TL_HIP_GGML_F16, BM, BN, 2><<<(unsigned)tiles, 512, 0, s>>>(
+                reinterpret_cast<const uint8_t*>(w16), nullptr, x16, y, m, w->n, w->k, w->nb);
+            dev_free(w16);
+        } else if (q4) {
             k_x_to_f16q<TL_HIP_GGML_Q4_0><<<(unsigned)cdiv(units, 256), 256, 0, s>>>(x, x16, units);
             k_qgemm_mfma<TL_HIP_GGML_Q4_0, BM, BN, 2><<<(unsigned)tiles, 512, 0, s>>>(w->qs, w->d, x16, y, m, w->n, w->k, w->nb);
         } else {
