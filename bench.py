@@ -274,6 +274,7 @@ def main():
     ap.add_argument("--no-extra", action="store_true", help="skip the prefill GEMM and attention legs")
     ap.add_argument("--gemm-only", action="store_true", help="only the prefill GEMM leg (counter runs)")
     ap.add_argument("--kquant-only", action="store_true", help="only the per-type matvec and Q4_K_M decode legs")
+    ap.add_argument("--attention-only", action="store_true", help="only the decode attention leg (counter runs)")
     ap.add_argument("--matvec-only", action="store_true",
                     help="only the 4096x4096 matvec timing plus a 64 MiB device copy (counter runs)")
     args = ap.parse_args()
@@ -292,6 +293,9 @@ def main():
 
     if args.gemm_only:
         print(json.dumps({"prefill_gemm": bench_gemm(dev)}), flush=True)
+        return
+    if args.attention_only:
+        print(json.dumps({"decode_attention": bench_attention(dev)}), flush=True)
         return
     if args.kquant_only:
         print(json.dumps({"quant_matvec": bench_quant_matvec(dev)}), flush=True)

@@ -484,7 +484,7 @@ __global__ __launch_bounds__(256) void k_attn_gq(AttnArgs a) {
         part[wave][g][kl * 8 + d] = o[j];
     }
     __syncthreads();
-    if (a.nsplit == 1) {
+    if (L <= GQ_CH) {  // the item's only split: normalise and store (the merge skips the item)
         for (int idx = tid; idx < G * D; idx += 256) {
             const int g = idx / D, d = idx % D;
             const float v = (part[0][g][d] + part[1][g][d]) + (part[2][g][d] + part[3][g][d]);
@@ -737,6 +737,7 @@ __global__ __launch_bounds__(256) void k_attn_merge_gq(AttnArgs a) {
     int64_t L = a.len.of(b);
     if (L > a.lmax) L = a.lmax;
     const int nact = (int)((L + a.chunk - 1) / a.chunk);
+    if (nact <= 1) return;  // written by its only split
     const int64_t stride = (int64_t)G * (D + 2);
     const float* base = a.ws + (((int64_t)b * a.hkv + h) * a.nsplit) * stride + g * (D + 2);
     float M = -INFINITY;
@@ -927,7 +928,7 @@ extern "C" tl_hip_tensor* tl_hip_attention_decode(const tl_hip_tensor* qh, const
     hipStream_t s = cur_stream();
     float* ws = (float*)dev_alloc(attn_workspace_floats((int)B, (int)hkv, (int)(hq / hkv), (int)D, 2 * nsplit) * 4);
     int rc = ws ? TL_HIP_OK : TL_HIP_ERR_ALLOC;
-    if (rc == TL_HIP_OK && L <= 1024 && attention_qh_supported(k->dtype, (int)D))
+    if (rc == TL_HIP_OK && !dec && attention_qh_supported(k->dtype, (int)D))
         rc = launch_attention_qh(q->f32(), k->data, v->data, k->dtype, o->f32(), (int)B, (int)hq, (int)hkv, (int)D,
                                  lmax, hkv * lmax * D, L, nullptr, 0, 0, scale, s);
     else if (rc == TL_HIP_OK && dec)

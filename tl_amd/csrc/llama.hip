@@ -388,6 +388,8 @@ static int enqueue_step(Llama* m, float penalty, hipStream_t s) {
             a.row_off = sg.row_off;
             if ((rc = launch_mv(sg.w, a, 1, EPI_ROPE_KV, true, l == 0, s))) return rc;
         }
+        // caches up to 4096 positions: one workgroup per query head in a single launch (the
+        // split form's merge launch costs more than its wider spread saves at these lengths)
         if (m->max_seq <= 4096 && attention_qh_supported(m->kv_f16 ? TL_HIP_F16 : TL_HIP_F32, (int)hd))
             rc = launch_attention_qh(m->q, m->kc[l], m->vc[l], m->kv_f16 ? TL_HIP_F16 : TL_HIP_F32, m->ao, 1, m->H,
                                      m->KV, (int)hd, m->max_seq, 0, 0, m->pos, 1, 0, 1.0f / sqrtf((float)hd), s);
