@@ -241,6 +241,16 @@ tl_hip_tensor* tl_hip_fused_add_rms_norm(const tl_hip_tensor* x, const tl_hip_te
  *   out [B, Hq, D] f32;  query head h reads KV head h / (Hq / Hkv). */
 tl_hip_tensor* tl_hip_attention_decode(const tl_hip_tensor* q, const tl_hip_tensor* k,
                                        const tl_hip_tensor* v, int64_t L, float scale);
+/* Causal prefill attention over an f16 KV cache: the same chatbot chain for sl > 1 with the
+ * causal mask (Tensor::new_causal_mask + add_4d, chatbot.tl:76-87), in one f16-MFMA kernel.
+ *   q [n, Hq, D] f32 holds the queries of positions pos0 .. pos0 + n - 1;
+ *   k, v [Hkv, Lmax, D] f16 with rows 0 .. pos0 + n - 1 valid; out [n, Hq, D] f32;
+ *   query i attends rows 0 .. pos0 + i; query head h reads KV head h / (Hq / Hkv).
+ * Covers D in {64, 128} with Hq / Hkv in {4, 8} (ArgumentError otherwise); the chatbot
+ * itself only prefills at pos0 = 0, later positions serve chunked prompts.  q, P, K and V
+ * enter the MFMAs in f16; scores, softmax and sums in f32. */
+tl_hip_tensor* tl_hip_attention_prefill(const tl_hip_tensor* q, const tl_hip_tensor* k,
+                                        const tl_hip_tensor* v, int64_t pos0, float scale);
 
 /* ------------------------------------------------------ Llama decoder driver ----- */
 /* The model composition of examples/apps/tinyllama/chatbot.tl:1-226 (Linear / RMSNorm /

@@ -197,6 +197,51 @@ def test_attention_grouped_split_lengths(dev, d, hq, hkv, lmax, L, B):
         assert_rel(got[b], ref, F32_TOL)
 
 
+@pytest.mark.parametrize("d,hq,hkv,lmax,pos0,n", [(64, 32, 4, 600, 0, 512), (64, 16, 2, 300, 0, 37),
+                                                  (128, 32, 8, 1100, 0, 1031), (128, 16, 4, 700, 333, 250),
+                                                  (64, 8, 1, 200, 45, 1), (128, 16, 2, 256, 100, 100)])
+def test_attention_prefill_causal(dev, d, hq, hkv, lmax, pos0, n):
+    """The f16-MFMA causal prefill against the oracle's chatbot attention: at pos0 = 0 the
+    masked form (chatbot.tl:76-81); later starts (chunked prompts) as one unmasked row per
+    query over the positions it sees.  Query counts off the kernel's 16 / 32-query block,
+    cache rows past the last query hold NaN (masked rows must not leak into the output)."""
+    rng = np.random.default_rng(0x71590000 + d + hq + pos0 + n)
+    q = rng.standard_normal((n, hq, d)).astype(np.float32)
+    k = rng.standard_normal((hkv, lmax, d)).astype(np.float16)
+    v = rng.standard_normal((hkv, lmax, d)).astype(np.float16)
+    k[:, pos0 + n:] = np.nan
+    v[:, pos0 + n:] = np.nan
+    scale = np.float32(1.0 / np.sqrt(d))
+    got = dev.attention_prefill(dev.tensor_new(q), dev.tensor_new_f16(k), dev.tensor_new_f16(v), pos0,
+                                scale).to_numpy()
+    assert got.shape == (n, hq, d) and np.isfinite(got).all()
+    kf, vf = k.astype(np.float32), v.astype(np.float32)
+    if pos0 == 0:
+        ref = oracle.attention(q, kf[:, :n], vf[:, :n], scale, n > 1).reshape(n, hq, d)
+        assert_rel(got, ref, F16_TOL)
+    else:
+        for i in sorted({0, 1, n // 2, n - 2, n - 1} & set(range(n))):
+            L = pos0 + i + 1
+            ref = oracle.attention(q[i][None], kf[:, :L], vf[:, :L], scale, False).reshape(hq, d)
+            assert_rel(got[i], ref, F16_TOL)
+
+
+def test_attention_prefill_errors(dev):
+    q = dev.tensor_new(np.zeros((4, 8, 64), np.float32))
+    kv = dev.tensor_new_f16(np.zeros((2, 16, 64), np.float16))
+    with pytest.raises(BackendError) as e:  # 4 query heads per KV head: fine; 13 + 4 > 16 rows
+        dev.attention_prefill(q, kv, kv, 13, 0.125)
+    assert e.value.variant == "ArgumentError"
+    kv4 = dev.tensor_new_f16(np.zeros((4, 16, 64), np.float16))
+    with pytest.raises(BackendError) as e:  # 2 query heads per KV head: not covered
+        dev.attention_prefill(q, kv4, kv4, 0, 0.125)
+    assert e.value.variant == "ArgumentError"
+    with pytest.raises(BackendError) as e:
+        dev.attention_prefill(q, dev.tensor_new(np.zeros((2, 16, 64), np.float32)), kv, 0, 0.125)
+    assert e.value.variant == "TypeMismatch"
+    assert dev.attention_prefill(q, kv, kv, 12, 0.125).to_numpy().shape == (4, 8, 64)
+
+
 def test_attention_decode_partial_length_and_f32_cache(dev):
     rng = np.random.default_rng(17)
     q = rng.standard_normal((2, 32, 64)).astype(np.float32)

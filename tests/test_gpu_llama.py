@@ -67,6 +67,39 @@ def test_f16_kv_and_f16_prefill_logits(small):
     gpu.configure(kv_f16=False)
 
 
+def test_f16_prefill_mfma_attention_chunks():
+    """The f16 prefill's MFMA attention in the decoder (head size 64, 8 query heads per KV
+    head, as TinyLlama): a 150-token prompt within the f16 tolerance 1e-2 of the oracle, then
+    the same prompt in chunks whose lengths are off the kernel's 16-query block, the later
+    ones starting at cache positions > 0 -- with per-token RoPE positions the chunked logits
+    equal the whole-prompt ones up to f16 rounding of the shorter GEMMs."""
+    cfg = LlamaConfig(2, 512, 8, 1, 512, 1000, max_seq=256)
+    tensors = list(synthetic_weights(cfg, 41))
+    gpu = HipLlama(cfg, kv_f16=True)
+    gpu.load(tensors)
+    cpu = oracle.Llama(cfg)
+    cpu.load(tensors)
+    try:
+        prompt = synthetic_prompt(cfg, 41, 150)
+        cpu.reset()
+        err = max_rel(gpu.forward(prompt, prefill_f16=True), cpu.forward(prompt))
+        assert err <= 1e-2, f"f16 prefill logits max-rel-err {err:.2e}"
+        err = max_rel(gpu.forward([9]), cpu.forward([9]))
+        assert err <= 1e-2, f"decode after f16 prefill: logits max-rel-err {err:.2e}"
+        gpu.configure(kv_f16=True, rope_per_token=True)
+        gpu.reset()
+        whole = gpu.forward(prompt, prefill_f16=True)
+        gpu.reset()
+        for chunk in (prompt[:37], prompt[37:58], prompt[58:]):
+            part = gpu.forward(chunk, prefill_f16=True)
+        assert gpu.position == 150
+        err = max_rel(part, whole)
+        assert err <= 1e-3, f"chunked vs whole prompt logits max-rel-err {err:.2e}"
+    finally:
+        gpu.close()
+        cpu.close()
+
+
 def test_position_aware_rope_changes_prefill(small):
     gpu, _ = small
     prompt = synthetic_prompt(SMALL, 14, 12)

@@ -94,6 +94,7 @@ PROTOS = {
     "tl_hip_fused_rms_norm": (P, [P, P, f32]),
     "tl_hip_fused_add_rms_norm": (P, [P, P, P, f32]),
     "tl_hip_attention_decode": (P, [P, P, P, i64, f32]),
+    "tl_hip_attention_prefill": (P, [P, P, P, i64, f32]),
     "tl_hip_llama_new": (P, [i32, i32, i32, i32, i32, i32, f32, f32, i32]),
     "tl_hip_llama_free": (i32, [P]),
     "tl_hip_llama_set_linear": (i32, [P, i32, i32, i32, u8p, sz]),

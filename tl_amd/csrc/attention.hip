@@ -659,6 +659,207 @@ __global__ __launch_bounds__(64 * W) void k_attn_qh(AttnArgs a, int G) {
     }
 }
 
+// ---- causal prefill form (f16 cache, f16 MFMA): one workgroup per (block of queries, KV head)
+// The workgroup's 128 rows are (query, head) pairs of its QB = 128 / G queries and the G heads
+// of the KV head; wavefront w owns rows 32 w .. 32 w + 31 (two 16-row tiles).  Per 64-position
+// KV tile (K row-major, V transposed, both in LDS):
+//   S^T = K Q^T   (v_mfma_f32_16x16x32_f16: A = K rows from LDS, B = q from registers), so a
+//                 lane holds row l % 16's scores for positions 4 (l / 16) .. +3 of each
+//                 16-position block -- every per-row quantity stays in the lane that owns it;
+//   online softmax per row (the row's 64 scores sit in the four lanes l % 16 + 16 g);
+//   O^T += V^T P^T with the k slots ordered as the scores already lie in the lanes
+//                 (slot group g, element e <-> position 32 ks + 16 (e / 4) + 4 g + e % 4),
+//                 so P never leaves the registers; V^T is read as two 8-byte runs.
+// Query i of the call sits at position pos0 + i and attends positions 0 .. pos0 + i.  Scores,
+// softmax and accumulation in f32; q, P, K, V enter the MFMAs in f16 (the f16 path).
+typedef _Float16 half8v __attribute__((ext_vector_type(8)));
+typedef float floatx4v __attribute__((ext_vector_type(4)));
+
+template <int D, int G>
+__global__ __launch_bounds__(256) void k_attn_prefill(const float* __restrict__ q, const __half* __restrict__ kc,
+                                                      const __half* __restrict__ vc, float* __restrict__ out,
+                                                      int n, int hkv, int64_t lmax, const int32_t* __restrict__ pos_dev,
+                                                      int64_t pos_host, float scale) {
+    constexpr int QB = 128 / G;   // queries per workgroup
+    constexpr int KT = 64;        // positions per KV tile
+    constexpr int KS = D / 32;    // MFMA k-steps over the head dim
+    constexpr int CPR = D / 8;    // 16-byte chunks per K row
+    __shared__ __attribute__((aligned(16))) _Float16 Ks[KT * D];  // row-major, chunk c of row r at c ^ (r & (CPR - 1))
+    __shared__ __attribute__((aligned(16))) _Float16 Vt[D * KT];  // [dim][pos], 8-byte run j of dim d at j ^ (d & 15)
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int col = lane & 15, g = lane >> 4;
+    const int qb = blockIdx.x, h = blockIdx.y;
+    const int hq = hkv * G;
+    const int64_t pos0 = pos_dev ? (int64_t)*pos_dev : pos_host;
+    const __half* kb = kc + (int64_t)h * lmax * D;
+    const __half* vb = vc + (int64_t)h * lmax * D;
+
+    // this lane's two rows (one per 16-row tile): query qi, head hh
+    int qi[2], hh[2];
+    int64_t prow[2];
+#pragma unroll
+    for (int rt = 0; rt < 2; rt++) {
+        const int r = 32 * wave + 16 * rt + col;
+        qi[rt] = qb * QB + r / G;
+        hh[rt] = h * G + r % G;
+        prow[rt] = pos0 + (qi[rt] < n ? qi[rt] : n - 1);
+    }
+    // B operand of S^T: q[row][32 ks + 8 g .. +7] * scale, in f16
+    half8v qop[2][KS];
+#pragma unroll
+    for (int rt = 0; rt < 2; rt++) {
+        const int qq = qi[rt] < n ? qi[rt] : n - 1;
+        const float* qp = q + ((int64_t)qq * hq + hh[rt]) * D;
+#pragma unroll
+        for (int ks = 0; ks < KS; ks++) {
+            const float4 a = reinterpret_cast<const float4*>(qp + 32 * ks + 8 * g)[0];
+            const float4 b = reinterpret_cast<const float4*>(qp + 32 * ks + 8 * g)[1];
+            qop[rt][ks] = half8v{(_Float16)(a.x * scale), (_Float16)(a.y * scale), (_Float16)(a.z * scale),
+                                 (_Float16)(a.w * scale), (_Float16)(b.x * scale), (_Float16)(b.y * scale),
+                                 (_Float16)(b.z * scale), (_Float16)(b.w * scale)};
+        }
+    }
+    floatx4v o[2][D / 16];  // O^T tiles: [row tile][dim tile], lane: dims 4 g .. +3 of row col
+#pragma unroll
+    for (int rt = 0; rt < 2; rt++)
+#pragma unroll
+        for (int dt = 0; dt < D / 16; dt++) o[rt][dt] = floatx4v{0.f, 0.f, 0.f, 0.f};
+    float mrow[2] = {-INFINITY, -INFINITY}, lrow[2] = {0.f, 0.f};
+
+    const int64_t last = pos0 + (int64_t)((qb + 1) * QB < n ? (qb + 1) * QB : n);  // positions needed
+    const int ntiles = (int)((last + KT - 1) / KT);
+    for (int tile = 0; tile < ntiles; tile++) {
+        const int64_t t0 = (int64_t)tile * KT;
+        __syncthreads();  // the previous tile's readers are done
+        // K tile: 64 rows x CPR chunks; V tile transposed into Vt.  Rows at or past `last` are
+        // zeros: they are masked out, and a zero P times a non-finite V would still poison O.
+        for (int u = tid; u < KT * CPR; u += 256) {
+            const int r = u / CPR, c = u % CPR;
+            const int64_t p = t0 + r;
+            uint4 kw = make_uint4(0u, 0u, 0u, 0u), vw = kw;
+            if (p < last) {
+                kw = *reinterpret_cast<const uint4*>(kb + p * D + 8 * c);
+                vw = *reinterpret_cast<const uint4*>(vb + p * D + 8 * c);
+            }
+            *reinterpret_cast<uint4*>(&Ks[r * D + 8 * (c ^ (r & (CPR - 1)))]) = kw;
+            const _Float16* vh = reinterpret_cast<const _Float16*>(&vw);
+#pragma unroll
+            for (int e = 0; e < 8; e++) {
+                const int d = 8 * c + e;
+                Vt[d * KT + 4 * ((r >> 2) ^ (d & 15)) + (r & 3)] = vh[e];
+            }
+        }
+        __syncthreads();
+        // S^T = K Q^T over the tile: [pos tile pt][row tile rt]
+        floatx4v st[4][2];
+#pragma unroll
+        for (int pt = 0; pt < 4; pt++)
+#pragma unroll
+            for (int rt = 0; rt < 2; rt++) st[pt][rt] = floatx4v{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int pt = 0; pt < 4; pt++) {
+            const int r = 16 * pt + col;
+#pragma unroll
+            for (int ks = 0; ks < KS; ks++) {
+                const int c = 4 * ks + g;
+                const half8v a = *reinterpret_cast<const half8v*>(&Ks[r * D + 8 * (c ^ (r & (CPR - 1)))]);
+#pragma unroll
+                for (int rt = 0; rt < 2; rt++)
+                    st[pt][rt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, qop[rt][ks], st[pt][rt], 0, 0, 0);
+            }
+        }
+        // causal mask, online softmax per row (row col's scores: this lane and lanes col + 16 g)
+        half8v pop[2][2];  // B operand of O^T: [k-step][row tile]
+#pragma unroll
+        for (int rt = 0; rt < 2; rt++) {
+            float mx = -INFINITY;
+#pragma unroll
+            for (int pt = 0; pt < 4; pt++)
+#pragma unroll
+                for (int i = 0; i < 4; i++) {
+                    const int64_t p = t0 + 16 * pt + 4 * g + i;
+                    if (p > prow[rt]) st[pt][rt][i] = -INFINITY;
+                    mx = fmaxf(mx, st[pt][rt][i]);
+                }
+            mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
+            mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+            const float mn = fmaxf(mrow[rt], mx);  // finite: position 0 is in every row's range
+            const float alpha = expf(mrow[rt] - mn);
+            float sum = 0.f;
+#pragma unroll
+            for (int pt = 0; pt < 4; pt++)
+#pragma unroll
+                for (int i = 0; i < 4; i++) {
+                    const float e = expf(st[pt][rt][i] - mn);
+                    st[pt][rt][i] = e;
+                    sum += e;
+                }
+            sum += __shfl_xor(sum, 16, 64);
+            sum += __shfl_xor(sum, 32, 64);
+            lrow[rt] = lrow[rt] * alpha + sum;
+            mrow[rt] = mn;
+#pragma unroll
+            for (int dt = 0; dt < D / 16; dt++) o[rt][dt] *= alpha;
+#pragma unroll
+            for (int ks = 0; ks < 2; ks++)
+#pragma unroll
+                for (int e = 0; e < 8; e++) pop[ks][rt][e] = (_Float16)st[2 * ks + e / 4][rt][e % 4];
+        }
+        // O^T += V^T P^T: A = V^T[dim tile][k slots], two 8-byte runs per k-step
+#pragma unroll
+        for (int dt = 0; dt < D / 16; dt++) {
+            const int d = 16 * dt + col;
+#pragma unroll
+            for (int ks = 0; ks < 2; ks++) {
+                const int j0 = (8 * ks + g) ^ (d & 15), j1 = (8 * ks + 4 + g) ^ (d & 15);
+                const uint2 lo = *reinterpret_cast<const uint2*>(&Vt[d * KT + 4 * j0]);
+                const uint2 hi = *reinterpret_cast<const uint2*>(&Vt[d * KT + 4 * j1]);
+                const half8v a = __builtin_bit_cast(half8v, make_uint4(lo.x, lo.y, hi.x, hi.y));
+#pragma unroll
+                for (int rt = 0; rt < 2; rt++)
+                    o[rt][dt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, pop[ks][rt], o[rt][dt], 0, 0, 0);
+            }
+        }
+    }
+    // out[query][head][dims 16 dt + 4 g .. +3] = O / l
+#pragma unroll
+    for (int rt = 0; rt < 2; rt++) {
+        if (qi[rt] >= n) continue;
+        const float rl = 1.0f / lrow[rt];
+        float* op = out + ((int64_t)qi[rt] * hq + hh[rt]) * D;
+#pragma unroll
+        for (int dt = 0; dt < D / 16; dt++)
+            *reinterpret_cast<float4*>(op + 16 * dt + 4 * g) =
+                make_float4(o[rt][dt][0] * rl, o[rt][dt][1] * rl, o[rt][dt][2] * rl, o[rt][dt][3] * rl);
+    }
+}
+
+bool attention_prefill_supported(int kv_dtype, int hq, int hkv, int D) {
+    const int G = hkv > 0 ? hq / hkv : 0;
+    return kv_dtype == TL_HIP_F16 && (D == 64 || D == 128) && (G == 4 || G == 8) && hq == G * hkv;
+}
+
+int launch_attention_prefill(const float* q, const void* k, const void* v, float* out, int n, int hq, int hkv,
+                             int D, int64_t lmax, const int32_t* pos_dev, int64_t pos_host, float scale,
+                             hipStream_t s) {
+    const int G = hq / hkv;
+    if (n < 1) return TL_HIP_OK;
+    dim3 grid((unsigned)cdiv(n, 128 / G), hkv);
+    const __half* kh = static_cast<const __half*>(k);
+    const __half* vh = static_cast<const __half*>(v);
+    if (D == 64 && G == 8) k_attn_prefill<64, 8><<<grid, 256, 0, s>>>(q, kh, vh, out, n, hkv, lmax, pos_dev, pos_host, scale);
+    else if (D == 64 && G == 4) k_attn_prefill<64, 4><<<grid, 256, 0, s>>>(q, kh, vh, out, n, hkv, lmax, pos_dev, pos_host, scale);
+    else if (D == 128 && G == 8) k_attn_prefill<128, 8><<<grid, 256, 0, s>>>(q, kh, vh, out, n, hkv, lmax, pos_dev, pos_host, scale);
+    else if (D == 128 && G == 4) k_attn_prefill<128, 4><<<grid, 256, 0, s>>>(q, kh, vh, out, n, hkv, lmax, pos_dev, pos_host, scale);
+    else {
+        set_error(TL_HIP_ERR_ARG, "ArgumentError: prefill attention covers f16 caches, head_dim 64 / 128, 4 or 8 query "
+                  "heads per KV head");
+        return TL_HIP_ERR_ARG;
+    }
+    hipError_t e = hipGetLastError();
+    return e == hipSuccess ? TL_HIP_OK : hip_fail(e, "prefill attention launch");
+}
+
 bool attention_qh_supported(int kv_dtype, int D) {
     return (kv_dtype == TL_HIP_F16 && (D == 64 || D == 128)) || (kv_dtype == TL_HIP_F32 && D == 64);
 }
@@ -938,6 +1139,58 @@ extern "C" tl_hip_tensor* tl_hip_attention_decode(const tl_hip_tensor* qh, const
         rc = launch_attention(q->f32(), k->data, v->data, k->dtype, o->f32(), ws, (int)B, (int)hq, (int)hkv,
                               (int)D, lmax, hkv * lmax * D, L, nullptr, 0, 0, chunk, nsplit, scale, s);
     dev_free(ws);  // stream-ordered: reused only by later work on the same stream
+    if (rc != TL_HIP_OK) {
+        tensor_drop(o);
+        return nullptr;
+    }
+    return H(o);
+}
+
+extern "C" tl_hip_tensor* tl_hip_attention_prefill(const tl_hip_tensor* qh, const tl_hip_tensor* kh,
+                                                   const tl_hip_tensor* vh, int64_t pos0, float scale) {
+    if (!qh || !kh || !vh) {
+        set_error(TL_HIP_ERR_NULL, "NullPointerError: q, k or v");
+        return nullptr;
+    }
+    if (!state()) return nullptr;
+    const Tensor* q = reinterpret_cast<const Tensor*>(qh);
+    const Tensor* k = reinterpret_cast<const Tensor*>(kh);
+    const Tensor* v = reinterpret_cast<const Tensor*>(vh);
+    if (q->dtype != TL_HIP_F32 || k->dtype != TL_HIP_F16 || v->dtype != TL_HIP_F16) {
+        set_error(TL_HIP_ERR_TYPE, "TypeMismatch: q must be f32, k and v f16");
+        return nullptr;
+    }
+    if (q->rank != 3 || k->rank != 3 || v->rank != 3) {
+        set_error(TL_HIP_ERR_SHAPE, "ShapeMismatch: q [n,Hq,D], k/v [Hkv,Lmax,D] expected");
+        return nullptr;
+    }
+    const int64_t n = q->shape[0], hq = q->shape[1], D = q->shape[2];
+    const int64_t hkv = k->shape[0], lmax = k->shape[1];
+    for (int i = 0; i < 3; i++)
+        if (k->shape[i] != v->shape[i]) {
+            set_error(TL_HIP_ERR_SHAPE, "ShapeMismatch: k and v shapes differ");
+            return nullptr;
+        }
+    if (k->shape[2] != D || hkv <= 0 || hq % hkv != 0) {
+        set_error(TL_HIP_ERR_SHAPE, "ShapeMismatch: q [%lld,%lld,%lld] vs kv [%lld,%lld,%lld]", (long long)n,
+                  (long long)hq, (long long)D, (long long)hkv, (long long)lmax, (long long)k->shape[2]);
+        return nullptr;
+    }
+    if (!attention_prefill_supported(TL_HIP_F16, (int)hq, (int)hkv, (int)D) || hkv > 65535) {
+        set_error(TL_HIP_ERR_ARG, "ArgumentError: prefill attention covers head_dim 64 / 128 with 4 or 8 query heads "
+                  "per KV head");
+        return nullptr;
+    }
+    if (n < 1 || pos0 < 0 || pos0 > lmax - n || n > INT32_MAX) {
+        set_error(TL_HIP_ERR_ARG, "ArgumentError: %lld queries from position %lld exceed the cache of %lld rows",
+                  (long long)n, (long long)pos0, (long long)lmax);
+        return nullptr;
+    }
+    int64_t oshape[3] = {n, hq, D};
+    Tensor* o = tensor_alloc(oshape, 3);
+    if (!o) return nullptr;
+    int rc = launch_attention_prefill(q->f32(), k->data, v->data, o->f32(), (int)n, (int)hq, (int)hkv, (int)D, lmax,
+                                      nullptr, pos0, scale, cur_stream());
     if (rc != TL_HIP_OK) {
         tensor_drop(o);
         return nullptr;

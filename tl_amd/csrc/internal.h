@@ -172,6 +172,13 @@ int launch_attention_gq(const float* q, const void* k, const void* v, float* out
                         int hkv, int D, int64_t lmax, int64_t kv_bstride, int64_t L, const int32_t* len_dev,
                         int len_add, int len_step, int nsplit, float scale, hipStream_t s);
 int attention_gq_splits(int64_t L);
+// Causal prefill with f16 MFMA (shapes of attention_prefill_supported): q [n, hq, D] f32 of
+// queries at positions pos0 + i over the cache [hkv, lmax, D] f16; out [n, hq, D].  pos0 is
+// *pos_dev when pos_dev is given, else pos_host; pos0 + n <= lmax.
+bool attention_prefill_supported(int kv_dtype, int hq, int hkv, int D);
+int launch_attention_prefill(const float* q, const void* k, const void* v, float* out, int n, int hq, int hkv,
+                             int D, int64_t lmax, const int32_t* pos_dev, int64_t pos_host, float scale,
+                             hipStream_t s);
 // Short-cache form: one workgroup per (query head, batch item); shapes: attention_qh_supported.
 bool attention_qh_supported(int kv_dtype, int D);
 int launch_attention_qh(const float* q, const void* k, const void* v, int kv_dtype, float* out,

@@ -320,8 +320,12 @@ static int enqueue_forward(Llama* m, int n, int f16, hipStream_t s) {
             k_rope_kv<float><<<cdiv(work, 256), 256, 0, s>>>(m->qkv, m->q, (float*)m->kc[l], (float*)m->vc[l],
                                                             m->cos_t, m->sin_t, m->pos, n, m->H, m->KV, (int)hd,
                                                             m->max_seq, m->rope_per_token);
-        // query i (absolute position pos + i) attends cache positions 0 .. pos + i
-        if (attention_gq_supported(m->kv_f16 ? TL_HIP_F16 : TL_HIP_F32, m->H, m->KV, (int)hd))
+        // query i (absolute position pos + i) attends cache positions 0 .. pos + i; the f16
+        // prefill uses the MFMA form, the f32 path the grouped-query split form
+        if (f16 && attention_prefill_supported(m->kv_f16 ? TL_HIP_F16 : TL_HIP_F32, m->H, m->KV, (int)hd))
+            rc = launch_attention_prefill(m->q, m->kc[l], m->vc[l], m->ao, n, m->H, m->KV, (int)hd, m->max_seq,
+                                          m->pos, 0, 1.0f / sqrtf((float)hd), s);
+        else if (attention_gq_supported(m->kv_f16 ? TL_HIP_F16 : TL_HIP_F32, m->H, m->KV, (int)hd))
             rc = launch_attention_gq(m->q, m->kc[l], m->vc[l], m->ao, m->ws, n, m->H, m->KV, (int)hd, m->max_seq, 0,
                                      0, m->pos, 1, 1, attention_gq_splits(m->host_pos + n),
                                      1.0f / sqrtf((float)hd), s);

@@ -255,3 +255,8 @@ class HipDevice:
     # -- decode attention over a KV cache
     def attention_decode(self, q, k, v, length, scale):
         return self._wrap(self.lib.tl_hip_attention_decode(q.handle, k.handle, v.handle, length, scale))
+
+    def attention_prefill(self, q, k, v, pos0, scale):
+        """Causal prefill attention (chatbot.tl:76-87 for sl > 1): q [n, Hq, D] f32 at positions
+        pos0 .. pos0 + n - 1, k / v [Hkv, Lmax, D] f16 caches -> [n, Hq, D] f32."""
+        return self._wrap(self.lib.tl_hip_attention_prefill(q.handle, k.handle, v.handle, pos0, scale))
