@@ -509,8 +509,10 @@ __global__ __launch_bounds__(256) void k_attn_gq(AttnArgs a) {
 // share a row (16 bytes each), so one load instruction covers 64 / LPR whole rows; the score
 // of a position is the LPR-lane sum of the partial dot products.  V rows are read by lane
 // (dim group dg = lane / 8, position slot = lane % 8), eight full rows per instruction.
-// Scores pass to the P.V lanes through LDS.  Softmax is online across rounds; the
-// wavefronts' (max, sum, o) records are merged through LDS at the end.  All arithmetic f32.
+// Scores pass to the P.V lanes through LDS; each lane turns one of them into a probability
+// (scores kept in log2 units, so one hardware exp2 per lane and round).  Softmax is online
+// across rounds; the wavefronts' (max, sum, o) records are merged through LDS at the end, with
+// the per-wavefront weights formed once.  All arithmetic f32.
 template <int LPR>
 __device__ __forceinline__ float row_sum(float v) {  // over aligned groups of LPR lanes
     static_assert(LPR == 8 || LPR == 16 || LPR == 32, "row width");
@@ -542,23 +544,26 @@ __global__ __launch_bounds__(64 * W) void k_attn_qh(AttnArgs a, int G) {
     constexpr int EPC = 16 / sizeof(KVT);  // elements per 16-byte load
     constexpr int LPR = D / EPC;           // lanes per K row
     constexpr int PPI = 64 / LPR;          // K rows per load instruction
-    constexpr int NI = C / PPI;            // K load instructions per round
+    constexpr int NI = C / PPI;            // K load instructions per round (= LPR)
     constexpr int DL = D / 8;              // dims per lane in P.V
     constexpr int VC = DL / EPC;           // 16-byte loads of a lane's V slice
+    static_assert(NI == LPR, "one score per lane and round");
     __shared__ float P[W][C];
-    __shared__ float wm[W], wl[W];
+    __shared__ float wm[W], wl[W], wf[W];
     __shared__ float wo[W][D];
     const int qh = blockIdx.x, b = blockIdx.y;
     const int h = qh / G;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int kl = lane % LPR, kr = lane / LPR;  // K: slice and row within an instruction
     const int slot = lane & 7, dg = lane >> 3;   // V: position slot and dim group
-    int64_t L = a.len.of(b);
-    if (L > a.lmax) L = a.lmax;
+    int64_t L64 = a.len.of(b);
+    if (L64 > a.lmax) L64 = a.lmax;
+    const uint32_t L = (uint32_t)L64;  // lmax * D < 2^31 (attention_qh_supported): 32-bit offsets
     const int hq = a.hkv * G;
     const KVT* kb = reinterpret_cast<const KVT*>(a.k) + (int64_t)b * a.kv_bstride + (int64_t)h * a.lmax * D;
     const KVT* vb = reinterpret_cast<const KVT*>(a.v) + (int64_t)b * a.kv_bstride + (int64_t)h * a.lmax * D;
     const float* qp = a.q + ((int64_t)b * hq + qh) * D;
+    const float sl2 = a.scale * 1.44269504088896341f;  // scores in log2 units: exp(x) = exp2(x log2 e)
 
     float qv[EPC];  // this lane's slice of q
 #pragma unroll
@@ -573,23 +578,23 @@ __global__ __launch_bounds__(64 * W) void k_attn_qh(AttnArgs a, int G) {
 #pragma unroll
     for (int i = 0; i < DL; i++) o[i] = 0.f;
 
-    for (int64_t base = (int64_t)wave * C; base < L; base += (int64_t)W * C) {
+    for (uint32_t base = (uint32_t)wave * C; base < L; base += (uint32_t)W * C) {
         uint4 kraw[NI], vraw[8][VC];
 #pragma unroll
         for (int c = 0; c < NI; c++) {
-            int64_t p = base + c * PPI + kr;
+            uint32_t p = base + c * PPI + kr;
             p = p < L ? p : L - 1;
             kraw[c] = *reinterpret_cast<const uint4*>(kb + p * D + kl * EPC);
         }
 #pragma unroll
         for (int j = 0; j < 8; j++) {
-            int64_t p = base + slot + 8 * j;
+            uint32_t p = base + slot + 8 * j;
             p = p < L ? p : L - 1;
 #pragma unroll
             for (int c = 0; c < VC; c++) vraw[j][c] = reinterpret_cast<const uint4*>(vb + p * D + dg * DL)[c];
         }
         // scores: position base + c * PPI + kr lives in register s[c] of its LPR lanes
-        float s[NI], mx = -INFINITY;
+        float s[NI];
 #pragma unroll
         for (int c = 0; c < NI; c++) {
             float kf[EPC];
@@ -597,24 +602,19 @@ __global__ __launch_bounds__(64 * W) void k_attn_qh(AttnArgs a, int G) {
             float t = 0.f;
 #pragma unroll
             for (int e = 0; e < EPC; e++) t = fmaf(qv[e], kf[e], t);
-            t = row_sum<LPR>(t);
-            s[c] = base + c * PPI + kr < L ? t * a.scale : -INFINITY;
-            mx = fmaxf(mx, s[c]);
+            s[c] = row_sum<LPR>(t) * sl2;
         }
-        const float mn = fmaxf(m, wave_max64(mx));
-        float es = 0.f;
+        // one probability per lane: lane kl of a row group takes position base + kl * PPI + kr
+        float sk = s[0];
 #pragma unroll
-        for (int c = 0; c < NI; c++) {
-            s[c] = expf(s[c] - mn);  // 0 for positions past the end
-            es += s[c];
-        }
-        const float alpha = expf(m - mn);
-        l = l * alpha + wave_sum64(kl == 0 ? es : 0.f);
+        for (int c = 1; c < NI; c++) sk = kl == c ? s[c] : sk;
+        const bool in = base + kl * PPI + kr < L;
+        const float mn = fmaxf(m, wave_max64(in ? sk : -INFINITY));  // position base is valid: finite
+        const float pk = in ? __builtin_amdgcn_exp2f(sk - mn) : 0.f;
+        const float alpha = __builtin_amdgcn_exp2f(m - mn);  // 0 on the first round (m = -inf)
+        l = l * alpha + wave_sum64(pk);
         m = mn;
-        if (kl == 0) {
-#pragma unroll
-            for (int c = 0; c < NI; c++) P[wave][c * PPI + kr] = s[c];
-        }
+        P[wave][kl * PPI + kr] = pk;
         __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
         __builtin_amdgcn_wave_barrier();
         __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
@@ -644,18 +644,20 @@ __global__ __launch_bounds__(64 * W) void k_attn_qh(AttnArgs a, int G) {
         wl[wave] = l;
     }
     __syncthreads();
+    if (wave == 0) {  // per-wavefront weights exp2(m_w - M) / sum_w l_w exp2(m_w - M)
+        const bool act = lane < W && wl[lane < W ? lane : 0] > 0.f;  // idle wavefronts add nothing
+        const float mw = act ? wm[lane] : -INFINITY;
+        const float M = wave_max64(mw);
+        const float f = act ? __builtin_amdgcn_exp2f(mw - M) : 0.f;
+        const float den = wave_sum64(act ? f * wl[lane] : 0.f);
+        if (lane < W) wf[lane] = f / den;
+    }
+    __syncthreads();
     for (int d = tid; d < D; d += 64 * W) {
-        float M = -INFINITY;
+        float num = 0.f;
 #pragma unroll
-        for (int w = 0; w < W; w++) M = fmaxf(M, wm[w]);
-        float num = 0.f, den = 0.f;
-#pragma unroll
-        for (int w = 0; w < W; w++) {
-            const float f = wl[w] > 0.f ? expf(wm[w] - M) : 0.f;  // idle wavefronts add nothing
-            num = fmaf(wo[w][d], f, num);
-            den = fmaf(wl[w], f, den);
-        }
-        a.out[((int64_t)b * hq + qh) * D + d] = num / den;
+        for (int w = 0; w < W; w++) num = fmaf(wo[w][d], wf[w], num);
+        a.out[((int64_t)b * hq + qh) * D + d] = num;
     }
 }
 
@@ -860,8 +862,9 @@ int launch_attention_prefill(const float* q, const void* k, const void* v, float
     return e == hipSuccess ? TL_HIP_OK : hip_fail(e, "prefill attention launch");
 }
 
-bool attention_qh_supported(int kv_dtype, int D) {
-    return (kv_dtype == TL_HIP_F16 && (D == 64 || D == 128)) || (kv_dtype == TL_HIP_F32 && D == 64);
+bool attention_qh_supported(int kv_dtype, int D, int64_t lmax) {
+    return ((kv_dtype == TL_HIP_F16 && (D == 64 || D == 128)) || (kv_dtype == TL_HIP_F32 && D == 64)) &&
+           lmax * D < (int64_t(1) << 31);
 }
 
 // Short-cache form; returns TL_HIP_ERR_ARG (no launch) for shapes it does not cover.
@@ -872,7 +875,7 @@ int launch_attention_qh(const float* q, const void* k, const void* v, int kv_dty
                scale};
     const int G = hq / hkv;
     dim3 grid(hq, B);
-    if (D == 64 && kv_dtype == TL_HIP_F16) k_attn_qh<64, __half, 16><<<grid, 64 * 16, 0, s>>>(a, G);
+    if (D == 64 && kv_dtype == TL_HIP_F16) k_attn_qh<64, __half, 8><<<grid, 64 * 8, 0, s>>>(a, G);
     else if (D == 128 && kv_dtype == TL_HIP_F16) k_attn_qh<128, __half, 8><<<grid, 64 * 8, 0, s>>>(a, G);
     else if (D == 64 && kv_dtype == TL_HIP_F32) k_attn_qh<64, float, 8><<<grid, 64 * 8, 0, s>>>(a, G);
     else {
@@ -1129,7 +1132,7 @@ extern "C" tl_hip_tensor* tl_hip_attention_decode(const tl_hip_tensor* qh, const
     hipStream_t s = cur_stream();
     float* ws = (float*)dev_alloc(attn_workspace_floats((int)B, (int)hkv, (int)(hq / hkv), (int)D, 2 * nsplit) * 4);
     int rc = ws ? TL_HIP_OK : TL_HIP_ERR_ALLOC;
-    if (rc == TL_HIP_OK && !dec && attention_qh_supported(k->dtype, (int)D))
+    if (rc == TL_HIP_OK && !dec && attention_qh_supported(k->dtype, (int)D, lmax))
         rc = launch_attention_qh(q->f32(), k->data, v->data, k->dtype, o->f32(), (int)B, (int)hq, (int)hkv, (int)D,
                                  lmax, hkv * lmax * D, L, nullptr, 0, 0, scale, s);
     else if (rc == TL_HIP_OK && dec)

@@ -180,7 +180,7 @@ int launch_attention_prefill(const float* q, const void* k, const void* v, float
                              int D, int64_t lmax, const int32_t* pos_dev, int64_t pos_host, float scale,
                              hipStream_t s);
 // Short-cache form: one workgroup per (query head, batch item); shapes: attention_qh_supported.
-bool attention_qh_supported(int kv_dtype, int D);
+bool attention_qh_supported(int kv_dtype, int D, int64_t lmax);
 int launch_attention_qh(const float* q, const void* k, const void* v, int kv_dtype, float* out,
                         int B, int hq, int hkv, int D, int64_t lmax, int64_t kv_bstride, int64_t L,
                         const int32_t* len_dev, int len_add, int len_step, float scale, hipStream_t s);

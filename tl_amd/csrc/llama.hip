@@ -394,7 +394,7 @@ static int enqueue_step(Llama* m, float penalty, hipStream_t s) {
         }
         // caches up to 4096 positions: one workgroup per query head in a single launch (the
         // split form's merge launch costs more than its wider spread saves at these lengths)
-        if (m->max_seq <= 4096 && attention_qh_supported(m->kv_f16 ? TL_HIP_F16 : TL_HIP_F32, (int)hd))
+        if (m->max_seq <= 4096 && attention_qh_supported(m->kv_f16 ? TL_HIP_F16 : TL_HIP_F32, (int)hd, m->max_seq))
             rc = launch_attention_qh(m->q, m->kc[l], m->vc[l], m->kv_f16 ? TL_HIP_F16 : TL_HIP_F32, m->ao, 1, m->H,
                                      m->KV, (int)hd, m->max_seq, 0, 0, m->pos, 1, 0, 1.0f / sqrtf((float)hd), s);
         else if (attention_gq_supported(m->kv_f16 ? TL_HIP_F16 : TL_HIP_F32, m->H, m->KV, (int)hd))
