@@ -153,7 +153,10 @@ __device__ __forceinline__ float xreduce(float (&v)[N], int lane) {
 
 constexpr int MV_MAX_RW = 32;  // rows per workgroup
 constexpr int XPAD = 36;       // floats per staged 32-float block: lane-per-block LDS reads hit distinct banks
-constexpr int XR = 8;          // float4 per thread staged ahead of the weight loads
+// float4 per thread staged ahead of the weight loads: k <= 8192 at 256 threads in one pass;
+// with the RMSNorm prologue (norm weights staged too) k <= 4096, which keeps those kernels at
+// three workgroups' worth of registers per SIMD
+constexpr int XR = 8, XR_NORM = 4;
 
 // Launch shape: S = 1 << s_shift row subsets of tc threads each (tc a multiple of 64 and,
 // when S > 1, a power of two 1 << tc_shift).
@@ -237,25 +240,26 @@ __global__ __launch_bounds__(256) void k_mv(MvArgs a, MvShape sh) {
         if (base == 0) {
             // (1) the activations (all passes) are staged once per workgroup in LDS with
             // coalesced loads -- a lane reading its own 128-byte block straight from memory
-            // would touch 64 cache lines per load instruction.  The first XR float4 per
+            // would touch 64 cache lines per load instruction.  The first XRK float4 per
             // thread are requested before the weights of the first pass, the stores follow
             // them, so the weight stream is in flight while the staging completes.
             const float* xsrc = EMBED ? a.x + (size_t)(*a.embed_id) * k : a.x;
             const uint32_t k4 = k >> 2, nthr = blockDim.x;
             float s2[M];
-            float4 xr[M][XR], gr[NORM ? XR : 1];
+            constexpr int XRK = NORM ? XR_NORM : XR;
+            float4 xr[M][XRK], gr[NORM ? XRK : 1];
 #pragma unroll
             for (int m = 0; m < M; m++) {
                 s2[m] = 0.f;
 #pragma unroll
-                for (int j = 0; j < XR; j++) {
+                for (int j = 0; j < XRK; j++) {
                     const uint32_t e = tid + j * nthr;
                     if (e < k4) xr[m][j] = reinterpret_cast<const float4*>(xsrc + m * k)[e];
                 }
             }
             if constexpr (NORM) {
 #pragma unroll
-                for (int j = 0; j < XR; j++) {
+                for (int j = 0; j < XRK; j++) {
                     const uint32_t e = tid + j * nthr;
                     if (e < k4) gr[j] = reinterpret_cast<const float4*>(a.norm_w)[e];
                 }
@@ -277,11 +281,11 @@ __global__ __launch_bounds__(256) void k_mv(MvArgs a, MvShape sh) {
 #pragma unroll
             for (int m = 0; m < M; m++) {
 #pragma unroll
-                for (int j = 0; j < XR; j++) {
+                for (int j = 0; j < XRK; j++) {
                     const uint32_t e = tid + j * nthr;
                     if (e < k4) stage(m, e, xr[m][j], NORM ? gr[j] : xr[m][j]);
                 }
-                for (uint32_t e = tid + XR * nthr; e < k4; e += nthr) {  // long rows only
+                for (uint32_t e = tid + XRK * nthr; e < k4; e += nthr) {  // long rows only
                     const float4 v = reinterpret_cast<const float4*>(xsrc + m * k)[e];
                     stage(m, e, v, NORM ? reinterpret_cast<const float4*>(a.norm_w)[e] : v);
                 }
