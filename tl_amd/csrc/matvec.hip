@@ -154,9 +154,10 @@ __device__ __forceinline__ float xreduce(float (&v)[N], int lane) {
 constexpr int MV_MAX_RW = 32;  // rows per workgroup
 constexpr int XPAD = 36;       // floats per staged 32-float block: lane-per-block LDS reads hit distinct banks
 // float4 per thread staged ahead of the weight loads: k <= 8192 at 256 threads in one pass;
-// with the RMSNorm prologue (norm weights staged too) k <= 4096, which keeps those kernels at
-// three workgroups' worth of registers per SIMD
-constexpr int XR = 8, XR_NORM = 4;
+// with the RMSNorm prologue (norm weights staged too) k <= 4096, and k <= 2048 when a thread
+// also holds eight rows' weights -- the register budget that keeps the wide decode grids
+// (704 / 1000 workgroups) resident in one pass; longer rows stage the rest in a loop
+constexpr int XR = 8, XR_NORM = 4, XR_NORM8 = 2;
 
 // Launch shape: S = 1 << s_shift row subsets of tc threads each (tc a multiple of 64 and,
 // when S > 1, a power of two 1 << tc_shift).
@@ -246,7 +247,7 @@ __global__ __launch_bounds__(256) void k_mv(MvArgs a, MvShape sh) {
             const float* xsrc = EMBED ? a.x + (size_t)(*a.embed_id) * k : a.x;
             const uint32_t k4 = k >> 2, nthr = blockDim.x;
             float s2[M];
-            constexpr int XRK = NORM ? XR_NORM : XR;
+            constexpr int XRK = NORM ? (RWT >= 8 ? XR_NORM8 : XR_NORM) : XR;
             float4 xr[M][XRK], gr[NORM ? XRK : 1];
 #pragma unroll
             for (int m = 0; m < M; m++) {
