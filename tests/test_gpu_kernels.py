@@ -90,6 +90,20 @@ def test_quant_gemm_f32_and_f16(dev, t, m, nk):
     assert_rel(y16, ref, F16_TOL)
 
 
+@pytest.mark.parametrize("t", [GGML_Q4_0, GGML_Q8_0])
+@pytest.mark.parametrize("m,n", [(512, 8192), (512, 8160), (300, 8192)])
+def test_quant_gemm_f16_tile_widths(dev, t, m, n):
+    """The f16 MFMA GEMM's two tile widths: 128 x 64 tiles when they give >= 512 workgroups
+    (512 x 8192 and a row count off the tile), 128 x 32 below that (300 rows: 3 x 128 row
+    tiles); short K keeps the oracle fast."""
+    k = 256
+    rng = np.random.default_rng(0x71530000 + m + n + t)
+    raw = blocks(t, rng, n, k)
+    x = rng.standard_normal((m, k)).astype(np.float32)
+    ref = oracle.qtensor_matmul(x, raw, t, n)
+    assert_rel(dev.tl_qtensor_matmul_f16(dev.tensor_new(x), QTensor(t, raw, (n, k))).to_numpy(), ref, F16_TOL)
+
+
 def test_qtensor_matmul_shapes_and_errors(dev):
     rng = np.random.default_rng(5)
     raw = random_q4_0_blocks(rng, 64, 128)

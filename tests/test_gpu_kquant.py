@@ -85,6 +85,18 @@ def test_kquant_gemm(dev, t, m, nk):
     assert_rel(dev.tl_qtensor_matmul_f16(xt, q).to_numpy(), ref, F16_TOL)
 
 
+@pytest.mark.parametrize("t", [GGML_Q4_K, GGML_Q6_K])
+def test_kquant_gemm_f16_wide_tiles(dev, t):
+    """512 x 8192 outputs: the f16 GEMM on the dequantized weights with 128 x 64 tiles (the
+    shapes above all take the 128 x 32 tiles); short K keeps the oracle fast."""
+    m, n, k = 512, 8192, 256
+    rng = np.random.default_rng(0x71570000 + t)
+    raw = blocks(t, rng, n, k)
+    x = rng.standard_normal((m, k)).astype(np.float32)
+    ref = oracle.qtensor_matmul(x, raw, t, n)
+    assert_rel(dev.tl_qtensor_matmul_f16(dev.tensor_new(x), QTensor(t, raw, (n, k))).to_numpy(), ref, F16_TOL)
+
+
 def test_kquant_upload_errors(dev):
     with pytest.raises(BackendError) as e:  # quantized.rs:347-352
         dev.qtensor_dequantize(QTensor(GGML_Q4_K, bytes(143), (1, 256)))
