@@ -289,7 +289,7 @@ __device__ __forceinline__ void lds_dma4(const void* src, void* lds) {
 #endif
 }
 
-template <int QT, int BM, int BN, int NS>  // NS pipeline stages (LDS: X + W per stage)
+template <int QT, int BM, int BN>
 __global__ __launch_bounds__(512) void k_qgemm_mfma(const uint8_t* __restrict__ qs, const __half* __restrict__ dsc,
                                                     const _Float16* __restrict__ x16, float* __restrict__ y,
                                                     int64_t m, int64_t n, int64_t k, int64_t nb) {
@@ -311,9 +311,15 @@ __global__ __launch_bounds__(512) void k_qgemm_mfma(const uint8_t* __restrict__ 
     //  * W: BN rows x CPR chunks, chunk c of row r at (c + (r >> RSH)) mod CPR, and BN x 4
     //    scales.  Both swizzles make the 16 lanes that read one operand column hit 16
     //    distinct 16-byte bank groups.
-    __shared__ __attribute__((aligned(16))) _Float16 Xs[NS][BM * 128];
-    __shared__ __attribute__((aligned(16))) uint8_t Wq[NS][BN * CPR * 16];
-    __shared__ __attribute__((aligned(16))) uint32_t Wd[NS][SCALED ? BN * Q_KR : 1];  // aligned word holding the scale
+    // Two stages, each its own LDS object: the compiler's wait insertion can then see that a
+    // stage being filled by DMA is not the one being read, and the next iteration's loads
+    // overlap this iteration's MFMAs (with one array indexed by stage it waits for them).
+    struct Stage {
+        _Float16 X[BM * 128];
+        uint8_t Wq[BN * CPR * 16];
+        uint32_t Wd[SCALED ? BN * Q_KR : 1];  // aligned word holding the scale
+    };
+    __shared__ __attribute__((aligned(16))) Stage S0, S1;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int sub = wave & 3, kh = wave >> 2;  // output sub-tile, k half
     const int wm = sub >> 1, wn = sub & 1, col = lane & 15, g = lane >> 4;
@@ -348,17 +354,17 @@ __global__ __launch_bounds__(512) void k_qgemm_mfma(const uint8_t* __restrict__ 
         const int64_t row = n0 + (slot >> 2) < n ? n0 + (slot >> 2) : n - 1;
         doff = (uint32_t)(((row * nb + (slot & 3)) >> 1) * 4);
     }
-    auto issue = [&](int64_t kb, int st) {
+    auto issue = [&](int64_t kb, Stage& st) {
         const char* src = reinterpret_cast<const char*>(x16) + kb * 64;  // 32 halves per block
 #pragma unroll
-        for (int u = 0; u < XI; u++) lds_dma16(src + xoff[u], &Xs[st][(wave * XI + u) * 64 * 8]);
+        for (int u = 0; u < XI; u++) lds_dma16(src + xoff[u], &st.X[(wave * XI + u) * 64 * 8]);
         if (wave < WW) {
 #pragma unroll
             for (int u = 0; u < WPT; u++)
-                lds_dma16(reinterpret_cast<const char*>(qs) + kb * QB + woff[u], &Wq[st][(wave * WPT + u) * 64 * 16]);
+                lds_dma16(reinterpret_cast<const char*>(qs) + kb * QB + woff[u], &st.Wq[(wave * WPT + u) * 64 * 16]);
         }
         if (DW > 0 && wave >= 8 - DW)  // kb even: whole words
-            lds_dma4(reinterpret_cast<const char*>(dsc) + kb * 2 + doff, &Wd[st][(wave - (8 - DW)) * 64]);
+            lds_dma4(reinterpret_cast<const char*>(dsc) + kb * 2 + doff, &st.Wd[(wave - (8 - DW)) * 64]);
     };
     uint32_t dpar[TN];  // which half of its word holds this lane's scale (kb is even)
 #pragma unroll
@@ -369,7 +375,7 @@ __global__ __launch_bounds__(512) void k_qgemm_mfma(const uint8_t* __restrict__ 
     }
     // This wavefront's half of the iteration: k-steps t = 2 kh, 2 kh + 1.  Every LDS read
     // (W quants, scale words, A fragments) is issued before the first use.
-    auto compute = [&](int st) {
+    auto compute = [&](const Stage& st) {
         // quant data of the wavefront's rows: the whole block (scaled types), or the two
         // operand words of its k-steps (f16 weights)
         constexpr int NW = SCALED ? QC : 2;
@@ -381,11 +387,11 @@ __global__ __launch_bounds__(512) void k_qgemm_mfma(const uint8_t* __restrict__ 
 #pragma unroll
             for (int h = 0; h < NW; h++) {
                 const int c = SCALED ? g * QC + h : g * QC + 2 * kh + h;
-                wr[j][h] = *reinterpret_cast<const uint4*>(&Wq[st][(r * CPR + ((c + (r >> RSH)) & (CPR - 1))) * 16]);
+                wr[j][h] = *reinterpret_cast<const uint4*>(&st.Wq[(r * CPR + ((c + (r >> RSH)) & (CPR - 1))) * 16]);
             }
-            if constexpr (SCALED) dw[j] = Wd[st][r * Q_KR + g];
+            if constexpr (SCALED) dw[j] = st.Wd[r * Q_KR + g];
         }
-        const _Float16* xs = Xs[st];
+        const _Float16* xs = st.X;
         half8 a[2][TM];
 #pragma unroll
         for (int tt = 0; tt < 2; tt++)
@@ -417,23 +423,27 @@ __global__ __launch_bounds__(512) void k_qgemm_mfma(const uint8_t* __restrict__ 
         }
     };
 
-    // Stage it % NS holds X and W of iteration it; the loads of it + 1 .. it + NS - 1 are in
-    // flight while it computes.  The barrier after the wait makes every wavefront's chunks
-    // visible and frees the stage iteration it - 1 read.
-    const int64_t iters = nb / Q_KR;
-    for (int64_t i0 = 0; i0 < NS - 1 && i0 < iters; i0++) issue(i0 * Q_KR, (int)i0);
-    for (int64_t it = 0; it < iters; it++) {
-        __builtin_amdgcn_s_waitcnt(0xF70);  // vmcnt(0); the encoding carries no lgkm / exp wait
+    // S0 holds the even iterations, S1 the odd ones; the loads of iteration it + 1 are in
+    // flight while it computes.  The wait + barrier at the top of an iteration make every
+    // wavefront's chunks visible and free the stage the previous iteration read.
+    const int64_t iters = nb / Q_KR;  // >= 1: K is a multiple of 128
+    auto step = [&](int64_t it, const Stage& cur, Stage& next) {
+        __builtin_amdgcn_s_waitcnt(0xF70);  // vmcnt(0): this iteration's DMA has landed
         __syncthreads();
         __builtin_amdgcn_sched_barrier(0);
-        if (it + NS - 1 < iters) issue((it + NS - 1) * Q_KR, (int)((it + NS - 1) % NS));
+        if (it + 1 < iters) issue((it + 1) * Q_KR, next);
         __builtin_amdgcn_sched_barrier(0);
-        compute((int)(it % NS));
+        compute(cur);
+    };
+    issue(0, S0);
+    for (int64_t it = 0; it < iters; it += 2) {
+        step(it, S0, S1);
+        if (it + 1 < iters) step(it + 1, S1, S0);
     }
-    // the k half kh = 1 hands its sums to kh = 0 through the (now free) X stages
-    static_assert(4 * TM * TN * 256 * 4 <= NS * BM * 128 * 2, "reduction space");
+    // the k half kh = 1 hands its sums to kh = 0 through the (now free) X tile of S0
+    static_assert(4 * TM * TN * 256 * 4 <= BM * 128 * 2, "reduction space");
     __syncthreads();
-    float* red = reinterpret_cast<float*>(&Xs[0][0]);
+    float* red = reinterpret_cast<float*>(S0.X);
     if (kh == 1) {
 #pragma unroll
         for (int i = 0; i < TM; i++)
@@ -491,8 +501,8 @@ int launch_quant_gemm(const QWeight* w, const float* x, float* y, int64_t m, hip
         const int64_t tiles = cdiv(m, BM) * cdiv(w->n, wide ? 64 : 32);
         auto gemm = [&](auto qt, const uint8_t* q, const __half* d) {
             constexpr int QT = decltype(qt)::value;
-            if (wide) k_qgemm_mfma<QT, BM, 64, 2><<<(unsigned)tiles, 512, 0, s>>>(q, d, x16, y, m, w->n, w->k, w->nb);
-            else k_qgemm_mfma<QT, BM, 32, 2><<<(unsigned)tiles, 512, 0, s>>>(q, d, x16, y, m, w->n, w->k, w->nb);
+            if (wide) k_qgemm_mfma<QT, BM, 64><<<(unsigned)tiles, 512, 0, s>>>(q, d, x16, y, m, w->n, w->k, w->nb);
+            else k_qgemm_mfma<QT, BM, 32><<<(unsigned)tiles, 512, 0, s>>>(q, d, x16, y, m, w->n, w->k, w->nb);
         };
         if (w->ggml_type == TL_HIP_GGML_Q4_K || w->ggml_type == TL_HIP_GGML_Q6_K) {
             // K-quants: dequantize once into f16 operand order (n * k halves), then the same
