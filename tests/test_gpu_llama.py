@@ -144,6 +144,39 @@ def test_tinyllama_greedy_golden():
     assert list(got16) == gold["tokens"]
 
 
+def _q8_handoff_plan(cfg, layer, which):
+    # each f16 GEMM input written in the operand order of its reader: Q8_0 and Q4_0 alternate
+    return {"attn_q": 8, "attn_k": 8, "attn_v": 8, "attn_output": 2, "ffn_gate": 8, "ffn_up": 8,
+            "ffn_down": 2}.get(which, 8)
+
+
+@pytest.mark.parametrize("plan", ["Q8_0", "q8_handoff", "Q4_K_M", "mixed"])
+def test_f16_prefill_weight_mixtures(plan):
+    """The f16 prefill (activations passed between GEMMs as f16 operand words, residual and
+    SwiGLU in the GEMM epilogues) over weight mixtures: all Q8_0, Q8_0 / Q4_0 alternating
+    between producer and reader, llama.cpp's Q4_K_M, and gate / up of different types (the
+    unfused path).  Head size 64 with 8 query heads per KV head (MFMA attention).  Logits
+    within the f16 tolerance of the oracle, then decode steps."""
+    cfg = LlamaConfig(2, 512, 8, 1, 512, 1000, max_seq=128)
+    gt = {"Q8_0": 8, "q8_handoff": _q8_handoff_plan, "Q4_K_M": "Q4_K_M", "mixed": _mixed_plan}[plan]
+    tensors = list(synthetic_weights(cfg, 43, ggml_type=gt))
+    gpu = HipLlama(cfg, kv_f16=True)
+    gpu.load(tensors, ggml_type=gt)
+    cpu = oracle.Llama(cfg)
+    cpu.load(tensors, ggml_type=gt)
+    try:
+        prompt = synthetic_prompt(cfg, 43, 77)
+        cpu.reset()
+        err = max_rel(gpu.forward(prompt, prefill_f16=True), cpu.forward(prompt))
+        assert err <= 1e-2, f"f16 prefill logits max-rel-err {err:.2e}"
+        for t in ([4], [998]):
+            err = max_rel(gpu.forward(t), cpu.forward(t))
+            assert err <= 1e-2, f"decode logits after the f16 prefill: max-rel-err {err:.2e}"
+    finally:
+        gpu.close()
+        cpu.close()
+
+
 def _mixed_plan(cfg, layer, which):
     # every grouping case of the loader: q | k | v in three runs, gate and up of different types
     return {"attn_q": 14, "attn_k": 12, "attn_v": 14, "ffn_gate": 14, "ffn_up": 12}.get(which, 12)

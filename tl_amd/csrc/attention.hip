@@ -681,7 +681,8 @@ template <int D, int G>
 __global__ __launch_bounds__(256) void k_attn_prefill(const float* __restrict__ q, const __half* __restrict__ kc,
                                                       const __half* __restrict__ vc, float* __restrict__ out,
                                                       int n, int hkv, int64_t lmax, const int32_t* __restrict__ pos_dev,
-                                                      int64_t pos_host, float scale) {
+                                                      int64_t pos_host, float scale, _Float16* __restrict__ out16,
+                                                      int order) {
     constexpr int QB = 128 / G;   // queries per workgroup
     constexpr int KT = 64;        // positions per KV tile
     constexpr int KS = D / 32;    // MFMA k-steps over the head dim
@@ -823,16 +824,26 @@ __global__ __launch_bounds__(256) void k_attn_prefill(const float* __restrict__ 
             }
         }
     }
-    // out[query][head][dims 16 dt + 4 g .. +3] = O / l
+    // out[query][head][dims 16 dt + 4 g .. +3] = O / l, f32 or (out16) f16 in the operand order
+    // of the GEMM that reads the [n, hq D] rows
 #pragma unroll
     for (int rt = 0; rt < 2; rt++) {
         if (qi[rt] >= n) continue;
         const float rl = 1.0f / lrow[rt];
-        float* op = out + ((int64_t)qi[rt] * hq + hh[rt]) * D;
+        if (out16) {
 #pragma unroll
-        for (int dt = 0; dt < D / 16; dt++)
-            *reinterpret_cast<float4*>(op + 16 * dt + 4 * g) =
-                make_float4(o[rt][dt][0] * rl, o[rt][dt][1] * rl, o[rt][dt][2] * rl, o[rt][dt][3] * rl);
+            for (int dt = 0; dt < D / 16; dt++)
+#pragma unroll
+                for (int i = 0; i < 4; i++)
+                    out16[f16q_index(qi[rt], (int64_t)hh[rt] * D + 16 * dt + 4 * g + i, (int64_t)hq * D, order)] =
+                        (_Float16)(o[rt][dt][i] * rl);
+        } else {
+            float* op = out + ((int64_t)qi[rt] * hq + hh[rt]) * D;
+#pragma unroll
+            for (int dt = 0; dt < D / 16; dt++)
+                *reinterpret_cast<float4*>(op + 16 * dt + 4 * g) =
+                    make_float4(o[rt][dt][0] * rl, o[rt][dt][1] * rl, o[rt][dt][2] * rl, o[rt][dt][3] * rl);
+        }
     }
 }
 
@@ -843,16 +854,16 @@ bool attention_prefill_supported(int kv_dtype, int hq, int hkv, int D) {
 
 int launch_attention_prefill(const float* q, const void* k, const void* v, float* out, int n, int hq, int hkv,
                              int D, int64_t lmax, const int32_t* pos_dev, int64_t pos_host, float scale,
-                             hipStream_t s) {
+                             hipStream_t s, _Float16* out16, int order) {
     const int G = hq / hkv;
     if (n < 1) return TL_HIP_OK;
     dim3 grid((unsigned)cdiv(n, 128 / G), hkv);
     const __half* kh = static_cast<const __half*>(k);
     const __half* vh = static_cast<const __half*>(v);
-    if (D == 64 && G == 8) k_attn_prefill<64, 8><<<grid, 256, 0, s>>>(q, kh, vh, out, n, hkv, lmax, pos_dev, pos_host, scale);
-    else if (D == 64 && G == 4) k_attn_prefill<64, 4><<<grid, 256, 0, s>>>(q, kh, vh, out, n, hkv, lmax, pos_dev, pos_host, scale);
-    else if (D == 128 && G == 8) k_attn_prefill<128, 8><<<grid, 256, 0, s>>>(q, kh, vh, out, n, hkv, lmax, pos_dev, pos_host, scale);
-    else if (D == 128 && G == 4) k_attn_prefill<128, 4><<<grid, 256, 0, s>>>(q, kh, vh, out, n, hkv, lmax, pos_dev, pos_host, scale);
+    if (D == 64 && G == 8) k_attn_prefill<64, 8><<<grid, 256, 0, s>>>(q, kh, vh, out, n, hkv, lmax, pos_dev, pos_host, scale, out16, order);
+    else if (D == 64 && G == 4) k_attn_prefill<64, 4><<<grid, 256, 0, s>>>(q, kh, vh, out, n, hkv, lmax, pos_dev, pos_host, scale, out16, order);
+    else if (D == 128 && G == 8) k_attn_prefill<128, 8><<<grid, 256, 0, s>>>(q, kh, vh, out, n, hkv, lmax, pos_dev, pos_host, scale, out16, order);
+    else if (D == 128 && G == 4) k_attn_prefill<128, 4><<<grid, 256, 0, s>>>(q, kh, vh, out, n, hkv, lmax, pos_dev, pos_host, scale, out16, order);
     else {
         set_error(TL_HIP_ERR_ARG, "ArgumentError: prefill attention covers f16 caches, head_dim 64 / 128, 4 or 8 query "
                   "heads per KV head");

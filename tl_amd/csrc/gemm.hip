@@ -13,9 +13,6 @@
 
 namespace tlhip {
 
-typedef _Float16 half8 __attribute__((ext_vector_type(8)));
-typedef float floatx4 __attribute__((ext_vector_type(4)));
-
 // Residency buffers of a quantized weight (layout at struct QWeight).
 struct QView {
     const uint8_t* qs;
@@ -291,8 +288,8 @@ __device__ __forceinline__ void lds_dma4(const void* src, void* lds) {
 
 template <int QT, int BM, int BN>
 __global__ __launch_bounds__(512) void k_qgemm_mfma(const uint8_t* __restrict__ qs, const __half* __restrict__ dsc,
-                                                    const _Float16* __restrict__ x16, float* __restrict__ y,
-                                                    int64_t m, int64_t n, int64_t k, int64_t nb) {
+                                                    const _Float16* __restrict__ x16, float* y, int64_t m,
+                                                    int64_t n, int64_t k, int64_t nb, GemmEpi ep) {
     constexpr int TM = BM / 32, TN = BN / 32;  // 16 x 16 tiles per wavefront
     constexpr int QB = QWords<QT>::BYTES;
     constexpr int QC = QB / 16;                // 16-byte chunks per quant block
@@ -462,12 +459,74 @@ __global__ __launch_bounds__(512) void k_qgemm_mfma(const uint8_t* __restrict__ 
 #pragma unroll
                 for (int e = 0; e < 4; e++) {
                     const int64_t r = m0 + wm * (BM / 2) + 16 * i + 4 * g + e;
-                    if (r < m && c < n) y[r * n + c] = acc[i][j][e] + o[e];
+                    const float v = acc[i][j][e] + o[e];
+                    if (ep.mode == GEMM_GLU16) {
+                        // columns (2i, 2i + 1) = (gate_i, up_i) sit in lanes col, col ^ 1
+                        const float u = __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(
+                                                                      __builtin_bit_cast(int, v), 0xB1, 0xF, 0xF, true));
+                        if ((col & 1) == 0 && r < m && c < n) {
+                            const float a = (v * (1.0f / (1.0f + expf(-v)))) * u;  // silu(gate) * up
+                            ep.out16[f16q_index(r, c >> 1, n >> 1, ep.order)] = (_Float16)a;
+                        }
+                    } else if (r < m && c < n) {
+                        y[r * n + c] = ep.mode == GEMM_RES ? ep.res[r * n + c] + v : v;
+                    }
                 }
             }
     }
 }
 
+
+int f16q_order(int ggml_type) { return ggml_type == TL_HIP_GGML_Q8_0 ? F16Q_Q8 : F16Q_Q4; }
+
+int launch_x_to_f16q(const float* x, _Float16* x16, int64_t m, int64_t k, int order, hipStream_t s) {
+    const int64_t units = m * (k / 32) * 4;
+    if (order == F16Q_Q8) k_x_to_f16q<TL_HIP_GGML_Q8_0><<<(unsigned)cdiv(units, 256), 256, 0, s>>>(x, x16, units);
+    else k_x_to_f16q<TL_HIP_GGML_Q4_0><<<(unsigned)cdiv(units, 256), 256, 0, s>>>(x, x16, units);
+    hipError_t e = hipGetLastError();
+    return e == hipSuccess ? TL_HIP_OK : hip_fail(e, "x -> f16 launch");
+}
+
+int launch_gemm_f16q(const QWeight* w, const _Float16* x16, float* y, int64_t m, const GemmEpi& ep,
+                     hipStream_t s) {
+    if (m < 1) return TL_HIP_OK;
+    if (w->nb % Q_KR != 0 || (ep.mode == GEMM_GLU16 && (w->n % 64 != 0))) {
+        set_error(TL_HIP_ERR_ARG, "ArgumentError: the f16 GEMM takes K in steps of 128 (SwiGLU output: N in steps "
+                  "of 64)");
+        return TL_HIP_ERR_ARG;
+    }
+    // 128 x 64 tiles when that gives at least two workgroups per CU, else 128 x 32 (twice
+    // the workgroups; measured at M = 512: 2048 x 2048 18.7 -> 15.5 us, 4096 x 4096
+    // 41.0 -> 37.3 us, while 11008 x 4096 is faster with the wide tile, 84.5 vs 101.7 us)
+    constexpr int BM = 128;
+    const bool wide = cdiv(m, BM) * cdiv(w->n, 64) >= 512;
+    const int64_t tiles = cdiv(m, BM) * cdiv(w->n, wide ? 64 : 32);
+    auto gemm = [&](auto qt, const uint8_t* q, const __half* d) {
+        constexpr int QT = decltype(qt)::value;
+        if (wide) k_qgemm_mfma<QT, BM, 64><<<(unsigned)tiles, 512, 0, s>>>(q, d, x16, y, m, w->n, w->k, w->nb, ep);
+        else k_qgemm_mfma<QT, BM, 32><<<(unsigned)tiles, 512, 0, s>>>(q, d, x16, y, m, w->n, w->k, w->nb, ep);
+    };
+    if (w->ggml_type == TL_HIP_GGML_Q4_K || w->ggml_type == TL_HIP_GGML_Q6_K) {
+        // K-quants: dequantize once into f16 operand order (n * k halves), then the same
+        // MFMA pipeline with the weights read as stored
+        _Float16* w16 = static_cast<_Float16*>(dev_alloc((size_t)w->n * w->k * sizeof(_Float16)));
+        if (!w16) return TL_HIP_ERR_ALLOC;
+        const QView qv{w->qs, w->d, w->hdr, w->qh, w->sc};
+        const int64_t wunits = w->n * w->nb;
+        if (w->ggml_type == TL_HIP_GGML_Q4_K)
+            k_dequant_f16q<TL_HIP_GGML_Q4_K><<<(unsigned)cdiv(wunits, 256), 256, 0, s>>>(qv, w16, wunits);
+        else
+            k_dequant_f16q<TL_HIP_GGML_Q6_K><<<(unsigned)cdiv(wunits, 256), 256, 0, s>>>(qv, w16, wunits);
+        gemm(std::integral_constant<int, TL_HIP_GGML_F16>{}, reinterpret_cast<const uint8_t*>(w16), nullptr);
+        dev_free(w16);
+    } else if (w->ggml_type == TL_HIP_GGML_Q4_0) {
+        gemm(std::integral_constant<int, TL_HIP_GGML_Q4_0>{}, w->qs, w->d);
+    } else {
+        gemm(std::integral_constant<int, TL_HIP_GGML_Q8_0>{}, w->qs, w->d);
+    }
+    hipError_t e = hipGetLastError();
+    return e == hipSuccess ? TL_HIP_OK : hip_fail(e, "quant gemm launch");
+}
 
 int launch_quant_gemm(const QWeight* w, const float* x, float* y, int64_t m, hipStream_t s,
                       int mode) {
@@ -476,7 +535,6 @@ int launch_quant_gemm(const QWeight* w, const float* x, float* y, int64_t m, hip
         set_error(TL_HIP_ERR_ARG, "ArgumentError: x must be 16-byte aligned");
         return TL_HIP_ERR_ARG;
     }
-    const bool q4 = w->ggml_type == TL_HIP_GGML_Q4_0;
     if (mode != 0 && w->nb % Q_KR != 0) mode = 0;  // the MFMA pipeline takes K in steps of 128
 
     if (mode == 0) {
@@ -492,43 +550,10 @@ int launch_quant_gemm(const QWeight* w, const float* x, float* y, int64_t m, hip
         // X -> f16 in the operand k order (a workspace of m * k halves), then the MFMA GEMM
         _Float16* x16 = static_cast<_Float16*>(dev_alloc((size_t)m * w->k * sizeof(_Float16)));
         if (!x16) return TL_HIP_ERR_ALLOC;
-        const int64_t units = m * w->nb * 4;
-        // 128 x 64 tiles when that gives at least two workgroups per CU, else 128 x 32 (twice
-        // the workgroups; measured at M = 512: 2048 x 2048 18.7 -> 15.5 us, 4096 x 4096
-        // 41.0 -> 37.3 us, while 11008 x 4096 is faster with the wide tile, 84.5 vs 101.7 us)
-        constexpr int BM = 128;
-        const bool wide = cdiv(m, BM) * cdiv(w->n, 64) >= 512;
-        const int64_t tiles = cdiv(m, BM) * cdiv(w->n, wide ? 64 : 32);
-        auto gemm = [&](auto qt, const uint8_t* q, const __half* d) {
-            constexpr int QT = decltype(qt)::value;
-            if (wide) k_qgemm_mfma<QT, BM, 64><<<(unsigned)tiles, 512, 0, s>>>(q, d, x16, y, m, w->n, w->k, w->nb);
-            else k_qgemm_mfma<QT, BM, 32><<<(unsigned)tiles, 512, 0, s>>>(q, d, x16, y, m, w->n, w->k, w->nb);
-        };
-        if (w->ggml_type == TL_HIP_GGML_Q4_K || w->ggml_type == TL_HIP_GGML_Q6_K) {
-            // K-quants: dequantize once into f16 operand order (n * k halves), then the same
-            // MFMA pipeline with the weights read as stored
-            _Float16* w16 = static_cast<_Float16*>(dev_alloc((size_t)w->n * w->k * sizeof(_Float16)));
-            if (!w16) {
-                dev_free(x16);
-                return TL_HIP_ERR_ALLOC;
-            }
-            const QView qv{w->qs, w->d, w->hdr, w->qh, w->sc};
-            const int64_t wunits = w->n * w->nb;
-            if (w->ggml_type == TL_HIP_GGML_Q4_K)
-                k_dequant_f16q<TL_HIP_GGML_Q4_K><<<(unsigned)cdiv(wunits, 256), 256, 0, s>>>(qv, w16, wunits);
-            else
-                k_dequant_f16q<TL_HIP_GGML_Q6_K><<<(unsigned)cdiv(wunits, 256), 256, 0, s>>>(qv, w16, wunits);
-            k_x_to_f16q<TL_HIP_GGML_Q4_0><<<(unsigned)cdiv(units, 256), 256, 0, s>>>(x, x16, units);
-            gemm(std::integral_constant<int, TL_HIP_GGML_F16>{}, reinterpret_cast<const uint8_t*>(w16), nullptr);
-            dev_free(w16);
-        } else if (q4) {
-            k_x_to_f16q<TL_HIP_GGML_Q4_0><<<(unsigned)cdiv(units, 256), 256, 0, s>>>(x, x16, units);
-            gemm(std::integral_constant<int, TL_HIP_GGML_Q4_0>{}, w->qs, w->d);
-        } else {
-            k_x_to_f16q<TL_HIP_GGML_Q8_0><<<(unsigned)cdiv(units, 256), 256, 0, s>>>(x, x16, units);
-            gemm(std::integral_constant<int, TL_HIP_GGML_Q8_0>{}, w->qs, w->d);
-        }
-        dev_free(x16);
+        int rc = launch_x_to_f16q(x, x16, m, w->k, f16q_order(w->ggml_type), s);
+        if (rc == TL_HIP_OK) rc = launch_gemm_f16q(w, x16, y, m, GemmEpi{GEMM_PLAIN, nullptr, nullptr, 0}, s);
+        dev_free(x16);  // stream-ordered: reused only by later work on the same stream
+        if (rc) return rc;
     }
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return hip_fail(e, "quant gemm launch");

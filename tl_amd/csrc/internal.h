@@ -138,12 +138,51 @@ int launch_quant_matvec(const QWeight* w, const float* x, float* y, int64_t m, h
                         const float* residual);
 int launch_quant_gemm(const QWeight* w, const float* x, float* y, int64_t m, hipStream_t s,
                       int mode);
+// The f16 MFMA GEMM on an input already in f16 operand order (x16 [m, k]: every 32-element
+// block stored as four 8-half words, the k slots of the MFMA operands).  Two orders: F16Q_Q4
+// (word t = elements 4t..4t+3, 16+4t..16+4t+3; Q4_0 and the f16-dequantized K-quants) and
+// F16Q_Q8 (word t = 8t, 8t+2, 8t+1, 8t+3, 8t+4, 8t+6, 8t+5, 8t+7; Q8_0).
+typedef _Float16 half8 __attribute__((ext_vector_type(8)));  // one operand word
+typedef float floatx4 __attribute__((ext_vector_type(4)));
+enum { F16Q_Q4 = 0, F16Q_Q8 = 1 };
+enum { GEMM_PLAIN = 0, GEMM_RES = 1, GEMM_GLU16 = 2 };
+// Epilogue: PLAIN y = v; RES y = res + v (res may be y); GLU16 columns (2i, 2i + 1) are
+// (gate_i, up_i) and silu(gate_i) * up_i goes to out16 [m, n / 2] in operand order `order`.
+struct GemmEpi {
+    int mode;
+    const float* res;
+    _Float16* out16;
+    int order;
+};
+__host__ __device__ inline int64_t f16q_index(int64_t r, int64_t e, int64_t k, int order) {
+    const int64_t b = e >> 5;
+    const int e32 = (int)(e & 31);
+    int t, slot;
+    if (order == F16Q_Q8) {
+        const int e8 = e32 & 7;
+        t = e32 >> 3;
+        slot = (e8 & 4) | ((e8 & 1) << 1) | ((e8 >> 1) & 1);
+    } else {
+        t = (e32 & 15) >> 2;
+        slot = (e32 & 3) + (e32 & 16 ? 4 : 0);
+    }
+    return ((r * (k >> 5) + b) * 4 + t) * 8 + slot;
+}
+int f16q_order(int ggml_type);  // the operand order the f16 GEMM of this weight type reads
+int launch_x_to_f16q(const float* x, _Float16* x16, int64_t m, int64_t k, int order, hipStream_t s);
+// K a multiple of 128 (TL_HIP_ERR_ARG otherwise); GLU16 also needs N a multiple of 64.
+int launch_gemm_f16q(const QWeight* w, const _Float16* x16, float* y, int64_t m, const GemmEpi& ep,
+                     hipStream_t s);
 int launch_matmul_f32(const float* a, const float* b, float* c, int64_t batch, int64_t m,
                       int64_t k, int64_t n, int64_t a_bstride, int64_t b_bstride,
                       hipStream_t s);
 
 int launch_rmsnorm(const float* x, const float* r, const float* w, float* out, int64_t rows,
                    int64_t n, float eps, int mode, hipStream_t s);
+// mode-0 RMSNorm of [rows, n] written as f16 in GEMM operand order `order` (n % 32 == 0,
+// n <= 8192): the value launch_rmsnorm produces, rounded once.
+int launch_rmsnorm_f16q(const float* x, const float* w, _Float16* out16, int64_t rows, int64_t n, float eps,
+                        int order, hipStream_t s);
 int launch_swiglu(const float* g, const float* u, float* o, int64_t n, int mode, hipStream_t s);
 int launch_softmax(const float* x, float* out, int64_t outer, int64_t as, int64_t inner,
                    hipStream_t s);
@@ -174,11 +213,12 @@ int launch_attention_gq(const float* q, const void* k, const void* v, float* out
 int attention_gq_splits(int64_t L);
 // Causal prefill with f16 MFMA (shapes of attention_prefill_supported): q [n, hq, D] f32 of
 // queries at positions pos0 + i over the cache [hkv, lmax, D] f16; out [n, hq, D].  pos0 is
-// *pos_dev when pos_dev is given, else pos_host; pos0 + n <= lmax.
+// *pos_dev when pos_dev is given, else pos_host; pos0 + n <= lmax.  With out16 the rows go
+// to f16 [n, hq D] in GEMM operand order `order` instead (hq D a multiple of 32).
 bool attention_prefill_supported(int kv_dtype, int hq, int hkv, int D);
 int launch_attention_prefill(const float* q, const void* k, const void* v, float* out, int n, int hq, int hkv,
                              int D, int64_t lmax, const int32_t* pos_dev, int64_t pos_host, float scale,
-                             hipStream_t s);
+                             hipStream_t s, _Float16* out16 = nullptr, int order = 0);
 // Short-cache form: one workgroup per (query head, batch item); shapes: attention_qh_supported.
 bool attention_qh_supported(int kv_dtype, int D, int64_t lmax);
 int launch_attention_qh(const float* q, const void* k, const void* v, int kv_dtype, float* out,

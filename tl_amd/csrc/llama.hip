@@ -125,6 +125,8 @@ struct Llama {
     float *x = nullptr, *h = nullptr, *qkv = nullptr, *q = nullptr, *ao = nullptr, *t = nullptr,
           *gu = nullptr, *act = nullptr, *logits = nullptr, *plogits = nullptr, *ws = nullptr;
     size_t ws_floats = 0;
+    // f16 GEMM inputs in operand order (fused prefill): [n, D] and [n, F]
+    _Float16 *xa16 = nullptr, *xb16 = nullptr;
     int32_t *ids = nullptr, *pos = nullptr, *tok = nullptr, *step = nullptr, *out_ids = nullptr;
     uint8_t* seen = nullptr;
     // greedy-argmax candidates of the LM-head matvec (one per workgroup)
@@ -170,6 +172,9 @@ static int ensure_tokens(Llama* m, int64_t n) {
     }
     dev_free(m->ids);
     dev_free(m->ws);
+    dev_free(m->xa16);
+    dev_free(m->xb16);
+    m->xa16 = m->xb16 = nullptr;
     const int64_t qkv_w = m->D + 2 * (int64_t)m->KV * m->hd;
     m->x = (float*)dev_alloc(n * m->D * 4);
     m->h = (float*)dev_alloc(n * m->D * 4);
@@ -180,6 +185,8 @@ static int ensure_tokens(Llama* m, int64_t n) {
     m->gu = (float*)dev_alloc(n * std::max(2 * (int64_t)m->F, qkv_w) * 4);  // also the q|k|v segment staging
     m->act = (float*)dev_alloc(n * (int64_t)m->F * 4);
     m->ids = (int32_t*)dev_alloc(n * 4);
+    m->xa16 = (_Float16*)dev_alloc(n * m->D * 2);
+    m->xb16 = (_Float16*)dev_alloc(n * (int64_t)m->F * 2);
     // attention workspace: B = n queries, splits of 64 positions over max_seq (the grouped-query
     // kernel's smallest split; 128-position splits use half of it)
     int nsplit = 2 * (int)cdiv(m->max_seq, 128);
@@ -187,7 +194,7 @@ static int ensure_tokens(Llama* m, int64_t n) {
     m->ws = (float*)dev_alloc(m->ws_floats * 4);
     for (float** b : bufs)
         if (!*b) return TL_HIP_ERR_ALLOC;
-    if (!m->ids || !m->ws) return TL_HIP_ERR_ALLOC;
+    if (!m->ids || !m->ws || !m->xa16 || !m->xb16) return TL_HIP_ERR_ALLOC;
     m->max_tok = n;
     free_graph(m);  // captured pointers changed
     return TL_HIP_OK;
@@ -290,17 +297,91 @@ static int check_ready(Llama* m) {
     return TL_HIP_OK;
 }
 
+// RoPE on the q|k rows of n tokens and the k / v append at the device position (prefill).
+static void prefill_rope_kv(Llama* m, int l, int n, hipStream_t s) {
+    const int64_t hd = m->hd;
+    int64_t work = (int64_t)n * ((m->H + m->KV) * hd / 2 + m->KV * hd);
+    if (m->kv_f16)
+        k_rope_kv<__half><<<cdiv(work, 256), 256, 0, s>>>(m->qkv, m->q, (__half*)m->kc[l], (__half*)m->vc[l],
+                                                         m->cos_t, m->sin_t, m->pos, n, m->H, m->KV, (int)hd,
+                                                         m->max_seq, m->rope_per_token);
+    else
+        k_rope_kv<float><<<cdiv(work, 256), 256, 0, s>>>(m->qkv, m->q, (float*)m->kc[l], (float*)m->vc[l],
+                                                        m->cos_t, m->sin_t, m->pos, n, m->H, m->KV, (int)hd,
+                                                        m->max_seq, m->rope_per_token);
+}
+
+// Causal attention of n prompt rows: query i (absolute position pos + i) attends cache
+// positions 0 .. pos + i.  The f16 prefill uses the MFMA form, the f32 path the grouped-query
+// split form.  Output to m->ao (f32) or, with out16, to f16 in GEMM operand order.
+static int prefill_attention(Llama* m, int l, int n, int f16, _Float16* out16, int order, hipStream_t s) {
+    const int64_t hd = m->hd;
+    const int kvt = m->kv_f16 ? TL_HIP_F16 : TL_HIP_F32;
+    if (f16 && attention_prefill_supported(kvt, m->H, m->KV, (int)hd))
+        return launch_attention_prefill(m->q, m->kc[l], m->vc[l], m->ao, n, m->H, m->KV, (int)hd, m->max_seq,
+                                        m->pos, 0, 1.0f / sqrtf((float)hd), s, out16, order);
+    int rc;
+    if (attention_gq_supported(kvt, m->H, m->KV, (int)hd))
+        rc = launch_attention_gq(m->q, m->kc[l], m->vc[l], m->ao, m->ws, n, m->H, m->KV, (int)hd, m->max_seq, 0, 0,
+                                 m->pos, 1, 1, attention_gq_splits(m->host_pos + n), 1.0f / sqrtf((float)hd), s);
+    else
+        rc = launch_attention(m->q, m->kc[l], m->vc[l], kvt, m->ao, m->ws, n, m->H, m->KV, (int)hd, m->max_seq, 0,
+                              0, m->pos, 1, 1, 64, (int)cdiv(m->host_pos + n, 64), 1.0f / sqrtf((float)hd), s);
+    if (rc == TL_HIP_OK && out16) rc = launch_x_to_f16q(m->ao, out16, n, m->D, order, s);
+    return rc;
+}
+
+// The f16 prefill of a layer with its activations handed between the GEMMs as f16 operand
+// words: RMSNorm -> f16 (qkv GEMM input), attention -> f16 (o-proj input), o-proj + residual
+// in the GEMM epilogue, RMSNorm -> f16, gate/up GEMM with SwiGLU in the epilogue -> f16
+// (down input), down + residual.  Same values as the unfused path, where each GEMM input is
+// converted from the f32 producer output.
+static bool fused_layer_ok(const Llama* m, int l) {
+    const QWeight* wgu = m->wgu[l];
+    if (!wgu || wgu->n % 64 || m->D % 32 || m->D > 8192) return false;
+    const int oq = f16q_order(m->qkv_segs[l][0].w->ggml_type);
+    for (const Seg& sg : m->qkv_segs[l])  // one operand order for the shared input, K in steps of 128
+        if (sg.w->nb % 4 || f16q_order(sg.w->ggml_type) != oq) return false;
+    return m->wo[l]->nb % 4 == 0 && wgu->nb % 4 == 0 && m->wdown[l]->nb % 4 == 0;
+}
+
+static int prefill_layer_fused(Llama* m, int l, int n, hipStream_t s) {
+    const int64_t D = m->D, qkv_w = D + 2 * (int64_t)m->KV * m->hd;
+    const GemmEpi plain{GEMM_PLAIN, nullptr, nullptr, 0}, res{GEMM_RES, m->x, nullptr, 0};
+    int rc;
+    const int oq = f16q_order(m->qkv_segs[l][0].w->ggml_type);
+    if ((rc = launch_rmsnorm_f16q(m->x, m->attn_norm[l], m->xa16, n, D, m->eps, oq, s))) return rc;
+    if (m->qkv_segs[l].size() == 1) {
+        if ((rc = launch_gemm_f16q(m->qkv_segs[l][0].w, m->xa16, m->qkv, n, plain, s))) return rc;
+    } else {
+        for (const Seg& sg : m->qkv_segs[l]) {  // each segment's columns of the [n, qkv_w] rows
+            if ((rc = launch_gemm_f16q(sg.w, m->xa16, m->gu, n, plain, s))) return rc;
+            TLH_CHECK_HIP(hipMemcpy2DAsync(m->qkv + sg.row_off, qkv_w * 4, m->gu, sg.w->n * 4, sg.w->n * 4, n,
+                                           hipMemcpyDeviceToDevice, s));
+        }
+    }
+    prefill_rope_kv(m, l, n, s);
+    if ((rc = prefill_attention(m, l, n, 1, m->xa16, f16q_order(m->wo[l]->ggml_type), s))) return rc;
+    if ((rc = launch_gemm_f16q(m->wo[l], m->xa16, m->x, n, res, s))) return rc;
+    if ((rc = launch_rmsnorm_f16q(m->x, m->ffn_norm[l], m->xa16, n, D, m->eps, f16q_order(m->wgu[l]->ggml_type), s)))
+        return rc;
+    const GemmEpi glu{GEMM_GLU16, nullptr, m->xb16, f16q_order(m->wdown[l]->ggml_type)};
+    if ((rc = launch_gemm_f16q(m->wgu[l], m->xa16, nullptr, n, glu, s))) return rc;
+    return launch_gemm_f16q(m->wdown[l], m->xb16, m->x, n, res, s);
+}
+
 // Enqueues one forward over n tokens whose ids are already in m->ids (device); leaves the
 // last row's logits in m->logits and advances the device position by n.
 static int enqueue_forward(Llama* m, int n, int f16, hipStream_t s) {
-    const int64_t D = m->D, hd = m->hd;
-    const int64_t qkv_w = D + 2 * (int64_t)m->KV * hd;
+    const int64_t D = m->D;
+    const int64_t qkv_w = D + 2 * (int64_t)m->KV * m->hd;
     int rc;
     k_embed<<<cdiv(n * D, 256), 256, 0, s>>>(m->emb, m->ids, m->x, n, D);
-    const int G = m->H / m->KV;
-    // splits of 64 positions up to the longest length of this call (host-known here)
-    const int nsplit = (int)cdiv(m->host_pos + n, 64);
     for (int l = 0; l < m->nl; l++) {
+        if (f16 && n > 4 && fused_layer_ok(m, l)) {
+            if ((rc = prefill_layer_fused(m, l, n, s))) return rc;
+            continue;
+        }
         if ((rc = launch_rmsnorm(m->x, nullptr, m->attn_norm[l], m->h, n, D, m->eps, 0, s))) return rc;
         if (m->qkv_segs[l].size() == 1) {
             if ((rc = linear(m->qkv_segs[l][0].w, m->h, m->qkv, n, nullptr, nullptr, f16, s))) return rc;
@@ -311,30 +392,9 @@ static int enqueue_forward(Llama* m, int n, int f16, hipStream_t s) {
                                                hipMemcpyDeviceToDevice, s));
             }
         }
-        int64_t work = (int64_t)n * ((m->H + m->KV) * hd / 2 + m->KV * hd);
-        if (m->kv_f16)
-            k_rope_kv<__half><<<cdiv(work, 256), 256, 0, s>>>(m->qkv, m->q, (__half*)m->kc[l], (__half*)m->vc[l],
-                                                             m->cos_t, m->sin_t, m->pos, n, m->H, m->KV, (int)hd,
-                                                             m->max_seq, m->rope_per_token);
-        else
-            k_rope_kv<float><<<cdiv(work, 256), 256, 0, s>>>(m->qkv, m->q, (float*)m->kc[l], (float*)m->vc[l],
-                                                            m->cos_t, m->sin_t, m->pos, n, m->H, m->KV, (int)hd,
-                                                            m->max_seq, m->rope_per_token);
-        // query i (absolute position pos + i) attends cache positions 0 .. pos + i; the f16
-        // prefill uses the MFMA form, the f32 path the grouped-query split form
-        if (f16 && attention_prefill_supported(m->kv_f16 ? TL_HIP_F16 : TL_HIP_F32, m->H, m->KV, (int)hd))
-            rc = launch_attention_prefill(m->q, m->kc[l], m->vc[l], m->ao, n, m->H, m->KV, (int)hd, m->max_seq,
-                                          m->pos, 0, 1.0f / sqrtf((float)hd), s);
-        else if (attention_gq_supported(m->kv_f16 ? TL_HIP_F16 : TL_HIP_F32, m->H, m->KV, (int)hd))
-            rc = launch_attention_gq(m->q, m->kc[l], m->vc[l], m->ao, m->ws, n, m->H, m->KV, (int)hd, m->max_seq, 0,
-                                     0, m->pos, 1, 1, attention_gq_splits(m->host_pos + n),
-                                     1.0f / sqrtf((float)hd), s);
-        else
-            rc = launch_attention(m->q, m->kc[l], m->vc[l], m->kv_f16 ? TL_HIP_F16 : TL_HIP_F32, m->ao, m->ws, n,
-                                  m->H, m->KV, (int)hd, m->max_seq, 0, 0, m->pos, 1, 1, 64, nsplit,
-                                  1.0f / sqrtf((float)hd), s);
+        prefill_rope_kv(m, l, n, s);
+        rc = prefill_attention(m, l, n, f16, nullptr, 0, s);
         if (rc) return rc;
-        (void)G;
         if ((rc = linear(m->wo[l], m->ao, m->x, n, m->x, m->t, f16, s))) return rc;
         if ((rc = launch_rmsnorm(m->x, nullptr, m->ffn_norm[l], m->h, n, D, m->eps, 0, s))) return rc;
         if (m->wgu[l]) {
@@ -538,7 +598,7 @@ int tl_hip_llama_free(tl_hip_llama* h) {
     for (void* p : m->vc) dev_free(p);
     void* bufs[] = {m->out_norm, m->emb, m->cos_t, m->sin_t, m->x, m->h, m->qkv, m->q, m->ao, m->t, m->gu,
                     m->act, m->logits, m->plogits, m->ws, m->ids, m->pos, m->tok, m->step, m->out_ids, m->seen,
-                    m->am_v, m->am_i, m->am_nan};
+                    m->am_v, m->am_i, m->am_nan, m->xa16, m->xb16};
     for (void* p : bufs) dev_free(p);
     delete m;
     return TL_HIP_OK;

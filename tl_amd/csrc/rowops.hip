@@ -130,6 +130,65 @@ __global__ __launch_bounds__(256) void k_rmsnorm_generic(const float* __restrict
     }
 }
 
+// RMSNorm mode 0 whose output goes straight to the f16 operand order of the GEMM that reads
+// it (the same f32 value as k_rmsnorm, rounded once to f16): the sum of squares in k_rmsnorm's
+// order (thread j's float4 j, j + 256, ...), then one 8-half word per (block, t) unit.
+template <int V>
+__global__ __launch_bounds__(256) void k_rmsnorm_f16q(const float* __restrict__ x, const float* __restrict__ w,
+                                                      _Float16* __restrict__ out16, int64_t n, float eps,
+                                                      int order) {
+    __shared__ float red[4];
+    const int64_t row = blockIdx.x;
+    const float* xr = x + row * n;
+    const float4* x4 = reinterpret_cast<const float4*>(xr);
+    const int64_t n4 = n >> 2;
+    float ss = 0.f;
+#pragma unroll
+    for (int i = 0; i < V; i++) {
+        const int64_t j = threadIdx.x + (int64_t)i * 256;
+        const float4 v = j < n4 ? x4[j] : make_float4(0.f, 0.f, 0.f, 0.f);
+        ss += v.x * v.x + v.y * v.y + v.z * v.z + v.w * v.w;
+    }
+    ss = block_sum(ss, red);
+    const float rms = sqrtf(ss / (float)n + eps);
+    const int64_t units = (n >> 5) * 4;
+    const float4* w4 = reinterpret_cast<const float4*>(w);
+    for (int64_t u = threadIdx.x; u < units; u += 256) {
+        // word t of block b: float4s (8b + t, 8b + 4 + t) in Q4 order, (8b + 2t, 8b + 2t + 1) in Q8
+        const int64_t b = u >> 2;
+        const int t = (int)(u & 3);
+        const int64_t i0 = order == F16Q_Q8 ? 8 * b + 2 * t : 8 * b + t, i1 = order == F16Q_Q8 ? i0 + 1 : i0 + 4;
+        const float4 e = x4[i0], f = x4[i1], we = w4[i0], wf = w4[i1];
+        const float v[8] = {(e.x / rms) * we.x, (e.y / rms) * we.y, (e.z / rms) * we.z, (e.w / rms) * we.w,
+                            (f.x / rms) * wf.x, (f.y / rms) * wf.y, (f.z / rms) * wf.z, (f.w / rms) * wf.w};
+        half8 h;
+        if (order == F16Q_Q8) {  // slots: e0 e2 e1 e3 f0 f2 f1 f3
+            h = half8{(_Float16)v[0], (_Float16)v[2], (_Float16)v[1], (_Float16)v[3],
+                      (_Float16)v[4], (_Float16)v[6], (_Float16)v[5], (_Float16)v[7]};
+        } else {
+            h = half8{(_Float16)v[0], (_Float16)v[1], (_Float16)v[2], (_Float16)v[3],
+                      (_Float16)v[4], (_Float16)v[5], (_Float16)v[6], (_Float16)v[7]};
+        }
+        reinterpret_cast<half8*>(out16)[row * units + u] = h;
+    }
+}
+
+int launch_rmsnorm_f16q(const float* x, const float* w, _Float16* out16, int64_t rows, int64_t n, float eps,
+                        int order, hipStream_t s) {
+    if (rows <= 0) return TL_HIP_OK;
+    const int64_t per = cdiv(n / 4, 256);
+    if (n % 32 != 0 || per > 8 || (uintptr_t)x % 16 != 0 || !w || (uintptr_t)w % 16 != 0) {
+        set_error(TL_HIP_ERR_ARG, "ArgumentError: f16 operand-order RMSNorm takes rows of 32k <= 8192 floats");
+        return TL_HIP_ERR_ARG;
+    }
+    if (per <= 1) k_rmsnorm_f16q<1><<<rows, 256, 0, s>>>(x, w, out16, n, eps, order);
+    else if (per <= 2) k_rmsnorm_f16q<2><<<rows, 256, 0, s>>>(x, w, out16, n, eps, order);
+    else if (per <= 4) k_rmsnorm_f16q<4><<<rows, 256, 0, s>>>(x, w, out16, n, eps, order);
+    else k_rmsnorm_f16q<8><<<rows, 256, 0, s>>>(x, w, out16, n, eps, order);
+    hipError_t e = hipGetLastError();
+    return e == hipSuccess ? TL_HIP_OK : hip_fail(e, "rmsnorm launch");
+}
+
 int launch_rmsnorm(const float* x, const float* r, const float* w, float* out, int64_t rows,
                    int64_t n, float eps, int mode, hipStream_t s) {
     if (rows <= 0 || n <= 0) return TL_HIP_OK;
