@@ -123,8 +123,10 @@ tl_hip_tensor* tl_hip_qtensor_dequantize(const tl_hip_qtensor* q);
  * m the tiled GEMM. */
 tl_hip_tensor* tl_hip_qtensor_matmul(const tl_hip_tensor* x, const tl_hip_qtensor* q);
 /* Same with the f16-MFMA prefill GEMM for m > 4 (dequant -> f16 LDS tiles -> MFMA,
- * f32 accumulate); tolerance class "f16 path".  Q4_K / Q6_K weights are first dequantized
- * into an f16 workspace in the MFMA operand order. */
+ * f32 accumulate); tolerance class "f16 path".  Q4_0, Q8_0 and Q4_K are dequantized in
+ * registers; a Q4_K tensor's first call builds its per-32-weight (d sc, -dmin m) f16 pairs
+ * (4 bytes per 32 weights, kept until the tensor is released).  Q6_K weights are first
+ * dequantized into an f16 workspace in the MFMA operand order. */
 tl_hip_tensor* tl_hip_qtensor_matmul_f16(const tl_hip_tensor* x, const tl_hip_qtensor* q);
 
 /* ---------------------------------------------------------------- GGUF files ----- */

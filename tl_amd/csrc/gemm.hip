@@ -9,6 +9,7 @@
 //                  for [batch, m, k] x [batch?, k, n].
 #include "internal.h"
 
+#include <mutex>
 #include <type_traits>
 
 namespace tlhip {
@@ -21,6 +22,24 @@ struct QView {
     const uint8_t* qh;
     const int8_t* sc;
 };
+
+// Q4_K sub-block j's d * scale and dmin * min from its super-block header (four words: f16 d |
+// f16 dmin, then the 12 packed 6-bit scale / min bytes), QTensor::get_scale_min_k4
+// (quantized.rs:405-415); both products are exact in f32.
+__device__ __forceinline__ void q4k_scale_min(const uint4& hd, int j, float* d1, float* m1) {
+    const int sh = 8 * (j & 3);
+    uint32_t sc, mn;
+    if (j < 4) {
+        sc = (hd.y >> sh) & 63;
+        mn = (hd.z >> sh) & 63;
+    } else {
+        const uint32_t lo = hd.w >> sh;
+        sc = (lo & 0xF) | (((hd.y >> sh) >> 2) & 0x30);
+        mn = ((lo >> 4) & 0xF) | (((hd.z >> sh) >> 2) & 0x30);
+    }
+    *d1 = __half2float(__ushort_as_half((uint16_t)(hd.x & 0xFFFF))) * (float)sc;
+    *m1 = __half2float(__ushort_as_half((uint16_t)(hd.x >> 16))) * (float)mn;
+}
 
 // Dequantise the 32 weights of unit blk into v[32] (f32, bit-identical to the reference's
 // dequantizers: Q4_0 d * (q - 8), Q8_0 d * q, Q4_K (d sc) q - dmin m, Q6_K (d sc) (q - 32)).
@@ -48,19 +67,8 @@ __device__ __forceinline__ void dequant_block(const QView& qv, int64_t blk, floa
 #pragma unroll
             for (int i = 0; i < 4; i++) v[4 * c + i] = d * (float)(int8_t)((q[c] >> (8 * i)) & 0xFF);
     } else if constexpr (QT == TL_HIP_GGML_Q4_K) {
-        const uint4 hd = reinterpret_cast<const uint4*>(qv.hdr)[blk >> 3];
-        const int j = (int)(blk & 7), sh = 8 * (j & 3);
-        uint32_t sc, mn;
-        if (j < 4) {
-            sc = (hd.y >> sh) & 63;
-            mn = (hd.z >> sh) & 63;
-        } else {
-            const uint32_t lo = hd.w >> sh;
-            sc = (lo & 0xF) | (((hd.y >> sh) >> 2) & 0x30);
-            mn = ((lo >> 4) & 0xF) | (((hd.z >> sh) >> 2) & 0x30);
-        }
-        const float d1 = __half2float(__ushort_as_half((uint16_t)(hd.x & 0xFFFF))) * (float)sc;
-        const float m1 = __half2float(__ushort_as_half((uint16_t)(hd.x >> 16))) * (float)mn;
+        float d1, m1;
+        q4k_scale_min(reinterpret_cast<const uint4*>(qv.hdr)[blk >> 3], (int)(blk & 7), &d1, &m1);
         uint4 w = *reinterpret_cast<const uint4*>(qv.qs + blk * 16);
         const uint32_t q[4] = {w.x, w.y, w.z, w.w};
 #pragma unroll
@@ -222,6 +230,11 @@ struct QWords<TL_HIP_GGML_Q8_0> {
     }
 };
 
+// Q4_K units are resident in the Q4_0 nibble order: the same operand words, built with the
+// unit's (d sc, -dmin m) pair in place of (d, -8 d).
+template <>
+struct QWords<TL_HIP_GGML_Q4_K> : QWords<TL_HIP_GGML_Q4_0> {};
+
 // f16 weights already in the operand order (k_dequant_f16q): block = 4 words of 8 halves,
 // word t is the operand of MFMA t as stored.
 template <>
@@ -296,6 +309,7 @@ __global__ __launch_bounds__(512) void k_qgemm_mfma(const uint8_t* __restrict__ 
     constexpr int CPR = Q_KR * QC;             // W chunks per row and iteration
     constexpr int RSH = CPR == 4 ? 2 : CPR == 8 ? 1 : 0;  // W chunk swizzle: + (row >> RSH)
     constexpr bool SCALED = QT != TL_HIP_GGML_F16;   // quant blocks carry an f16 scale
+    constexpr bool K4 = QT == TL_HIP_GGML_Q4_K;      // scales: one (d sc, -dmin m) word per unit
     constexpr int XI = BM * 16 / 512;          // X chunks per thread per iteration
     constexpr int WCH = BN * CPR;              // W chunks per iteration
     constexpr int WPT = WCH >= 512 ? WCH / 512 : 1;  // W DMA instructions per issuing wavefront
@@ -349,7 +363,8 @@ __global__ __launch_bounds__(512) void k_qgemm_mfma(const uint8_t* __restrict__ 
     if (DW > 0 && wave >= 8 - DW) {  // the 4-byte word that holds scale (row, block)
         const int slot = (wave - (8 - DW)) * 64 + lane;
         const int64_t row = n0 + (slot >> 2) < n ? n0 + (slot >> 2) : n - 1;
-        doff = (uint32_t)(((row * nb + (slot & 3)) >> 1) * 4);
+        // Q4_0 / Q8_0: the word holding the f16 d of (row, block); Q4_K: its (d sc, -dmin m) word
+        doff = (uint32_t)(K4 ? (row * nb + (slot & 3)) * 4 : ((row * nb + (slot & 3)) >> 1) * 4);
     }
     auto issue = [&](int64_t kb, Stage& st) {
         const char* src = reinterpret_cast<const char*>(x16) + kb * 64;  // 32 halves per block
@@ -361,7 +376,7 @@ __global__ __launch_bounds__(512) void k_qgemm_mfma(const uint8_t* __restrict__ 
                 lds_dma16(reinterpret_cast<const char*>(qs) + kb * QB + woff[u], &st.Wq[(wave * WPT + u) * 64 * 16]);
         }
         if (DW > 0 && wave >= 8 - DW)  // kb even: whole words
-            lds_dma4(reinterpret_cast<const char*>(dsc) + kb * 2 + doff, &st.Wd[(wave - (8 - DW)) * 64]);
+            lds_dma4(reinterpret_cast<const char*>(dsc) + kb * (K4 ? 4 : 2) + doff, &st.Wd[(wave - (8 - DW)) * 64]);
     };
     uint32_t dpar[TN];  // which half of its word holds this lane's scale (kb is even)
 #pragma unroll
@@ -399,7 +414,11 @@ __global__ __launch_bounds__(512) void k_qgemm_mfma(const uint8_t* __restrict__ 
         half2v d2[TN], m8d2[TN];
 #pragma unroll
         for (int j = 0; j < TN; j++) {
-            if constexpr (SCALED) {
+            if constexpr (K4) {
+                const uint32_t a = dw[j] & 0xFFFFu, b = dw[j] >> 16;
+                d2[j] = __builtin_bit_cast(half2v, a | (a << 16));
+                m8d2[j] = __builtin_bit_cast(half2v, b | (b << 16));
+            } else if constexpr (SCALED) {
                 const uint32_t b = (dw[j] >> dpar[j]) & 0xFFFFu;
                 d2[j] = __builtin_bit_cast(half2v, b | (b << 16));
                 m8d2[j] = d2[j] * half2v{(_Float16)-8.0f, (_Float16)-8.0f};
@@ -411,7 +430,7 @@ __global__ __launch_bounds__(512) void k_qgemm_mfma(const uint8_t* __restrict__ 
 #pragma unroll
             for (int j = 0; j < TN; j++) {
                 half8 bop;
-                if constexpr (QT == TL_HIP_GGML_Q4_0) bop = QWords<QT>::operand(wr[j][0], t, d2[j], m8d2[j]);
+                if constexpr (QT == TL_HIP_GGML_Q4_0 || K4) bop = QWords<QT>::operand(wr[j][0], t, d2[j], m8d2[j]);
                 else if constexpr (QT == TL_HIP_GGML_Q8_0) bop = QWords<QT>::operand(wr[j], t, d2[j], m8d2[j]);
                 else bop = __builtin_bit_cast(half8, wr[j][tt]);
 #pragma unroll
@@ -477,6 +496,29 @@ __global__ __launch_bounds__(512) void k_qgemm_mfma(const uint8_t* __restrict__ 
 }
 
 
+// one word per Q4_K unit: f16 d * scale (low half) and f16 -(dmin * min) (high half)
+__global__ __launch_bounds__(256) void k_q4k_unit_scales(const uint8_t* __restrict__ hdr, uint32_t* __restrict__ us,
+                                                         int64_t units) {
+    const int64_t u = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (u >= units) return;
+    float d1, m1;
+    q4k_scale_min(reinterpret_cast<const uint4*>(hdr)[u >> 3], (int)(u & 7), &d1, &m1);
+    const _Float16 a = (_Float16)d1, b = (_Float16)(-m1);
+    us[u] = (uint32_t)__builtin_bit_cast(uint16_t, a) | ((uint32_t)__builtin_bit_cast(uint16_t, b) << 16);
+}
+
+int q4k_build_unit_scales(QWeight* w, hipStream_t s) {
+    static std::mutex mu;  // one build per tensor when threads share it
+    std::lock_guard<std::mutex> lk(mu);
+    if (w->ggml_type != TL_HIP_GGML_Q4_K || w->us) return TL_HIP_OK;
+    const int64_t units = w->n * w->nb;
+    w->us = static_cast<uint32_t*>(dev_alloc((size_t)units * 4));
+    if (!w->us) return TL_HIP_ERR_ALLOC;
+    k_q4k_unit_scales<<<(unsigned)cdiv(units, 256), 256, 0, s>>>(w->hdr, w->us, units);
+    hipError_t e = hipGetLastError();
+    return e == hipSuccess ? TL_HIP_OK : hip_fail(e, "Q4_K unit scales launch");
+}
+
 int f16q_order(int ggml_type) { return ggml_type == TL_HIP_GGML_Q8_0 ? F16Q_Q8 : F16Q_Q4; }
 
 int launch_x_to_f16q(const float* x, _Float16* x16, int64_t m, int64_t k, int order, hipStream_t s) {
@@ -497,16 +539,22 @@ int launch_gemm_f16q(const QWeight* w, const _Float16* x16, float* y, int64_t m,
     }
     // 128 x 64 tiles when that gives at least two workgroups per CU, else 128 x 32 (twice
     // the workgroups; measured at M = 512: 2048 x 2048 18.7 -> 15.5 us, 4096 x 4096
-    // 41.0 -> 37.3 us, while 11008 x 4096 is faster with the wide tile, 84.5 vs 101.7 us)
+    // 41.0 -> 37.3 us, while 11008 x 4096 is faster with the wide tile, 84.5 vs 101.7 us).
+    // f16 weights (K-quants) move 3.5x the bytes per tile: 128 x 32 only when 128 x 64 would
+    // leave half the CUs idle (2560 x 2048: 16.8 us wide vs 24.8 narrow; 2048 x 2048: 16.6 vs 13.5)
     constexpr int BM = 128;
-    const bool wide = cdiv(m, BM) * cdiv(w->n, 64) >= 512;
+    const bool f16w = (w->ggml_type == TL_HIP_GGML_Q4_K && !w->us) || w->ggml_type == TL_HIP_GGML_Q6_K;
+    const int64_t wide_tiles = cdiv(m, BM) * cdiv(w->n, 64);
+    const bool wide = f16w ? wide_tiles > 128 : wide_tiles >= 512;
     const int64_t tiles = cdiv(m, BM) * cdiv(w->n, wide ? 64 : 32);
     auto gemm = [&](auto qt, const uint8_t* q, const __half* d) {
         constexpr int QT = decltype(qt)::value;
         if (wide) k_qgemm_mfma<QT, BM, 64><<<(unsigned)tiles, 512, 0, s>>>(q, d, x16, y, m, w->n, w->k, w->nb, ep);
         else k_qgemm_mfma<QT, BM, 32><<<(unsigned)tiles, 512, 0, s>>>(q, d, x16, y, m, w->n, w->k, w->nb, ep);
     };
-    if (w->ggml_type == TL_HIP_GGML_Q4_K || w->ggml_type == TL_HIP_GGML_Q6_K) {
+    if (w->ggml_type == TL_HIP_GGML_Q4_K && w->us) {
+        gemm(std::integral_constant<int, TL_HIP_GGML_Q4_K>{}, w->qs, reinterpret_cast<const __half*>(w->us));
+    } else if (w->ggml_type == TL_HIP_GGML_Q4_K || w->ggml_type == TL_HIP_GGML_Q6_K) {
         // K-quants: dequantize once into f16 operand order (n * k halves), then the same
         // MFMA pipeline with the weights read as stored
         _Float16* w16 = static_cast<_Float16*>(dev_alloc((size_t)w->n * w->k * sizeof(_Float16)));
@@ -550,7 +598,9 @@ int launch_quant_gemm(const QWeight* w, const float* x, float* y, int64_t m, hip
         // X -> f16 in the operand k order (a workspace of m * k halves), then the MFMA GEMM
         _Float16* x16 = static_cast<_Float16*>(dev_alloc((size_t)m * w->k * sizeof(_Float16)));
         if (!x16) return TL_HIP_ERR_ALLOC;
-        int rc = launch_x_to_f16q(x, x16, m, w->k, f16q_order(w->ggml_type), s);
+        // a Q4_K tensor gets its unit scales on its first f16 GEMM (kept with the tensor)
+        int rc = q4k_build_unit_scales(const_cast<QWeight*>(w), s);
+        if (rc == TL_HIP_OK) rc = launch_x_to_f16q(x, x16, m, w->k, f16q_order(w->ggml_type), s);
         if (rc == TL_HIP_OK) rc = launch_gemm_f16q(w, x16, y, m, GemmEpi{GEMM_PLAIN, nullptr, nullptr, 0}, s);
         dev_free(x16);  // stream-ordered: reused only by later work on the same stream
         if (rc) return rc;

@@ -79,6 +79,7 @@ struct QWeight {
     uint8_t* hdr = nullptr;  // Q4_K
     uint8_t* qh = nullptr;   // Q6_K
     int8_t* sc = nullptr;    // Q6_K
+    uint32_t* us = nullptr;  // Q4_K: per-unit f16 pair (d sc, -dmin m) for the f16 GEMM, built on request
     int64_t shape[TL_HIP_MAX_RANK] = {0};
     int rank = 0;
     std::atomic<int> refs{1};
@@ -173,6 +174,9 @@ int launch_x_to_f16q(const float* x, _Float16* x16, int64_t m, int64_t k, int or
 // K a multiple of 128 (TL_HIP_ERR_ARG otherwise); GLU16 also needs N a multiple of 64.
 int launch_gemm_f16q(const QWeight* w, const _Float16* x16, float* y, int64_t m, const GemmEpi& ep,
                      hipStream_t s);
+// Q4_K weights: builds w->us (4 bytes per 32 weights) on stream s, after which the f16 GEMM
+// dequantizes them in registers like Q4_0 instead of through an f16 copy per call.
+int q4k_build_unit_scales(QWeight* w, hipStream_t s);
 int launch_matmul_f32(const float* a, const float* b, float* c, int64_t batch, int64_t m,
                       int64_t k, int64_t n, int64_t a_bstride, int64_t b_bstride,
                       hipStream_t s);

@@ -345,6 +345,12 @@ static bool fused_layer_ok(const Llama* m, int l) {
     return m->wo[l]->nb % 4 == 0 && wgu->nb % 4 == 0 && m->wdown[l]->nb % 4 == 0;
 }
 
+// the f16 GEMM of a prefill; a Q4_K weight gets its unit scales on first use
+static int gemm16(QWeight* w, const _Float16* x16, float* y, int n, const GemmEpi& ep, hipStream_t s) {
+    const int rc = q4k_build_unit_scales(w, s);
+    return rc ? rc : launch_gemm_f16q(w, x16, y, n, ep, s);
+}
+
 static int prefill_layer_fused(Llama* m, int l, int n, hipStream_t s) {
     const int64_t D = m->D, qkv_w = D + 2 * (int64_t)m->KV * m->hd;
     const GemmEpi plain{GEMM_PLAIN, nullptr, nullptr, 0}, res{GEMM_RES, m->x, nullptr, 0};
@@ -352,22 +358,22 @@ static int prefill_layer_fused(Llama* m, int l, int n, hipStream_t s) {
     const int oq = f16q_order(m->qkv_segs[l][0].w->ggml_type);
     if ((rc = launch_rmsnorm_f16q(m->x, m->attn_norm[l], m->xa16, n, D, m->eps, oq, s))) return rc;
     if (m->qkv_segs[l].size() == 1) {
-        if ((rc = launch_gemm_f16q(m->qkv_segs[l][0].w, m->xa16, m->qkv, n, plain, s))) return rc;
+        if ((rc = gemm16(m->qkv_segs[l][0].w, m->xa16, m->qkv, n, plain, s))) return rc;
     } else {
         for (const Seg& sg : m->qkv_segs[l]) {  // each segment's columns of the [n, qkv_w] rows
-            if ((rc = launch_gemm_f16q(sg.w, m->xa16, m->gu, n, plain, s))) return rc;
+            if ((rc = gemm16(sg.w, m->xa16, m->gu, n, plain, s))) return rc;
             TLH_CHECK_HIP(hipMemcpy2DAsync(m->qkv + sg.row_off, qkv_w * 4, m->gu, sg.w->n * 4, sg.w->n * 4, n,
                                            hipMemcpyDeviceToDevice, s));
         }
     }
     prefill_rope_kv(m, l, n, s);
     if ((rc = prefill_attention(m, l, n, 1, m->xa16, f16q_order(m->wo[l]->ggml_type), s))) return rc;
-    if ((rc = launch_gemm_f16q(m->wo[l], m->xa16, m->x, n, res, s))) return rc;
+    if ((rc = gemm16(m->wo[l], m->xa16, m->x, n, res, s))) return rc;
     if ((rc = launch_rmsnorm_f16q(m->x, m->ffn_norm[l], m->xa16, n, D, m->eps, f16q_order(m->wgu[l]->ggml_type), s)))
         return rc;
     const GemmEpi glu{GEMM_GLU16, nullptr, m->xb16, f16q_order(m->wdown[l]->ggml_type)};
-    if ((rc = launch_gemm_f16q(m->wgu[l], m->xa16, nullptr, n, glu, s))) return rc;
-    return launch_gemm_f16q(m->wdown[l], m->xb16, m->x, n, res, s);
+    if ((rc = gemm16(m->wgu[l], m->xa16, nullptr, n, glu, s))) return rc;
+    return gemm16(m->wdown[l], m->xb16, m->x, n, res, s);
 }
 
 // Enqueues one forward over n tokens whose ids are already in m->ids (device); leaves the

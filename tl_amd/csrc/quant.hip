@@ -274,6 +274,7 @@ static void q_free(QWeight* w) {
     dev_free(w->hdr);
     dev_free(w->qh);
     dev_free(w->sc);
+    dev_free(w->us);
     delete w;
 }
 
