@@ -338,7 +338,8 @@ def main():
         kq = {"workload": "same decoder with llama.cpp's Q4_K_M type mixture (Q4_K; Q6_K for the LM head and "
                           "attn_v / ffn_down of 11 of 22 layers)", "value": round(kq_tok_s, 2), "unit": "tok/s",
               "steps": 64, "ms_per_step": round(kq_decode_s * 1e3 / 64, 4), "prefill_ms": round(kq_prefill_s * 1e3, 2),
-              "prefill_path": "f16 MFMA GEMM, K-quant weights dequantized to f16 operand order per call"}
+              "prefill_path": "fused f16 MFMA prefill; Q4_K dequantized in registers (per-unit scale pairs built "
+                             "once per tensor), Q6_K dequantized to f16 operand order per call"}
 
     cpu = None
     if not args.no_cpu_baseline:
@@ -374,7 +375,7 @@ def main():
         },
         "roofline": {
             "bound": "hbm",
-            "kernel": "k_matvec Q4_0 4096x4096 (m=1)",
+            "kernel": "k_mv<Q4_0> 4096x4096 (m=1)",
             "achieved": round(achieved, 1),
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
