@@ -100,6 +100,35 @@ def test_f16_prefill_mfma_attention_chunks():
         cpu.close()
 
 
+@pytest.mark.parametrize("kv_f16", [True, False])
+def test_long_cache_decode_paths(kv_f16):
+    """Caches longer than 4096 positions: decode attention takes the grouped-query split form
+    (f16 cache) or the general split form (f32 cache) instead of the one-launch per-head
+    kernel; logits against the oracle (1e-2 with the f16 cache, 1e-4 with f32), graph and
+    eager greedy tokens equal to the oracle's."""
+    cfg = LlamaConfig(2, 512, 8, 1, 512, 1000, max_seq=5000)
+    tensors = list(synthetic_weights(cfg, 47))
+    gpu = HipLlama(cfg, kv_f16=kv_f16)
+    gpu.load(tensors)
+    cpu = oracle.Llama(cfg)
+    cpu.load(tensors)
+    tol = 1e-2 if kv_f16 else 1e-4
+    try:
+        prompt = synthetic_prompt(cfg, 47, 40)
+        cpu.reset()
+        err = max_rel(gpu.forward(prompt), cpu.forward(prompt))
+        assert err <= tol, f"prefill logits max-rel-err {err:.2e}"
+        for t in ([11], [512], [7]):
+            err = max_rel(gpu.forward(t), cpu.forward(t))
+            assert err <= tol, f"decode logits max-rel-err {err:.2e}"
+        if not kv_f16:
+            for use_graph in (True, False):
+                assert list(greedy_generate(gpu, prompt, 12, use_graph=use_graph)) == list(cpu.greedy(prompt, 12))
+    finally:
+        gpu.close()
+        cpu.close()
+
+
 def test_position_aware_rope_changes_prefill(small):
     gpu, _ = small
     prompt = synthetic_prompt(SMALL, 14, 12)
