@@ -707,7 +707,9 @@ __global__ __launch_bounds__(256) void k_attn_prefill(const float* __restrict__ 
         hh[rt] = h * G + r % G;
         prow[rt] = pos0 + (qi[rt] < n ? qi[rt] : n - 1);
     }
-    // B operand of S^T: q[row][32 ks + 8 g .. +7] * scale, in f16
+    // B operand of S^T: q[row][32 ks + 8 g .. +7] * scale * log2(e), in f16: scores in log2
+    // units, so the softmax exponentials are single hardware exp2 instructions
+    const float sl2 = scale * 1.44269504088896341f;
     half8v qop[2][KS];
 #pragma unroll
     for (int rt = 0; rt < 2; rt++) {
@@ -717,9 +719,9 @@ __global__ __launch_bounds__(256) void k_attn_prefill(const float* __restrict__ 
         for (int ks = 0; ks < KS; ks++) {
             const float4 a = reinterpret_cast<const float4*>(qp + 32 * ks + 8 * g)[0];
             const float4 b = reinterpret_cast<const float4*>(qp + 32 * ks + 8 * g)[1];
-            qop[rt][ks] = half8v{(_Float16)(a.x * scale), (_Float16)(a.y * scale), (_Float16)(a.z * scale),
-                                 (_Float16)(a.w * scale), (_Float16)(b.x * scale), (_Float16)(b.y * scale),
-                                 (_Float16)(b.z * scale), (_Float16)(b.w * scale)};
+            qop[rt][ks] = half8v{(_Float16)(a.x * sl2), (_Float16)(a.y * sl2), (_Float16)(a.z * sl2),
+                                 (_Float16)(a.w * sl2), (_Float16)(b.x * sl2), (_Float16)(b.y * sl2),
+                                 (_Float16)(b.z * sl2), (_Float16)(b.w * sl2)};
         }
     }
     floatx4v o[2][D / 16];  // O^T tiles: [row tile][dim tile], lane: dims 4 g .. +3 of row col
@@ -731,27 +733,40 @@ __global__ __launch_bounds__(256) void k_attn_prefill(const float* __restrict__ 
 
     const int64_t last = pos0 + (int64_t)((qb + 1) * QB < n ? (qb + 1) * QB : n);  // positions needed
     const int ntiles = (int)((last + KT - 1) / KT);
+    // K / V tile rows as raw 16-byte chunks, one tile ahead: the loads of tile + 1 are in
+    // flight while tile computes.  Rows at or past `last` are zeros: they are masked out, and
+    // a zero P times a non-finite V would still poison O.
+    constexpr int TU = KT * CPR / 256;  // chunks per thread and tile
+    uint4 kn[TU], vn[TU];
+    auto fetch = [&](int tile) {
+#pragma unroll
+        for (int i = 0; i < TU; i++) {
+            const int u = tid + 256 * i, r = u / CPR, c = u % CPR;
+            const int64_t p = (int64_t)tile * KT + r;
+            kn[i] = vn[i] = make_uint4(0u, 0u, 0u, 0u);
+            if (p < last) {
+                kn[i] = *reinterpret_cast<const uint4*>(kb + p * D + 8 * c);
+                vn[i] = *reinterpret_cast<const uint4*>(vb + p * D + 8 * c);
+            }
+        }
+    };
+    fetch(0);
     for (int tile = 0; tile < ntiles; tile++) {
         const int64_t t0 = (int64_t)tile * KT;
         __syncthreads();  // the previous tile's readers are done
-        // K tile: 64 rows x CPR chunks; V tile transposed into Vt.  Rows at or past `last` are
-        // zeros: they are masked out, and a zero P times a non-finite V would still poison O.
-        for (int u = tid; u < KT * CPR; u += 256) {
-            const int r = u / CPR, c = u % CPR;
-            const int64_t p = t0 + r;
-            uint4 kw = make_uint4(0u, 0u, 0u, 0u), vw = kw;
-            if (p < last) {
-                kw = *reinterpret_cast<const uint4*>(kb + p * D + 8 * c);
-                vw = *reinterpret_cast<const uint4*>(vb + p * D + 8 * c);
-            }
-            *reinterpret_cast<uint4*>(&Ks[r * D + 8 * (c ^ (r & (CPR - 1)))]) = kw;
-            const _Float16* vh = reinterpret_cast<const _Float16*>(&vw);
+        // K tile row-major (chunk swizzle), V tile transposed into Vt
+#pragma unroll
+        for (int i = 0; i < TU; i++) {
+            const int u = tid + 256 * i, r = u / CPR, c = u % CPR;
+            *reinterpret_cast<uint4*>(&Ks[r * D + 8 * (c ^ (r & (CPR - 1)))]) = kn[i];
+            const _Float16* vh = reinterpret_cast<const _Float16*>(&vn[i]);
 #pragma unroll
             for (int e = 0; e < 8; e++) {
                 const int d = 8 * c + e;
                 Vt[d * KT + 4 * ((r >> 2) ^ (d & 15)) + (r & 3)] = vh[e];
             }
         }
+        if (tile + 1 < ntiles) fetch(tile + 1);
         __syncthreads();
         // S^T = K Q^T over the tile: [pos tile pt][row tile rt]
         floatx4v st[4][2];
@@ -787,13 +802,13 @@ __global__ __launch_bounds__(256) void k_attn_prefill(const float* __restrict__ 
             mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
             mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
             const float mn = fmaxf(mrow[rt], mx);  // finite: position 0 is in every row's range
-            const float alpha = expf(mrow[rt] - mn);
+            const float alpha = __builtin_amdgcn_exp2f(mrow[rt] - mn);  // 0 on the first tile
             float sum = 0.f;
 #pragma unroll
             for (int pt = 0; pt < 4; pt++)
 #pragma unroll
                 for (int i = 0; i < 4; i++) {
-                    const float e = expf(st[pt][rt][i] - mn);
+                    const float e = __builtin_amdgcn_exp2f(st[pt][rt][i] - mn);  // 0 for masked
                     st[pt][rt][i] = e;
                     sum += e;
                 }
