@@ -299,6 +299,9 @@ __device__ __forceinline__ void lds_dma4(const void* src, void* lds) {
 #endif
 }
 
+// X-tile chunk swizzle of row r (mod 16): a bijection of the 16 chunks for every row
+__device__ __forceinline__ int xsw(int r) { return ((2 * r) & 15) ^ ((r >> 3) & 1); }
+
 template <int QT, int BM, int BN>
 __global__ __launch_bounds__(512) void k_qgemm_mfma(const uint8_t* __restrict__ qs, const __half* __restrict__ dsc,
                                                     const _Float16* __restrict__ x16, float* y, int64_t m,
@@ -307,7 +310,6 @@ __global__ __launch_bounds__(512) void k_qgemm_mfma(const uint8_t* __restrict__ 
     constexpr int QB = QWords<QT>::BYTES;
     constexpr int QC = QB / 16;                // 16-byte chunks per quant block
     constexpr int CPR = Q_KR * QC;             // W chunks per row and iteration
-    constexpr int RSH = CPR == 4 ? 2 : CPR == 8 ? 1 : 0;  // W chunk swizzle: + (row >> RSH)
     constexpr bool SCALED = QT != TL_HIP_GGML_F16;   // quant blocks carry an f16 scale
     constexpr bool K4 = QT == TL_HIP_GGML_Q4_K;      // scales: one (d sc, -dmin m) word per unit
     constexpr int XI = BM * 16 / 512;          // X chunks per thread per iteration
@@ -317,11 +319,15 @@ __global__ __launch_bounds__(512) void k_qgemm_mfma(const uint8_t* __restrict__ 
     constexpr int DW = SCALED ? BN * Q_KR / 64 : 0;  // wavefronts that issue one scale DMA instruction
     static_assert(XI >= 1 && WW >= 1 && WW * WPT * 64 == WCH && DW <= 8, "tile");
     // Every operand reaches LDS through global_load_lds (a wavefront's instruction writes 64
-    // consecutive LDS elements, one per lane), so no load in the main loop writes a VGPR.
-    //  * X: row r's 16-byte chunk c (= block * 4 + word) sits at c ^ (r & 15);
-    //  * W: BN rows x CPR chunks, chunk c of row r at (c + (r >> RSH)) mod CPR, and BN x 4
-    //    scales.  Both swizzles make the 16 lanes that read one operand column hit 16
-    //    distinct 16-byte bank groups.
+    //  consecutive LDS elements, one per lane), so no load in the main loop writes a VGPR.
+    //  * X: row r's 16-byte chunk c (= block * 4 + word) sits at c ^ xsw(r & 15);
+    //  * W: chunk-major within each group of 16 rows (chunk c of row r at
+    //    16 CPR (r / 16) + 16 c + r % 16); f16 weights (16 chunks a row, the shape of the X
+    //    tile) row-major with the X swizzle, which keeps a DMA instruction on 4 rows; and BN x 4
+    //    scale words.
+    //  Both layouts measured free of LDS bank conflicts for the fragment reads below on
+    //  gfx950 (rocprofv3 SQ_LDS_BANK_CONFLICT), where a plain c ^ r row swizzle cost ~3.9
+    //  extra cycles per 16-byte read.
     // Two stages, each its own LDS object: the compiler's wait insertion can then see that a
     // stage being filled by DMA is not the one being read, and the next iteration's loads
     // overlap this iteration's MFMAs (with one array indexed by stage it waits for them).
@@ -348,14 +354,16 @@ __global__ __launch_bounds__(512) void k_qgemm_mfma(const uint8_t* __restrict__ 
     uint32_t xoff[XI], woff[WPT] = {}, doff = 0;
 #pragma unroll
     for (int u = 0; u < XI; u++) {
-        const int slot = (wave * XI + u) * 64 + lane, r = slot >> 4, c = (slot & 15) ^ (r & 15);
+        const int slot = (wave * XI + u) * 64 + lane, r = slot >> 4, c = (slot & 15) ^ xsw(r & 15);
         const int64_t row = m0 + r < m ? m0 + r : m - 1;  // rows past m feed outputs that are not stored
         xoff[u] = (uint32_t)((row * k + (c >> 2) * 32 + (c & 3) * 8) * 2);
     }
     if (wave < WW) {
 #pragma unroll
         for (int u = 0; u < WPT; u++) {
-            const int slot = (wave * WPT + u) * 64 + lane, r = slot / CPR, c = (slot % CPR - (r >> RSH)) & (CPR - 1);
+            const int slot = (wave * WPT + u) * 64 + lane, within = slot % (16 * CPR);
+            const int r = CPR == 16 ? slot >> 4 : slot / (16 * CPR) * 16 + within % 16;
+            const int c = CPR == 16 ? (slot & 15) ^ xsw(r & 15) : within / 16;
             const int64_t row = n0 + r < n ? n0 + r : n - 1;
             woff[u] = (uint32_t)((row * nb + c / QC) * QB + (c % QC) * 16);
         }
@@ -399,7 +407,8 @@ __global__ __launch_bounds__(512) void k_qgemm_mfma(const uint8_t* __restrict__ 
 #pragma unroll
             for (int h = 0; h < NW; h++) {
                 const int c = SCALED ? g * QC + h : g * QC + 2 * kh + h;
-                wr[j][h] = *reinterpret_cast<const uint4*>(&st.Wq[(r * CPR + ((c + (r >> RSH)) & (CPR - 1))) * 16]);
+                const int pos = CPR == 16 ? r * 16 + (c ^ xsw(r & 15)) : (r >> 4) * 16 * CPR + c * 16 + (r & 15);
+                wr[j][h] = *reinterpret_cast<const uint4*>(&st.Wq[pos * 16]);
             }
             if constexpr (SCALED) dw[j] = st.Wd[r * Q_KR + g];
         }
@@ -409,7 +418,7 @@ __global__ __launch_bounds__(512) void k_qgemm_mfma(const uint8_t* __restrict__ 
         for (int tt = 0; tt < 2; tt++)
 #pragma unroll
             for (int i = 0; i < TM; i++)
-                a[tt][i] = *reinterpret_cast<const half8*>(xs + (wm * (BM / 2) + 16 * i + col) * 128 + ((g * 4 + 2 * kh + tt) ^ col) * 8);
+                a[tt][i] = *reinterpret_cast<const half8*>(xs + (wm * (BM / 2) + 16 * i + col) * 128 + ((g * 4 + 2 * kh + tt) ^ xsw(col)) * 8);
         __builtin_amdgcn_sched_barrier(0);
         half2v d2[TN], m8d2[TN];
 #pragma unroll
