@@ -230,11 +230,23 @@ int64_t tl_hip_tensor_argmax_all(const tl_hip_tensor* x);
 tl_hip_tensor* tl_hip_tensor_repetition_penalty(const tl_hip_tensor* logits,
                                                 const tl_hip_tensor* tokens, double penalty);
 
-/* GpuFusedOps (crates/tl_backend/src/fused_ops.rs:15-57; tl_cpu fused_ops.rs:15-85) */
+/* GpuFusedOps (crates/tl_backend/src/fused_ops.rs:15-57; tl_cpu fused_ops.rs:15-131) */
 tl_hip_tensor* tl_hip_fused_silu_mul(const tl_hip_tensor* gate, const tl_hip_tensor* up);
 tl_hip_tensor* tl_hip_fused_rms_norm(const tl_hip_tensor* x, const tl_hip_tensor* w, float eps);
 tl_hip_tensor* tl_hip_fused_add_rms_norm(const tl_hip_tensor* x, const tl_hip_tensor* residual,
                                          const tl_hip_tensor* w, float eps);
+/* GpuFusedOps::fused_rotary_emb (fused_ops.rs:38-42; tl_cpu fused_ops.rs:87-108): half-split
+ * pairs rotated by cos / sin of freqs[p] as tl_cpu computes it -- for inputs longer than one
+ * head vector the reference's pair indexing (base = id - id % (head_dim / 2)) overlaps
+ * consecutive vectors, and this entry returns the same values.  ArgumentError when
+ * head_dim < 2, freqs has fewer than head_dim / 2 entries or x fewer than head_dim. */
+tl_hip_tensor* tl_hip_fused_rotary_emb(const tl_hip_tensor* x, const tl_hip_tensor* freqs, int64_t head_dim);
+/* GpuFusedOps::fused_add_relu (fused_ops.rs:47-51; tl_cpu fused_ops.rs:110-120):
+ * max(a + b, 0); ShapeMismatch when the element counts differ. */
+tl_hip_tensor* tl_hip_fused_add_relu(const tl_hip_tensor* a, const tl_hip_tensor* b);
+/* GpuFusedOps::fused_bias_gelu (fused_ops.rs:53-56; tl_cpu fused_ops.rs:122-131 with gelu at
+ * 20-22): gelu(x + bias[i % len(bias)]) with tl_cpu's constant 2/sqrt(pi). */
+tl_hip_tensor* tl_hip_fused_bias_gelu(const tl_hip_tensor* x, const tl_hip_tensor* bias);
 
 /* Single-query decode attention over an f16 KV cache: the chatbot's
  * transpose/cat_4d/repeat_interleave/matmul_4d/scale/softmax/matmul_4d chain

@@ -38,6 +38,9 @@ _PROTOS = {
     "tlo_apply_rope": (None, [_f32p, _i64, _i64, _f32p, _i64, _f32p, _i64, _f32p]),
     "tlo_silu": (None, [_f32p, _i64, _f32p]),
     "tlo_fused_silu_mul": (None, [_f32p, _f32p, _i64, _f32p]),
+    "tlo_fused_rotary_emb": (None, [_f32p, _i64, _f32p, _i64, _f32p]),
+    "tlo_fused_add_relu": (None, [_f32p, _f32p, _i64, _f32p]),
+    "tlo_fused_bias_gelu": (None, [_f32p, _i64, _f32p, _i64, _f32p]),
     "tlo_binop": (_int, [_int, _f32p, _i64p, _int, _f32p, _i64p, _int, _f32p, _i64p]),
     "tlo_scale": (None, [_f32p, _i64, _f64, _f32p]),
     "tlo_softmax": (_int, [_f32p, _i64p, _int, _int, _f32p]),
@@ -202,6 +205,28 @@ def fused_silu_mul(g, u):
     g, u = _f(g), _f(u)
     out = np.empty_like(g)
     lib().tlo_fused_silu_mul(_p(g), _p(u), g.size, _p(out))
+    return out
+
+
+def fused_rotary_emb(x, freqs, head_dim):
+    """tl_cpu fused_rotary_emb (fused_ops.rs:87-108): half-split pairs, cos / sin of freqs."""
+    x, freqs = _f(x), _f(freqs)
+    out = np.empty_like(x)
+    lib().tlo_fused_rotary_emb(_p(x), x.size, _p(freqs), int(head_dim), _p(out))
+    return out
+
+
+def fused_add_relu(a, b):
+    a, b = _f(a), _f(b)
+    out = np.empty_like(a)
+    lib().tlo_fused_add_relu(_p(a), _p(b), a.size, _p(out))
+    return out
+
+
+def fused_bias_gelu(x, bias):
+    x, bias = _f(x), _f(bias)
+    out = np.empty_like(x)
+    lib().tlo_fused_bias_gelu(_p(x), x.size, _p(bias), bias.size, _p(out))
     return out
 
 

@@ -27,6 +27,13 @@
  *   tlo_apply_rope          pos-0 identity (cuda_shader_test.rs:332-355), rotation norm
  *   tlo_softmax             rows sum to 1, monotone (cpu_tensor_tests.rs:439-449)
  *   tlo_argmax_last         hand-built tie cases (last maximum wins)
+ *   tlo_fused_add_relu      reference KAT (tl_cuda new_ops_comprehensive_test.rs:624-632)
+ *   tlo_fused_bias_gelu     reference KAT gelu(0) = 0 (new_ops_comprehensive_test.rs:687-693),
+ *                           signs at +-1.1 (tl_metal fused_ops_test.rs:60-75), limits
+ *                           gelu(v) -> v / 0 for large |v|, bias broadcast i % nbias
+ *   tlo_fused_rotary_emb    one head vector: the textbook half-split rotation (norm of each
+ *                           pair kept, f = 0 identity, f = pi/2 (x0, x1) -> (-x1, x0));
+ *                           several vectors: brute-force replay of the reference loop
  *   remaining glue ops      numpy equivalents on small inputs
  */
 #include <math.h>
@@ -423,6 +430,45 @@ void tlo_silu(const float* x, int64_t n, float* out) {
  * (g / (1 + exp(-g))) * u. */
 void tlo_fused_silu_mul(const float* g, const float* u, int64_t n, float* out) {
     for (int64_t i = 0; i < n; i++) out[i] = (g[i] / (1.0f + expf(-g[i]))) * u[i];
+}
+
+/* GpuFusedOps::fused_rotary_emb for CpuTensor (crates/tl_cpu/src/fused_ops.rs:87-108): for id
+ * in 0 .. count / 2, with half = head_dim / 2, p = id % half, base = id - p, f = freqs[p]:
+ *   out[base + p]        = x[base + p] cos f - x[base + p + half] sin f
+ *   out[base + p + half] = x[base + p] sin f + x[base + p + half] cos f
+ * in id order over a zero-filled output, cos / sin of f32 (f32::cos / f32::sin).  Past the
+ * first head vector the pairs of consecutive ids overlap (base steps by half, not head_dim),
+ * and later ids overwrite earlier ones; restated as the reference loop, quirk included. */
+void tlo_fused_rotary_emb(const float* x, int64_t count, const float* freqs, int64_t head_dim, float* out) {
+    const int64_t half = head_dim / 2;
+    for (int64_t i = 0; i < count; i++) out[i] = 0.0f;
+    if (half <= 0) return;
+    for (int64_t id = 0; id < count / 2; id++) {
+        const int64_t p = id % half, base = id - p;
+        const float f = freqs[p], c = cosf(f), sn = sinf(f);
+        const float x0 = x[base + p], x1 = x[base + p + half];
+        out[base + p] = x0 * c - x1 * sn;
+        out[base + p + half] = x0 * sn + x1 * c;
+    }
+}
+
+/* GpuFusedOps::fused_add_relu for CpuTensor (crates/tl_cpu/src/fused_ops.rs:110-120):
+ * (a + b).max(0.0); f32::max returns the other operand when one is NaN. */
+void tlo_fused_add_relu(const float* a, const float* b, int64_t n, float* out) {
+    for (int64_t i = 0; i < n; i++) out[i] = fmaxf(a[i] + b[i], 0.0f);
+}
+
+/* GpuFusedOps::fused_bias_gelu for CpuTensor (crates/tl_cpu/src/fused_ops.rs:122-131) with the
+ * crate's gelu (fused_ops.rs:20-22): v = x + bias[i % nbias];
+ * 0.5 v (1 + tanh(FRAC_2_SQRT_PI (v + 0.044715 v^3))), v^3 = powi(3) = (v v) v.  The constant
+ * is 2/sqrt(pi) as the reference writes it (the textbook tanh form has sqrt(2/pi)). */
+void tlo_fused_bias_gelu(const float* x, int64_t n, const float* bias, int64_t nbias, float* out) {
+    const float k = 1.12837916709551257390f;  /* f32 FRAC_2_SQRT_PI */
+    for (int64_t i = 0; i < n; i++) {
+        const float v = x[i] + bias[i % nbias];
+        const float v3 = (v * v) * v;
+        out[i] = 0.5f * v * (1.0f + tanhf(k * (v + 0.044715f * v3)));
+    }
 }
 
 /* CpuTensor::elementwise_binop (crates/tl_cpu/src/tensor.rs:549-609): numpy broadcasting;

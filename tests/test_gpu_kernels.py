@@ -135,6 +135,36 @@ def test_rms_norm(dev):
                F32_TOL)
 
 
+def test_fused_tier2_ops(dev):
+    """fused_rotary_emb / fused_add_relu / fused_bias_gelu against the oracle (tl_cpu
+    semantics): one head vector and a [16, 32, 64] input (the reference's overlapping pair
+    indexing past the first vector), NaN in add_relu, bias broadcast, error paths."""
+    rng = np.random.default_rng(0x71510002)
+    f = rng.uniform(-4, 4, 32).astype(np.float32)
+    for shape in ((64,), (16, 32, 64), (5, 64)):
+        x = rng.standard_normal(shape).astype(np.float32)
+        got = dev.fused_rotary_emb(dev.tensor_new(x), dev.tensor_new(f), 64).to_numpy()
+        assert got.shape == shape
+        assert_rel(got, oracle.fused_rotary_emb(x, f, 64), F32_TOL)
+    a = rng.standard_normal((512, 4096)).astype(np.float32)
+    b = rng.standard_normal((512, 4096)).astype(np.float32)
+    a[0, :3] = [np.nan, -1.0, 1.0]
+    got = dev.fused_add_relu(dev.tensor_new(a), dev.tensor_new(b)).to_numpy()
+    np.testing.assert_array_equal(got, oracle.fused_add_relu(a, b))  # add and max are exact
+    bias = rng.standard_normal(4096).astype(np.float32)
+    assert_rel(dev.fused_bias_gelu(dev.tensor_new(a[1:]), dev.tensor_new(bias)).to_numpy(),
+               oracle.fused_bias_gelu(a[1:], bias), F32_TOL)
+    with pytest.raises(BackendError) as e:
+        dev.fused_add_relu(dev.tensor_new(a), dev.tensor_new(b[:1]))
+    assert e.value.variant == "ShapeMismatch"
+    with pytest.raises(BackendError) as e:  # fewer than head_dim / 2 freqs
+        dev.fused_rotary_emb(dev.tensor_new(a[0, :64]), dev.tensor_new(f[:8]), 64)
+    assert e.value.variant == "ArgumentError"
+    with pytest.raises(BackendError) as e:
+        dev.fused_bias_gelu(dev.tensor_new(a), dev.tensor_new(np.zeros(0, np.float32)))
+    assert e.value.variant == "ArgumentError"
+
+
 def test_rope(dev):
     rng = np.random.default_rng(0x71510001)
     x = rng.standard_normal((512, 32, 128)).astype(np.float32)

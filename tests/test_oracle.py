@@ -258,3 +258,63 @@ def test_attention_direct_equals_op_chain():
         sm = oracle.softmax(sc, 3)
         ao = oracle.transpose(oracle.matmul(sm, vw), 1, 2).reshape(s, nh * hd)
         assert np.array_equal(got, ao)
+
+
+def test_fused_add_relu_pins():
+    # known answer of the reference (tl_cuda new_ops_comprehensive_test.rs:624-632)
+    a = np.array([-1.0, 2.0, -3.0, 4.0], np.float32)
+    b = np.array([0.5, -3.0, 5.0, -1.0], np.float32)
+    np.testing.assert_array_equal(oracle.fused_add_relu(a, b), [0.0, 0.0, 2.0, 3.0])
+    # f32::max(NaN, 0) is 0
+    assert oracle.fused_add_relu(np.array([np.nan], np.float32), np.array([1.0], np.float32))[0] == 0.0
+
+
+def test_fused_bias_gelu_pins():
+    # gelu(0 + 0) = 0 (new_ops_comprehensive_test.rs:687-693)
+    np.testing.assert_array_equal(oracle.fused_bias_gelu(np.zeros((2, 2), np.float32), np.zeros(2, np.float32)), 0)
+    # signs at +-1.1 (tl_metal fused_ops_test.rs:60-75)
+    y = oracle.fused_bias_gelu(np.array([1.0, -1.0], np.float32), np.array([0.1, -0.1], np.float32))
+    assert y[0] > 0.9 and y[1] < 0.0
+    # limits: gelu(v) -> v for large v, -> 0 for very negative v
+    np.testing.assert_allclose(oracle.fused_bias_gelu(np.array([20.0, -20.0], np.float32), np.zeros(1, np.float32)),
+                               [20.0, 0.0], atol=1e-6)
+    # bias broadcast i % len(bias): the same as adding the tiled bias first
+    rng = np.random.default_rng(5)
+    x = rng.standard_normal((3, 7)).astype(np.float32)
+    bias = rng.standard_normal(7).astype(np.float32)
+    np.testing.assert_array_equal(oracle.fused_bias_gelu(x, bias),
+                                  oracle.fused_bias_gelu((x + bias).astype(np.float32), np.zeros(1, np.float32)))
+    # the reference's constant is 2/sqrt(pi): gelu(1) = 0.5 (1 + tanh(2/sqrt(pi) 1.044715)),
+    # not the textbook sqrt(2/pi) value 0.8412
+    g1 = oracle.fused_bias_gelu(np.array([1.0], np.float32), np.zeros(1, np.float32))[0]
+    assert abs(g1 - 0.5 * (1 + np.tanh(2 / np.sqrt(np.pi) * 1.044715))) < 1e-6
+    assert abs(g1 - 0.8412) > 0.05
+
+
+def _rotary_replay(x, f, hd):
+    # the reference loop (tl_cpu fused_ops.rs:87-108), element by element in float64
+    half, out = hd // 2, np.zeros(x.size, np.float64)
+    for i in range(x.size // 2):
+        p = i % half
+        base = i - p
+        c, s = np.cos(np.float64(f[p])), np.sin(np.float64(f[p]))
+        x0, x1 = float(x[base + p]), float(x[base + p + half])
+        out[base + p] = x0 * c - x1 * s
+        out[base + p + half] = x0 * s + x1 * c
+    return out
+
+
+def test_fused_rotary_emb_pins():
+    rng = np.random.default_rng(6)
+    hd = 8
+    x = rng.standard_normal(hd).astype(np.float32)
+    f = rng.uniform(-3, 3, hd // 2).astype(np.float32)
+    y = oracle.fused_rotary_emb(x, f, hd)
+    # one head vector: each (x_p, x_{p+half}) pair rotated, norms kept
+    np.testing.assert_allclose(y[:4] ** 2 + y[4:] ** 2, x[:4] ** 2 + x[4:] ** 2, rtol=1e-5)
+    np.testing.assert_array_equal(oracle.fused_rotary_emb(x, np.zeros(4, np.float32), hd), x)
+    q = oracle.fused_rotary_emb(x, np.full(4, np.pi / 2, np.float32), hd)
+    np.testing.assert_allclose(q, np.concatenate([-x[4:], x[:4]]), atol=1e-6)
+    # several vectors: the reference loop replayed (pairs of consecutive vectors overlap)
+    x3 = rng.standard_normal(3 * hd + 4).astype(np.float32)
+    np.testing.assert_allclose(oracle.fused_rotary_emb(x3, f, hd), _rotary_replay(x3, f, hd), rtol=2e-6, atol=2e-6)

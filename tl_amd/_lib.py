@@ -91,6 +91,9 @@ PROTOS = {
     "tl_hip_tensor_argmax_all": (i64, [P]),
     "tl_hip_tensor_repetition_penalty": (P, [P, P, f64]),
     "tl_hip_fused_silu_mul": (P, [P, P]),
+    "tl_hip_fused_rotary_emb": (P, [P, P, i64]),
+    "tl_hip_fused_add_relu": (P, [P, P]),
+    "tl_hip_fused_bias_gelu": (P, [P, P]),
     "tl_hip_fused_rms_norm": (P, [P, P, f32]),
     "tl_hip_fused_add_rms_norm": (P, [P, P, P, f32]),
     "tl_hip_attention_decode": (P, [P, P, P, i64, f32]),

@@ -622,6 +622,46 @@ int launch_rope_table(float* out, int64_t seq_len, int64_t dim, float base, int 
 
 }  // namespace tlhip
 
+// GpuFusedOps::fused_rotary_emb as tl_cpu computes it (fused_ops.rs:87-108): the reference
+// loop over id < count / 2 writes out[id] (first element of id's pair) and out[id + half]
+// (second element), later ids overwriting earlier ones on a zero-filled output.  Element i
+// therefore holds the first-element value of id = i when i < count / 2, else the
+// second-element value of id = i - half when that id exists, else 0 -- one thread per
+// element, no write order to keep.
+__global__ void k_fused_rotary(const float* __restrict__ x, const float* __restrict__ freqs, float* __restrict__ o,
+                               int64_t count, int64_t half) {
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= count) return;
+    const int64_t h2 = count / 2;
+    const bool first = i < h2, second = !first && i - half >= 0 && i - half < h2;
+    float v = 0.f;
+    if (first || second) {
+        const int64_t id = first ? i : i - half;
+        const float f = freqs[id % half], c = cosf(f), sn = sinf(f);
+        const float x0 = x[id], x1 = x[id + half];
+        v = first ? x0 * c - x1 * sn : x0 * sn + x1 * c;
+    }
+    o[i] = v;
+}
+
+// GpuFusedOps::fused_add_relu (tl_cpu fused_ops.rs:110-120): (a + b).max(0), NaN -> 0
+__global__ void k_fused_add_relu(const float* __restrict__ a, const float* __restrict__ b, float* __restrict__ o,
+                                 int64_t n) {
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) o[i] = fmaxf(a[i] + b[i], 0.f);
+}
+
+// GpuFusedOps::fused_bias_gelu (tl_cpu fused_ops.rs:122-131) with that crate's gelu
+// (fused_ops.rs:20-22): v = x + bias[i % nbias], 0.5 v (1 + tanh(2/sqrt(pi) (v + 0.044715 v^3)))
+__global__ void k_fused_bias_gelu(const float* __restrict__ x, const float* __restrict__ bias, float* __restrict__ o,
+                                  int64_t n, int64_t nbias) {
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= n) return;
+    const float v = x[i] + bias[i % nbias];
+    const float v3 = (v * v) * v;
+    o[i] = 0.5f * v * (1.0f + tanhf(1.12837916709551257390f * (v + 0.044715f * v3)));
+}
+
 // =============================================================== C ABI wrappers ======
 using namespace tlhip;
 
@@ -769,6 +809,52 @@ tl_hip_tensor* tl_hip_tensor_silu(const tl_hip_tensor* x) {
     if (!o) return nullptr;
     if (t->numel) k_silu<<<cdiv(t->numel, 256), 256, 0, cur_stream()>>>(t->f32(), o->f32(), t->numel);
     return finish(o, last_launch("silu launch"));
+}
+
+tl_hip_tensor* tl_hip_fused_rotary_emb(const tl_hip_tensor* x, const tl_hip_tensor* freqs, int64_t head_dim) {
+    if (!need(x, "input") || !need(freqs, "freqs")) return nullptr;
+    const Tensor* t = CT(x);
+    const int64_t half = head_dim / 2, count = t->numel;
+    // the reference indexes freqs[0 .. half) and x[0 .. count / 2 + half) (fused_ops.rs:93-100)
+    if (half < 1 || CT(freqs)->numel < half || (count > 0 && count / 2 + half > count)) {
+        set_error(TL_HIP_ERR_ARG, "ArgumentError: fused_rotary_emb: head_dim %lld with %lld elements and %lld freqs",
+                  (long long)head_dim, (long long)count, (long long)CT(freqs)->numel);
+        return nullptr;
+    }
+    Tensor* o = tensor_alloc(t->shape, t->rank);
+    if (!o) return nullptr;
+    if (count)
+        k_fused_rotary<<<cdiv(count, 256), 256, 0, cur_stream()>>>(t->f32(), CT(freqs)->f32(), o->f32(), count, half);
+    return finish(o, last_launch("fused rotary launch"));
+}
+
+tl_hip_tensor* tl_hip_fused_add_relu(const tl_hip_tensor* a, const tl_hip_tensor* b) {
+    if (!need(a, "lhs") || !need(b, "rhs")) return nullptr;
+    if (CT(a)->numel != CT(b)->numel) {  // the reference asserts equal counts (fused_ops.rs:112)
+        set_error(TL_HIP_ERR_SHAPE, "ShapeMismatch: fused_add_relu: shape mismatch");
+        return nullptr;
+    }
+    const Tensor* t = CT(a);
+    Tensor* o = tensor_alloc(t->shape, t->rank);
+    if (!o) return nullptr;
+    if (t->numel)
+        k_fused_add_relu<<<cdiv(t->numel, 256), 256, 0, cur_stream()>>>(t->f32(), CT(b)->f32(), o->f32(), t->numel);
+    return finish(o, last_launch("fused add-relu launch"));
+}
+
+tl_hip_tensor* tl_hip_fused_bias_gelu(const tl_hip_tensor* x, const tl_hip_tensor* bias) {
+    if (!need(x, "input") || !need(bias, "bias")) return nullptr;
+    if (CT(bias)->numel < 1) {  // i % 0 in the reference
+        set_error(TL_HIP_ERR_ARG, "ArgumentError: fused_bias_gelu: empty bias");
+        return nullptr;
+    }
+    const Tensor* t = CT(x);
+    Tensor* o = tensor_alloc(t->shape, t->rank);
+    if (!o) return nullptr;
+    if (t->numel)
+        k_fused_bias_gelu<<<cdiv(t->numel, 256), 256, 0, cur_stream()>>>(t->f32(), CT(bias)->f32(), o->f32(), t->numel,
+                                                                          CT(bias)->numel);
+    return finish(o, last_launch("fused bias-gelu launch"));
 }
 
 tl_hip_tensor* tl_hip_fused_silu_mul(const tl_hip_tensor* g, const tl_hip_tensor* u) {

@@ -252,6 +252,15 @@ class HipDevice:
     def fused_add_rms_norm(self, x, residual, w, eps):
         return self._wrap(self.lib.tl_hip_fused_add_rms_norm(x.handle, residual.handle, w.handle, eps))
 
+    def fused_rotary_emb(self, x, freqs, head_dim):
+        return self._wrap(self.lib.tl_hip_fused_rotary_emb(x.handle, freqs.handle, head_dim))
+
+    def fused_add_relu(self, a, b):
+        return self._wrap(self.lib.tl_hip_fused_add_relu(a.handle, b.handle))
+
+    def fused_bias_gelu(self, x, bias):
+        return self._wrap(self.lib.tl_hip_fused_bias_gelu(x.handle, bias.handle))
+
     # -- decode attention over a KV cache
     def attention_decode(self, q, k, v, length, scale):
         return self._wrap(self.lib.tl_hip_attention_decode(q.handle, k.handle, v.handle, length, scale))
