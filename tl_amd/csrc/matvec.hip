@@ -10,8 +10,9 @@
 // (TC = the block count nb rounded up to wavefronts, at most 256).  Thread (s, t) owns block
 // columns t, t + TC, ... (BT per pass) of the RW / S rows s, s + S, ...:
 //   * one load instruction covers TC consecutive 16-byte quant blocks of one row;
-//   * the thread's activation blocks (32 floats each) are loaded once, straight into
-//     registers, and reused for its rows -- no LDS staging and no barrier before the math;
+//   * the activations are staged once per workgroup in LDS (coalesced loads, 36-float pitch
+//     per 32-float block so that lane-consecutive blocks read distinct banks); each thread
+//     reads its blocks from there and reuses them for its rows;
 //   * the K dimension is split across the wavefronts of a subset.  Row sums are formed by a
 //     transpose-reduce inside each wavefront (each exchange step halves the number of
 //     values a lane carries: N - 1 exchanges for N values instead of 6 per value) and one
@@ -20,7 +21,8 @@
 //     after the weight loads, so no memory round trip is left after the reduction.
 //
 // Per unit the thread forms d * (sum_j x_j q_j - 8 sum_j x_j) (Q4_0; Q8_0 uses q ^ 0x80 and
-// 128), one byte->float conversion and one FMA per weight, f32 throughout.  The K-quants use
+// 128), f32 throughout: one FMA per weight, plus one byte->float conversion per weight (Q8_0,
+// Q6_K) or per two weights (the 4-bit types, through the fp8 pair conversion).  The K-quants use
 // the same dot products with their own scale terms: Q4_K (d sc) sum x q - (dmin m) sum x
 // with (sc, m) decoded from the super-block header; Q6_K rebuilds each 6-bit value as one
 // byte (low nibble | high bits << 4) and forms sum over its two 16-weight halves of
@@ -47,6 +49,8 @@
 #include "internal.h"
 
 namespace tlhip {
+
+typedef float float2v __attribute__((ext_vector_type(2)));
 
 template <int QT>
 struct QB_;
@@ -197,127 +201,54 @@ __global__ __launch_bounds__(256) void k_mv(MvArgs a, MvShape sh) {
 #pragma unroll
         for (int r = 0; r < RWT; r++) acc[m][r] = 0.f;
 
-    for (uint32_t base = 0; base < nb; base += (uint32_t)(BT * TC)) {
-        uint32_t bc[BT];
-        bool valid[BT];
+    constexpr bool K4 = QT == TL_HIP_GGML_Q4_K, K6 = QT == TL_HIP_GGML_Q6_K;
+    constexpr bool NIB = QT == TL_HIP_GGML_Q4_0 || K4;  // 4-bit quants in Q4_0 nibble order
+    uint32_t bc[BT];
+    bool valid[BT];
+    uint4 w[BT][RWT][QW];
+    uint16_t dh[BT][RWT];           // Q4_0 / Q8_0 / Q6_K (super-block) scale, f16 bits
+    uint4 kh[BT][K4 ? RWT : 1];     // Q4_K super-block header
+    uint2 h6[BT][K6 ? RWT : 1];     // Q6_K high bits
+    uint32_t s6[BT][K6 ? RWT : 1];  // Q6_K scale pair
+    auto set_cols = [&](uint32_t base) {
 #pragma unroll
         for (int i = 0; i < BT; i++) {
             const uint32_t b = base + (uint32_t)(tcol + i * TC);
             valid[i] = b < nb;
             bc[i] = valid[i] ? b : nb - 1;  // past the end: read the last column, scale 0
         }
-        constexpr bool K4 = QT == TL_HIP_GGML_Q4_K, K6 = QT == TL_HIP_GGML_Q6_K;
-        uint4 w[BT][RWT][QW];
-        float dd[BT][RWT];                  // Q4_0 / Q8_0 / Q6_K (super-block) scale
-        uint4 kh[BT][K4 ? RWT : 1];         // Q4_K super-block header
-        uint2 h6[BT][K6 ? RWT : 1];         // Q6_K high bits
-        uint32_t s6[BT][K6 ? RWT : 1];      // Q6_K scale pair
-        auto load_w = [&]() {
+    };
+    // Scale data is kept as loaded and decoded in the math, so nothing before the staging
+    // barrier waits for the weight stream.
+    auto load_w = [&]() {
 #pragma unroll
-            for (int i = 0; i < BT; i++) {
+        for (int i = 0; i < BT; i++) {
 #pragma unroll
-                for (int r = 0; r < RWT; r++) {
-                    uint32_t row = my_row0 + (uint32_t)(S * r);
-                    row = row < n ? row : n - 1;
-                    const uint32_t blk = __umul24(row, nb) + bc[i];
-                    const uint4* p = reinterpret_cast<const uint4*>(a.qs + (size_t)blk * QB);
+            for (int r = 0; r < RWT; r++) {
+                uint32_t row = my_row0 + (uint32_t)(S * r);
+                row = row < n ? row : n - 1;
+                const uint32_t blk = __umul24(row, nb) + bc[i];
+                const uint4* p = reinterpret_cast<const uint4*>(a.qs + (size_t)blk * QB);
 #pragma unroll
-                    for (int c = 0; c < QW; c++) w[i][r][c] = p[c];
-                    if constexpr (K4) {
-                        kh[i][r] = reinterpret_cast<const uint4*>(a.hdr)[blk >> 3];
-                    } else if constexpr (K6) {
-                        h6[i][r] = reinterpret_cast<const uint2*>(a.qh)[blk];
-                        s6[i][r] = reinterpret_cast<const uint16_t*>(a.sc)[blk];
-                        const float dv = __half2float(a.d[blk >> 3]);
-                        dd[i][r] = valid[i] ? dv : 0.f;
-                    } else {
-                        const float dv = __half2float(a.d[blk]);
-                        dd[i][r] = valid[i] ? dv : 0.f;
-                    }
+                for (int c = 0; c < QW; c++) w[i][r][c] = p[c];
+                if constexpr (K4) {
+                    kh[i][r] = reinterpret_cast<const uint4*>(a.hdr)[blk >> 3];
+                } else if constexpr (K6) {
+                    h6[i][r] = reinterpret_cast<const uint2*>(a.qh)[blk];
+                    s6[i][r] = reinterpret_cast<const uint16_t*>(a.sc)[blk];
+                    dh[i][r] = reinterpret_cast<const uint16_t*>(a.d)[blk >> 3];
+                } else {
+                    dh[i][r] = reinterpret_cast<const uint16_t*>(a.d)[blk];
                 }
             }
-        };
-
-        if (base == 0) {
-            // (1) the activations (all passes) are staged once per workgroup in LDS with
-            // coalesced loads -- a lane reading its own 128-byte block straight from memory
-            // would touch 64 cache lines per load instruction.  The first XRK float4 per
-            // thread are requested before the weights of the first pass, the stores follow
-            // them, so the weight stream is in flight while the staging completes.
-            const float* xsrc = EMBED ? a.x + (size_t)(*a.embed_id) * k : a.x;
-            const uint32_t k4 = k >> 2, nthr = blockDim.x;
-            float s2[M];
-            constexpr int XRK = NORM ? (RWT >= 8 ? XR_NORM8 : XR_NORM) : XR;
-            float4 xr[M][XRK], gr[NORM ? XRK : 1];
-#pragma unroll
-            for (int m = 0; m < M; m++) {
-                s2[m] = 0.f;
-#pragma unroll
-                for (int j = 0; j < XRK; j++) {
-                    const uint32_t e = tid + j * nthr;
-                    if (e < k4) xr[m][j] = reinterpret_cast<const float4*>(xsrc + m * k)[e];
-                }
-            }
-            if constexpr (NORM) {
-#pragma unroll
-                for (int j = 0; j < XRK; j++) {
-                    const uint32_t e = tid + j * nthr;
-                    if (e < k4) gr[j] = reinterpret_cast<const float4*>(a.norm_w)[e];
-                }
-            }
-            load_w();
-            auto stage = [&](int m, uint32_t e, float4 v, float4 g) {
-                if constexpr (EMBED) {
-                    if (blockIdx.x == 0 && a.x_out) reinterpret_cast<float4*>(a.x_out)[e] = v;
-                }
-                if constexpr (NORM) {
-                    s2[m] = fmaf(v.x, v.x, fmaf(v.y, v.y, fmaf(v.z, v.z, fmaf(v.w, v.w, s2[m]))));
-                    v.x *= g.x;
-                    v.y *= g.y;
-                    v.z *= g.z;
-                    v.w *= g.w;
-                }
-                *reinterpret_cast<float4*>(xs + (m * nb + (e >> 3)) * XPAD + (e & 7) * 4) = v;
-            };
-#pragma unroll
-            for (int m = 0; m < M; m++) {
-#pragma unroll
-                for (int j = 0; j < XRK; j++) {
-                    const uint32_t e = tid + j * nthr;
-                    if (e < k4) stage(m, e, xr[m][j], NORM ? gr[j] : xr[m][j]);
-                }
-                for (uint32_t e = tid + XRK * nthr; e < k4; e += nthr) {  // long rows only
-                    const float4 v = reinterpret_cast<const float4*>(xsrc + m * k)[e];
-                    stage(m, e, v, NORM ? reinterpret_cast<const float4*>(a.norm_w)[e] : v);
-                }
-            }
-            if constexpr (NORM) {
-#pragma unroll
-                for (int m = 0; m < M; m++) {
-                    const float ss = wsum(s2[m]);
-                    if (lane == 0) ssq[wave][m] = ss;
-                }
-            }
-            if constexpr (EPI == EPI_RES) {
-                if (tid < M * RW && row0 + (tid & (RW - 1)) < n)
-                    pre_res = a.res[(tid >> rw_shift) * n + row0 + (tid & (RW - 1))];
-            } else if constexpr (EPI == EPI_ROPE_KV) {
-                pre_pos = (uint32_t)*a.pos;
-                const uint32_t r0 = row0 + 2 * tid + (uint32_t)a.row_off;
-                if (tid < RW / 2 && row0 + 2 * tid < n && r0 < (uint32_t)(a.q_rows + a.kv_rows)) {
-                    const uint32_t i = (r0 < (uint32_t)a.q_rows ? r0 : r0 - a.q_rows) % (uint32_t)a.hd;
-                    pre_c = a.cos_t[pre_pos * a.hd + i];
-                    pre_s = a.sin_t[pre_pos * a.hd + i];
-                }
-            } else if constexpr (EPI == EPI_ARGMAX) {
-                if (a.seen && tid < RW && row0 + tid < n) pre_seen = a.seen[row0 + tid];
-            }
-            __syncthreads();
-        } else {
-            load_w();
         }
+    };
+    auto scale = [&](int i, int r) {
+        return valid[i] ? __half2float(__ushort_as_half(dh[i][r])) : 0.f;
+    };
 
-        // (3) block dot products
+    // block dot products of one pass
+    auto compute = [&]() {
 #pragma unroll
         for (int i = 0; i < BT; i++) {
             float xv[M][1][32];  // this thread's block of the staged activations
@@ -346,29 +277,43 @@ __global__ __launch_bounds__(256) void k_mv(MvArgs a, MvShape sh) {
                 sxh[m] = sx1;
                 sx[m] = sx0 + sx1;
             }
-            // row outer, activation row inner: each quant word is unpacked once.  Q4_0 high
-            // nibbles are taken in place (16 q, one AND) and the factor 1/16 applied to their
-            // sum, which is exact.
+            // row outer, activation row inner: each quant word is unpacked once
 #pragma unroll
             for (int r = 0; r < RWT; r++) {
                 float s0[M], s1[M];
 #pragma unroll
                 for (int m = 0; m < M; m++) s0[m] = s1[m] = 0.f;
-                if constexpr (QT == TL_HIP_GGML_Q4_0 || QT == TL_HIP_GGML_Q4_K) {
+                if constexpr (NIB) {
+                    // a byte n < 16 read as OCP e4m3 is exactly n * 2^-9 (exponent field 0 or 1),
+                    // so one v_cvt_pk_f32_fp8 turns two nibbles into floats; the sums carry the
+                    // factor 2^-9 exactly and it is removed once per unit
                     const uint32_t q[4] = {w[i][r][0].x, w[i][r][0].y, w[i][r][0].z, w[i][r][0].w};
 #pragma unroll
                     for (int c = 0; c < 4; c++) {
-                        const uint32_t lo = q[c] & 0x0F0F0F0Fu, hi = q[c] & 0xF0F0F0F0u;
+                        const uint32_t lo = q[c] & 0x0F0F0F0Fu, hi = (q[c] >> 4) & 0x0F0F0F0Fu;
+                        const float2v l01 = __builtin_amdgcn_cvt_pk_f32_fp8((int)lo, false);
+                        const float2v l23 = __builtin_amdgcn_cvt_pk_f32_fp8((int)lo, true);
+                        const float2v h01 = __builtin_amdgcn_cvt_pk_f32_fp8((int)hi, false);
+                        const float2v h23 = __builtin_amdgcn_cvt_pk_f32_fp8((int)hi, true);
 #pragma unroll
                         for (int m = 0; m < M; m++) {
-                            s0[m] = fma4b(lo, xv[m][0] + 4 * c, s0[m]);
-                            s1[m] = fma4b(hi, xv[m][0] + 16 + 4 * c, s1[m]);
+                            const float* xl = xv[m][0] + 4 * c;
+                            const float* xh = xv[m][0] + 16 + 4 * c;
+                            s0[m] = fmaf(xl[0], l01.x, s0[m]);
+                            s0[m] = fmaf(xl[1], l01.y, s0[m]);
+                            s0[m] = fmaf(xl[2], l23.x, s0[m]);
+                            s0[m] = fmaf(xl[3], l23.y, s0[m]);
+                            s1[m] = fmaf(xh[0], h01.x, s1[m]);
+                            s1[m] = fmaf(xh[1], h01.y, s1[m]);
+                            s1[m] = fmaf(xh[2], h23.x, s1[m]);
+                            s1[m] = fmaf(xh[3], h23.y, s1[m]);
                         }
                     }
                     if constexpr (QT == TL_HIP_GGML_Q4_0) {
+                        const float dd = scale(i, r);
 #pragma unroll
                         for (int m = 0; m < M; m++)
-                            acc[m][r] = fmaf(dd[i][r], fmaf(s1[m], 0.0625f, s0[m]) - 8.f * sx[m], acc[m][r]);
+                            acc[m][r] = fmaf(dd, (s0[m] + s1[m]) * 512.f - 8.f * sx[m], acc[m][r]);
                     } else {
                         // unit = sub-block bc & 7: du * sum x q - mu * sum x
                         float du, mu;
@@ -377,7 +322,7 @@ __global__ __launch_bounds__(256) void k_mv(MvArgs a, MvShape sh) {
                         mu = valid[i] ? mu : 0.f;
 #pragma unroll
                         for (int m = 0; m < M; m++)
-                            acc[m][r] = fmaf(du, fmaf(s1[m], 0.0625f, s0[m]), fmaf(-mu, sx[m], acc[m][r]));
+                            acc[m][r] = fmaf(du, (s0[m] + s1[m]) * 512.f, fmaf(-mu, sx[m], acc[m][r]));
                     }
                 } else if constexpr (QT == TL_HIP_GGML_Q6_K) {
                     // 6-bit values rebuilt per byte: low nibble | high 2 bits << 4
@@ -393,8 +338,9 @@ __global__ __launch_bounds__(256) void k_mv(MvArgs a, MvShape sh) {
                             s1[m] = fma4b(hi, xv[m][0] + 16 + 4 * c, s1[m]);
                         }
                     }
-                    const float e0 = dd[i][r] * (float)(int8_t)(s6[i][r] & 0xFF);
-                    const float e1 = dd[i][r] * (float)(int8_t)(s6[i][r] >> 8);
+                    const float dd = scale(i, r);
+                    const float e0 = dd * (float)(int8_t)(s6[i][r] & 0xFF);
+                    const float e1 = dd * (float)(int8_t)(s6[i][r] >> 8);
 #pragma unroll
                     for (int m = 0; m < M; m++)
                         acc[m][r] = fmaf(e0, fmaf(-32.f, sxl[m], s0[m]), fmaf(e1, fmaf(-32.f, sxh[m], s1[m]), acc[m][r]));
@@ -410,12 +356,98 @@ __global__ __launch_bounds__(256) void k_mv(MvArgs a, MvShape sh) {
                             s1[m] = fma4b(hi, xv[m][0] + 16 + 4 * c, s1[m]);
                         }
                     }
+                    const float dd = scale(i, r);
 #pragma unroll
                     for (int m = 0; m < M; m++)
-                        acc[m][r] = fmaf(dd[i][r], (s0[m] + s1[m]) - 128.f * sx[m], acc[m][r]);
+                        acc[m][r] = fmaf(dd, (s0[m] + s1[m]) - 128.f * sx[m], acc[m][r]);
                 }
             }
         }
+    };
+
+    // (1) first pass, with the activations (all passes) staged once per workgroup in LDS by
+    // coalesced loads -- a lane reading its own 128-byte block straight from memory would
+    // touch 64 cache lines per load instruction.  The first XRK float4 per thread are
+    // requested before the weights of the first pass and stored once they arrive, so the
+    // weight stream is in flight while the staging completes.
+    if constexpr (EPI == EPI_ROPE_KV) pre_pos = (uint32_t)*a.pos;
+    set_cols(0);
+    {
+        const float* xsrc = EMBED ? a.x + (size_t)(*a.embed_id) * k : a.x;
+        const uint32_t k4 = k >> 2, nthr = blockDim.x;
+        float s2[M];
+        constexpr int XRK = NORM ? (RWT >= 8 ? XR_NORM8 : XR_NORM) : XR;
+        float4 xr[M][XRK], gr[NORM ? XRK : 1];
+#pragma unroll
+        for (int m = 0; m < M; m++) {
+            s2[m] = 0.f;
+#pragma unroll
+            for (int j = 0; j < XRK; j++) {
+                const uint32_t e = tid + j * nthr;
+                if (e < k4) xr[m][j] = reinterpret_cast<const float4*>(xsrc + m * k)[e];
+            }
+        }
+        if constexpr (NORM) {
+#pragma unroll
+            for (int j = 0; j < XRK; j++) {
+                const uint32_t e = tid + j * nthr;
+                if (e < k4) gr[j] = reinterpret_cast<const float4*>(a.norm_w)[e];
+            }
+        }
+        load_w();
+        auto stage = [&](int m, uint32_t e, float4 v, float4 g) {
+            if constexpr (EMBED) {
+                if (blockIdx.x == 0 && a.x_out) reinterpret_cast<float4*>(a.x_out)[e] = v;
+            }
+            if constexpr (NORM) {
+                s2[m] = fmaf(v.x, v.x, fmaf(v.y, v.y, fmaf(v.z, v.z, fmaf(v.w, v.w, s2[m]))));
+                v.x *= g.x;
+                v.y *= g.y;
+                v.z *= g.z;
+                v.w *= g.w;
+            }
+            *reinterpret_cast<float4*>(xs + (m * nb + (e >> 3)) * XPAD + (e & 7) * 4) = v;
+        };
+#pragma unroll
+        for (int m = 0; m < M; m++) {
+#pragma unroll
+            for (int j = 0; j < XRK; j++) {
+                const uint32_t e = tid + j * nthr;
+                if (e < k4) stage(m, e, xr[m][j], NORM ? gr[j] : xr[m][j]);
+            }
+            for (uint32_t e = tid + XRK * nthr; e < k4; e += nthr) {  // long rows only
+                const float4 v = reinterpret_cast<const float4*>(xsrc + m * k)[e];
+                stage(m, e, v, NORM ? reinterpret_cast<const float4*>(a.norm_w)[e] : v);
+            }
+        }
+        if constexpr (NORM) {
+#pragma unroll
+            for (int m = 0; m < M; m++) {
+                const float ss = wsum(s2[m]);
+                if (lane == 0) ssq[wave][m] = ss;
+            }
+        }
+    }
+    if constexpr (EPI == EPI_RES) {
+        if (tid < M * RW && row0 + (tid & (RW - 1)) < n)
+            pre_res = a.res[(tid >> rw_shift) * n + row0 + (tid & (RW - 1))];
+    } else if constexpr (EPI == EPI_ROPE_KV) {
+        const uint32_t r0 = row0 + 2 * tid + (uint32_t)a.row_off;
+        if (tid < RW / 2 && row0 + 2 * tid < n && r0 < (uint32_t)(a.q_rows + a.kv_rows)) {
+            const uint32_t i = (r0 < (uint32_t)a.q_rows ? r0 : r0 - a.q_rows) % (uint32_t)a.hd;
+            pre_c = a.cos_t[pre_pos * a.hd + i];
+            pre_s = a.sin_t[pre_pos * a.hd + i];
+        }
+    } else if constexpr (EPI == EPI_ARGMAX) {
+        if (a.seen && tid < RW && row0 + tid < n) pre_seen = a.seen[row0 + tid];
+    }
+    __syncthreads();
+    compute();
+    // (2) further passes: rows of more than BT * TC blocks
+    for (uint32_t base = (uint32_t)(BT * TC); base < nb; base += (uint32_t)(BT * TC)) {
+        set_cols(base);
+        load_w();
+        compute();
     }
 
     // (4) thread partials -> row sums: transpose-reduce per wavefront, then across wavefronts
