@@ -574,6 +574,13 @@ __global__ __launch_bounds__(256) void k_mv(MvArgs a, MvShape sh) {
 // recorded, penalty mask updated, position advanced.
 __global__ __launch_bounds__(256) void k_argmax_finish(MvArgs a, int nwg) {
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    // the step counter and the position are read with the candidates, one memory round trip
+    // (read after the stores below they would each cost another)
+    int step0 = 0, pos0 = 0;
+    if (tid == 0) {
+        if (a.out_ids) step0 = *a.step;
+        if (a.pos_inc) pos0 = *a.pos_inc;
+    }
     float bv = -INFINITY;
     int bi = -1, nan = 0;
     for (int i = tid; i < nwg; i += 256) {
@@ -618,12 +625,11 @@ __global__ __launch_bounds__(256) void k_argmax_finish(MvArgs a, int nwg) {
         }
         *a.tok_out = bi;
         if (a.out_ids) {
-            const int s = *a.step;
-            if (s < a.max_out) a.out_ids[s] = bi;
-            *a.step = s + 1;
+            if (step0 < a.max_out) a.out_ids[step0] = bi;
+            *a.step = step0 + 1;
         }
         if (a.seen_out) a.seen_out[bi] = 1;
-        if (a.pos_inc) *a.pos_inc += 1;
+        if (a.pos_inc) *a.pos_inc = pos0 + 1;
     }
 }
 
