@@ -16,6 +16,7 @@ for one decoder layer + the LM head at the same shapes, extrapolated to 22 layer
 Prints one JSON line on stdout; progress goes to stderr.
 """
 import argparse
+import itertools
 import json
 import os
 import sys
@@ -45,10 +46,10 @@ def matvec_bytes(t, n=MATVEC_N, k=MATVEC_K):
     return n * k // per[0] * per[1] + k * 4 + n * 4
 
 
-def bench_matvec(dev, t=2, launches=340, min_bytes=320 << 20):
-    """Average seconds of one 4096 x 4096 matvec (m = 1) of GGML type t, launched back to back
-    over enough resident weight copies (>= 320 MB) that the 256 MB Infinity Cache cannot
-    serve them."""
+def bench_matvec(dev, t=2, launches=340, min_bytes=320 << 20, n=MATVEC_N, k=MATVEC_K):
+    """Average seconds of one n x k matvec (m = 1, default 4096 x 4096) of GGML type t,
+    launched back to back over enough resident weight copies (>= 320 MB) that the 256 MB
+    Infinity Cache cannot serve them."""
     import ctypes as C
 
     from tl_amd import QTensor
@@ -57,12 +58,12 @@ def bench_matvec(dev, t=2, launches=340, min_bytes=320 << 20):
     gen = {2: random_q4_0_blocks, 8: random_q8_0_blocks, 12: random_q4_k_blocks, 14: random_q6_k_blocks}[t]
     lib = dev.lib
     rng = np.random.default_rng(0x71510000)
-    raw = gen(rng, MATVEC_N, MATVEC_K)
+    raw = gen(rng, n, k)
     copies = -(-min_bytes // raw.nbytes)
-    ws = [QTensor(t, raw, (MATVEC_N, MATVEC_K)) for _ in range(copies)]
+    ws = [QTensor(t, raw, (n, k)) for _ in range(copies)]
     hs = [w.upload(lib) for w in ws]
-    x = dev.tensor_new(rng.standard_normal((1, MATVEC_K)).astype(np.float32))
-    y = dev.tensor_zeros((1, MATVEC_N))
+    x = dev.tensor_new(rng.standard_normal((1, k)).astype(np.float32))
+    y = dev.tensor_zeros((1, n))
     stream = lib.tl_hip_stream()
     for i in range(2 * copies):  # warm-up
         if lib.tl_hip_launch_quant_matvec(hs[i % copies], C.c_void_p(x.data_ptr), C.c_void_p(y.data_ptr), 1, stream):
@@ -98,6 +99,19 @@ def bench_quant_matvec(dev):
     return rows
 
 
+def bench_matvec_shapes(dev):
+    """configs[2] at M = 1: the Q4_0 and Q8_0 matvec at the three (N, K) shapes (GB/s)."""
+    rows = []
+    for t, name in ((2, "Q4_0"), (8, "Q8_0")):
+        for n, k in GEMM_SHAPES:
+            sec = bench_matvec(dev, t, launches=200, n=n, k=k)
+            gbs = matvec_bytes(t, n, k) / sec / 1e9
+            rows.append({"type": name, "n": n, "k": k, "bytes": matvec_bytes(t, n, k), "us": round(sec * 1e6, 3),
+                         "gbs": round(gbs, 1), "frac": round(gbs / HBM_PEAK_GBS, 4)})
+            log(f"[bench] matvec {name} M=1 N={n} K={k}: {sec * 1e6:.2f} us, {gbs:.0f} GB/s")
+    return rows
+
+
 MFMA_F16_PEAK_TFLOPS = 2500.0
 GEMM_SHAPES = [(4096, 4096), (11008, 4096), (4096, 11008)]  # configs[2] (N, K), M = 512
 ATTN_CASES = [(512, 1), (2048, 1), (8192, 1), (512, 8), (2048, 8), (8192, 8)]  # configs[3] (L, B)
@@ -124,9 +138,10 @@ def _timed(dev, launch, reps):
     return ms.value / 1e3 / reps
 
 
-def bench_gemm(dev, m=512, reps=20):
+def bench_gemm(dev, ms=(512, 128, 16), reps=20):
     """Quantized prefill GEMM on the f16 MFMA path (tl_hip_launch_quant_gemm, mode 1: the
-    f32 -> f16 operand conversion + the MFMA kernel) at the configs[2] shapes."""
+    f32 -> f16 operand conversion + the MFMA kernel) at the configs[2] shapes and M values
+    (M = 1 is the matvec leg).  GB/s counts the quant weights + X + Y once."""
     import ctypes as C
 
     from tl_amd import GGML_Q4_0, GGML_Q8_0, QTensor
@@ -134,24 +149,31 @@ def bench_gemm(dev, m=512, reps=20):
 
     lib = dev.lib
     rows = []
-    for t, gen, name in ((GGML_Q4_0, random_q4_0_blocks, "Q4_0"), (GGML_Q8_0, random_q8_0_blocks, "Q8_0")):
-        for n, k in GEMM_SHAPES:
-            rng = np.random.default_rng(0x71520000 + n + k)
-            q = QTensor(t, gen(rng, n, k), (n, k))
-            h = q.upload(lib)
-            x = dev.tensor_new(rng.standard_normal((m, k)).astype(np.float32))
-            y = dev.tensor_zeros((m, n))
-            stream = lib.tl_hip_stream()
+    types = ((GGML_Q4_0, random_q4_0_blocks, "Q4_0"), (GGML_Q8_0, random_q8_0_blocks, "Q8_0"))
+    for m, (t, gen, name), (n, k) in itertools.product(ms, types, GEMM_SHAPES):
+        rng = np.random.default_rng(0x71520000 + n + k)
+        raw = gen(rng, n, k)
+        # below M = 512 the weight stream bounds the call: rotate copies past the Infinity Cache
+        copies = 1 if m >= 512 else -(-(320 << 20) // raw.nbytes)
+        qs = [QTensor(t, raw, (n, k)) for _ in range(copies)]
+        hs = [q.upload(lib) for q in qs]
+        x = dev.tensor_new(rng.standard_normal((m, k)).astype(np.float32))
+        y = dev.tensor_zeros((m, n))
+        stream = lib.tl_hip_stream()
 
-            def launch(i):
-                if lib.tl_hip_launch_quant_gemm(h, C.c_void_p(x.data_ptr), C.c_void_p(y.data_ptr), m, 1, stream):
-                    raise RuntimeError(lib.tl_hip_last_error())
-            sec = _timed(dev, launch, reps)
-            tflops = 2.0 * m * n * k / sec / 1e12
-            rows.append({"type": name, "m": m, "n": n, "k": k, "us": round(sec * 1e6, 2),
-                         "tflops": round(tflops, 1), "frac": round(tflops / MFMA_F16_PEAK_TFLOPS, 4)})
-            log(f"[bench] prefill GEMM {name} M={m} N={n} K={k}: {sec * 1e6:.1f} us, {tflops:.0f} TFLOP/s "
-                f"({100 * tflops / MFMA_F16_PEAK_TFLOPS:.1f}% of dense f16 MFMA peak)")
+        def launch(i):
+            if lib.tl_hip_launch_quant_gemm(hs[i % copies], C.c_void_p(x.data_ptr), C.c_void_p(y.data_ptr), m, 1,
+                                            stream):
+                raise RuntimeError(lib.tl_hip_last_error())
+        sec = _timed(dev, launch, max(reps, 2 * copies))
+        tflops = 2.0 * m * n * k / sec / 1e12
+        gbs = (matvec_bytes(t, n, k) - 4 * (n + k) + 4 * m * (n + k)) / sec / 1e9
+        rows.append({"type": name, "m": m, "n": n, "k": k, "us": round(sec * 1e6, 2),
+                     "tflops": round(tflops, 1), "frac": round(tflops / MFMA_F16_PEAK_TFLOPS, 4),
+                     "gbs": round(gbs, 1)})
+        log(f"[bench] prefill GEMM {name} M={m} N={n} K={k}: {sec * 1e6:.1f} us, {tflops:.0f} TFLOP/s "
+            f"({100 * tflops / MFMA_F16_PEAK_TFLOPS:.1f}% of dense f16 MFMA peak), {gbs:.0f} GB/s")
+        for q in qs:
             q.release()
     return rows
 
@@ -325,9 +347,10 @@ def main():
                           "copy_bytes": nbytes}), flush=True)
         return
 
-    gemm = attn = qmv = None
+    gemm = attn = qmv = qmv2 = None
     if not args.no_extra:
         qmv = bench_quant_matvec(dev)
+        qmv2 = bench_matvec_shapes(dev)
         gemm = bench_gemm(dev)
         attn = bench_attention(dev)
 
@@ -388,7 +411,8 @@ def main():
                          "peak": MFMA_F16_PEAK_TFLOPS, "shapes": gemm},
         "decode_attention": {"kv": "f16", "hq": 32, "hkv": 8, "head_dim": 128, "unit": "GB/s",
                              "peak": HBM_PEAK_GBS, "cases": attn},
-        "quant_matvec": {"shape": "4096x4096, m=1", "unit": "GB/s", "peak": HBM_PEAK_GBS, "types": qmv},
+        "quant_matvec": {"shape": "4096x4096, m=1", "unit": "GB/s", "peak": HBM_PEAK_GBS, "types": qmv,
+                         "configs2_m1": qmv2},
         "q4_k_m_decode": kq,
     }
     print(json.dumps(out), flush=True)

@@ -91,6 +91,21 @@ def test_quant_gemm_f32_and_f16(dev, t, m, nk):
 
 
 @pytest.mark.parametrize("t", [GGML_Q4_0, GGML_Q8_0])
+@pytest.mark.parametrize("m", [33, 64, 65])
+@pytest.mark.parametrize("nk", [(1000, 2176), (4096, 1152)])
+def test_quant_gemm_f16_split_k(dev, t, m, nk):
+    """Short inputs on the f16 GEMM: 64-row tiles (33, 64 rows) or 128-row tiles (65), the K
+    range split over workgroup rows (17 and 9 iterations of 128: uneven splits) with the
+    partial tiles added in order by a second kernel; within the f16 tolerance of the oracle."""
+    n, k = nk
+    rng = np.random.default_rng(0x71540000 + m + n + t)
+    raw = blocks(t, rng, n, k)
+    x = rng.standard_normal((m, k)).astype(np.float32)
+    ref = oracle.qtensor_matmul(x, raw, t, n)
+    assert_rel(dev.tl_qtensor_matmul_f16(dev.tensor_new(x), QTensor(t, raw, (n, k))).to_numpy(), ref, F16_TOL)
+
+
+@pytest.mark.parametrize("t", [GGML_Q4_0, GGML_Q8_0])
 @pytest.mark.parametrize("m,n", [(512, 8192), (512, 8160), (300, 8192)])
 def test_quant_gemm_f16_tile_widths(dev, t, m, n):
     """The f16 MFMA GEMM's two tile widths: 128 x 64 tiles when they give >= 512 workgroups

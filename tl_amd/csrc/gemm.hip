@@ -9,6 +9,7 @@
 //                  for [batch, m, k] x [batch?, k, n].
 #include "internal.h"
 
+#include <algorithm>
 #include <mutex>
 #include <type_traits>
 
@@ -451,20 +452,26 @@ __global__ __launch_bounds__(512) void k_qgemm_mfma(const uint8_t* __restrict__ 
     // S0 holds the even iterations, S1 the odd ones; the loads of iteration it + 1 are in
     // flight while it computes.  The wait + barrier at the top of an iteration make every
     // wavefront's chunks visible and free the stage the previous iteration read.
+    // Split K (gridDim.y > 1): workgroup row blockIdx.y takes iterations [it0, it1) and stores
+    // its partial tile in slice blockIdx.y of y (m x n floats each); the launch makes every
+    // range non-empty.
     const int64_t iters = nb / Q_KR;  // >= 1: K is a multiple of 128
+    const int64_t per = (iters + gridDim.y - 1) / gridDim.y;
+    const int64_t it0 = (int64_t)blockIdx.y * per, it1 = it0 + per < iters ? it0 + per : iters;
     auto step = [&](int64_t it, const Stage& cur, Stage& next) {
         __builtin_amdgcn_s_waitcnt(0xF70);  // vmcnt(0): this iteration's DMA has landed
         __syncthreads();
         __builtin_amdgcn_sched_barrier(0);
-        if (it + 1 < iters) issue((it + 1) * Q_KR, next);
+        if (it + 1 < it1) issue((it + 1) * Q_KR, next);
         __builtin_amdgcn_sched_barrier(0);
         compute(cur);
     };
-    issue(0, S0);
-    for (int64_t it = 0; it < iters; it += 2) {
+    issue(it0 * Q_KR, S0);
+    for (int64_t it = it0; it < it1; it += 2) {
         step(it, S0, S1);
-        if (it + 1 < iters) step(it + 1, S1, S0);
+        if (it + 1 < it1) step(it + 1, S1, S0);
     }
+    float* const yb = y + (int64_t)blockIdx.y * m * n;
     // the k half kh = 1 hands its sums to kh = 0 through the (now free) X tile of S0
     static_assert(4 * TM * TN * 256 * 4 <= BM * 128 * 2, "reduction space");
     __syncthreads();
@@ -497,7 +504,7 @@ __global__ __launch_bounds__(512) void k_qgemm_mfma(const uint8_t* __restrict__ 
                             ep.out16[f16q_index(r, c >> 1, n >> 1, ep.order)] = (_Float16)a;
                         }
                     } else if (r < m && c < n) {
-                        y[r * n + c] = ep.mode == GEMM_RES ? ep.res[r * n + c] + v : v;
+                        yb[r * n + c] = ep.mode == GEMM_RES ? ep.res[r * n + c] + v : v;
                     }
                 }
             }
@@ -538,6 +545,31 @@ int launch_x_to_f16q(const float* x, _Float16* x16, int64_t m, int64_t k, int or
     return e == hipSuccess ? TL_HIP_OK : hip_fail(e, "x -> f16 launch");
 }
 
+// Split-K sum: y = [res +] the nsp partial slices, added in slice order (the result does not
+// depend on scheduling).  y may alias res.
+__global__ __launch_bounds__(256) void k_splitk_sum(const float* __restrict__ part, float* y, const float* res,
+                                                    int64_t mn, int nsp) {
+    const int64_t i = ((int64_t)blockIdx.x * 256 + threadIdx.x) * 4;
+    if (i >= mn) return;
+    if (i + 4 <= mn) {
+        float4 v = res ? *reinterpret_cast<const float4*>(res + i) : float4{0.f, 0.f, 0.f, 0.f};
+        for (int p = 0; p < nsp; p++) {
+            const float4 t = *reinterpret_cast<const float4*>(part + p * mn + i);
+            v.x += t.x;
+            v.y += t.y;
+            v.z += t.z;
+            v.w += t.w;
+        }
+        *reinterpret_cast<float4*>(y + i) = v;
+    } else {
+        for (int64_t j = i; j < mn; j++) {
+            float v = res ? res[j] : 0.f;
+            for (int p = 0; p < nsp; p++) v += part[p * mn + j];
+            y[j] = v;
+        }
+    }
+}
+
 int launch_gemm_f16q(const QWeight* w, const _Float16* x16, float* y, int64_t m, const GemmEpi& ep,
                      hipStream_t s) {
     if (m < 1) return TL_HIP_OK;
@@ -555,11 +587,41 @@ int launch_gemm_f16q(const QWeight* w, const _Float16* x16, float* y, int64_t m,
     const bool f16w = (w->ggml_type == TL_HIP_GGML_Q4_K && !w->us) || w->ggml_type == TL_HIP_GGML_Q6_K;
     const int64_t wide_tiles = cdiv(m, BM) * cdiv(w->n, 64);
     const bool wide = f16w ? wide_tiles > 128 : wide_tiles >= 512;
-    const int64_t tiles = cdiv(m, BM) * cdiv(w->n, wide ? 64 : 32);
+    // Short inputs: 32- or 64-row tiles when M fits them, and with fewer tiles than CUs (than
+    // 512 for M <= 32, where the K loop's latency dominates) the K range split over up to 16
+    // workgroup rows until about 512 workgroups run; partial tiles go to a workspace that
+    // k_splitk_sum adds up (with the residual).  The SwiGLU epilogue is not linear and keeps
+    // one workgroup per tile.  (Measured at M = 16 / 128: 4096 x 4096
+    // 27.1 -> 13.1 / 28.9 -> 21.7 us, 4096 x 11008 63.5 -> 22.0 / 70.6 -> 36.7 us per call
+    // including the X conversion; splitting the 344 tiles of 11008 x 4096 in two at M = 128
+    // was slower, 37.0 -> 44.7 us, and faster at M = 16, 23.6 -> 20.5 us.)
+    const int bm = wide ? BM : m <= 32 ? 32 : m <= 64 ? 64 : BM;
+    const int64_t tiles = cdiv(m, bm) * cdiv(w->n, wide ? 64 : 32);
+    const int64_t iters = w->nb / Q_KR;
+    int64_t nsp = 1;
+    if (!wide && ep.mode != GEMM_GLU16 && tiles < (m <= 32 ? 512 : 256)) {
+        nsp = std::min<int64_t>(std::min<int64_t>(cdiv(512, tiles), iters), 16);
+        nsp = cdiv(iters, cdiv(iters, nsp));  // every split non-empty
+    }
+    float* part = nullptr;
+    if (nsp > 1) {
+        part = static_cast<float*>(dev_alloc((size_t)nsp * m * w->n * sizeof(float)));
+        if (!part) return TL_HIP_ERR_ALLOC;
+    }
+    const GemmEpi pe = nsp > 1 ? GemmEpi{GEMM_PLAIN, nullptr, nullptr, 0} : ep;
+    float* const out = nsp > 1 ? part : y;
+    const dim3 grid((unsigned)tiles, (unsigned)nsp);
     auto gemm = [&](auto qt, const uint8_t* q, const __half* d) {
         constexpr int QT = decltype(qt)::value;
-        if (wide) k_qgemm_mfma<QT, BM, 64><<<(unsigned)tiles, 512, 0, s>>>(q, d, x16, y, m, w->n, w->k, w->nb, ep);
-        else k_qgemm_mfma<QT, BM, 32><<<(unsigned)tiles, 512, 0, s>>>(q, d, x16, y, m, w->n, w->k, w->nb, ep);
+        if (wide) k_qgemm_mfma<QT, BM, 64><<<grid, 512, 0, s>>>(q, d, x16, out, m, w->n, w->k, w->nb, pe);
+        else if (bm == 32) k_qgemm_mfma<QT, 32, 32><<<grid, 512, 0, s>>>(q, d, x16, out, m, w->n, w->k, w->nb, pe);
+        else if (bm == 64) k_qgemm_mfma<QT, 64, 32><<<grid, 512, 0, s>>>(q, d, x16, out, m, w->n, w->k, w->nb, pe);
+        else k_qgemm_mfma<QT, BM, 32><<<grid, 512, 0, s>>>(q, d, x16, out, m, w->n, w->k, w->nb, pe);
+        if (nsp > 1) {
+            const int64_t mn = m * w->n;
+            k_splitk_sum<<<(unsigned)cdiv(cdiv(mn, 4), 256), 256, 0, s>>>(
+                part, y, ep.mode == GEMM_RES ? ep.res : nullptr, mn, (int)nsp);
+        }
     };
     if (w->ggml_type == TL_HIP_GGML_Q4_K && w->us) {
         gemm(std::integral_constant<int, TL_HIP_GGML_Q4_K>{}, w->qs, reinterpret_cast<const __half*>(w->us));
@@ -581,6 +643,7 @@ int launch_gemm_f16q(const QWeight* w, const _Float16* x16, float* y, int64_t m,
     } else {
         gemm(std::integral_constant<int, TL_HIP_GGML_Q8_0>{}, w->qs, w->d);
     }
+    if (part) dev_free(part);  // stream-ordered: reused only by later work on the same stream
     hipError_t e = hipGetLastError();
     return e == hipSuccess ? TL_HIP_OK : hip_fail(e, "quant gemm launch");
 }

@@ -423,7 +423,7 @@ static int enqueue_forward(Llama* m, int n, int f16, hipStream_t s) {
 
 // One greedy decode step from the token in m->tok (device), five kernels per layer:
 //   [embed (layer 0) +] RMSNorm + q|k|v matvec + RoPE + KV append   (EPI_ROPE_KV)
-//   attention over the cache (split-L, in-kernel merge)
+//   attention over the cache (one workgroup per query head; the split form beyond 4096)
 //   o-proj matvec + residual                                         (EPI_RES)
 //   RMSNorm + gate/up matvec + SwiGLU                                (EPI_GLU)
 //   down matvec + residual                                           (EPI_RES)
