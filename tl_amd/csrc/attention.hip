@@ -560,6 +560,15 @@ __global__ __launch_bounds__(64 * W) void k_attn_qh(AttnArgs a, int G) {
     if (L64 > a.lmax) L64 = a.lmax;
     const uint32_t L = (uint32_t)L64;  // lmax * D < 2^31 (attention_qh_supported): 32-bit offsets
     const int hq = a.hkv * G;
+    // gridDim.z > 1: this workgroup covers positions [p0, p1), a share of whole rounds (the
+    // first share is never empty), and leaves an unnormalised partial record
+    const uint32_t ns = gridDim.z;
+    uint32_t p0 = 0, p1 = L;
+    if (ns > 1) {
+        const uint32_t per = ((L + ns - 1) / ns + C - 1) / C * C;
+        p0 = blockIdx.z * per < L ? blockIdx.z * per : L;
+        p1 = p0 + per < L ? p0 + per : L;
+    }
     const KVT* kb = reinterpret_cast<const KVT*>(a.k) + (int64_t)b * a.kv_bstride + (int64_t)h * a.lmax * D;
     const KVT* vb = reinterpret_cast<const KVT*>(a.v) + (int64_t)b * a.kv_bstride + (int64_t)h * a.lmax * D;
     const float* qp = a.q + ((int64_t)b * hq + qh) * D;
@@ -578,18 +587,18 @@ __global__ __launch_bounds__(64 * W) void k_attn_qh(AttnArgs a, int G) {
 #pragma unroll
     for (int i = 0; i < DL; i++) o[i] = 0.f;
 
-    for (uint32_t base = (uint32_t)wave * C; base < L; base += (uint32_t)W * C) {
+    for (uint32_t base = p0 + (uint32_t)wave * C; base < p1; base += (uint32_t)W * C) {
         uint4 kraw[NI], vraw[8][VC];
 #pragma unroll
         for (int c = 0; c < NI; c++) {
             uint32_t p = base + c * PPI + kr;
-            p = p < L ? p : L - 1;
+            p = p < p1 ? p : p1 - 1;
             kraw[c] = *reinterpret_cast<const uint4*>(kb + p * D + kl * EPC);
         }
 #pragma unroll
         for (int j = 0; j < 8; j++) {
             uint32_t p = base + slot + 8 * j;
-            p = p < L ? p : L - 1;
+            p = p < p1 ? p : p1 - 1;
 #pragma unroll
             for (int c = 0; c < VC; c++) vraw[j][c] = reinterpret_cast<const uint4*>(vb + p * D + dg * DL)[c];
         }
@@ -608,7 +617,7 @@ __global__ __launch_bounds__(64 * W) void k_attn_qh(AttnArgs a, int G) {
         float sk = s[0];
 #pragma unroll
         for (int c = 1; c < NI; c++) sk = kl == c ? s[c] : sk;
-        const bool in = base + kl * PPI + kr < L;
+        const bool in = base + kl * PPI + kr < p1;
         const float mn = fmaxf(m, wave_max64(in ? sk : -INFINITY));  // position base is valid: finite
         const float pk = in ? __builtin_amdgcn_exp2f(sk - mn) : 0.f;
         const float alpha = __builtin_amdgcn_exp2f(m - mn);  // 0 on the first round (m = -inf)
@@ -644,20 +653,24 @@ __global__ __launch_bounds__(64 * W) void k_attn_qh(AttnArgs a, int G) {
         wl[wave] = l;
     }
     __syncthreads();
+    // record of a split: [o (D floats, relative to M) | M | l | 0 | 0], D + 4 floats
+    float* rec = ns > 1 ? a.ws + (((int64_t)b * hq + qh) * ns + blockIdx.z) * (D + 4) : nullptr;
     if (wave == 0) {  // per-wavefront weights exp2(m_w - M) / sum_w l_w exp2(m_w - M)
         const bool act = lane < W && wl[lane < W ? lane : 0] > 0.f;  // idle wavefronts add nothing
         const float mw = act ? wm[lane] : -INFINITY;
-        const float M = wave_max64(mw);
+        const float M = wave_max64(mw);  // -inf for an empty share: every weight 0, l = 0
         const float f = act ? __builtin_amdgcn_exp2f(mw - M) : 0.f;
         const float den = wave_sum64(act ? f * wl[lane] : 0.f);
-        if (lane < W) wf[lane] = f / den;
+        if (lane < W) wf[lane] = rec ? f : f / den;
+        if (rec && lane == 0) *reinterpret_cast<float4*>(rec + D) = float4{M, den, 0.f, 0.f};
     }
     __syncthreads();
     for (int d = tid; d < D; d += 64 * W) {
         float num = 0.f;
 #pragma unroll
         for (int w = 0; w < W; w++) num = fmaf(wo[w][d], wf[w], num);
-        a.out[((int64_t)b * hq + qh) * D + d] = num;
+        if (rec) rec[d] = num;
+        else a.out[((int64_t)b * hq + qh) * D + d] = num;
     }
 }
 
@@ -896,11 +909,16 @@ bool attention_qh_supported(int kv_dtype, int D, int64_t lmax) {
 // Short-cache form; returns TL_HIP_ERR_ARG (no launch) for shapes it does not cover.
 int launch_attention_qh(const float* q, const void* k, const void* v, int kv_dtype, float* out,
                         int B, int hq, int hkv, int D, int64_t lmax, int64_t kv_bstride, int64_t L,
-                        const int32_t* len_dev, int len_add, int len_step, float scale, hipStream_t s) {
-    AttnArgs a{q, k, v, out, nullptr, hkv, lmax, kv_bstride, AttnLen{L, len_dev, len_add, len_step}, 64, 1,
+                        const int32_t* len_dev, int len_add, int len_step, float scale, hipStream_t s,
+                        float* part, int nsplit) {
+    if (nsplit < 1 || nsplit > 8 || (nsplit > 1 && !part)) {
+        set_error(TL_HIP_ERR_ARG, "ArgumentError: %d position shares per head (1..8, >1 with a record buffer)", nsplit);
+        return TL_HIP_ERR_ARG;
+    }
+    AttnArgs a{q, k, v, out, part, hkv, lmax, kv_bstride, AttnLen{L, len_dev, len_add, len_step}, 64, nsplit,
                scale};
     const int G = hq / hkv;
-    dim3 grid(hq, B);
+    dim3 grid(hq, B, nsplit);
     if (D == 64 && kv_dtype == TL_HIP_F16) k_attn_qh<64, __half, 8><<<grid, 64 * 8, 0, s>>>(a, G);
     else if (D == 128 && kv_dtype == TL_HIP_F16) k_attn_qh<128, __half, 8><<<grid, 64 * 8, 0, s>>>(a, G);
     else if (D == 64 && kv_dtype == TL_HIP_F32) k_attn_qh<64, float, 8><<<grid, 64 * 8, 0, s>>>(a, G);

@@ -458,11 +458,16 @@ static int enqueue_step(Llama* m, float penalty, hipStream_t s) {
             a.row_off = sg.row_off;
             if ((rc = launch_mv(sg.w, a, 1, EPI_ROPE_KV, true, l == 0, s))) return rc;
         }
-        // caches up to 4096 positions: one workgroup per query head in a single launch (the
-        // split form's merge launch costs more than its wider spread saves at these lengths)
-        if (m->max_seq <= 4096 && attention_qh_supported(m->kv_f16 ? TL_HIP_F16 : TL_HIP_F32, (int)hd, m->max_seq))
+        // caches up to 4096 positions: two workgroups per query head (each half the positions)
+        // in a single launch, their records merged by the o-projection as it stages its input
+        // (the split form's merge launch costs more than its wider spread saves here)
+        const bool qh = m->max_seq <= 4096 &&
+                        attention_qh_supported(m->kv_f16 ? TL_HIP_F16 : TL_HIP_F32, (int)hd, m->max_seq);
+        const bool shares = qh && hd % 4 == 0 && m->ws_floats >= (int64_t)m->H * 2 * (hd + 4);
+        if (qh)
             rc = launch_attention_qh(m->q, m->kc[l], m->vc[l], m->kv_f16 ? TL_HIP_F16 : TL_HIP_F32, m->ao, 1, m->H,
-                                     m->KV, (int)hd, m->max_seq, 0, 0, m->pos, 1, 0, 1.0f / sqrtf((float)hd), s);
+                                     m->KV, (int)hd, m->max_seq, 0, 0, m->pos, 1, 0, 1.0f / sqrtf((float)hd), s,
+                                     shares ? m->ws : nullptr, shares ? 2 : 1);
         else if (attention_gq_supported(m->kv_f16 ? TL_HIP_F16 : TL_HIP_F32, m->H, m->KV, (int)hd))
             rc = launch_attention_gq(m->q, m->kc[l], m->vc[l], m->ao, m->ws, 1, m->H, m->KV, (int)hd, m->max_seq, 0,
                                      0, m->pos, 1, 0, attention_gq_splits(m->max_seq), 1.0f / sqrtf((float)hd), s);
@@ -472,7 +477,9 @@ static int enqueue_step(Llama* m, float penalty, hipStream_t s) {
                                   1.0f / sqrtf((float)hd), s);
         if (rc) return rc;
         MvArgs o = {};
-        o.x = m->ao;
+        o.x = shares ? nullptr : m->ao;
+        o.attn_rec = shares ? m->ws : nullptr;
+        o.attn_hd = (int)hd;
         o.y = m->x;
         o.res = m->x;
         if ((rc = launch_mv(m->wo[l], o, 1, EPI_RES, false, false, s))) return rc;

@@ -172,7 +172,17 @@ struct MvShape {
 // Thread (sub, tcol) owns block columns tcol + tc * (i + BT * pass) of rows
 // row0 + sub + S * j, j < RWT.  Rows per workgroup RW = S * RWT.  Offsets are 32-bit
 // (checked at launch: the quant array is below 2 GiB).
-template <int QT, int BT, int RWT, int M, int EPI, bool NORM, bool EMBED>
+// Two attention records of a head merged into x: o = (f0 o0 + f1 o1) / (f0 l0 + f1 l1),
+// f_s = exp2(m_s - max(m0, m1)) (scores in log2 units; an empty share has m = -inf, f = 0).
+__device__ __forceinline__ float4 merge_shares(float4 o0, float4 o1, float4 st) {
+    const float mx = fmaxf(st.x, st.z);
+    const float f0 = __builtin_amdgcn_exp2f(st.x - mx), f1 = __builtin_amdgcn_exp2f(st.z - mx);
+    const float inv = 1.0f / fmaf(f0, st.y, f1 * st.w);
+    return float4{fmaf(f0, o0.x, f1 * o1.x) * inv, fmaf(f0, o0.y, f1 * o1.y) * inv,
+                  fmaf(f0, o0.z, f1 * o1.z) * inv, fmaf(f0, o0.w, f1 * o1.w) * inv};
+}
+
+template <int QT, int BT, int RWT, int M, int EPI, bool NORM, bool EMBED, bool MERGE = false>
 __global__ __launch_bounds__(256) void k_mv(MvArgs a, MvShape sh) {
     constexpr int QB = QB_<QT>::v, QW = QB / 16;  // 16-byte loads per block
     constexpr int N = M * RWT;
@@ -376,15 +386,30 @@ __global__ __launch_bounds__(256) void k_mv(MvArgs a, MvShape sh) {
         const float* xsrc = EMBED ? a.x + (size_t)(*a.embed_id) * k : a.x;
         const uint32_t k4 = k >> 2, nthr = blockDim.x;
         float s2[M];
-        constexpr int XRK = NORM ? (RWT >= 8 ? XR_NORM8 : XR_NORM) : XR;
+        constexpr int XRK = (NORM || MERGE) ? (RWT >= 8 ? XR_NORM8 : XR_NORM) : XR;
         float4 xr[M][XRK], gr[NORM ? XRK : 1];
+        float4 xr1[MERGE ? XRK : 1], st[MERGE ? XRK : 1];  // MERGE: share 1's o, (m0, l0, m1, l1)
+        const uint32_t rhd = (uint32_t)a.attn_hd, rst = 2 * (rhd + 4);  // record pitch per head
+        auto load_rec = [&](uint32_t e, float4& o0, float4& o1, float4& stat) {
+            const uint32_t h = (4 * e) / rhd, d = 4 * e - h * rhd;
+            const float* r = a.attn_rec + (size_t)h * rst;
+            o0 = *reinterpret_cast<const float4*>(r + d);
+            o1 = *reinterpret_cast<const float4*>(r + rhd + 4 + d);
+            const float2 s0 = *reinterpret_cast<const float2*>(r + rhd);
+            const float2 s1 = *reinterpret_cast<const float2*>(r + 2 * rhd + 4);
+            stat = float4{s0.x, s0.y, s1.x, s1.y};
+        };
 #pragma unroll
         for (int m = 0; m < M; m++) {
             s2[m] = 0.f;
 #pragma unroll
             for (int j = 0; j < XRK; j++) {
                 const uint32_t e = tid + j * nthr;
-                if (e < k4) xr[m][j] = reinterpret_cast<const float4*>(xsrc + m * k)[e];
+                if constexpr (MERGE) {
+                    if (e < k4) load_rec(e, xr[0][j], xr1[j], st[j]);
+                } else {
+                    if (e < k4) xr[m][j] = reinterpret_cast<const float4*>(xsrc + m * k)[e];
+                }
             }
         }
         if constexpr (NORM) {
@@ -413,10 +438,21 @@ __global__ __launch_bounds__(256) void k_mv(MvArgs a, MvShape sh) {
 #pragma unroll
             for (int j = 0; j < XRK; j++) {
                 const uint32_t e = tid + j * nthr;
-                if (e < k4) stage(m, e, xr[m][j], NORM ? gr[j] : xr[m][j]);
+                if constexpr (MERGE) {
+                    if (e < k4) stage(m, e, merge_shares(xr[0][j], xr1[j], st[j]), xr[0][j]);
+                } else {
+                    if (e < k4) stage(m, e, xr[m][j], NORM ? gr[j] : xr[m][j]);
+                }
             }
             for (uint32_t e = tid + XRK * nthr; e < k4; e += nthr) {  // long rows only
-                const float4 v = reinterpret_cast<const float4*>(xsrc + m * k)[e];
+                float4 v;
+                if constexpr (MERGE) {
+                    float4 o0, o1, stat;
+                    load_rec(e, o0, o1, stat);
+                    v = merge_shares(o0, o1, stat);
+                } else {
+                    v = reinterpret_cast<const float4*>(xsrc + m * k)[e];
+                }
                 stage(m, e, v, NORM ? reinterpret_cast<const float4*>(a.norm_w)[e] : v);
             }
         }
@@ -667,10 +703,10 @@ static MvPlan mv_plan(int64_t n, int64_t nb, int qt) {
     return p;
 }
 
-template <int QT, int BT, int RWT, int M, int EPI, bool NORM, bool EMBED>
+template <int QT, int BT, int RWT, int M, int EPI, bool NORM, bool EMBED, bool MERGE = false>
 static int run(const MvArgs& a, const MvPlan& p, hipStream_t s) {
     const size_t lds = (size_t)M * a.nb * XPAD * sizeof(float);
-    auto kern = k_mv<QT, BT, RWT, M, EPI, NORM, EMBED>;
+    auto kern = k_mv<QT, BT, RWT, M, EPI, NORM, EMBED, MERGE>;
     if (lds > 64 * 1024) {
         hipError_t e = hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
         if (e != hipSuccess) return hip_fail(e, "hipFuncSetAttribute(LDS)");
@@ -683,17 +719,17 @@ static int run(const MvArgs& a, const MvPlan& p, hipStream_t s) {
 
 // (BT, RWT) combinations the plan can produce: Q4_0 (1, 8|4|2), (2, 8|4|2);
 // Q8_0 (1, 8|4|2), (2, 4|2).
-template <int QT, int M, int EPI, bool NORM, bool EMBED>
+template <int QT, int M, int EPI, bool NORM, bool EMBED, bool MERGE = false>
 static int run_p(const MvArgs& a, const MvPlan& p, hipStream_t s) {
     if (p.BT == 1) {
-        if (p.RWT == 8) return run<QT, 1, 8, M, EPI, NORM, EMBED>(a, p, s);
-        if (p.RWT == 4) return run<QT, 1, 4, M, EPI, NORM, EMBED>(a, p, s);
-        return run<QT, 1, 2, M, EPI, NORM, EMBED>(a, p, s);
+        if (p.RWT == 8) return run<QT, 1, 8, M, EPI, NORM, EMBED, MERGE>(a, p, s);
+        if (p.RWT == 4) return run<QT, 1, 4, M, EPI, NORM, EMBED, MERGE>(a, p, s);
+        return run<QT, 1, 2, M, EPI, NORM, EMBED, MERGE>(a, p, s);
     }
     if constexpr (QT == TL_HIP_GGML_Q4_0)
-        if (p.RWT == 8) return run<QT, 2, 8, M, EPI, NORM, EMBED>(a, p, s);
-    if (p.RWT == 4) return run<QT, 2, 4, M, EPI, NORM, EMBED>(a, p, s);
-    return run<QT, 2, 2, M, EPI, NORM, EMBED>(a, p, s);
+        if (p.RWT == 8) return run<QT, 2, 8, M, EPI, NORM, EMBED, MERGE>(a, p, s);
+    if (p.RWT == 4) return run<QT, 2, 4, M, EPI, NORM, EMBED, MERGE>(a, p, s);
+    return run<QT, 2, 2, M, EPI, NORM, EMBED, MERGE>(a, p, s);
 }
 
 template <int QT>
@@ -703,7 +739,9 @@ static int run_t(const MvArgs& a, int m, int epi, bool norm, bool embed, const M
         return run_p<QT, 2, EPI_PLAIN, false, false>(a, p, s);
     }
     switch (epi) {
-        case EPI_RES: return run_p<QT, 1, EPI_RES, false, false>(a, p, s);
+        case EPI_RES:
+            if (a.attn_rec) return run_p<QT, 1, EPI_RES, false, false, true>(a, p, s);
+            return run_p<QT, 1, EPI_RES, false, false>(a, p, s);
         case EPI_GLU:
             return norm ? run_p<QT, 1, EPI_GLU, true, false>(a, p, s) : run_p<QT, 1, EPI_GLU, false, false>(a, p, s);
         case EPI_ROPE_KV:
@@ -753,6 +791,12 @@ int launch_mv(const QWeight* w, MvArgs a, int m, int epi, bool norm, bool embed,
     if ((epi == EPI_GLU || epi == EPI_ROPE_KV) && (a.n % 2)) {
         set_error(TL_HIP_ERR_SHAPE, "ShapeMismatch: paired epilogue needs an even row count");
         return TL_HIP_ERR_SHAPE;
+    }
+    if (a.attn_rec && (m != 1 || epi != EPI_RES || norm || embed || a.attn_hd < 4 || a.attn_hd % 4 ||
+                       a.k % a.attn_hd || (reinterpret_cast<uintptr_t>(a.attn_rec) & 15))) {
+        set_error(TL_HIP_ERR_ARG, "ArgumentError: attention-record input needs m = 1, the residual epilogue, "
+                  "head size a multiple of 4 dividing k, 16-byte aligned records");
+        return TL_HIP_ERR_ARG;
     }
     switch (w->ggml_type) {
         case TL_HIP_GGML_Q4_0: return run_t<TL_HIP_GGML_Q4_0>(a, m, epi, norm, embed, p, s);
