@@ -113,8 +113,8 @@ struct MvArgs {
     int q_rows, kv_rows, hd, kv_f16;
     int64_t max_seq;
     int64_t row_off;  // rows of this weight start at row_off of the q | k | v projection
-    // x formed from two attention records per head (launch_attention_qh with nsplit 2):
-    // x[h * attn_hd + d] = merge of records (h, 0) and (h, 1); M = 1, EPI_RES, no prologue
+    // x formed from ATTN_SHARES attention records per head (launch_attention_qh with that
+    // nsplit): x[h * attn_hd + d] = merge of records (h, 0 ..); M = 1, EPI_RES, no prologue
     const float* attn_rec;
     int attn_hd;
     // EPI_ARGMAX
@@ -229,10 +229,12 @@ int launch_attention_prefill(const float* q, const void* k, const void* v, float
                              hipStream_t s, _Float16* out16 = nullptr, int order = 0);
 // Short-cache form: one workgroup per (query head, batch item); shapes: attention_qh_supported.
 bool attention_qh_supported(int kv_dtype, int D, int64_t lmax);
+// position shares per query head in the decoder's attention (records merged by the o-projection)
+constexpr int ATTN_SHARES = 4;  // 2 shares: 1810-1820 tok/s, 4: 1840-1843 (records loaded before the weights)
 // nsplit > 1: each head's positions in nsplit shares of whole 64-position rounds, one
 // workgroup each, leaving unnormalised records [o (D) | max | sum | 0 | 0] (D + 4 floats) at
 // part[((b * hq + head) * nsplit + share)] instead of writing out; the decode o-projection
-// merges two shares in its activation staging (MvArgs::attn_rec).
+// merges ATTN_SHARES shares in its activation staging (MvArgs::attn_rec).
 int launch_attention_qh(const float* q, const void* k, const void* v, int kv_dtype, float* out,
                         int B, int hq, int hkv, int D, int64_t lmax, int64_t kv_bstride, int64_t L,
                         const int32_t* len_dev, int len_add, int len_step, float scale, hipStream_t s,

@@ -458,16 +458,16 @@ static int enqueue_step(Llama* m, float penalty, hipStream_t s) {
             a.row_off = sg.row_off;
             if ((rc = launch_mv(sg.w, a, 1, EPI_ROPE_KV, true, l == 0, s))) return rc;
         }
-        // caches up to 4096 positions: two workgroups per query head (each half the positions)
-        // in a single launch, their records merged by the o-projection as it stages its input
-        // (the split form's merge launch costs more than its wider spread saves here)
+        // caches up to 4096 positions: ATTN_SHARES workgroups per query head (each a share of
+        // the positions) in a single launch, their records merged by the o-projection as it
+        // stages its input (the split form's merge launch costs more than it saves here)
         const bool qh = m->max_seq <= 4096 &&
                         attention_qh_supported(m->kv_f16 ? TL_HIP_F16 : TL_HIP_F32, (int)hd, m->max_seq);
-        const bool shares = qh && hd % 4 == 0 && m->ws_floats >= (int64_t)m->H * 2 * (hd + 4);
+        const bool shares = qh && hd % 4 == 0 && m->ws_floats >= (size_t)m->H * ATTN_SHARES * (hd + 4);
         if (qh)
             rc = launch_attention_qh(m->q, m->kc[l], m->vc[l], m->kv_f16 ? TL_HIP_F16 : TL_HIP_F32, m->ao, 1, m->H,
                                      m->KV, (int)hd, m->max_seq, 0, 0, m->pos, 1, 0, 1.0f / sqrtf((float)hd), s,
-                                     shares ? m->ws : nullptr, shares ? 2 : 1);
+                                     shares ? m->ws : nullptr, shares ? ATTN_SHARES : 1);
         else if (attention_gq_supported(m->kv_f16 ? TL_HIP_F16 : TL_HIP_F32, m->H, m->KV, (int)hd))
             rc = launch_attention_gq(m->q, m->kc[l], m->vc[l], m->ao, m->ws, 1, m->H, m->KV, (int)hd, m->max_seq, 0,
                                      0, m->pos, 1, 0, attention_gq_splits(m->max_seq), 1.0f / sqrtf((float)hd), s);

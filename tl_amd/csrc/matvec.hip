@@ -172,14 +172,38 @@ struct MvShape {
 // Thread (sub, tcol) owns block columns tcol + tc * (i + BT * pass) of rows
 // row0 + sub + S * j, j < RWT.  Rows per workgroup RW = S * RWT.  Offsets are 32-bit
 // (checked at launch: the quant array is below 2 GiB).
-// Two attention records of a head merged into x: o = (f0 o0 + f1 o1) / (f0 l0 + f1 l1),
-// f_s = exp2(m_s - max(m0, m1)) (scores in log2 units; an empty share has m = -inf, f = 0).
-__device__ __forceinline__ float4 merge_shares(float4 o0, float4 o1, float4 st) {
-    const float mx = fmaxf(st.x, st.z);
-    const float f0 = __builtin_amdgcn_exp2f(st.x - mx), f1 = __builtin_amdgcn_exp2f(st.z - mx);
-    const float inv = 1.0f / fmaf(f0, st.y, f1 * st.w);
-    return float4{fmaf(f0, o0.x, f1 * o1.x) * inv, fmaf(f0, o0.y, f1 * o1.y) * inv,
-                  fmaf(f0, o0.z, f1 * o1.z) * inv, fmaf(f0, o0.w, f1 * o1.w) * inv};
+// The attention records of a head merged into x: o = sum_s f_s o_s / sum_s f_s l_s,
+// f_s = exp2(m_s - max_s m_s) (scores in log2 units; an empty share has m = -inf, f = 0).
+// Record (h, s) sits at rec + (h * ATTN_SHARES + s) * (hd + 4): [o (hd) | m | l | 0 | 0].
+// Loading and merging are separate steps so the weight loads can be issued in between.
+__device__ __forceinline__ void load_shares(const float* __restrict__ rec, uint32_t e, uint32_t hd,
+                                            float4 (&o)[ATTN_SHARES], float2 (&st)[ATTN_SHARES]) {
+    const uint32_t h = (4 * e) / hd, d = 4 * e - h * hd;
+    const float* r = rec + (size_t)h * ATTN_SHARES * (hd + 4);
+#pragma unroll
+    for (int s = 0; s < ATTN_SHARES; s++) {
+        o[s] = *reinterpret_cast<const float4*>(r + s * (hd + 4) + d);
+        st[s] = *reinterpret_cast<const float2*>(r + s * (hd + 4) + hd);
+    }
+}
+
+__device__ __forceinline__ float4 merge_shares(const float4 (&o)[ATTN_SHARES], const float2 (&st)[ATTN_SHARES]) {
+    float mx = st[0].x;
+#pragma unroll
+    for (int s = 1; s < ATTN_SHARES; s++) mx = fmaxf(mx, st[s].x);
+    float4 num = {0.f, 0.f, 0.f, 0.f};
+    float den = 0.f;
+#pragma unroll
+    for (int s = 0; s < ATTN_SHARES; s++) {
+        const float f = __builtin_amdgcn_exp2f(st[s].x - mx);
+        den = fmaf(f, st[s].y, den);
+        num.x = fmaf(f, o[s].x, num.x);
+        num.y = fmaf(f, o[s].y, num.y);
+        num.z = fmaf(f, o[s].z, num.z);
+        num.w = fmaf(f, o[s].w, num.w);
+    }
+    const float inv = 1.0f / den;
+    return float4{num.x * inv, num.y * inv, num.z * inv, num.w * inv};
 }
 
 template <int QT, int BT, int RWT, int M, int EPI, bool NORM, bool EMBED, bool MERGE = false>
@@ -386,19 +410,12 @@ __global__ __launch_bounds__(256) void k_mv(MvArgs a, MvShape sh) {
         const float* xsrc = EMBED ? a.x + (size_t)(*a.embed_id) * k : a.x;
         const uint32_t k4 = k >> 2, nthr = blockDim.x;
         float s2[M];
-        constexpr int XRK = (NORM || MERGE) ? (RWT >= 8 ? XR_NORM8 : XR_NORM) : XR;
+        constexpr int XRK = MERGE ? 2 : NORM ? (RWT >= 8 ? XR_NORM8 : XR_NORM) : XR;
         float4 xr[M][XRK], gr[NORM ? XRK : 1];
-        float4 xr1[MERGE ? XRK : 1], st[MERGE ? XRK : 1];  // MERGE: share 1's o, (m0, l0, m1, l1)
-        const uint32_t rhd = (uint32_t)a.attn_hd, rst = 2 * (rhd + 4);  // record pitch per head
-        auto load_rec = [&](uint32_t e, float4& o0, float4& o1, float4& stat) {
-            const uint32_t h = (4 * e) / rhd, d = 4 * e - h * rhd;
-            const float* r = a.attn_rec + (size_t)h * rst;
-            o0 = *reinterpret_cast<const float4*>(r + d);
-            o1 = *reinterpret_cast<const float4*>(r + rhd + 4 + d);
-            const float2 s0 = *reinterpret_cast<const float2*>(r + rhd);
-            const float2 s1 = *reinterpret_cast<const float2*>(r + 2 * rhd + 4);
-            stat = float4{s0.x, s0.y, s1.x, s1.y};
-        };
+        // MERGE: the attention records (written by the launch just before) are requested
+        // here and merged at staging, after the weight loads are issued
+        float4 ro[MERGE ? XRK : 1][ATTN_SHARES];
+        float2 rs[MERGE ? XRK : 1][ATTN_SHARES];
 #pragma unroll
         for (int m = 0; m < M; m++) {
             s2[m] = 0.f;
@@ -406,7 +423,7 @@ __global__ __launch_bounds__(256) void k_mv(MvArgs a, MvShape sh) {
             for (int j = 0; j < XRK; j++) {
                 const uint32_t e = tid + j * nthr;
                 if constexpr (MERGE) {
-                    if (e < k4) load_rec(e, xr[0][j], xr1[j], st[j]);
+                    if (e < k4) load_shares(a.attn_rec, e, (uint32_t)a.attn_hd, ro[j], rs[j]);
                 } else {
                     if (e < k4) xr[m][j] = reinterpret_cast<const float4*>(xsrc + m * k)[e];
                 }
@@ -439,7 +456,10 @@ __global__ __launch_bounds__(256) void k_mv(MvArgs a, MvShape sh) {
             for (int j = 0; j < XRK; j++) {
                 const uint32_t e = tid + j * nthr;
                 if constexpr (MERGE) {
-                    if (e < k4) stage(m, e, merge_shares(xr[0][j], xr1[j], st[j]), xr[0][j]);
+                    if (e < k4) {
+                        const float4 v = merge_shares(ro[j], rs[j]);
+                        stage(m, e, v, v);
+                    }
                 } else {
                     if (e < k4) stage(m, e, xr[m][j], NORM ? gr[j] : xr[m][j]);
                 }
@@ -447,9 +467,10 @@ __global__ __launch_bounds__(256) void k_mv(MvArgs a, MvShape sh) {
             for (uint32_t e = tid + XRK * nthr; e < k4; e += nthr) {  // long rows only
                 float4 v;
                 if constexpr (MERGE) {
-                    float4 o0, o1, stat;
-                    load_rec(e, o0, o1, stat);
-                    v = merge_shares(o0, o1, stat);
+                    float4 o[ATTN_SHARES];
+                    float2 st[ATTN_SHARES];
+                    load_shares(a.attn_rec, e, (uint32_t)a.attn_hd, o, st);
+                    v = merge_shares(o, st);
                 } else {
                     v = reinterpret_cast<const float4*>(xsrc + m * k)[e];
                 }
