@@ -919,10 +919,18 @@ int launch_attention_qh(const float* q, const void* k, const void* v, int kv_dty
                scale};
     const int G = hq / hkv;
     dim3 grid(hq, B, nsplit);
-    if (D == 64 && kv_dtype == TL_HIP_F16) k_attn_qh<64, __half, 8><<<grid, 64 * 8, 0, s>>>(a, G);
-    else if (D == 128 && kv_dtype == TL_HIP_F16) k_attn_qh<128, __half, 8><<<grid, 64 * 8, 0, s>>>(a, G);
-    else if (D == 64 && kv_dtype == TL_HIP_F32) k_attn_qh<64, float, 8><<<grid, 64 * 8, 0, s>>>(a, G);
-    else {
+    // a workgroup with a share of the positions has fewer rounds for its wavefronts: 4 of them
+    const bool w4 = nsplit > 1;
+    if (D == 64 && kv_dtype == TL_HIP_F16) {
+        if (w4) k_attn_qh<64, __half, 4><<<grid, 64 * 4, 0, s>>>(a, G);
+        else k_attn_qh<64, __half, 8><<<grid, 64 * 8, 0, s>>>(a, G);
+    } else if (D == 128 && kv_dtype == TL_HIP_F16) {
+        if (w4) k_attn_qh<128, __half, 4><<<grid, 64 * 4, 0, s>>>(a, G);
+        else k_attn_qh<128, __half, 8><<<grid, 64 * 8, 0, s>>>(a, G);
+    } else if (D == 64 && kv_dtype == TL_HIP_F32) {
+        if (w4) k_attn_qh<64, float, 4><<<grid, 64 * 4, 0, s>>>(a, G);
+        else k_attn_qh<64, float, 8><<<grid, 64 * 8, 0, s>>>(a, G);
+    } else {
         set_error(TL_HIP_ERR_ARG, "ArgumentError: short-cache attention covers head_dim 64 / 128 (f16 cache) and 64 (f32)");
         return TL_HIP_ERR_ARG;
     }
