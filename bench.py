@@ -179,6 +179,49 @@ def bench_gemm(dev, ms=(512, 128, 16), reps=20):
     return rows
 
 
+def bench_row_ops(dev, reps=60, min_bytes=320 << 20):
+    """configs[1] row ops on f32 activations, each input uploaded in enough copies (>= 320 MB)
+    that the Infinity Cache cannot serve it: GB/s of the algorithmic bytes (every input read
+    once, the output written once)."""
+    rng = np.random.default_rng(0x71510001)
+    x = rng.standard_normal((512, 4096)).astype(np.float32)
+    w = rng.uniform(0.5, 1.5, 4096).astype(np.float32)
+    xr = rng.standard_normal((512, 32, 128)).astype(np.float32)
+    g = rng.standard_normal((512, 11008)).astype(np.float32)
+    u = rng.standard_normal((512, 11008)).astype(np.float32)
+    lg = (3.0 * rng.standard_normal((512, 32000))).astype(np.float32)
+    wt = dev.tensor_new(w)
+    cos, sin = dev.tensor_rope_new_cos(128, 512, 10000.0), dev.tensor_rope_new_sin(128, 512, 10000.0)
+    cases = [
+        ("rms_norm", "[512, 4096] * w[4096], eps 1e-5", 16_793_600, (x,),
+         lambda t: dev.tensor_rms_norm(t[0], wt, 1e-5)),
+        ("apply_rope (per-token positions)", "[512, 32, 128], tables [512, 128]", 16_777_216 + 524_288, (xr,),
+         lambda t: dev.tensor_apply_rope_pos(t[0], cos, sin, 0, 32)),
+        ("fused_silu_mul", "gate, up [512, 11008]", 67_633_152, (g, u),
+         lambda t: dev.fused_silu_mul(t[0], t[1])),
+        ("softmax (last axis)", "[512, 32000]", 131_072_000, (lg,),
+         lambda t: dev.tensor_softmax(t[0], -1)),
+    ]
+    rows = []
+    for name, shape, nbytes, arrays, call in cases:
+        copies = -(-min_bytes // sum(a.nbytes for a in arrays))
+        ins = [tuple(dev.tensor_new(a) for a in arrays) for _ in range(copies)]
+
+        def launch(i):
+            call(ins[i % copies]).release()
+        sec = _timed(dev, launch, max(reps, copies))
+        gbs = nbytes / sec / 1e9
+        rows.append({"op": name, "shape": shape, "bytes": nbytes, "us": round(sec * 1e6, 2), "gbs": round(gbs, 1),
+                     "frac": round(gbs / HBM_PEAK_GBS, 4)})
+        log(f"[bench] {name} {shape}: {sec * 1e6:.1f} us, {gbs:.0f} GB/s ({100 * gbs / HBM_PEAK_GBS:.1f}% of HBM peak)")
+        for t in ins:
+            for h in t:
+                h.release()
+    for t in (wt, cos, sin):
+        t.release()
+    return rows
+
+
 def bench_attention(dev, reps=20, hq=32, hkv=8, d=128, min_bytes=300 << 20):
     """Decode attention over an f16 KV cache at the configs[3] cases, rotating KV copies so
     that at least 300 MB are touched (the 256 MB Infinity Cache cannot hold them)."""
@@ -348,10 +391,11 @@ def main():
                           "copy_bytes": nbytes}), flush=True)
         return
 
-    gemm = attn = qmv = qmv2 = None
+    gemm = attn = qmv = qmv2 = rowops = None
     if not args.no_extra:
         qmv = bench_quant_matvec(dev)
         qmv2 = bench_matvec_shapes(dev)
+        rowops = bench_row_ops(dev)
         gemm = bench_gemm(dev)
         attn = bench_attention(dev)
 
@@ -414,6 +458,7 @@ def main():
                              "peak": HBM_PEAK_GBS, "cases": attn},
         "quant_matvec": {"shape": "4096x4096, m=1", "unit": "GB/s", "peak": HBM_PEAK_GBS, "types": qmv,
                          "configs2_m1": qmv2},
+        "row_ops": {"config": "configs[1]", "unit": "GB/s", "peak": HBM_PEAK_GBS, "ops": rowops},
         "q4_k_m_decode": kq,
     }
     print(json.dumps(out), flush=True)
