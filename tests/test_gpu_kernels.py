@@ -219,6 +219,12 @@ def test_softmax(dev):
     np.testing.assert_allclose(got.sum(-1), 1.0, rtol=1e-4)
     y = (rng.standard_normal((4, 33, 6)) * 3).astype(np.float32)  # middle axis, odd size
     assert_rel(dev.tensor_softmax(dev.tensor_new(y), 1).to_numpy(), oracle.softmax(y, 1), F32_TOL)
+    # causal-mask rows (the chatbot adds -inf above the diagonal): masked entries exactly 0
+    z = (rng.standard_normal((64, 4096)) * 3).astype(np.float32)
+    z[np.triu_indices(64, 1, 4096)] = -np.inf
+    gz = dev.tensor_softmax(dev.tensor_new(z), -1).to_numpy()
+    assert_rel(gz, oracle.softmax(z, -1), F32_TOL)
+    assert np.all(gz[np.triu_indices(64, 1, 4096)] == 0.0)
 
 
 # ------------------------------------------------------------------ decode attention (config 3)

@@ -364,29 +364,35 @@ __global__ __launch_bounds__(512) void k_softmax_row(const float* __restrict__ x
         mx = fmaxf(mx, fmaxf(fmaxf(v[i].x, v[i].y), fmaxf(v[i].z, v[i].w)));
     }
     mx = block_max(mx, red);
+    // exp(x - max) as the hardware exp2 of (x - max) log2 e and one reciprocal per row: about
+    // 2e-6 relative error against expf and the divide, and four VALU instructions per element
+    // instead of ~25, which kept the kernel VALU-bound after its single read (27.8 us at
+    // [512, 32000] before, ~60 % of HBM peak)
+    constexpr float L2E = 1.44269504088896341f;
     float sum = 0.f;
 #pragma unroll
     for (int i = 0; i < V; i++) {
         int64_t j = threadIdx.x + (int64_t)i * 512;
         if (j < n4) {
-            v[i].x = expf(v[i].x - mx);
-            v[i].y = expf(v[i].y - mx);
-            v[i].z = expf(v[i].z - mx);
-            v[i].w = expf(v[i].w - mx);
+            v[i].x = __builtin_amdgcn_exp2f((v[i].x - mx) * L2E);
+            v[i].y = __builtin_amdgcn_exp2f((v[i].y - mx) * L2E);
+            v[i].z = __builtin_amdgcn_exp2f((v[i].z - mx) * L2E);
+            v[i].w = __builtin_amdgcn_exp2f((v[i].w - mx) * L2E);
             sum += (v[i].x + v[i].y) + (v[i].z + v[i].w);
         }
     }
     sum = block_sum(sum, red);
+    const float inv = 1.0f / sum;
     float4* o = reinterpret_cast<float4*>(out + row * n);
 #pragma unroll
     for (int i = 0; i < V; i++) {
         int64_t j = threadIdx.x + (int64_t)i * 512;
         if (j < n4) {
             float4 r;
-            r.x = v[i].x / sum;
-            r.y = v[i].y / sum;
-            r.z = v[i].z / sum;
-            r.w = v[i].w / sum;
+            r.x = v[i].x * inv;
+            r.y = v[i].y * inv;
+            r.z = v[i].z * inv;
+            r.w = v[i].w * inv;
             o[j] = r;
         }
     }
