@@ -211,14 +211,15 @@ template <>
 struct QWords<TL_HIP_GGML_Q8_0> {
     static constexpr int BYTES = 32;
     // words 2t, 2t+1 = elements 8t .. 8t+7 as pairs (8t, 8t+2) (8t+1, 8t+3) (8t+4, 8t+6)
-    // (8t+5, 8t+7); (q ^ 0x80) | 0x6400 is 1024 + q + 128
-    __device__ static half8 operand(const uint4 (&raw)[2], int t, half2v d2, half2v) {
-        const uint32_t src[8] = {raw[0].x, raw[0].y, raw[0].z, raw[0].w, raw[1].x, raw[1].y, raw[1].z, raw[1].w};
+    // (8t+5, 8t+7); (q ^ 0x80) | 0x6400 is 1024 + q + 128.  raw = the block's 16 bytes that
+    // hold k-steps 2 kh and 2 kh + 1; tt selects the step (words 2 tt, 2 tt + 1).
+    __device__ static half8 operand(const uint4& raw, int tt, half2v d2) {
+        const uint32_t src[4] = {raw.x, raw.y, raw.z, raw.w};
         const half2v off = {(_Float16)-1152.0f, (_Float16)-1152.0f};
         half8 r;
 #pragma unroll
         for (int h = 0; h < 2; h++) {
-            const uint32_t w = src[2 * t + h] ^ 0x80808080u;
+            const uint32_t w = src[2 * tt + h] ^ 0x80808080u;
 #pragma unroll
             for (int p = 0; p < 2; p++) {
                 const uint32_t bits = ((w >> (8 * p)) & 0x00FF00FFu) | 0x64006400u;
@@ -397,9 +398,12 @@ __global__ __launch_bounds__(512) void k_qgemm_mfma(const uint8_t* __restrict__ 
     // This wavefront's half of the iteration: k-steps t = 2 kh, 2 kh + 1.  Every LDS read
     // (W quants, scale words, A fragments) is issued before the first use.
     auto compute = [&](const Stage& st) {
-        // quant data of the wavefront's rows: the whole block (scaled types), or the two
-        // operand words of its k-steps (f16 weights)
-        constexpr int NW = SCALED ? QC : 2;
+        // quant data of the wavefront's rows: the whole block (4-bit types), the 16 bytes of
+        // its k half (Q8_0: words 4 kh .. 4 kh + 3), or the two operand words of its k-steps
+        // (f16 weights) -- chunks picked by the wavefront's k half at the read, so the
+        // operand build indexes its words with compile-time values only
+        constexpr bool Q8 = QT == TL_HIP_GGML_Q8_0;
+        constexpr int NW = Q8 ? 1 : SCALED ? QC : 2;
         uint4 wr[TN][NW];
         uint32_t dw[TN];
 #pragma unroll
@@ -407,7 +411,7 @@ __global__ __launch_bounds__(512) void k_qgemm_mfma(const uint8_t* __restrict__ 
             const int r = wn * (BN / 2) + 16 * j + col;
 #pragma unroll
             for (int h = 0; h < NW; h++) {
-                const int c = SCALED ? g * QC + h : g * QC + 2 * kh + h;
+                const int c = Q8 ? g * QC + kh : SCALED ? g * QC + h : g * QC + 2 * kh + h;
                 const int pos = CPR == 16 ? r * 16 + (c ^ xsw(r & 15)) : (r >> 4) * 16 * CPR + c * 16 + (r & 15);
                 wr[j][h] = *reinterpret_cast<const uint4*>(&st.Wq[pos * 16]);
             }
@@ -441,7 +445,7 @@ __global__ __launch_bounds__(512) void k_qgemm_mfma(const uint8_t* __restrict__ 
             for (int j = 0; j < TN; j++) {
                 half8 bop;
                 if constexpr (QT == TL_HIP_GGML_Q4_0 || K4) bop = QWords<QT>::operand(wr[j][0], t, d2[j], m8d2[j]);
-                else if constexpr (QT == TL_HIP_GGML_Q8_0) bop = QWords<QT>::operand(wr[j], t, d2[j], m8d2[j]);
+                else if constexpr (QT == TL_HIP_GGML_Q8_0) bop = QWords<QT>::operand(wr[j][0], tt, d2[j]);
                 else bop = __builtin_bit_cast(half8, wr[j][tt]);
 #pragma unroll
                 for (int i = 0; i < TM; i++) acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[tt][i], bop, acc[i][j], 0, 0, 0);
