@@ -356,6 +356,7 @@ def main():
     ap.add_argument("--no-graph", action="store_true", help="eager launches instead of hipGraph replay")
     ap.add_argument("--no-extra", action="store_true", help="skip the prefill GEMM and attention legs")
     ap.add_argument("--gemm-only", action="store_true", help="only the prefill GEMM leg (counter runs)")
+    ap.add_argument("--gemm-m", type=int, default=0, help="with --gemm-only: this M only (default 512, 128, 16)")
     ap.add_argument("--kquant-only", action="store_true", help="only the per-type matvec and Q4_K_M decode legs")
     ap.add_argument("--attention-only", action="store_true", help="only the decode attention leg (counter runs)")
     ap.add_argument("--matvec-only", action="store_true",
@@ -375,7 +376,8 @@ def main():
         sys.exit("prompt + warmup + steps exceed the 2048-position cache")
 
     if args.gemm_only:
-        print(json.dumps({"prefill_gemm": bench_gemm(dev)}), flush=True)
+        print(json.dumps({"prefill_gemm": bench_gemm(dev, ms=(args.gemm_m,) if args.gemm_m else (512, 128, 16))}),
+              flush=True)
         return
     if args.attention_only:
         print(json.dumps({"decode_attention": bench_attention(dev)}), flush=True)

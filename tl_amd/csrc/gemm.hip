@@ -550,7 +550,8 @@ int launch_x_to_f16q(const float* x, _Float16* x16, int64_t m, int64_t k, int or
 }
 
 // Split-K sum: y = [res +] the nsp partial slices, added in slice order (the result does not
-// depend on scheduling).  y may alias res.
+// depend on scheduling).  y may alias res; y, res and part are 16-byte aligned (the launch
+// splits K only then).
 __global__ __launch_bounds__(256) void k_splitk_sum(const float* __restrict__ part, float* y, const float* res,
                                                     int64_t mn, int nsp) {
     const int64_t i = ((int64_t)blockIdx.x * 256 + threadIdx.x) * 4;
@@ -603,7 +604,8 @@ int launch_gemm_f16q(const QWeight* w, const _Float16* x16, float* y, int64_t m,
     const int64_t tiles = cdiv(m, bm) * cdiv(w->n, wide ? 64 : 32);
     const int64_t iters = w->nb / Q_KR;
     int64_t nsp = 1;
-    if (!wide && ep.mode != GEMM_GLU16 && tiles < (m <= 32 ? 512 : 256)) {
+    const bool vec_ok = ((reinterpret_cast<uintptr_t>(y) | reinterpret_cast<uintptr_t>(ep.res)) & 15) == 0;
+    if (!wide && ep.mode != GEMM_GLU16 && vec_ok && tiles < (m <= 32 ? 512 : 256)) {
         nsp = std::min<int64_t>(std::min<int64_t>(cdiv(512, tiles), iters), 16);
         nsp = cdiv(iters, cdiv(iters, nsp));  // every split non-empty
     }
