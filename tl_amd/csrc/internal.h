@@ -230,7 +230,7 @@ int launch_attention_prefill(const float* q, const void* k, const void* v, float
 // Short-cache form: one workgroup per (query head, batch item); shapes: attention_qh_supported.
 bool attention_qh_supported(int kv_dtype, int D, int64_t lmax);
 // position shares per query head in the decoder's attention (records merged by the o-projection)
-constexpr int ATTN_SHARES = 4;  // 2 shares: 1810-1820 tok/s, 4: 1840-1843 (records loaded before the weights)
+constexpr int ATTN_SHARES = 4;  // 2 shares: 1810-1820 tok/s, 4: 1840-1843, 8: 1787 (merge cost)
 // nsplit > 1: each head's positions in nsplit shares of whole 64-position rounds, one
 // workgroup each, leaving unnormalised records [o (D) | max | sum | 0 | 0] (D + 4 floats) at
 // part[((b * hq + head) * nsplit + share)] instead of writing out; the decode o-projection
