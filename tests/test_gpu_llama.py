@@ -129,6 +129,27 @@ def test_long_cache_decode_paths(kv_f16):
         cpu.close()
 
 
+@pytest.mark.parametrize("use_graph", [True, False])
+def test_decode_attention_share_boundaries(use_graph):
+    """The decode step splits each head's cache positions into shares of whole 64-position
+    rounds (some empty while the cache is short) whose records the o-projection merges.  200
+    greedy tokens after a 59-token prompt cover cache lengths 60-259 -- shares filling,
+    starting and empty at 64, 128, 192 and 256 -- and must equal the oracle's (f32 cache)."""
+    cfg = LlamaConfig(2, 256, 4, 2, 512, 1000, max_seq=320)
+    tensors = list(synthetic_weights(cfg, 53))
+    gpu = HipLlama(cfg, kv_f16=False)
+    gpu.load(tensors)
+    cpu = oracle.Llama(cfg)
+    cpu.load(tensors)
+    try:
+        prompt = synthetic_prompt(cfg, 53, 59)
+        got = greedy_generate(gpu, prompt, 200, use_graph=use_graph)
+        assert list(got) == list(cpu.greedy(prompt, 200))
+    finally:
+        gpu.close()
+        cpu.close()
+
+
 def test_position_aware_rope_changes_prefill(small):
     gpu, _ = small
     prompt = synthetic_prompt(SMALL, 14, 12)
