@@ -527,23 +527,24 @@ __global__ __launch_bounds__(256) void k_mv(MvArgs a, MvShape sh) {
                 for (int q = 0; q < (int)(blockDim.x >> 6); q++) ss += ssq[q][m];
                 acc_s = acc_s / sqrtf(ss / (float)k + a.eps);
             }
-            ys[m][rl] = acc_s;
+            if constexpr (EPI == EPI_PLAIN || EPI == EPI_RES) {
+                // the thread that forms row rl's sum stores it (its residual was loaded by
+                // this thread too): no LDS round trip and no second barrier
+                const uint32_t row = row0 + rl;
+                if (row < n) {
+                    float v = acc_s;
+                    if constexpr (EPI == EPI_RES) v = pre_res + v;
+                    a.y[m * n + row] = v;
+                }
+            } else {
+                ys[m][rl] = acc_s;
+            }
         }
-        __syncthreads();
+        if constexpr (EPI != EPI_PLAIN && EPI != EPI_RES) __syncthreads();
     }
 
     // (5) epilogue
-    if constexpr (EPI == EPI_PLAIN || EPI == EPI_RES) {
-        if (tid < M * RW) {
-            const int m = tid >> rw_shift, rl = tid & (RW - 1);
-            const uint32_t row = row0 + rl;
-            if (row < n) {
-                float v = ys[m][rl];
-                if constexpr (EPI == EPI_RES) v = pre_res + v;
-                a.y[m * n + row] = v;
-            }
-        }
-    } else if constexpr (EPI == EPI_GLU) {
+    if constexpr (EPI == EPI_GLU) {
         const uint32_t half_n = n / 2;
         if (tid < M * (RW / 2)) {
             const int m = tid >> (rw_shift - 1), p = tid & (RW / 2 - 1);
