@@ -508,6 +508,7 @@ __global__ __launch_bounds__(256) void k_mv(MvArgs a, MvShape sh) {
     }
 
     // (4) thread partials -> row sums: transpose-reduce per wavefront, then across wavefronts
+    float row_v = 0.f;
     {
         float v[N];
 #pragma unroll
@@ -536,11 +537,13 @@ __global__ __launch_bounds__(256) void k_mv(MvArgs a, MvShape sh) {
                     if constexpr (EPI == EPI_RES) v = pre_res + v;
                     a.y[m * n + row] = v;
                 }
+            } else if constexpr (EPI == EPI_ARGMAX) {
+                row_v = acc_s;  // row tid (m = 0, RW <= 64: wavefront 0)
             } else {
                 ys[m][rl] = acc_s;
             }
         }
-        if constexpr (EPI != EPI_PLAIN && EPI != EPI_RES) __syncthreads();
+        if constexpr (EPI == EPI_GLU || EPI == EPI_ROPE_KV) __syncthreads();
     }
 
     // (5) epilogue
@@ -595,32 +598,35 @@ __global__ __launch_bounds__(256) void k_mv(MvArgs a, MvShape sh) {
     } else if constexpr (EPI == EPI_ARGMAX) {
         // logits, penalised logits, then this workgroup's greedy candidate (the left fold of
         // tensor.rs:1633-1637 over its rows: keep the best only when strictly greater)
-        if (tid < RW) {
-            const uint32_t row = row0 + tid;
-            if (row < n) {
-                float v = ys[0][tid];
+        // Rows 0 .. RW - 1 sit in lanes 0 .. RW - 1 of wavefront 0 (RW <= 64).  Without NaNs the
+        // fold equals (greater value, then larger index), reduced across the lanes; with a NaN
+        // the flag makes k_argmax_finish replay the sequential fold over the penalised logits.
+        if (wave == 0) {
+            const uint32_t row = row0 + lane;
+            const bool live = lane < RW && row < n;
+            float v = row_v;
+            if (live) {
                 a.y[row] = v;
                 if (pre_seen) v = v > 0.0f ? v / a.penalty : v * a.penalty;
                 a.plogits[row] = v;
-                ys[0][tid] = v;
             }
-        }
-        __syncthreads();
-        if (tid == 0) {
-            const int cnt = (int)((n - row0) < (uint32_t)RW ? (n - row0) : (uint32_t)RW);
-            float bv = ys[0][0];
-            int bi = 0, nan = bv != bv;
-            for (int i = 1; i < cnt; i++) {
-                const float v = ys[0][i];
-                nan |= v != v;
-                if (!(bv > v)) {
-                    bv = v;
-                    bi = i;
+            float bv = live ? v : -INFINITY;
+            int bi = live ? lane : -1, nan = live && v != v;
+#pragma unroll
+            for (int off = 32; off >= 1; off >>= 1) {
+                const float ov = __shfl_xor(bv, off, 64);
+                const int oi = __shfl_xor(bi, off, 64);
+                if (oi >= 0 && (bi < 0 || ov > bv || (ov == bv && oi > bi))) {
+                    bv = ov;
+                    bi = oi;
                 }
+                nan |= __shfl_xor(nan, off, 64);
             }
-            a.part_v[blockIdx.x] = bv;
-            a.part_i[blockIdx.x] = (int32_t)(row0 + bi);
-            a.part_nan[blockIdx.x] = nan;
+            if (lane == 0) {
+                a.part_v[blockIdx.x] = bv;
+                a.part_i[blockIdx.x] = (int32_t)(row0 + bi);
+                a.part_nan[blockIdx.x] = nan;
+            }
         }
     }
 }
