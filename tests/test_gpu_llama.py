@@ -150,6 +150,35 @@ def test_decode_attention_share_boundaries(use_graph):
         cpu.close()
 
 
+@pytest.mark.parametrize("penalty", [1.0, 1.1])
+def test_greedy_ties_take_the_last_index(penalty):
+    """Every LM-head row equal: all logits tie, and the greedy choice must follow tensor.rs's
+    fold (the last maximum) through the per-workgroup candidates and their merge -- the last
+    vocabulary index without a penalty; with a penalty each chosen token drops below the
+    others and the choice walks down the ties.  Graph and eager tokens equal the oracle's."""
+    cfg = LlamaConfig(2, 256, 4, 2, 512, 1000, max_seq=128)
+    tensors = []
+    for kind, layer, which, payload in synthetic_weights(cfg, 61):
+        if kind == "linear" and layer == -1:
+            rows = np.ascontiguousarray(payload).reshape(cfg.vocab, -1)
+            payload = np.repeat(rows[:1], cfg.vocab, axis=0).reshape(np.shape(payload))
+        tensors.append((kind, layer, which, payload))
+    gpu = HipLlama(cfg)
+    gpu.load(tensors)
+    cpu = oracle.Llama(cfg)
+    cpu.load(tensors)
+    try:
+        prompt = synthetic_prompt(cfg, 61, 10)
+        want = list(cpu.greedy(prompt, 12, penalty=penalty))
+        if penalty == 1.0:
+            assert want == [cfg.vocab - 1] * 12
+        for use_graph in (True, False):
+            assert list(greedy_generate(gpu, prompt, 12, penalty=penalty, use_graph=use_graph)) == want
+    finally:
+        gpu.close()
+        cpu.close()
+
+
 def test_position_aware_rope_changes_prefill(small):
     gpu, _ = small
     prompt = synthetic_prompt(SMALL, 14, 12)
