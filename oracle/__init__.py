@@ -329,6 +329,48 @@ def attention(q, kc, vc, scale_, causal):
     return out
 
 
+# Linear weights of one decoder block in slot order: Attention::from_map q, k, v, output and
+# MLP::from_map gate, up, down (chatbot.tl:23-26, 43-47); slot 7 stands for the LM head
+# "output.weight" (chatbot.tl:154).
+LINEAR_SLOTS = ("attn_q", "attn_k", "attn_v", "attn_output", "ffn_gate", "ffn_up", "ffn_down")
+
+GGML_Q4_0, GGML_Q8_0, GGML_Q4_K, GGML_Q6_K = 2, 8, 12, 14
+
+
+def linear_shape(cfg, name):
+    """Row-major [n, k] of a linear weight (gguf.rs:129-136 order) for the chatbot's model:
+    q / output [D, D], k / v [Hkv hd, D] (the reshape to [1, sl, 4, 64], chatbot.tl:53-54),
+    gate / up [F, D], down [D, F], LM head [vocab, D]."""
+    D, F = cfg.d_model, cfg.ffn_dim
+    kvd = cfg.n_kv_heads * (D // cfg.n_heads)
+    return {"attn_q": (D, D), "attn_k": (kvd, D), "attn_v": (kvd, D), "attn_output": (D, D),
+            "ffn_gate": (F, D), "ffn_up": (F, D), "ffn_down": (D, F), "output": (cfg.vocab, D)}[name]
+
+
+def q4_k_m_type(n_layers, layer, name):
+    """GGML type of a linear weight in a llama.cpp "Q4_K_M" file -- the third-party rule
+    (llama.cpp llama_tensor_get_type, not part of the reference) that decides the type mixture of
+    the chatbot's own checkpoint (chatbot.tl:119): output.weight (layer -1) Q6_K; attn_v and
+    ffn_down Q6_K in the layers where use_more_bits(i, n) holds, i.e. i < n/8, i >= 7n/8 or
+    (i - n/8) % 3 == 2 (integer division); every other linear Q4_K."""
+    if layer < 0:
+        return GGML_Q6_K
+    more = layer < n_layers // 8 or layer >= 7 * n_layers // 8 or (layer - n_layers // 8) % 3 == 2
+    if name in ("attn_v", "ffn_down") and more:
+        return GGML_Q6_K
+    return GGML_Q4_K
+
+
+def weight_type(plan, cfg, layer, name):
+    """GGML type of one linear weight under a type plan: an int for every linear, "Q4_K_M" for
+    q4_k_m_type, or a callable (cfg, layer, name)."""
+    if callable(plan):
+        return int(plan(cfg, layer, name))
+    if plan == "Q4_K_M":
+        return q4_k_m_type(cfg.n_layers, layer, name)
+    return int(plan)
+
+
 class Llama:
     """The chatbot.tl decoder on the CPU oracle (bit-identical to the tl_cpu op chain)."""
 
@@ -339,9 +381,10 @@ class Llama:
         if not self.h:
             raise OracleError("tlo_llama_new failed")
 
-    def load(self, tensors, ggml_type=2):
+    def load(self, tensors, ggml_type=GGML_Q4_0):
+        """tensors: (kind, layer, which, payload) with kind "embedding" / "norm" / "linear";
+        a linear's payload is its GGUF block bytes, typed by the plan `ggml_type`."""
         cfg = self.cfg
-        from tl_amd.llama import SLOTS, linear_type  # shapes and type plan only (host-side naming)
         for kind, layer, which, payload in tensors:
             if kind == "embedding":
                 p = _f(payload)
@@ -350,10 +393,10 @@ class Llama:
                 p = _f(payload)
                 _rc(lib().tlo_llama_set_norm(self.h, layer, which, _p(p)), "set_norm")
             else:
-                name = SLOTS[which] if layer >= 0 else "output"
-                n, k = cfg.linear_shape(name)
+                name = LINEAR_SLOTS[which] if layer >= 0 else "output"
+                n, k = linear_shape(cfg, name)
                 p = np.ascontiguousarray(payload, dtype=np.uint8)
-                t = linear_type(ggml_type, cfg, layer, name)
+                t = weight_type(ggml_type, cfg, layer, name)
                 _rc(lib().tlo_llama_set_linear(self.h, layer, which, p.ctypes.data_as(_u8p), p.size, t, n, k),
                     "set_linear")
 

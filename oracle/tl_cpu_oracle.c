@@ -31,6 +31,11 @@
  *   tlo_fused_bias_gelu     reference KAT gelu(0) = 0 (new_ops_comprehensive_test.rs:687-693),
  *                           signs at +-1.1 (tl_metal fused_ops_test.rs:60-75), limits
  *                           gelu(v) -> v / 0 for large |v|, bias broadcast i % nbias
+ *   tlo_fused_silu_mul      reference KATs f(0,1) = 0, f(1,1) = 0.7311 (tl_cuda
+ *                           new_ops_comprehensive_test.rs:635-645), fused vs unfused within
+ *                           1e-4 (tl_metal fused_ops_test.rs:42-56), float64 closed form
+ *   tlo_binop               numpy float32 add / mul / sub / div with broadcasting, IEEE
+ *                           specials, the ShapeMismatch rule (tests/test_oracle_model.py)
  *   tlo_fused_rotary_emb    one head vector: the textbook half-split rotation (norm of each
  *                           pair kept, f = 0 identity, f = pi/2 (x0, x1) -> (-x1, x0));
  *                           several vectors: brute-force replay of the reference loop

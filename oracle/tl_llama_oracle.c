@@ -12,6 +12,10 @@
  *   - attention = transpose / cat_4d / repeat_interleave / matmul_4d / scale / +mask /
  *     softmax / matmul_4d (chatbot.tl:50-90) computed directly with the same per-element
  *     operation order (tlo_attention_compose checks this against the literal op chain).
+ * Pinned by tests/test_oracle_model.py: logits and greedy ids bit-equal to a literal replay of
+ * the chatbot's op chain (one oracle op per program line, each op pinned on its own) over a
+ * 6-token prefill at position 0 plus three decode steps, Q4_0 / Q8_0 / Q4_K_M weights, with
+ * and without the repetition penalty 1.1 (chatbot.tl:188).
  * Model hyper-parameters are arguments; the chatbot hard-codes TinyLlama's
  * (chatbot.tl:51-54, 73, 83, 151, 168, 181).
  */
