@@ -294,9 +294,12 @@ def cpu_baseline(cfg, L):
     return tok_s, t_layer, t_head
 
 
-def bench_decode(dev, cfg, ggml_type, args, steps=None):
+def bench_decode(dev, cfg, ggml_type, args, steps=None, variants=()):
     """Prefill of the prompt, then warm-up and timed greedy decode tokens (hipGraph replay
-    unless --no-graph); returns (tok/s, decode seconds, prefill seconds)."""
+    unless --no-graph); returns (tok/s, decode seconds, prefill seconds, 32-token prefill
+    seconds, variant rows).  The warm-up generate captures the decode step; the timed one
+    must replay it without a new capture (checked with the library's capture counter).
+    `variants` are further (kv, penalty) settings timed the same way on the same weights."""
     from tl_amd.llama import HipLlama, synthetic_prompt, synthetic_weights
 
     steps = steps or args.steps
@@ -329,20 +332,39 @@ def bench_decode(dev, cfg, ggml_type, args, steps=None):
         dev.synchronize()
         short_s = time.perf_counter() - t0
     log(f"[bench] prefill 32 tokens: {short_s * 1e3:.2f} ms")
-    model.reset()
-    model.forward(prompt, prefill_f16=True, want_logits=False)
-    first = model.sample_greedy(1.0, prompt)
-    warm = model.generate(first, args.warmup, use_graph=not args.no_graph) if args.warmup else np.array([first])
-    nxt = int(warm[-1]) if args.warmup else first
-    dev.synchronize()
-    t0 = time.perf_counter()
-    model.generate(nxt, steps, use_graph=not args.no_graph)  # ends with a stream synchronize
-    dev.synchronize()
-    decode_s = time.perf_counter() - t0
+
+    def timed_decode(penalty):
+        model.reset()
+        model.forward(prompt, prefill_f16=True, want_logits=False)
+        first = model.sample_greedy(penalty, prompt)
+        hist = np.concatenate([prompt, [first]]).astype(np.int32)
+        warm = model.generate(first, args.warmup, penalty, hist, use_graph=not args.no_graph) \
+            if args.warmup else np.array([first], np.int32)
+        nxt = int(warm[-1])
+        hist = np.concatenate([hist, warm[:-1]]).astype(np.int32)
+        builds = model.lib.tl_hip_llama_graph_builds(model.h)
+        dev.synchronize()
+        t0 = time.perf_counter()
+        model.generate(nxt, steps, penalty, hist, use_graph=not args.no_graph)  # ends with a stream synchronize
+        dev.synchronize()
+        dt = time.perf_counter() - t0
+        if args.warmup and not args.no_graph and model.lib.tl_hip_llama_graph_builds(model.h) != builds:
+            raise RuntimeError("the timed decode captured a new graph")
+        return dt
+
+    decode_s = timed_decode(1.0)
     tok_s = steps / decode_s
     log(f"[bench] decode {steps} tokens: {decode_s * 1e3:.1f} ms -> {tok_s:.1f} tok/s")
+    rows = []
+    for kv, pen in variants:
+        model.configure(kv_f16=(kv == "f16"))
+        dt = timed_decode(pen)
+        rows.append({"kv_cache": kv, "repetition_penalty": pen, "value": round(steps / dt, 2), "unit": "tok/s",
+                     "ms_per_step": round(dt * 1e3 / steps, 4)})
+        log(f"[bench] decode {steps} tokens, {kv} KV cache, penalty {pen}: {dt * 1e3:.1f} ms -> "
+            f"{steps / dt:.1f} tok/s")
     model.close()
-    return tok_s, decode_s, prefill_s, short_s
+    return tok_s, decode_s, prefill_s, short_s, rows
 
 
 def main():
@@ -384,7 +406,7 @@ def main():
         return
     if args.kquant_only:
         print(json.dumps({"quant_matvec": bench_quant_matvec(dev)}), flush=True)
-        tok_s, decode_s, prefill_s, _ = bench_decode(dev, cfg, "Q4_K_M", args, steps=64)
+        tok_s, decode_s, prefill_s, _, _ = bench_decode(dev, cfg, "Q4_K_M", args, steps=64)
         print(json.dumps({"q4_k_m_decode_tok_s": round(tok_s, 2), "prefill_ms": round(prefill_s * 1e3, 2)}),
               flush=True)
         return
@@ -414,10 +436,12 @@ def main():
         gemm = bench_gemm(dev)
         attn = bench_attention(dev)
 
-    tok_s, decode_s, prefill_s, short_s = bench_decode(dev, cfg, 2, args)
+    other_kv = "f32" if args.kv == "f16" else "f16"
+    tok_s, decode_s, prefill_s, short_s, variants = bench_decode(
+        dev, cfg, 2, args, variants=[(args.kv, 1.1), (other_kv, 1.0)])
     kq = None
     if not args.no_extra:
-        kq_tok_s, kq_decode_s, kq_prefill_s, kq_short_s = bench_decode(dev, cfg, "Q4_K_M", args, steps=64)
+        kq_tok_s, kq_decode_s, kq_prefill_s, kq_short_s, _ = bench_decode(dev, cfg, "Q4_K_M", args, steps=64)
         kq = {"workload": "same decoder with llama.cpp's Q4_K_M type mixture (Q4_K; Q6_K for the LM head and "
                           "attn_v / ffn_down of 11 of 22 layers)", "value": round(kq_tok_s, 2), "unit": "tok/s",
               "steps": 64, "ms_per_step": round(kq_decode_s * 1e3 / 64, 4), "prefill_ms": round(kq_prefill_s * 1e3, 2),
@@ -455,9 +479,12 @@ def main():
                         f"{args.prompt}-token prompt then greedy decode at batch 1",
             "prompt_tokens": args.prompt,
             "kv_cache": args.kv,
+            "repetition_penalty": 1.0,
             "prefill_ms": round(prefill_s * 1e3, 2),
             "prefill_32_ms": round(short_s * 1e3, 3),
         },
+        "decode_variants": {"note": "the same model and prompt: the chatbot's repetition penalty 1.1 "
+                                    "(chatbot.tl:188) and the other KV-cache element type", "runs": variants},
         "roofline": {
             "bound": "hbm",
             "kernel": "k_mv<Q4_0> 4096x4096 (m=1)",
@@ -466,6 +493,8 @@ def main():
             "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBS, 4),
             "traffic": MATVEC_TRAFFIC,
+            "traffic_source": "not measured in this run: FETCH_SIZE + WRITE_SIZE counter runs of "
+                              "`bench.py --matvec-only` (profiles/q4_0_matvec_4096x4096.md)",
             "avg_launch_us": round(avg_s * 1e6, 3),
         },
         "cpu_baseline": cpu,

@@ -9,8 +9,14 @@
  *     message readable with tl_hip_last_error() -- the LAST_ERROR + sentinel convention of
  *     device_ffi.rs:22-80, 106-113.  Nothing aborts or panics.
  *   - Status codes mirror tl_backend::BackendError (crates/tl_backend/src/error.rs:7-17).
- *   - All device work is ordered on one HIP stream per process (tl_hip_stream); calls that
- *     return data to the host synchronise that stream.
+ *   - All device work is ordered on one HIP stream per process (tl_hip_stream) unless the
+ *     calling thread redirects it (tl_hip_set_stream) or a launcher is given a stream; calls
+ *     that return data to the host synchronise the stream they ran on.
+ *   - Device memory is cached and reused in stream order: releasing a tensor (or any freed
+ *     temporary) "frees it on" the calling thread's current stream, and that memory is reused
+ *     at once by later work on the same stream, by work on other streams only after the
+ *     work queued before the release has completed.  Release a tensor on the stream of its
+ *     last use, or synchronise that stream first.
  * Every entry point names the reference interface it replaces.
  */
 #ifndef TL_HIP_H
@@ -63,7 +69,8 @@ int tl_hip_init(int device);
 int tl_hip_device_count(void);
 /* Library stream as a hipStream_t (GpuStream, tl_backend stream.rs:12-31). */
 void* tl_hip_stream(void);
-/* Redirects library work to a caller stream (NULL restores the library stream). */
+/* Redirects the calling thread's library work to a caller stream (NULL restores the library
+ * stream).  Stream priorities other than the default are not supported. */
 int tl_hip_set_stream(void* hip_stream);
 int tl_hip_synchronize(void);
 /* Device-memory plumbing for C callers and tests. */
@@ -81,6 +88,10 @@ int tl_hip_event_destroy(void* ev);
  * library stream, so that work enqueued behind it is timed back-to-back on the GPU rather
  * than at the host's launch rate.  Timing plumbing; no reference counterpart. */
 int tl_hip_stall(uint32_t us);
+/* Fault injection for error-path tests: the allocation after `after` more successful ones
+ * fails with AllocationError (after < 0 disables).  No reference counterpart; the reference
+ * panics on allocation failure (tl_cuda tensor.rs:128-141). */
+int tl_hip_debug_fail_alloc(int64_t after);
 
 /* ---------------------------------------------------------------- tensors -------- */
 /* IDevice::tensor_new (crates/tl_backend/src/device.rs:21-26): f32 host data -> device. */
@@ -169,6 +180,10 @@ int tl_hip_launch_quant_matvec(const tl_hip_qtensor* w, const float* x, float* y
                                void* stream);
 int tl_hip_launch_quant_gemm(const tl_hip_qtensor* w, const float* x, float* y, int64_t m,
                              int use_f16_mfma, void* stream);
+/* Tile plan of the calling thread's last f16-MFMA GEMM launch: rows and columns of one
+ * workgroup's output tile and the number of K splits (1 = unsplit).  Instrumentation for the
+ * parity tests (which kernel variant ran); no reference counterpart. */
+int tl_hip_debug_last_gemm_plan(int* tile_m, int* tile_n, int* k_splits);
 
 /* ------------------------------------------------------------ tensor operators --- */
 /* IDevice::tensor_matmul (device.rs:258; tl_cpu tensor.rs:1248-1313): [.., m, k] x
@@ -296,6 +311,10 @@ int tl_hip_llama_configure(tl_hip_llama* m, int kv_f16, int rope_per_token);
 int tl_hip_llama_reset(tl_hip_llama* m);
 /* Number of cached positions (the chatbot's start_pos for the next call). */
 int64_t tl_hip_llama_position(const tl_hip_llama* m);
+/* Number of times the decode step has been captured as a hipGraph so far (instrumentation:
+ * a capture happens on the first graph decode and after a change of weights, configuration or
+ * penalty value; no reference counterpart). */
+int64_t tl_hip_llama_graph_builds(const tl_hip_llama* m);
 /* One pass of the decode-loop body (chatbot.tl:174-187) over n new token ids at the
  * current cache position; writes the last row's logits [vocab] to logits_out (host,
  * may be NULL). prefill_f16 selects the f16-MFMA GEMM for the n > 4 linears. */

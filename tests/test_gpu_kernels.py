@@ -3,6 +3,7 @@ called through the C ABI (tl_amd binds libtl_hip.so with ctypes).
 
 max-rel-err = max_i |a_i - b_i| / max(max_j |b_j|, 1e-30); bounds from the north star:
 bit-exact for dequant, 1e-4 for f32 paths, 1e-2 for f16 paths."""
+import ctypes as C
 import json
 import os
 
@@ -10,7 +11,7 @@ import numpy as np
 import pytest
 
 import oracle
-from tl_amd import GGML_Q4_0, GGML_Q8_0, BackendError, QTensor
+from tl_amd import GGML_Q4_0, GGML_Q8_0, BackendError, QTensor, _lib
 from tl_amd.quant import random_q4_0_blocks, random_q8_0_blocks
 
 pytestmark = pytest.mark.gpu
@@ -88,6 +89,44 @@ def test_quant_gemm_f32_and_f16(dev, t, m, nk):
     assert_rel(y32, ref, F32_TOL)
     y16 = dev.tl_qtensor_matmul_f16(xt, q).to_numpy()
     assert_rel(y16, ref, F16_TOL)
+
+
+def _gemm_plan():
+    lib = _lib.load()
+    v = [C.c_int32() for _ in range(3)]
+    assert lib.tl_hip_debug_last_gemm_plan(*[C.byref(x) for x in v]) == 0
+    return tuple(x.value for x in v)
+
+
+@pytest.mark.parametrize("t", [GGML_Q4_0, GGML_Q8_0])
+@pytest.mark.parametrize("nk", [(11008, 4096), (4096, 11008), (4096, 4096)])
+def test_quant_gemm_f16_full_size_m512(dev, t, nk):
+    """The prefill GEMMs bench.py times, at their full configs[2] size (M = 512, every row of
+    W): the f16 MFMA path against the oracle's threaded f32 product (bit-identical to the
+    faithful loop) within the f16 tolerance, and the launch plan that ran -- unsplit 128 x 64
+    tiles (11008 x 4096) or 128 x 32 tiles (the 4096-row shapes, fewer than 512 wide tiles)."""
+    n, k = nk
+    m = 512
+    rng = np.random.default_rng(0x71550000 + n + t)
+    raw = blocks(t, rng, n, k)
+    x = rng.standard_normal((m, k)).astype(np.float32)
+    y16 = dev.tl_qtensor_matmul_f16(dev.tensor_new(x), QTensor(t, raw, (n, k))).to_numpy()
+    assert _gemm_plan() == ((128, 64, 1) if n == 11008 else (128, 32, 1))
+    ref = oracle.qtensor_matmul(x, raw, t, n, fast=True)
+    assert_rel(y16, ref, F16_TOL)
+
+
+@pytest.mark.parametrize("k,m", [(17408, 2), (17408, 4), (34816, 1)])
+def test_qtensor_matmul_long_rows_take_the_gemm(dev, k, m):
+    """Rows too long for the LDS-staged matvec (k >= 17408 at 2-4 rows, >= 34816 at one):
+    tl_qtensor_matmul takes the tiled f32 GEMM instead of returning an error, as the
+    reference accepts any [n, k] weight (system.rs:180-382)."""
+    n = 96
+    rng = np.random.default_rng(0x71560000 + k + m)
+    raw = blocks(GGML_Q4_0, rng, n, k)
+    x = rng.standard_normal((m, k)).astype(np.float32)
+    y = dev.tl_qtensor_matmul(dev.tensor_new(x), QTensor(GGML_Q4_0, raw, (n, k))).to_numpy()
+    assert_rel(y, oracle.qtensor_matmul(x, raw, GGML_Q4_0, n), F32_TOL)
 
 
 @pytest.mark.parametrize("t", [GGML_Q4_0, GGML_Q8_0])

@@ -179,6 +179,62 @@ def test_greedy_ties_take_the_last_index(penalty):
         cpu.close()
 
 
+def test_graph_follows_the_penalty_value(small):
+    """The penalty reaches the captured step as a kernel argument: a generate with another
+    penalty value must capture again (graph tokens = eager = oracle for 1.1, then 0.5 -- a
+    penalty below 1 raises the positive logits of seen tokens, so the ids differ), and a
+    longer generate with unchanged settings must replay without a new capture."""
+    gpu, cpu = small
+    gpu.configure(kv_f16=False)
+    prompt = synthetic_prompt(SMALL, 15, 13)
+    wants = {}
+    for pen in (1.1, 0.5):
+        wants[pen] = list(cpu.greedy(prompt, 24, penalty=pen))
+    assert wants[1.1] != wants[0.5], "penalties chosen too close to tell the graphs apart"
+    builds = lambda: int(gpu.lib.tl_hip_llama_graph_builds(gpu.h))
+    for pen in (1.1, 0.5, 1.1):
+        b0 = builds()
+        assert list(greedy_generate(gpu, prompt, 24, penalty=pen, use_graph=True)) == wants[pen]
+        assert builds() == b0 + 1
+        assert list(greedy_generate(gpu, prompt, 24, penalty=pen, use_graph=False)) == wants[pen]
+    b0 = builds()
+    for n in (8, 30):   # same settings, fewer and more steps: replays only
+        assert list(greedy_generate(gpu, prompt, n, penalty=1.1, use_graph=True)) == \
+            list(cpu.greedy(prompt, n, penalty=1.1))
+    assert builds() == b0
+
+
+def test_failed_activation_grow_leaves_the_model_usable():
+    """An allocation failure while the activation buffers grow for a longer call returns
+    AllocationError and leaves no stale buffer or captured step behind: the next short call
+    allocates again, and greedy tokens (graph and eager) still equal the oracle's."""
+    from tl_amd import BackendError
+    tensors = list(synthetic_weights(SMALL, 17))
+    gpu = HipLlama(SMALL)
+    gpu.load(tensors)
+    cpu = oracle.Llama(SMALL)
+    cpu.load(tensors)
+    try:
+        prompt = synthetic_prompt(SMALL, 17, 9)
+        want = list(cpu.greedy(prompt, 10))
+        assert list(greedy_generate(gpu, prompt, 10)) == want        # step captured at 9 tokens
+        for fail_after in (0, 3):
+            gpu.reset()
+            gpu.lib.tl_hip_debug_fail_alloc(fail_after)
+            try:
+                with pytest.raises(BackendError) as e:
+                    gpu.forward(synthetic_prompt(SMALL, 18, 100 + fail_after))
+            finally:
+                gpu.lib.tl_hip_debug_fail_alloc(-1)
+            assert e.value.variant == "AllocationError"
+            assert gpu.position == 0
+            for use_graph in (True, False):
+                assert list(greedy_generate(gpu, prompt, 10, use_graph=use_graph)) == want
+    finally:
+        gpu.close()
+        cpu.close()
+
+
 def test_position_aware_rope_changes_prefill(small):
     gpu, _ = small
     prompt = synthetic_prompt(SMALL, 14, 12)

@@ -36,6 +36,7 @@ PROTOS = {
     "tl_hip_event_elapsed_ms": (i32, [P, P, f32p]),
     "tl_hip_event_destroy": (i32, [P]),
     "tl_hip_stall": (i32, [C.c_uint32]),
+    "tl_hip_debug_fail_alloc": (i32, [i64]),
     "tl_hip_tensor_new": (P, [f32p, i64p, i32]),
     "tl_hip_tensor_new_f16": (P, [u16p, i64p, i32]),
     "tl_hip_tensor_zeros": (P, [i64p, i32, i32]),
@@ -67,6 +68,7 @@ PROTOS = {
     "tl_hip_llama_load_gguf": (i32, [P, P]),
     "tl_hip_launch_quant_matvec": (i32, [P, P, P, i64, P]),
     "tl_hip_launch_quant_gemm": (i32, [P, P, P, i64, i32, P]),
+    "tl_hip_debug_last_gemm_plan": (i32, [i32p, i32p, i32p]),
     "tl_hip_tensor_matmul": (P, [P, P]),
     "tl_hip_tensor_transpose_2d": (P, [P]),
     "tl_hip_tensor_transpose": (P, [P, i64, i64]),
@@ -106,6 +108,7 @@ PROTOS = {
     "tl_hip_llama_configure": (i32, [P, i32, i32]),
     "tl_hip_llama_reset": (i32, [P]),
     "tl_hip_llama_position": (i64, [P]),
+    "tl_hip_llama_graph_builds": (i64, [P]),
     "tl_hip_llama_forward": (i32, [P, i32p, i32, f32p, i32]),
     "tl_hip_llama_sample_greedy": (C.c_int32, [P, f64, i32p, i32]),
     "tl_hip_llama_generate": (i32, [P, C.c_int32, i32, i32p, f64, i32p, i32, i32]),

@@ -532,7 +532,7 @@ int q4k_build_unit_scales(QWeight* w, hipStream_t s) {
     std::lock_guard<std::mutex> lk(mu);
     if (w->ggml_type != TL_HIP_GGML_Q4_K || w->us) return TL_HIP_OK;
     const int64_t units = w->n * w->nb;
-    w->us = static_cast<uint32_t*>(dev_alloc((size_t)units * 4));
+    w->us = static_cast<uint32_t*>(dev_alloc_on((size_t)units * 4, s));
     if (!w->us) return TL_HIP_ERR_ALLOC;
     k_q4k_unit_scales<<<(unsigned)cdiv(units, 256), 256, 0, s>>>(w->hdr, w->us, units);
     hipError_t e = hipGetLastError();
@@ -575,6 +575,9 @@ __global__ __launch_bounds__(256) void k_splitk_sum(const float* __restrict__ pa
     }
 }
 
+// tile plan of the calling thread's last f16 GEMM launch (tl_hip_debug_last_gemm_plan)
+static thread_local int tls_plan[3] = {0, 0, 0};
+
 int launch_gemm_f16q(const QWeight* w, const _Float16* x16, float* y, int64_t m, const GemmEpi& ep,
                      hipStream_t s) {
     if (m < 1) return TL_HIP_OK;
@@ -610,9 +613,12 @@ int launch_gemm_f16q(const QWeight* w, const _Float16* x16, float* y, int64_t m,
         nsp = std::min<int64_t>(std::min<int64_t>(cdiv(512, tiles), iters), 16);
         nsp = cdiv(iters, cdiv(iters, nsp));  // every split non-empty
     }
+    tls_plan[0] = bm;
+    tls_plan[1] = wide ? 64 : 32;
+    tls_plan[2] = (int)nsp;
     float* part = nullptr;
     if (nsp > 1) {
-        part = static_cast<float*>(dev_alloc((size_t)nsp * m * w->n * sizeof(float)));
+        part = static_cast<float*>(dev_alloc_on((size_t)nsp * m * w->n * sizeof(float), s));
         if (!part) return TL_HIP_ERR_ALLOC;
     }
     const GemmEpi pe = nsp > 1 ? GemmEpi{GEMM_PLAIN, nullptr, nullptr, 0} : ep;
@@ -635,7 +641,7 @@ int launch_gemm_f16q(const QWeight* w, const _Float16* x16, float* y, int64_t m,
     } else if (w->ggml_type == TL_HIP_GGML_Q4_K || w->ggml_type == TL_HIP_GGML_Q6_K) {
         // K-quants: dequantize once into f16 operand order (n * k halves), then the same
         // MFMA pipeline with the weights read as stored
-        _Float16* w16 = static_cast<_Float16*>(dev_alloc((size_t)w->n * w->k * sizeof(_Float16)));
+        _Float16* w16 = static_cast<_Float16*>(dev_alloc_on((size_t)w->n * w->k * sizeof(_Float16), s));
         if (!w16) return TL_HIP_ERR_ALLOC;
         const QView qv{w->qs, w->d, w->hdr, w->qh, w->sc};
         const int64_t wunits = w->n * w->nb;
@@ -644,13 +650,13 @@ int launch_gemm_f16q(const QWeight* w, const _Float16* x16, float* y, int64_t m,
         else
             k_dequant_f16q<TL_HIP_GGML_Q6_K><<<(unsigned)cdiv(wunits, 256), 256, 0, s>>>(qv, w16, wunits);
         gemm(std::integral_constant<int, TL_HIP_GGML_F16>{}, reinterpret_cast<const uint8_t*>(w16), nullptr);
-        dev_free(w16);
+        dev_free_on(w16, s);
     } else if (w->ggml_type == TL_HIP_GGML_Q4_0) {
         gemm(std::integral_constant<int, TL_HIP_GGML_Q4_0>{}, w->qs, w->d);
     } else {
         gemm(std::integral_constant<int, TL_HIP_GGML_Q8_0>{}, w->qs, w->d);
     }
-    if (part) dev_free(part);  // stream-ordered: reused only by later work on the same stream
+    if (part) dev_free_on(part, s);  // freed on s: reused at once only by later work on s
     hipError_t e = hipGetLastError();
     return e == hipSuccess ? TL_HIP_OK : hip_fail(e, "quant gemm launch");
 }
@@ -675,13 +681,13 @@ int launch_quant_gemm(const QWeight* w, const float* x, float* y, int64_t m, hip
         }
     } else {
         // X -> f16 in the operand k order (a workspace of m * k halves), then the MFMA GEMM
-        _Float16* x16 = static_cast<_Float16*>(dev_alloc((size_t)m * w->k * sizeof(_Float16)));
+        _Float16* x16 = static_cast<_Float16*>(dev_alloc_on((size_t)m * w->k * sizeof(_Float16), s));
         if (!x16) return TL_HIP_ERR_ALLOC;
         // a Q4_K tensor gets its unit scales on its first f16 GEMM (kept with the tensor)
         int rc = q4k_build_unit_scales(const_cast<QWeight*>(w), s);
         if (rc == TL_HIP_OK) rc = launch_x_to_f16q(x, x16, m, w->k, f16q_order(w->ggml_type), s);
         if (rc == TL_HIP_OK) rc = launch_gemm_f16q(w, x16, y, m, GemmEpi{GEMM_PLAIN, nullptr, nullptr, 0}, s);
-        dev_free(x16);  // stream-ordered: reused only by later work on the same stream
+        dev_free_on(x16, s);  // freed on s: reused at once only by later work on s
         if (rc) return rc;
     }
     hipError_t e = hipGetLastError();
@@ -768,3 +774,14 @@ int launch_matmul_f32(const float* a, const float* b, float* c, int64_t batch, i
 }
 
 }  // namespace tlhip
+
+extern "C" int tl_hip_debug_last_gemm_plan(int* tile_m, int* tile_n, int* k_splits) {
+    if (!tile_m || !tile_n || !k_splits) {
+        tlhip::set_error(TL_HIP_ERR_NULL, "NullPointerError: output");
+        return TL_HIP_ERR_NULL;
+    }
+    *tile_m = tlhip::tls_plan[0];
+    *tile_n = tlhip::tls_plan[1];
+    *k_splits = tlhip::tls_plan[2];
+    return TL_HIP_OK;
+}

@@ -34,10 +34,15 @@ DeviceState* state();      // initialises device 0 on first use; nullptr on fail
 hipStream_t cur_stream();  // library stream (or the override set by tl_hip_set_stream)
 
 // ---- stream-ordered caching allocator --------------------------------------------
-// Every library kernel runs on one stream, so a block freed after its last use on that
-// stream can be handed to the next request without a device synchronisation.
-void* dev_alloc(size_t bytes);  // nullptr + AllocationError on failure
-void dev_free(void* p);
+// A block is freed on the stream of its last use; a request on that stream reuses it with
+// no synchronisation, a request on another stream only after the free's event completed.
+void* dev_alloc(size_t bytes);  // on cur_stream(); nullptr + AllocationError on failure
+void dev_free(void* p);         // on cur_stream()
+void* dev_alloc_on(size_t bytes, hipStream_t s);
+void dev_free_on(void* p, hipStream_t s);
+// Marks that work runs on stream s; the first stream other than the library stream switches
+// the allocator to event-tagged frees.
+void note_stream(hipStream_t s);
 
 // ---- tensors ---------------------------------------------------------------------
 struct Tensor {
@@ -137,6 +142,7 @@ struct QWeight;
 int launch_mv(const QWeight* w, MvArgs a, int m, int epi, bool norm, bool embed, hipStream_t s);
 // workgroups (= argmax partial slots) of a matvec over n rows
 int mv_partials(int64_t n);
+bool matvec_fits(const QWeight* w, int64_t m);  // the LDS-staged matvec takes this product
 
 // kernel entry points shared across translation units (all on the given stream)
 int launch_quant_matvec(const QWeight* w, const float* x, float* y, int64_t m, hipStream_t s,

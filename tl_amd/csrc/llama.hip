@@ -135,7 +135,10 @@ struct Llama {
     int max_out = 0;
     int64_t host_pos = 0;
     hipGraphExec_t graph = nullptr;
-    int graph_key[3] = {-1, -1, -1};  // (penalty on, kv_f16, rope_per_token) it was built for
+    // what the captured step was built for: penalty bits (the value is a kernel argument),
+    // kv_f16, rope_per_token
+    uint32_t graph_key[3] = {0xffffffffu, 0xffffffffu, 0xffffffffu};
+    int64_t graph_builds = 0;
 };
 
 static Llama* L_(tl_hip_llama* h) { return reinterpret_cast<Llama*>(h); }
@@ -163,8 +166,13 @@ static int alloc_kv(Llama* m) {
     return TL_HIP_OK;
 }
 
+// Activation buffers for n tokens per call.  A failed grow leaves no buffer at all and
+// max_tok 0, so the next call of any size allocates again instead of running on freed memory;
+// the captured decode step (which holds the old pointers) is dropped first.
 static int ensure_tokens(Llama* m, int64_t n) {
     if (n <= m->max_tok) return TL_HIP_OK;
+    free_graph(m);
+    m->max_tok = 0;
     float** bufs[] = {&m->x, &m->h, &m->qkv, &m->q, &m->ao, &m->t, &m->gu, &m->act};
     for (float** b : bufs) {
         dev_free(*b);
@@ -174,7 +182,10 @@ static int ensure_tokens(Llama* m, int64_t n) {
     dev_free(m->ws);
     dev_free(m->xa16);
     dev_free(m->xb16);
+    m->ids = nullptr;
+    m->ws = nullptr;
     m->xa16 = m->xb16 = nullptr;
+    m->ws_floats = 0;
     const int64_t qkv_w = m->D + 2 * (int64_t)m->KV * m->hd;
     m->x = (float*)dev_alloc(n * m->D * 4);
     m->h = (float*)dev_alloc(n * m->D * 4);
@@ -192,11 +203,22 @@ static int ensure_tokens(Llama* m, int64_t n) {
     int nsplit = 2 * (int)cdiv(m->max_seq, 128);
     m->ws_floats = attn_workspace_floats((int)n, m->KV, m->H / m->KV, m->hd, nsplit);
     m->ws = (float*)dev_alloc(m->ws_floats * 4);
-    for (float** b : bufs)
-        if (!*b) return TL_HIP_ERR_ALLOC;
-    if (!m->ids || !m->ws || !m->xa16 || !m->xb16) return TL_HIP_ERR_ALLOC;
+    bool ok = m->ids && m->ws && m->xa16 && m->xb16;
+    for (float** b : bufs) ok = ok && *b;
+    if (!ok) {
+        for (float** b : bufs) {
+            dev_free(*b);
+            *b = nullptr;
+        }
+        void** rest[] = {(void**)&m->ids, (void**)&m->ws, (void**)&m->xa16, (void**)&m->xb16};
+        for (void** b : rest) {
+            dev_free(*b);
+            *b = nullptr;
+        }
+        m->ws_floats = 0;
+        return TL_HIP_ERR_ALLOC;
+    }
     m->max_tok = n;
-    free_graph(m);  // captured pointers changed
     return TL_HIP_OK;
 }
 
@@ -573,8 +595,12 @@ tl_hip_llama* tl_hip_llama_new(int n_layers, int d_model, int n_heads, int n_kv_
     m->am_v = (float*)dev_alloc((size_t)parts * 4);
     m->am_i = (int32_t*)dev_alloc((size_t)parts * 4);
     m->am_nan = (int32_t*)dev_alloc((size_t)parts * 4);
+    // generated ids of one generate call: at most max_seq (the cache bounds the steps), so the
+    // captured step never has to be rebuilt for a longer call
+    m->out_ids = (int32_t*)dev_alloc((size_t)max_seq * 4);
+    m->max_out = max_seq;
     int rc = (m->cos_t && m->sin_t && m->logits && m->plogits && m->pos && m->tok && m->step && m->seen &&
-              m->am_v && m->am_i && m->am_nan)
+              m->am_v && m->am_i && m->am_nan && m->out_ids)
                  ? TL_HIP_OK : TL_HIP_ERR_ALLOC;
     if (rc == TL_HIP_OK) rc = launch_rope_table(m->cos_t, max_seq, m->hd, rope_theta, 0, s);
     if (rc == TL_HIP_OK) rc = launch_rope_table(m->sin_t, max_seq, m->hd, rope_theta, 1, s);
@@ -813,6 +839,14 @@ int tl_hip_llama_reset(tl_hip_llama* h) {
     return TL_HIP_OK;
 }
 
+int64_t tl_hip_llama_graph_builds(const tl_hip_llama* h) {
+    if (!h) {
+        set_error(TL_HIP_ERR_NULL, "NullPointerError: model");
+        return -1;
+    }
+    return reinterpret_cast<const Llama*>(h)->graph_builds;
+}
+
 int64_t tl_hip_llama_position(const tl_hip_llama* h) {
     if (!h) {
         set_error(TL_HIP_ERR_NULL, "NullPointerError: model");
@@ -912,13 +946,6 @@ int tl_hip_llama_generate(tl_hip_llama* h, int32_t first, int n_steps, int32_t* 
     }
     hipStream_t s = cur_stream();
     if ((rc = ensure_tokens(m, 1))) return rc;
-    if (n_steps > m->max_out) {
-        free_graph(m);
-        dev_free(m->out_ids);
-        m->out_ids = (int32_t*)dev_alloc((size_t)n_steps * 4);
-        if (!m->out_ids) return TL_HIP_ERR_ALLOC;
-        m->max_out = n_steps;
-    }
     const float pen = (float)repetition_penalty;
     if (pen != 1.0f) {
         // the ids the penalty sees: history plus the token being fed (chatbot.tl:188, 221)
@@ -934,14 +961,18 @@ int tl_hip_llama_generate(tl_hip_llama* h, int32_t first, int n_steps, int32_t* 
     TLH_CHECK_HIP(hipMemcpyAsync(m->step, &zero, 4, hipMemcpyHostToDevice, s));
     TLH_CHECK_HIP(hipStreamSynchronize(s));
     if (use_graph) {
-        const int key[3] = {pen != 1.0f, m->kv_f16, m->rope_per_token};
+        uint32_t key[3] = {0, (uint32_t)m->kv_f16, (uint32_t)m->rope_per_token};
+        std::memcpy(&key[0], &pen, 4);
         if (m->graph && std::memcmp(key, m->graph_key, sizeof(key)) != 0) free_graph(m);
         if (!m->graph) {
             hipGraph_t g;
             TLH_CHECK_HIP(hipStreamBeginCapture(s, hipStreamCaptureModeThreadLocal));
             rc = enqueue_step(m, pen, s);
             hipError_t e = hipStreamEndCapture(s, &g);
-            if (rc) return rc;
+            if (rc) {
+                if (e == hipSuccess) (void)hipGraphDestroy(g);
+                return rc;
+            }
             if (e != hipSuccess) return hip_fail(e, "hipStreamEndCapture");
             e = hipGraphInstantiate(&m->graph, g, nullptr, nullptr, 0);
             (void)hipGraphDestroy(g);
@@ -950,6 +981,7 @@ int tl_hip_llama_generate(tl_hip_llama* h, int32_t first, int n_steps, int32_t* 
                 return hip_fail(e, "hipGraphInstantiate");
             }
             std::memcpy(m->graph_key, key, sizeof(key));
+            m->graph_builds++;
         }
         for (int i = 0; i < n_steps; i++) TLH_CHECK_HIP(hipGraphLaunch(m->graph, s));
     } else {

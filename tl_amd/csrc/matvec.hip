@@ -834,6 +834,15 @@ int launch_mv(const QWeight* w, MvArgs a, int m, int epi, bool norm, bool embed,
     }
 }
 
+// Whether the LDS-staged matvec takes an m-row product with this weight (rows staged two at
+// a time must fit 150 KiB of LDS; the quant array stays below 2 GiB).
+bool matvec_fits(const QWeight* w, int64_t m) {
+    const int64_t mm = m >= 2 ? 2 : 1;
+    return m >= 1 && m <= 4 && w->n >= 1 && w->nb >= 1 &&
+           (uint64_t)w->n * w->nb * (w->ggml_type == TL_HIP_GGML_Q8_0 ? 32 : 16) < (1ull << 31) &&
+           (size_t)mm * w->nb * XPAD * sizeof(float) <= 150 * 1024;
+}
+
 // Upper bound on the workgroups (= argmax partial slots) of a matvec over n rows.
 int mv_partials(int64_t n) { return (int)cdiv(n, MV_MIN_RW); }
 

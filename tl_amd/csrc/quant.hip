@@ -417,7 +417,9 @@ static tl_hip_tensor* qmatmul(const tl_hip_tensor* xh, const tl_hip_qtensor* qh,
     if (!y) return nullptr;
     int rc = TL_HIP_OK;
     if (m > 0) {
-        if (m <= 4)
+        // the matvec for up to 4 rows when its LDS staging holds the rows, else the GEMM
+        // (which takes any k, as tl_qtensor_matmul does)
+        if (matvec_fits(w, m))
             rc = launch_quant_matvec(w, x->f32(), y->f32(), m, cur_stream(), nullptr);
         else
             rc = launch_quant_gemm(w, x->f32(), y->f32(), m, cur_stream(), f16);
@@ -444,6 +446,7 @@ int tl_hip_launch_quant_matvec(const tl_hip_qtensor* h, const float* x, float* y
         return TL_HIP_ERR_NULL;
     }
     if (!state()) return tl_hip_last_status();
+    note_stream((hipStream_t)stream);
     return launch_quant_matvec(reinterpret_cast<const QWeight*>(h), x, y, m,
                                stream ? (hipStream_t)stream : cur_stream(), nullptr);
 }
@@ -455,6 +458,7 @@ int tl_hip_launch_quant_gemm(const tl_hip_qtensor* h, const float* x, float* y, 
         return TL_HIP_ERR_NULL;
     }
     if (!state()) return tl_hip_last_status();
+    note_stream((hipStream_t)stream);
     return launch_quant_gemm(reinterpret_cast<const QWeight*>(h), x, y, m,
                              stream ? (hipStream_t)stream : cur_stream(), use_f16_mfma);
 }

@@ -6,7 +6,9 @@
 // after every launch (ops/llm.rs:91).  Here all work is ordered on one non-null stream and
 // nothing synchronises except calls that hand data back to the host.
 #include "internal.h"
+#include "block_cache.h"
 
+#include <atomic>
 #include <cstdarg>
 #include <cstdio>
 #include <cstring>
@@ -86,45 +88,73 @@ hipStream_t cur_stream() {
 }
 
 // ---- allocator ---------------------------------------------------------------------
-// Size classes: 256-byte granules up to 1 MiB, then powers of two.  Freed blocks are kept
-// per class and reused in stream order.
+// Size-class cache of freed blocks (block_cache.h).  While every call runs on the library
+// stream, a freed block is reused by the next request with no synchronisation (stream order).
+// Once work is seen on another stream (tl_hip_set_stream or a launcher's stream argument),
+// each free also records an event on the freeing stream, and a request on a different stream
+// takes the block only after that event has completed.
 static std::mutex g_alloc_mu;
-static std::multimap<size_t, void*> g_free;      // class size -> block
+static BlockCache<hipStream_t, hipEvent_t> g_cache;
 static std::map<void*, size_t> g_live;           // block -> class size
-static size_t g_cached_bytes = 0;
+static std::vector<hipEvent_t> g_ev_pool;
+static std::atomic<bool> g_multi{false};
+static std::atomic<int64_t> g_fail_after{-1};    // fault injection: allocations until a failure
 
-static size_t size_class(size_t b) {
-    if (b == 0) b = 1;
-    if (b <= (1u << 20)) return (b + 255) & ~size_t(255);
-    size_t c = size_t(1) << 20;
-    while (c < b) c <<= 1;
-    return c;
+void note_stream(hipStream_t s) {
+    if (!s || g_multi.load(std::memory_order_acquire) || !state() || s == g_state.stream) return;
+    std::lock_guard<std::mutex> lk(g_alloc_mu);
+    if (g_multi.load()) return;
+    // every block cached so far was used on the library stream only
+    (void)hipStreamSynchronize(g_state.stream);
+    g_cache.mark_all_idle();
+    g_multi.store(true, std::memory_order_release);
+}
+
+static hipEvent_t pool_event_locked() {
+    if (!g_ev_pool.empty()) {
+        hipEvent_t ev = g_ev_pool.back();
+        g_ev_pool.pop_back();
+        return ev;
+    }
+    hipEvent_t ev = nullptr;
+    if (hipEventCreateWithFlags(&ev, hipEventDisableTiming) != hipSuccess) {
+        (void)hipGetLastError();
+        return nullptr;
+    }
+    return ev;
 }
 
 static void release_cache_locked() {
-    for (auto& kv : g_free) (void)hipFree(kv.second);
-    g_free.clear();
-    g_cached_bytes = 0;
+    (void)hipDeviceSynchronize();
+    g_cache.drain([](void* p, hipEvent_t ev) {
+        (void)hipFree(p);
+        if (ev) g_ev_pool.push_back(ev);
+    });
 }
 
-void* dev_alloc(size_t bytes) {
+void* dev_alloc_on(size_t bytes, hipStream_t s) {
     if (!state()) return nullptr;
-    size_t c = size_class(bytes);
+    const size_t c = block_size_class(bytes);
     std::lock_guard<std::mutex> lk(g_alloc_mu);
-    auto it = g_free.find(c);
-    if (it != g_free.end()) {
-        void* p = it->second;
-        g_free.erase(it);
-        g_cached_bytes -= c;
+    const int64_t left = g_fail_after.load();
+    if (left >= 0) {
+        g_fail_after.store(left - 1);
+        if (left == 0) {
+            set_error(TL_HIP_ERR_ALLOC, "AllocationError: injected failure of a %zu-byte allocation", c);
+            return nullptr;
+        }
+    }
+    void* p = g_cache.take(
+        c, s, [](hipEvent_t ev) { return hipEventQuery(ev) == hipSuccess; },
+        [](hipEvent_t ev) { g_ev_pool.push_back(ev); });
+    if (p) {
         g_live[p] = c;
         return p;
     }
-    void* p = nullptr;
     hipError_t e = hipMalloc(&p, c);
     if (e != hipSuccess) {
         (void)hipGetLastError();
         // cached blocks may be what stands in the way: return them and retry once
-        (void)hipStreamSynchronize(g_state.stream);
         release_cache_locked();
         e = hipMalloc(&p, c);
         if (e != hipSuccess) {
@@ -138,15 +168,26 @@ void* dev_alloc(size_t bytes) {
     return p;
 }
 
-void dev_free(void* p) {
+void dev_free_on(void* p, hipStream_t s) {
     if (!p) return;
     std::lock_guard<std::mutex> lk(g_alloc_mu);
     auto it = g_live.find(p);
     if (it == g_live.end()) return;
-    g_free.emplace(it->second, p);
-    g_cached_bytes += it->second;
+    hipEvent_t ev = nullptr;
+    if (g_multi.load()) {
+        ev = pool_event_locked();
+        if (ev && hipEventRecord(ev, s) != hipSuccess) {
+            (void)hipGetLastError();
+            g_ev_pool.push_back(ev);
+            ev = nullptr;  // then only work on s itself may reuse the block
+        }
+    }
+    g_cache.put(p, it->second, s, ev);
     g_live.erase(it);
 }
+
+void* dev_alloc(size_t bytes) { return dev_alloc_on(bytes, cur_stream()); }
+void dev_free(void* p) { dev_free_on(p, cur_stream()); }
 
 size_t dtype_size(int dtype) { return dtype == TL_HIP_F16 ? 2 : 4; }
 
@@ -160,6 +201,10 @@ Tensor* tensor_alloc(const int64_t* shape, int rank, int dtype) {
         if (shape[i] < 0) {
             set_error(TL_HIP_ERR_SHAPE, "ShapeMismatch: negative dimension %lld",
                       (long long)shape[i]);
+            return nullptr;
+        }
+        if (shape[i] && n > (INT64_MAX / 4) / shape[i]) {
+            set_error(TL_HIP_ERR_ALLOC, "AllocationError: tensor of more than 2^61 elements");
             return nullptr;
         }
         n *= shape[i];
@@ -219,7 +264,13 @@ void* tl_hip_stream(void) { return (void*)cur_stream(); }
 
 int tl_hip_set_stream(void* s) {
     if (!state()) return tls_status;
+    note_stream((hipStream_t)s);
     tls_stream_override = (hipStream_t)s;
+    return TL_HIP_OK;
+}
+
+int tl_hip_debug_fail_alloc(int64_t after) {
+    g_fail_after.store(after < 0 ? -1 : after);
     return TL_HIP_OK;
 }
 
