@@ -263,6 +263,16 @@ tl_hip_tensor* tl_hip_fused_add_relu(const tl_hip_tensor* a, const tl_hip_tensor
  * 20-22): gelu(x + bias[i % len(bias)]) with tl_cpu's constant 2/sqrt(pi). */
 tl_hip_tensor* tl_hip_fused_bias_gelu(const tl_hip_tensor* x, const tl_hip_tensor* bias);
 
+/* IDevice::tensor_scaled_dot_product_attention (crates/tl_backend/src/device.rs:180-186; tl_cpu
+ * device_impl.rs:775-872): q [batch, heads, seq_q, d_k], [heads, seq_q, d_k] or [seq_q, d_k];
+ * k [.., seq_k, d_k] and v [.., seq_k, d_v] with the same leading dimensions (one KV head per
+ * query head); all f32.  scores = q k^T * (1 / sqrt(d_k)); mask (f32, may be NULL) is read as
+ * flat [seq_q, seq_k] data shared by every (batch, head): a score whose mask element exists and
+ * equals 0 becomes -1e9, any other mask value leaves it unchanged; softmax over the keys; out
+ * [.., seq_q, d_v] = softmax . v.  f32 arithmetic (tolerance class "f32 path"). */
+tl_hip_tensor* tl_hip_tensor_scaled_dot_product_attention(const tl_hip_tensor* q, const tl_hip_tensor* k,
+                                                          const tl_hip_tensor* v, const tl_hip_tensor* mask);
+
 /* Single-query decode attention over an f16 KV cache: the chatbot's
  * transpose/cat_4d/repeat_interleave/matmul_4d/scale/softmax/matmul_4d chain
  * (examples/apps/tinyllama/chatbot.tl:63-87) for sl = 1, in one fused split-L kernel pair.

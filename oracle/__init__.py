@@ -51,6 +51,7 @@ _PROTOS = {
     "tlo_embedding": (_int, [_f32p, _i64, _i64, _f32p, _i64, _f32p]),
     "tlo_argmax_last": (_i64, [_f32p, _i64]),
     "tlo_repetition_penalty": (None, [_f32p, _i64, _i64, _f32p, _i64, _f64, _f32p]),
+    "tlo_sdpa": (None, [_f32p, _f32p, _f32p, _f32p, _i64, _i64, _i64, _i64, _i64, _i64, _f32p]),
     "tlo_attention": (_int, [_f32p, _f32p, _f32p, _i64, _i64, _i64, _i64, _i64, _f32, _int, _f32p]),
     "tlo_llama_new": (C.c_void_p, [_int, _int, _int, _int, _int, _int, _f32, _f32, _int]),
     "tlo_llama_free": (None, [C.c_void_p]),
@@ -369,6 +370,20 @@ def weight_type(plan, cfg, layer, name):
     if plan == "Q4_K_M":
         return q4_k_m_type(cfg.n_layers, layer, name)
     return int(plan)
+
+
+def sdpa(q, k, v, mask=None):
+    """IDevice::tensor_scaled_dot_product_attention on tl_cpu (device_impl.rs:775-872): q [.., sq, dk]
+    (rank 2-4), k [.., sk, dk], v [.., sk, dv] with the same leading dims; mask == 0 -> -1e9."""
+    q, k, v = _f(q), _f(k), _f(v)
+    sq, dk = q.shape[-2], q.shape[-1]
+    sk, dv = k.shape[-2], v.shape[-1]
+    slices = int(np.prod(q.shape[:-2])) if q.ndim > 2 else 1
+    out = np.empty(tuple(q.shape[:-2]) + (sq, dv), dtype=np.float32)
+    m = _f(mask) if mask is not None else None
+    lib().tlo_sdpa(_p(q), _p(k), _p(v), _p(m) if m is not None else None, m.size if m is not None else 0,
+                   slices, sq, sk, dk, dv, _p(out))
+    return out
 
 
 class Llama:

@@ -39,6 +39,10 @@
  *   tlo_fused_rotary_emb    one head vector: the textbook half-split rotation (norm of each
  *                           pair kept, f = 0 identity, f = pi/2 (x0, x1) -> (-x1, x0));
  *                           several vectors: brute-force replay of the reference loop
+ *   tlo_sdpa                a causal ones-mask equals the pinned chatbot attention chain bit for
+ *                           bit (tests/test_oracle_model.py); float64 softmax(QK^T/sqrt(d_k))V;
+ *                           mask == 0 drops a key, a fully masked row averages V; seq_k = 1
+ *                           returns the V row
  *   remaining glue ops      numpy equivalents on small inputs
  */
 #include <math.h>
@@ -656,4 +660,51 @@ void tlo_repetition_penalty(const float* logits, int64_t rows, int64_t vocab, co
             out[r * vocab + i] = v > 0.0f ? v / p : v * p;
         }
     free(seen);
+}
+
+/* CpuDevice::tensor_scaled_dot_product_attention (crates/tl_cpu/src/device_impl.rs:775-872):
+ * for every (batch, head) slice, scores[i][j] = (sum_d q[i][d] k[j][d]) * (1 / sqrt(d_k)),
+ * the sum from 0 left to right (scale at 800, scores 811-823); where a mask is given, a score
+ * whose flat index i * seq_k + j lies inside the mask and whose mask value == 0.0 becomes -1e9
+ * (825-834; every other mask value leaves the score as it is, and the same [seq_q, seq_k]
+ * mask serves every slice); per row max by fold(-inf, f32::max), e = exp(s - max) summed left
+ * to right, each e divided by the sum (835-849); out[i][d] = sum_l p[i][l] v[l][d] (850-861).
+ * K and V hold the same (batch, head) slices as Q.  A row with seq_k = 0 gives zeros. */
+void tlo_sdpa(const float* q, const float* k, const float* v, const float* mask, int64_t mask_len,
+              int64_t slices, int64_t seq_q, int64_t seq_k, int64_t d_k, int64_t d_v, float* out) {
+    const float scale = 1.0f / sqrtf((float)d_k);
+    float* scores = (float*)malloc(sizeof(float) * (size_t)(seq_q * seq_k > 0 ? seq_q * seq_k : 1));
+    for (int64_t bh = 0; bh < slices; bh++) {
+        const float* Q = q + bh * seq_q * d_k;
+        const float* K = k + bh * seq_k * d_k;
+        const float* V = v + bh * seq_k * d_v;
+        for (int64_t i = 0; i < seq_q; i++)
+            for (int64_t j = 0; j < seq_k; j++) {
+                float s = 0.0f;
+                for (int64_t d = 0; d < d_k; d++) s += Q[i * d_k + d] * K[j * d_k + d];
+                scores[i * seq_k + j] = s * scale;
+            }
+        if (mask)
+            for (int64_t i = 0; i < seq_q; i++)
+                for (int64_t j = 0; j < seq_k; j++)
+                    if (mask_len > i * seq_k + j && mask[i * seq_k + j] == 0.0f) scores[i * seq_k + j] = -1e9f;
+        for (int64_t i = 0; i < seq_q; i++) {
+            float mx = -INFINITY;
+            for (int64_t j = 0; j < seq_k; j++) mx = fmaxf(mx, scores[i * seq_k + j]);
+            float sum = 0.0f;
+            for (int64_t j = 0; j < seq_k; j++) {
+                scores[i * seq_k + j] = expf(scores[i * seq_k + j] - mx);
+                sum += scores[i * seq_k + j];
+            }
+            for (int64_t j = 0; j < seq_k; j++) scores[i * seq_k + j] /= sum;
+        }
+        float* O = out + bh * seq_q * d_v;
+        for (int64_t i = 0; i < seq_q; i++)
+            for (int64_t j = 0; j < d_v; j++) {
+                float s = 0.0f;
+                for (int64_t l = 0; l < seq_k; l++) s += scores[i * seq_k + l] * V[l * d_v + j];
+                O[i * d_v + j] = s;
+            }
+    }
+    free(scores);
 }

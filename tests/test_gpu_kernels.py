@@ -418,3 +418,57 @@ def test_embedding_argmax_penalty(dev):
     tok = np.array([3, 3, 499, 17, -1], np.float32)
     got = dev.tensor_repetition_penalty(dev.tensor_new(lg), dev.tensor_new(tok), 1.1).to_numpy()
     assert np.array_equal(got, oracle.repetition_penalty(lg, tok, 1.1))
+
+
+# ------------------------------------------------------ scaled dot-product attention
+@pytest.mark.parametrize("qshape,sk,dv,mask", [
+    ((2, 4, 33, 64), 33, 64, "causal"),      # 4-D, causal ones mask (the chatbot's case)
+    ((2, 4, 1, 128), 700, 128, None),        # decode-like: one query, many keys
+    ((8, 17, 32), 129, 48, "random"),        # 3-D, d_v != d_k, zeros drop keys
+    ((5, 16), 3, 7, "rowzero"),              # 2-D, a fully masked row
+    ((3, 300, 64), 300, 64, "short"),        # mask shorter than seq_q * seq_k
+])
+def test_scaled_dot_product_attention(dev, qshape, sk, dv, mask):
+    """tensor_scaled_dot_product_attention against the oracle's restatement of tl_cpu
+    (device_impl.rs:775-872) within the f32 tolerance: scale 1/sqrt(d_k), mask == 0 -> -1e9,
+    other mask values ignored, ranks 2-4."""
+    rng = np.random.default_rng(0x71570000 + sk + dv)
+    q = rng.standard_normal(qshape).astype(np.float32)
+    k = rng.standard_normal(qshape[:-2] + (sk, qshape[-1])).astype(np.float32)
+    v = rng.standard_normal(qshape[:-2] + (sk, dv)).astype(np.float32)
+    sq = qshape[-2]
+    m = None
+    if mask == "causal":
+        m = np.tril(np.ones((sq, sk), np.float32))
+    elif mask == "random":
+        keep = rng.random((sq, sk)) > 0.5
+        m = np.where(keep, rng.choice([1.0, -np.inf, 3.0], (sq, sk)), 0.0).astype(np.float32)
+    elif mask == "rowzero":
+        m = np.ones((sq, sk), np.float32)
+        m[2] = 0.0
+    elif mask == "short":
+        m = (rng.random(sq * sk // 3) > 0.3).astype(np.float32)
+    ref = oracle.sdpa(q, k, v, m)
+    got = dev.tensor_scaled_dot_product_attention(dev.tensor_new(q), dev.tensor_new(k), dev.tensor_new(v),
+                                                  dev.tensor_new(m) if m is not None else None).to_numpy()
+    assert got.shape == ref.shape
+    assert_rel(got, ref, F32_TOL)
+
+
+def test_scaled_dot_product_attention_errors(dev):
+    t = dev.tensor_new
+    q = t(np.zeros((2, 3, 8), np.float32))
+    with pytest.raises(BackendError) as e:   # head dims differ
+        dev.tensor_scaled_dot_product_attention(q, t(np.zeros((2, 3, 4), np.float32)), t(np.zeros((2, 3, 4), np.float32)))
+    assert e.value.variant == "ShapeMismatch"
+    with pytest.raises(BackendError) as e:   # batch / heads differ
+        dev.tensor_scaled_dot_product_attention(q, t(np.zeros((3, 3, 8), np.float32)), t(np.zeros((3, 3, 8), np.float32)))
+    assert e.value.variant == "ShapeMismatch"
+    with pytest.raises(BackendError) as e:   # rank 1
+        v1 = t(np.zeros(8, np.float32))
+        dev.tensor_scaled_dot_product_attention(v1, v1, v1)
+    assert e.value.variant == "ShapeMismatch"
+    # no keys: zeros of [.., seq_q, d_v]
+    out = dev.tensor_scaled_dot_product_attention(q, t(np.zeros((2, 0, 8), np.float32)),
+                                                  t(np.zeros((2, 0, 5), np.float32))).to_numpy()
+    assert out.shape == (2, 3, 5) and np.all(out == 0)

@@ -239,3 +239,59 @@ def test_q4_k_m_type_plan_for_tinyllama():
     assert oracle.q4_k_m_type(22, -1, "output") == 14
     # the 4-layer toy models of the GPU tests: i < 0 never, i >= 3, (i - 0) % 3 == 2
     assert [oracle.q4_k_m_type(4, i, "attn_v") for i in range(4)] == [12, 12, 14, 14]
+
+
+def test_sdpa_with_causal_ones_mask_is_the_chatbot_chain():
+    """tlo_sdpa (device_impl.rs:775-872) with a lower-triangular ones mask and one KV head per
+    query head equals the chatbot's attention chain with the causal mask (pinned above, and
+    against the literal op chain in test_oracle.py) bit for bit: the scale is 1/sqrt(64) =
+    0.125 exactly, -1e9 and -inf both vanish in exp, and every sum runs in the same order."""
+    rng = np.random.default_rng(31)
+    sl, nh, hd = 7, 3, 64
+    q = rng.standard_normal((sl, nh, hd)).astype(np.float32)
+    kc = rng.standard_normal((nh, sl, hd)).astype(np.float32)
+    vc = rng.standard_normal((nh, sl, hd)).astype(np.float32)
+    chain = oracle.attention(q, kc, vc, 0.125, True).reshape(sl, nh, hd)
+    mask = np.tril(np.ones((sl, sl), np.float32))
+    got = oracle.sdpa(q.transpose(1, 0, 2), kc, vc, mask)
+    assert np.array_equal(got.transpose(1, 0, 2).view(np.uint32), chain.view(np.uint32))
+
+
+def _sdpa64(q, k, v, keep=None):
+    s = q.astype(np.float64) @ np.swapaxes(k.astype(np.float64), -1, -2) / np.sqrt(q.shape[-1])
+    if keep is not None:
+        s = np.where(keep, s, -np.inf)
+    p = np.exp(s - s.max(-1, keepdims=True))
+    return (p / p.sum(-1, keepdims=True)) @ v.astype(np.float64)
+
+
+def test_sdpa_closed_forms_and_mask_rule():
+    rng = np.random.default_rng(32)
+    for shape_q, sk, dv in [((2, 3, 5, 16), 9, 24), ((4, 6, 32), 6, 32), ((5, 8), 11, 3)]:
+        q = rng.standard_normal(shape_q).astype(np.float32)
+        k = rng.standard_normal(shape_q[:-2] + (sk, shape_q[-1])).astype(np.float32)
+        v = rng.standard_normal(shape_q[:-2] + (sk, dv)).astype(np.float32)
+        out = oracle.sdpa(q, k, v)
+        assert out.shape == shape_q[:-1] + (dv,)
+        np.testing.assert_allclose(out, _sdpa64(q, k, v), rtol=1e-5, atol=1e-5)
+        # mask == 0 drops a key (each row keeps at least one); other values change nothing
+        sq = shape_q[-2]
+        keep = rng.random((sq, sk)) > 0.4
+        keep[:, 0] = True
+        mask = np.where(keep, rng.choice([1.0, -np.inf, 5.0, np.nan], (sq, sk)), 0.0).astype(np.float32)
+        np.testing.assert_allclose(oracle.sdpa(q, k, v, mask), _sdpa64(q, k, v, keep), rtol=1e-5, atol=1e-5)
+        assert np.array_equal(oracle.sdpa(q, k, v, np.ones((sq, sk), np.float32)), out)
+        # a fully masked row gives every key the same weight: the mean of V
+        full = mask.copy()
+        full[0] = 0.0
+        got = oracle.sdpa(q, k, v, full)
+        np.testing.assert_allclose(got[..., 0, :], v.astype(np.float64).mean(-2), rtol=1e-5, atol=1e-6)
+        # a mask shorter than seq_q * seq_k masks only the entries it holds
+        short = np.zeros(sk, np.float32)       # row 0 fully masked, the rest unmasked
+        got = oracle.sdpa(q, k, v, short)
+        np.testing.assert_allclose(got[..., 1:, :], out[..., 1:, :], rtol=0, atol=0)
+    # one key: the output is that key's V row
+    q = rng.standard_normal((2, 4, 8)).astype(np.float32)
+    k = rng.standard_normal((2, 1, 8)).astype(np.float32)
+    v = rng.standard_normal((2, 1, 5)).astype(np.float32)
+    assert np.array_equal(oracle.sdpa(q, k, v), np.repeat(v, 4, axis=1))

@@ -1252,3 +1252,155 @@ extern "C" tl_hip_tensor* tl_hip_attention_prefill(const tl_hip_tensor* qh, cons
     }
     return H(o);
 }
+
+// ------------------------------------------------- scaled dot-product attention op ----
+// IDevice::tensor_scaled_dot_product_attention with the tl_cpu semantics
+// (crates/tl_cpu/src/device_impl.rs:775-872): per (slice, query row), scores
+// s_j = (q . k_j) * (1 / sqrt(d_k)); where a mask is given, s_j = -1e9 when the mask's flat
+// element i * seq_k + j exists and equals 0 (the same [seq_q, seq_k] mask for every slice);
+// softmax over j (max, exp, sum, divide); out = sum_j p_j v_j.  One workgroup per query row:
+// the q row sits in LDS, one wavefront forms each score (lanes over d, DPP reduction) into the
+// row's slice of a score workspace, the workgroup reduces max and sum, normalises in place,
+// and each thread accumulates output columns over the keys in key order.
+__device__ __forceinline__ float sdpa_wmax(float v) {
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, 64));
+    return v;
+}
+
+__device__ __forceinline__ float sdpa_wsum(float v) {
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off, 64);
+    return v;
+}
+
+__global__ __launch_bounds__(256) void k_sdpa(const float* __restrict__ q, const float* __restrict__ k,
+                                              const float* __restrict__ v, const float* __restrict__ mask,
+                                              int64_t mask_len, float* __restrict__ out, float* __restrict__ sc,
+                                              int64_t sq, int64_t sk, int dk, int dv, float scale) {
+    extern __shared__ float qs[];  // [dk]
+    __shared__ float red[4];
+    const int64_t row = blockIdx.x;  // slice * sq + i
+    const int64_t slice = row / sq, i = row - slice * sq;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const float* kb = k + slice * sk * dk;
+    const float* vb = v + slice * sk * dv;
+    float* s = sc + row * sk;
+    for (int d = tid; d < dk; d += 256) qs[d] = q[row * dk + d];
+    __syncthreads();
+    for (int64_t j = wave; j < sk; j += 4) {
+        const float* kr = kb + j * dk;
+        float p = 0.f;
+        for (int d = lane; d < dk; d += 64) p = fmaf(qs[d], kr[d], p);
+        p = sdpa_wsum(p);
+        if (lane == 0) {
+            float x = p * scale;
+            const int64_t mi = i * sk + j;
+            if (mask && mi < mask_len && mask[mi] == 0.0f) x = -1e9f;
+            s[j] = x;
+        }
+    }
+    __syncthreads();
+    float mx = -INFINITY;
+    for (int64_t j = tid; j < sk; j += 256) mx = fmaxf(mx, s[j]);
+    mx = sdpa_wmax(mx);
+    if (lane == 0) red[wave] = mx;
+    __syncthreads();
+    mx = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+    __syncthreads();
+    float sum = 0.f;
+    for (int64_t j = tid; j < sk; j += 256) {
+        const float e = expf(s[j] - mx);
+        s[j] = e;
+        sum += e;
+    }
+    sum = sdpa_wsum(sum);
+    if (lane == 0) red[wave] = sum;
+    __syncthreads();
+    sum = (red[0] + red[1]) + (red[2] + red[3]);
+    for (int64_t j = tid; j < sk; j += 256) s[j] = s[j] / sum;
+    __syncthreads();
+    for (int d = tid; d < dv; d += 256) {
+        float acc = 0.f;
+        for (int64_t j = 0; j < sk; j++) acc = fmaf(s[j], vb[j * dv + d], acc);
+        out[row * dv + d] = acc;
+    }
+}
+
+extern "C" tl_hip_tensor* tl_hip_tensor_scaled_dot_product_attention(const tl_hip_tensor* qh, const tl_hip_tensor* kh,
+                                                                     const tl_hip_tensor* vh,
+                                                                     const tl_hip_tensor* maskh) {
+    if (!qh || !kh || !vh) {
+        set_error(TL_HIP_ERR_NULL, "NullPointerError: q, k or v");
+        return nullptr;
+    }
+    if (!state()) return nullptr;
+    const Tensor* q = reinterpret_cast<const Tensor*>(qh);
+    const Tensor* k = reinterpret_cast<const Tensor*>(kh);
+    const Tensor* v = reinterpret_cast<const Tensor*>(vh);
+    const Tensor* mk = reinterpret_cast<const Tensor*>(maskh);
+    if (q->dtype != TL_HIP_F32 || k->dtype != TL_HIP_F32 || v->dtype != TL_HIP_F32 ||
+        (mk && mk->dtype != TL_HIP_F32)) {
+        set_error(TL_HIP_ERR_TYPE, "TypeMismatch: q, k, v and mask must be f32");
+        return nullptr;
+    }
+    const int r = q->rank;
+    if (r < 2 || r > 4 || k->rank != r || v->rank != r) {
+        set_error(TL_HIP_ERR_SHAPE, "ShapeMismatch: q, k, v must share a rank of 2, 3 or 4 ([batch, heads,] seq, dim)");
+        return nullptr;
+    }
+    int64_t slices = 1;
+    for (int d = 0; d < r - 2; d++) {
+        if (k->shape[d] != q->shape[d] || v->shape[d] != q->shape[d]) {
+            set_error(TL_HIP_ERR_SHAPE, "ShapeMismatch: q, k, v differ in batch / head dimensions");
+            return nullptr;
+        }
+        slices *= q->shape[d];
+    }
+    const int64_t sq = q->shape[r - 2], dk = q->shape[r - 1], sk = k->shape[r - 2], dv = v->shape[r - 1];
+    if (k->shape[r - 1] != dk || v->shape[r - 2] != sk) {
+        set_error(TL_HIP_ERR_SHAPE, "ShapeMismatch: k [.., %lld, %lld] and v [.., %lld, %lld] for q [.., %lld, %lld]",
+                  (long long)sk, (long long)k->shape[r - 1], (long long)v->shape[r - 2], (long long)dv,
+                  (long long)sq, (long long)dk);
+        return nullptr;
+    }
+    if (dk > 16384 || dv > 65536 || slices * sq > INT32_MAX) {
+        set_error(TL_HIP_ERR_ARG, "ArgumentError: head dimension or row count too large");
+        return nullptr;
+    }
+    int64_t oshape[4];
+    for (int d = 0; d < r - 2; d++) oshape[d] = q->shape[d];
+    oshape[r - 2] = sq;
+    oshape[r - 1] = dv;
+    Tensor* o = tensor_alloc(oshape, r);
+    if (!o) return nullptr;
+    hipStream_t s = cur_stream();
+    if (o->numel == 0) return H(o);
+    if (sk == 0) {  // no keys: every output sum is empty
+        hipError_t e = hipMemsetAsync(o->data, 0, o->numel * 4, s);
+        if (e != hipSuccess) {
+            hip_fail(e, "hipMemsetAsync");
+            tensor_drop(o);
+            return nullptr;
+        }
+        return H(o);
+    }
+    float* ws = (float*)dev_alloc((size_t)(slices * sq) * sk * 4);
+    if (!ws) {
+        tensor_drop(o);
+        return nullptr;
+    }
+    // 1 / sqrt(d_k) as tl_cpu computes it in f32 (device_impl.rs:800)
+    const float scale = 1.0f / sqrtf((float)dk);
+    k_sdpa<<<(unsigned)(slices * sq), 256, (size_t)(dk > 0 ? dk : 1) * 4, s>>>(
+        q->f32(), k->f32(), v->f32(), mk ? mk->f32() : nullptr, mk ? mk->numel : 0, o->f32(), ws, sq, sk, (int)dk,
+        (int)dv, scale);
+    hipError_t e = hipGetLastError();
+    dev_free(ws);
+    if (e != hipSuccess) {
+        hip_fail(e, "sdpa launch");
+        tensor_drop(o);
+        return nullptr;
+    }
+    return H(o);
+}

@@ -261,6 +261,12 @@ class HipDevice:
     def fused_bias_gelu(self, x, bias):
         return self._wrap(self.lib.tl_hip_fused_bias_gelu(x.handle, bias.handle))
 
+    def tensor_scaled_dot_product_attention(self, q, k, v, mask=None):
+        """IDevice::tensor_scaled_dot_product_attention (device.rs:180-186): softmax(q k^T /
+        sqrt(d_k), mask == 0 -> -1e9) v over [batch, heads,] seq, dim tensors."""
+        return self._wrap(self.lib.tl_hip_tensor_scaled_dot_product_attention(
+            q.handle, k.handle, v.handle, mask.handle if mask is not None else None))
+
     # -- decode attention over a KV cache
     def attention_decode(self, q, k, v, length, scale):
         return self._wrap(self.lib.tl_hip_attention_decode(q.handle, k.handle, v.handle, length, scale))
