@@ -180,6 +180,17 @@ int tl_hip_launch_quant_matvec(const tl_hip_qtensor* w, const float* x, float* y
                                void* stream);
 int tl_hip_launch_quant_gemm(const tl_hip_qtensor* w, const float* x, float* y, int64_t m,
                              int use_f16_mfma, void* stream);
+/* Allocation-free variant of tl_hip_launch_quant_gemm (no counterpart in the reference): for
+ * callers that cannot allocate device memory -- code under hipGraph capture, serving loops
+ * that forbid hipMalloc.  Same arguments and results; calls no hipMalloc / hipFree.  The f16
+ * MFMA path keeps its workspace (X converted to f16: m * k * 2 bytes rounded up to 256, then
+ * the split-K partial tiles of short inputs) in a fixed 32 MiB device array per GPU, held until
+ * the process ends; calls needing more are ArgumentError, as are weights that need an f16 copy
+ * for the MFMA path (Q6_K, and Q4_K before its first f16 GEMM through an allocating entry).
+ * The f32 path (use_f16_mfma = 0) needs no workspace.  Every call on a GPU shares that array:
+ * calls on one stream are ordered, calls that overlap on different streams race. */
+int tl_hip_launch_quant_gemm_noalloc(const tl_hip_qtensor* w, const float* x, float* y, int64_t m,
+                                     int use_f16_mfma, void* stream);
 /* Tile plan of the calling thread's last f16-MFMA GEMM launch: rows and columns of one
  * workgroup's output tile and the number of K splits (1 = unsplit).  Instrumentation for the
  * parity tests (which kernel variant ran); no reference counterpart. */

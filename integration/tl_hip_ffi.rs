@@ -142,6 +142,14 @@ extern "C" {
         use_f16_mfma: i32,
         stream: *mut c_void,
     ) -> i32;
+    pub fn tl_hip_launch_quant_gemm_noalloc(
+        w: *const tl_hip_qtensor,
+        x: *const f32,
+        y: *mut f32,
+        m: i64,
+        use_f16_mfma: i32,
+        stream: *mut c_void,
+    ) -> i32;
     pub fn tl_hip_debug_last_gemm_plan(
         tile_m: *mut i32,
         tile_n: *mut i32,

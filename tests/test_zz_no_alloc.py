@@ -1,0 +1,88 @@
+"""tl_hip_launch_quant_gemm_noalloc (the allocation-free GEMM entry) against the allocating
+tl_hip_launch_quant_gemm on the same inputs, called through the C ABI: two calls in a row,
+the second with a smaller input (short-input tiles with split-K partials in the scratch), and
+the size and type limits of its fixed scratch."""
+import ctypes as C
+
+import numpy as np
+import pytest
+
+import oracle
+from tl_amd import GGML_Q4_0, GGML_Q4_K, GGML_Q6_K, GGML_Q8_0, QTensor, _lib
+from tl_amd.quant import random_q4_0_blocks, random_q4_k_blocks, random_q6_k_blocks, random_q8_0_blocks
+
+pytestmark = pytest.mark.gpu
+
+_GEN = {GGML_Q4_0: random_q4_0_blocks, GGML_Q8_0: random_q8_0_blocks}
+
+
+def _plan(lib):
+    v = [C.c_int32() for _ in range(3)]
+    assert lib.tl_hip_debug_last_gemm_plan(*[C.byref(x) for x in v]) == 0
+    return tuple(x.value for x in v)
+
+
+def _run(dev, lib, entry, hw, x, n):
+    m = x.shape[0]
+    xt = dev.tensor_new(x)
+    yt = dev.tensor_new(np.full((m, n), np.nan, np.float32))
+    rc = entry(hw, C.c_void_p(xt.data_ptr), C.c_void_p(yt.data_ptr), m, 1, None)
+    assert rc == 0, lib.tl_hip_last_error()
+    return yt.to_numpy(), _plan(lib)
+
+
+@pytest.mark.parametrize("t", [GGML_Q4_0, GGML_Q8_0])
+def test_noalloc_gemm_equals_the_allocating_entry(dev, t):
+    lib = _lib.load()
+    rng = np.random.default_rng(0x71580000 + t)
+    n, k = 4096, 4096
+    raw = _GEN[t](rng, n, k)
+    w = QTensor(t, raw, (n, k))
+    hw = w.upload(lib)
+    for m in (512, 16):   # the second call smaller: 32-row tiles, K split 16 ways
+        x = rng.standard_normal((m, k)).astype(np.float32)
+        want, want_plan = _run(dev, lib, lib.tl_hip_launch_quant_gemm, hw, x, n)
+        got, got_plan = _run(dev, lib, lib.tl_hip_launch_quant_gemm_noalloc, hw, x, n)
+        assert got_plan == want_plan
+        assert np.array_equal(got.view(np.uint32), want.view(np.uint32)), f"m={m}: results differ"
+        ref = oracle.qtensor_matmul(x, raw, t, n)
+        err = float(np.max(np.abs(got - ref)) / np.max(np.abs(ref)))
+        assert err <= 1e-2, f"m={m}: max-rel-err {err:.2e} vs the oracle"
+    assert _plan(lib)[2] > 1  # the short call did use split-K partials in the scratch
+
+
+def test_noalloc_gemm_limits(dev):
+    lib = _lib.load()
+    rng = np.random.default_rng(0x71580100)
+    k = 4096
+    w = QTensor(GGML_Q4_0, random_q4_0_blocks(rng, 256, k), (256, k))
+    hw = w.upload(lib)
+    big = dev.tensor_new(np.zeros((4100, k), np.float32))   # 4100 x 4096 f16 > 32 MiB
+    y = dev.tensor_new(np.zeros((4100, 256), np.float32))
+    lib.tl_hip_clear_error()
+    assert lib.tl_hip_launch_quant_gemm_noalloc(hw, C.c_void_p(big.data_ptr), C.c_void_p(y.data_ptr), 4100, 1,
+                                                None) == 8
+    assert b"scratch" in lib.tl_hip_last_error()
+    # Q6_K needs an f16 copy of the weight for the MFMA path: rejected; the f32 path runs
+    w6 = QTensor(GGML_Q6_K, random_q6_k_blocks(rng, 256, k), (256, k))
+    h6 = w6.upload(lib)
+    x = rng.standard_normal((8, k)).astype(np.float32)
+    xt = dev.tensor_new(x)
+    yt = dev.tensor_new(np.zeros((8, 256), np.float32))
+    assert lib.tl_hip_launch_quant_gemm_noalloc(h6, C.c_void_p(xt.data_ptr), C.c_void_p(yt.data_ptr), 8, 1,
+                                                None) == 8
+    assert lib.tl_hip_launch_quant_gemm_noalloc(h6, C.c_void_p(xt.data_ptr), C.c_void_p(yt.data_ptr), 8, 0,
+                                                None) == 0
+    ref = oracle.qtensor_matmul(x, w6.data, GGML_Q6_K, 256)
+    assert float(np.max(np.abs(yt.to_numpy() - ref)) / np.max(np.abs(ref))) <= 1e-4
+    # Q4_K takes the MFMA path once its per-unit scales exist (built by an allocating f16 call)
+    w4 = QTensor(GGML_Q4_K, random_q4_k_blocks(rng, 256, k), (256, k))
+    h4 = w4.upload(lib)
+    assert lib.tl_hip_launch_quant_gemm_noalloc(h4, C.c_void_p(xt.data_ptr), C.c_void_p(yt.data_ptr), 8, 1,
+                                                None) == 8
+    assert lib.tl_hip_launch_quant_gemm(h4, C.c_void_p(xt.data_ptr), C.c_void_p(yt.data_ptr), 8, 1, None) == 0
+    want = yt.to_numpy()
+    yt2 = dev.tensor_new(np.zeros((8, 256), np.float32))
+    assert lib.tl_hip_launch_quant_gemm_noalloc(h4, C.c_void_p(xt.data_ptr), C.c_void_p(yt2.data_ptr), 8, 1,
+                                                None) == 0
+    assert np.array_equal(yt2.to_numpy(), want)

@@ -578,14 +578,17 @@ __global__ __launch_bounds__(256) void k_splitk_sum(const float* __restrict__ pa
 // tile plan of the calling thread's last f16 GEMM launch (tl_hip_debug_last_gemm_plan)
 static thread_local int tls_plan[3] = {0, 0, 0};
 
-int launch_gemm_f16q(const QWeight* w, const _Float16* x16, float* y, int64_t m, const GemmEpi& ep,
-                     hipStream_t s) {
-    if (m < 1) return TL_HIP_OK;
-    if (w->nb % Q_KR != 0 || (ep.mode == GEMM_GLU16 && (w->n % 64 != 0))) {
-        set_error(TL_HIP_ERR_ARG, "ArgumentError: the f16 GEMM takes K in steps of 128 (SwiGLU output: N in steps "
-                  "of 64)");
-        return TL_HIP_ERR_ARG;
-    }
+namespace {
+// Launch plan of one f16 GEMM: row tile bm, wide (128 x 64) or narrow (x 32) tiles, tile count
+// and K splits.
+struct F16qPlan {
+    int bm;
+    bool wide;
+    int64_t tiles, nsp;
+};
+}  // namespace
+
+static F16qPlan plan_f16q(const QWeight* w, int64_t m, const GemmEpi& ep, const float* y) {
     // 128 x 64 tiles when that gives at least two workgroups per CU, else 128 x 32 (twice
     // the workgroups; measured at M = 512: 2048 x 2048 18.7 -> 15.5 us, 4096 x 4096
     // 41.0 -> 37.3 us, while 11008 x 4096 is faster with the wide tile, 84.5 vs 101.7 us).
@@ -613,13 +616,41 @@ int launch_gemm_f16q(const QWeight* w, const _Float16* x16, float* y, int64_t m,
         nsp = std::min<int64_t>(std::min<int64_t>(cdiv(512, tiles), iters), 16);
         nsp = cdiv(iters, cdiv(iters, nsp));  // every split non-empty
     }
+    return F16qPlan{bm, wide, tiles, nsp};
+}
+
+// part_ws / noalloc: the split-K partials go to the caller's workspace and nothing is
+// allocated (weights that need an f16 copy are then rejected); otherwise the allocator
+// provides the workspace.
+int launch_gemm_f16q(const QWeight* w, const _Float16* x16, float* y, int64_t m, const GemmEpi& ep,
+                     hipStream_t s, bool noalloc, float* part_ws) {
+    if (m < 1) return TL_HIP_OK;
+    if (w->nb % Q_KR != 0 || (ep.mode == GEMM_GLU16 && (w->n % 64 != 0))) {
+        set_error(TL_HIP_ERR_ARG, "ArgumentError: the f16 GEMM takes K in steps of 128 (SwiGLU output: N in steps "
+                  "of 64)");
+        return TL_HIP_ERR_ARG;
+    }
+    const bool needs_w16 = (w->ggml_type == TL_HIP_GGML_Q4_K && !w->us) || w->ggml_type == TL_HIP_GGML_Q6_K;
+    if (noalloc && needs_w16) {
+        set_error(TL_HIP_ERR_ARG, "ArgumentError: a %s weight needs an f16 copy for the MFMA GEMM, which the "
+                  "allocation-free entry cannot make", ggml_type_name(w->ggml_type));
+        return TL_HIP_ERR_ARG;
+    }
+    constexpr int BM = 128;
+    const F16qPlan plan = plan_f16q(w, m, ep, y);
+    const int bm = plan.bm;
+    const bool wide = plan.wide;
+    const int64_t tiles = plan.tiles, nsp = plan.nsp;
     tls_plan[0] = bm;
     tls_plan[1] = wide ? 64 : 32;
     tls_plan[2] = (int)nsp;
     float* part = nullptr;
     if (nsp > 1) {
-        part = static_cast<float*>(dev_alloc_on((size_t)nsp * m * w->n * sizeof(float), s));
-        if (!part) return TL_HIP_ERR_ALLOC;
+        part = noalloc ? part_ws : static_cast<float*>(dev_alloc_on((size_t)nsp * m * w->n * sizeof(float), s));
+        if (!part) {
+            if (noalloc) set_error(TL_HIP_ERR_ARG, "ArgumentError: no workspace for the split-K partials");
+            return noalloc ? TL_HIP_ERR_ARG : TL_HIP_ERR_ALLOC;
+        }
     }
     const GemmEpi pe = nsp > 1 ? GemmEpi{GEMM_PLAIN, nullptr, nullptr, 0} : ep;
     float* const out = nsp > 1 ? part : y;
@@ -656,7 +687,7 @@ int launch_gemm_f16q(const QWeight* w, const _Float16* x16, float* y, int64_t m,
     } else {
         gemm(std::integral_constant<int, TL_HIP_GGML_Q8_0>{}, w->qs, w->d);
     }
-    if (part) dev_free_on(part, s);  // freed on s: reused at once only by later work on s
+    if (part && !noalloc) dev_free_on(part, s);  // freed on s: reused at once only by later work on s
     hipError_t e = hipGetLastError();
     return e == hipSuccess ? TL_HIP_OK : hip_fail(e, "quant gemm launch");
 }
@@ -771,6 +802,89 @@ int launch_matmul_f32(const float* a, const float* b, float* c, int64_t batch, i
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return hip_fail(e, "matmul launch");
     return TL_HIP_OK;
+}
+
+
+// ------------------------------------------------------ allocation-free GEMM entry ----
+// The workspace of tl_hip_launch_quant_gemm_noalloc: the f16 copy of X (m * k halves, rounded
+// up to 256 bytes) followed by the split-K partial tiles (nsp * m * n floats).  One array per
+// GPU, held until the process ends; its device address is looked up once per device.
+constexpr size_t NOALLOC_SCRATCH_BYTES = size_t(32) << 20;
+static __device__ __align__(256) uint8_t scratch[NOALLOC_SCRATCH_BYTES];
+
+static std::mutex g_scratch_mu;
+constexpr int SCRATCH_MAX_DEVICES = 64;
+static uint8_t* g_scratch_ptr[SCRATCH_MAX_DEVICES] = {};
+
+// Device address of `scratch` on device dev (the host-side name is only a stand-in).
+static uint8_t* scratch_on(int dev) {
+    if (dev < 0 || dev >= SCRATCH_MAX_DEVICES) {
+        set_error(TL_HIP_ERR_DEVICE, "DeviceError: device %d outside the scratch table", dev);
+        return nullptr;
+    }
+    std::lock_guard<std::mutex> lk(g_scratch_mu);
+    if (!g_scratch_ptr[dev]) {
+        int cur = -1;
+        hipError_t e = hipGetDevice(&cur);
+        if (e == hipSuccess && cur != dev) e = hipSetDevice(dev);
+        void* p = nullptr;
+        if (e == hipSuccess) e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (cur >= 0 && cur != dev) (void)hipSetDevice(cur);
+        if (e != hipSuccess || !p) {
+            hip_fail(e != hipSuccess ? e : hipErrorInvalidSymbol, "hipGetSymbolAddress(scratch)");
+            return nullptr;
+        }
+        g_scratch_ptr[dev] = static_cast<uint8_t*>(p);
+    }
+    return g_scratch_ptr[dev];
+}
+
+extern "C" int tl_hip_launch_quant_gemm_noalloc(const tl_hip_qtensor* h, const float* x, float* y, int64_t m,
+                                                int use_f16_mfma, void* stream) {
+    if (!h || !x || !y) {
+        set_error(TL_HIP_ERR_NULL, "NullPointerError: weight, x or y");
+        return TL_HIP_ERR_NULL;
+    }
+    DeviceState* st = state();
+    if (!st) return tl_hip_last_status();
+    const QWeight* w = reinterpret_cast<const QWeight*>(h);
+    hipStream_t s = stream ? (hipStream_t)stream : cur_stream();
+    if (m < 1) return TL_HIP_OK;
+    if (!use_f16_mfma || w->nb % Q_KR != 0) return launch_quant_gemm(w, x, y, m, s, 0);  // f32 path: no workspace
+    if ((reinterpret_cast<uintptr_t>(x) & 15) != 0) {
+        set_error(TL_HIP_ERR_ARG, "ArgumentError: x must be 16-byte aligned");
+        return TL_HIP_ERR_ARG;
+    }
+    const GemmEpi plain{GEMM_PLAIN, nullptr, nullptr, 0};
+    if (m > (int64_t)(NOALLOC_SCRATCH_BYTES / 2 / (size_t)w->k)) {
+        set_error(TL_HIP_ERR_ARG, "ArgumentError: %lld x %lld input exceeds the %zu MiB scratch of the allocation-free "
+                  "GEMM", (long long)m, (long long)w->k, NOALLOC_SCRATCH_BYTES >> 20);
+        return TL_HIP_ERR_ARG;
+    }
+    const size_t x16_bytes = ((size_t)m * w->k * 2 + 255) & ~size_t(255);
+    const F16qPlan plan = plan_f16q(w, m, plain, y);
+    const size_t part_bytes = plan.nsp > 1 ? (size_t)plan.nsp * m * w->n * 4 : 0;
+    if (x16_bytes + part_bytes > NOALLOC_SCRATCH_BYTES) {
+        set_error(TL_HIP_ERR_ARG, "ArgumentError: the call needs %zu bytes of scratch (X in f16 + split-K partials), "
+                  "the allocation-free GEMM has %zu MiB", x16_bytes + part_bytes, NOALLOC_SCRATCH_BYTES >> 20);
+        return TL_HIP_ERR_ARG;
+    }
+    if (w->ggml_type == TL_HIP_GGML_Q6_K || (w->ggml_type == TL_HIP_GGML_Q4_K && !w->us)) {
+        set_error(TL_HIP_ERR_ARG, "ArgumentError: a %s weight needs an f16 copy for the MFMA GEMM, which the "
+                  "allocation-free entry cannot make (use_f16_mfma = 0 takes the f32 path)",
+                  ggml_type_name(w->ggml_type));
+        return TL_HIP_ERR_ARG;
+    }
+    note_stream(s);
+    uint8_t* base = scratch_on(st->device);
+    if (!base) return tl_hip_last_status();
+    _Float16* x16 = reinterpret_cast<_Float16*>(base);
+    int rc = launch_x_to_f16q(x, x16, m, w->k, f16q_order(w->ggml_type), s);
+    if (rc == TL_HIP_OK)
+        rc = launch_gemm_f16q(w, x16, y, m, plain, s, true, reinterpret_cast<float*>(base + x16_bytes));
+    if (rc) return rc;
+    hipError_t e = hipGetLastError();
+    return e == hipSuccess ? TL_HIP_OK : hip_fail(e, "quant gemm launch");
 }
 
 }  // namespace tlhip

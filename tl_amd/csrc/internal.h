@@ -182,8 +182,9 @@ __host__ __device__ inline int64_t f16q_index(int64_t r, int64_t e, int64_t k, i
 int f16q_order(int ggml_type);  // the operand order the f16 GEMM of this weight type reads
 int launch_x_to_f16q(const float* x, _Float16* x16, int64_t m, int64_t k, int order, hipStream_t s);
 // K a multiple of 128 (TL_HIP_ERR_ARG otherwise); GLU16 also needs N a multiple of 64.
+// noalloc: split-K partials in part_ws (sized by the caller), nothing allocated.
 int launch_gemm_f16q(const QWeight* w, const _Float16* x16, float* y, int64_t m, const GemmEpi& ep,
-                     hipStream_t s);
+                     hipStream_t s, bool noalloc = false, float* part_ws = nullptr);
 // Q4_K weights: builds w->us (4 bytes per 32 weights) on stream s, after which the f16 GEMM
 // dequantizes them in registers like Q4_0 instead of through an f16 copy per call.
 int q4k_build_unit_scales(QWeight* w, hipStream_t s);
