@@ -252,46 +252,143 @@ def bench_attention(dev, reps=20, hq=32, hkv=8, d=128, min_bytes=300 << 20):
     return rows
 
 
-def cpu_baseline(cfg, L):
-    """Faithful tl_cpu decode cost for one token at cache length L: per layer the seven
-    linears as matmul_impl over the cached transposed f32 weights (system.rs:193-222,
-    tensor.rs:1284-1305), the attention composition, RMSNorm / RoPE / SiLU; plus the LM head.
-    One layer is timed and multiplied by n_layers."""
-    import oracle
-    from tl_amd.llama import SLOTS, synthetic_linear
+def _host_cpu():
+    """Host CPU model, the cores this process may use, and the core the CPU legs are pinned to."""
+    model = "unknown"
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    model = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    cores = sorted(os.sched_getaffinity(0))
+    return {"cpu_model": model, "nproc": len(cores), "os_cpu_count": os.cpu_count(), "pinned_core": cores[0]}
 
+
+def _cpu_time(fn, reps=1):
+    t0 = time.perf_counter()
+    for _ in range(reps):
+        fn()
+    return (time.perf_counter() - t0) / reps
+
+
+def cpu_baseline(cfg, L):
+    """The reference's tl_cpu path restated by the oracle, on one host core (the process is
+    pinned to it first; tl_cpu is single-threaded and scalar).  Legs:
+      * decode token: per layer the seven linears as matmul_impl over the cached transposed f32
+        weights (system.rs:193-222, tensor.rs:1284-1305), RMSNorm with real norm weights, RoPE,
+        the chatbot's attention chain at cache length L (transpose / repeat_interleave /
+        matmul_4d / scale / softmax / matmul_4d, chatbot.tl:63-87), SiLU, mul, residual adds;
+        one layer timed and multiplied by n_layers, plus the LM head;
+      * the configs[0] matvec (4096 x 4096, Q4_0 and Q8_0): cold = dequantize + transpose +
+        matmul_impl (the first tl_qtensor_matmul of a weight, system.rs:193-221), steady = the
+        cached transposed matmul only;
+      * the configs[1] row ops at full size;
+      * one configs[2] GEMM (M = 512, 4096 x 4096, Q4_0) on the first 16 rows of X, scaled x32;
+      * the configs[3] attention at L = 512, B = 1 through the literal op chain.
+    Returns (tok/s, the cpu_baseline object without its "value")."""
+    import oracle
+    from tl_amd.llama import SLOTS, synthetic_linear, synthetic_norm
+    from tl_amd.quant import random_q4_0_blocks, random_q8_0_blocks
+
+    host = _host_cpu()
+    allowed = os.sched_getaffinity(0)
+    os.sched_setaffinity(0, {host["pinned_core"]})
     rng = np.random.default_rng(5)
-    D, H, KV, hd, F = cfg.d_model, cfg.n_heads, cfg.n_kv_heads, cfg.head_dim, cfg.ffn_dim
+    legs = {}
+    # -- decode token (configs[4] shape)
+    D, H, KV, hd = cfg.d_model, cfg.n_heads, cfg.n_kv_heads, cfg.head_dim
     wts = {}
     for w in SLOTS + ["output"]:
         n, k = cfg.linear_shape(w)
-        raw = synthetic_linear(cfg, 99, 0 if w != "output" else -1, w)
+        raw = synthetic_linear(cfg, 1234, 0 if w != "output" else -1, w)
         wts[w] = np.ascontiguousarray(oracle.dequantize(2, raw, n * k).reshape(n, k).T)
     x = rng.standard_normal((1, D)).astype(np.float32)
-    nw = np.ones(D, np.float32)
-    cos_t = oracle.rope_table(1, hd, 10000.0)
-    sin_t = oracle.rope_table(1, hd, 10000.0, sin=True)
-    kc = rng.standard_normal((KV, L, hd)).astype(np.float32)
-    vc = rng.standard_normal((KV, L, hd)).astype(np.float32)
-    t0 = time.perf_counter()
-    h = oracle.rms_norm(x, nw, 1e-5)
-    q = oracle.matmul(h, wts["attn_q"])
-    k = oracle.matmul(h, wts["attn_k"])
-    oracle.matmul(h, wts["attn_v"])
-    q = oracle.apply_rope(q.reshape(H, hd), cos_t, sin_t)
-    oracle.apply_rope(k.reshape(KV, hd), cos_t, sin_t)
-    ao = oracle.attention(q.reshape(1, H, hd), kc, vc, 0.125, False)
-    x2 = oracle.binop("add", x, oracle.matmul(ao, wts["attn_output"]))
-    h2 = oracle.rms_norm(x2, nw, 1e-5)
-    g = oracle.silu(oracle.matmul(h2, wts["ffn_gate"]))
-    u = oracle.matmul(h2, wts["ffn_up"])
-    oracle.binop("add", x2, oracle.matmul(oracle.binop("mul", g, u), wts["ffn_down"]))
-    t_layer = time.perf_counter() - t0
-    t0 = time.perf_counter()
-    oracle.matmul(oracle.rms_norm(x2, nw, 1e-5), wts["output"])
-    t_head = time.perf_counter() - t0
+    an, fn = synthetic_norm(cfg, 1234, 0, 0), synthetic_norm(cfg, 1234, 0, 1)
+    cos_t = oracle.rope_table(L + 1, hd, cfg.rope_theta)
+    sin_t = oracle.rope_table(L + 1, hd, cfg.rope_theta, sin=True)
+    kc = rng.standard_normal((1, KV, L, hd)).astype(np.float32)
+    vc = rng.standard_normal((1, KV, L, hd)).astype(np.float32)
+
+    def attn_chain(q4, k4, v4, kcache, vcache, sp):
+        # chatbot.tl:60-87 for sl = 1 at start position sp
+        cs, ss = oracle.narrow(cos_t, 0, sp, 1), oracle.narrow(sin_t, 0, sp, 1)
+        qr, kr = oracle.apply_rope(q4, cs, ss), oracle.apply_rope(k4, cs, ss)
+        k_tot = oracle.cat(kcache, oracle.transpose(kr, 1, 2), 2)
+        v_tot = oracle.cat(vcache, oracle.transpose(v4, 1, 2), 2)
+        kw = oracle.repeat_interleave(k_tot, q4.shape[2] // k4.shape[2], 1)
+        vw = oracle.repeat_interleave(v_tot, q4.shape[2] // k4.shape[2], 1)
+        sm = oracle.scale(oracle.matmul(oracle.transpose(qr, 1, 2), oracle.transpose(kw, 2, 3)),
+                          1.0 / np.sqrt(q4.shape[3]))
+        return oracle.transpose(oracle.matmul(oracle.softmax(sm, 3), vw), 1, 2)
+
+    def layer():
+        h = oracle.rms_norm(x, an, cfg.eps)
+        q = oracle.matmul(h, wts["attn_q"]).reshape(1, 1, H, hd)
+        k = oracle.matmul(h, wts["attn_k"]).reshape(1, 1, KV, hd)
+        v = oracle.matmul(h, wts["attn_v"]).reshape(1, 1, KV, hd)
+        ao = attn_chain(q, k, v, kc, vc, L - 1).reshape(1, D)
+        x2 = oracle.binop("add", x, oracle.matmul(ao, wts["attn_output"]))
+        h2 = oracle.rms_norm(x2, fn, cfg.eps)
+        g = oracle.silu(oracle.matmul(h2, wts["ffn_gate"]))
+        u = oracle.matmul(h2, wts["ffn_up"])
+        return oracle.binop("add", x2, oracle.matmul(oracle.binop("mul", g, u), wts["ffn_down"]))
+
+    t_layer = _cpu_time(layer)
+    x2 = layer()
+    t_head = _cpu_time(lambda: oracle.matmul(oracle.rms_norm(x2, an, cfg.eps), wts["output"]))
     tok_s = 1.0 / (cfg.n_layers * t_layer + t_head)
-    return tok_s, t_layer, t_head
+    legs["decode_token"] = {"s": round(cfg.n_layers * t_layer + t_head, 3), "layer_s": round(t_layer, 3),
+                            "lm_head_s": round(t_head, 3), "cache_len": L}
+    del wts
+    # -- configs[0]: 4096 x 4096 matvec, cold and steady
+    n = k = 4096
+    xv = rng.standard_normal((1, k)).astype(np.float32)
+    for t, name, gen in ((2, "Q4_0", random_q4_0_blocks), (8, "Q8_0", random_q8_0_blocks)):
+        raw = gen(np.random.default_rng(0x71510000), n, k)
+        cold = _cpu_time(lambda: oracle.qtensor_matmul(xv, raw, t, n, fast=False))
+        wt = np.ascontiguousarray(oracle.dequantize(t, raw, n * k).reshape(n, k).T)
+        steady = _cpu_time(lambda: oracle.matmul(xv, wt), reps=3)
+        legs[f"matvec_{name}_4096"] = {"cold_s": round(cold, 4), "steady_s": round(steady, 4),
+                                       "steady_gbs_f32_weights": round(n * k * 4 / steady / 1e9, 2)}
+        del wt
+    # -- configs[1]: row ops at full size
+    xr = rng.standard_normal((512, 4096)).astype(np.float32)
+    w1 = rng.uniform(0.5, 1.5, 4096).astype(np.float32)
+    xq = rng.standard_normal((512, 32, 128)).astype(np.float32)
+    c1, s1 = oracle.rope_table(512, 128, 10000.0), oracle.rope_table(512, 128, 10000.0, sin=True)
+    g1 = rng.standard_normal((512, 11008)).astype(np.float32)
+    u1 = rng.standard_normal((512, 11008)).astype(np.float32)
+    lg = (3.0 * rng.standard_normal((512, 32000))).astype(np.float32)
+    legs["row_ops"] = {
+        "rms_norm_512x4096_s": round(_cpu_time(lambda: oracle.rms_norm(xr, w1, 1e-5)), 4),
+        "apply_rope_512x32x128_s": round(_cpu_time(lambda: oracle.apply_rope(xq, c1, s1)), 4),
+        "silu_mul_512x11008_s": round(_cpu_time(lambda: oracle.binop("mul", oracle.silu(g1), u1)), 4),
+        "softmax_512x32000_s": round(_cpu_time(lambda: oracle.softmax(lg, -1)), 4),
+    }
+    del g1, u1, lg
+    # -- configs[2]: M = 512 GEMM, 4096 x 4096 Q4_0, rows 0..15 of X timed, x 32
+    raw = random_q4_0_blocks(np.random.default_rng(0x71520000), n, k)
+    wt = np.ascontiguousarray(oracle.dequantize(2, raw, n * k).reshape(n, k).T)
+    xg = rng.standard_normal((16, k)).astype(np.float32)
+    tg = _cpu_time(lambda: oracle.matmul(xg, wt)) * 32
+    legs["gemm_Q4_0_m512_4096"] = {"s": round(tg, 3), "sample": "rows 0..15 of X timed, scaled x 32",
+                                   "gflops": round(2 * 512 * n * k / tg / 1e9, 3)}
+    del wt
+    # -- configs[3]: decode attention L = 512, B = 1 (Hq 32, Hkv 8, D 128) through the op chain
+    La = 512
+    qa = rng.standard_normal((1, 1, 32, 128)).astype(np.float32)
+    ka = rng.standard_normal((1, 1, 8, 128)).astype(np.float32)
+    va = rng.standard_normal((1, 1, 8, 128)).astype(np.float32)
+    kca = rng.standard_normal((1, 8, La - 1, 128)).astype(np.float16).astype(np.float32)
+    vca = rng.standard_normal((1, 8, La - 1, 128)).astype(np.float16).astype(np.float32)
+    cos_t = oracle.rope_table(La, 128, 10000.0)
+    sin_t = oracle.rope_table(La, 128, 10000.0, sin=True)
+    legs["attention_L512_B1"] = {"s": round(_cpu_time(lambda: attn_chain(qa, ka, va, kca, vca, La - 1), reps=3), 5)}
+    os.sched_setaffinity(0, allowed)
+    return tok_s, {"host": host, "legs": legs}
 
 
 def bench_decode(dev, cfg, ggml_type, args, steps=None, variants=()):
@@ -451,14 +548,17 @@ def main():
 
     cpu = None
     if not args.no_cpu_baseline:
-        log("[bench] CPU baseline (oracle, 1 thread) ...")
+        log("[bench] CPU baseline (oracle, 1 pinned core) ...")
         L = args.prompt + args.warmup + args.steps // 2
-        cpu_tok_s, t_layer, t_head = cpu_baseline(cfg, L)
+        cpu_tok_s, extra = cpu_baseline(cfg, L)
+        leg = extra["legs"]["decode_token"]
         cpu = {"value": round(cpu_tok_s, 4), "unit": "tok/s", "cores": 1, "kind": "port",
-               "sample": f"one decode token at cache length {L}: 1 layer timed ({t_layer:.2f} s: 7 linears in "
-                         f"tl_cpu matmul_impl order over cached transposed f32 weights + attention + norms) x "
-                         f"{cfg.n_layers} + LM head ({t_head:.2f} s)"}
-        log(f"[bench] CPU {cpu_tok_s:.4f} tok/s")
+               "sample": f"one decode token at cache length {L}: 1 layer timed ({leg['layer_s']:.2f} s: 7 linears "
+                         f"in tl_cpu matmul_impl order over cached transposed f32 weights, the chatbot's "
+                         f"attention op chain, norms) x {cfg.n_layers} + LM head ({leg['lm_head_s']:.2f} s)",
+               **extra}
+        log(f"[bench] CPU {cpu_tok_s:.4f} tok/s on {extra['host']['cpu_model']} (core "
+            f"{extra['host']['pinned_core']} of {extra['host']['nproc']}); legs {json.dumps(extra['legs'])}")
 
     out = {
         "metric": "Q4_0 decode tok/s (batch 1)",
