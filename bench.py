@@ -47,10 +47,11 @@ def matvec_bytes(t, n=MATVEC_N, k=MATVEC_K):
     return n * k // per[0] * per[1] + k * 4 + n * 4
 
 
-def bench_matvec(dev, t=2, launches=340, min_bytes=320 << 20, n=MATVEC_N, k=MATVEC_K):
+def bench_matvec(dev, t=2, launches=340, min_bytes=320 << 20, n=MATVEC_N, k=MATVEC_K, floor=False):
     """Average seconds of one n x k matvec (m = 1, default 4096 x 4096) of GGML type t,
     launched back to back over enough resident weight copies (>= 320 MB) that the 256 MB
-    Infinity Cache cannot serve them."""
+    Infinity Cache cannot serve them.  floor=True times tl_hip_read_floor instead: the same
+    launch shape and copies, reading the weight bytes and computing nothing."""
     import ctypes as C
 
     from tl_amd import QTensor
@@ -66,8 +67,14 @@ def bench_matvec(dev, t=2, launches=340, min_bytes=320 << 20, n=MATVEC_N, k=MATV
     x = dev.tensor_new(rng.standard_normal((1, k)).astype(np.float32))
     y = dev.tensor_zeros((1, n))
     stream = lib.tl_hip_stream()
+    xp, yp = C.c_void_p(x.data_ptr), C.c_void_p(y.data_ptr)
+
+    def launch(i):
+        if floor:
+            return lib.tl_hip_read_floor(hs[i % copies], stream)
+        return lib.tl_hip_launch_quant_matvec(hs[i % copies], xp, yp, 1, stream)
     for i in range(2 * copies):  # warm-up
-        if lib.tl_hip_launch_quant_matvec(hs[i % copies], C.c_void_p(x.data_ptr), C.c_void_p(y.data_ptr), 1, stream):
+        if launch(i):
             raise RuntimeError(lib.tl_hip_last_error())
     dev.synchronize()
     e0, e1 = lib.tl_hip_event_create(), lib.tl_hip_event_create()
@@ -76,7 +83,7 @@ def bench_matvec(dev, t=2, launches=340, min_bytes=320 << 20, n=MATVEC_N, k=MATV
     lib.tl_hip_stall(20000)
     lib.tl_hip_event_record(e0)
     for i in range(launches):
-        lib.tl_hip_launch_quant_matvec(hs[i % copies], C.c_void_p(x.data_ptr), C.c_void_p(y.data_ptr), 1, stream)
+        launch(i)
     lib.tl_hip_event_record(e1)
     ms = C.c_float()
     lib.tl_hip_event_elapsed_ms(e0, e1, C.byref(ms))
@@ -478,6 +485,8 @@ def main():
     ap.add_argument("--gemm-m", type=int, default=0, help="with --gemm-only: this M only (default 512, 128, 16)")
     ap.add_argument("--kquant-only", action="store_true", help="only the per-type matvec and Q4_K_M decode legs")
     ap.add_argument("--attention-only", action="store_true", help="only the decode attention leg (counter runs)")
+    ap.add_argument("--read-floor", action="store_true",
+                    help="only the 4096x4096 matvec and its one-launch read floor (same shape and copies)")
     ap.add_argument("--matvec-only", action="store_true",
                     help="only the 4096x4096 matvec timing plus a 64 MiB device copy (counter runs)")
     args = ap.parse_args()
@@ -512,6 +521,12 @@ def main():
     avg_s = bench_matvec(dev)
     achieved = MATVEC_BYTES / avg_s / 1e9
     log(f"[bench] matvec avg {avg_s * 1e6:.2f} us -> {achieved:.0f} GB/s")
+    floor_s = bench_matvec(dev, floor=True)
+    log(f"[bench] read floor (the matvec's loads only, same copies) {floor_s * 1e6:.2f} us -> "
+        f"{MATVEC_BYTES / floor_s / 1e9:.0f} GB/s")
+    if args.read_floor:
+        print(json.dumps({"matvec_avg_us": round(avg_s * 1e6, 3), "floor_us": round(floor_s * 1e6, 3)}), flush=True)
+        return
     if args.matvec_only:
         # reference dispatch for the FETCH_SIZE / WRITE_SIZE scale: a device copy of 64 MiB
         import ctypes as C
@@ -596,6 +611,9 @@ def main():
             "traffic_source": "not measured in this run: FETCH_SIZE + WRITE_SIZE counter runs of "
                               "`bench.py --matvec-only` (profiles/q4_0_matvec_4096x4096.md)",
             "avg_launch_us": round(avg_s * 1e6, 3),
+            "floor_us": round(floor_s * 1e6, 3),
+            "floor_note": "tl_hip_read_floor: the matvec's own loads (launch plan, access pattern, quant bytes + "
+                          "scales) over the same weight copies, with no math, reduction or store",
         },
         "cpu_baseline": cpu,
         "prefill_gemm": {"path": "f16 MFMA (v_mfma_f32_16x16x32_f16), f32 accumulate", "unit": "TFLOP/s",

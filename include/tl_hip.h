@@ -180,6 +180,11 @@ int tl_hip_launch_quant_matvec(const tl_hip_qtensor* w, const float* x, float* y
                                void* stream);
 int tl_hip_launch_quant_gemm(const tl_hip_qtensor* w, const float* x, float* y, int64_t m,
                              int use_f16_mfma, void* stream);
+/* The one-launch floor of the decode matvec over w: the loads of the m = 1 matvec -- its
+ * launch plan and access pattern, quant bytes and scale data -- with no arithmetic, reduction
+ * or store; the time a matvec of w cannot beat.  Timing plumbing for the roofline; no
+ * reference counterpart. */
+int tl_hip_read_floor(const tl_hip_qtensor* w, void* stream);
 /* Allocation-free variant of tl_hip_launch_quant_gemm (no counterpart in the reference): for
  * callers that cannot allocate device memory -- code under hipGraph capture, serving loops
  * that forbid hipMalloc.  Same arguments and results; calls no hipMalloc / hipFree.  The f16

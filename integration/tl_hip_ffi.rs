@@ -142,6 +142,7 @@ extern "C" {
         use_f16_mfma: i32,
         stream: *mut c_void,
     ) -> i32;
+    pub fn tl_hip_read_floor(w: *const tl_hip_qtensor, stream: *mut c_void) -> i32;
     pub fn tl_hip_launch_quant_gemm_noalloc(
         w: *const tl_hip_qtensor,
         x: *const f32,

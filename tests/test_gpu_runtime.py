@@ -117,3 +117,19 @@ def test_launcher_on_a_caller_stream(dev):
     finally:
         hip.hipStreamSynchronize(other)
         hip.hipStreamDestroy(other)
+
+
+@pytest.mark.parametrize("t", [2, 8, 12, 14])
+def test_read_floor_launches_for_every_type(dev, t):
+    """tl_hip_read_floor (the roofline's one-launch read of a weight) runs for every resident
+    type and leaves the library usable."""
+    from tl_amd.quant import random_q4_0_blocks, random_q4_k_blocks, random_q6_k_blocks, random_q8_0_blocks
+    lib = _lib.load()
+    gen = {2: random_q4_0_blocks, 8: random_q8_0_blocks, 12: random_q4_k_blocks, 14: random_q6_k_blocks}[t]
+    rng = np.random.default_rng(0x5109 + t)
+    w = QTensor(t, gen(rng, 512, 2048), (512, 2048))
+    hw = w.upload(lib)
+    for _ in range(3):
+        assert lib.tl_hip_read_floor(hw, None) == 0
+    assert lib.tl_hip_synchronize() == 0
+    assert lib.tl_hip_read_floor(None, None) == 4

@@ -69,6 +69,7 @@ PROTOS = {
     "tl_hip_launch_quant_matvec": (i32, [P, P, P, i64, P]),
     "tl_hip_launch_quant_gemm": (i32, [P, P, P, i64, i32, P]),
     "tl_hip_launch_quant_gemm_noalloc": (i32, [P, P, P, i64, i32, P]),
+    "tl_hip_read_floor": (i32, [P, P]),
     "tl_hip_debug_last_gemm_plan": (i32, [i32p, i32p, i32p]),
     "tl_hip_tensor_matmul": (P, [P, P]),
     "tl_hip_tensor_transpose_2d": (P, [P]),

@@ -83,8 +83,19 @@ struct AttnArgs {
     float scale;
 };
 
+// Every AttnArgs field the kernels' prologues read, fetched from the kernel-argument buffer in
+// one round of scalar loads: left to the compiler, loads placed after the prologue's branches
+// wait for an earlier round to return (three or four dependent memory round trips before the
+// first K load).
+__device__ __forceinline__ void attn_args_prefetch(const AttnArgs& a) {
+    asm volatile("" : : "s"(a.q), "s"(a.k), "s"(a.v), "s"(a.out), "s"(a.ws), "s"(a.hkv), "s"(a.lmax), "s"(a.kv_bstride),
+                 "s"(a.len.L), "s"(a.len.len_dev), "s"(a.len.len_add), "s"(a.len.len_step), "s"(a.chunk),
+                 "s"(a.nsplit), "s"(a.scale));
+}
+
 template <int D, int G, typename KVT>
 __global__ __launch_bounds__(256) void k_attn(AttnArgs a) {
+    attn_args_prefetch(a);
     constexpr int DL = D / 8;  // dims per lane
     __shared__ float sc[G][ATT_MAX_CHUNK];
     __shared__ float stat[G][2];
@@ -237,6 +248,7 @@ __global__ __launch_bounds__(256) void k_attn(AttnArgs a) {
 // splits are read in parallel into LDS, then each output element sums its o_s in split order.
 template <int D, int G>
 __global__ __launch_bounds__(256) void k_attn_merge(AttnArgs a) {
+    attn_args_prefetch(a);
     __shared__ float sm[G][ATT_MAX_SPLITS], sf[G][ATT_MAX_SPLITS], sden[G];
     const int h = blockIdx.x, b = blockIdx.y, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     int64_t L = a.len.of(b);
@@ -367,6 +379,7 @@ __device__ __forceinline__ void tr_halve(float (&v)[N], int lane) {
 
 template <int D, int G, int PW>  // PW positions per wavefront, 4 PW per workgroup (split)
 __global__ __launch_bounds__(256) void k_attn_gq(AttnArgs a) {
+    attn_args_prefetch(a);
     constexpr int GQ_PW = PW, GQ_CH = 4 * PW;
     constexpr int LPR = D / 8;          // lanes per row (16 bytes of f16 each)
     constexpr int RPI = 64 / LPR;       // rows per load instruction
@@ -540,6 +553,7 @@ __device__ __forceinline__ void cvt16<float>(const uint4& w, float* f) {
 
 template <int D, typename KVT, int W>
 __global__ __launch_bounds__(64 * W) void k_attn_qh(AttnArgs a, int G) {
+    attn_args_prefetch(a);
     constexpr int C = 64;                  // positions per wavefront and round
     constexpr int EPC = 16 / sizeof(KVT);  // elements per 16-byte load
     constexpr int LPR = D / EPC;           // lanes per K row
@@ -696,6 +710,9 @@ __global__ __launch_bounds__(256) void k_attn_prefill(const float* __restrict__ 
                                                       int n, int hkv, int64_t lmax, const int32_t* __restrict__ pos_dev,
                                                       int64_t pos_host, float scale, _Float16* __restrict__ out16,
                                                       int order) {
+    // arguments in one round of scalar loads (left to the compiler: three dependent rounds)
+    asm volatile("" : : "s"(q), "s"(kc), "s"(vc), "s"(out), "s"(n), "s"(hkv), "s"(lmax), "s"(pos_dev), "s"(pos_host),
+                 "s"(scale), "s"(out16), "s"(order));
     constexpr int QB = 128 / G;   // queries per workgroup
     constexpr int KT = 64;        // positions per KV tile
     constexpr int KS = D / 32;    // MFMA k-steps over the head dim
@@ -984,6 +1001,7 @@ static int attn_dispatch(const AttnArgs& a, int B, int hq, int D, hipStream_t s)
 // through LDS.  out = sum_s o_s e^(m_s - M) / sum_s l_s e^(m_s - M).
 template <int D, int G>
 __global__ __launch_bounds__(256) void k_attn_merge_gq(AttnArgs a) {
+    attn_args_prefetch(a);
     constexpr int NC = D / 4, NG = 256 / NC;  // float4 columns, split groups
     constexpr int U = 8;                       // splits per thread held in registers
     __shared__ float4 acc[NG][NC];

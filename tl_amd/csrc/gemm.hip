@@ -249,6 +249,7 @@ struct QWords<TL_HIP_GGML_F16> {
 template <int QT>
 __global__ __launch_bounds__(256) void k_x_to_f16q(const float* __restrict__ x, _Float16* __restrict__ x16,
                                                    int64_t units) {
+    asm volatile("" : : "s"(x), "s"(x16), "s"(units));  // arguments in one round of scalar loads
     const int64_t u = (int64_t)blockIdx.x * 256 + threadIdx.x;  // = row * nb * 4 + block * 4 + t
     if (u >= units) return;
     const int t = (int)(u & 3);
@@ -308,6 +309,10 @@ template <int QT, int BM, int BN>
 __global__ __launch_bounds__(512) void k_qgemm_mfma(const uint8_t* __restrict__ qs, const __half* __restrict__ dsc,
                                                     const _Float16* __restrict__ x16, float* y, int64_t m,
                                                     int64_t n, int64_t k, int64_t nb, GemmEpi ep) {
+    // every argument, fetched from the kernel-argument buffer in one round of scalar loads
+    // (left to the compiler, three dependent rounds precede the first tile load)
+    asm volatile("" : : "s"(qs), "s"(dsc), "s"(x16), "s"(y), "s"(m), "s"(n), "s"(k), "s"(nb), "s"(ep.mode),
+                 "s"(ep.res), "s"(ep.out16), "s"(ep.order));
     constexpr int TM = BM / 32, TN = BN / 32;  // 16 x 16 tiles per wavefront
     constexpr int QB = QWords<QT>::BYTES;
     constexpr int QC = QB / 16;                // 16-byte chunks per quant block
@@ -554,6 +559,7 @@ int launch_x_to_f16q(const float* x, _Float16* x16, int64_t m, int64_t k, int or
 // splits K only then).
 __global__ __launch_bounds__(256) void k_splitk_sum(const float* __restrict__ part, float* y, const float* res,
                                                     int64_t mn, int nsp) {
+    asm volatile("" : : "s"(part), "s"(y), "s"(res), "s"(mn), "s"(nsp));  // arguments in one round
     const int64_t i = ((int64_t)blockIdx.x * 256 + threadIdx.x) * 4;
     if (i >= mn) return;
     if (i + 4 <= mn) {

@@ -143,6 +143,7 @@ int launch_mv(const QWeight* w, MvArgs a, int m, int epi, bool norm, bool embed,
 // workgroups (= argmax partial slots) of a matvec over n rows
 int mv_partials(int64_t n);
 bool matvec_fits(const QWeight* w, int64_t m);  // the LDS-staged matvec takes this product
+int launch_read_floor(const QWeight* w, hipStream_t s);  // read of w's arrays, matvec launch shape
 
 // kernel entry points shared across translation units (all on the given stream)
 int launch_quant_matvec(const QWeight* w, const float* x, float* y, int64_t m, hipStream_t s,

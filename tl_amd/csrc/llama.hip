@@ -43,6 +43,9 @@ __global__ void k_rope_kv(const float* __restrict__ qkv, float* __restrict__ qou
                           const float* __restrict__ ct, const float* __restrict__ st,
                           const int32_t* __restrict__ pos_dev, int n, int H, int KV, int hd,
                           int64_t max_seq, int per_token) {
+    // arguments in one round of scalar loads (left to the compiler: three dependent rounds)
+    asm volatile("" : : "s"(qkv), "s"(qout), "s"(kc), "s"(vc), "s"(ct), "s"(st), "s"(pos_dev), "s"(n), "s"(H),
+                 "s"(KV), "s"(hd), "s"(max_seq), "s"(per_token));
     const int row = H * hd + 2 * KV * hd;
     const int pairs = (H + KV) * hd / 2;  // rotated pairs per token
     const int vals = KV * hd;             // copied v values per token

@@ -212,6 +212,20 @@ __global__ __launch_bounds__(256) void k_mv(MvArgs a, MvShape sh) {
     constexpr int N = M * RWT;
     constexpr int RWT_SHIFT = RWT == 1 ? 0 : RWT == 2 ? 1 : RWT == 4 ? 2 : RWT == 8 ? 3 : 4;
     static_assert(N <= 64 && (N & (N - 1)) == 0 && (1 << RWT_SHIFT) == RWT, "RWT, M * RWT: powers of two");
+    // Every kernel argument the prologue needs, fetched from the argument buffer in one round
+    // of scalar loads: left to the compiler, loads placed after the prologue's branches wait
+    // for the first round to return (two or three dependent rounds before the first weight
+    // load, each one a memory round trip).
+    asm volatile("" : : "s"(a.qs), "s"(a.d), "s"(a.n), "s"(a.k), "s"(a.nb), "s"(a.x), "s"(sh.tc), "s"(sh.tc_shift),
+                 "s"(sh.s_shift));
+    if constexpr (QT == TL_HIP_GGML_Q4_K) asm volatile("" : : "s"(a.hdr));
+    if constexpr (QT == TL_HIP_GGML_Q6_K) asm volatile("" : : "s"(a.qh), "s"(a.sc));
+    if constexpr (NORM) asm volatile("" : : "s"(a.norm_w));
+    if constexpr (EMBED) asm volatile("" : : "s"(a.embed_id), "s"(a.x_out));
+    if constexpr (MERGE) asm volatile("" : : "s"(a.attn_rec), "s"(a.attn_hd));
+    if constexpr (EPI == EPI_RES) asm volatile("" : : "s"(a.res));
+    if constexpr (EPI == EPI_ROPE_KV) asm volatile("" : : "s"(a.pos), "s"(a.cos_t), "s"(a.sin_t), "s"(a.row_off));
+    if constexpr (EPI == EPI_ARGMAX) asm volatile("" : : "s"(a.seen));
     extern __shared__ float xs[];  // [M][nb][XPAD] staged activations (x * norm weight with NORM)
     __shared__ float red[4][N];
     __shared__ float ys[M][MV_MAX_RW];
@@ -637,6 +651,9 @@ __global__ __launch_bounds__(256) void k_mv(MvArgs a, MvShape sh) {
 // replays that fold over the penalised logits.  Then the decode-step bookkeeping: token
 // recorded, penalty mask updated, position advanced.
 __global__ __launch_bounds__(256) void k_argmax_finish(MvArgs a, int nwg) {
+    // the arguments read below, fetched from the kernel-argument buffer in one round
+    asm volatile("" : : "s"(a.part_v), "s"(a.part_i), "s"(a.part_nan), "s"(a.out_ids), "s"(a.step), "s"(a.pos_inc),
+                 "s"(a.tok_out), "s"(a.seen_out), "s"(a.max_out), "s"(a.n), "s"(a.plogits), "s"(nwg));
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     // the step counter and the position are read with the candidates, one memory round trip
     // (read after the stores below they would each cost another)
@@ -841,6 +858,103 @@ bool matvec_fits(const QWeight* w, int64_t m) {
     return m >= 1 && m <= 4 && w->n >= 1 && w->nb >= 1 &&
            (uint64_t)w->n * w->nb * (w->ggml_type == TL_HIP_GGML_Q8_0 ? 32 : 16) < (1ull << 31) &&
            (size_t)mm * w->nb * XPAD * sizeof(float) <= 150 * 1024;
+}
+
+// ------------------------------------------------------------ one-launch read floor ----
+// The loads of k_mv with its launch plan and access pattern -- thread (sub, tcol) reads unit
+// columns tcol + TC i of rows row0 + sub + S r, quant bytes and scale data as the matvec does --
+// and nothing else: the XOR of the loaded words goes to an empty asm statement, which keeps
+// the loads (and the wait for them) without a store.  The time of a launch that only moves
+// the weight stream the way the matvec moves it.
+template <int QT, int BT, int RWT>
+__global__ __launch_bounds__(256) void k_read_floor(MvArgs a, MvShape sh) {
+    constexpr int QB = QB_<QT>::v, QW = QB / 16;
+    // the kernel arguments the loads need, fetched from the argument buffer in one round
+    asm volatile("" : : "s"(a.qs), "s"(a.d), "s"(a.hdr), "s"(a.qh), "s"(a.sc), "s"(a.n), "s"(a.nb), "s"(sh.tc),
+                 "s"(sh.tc_shift), "s"(sh.s_shift));
+    const int tid = threadIdx.x;
+    const int TC = sh.tc, S = 1 << sh.s_shift;
+    const int tcol = sh.s_shift ? (tid & (TC - 1)) : tid;
+    const int sub = sh.s_shift ? (tid >> sh.tc_shift) : 0;
+    const uint32_t nb = (uint32_t)a.nb, n = (uint32_t)a.n;
+    const uint32_t my_row0 = blockIdx.x * (uint32_t)(RWT << sh.s_shift) + sub;
+    uint32_t acc = 0;
+    for (uint32_t base = 0; base < nb; base += (uint32_t)(BT * TC)) {
+        uint4 w[BT][RWT][QW];
+        uint4 extra[BT][RWT];
+#pragma unroll
+        for (int i = 0; i < BT; i++) {
+            const uint32_t b0 = base + (uint32_t)(tcol + i * TC);
+            const uint32_t b = b0 < nb ? b0 : nb - 1;
+#pragma unroll
+            for (int r = 0; r < RWT; r++) {
+                uint32_t row = my_row0 + (uint32_t)(S * r);
+                row = row < n ? row : n - 1;
+                const uint32_t blk = __umul24(row, nb) + b;
+                const uint4* p = reinterpret_cast<const uint4*>(a.qs + (size_t)blk * QB);
+#pragma unroll
+                for (int c = 0; c < QW; c++) w[i][r][c] = p[c];
+                if constexpr (QT == TL_HIP_GGML_Q4_K) {
+                    extra[i][r] = reinterpret_cast<const uint4*>(a.hdr)[blk >> 3];
+                } else if constexpr (QT == TL_HIP_GGML_Q6_K) {
+                    const uint2 hq = reinterpret_cast<const uint2*>(a.qh)[blk];
+                    extra[i][r] = uint4{hq.x, hq.y, reinterpret_cast<const uint16_t*>(a.sc)[blk],
+                                        reinterpret_cast<const uint16_t*>(a.d)[blk >> 3]};
+                } else {
+                    extra[i][r] = uint4{reinterpret_cast<const uint16_t*>(a.d)[blk], 0u, 0u, 0u};
+                }
+            }
+        }
+#pragma unroll
+        for (int i = 0; i < BT; i++)
+#pragma unroll
+            for (int r = 0; r < RWT; r++) {
+#pragma unroll
+                for (int c = 0; c < QW; c++) acc ^= w[i][r][c].x ^ w[i][r][c].y ^ w[i][r][c].z ^ w[i][r][c].w;
+                acc ^= extra[i][r].x ^ extra[i][r].y ^ extra[i][r].z ^ extra[i][r].w;
+            }
+    }
+    asm volatile("" : : "v"(acc));
+}
+
+template <int QT>
+static int run_floor(const MvArgs& a, const MvPlan& p, hipStream_t s) {
+    const dim3 grid((unsigned)p.grid), block((unsigned)(p.S * p.TC));
+    if (p.BT == 1) {
+        if (p.RWT == 8) k_read_floor<QT, 1, 8><<<grid, block, 0, s>>>(a, p.shape());
+        else if (p.RWT == 4) k_read_floor<QT, 1, 4><<<grid, block, 0, s>>>(a, p.shape());
+        else k_read_floor<QT, 1, 2><<<grid, block, 0, s>>>(a, p.shape());
+    } else {
+        if (p.RWT == 8) k_read_floor<QT, 2, 8><<<grid, block, 0, s>>>(a, p.shape());
+        else if (p.RWT == 4) k_read_floor<QT, 2, 4><<<grid, block, 0, s>>>(a, p.shape());
+        else k_read_floor<QT, 2, 2><<<grid, block, 0, s>>>(a, p.shape());
+    }
+    hipError_t e = hipGetLastError();
+    return e == hipSuccess ? TL_HIP_OK : hip_fail(e, "read floor launch");
+}
+
+int launch_read_floor(const QWeight* w, hipStream_t s) {
+    if (w->n < 1 || w->nb < 1 ||
+        (uint64_t)w->n * w->nb * (w->ggml_type == TL_HIP_GGML_Q8_0 ? 32 : 16) >= (1ull << 31)) {
+        set_error(TL_HIP_ERR_ARG, "ArgumentError: weight outside the decode matvec's limits");
+        return TL_HIP_ERR_ARG;
+    }
+    MvArgs a = {};
+    a.qs = w->qs;
+    a.d = w->d;
+    a.hdr = w->hdr;
+    a.qh = w->qh;
+    a.sc = w->sc;
+    a.n = w->n;
+    a.k = w->k;
+    a.nb = w->nb;
+    const MvPlan p = mv_plan(w->n, w->nb, w->ggml_type);
+    switch (w->ggml_type) {
+        case TL_HIP_GGML_Q4_0: return run_floor<TL_HIP_GGML_Q4_0>(a, p, s);
+        case TL_HIP_GGML_Q8_0: return run_floor<TL_HIP_GGML_Q8_0>(a, p, s);
+        case TL_HIP_GGML_Q4_K: return run_floor<TL_HIP_GGML_Q4_K>(a, p, s);
+        default: return run_floor<TL_HIP_GGML_Q6_K>(a, p, s);
+    }
 }
 
 // Upper bound on the workgroups (= argmax partial slots) of a matvec over n rows.

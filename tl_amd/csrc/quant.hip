@@ -451,6 +451,16 @@ int tl_hip_launch_quant_matvec(const tl_hip_qtensor* h, const float* x, float* y
                                stream ? (hipStream_t)stream : cur_stream(), nullptr);
 }
 
+int tl_hip_read_floor(const tl_hip_qtensor* h, void* stream) {
+    if (!h) {
+        set_error(TL_HIP_ERR_NULL, "NullPointerError: weight");
+        return TL_HIP_ERR_NULL;
+    }
+    if (!state()) return tl_hip_last_status();
+    note_stream((hipStream_t)stream);
+    return launch_read_floor(reinterpret_cast<const QWeight*>(h), stream ? (hipStream_t)stream : cur_stream());
+}
+
 int tl_hip_launch_quant_gemm(const tl_hip_qtensor* h, const float* x, float* y, int64_t m,
                              int use_f16_mfma, void* stream) {
     if (!h || !x || !y) {
