@@ -23,6 +23,10 @@ CFLAGS = [
     "-Wno-unused-result",
     # packed-fp32 instructions are disabled for all device code on this platform
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    # leading scalar / pointer kernel arguments (up to 16 dwords) are preloaded into SGPRs at
+    # dispatch instead of being fetched from the kernel-argument buffer by the first wave: one
+    # memory round trip less before a kernel's first load (~0.3 us per launch on MI355X)
+    "-mllvm", "-amdgpu-kernarg-preload-count=16",
     "-I" + os.path.join(HERE, "..", "include"),
 ]
 

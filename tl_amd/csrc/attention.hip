@@ -551,9 +551,26 @@ __device__ __forceinline__ void cvt16<float>(const uint4& w, float* f) {
     f[3] = __uint_as_float(w.w);
 }
 
+// The arguments the first loads need lead, as scalars and pointers preloaded into SGPRs at
+// dispatch (14 dwords: the KV-head count, G and the share count share one); the rest of AttnArgs (the split
+// record buffer, the output, the score scale, the host length) is loaded from the argument
+// buffer while the first K / V loads are in flight.
 template <int D, typename KVT, int W>
-__global__ __launch_bounds__(64 * W) void k_attn_qh(AttnArgs a, int G) {
-    attn_args_prefetch(a);
+__global__ __launch_bounds__(64 * W) void k_attn_qh(const float* __restrict__ q_p, const void* __restrict__ k_p,
+                                                    const void* __restrict__ v_p, const int32_t* __restrict__ len_dev,
+                                                    int64_t kv_bstride, int lmax_p, uint32_t hkv_g, int len_add,
+                                                    int len_step, AttnArgs a) {
+    a.q = q_p;
+    a.k = k_p;
+    a.v = v_p;
+    a.kv_bstride = kv_bstride;
+    a.lmax = lmax_p;
+    a.hkv = (int)(hkv_g & 0xffffu);
+    a.len.len_dev = len_dev;
+    a.len.len_add = len_add;
+    a.len.len_step = len_step;
+    const int G = (int)((hkv_g >> 16) & 0xffu);
+    const uint32_t ns = hkv_g >> 24;  // = gridDim.z, without a load of the dispatch packet
     constexpr int C = 64;                  // positions per wavefront and round
     constexpr int EPC = 16 / sizeof(KVT);  // elements per 16-byte load
     constexpr int LPR = D / EPC;           // lanes per K row
@@ -570,25 +587,9 @@ __global__ __launch_bounds__(64 * W) void k_attn_qh(AttnArgs a, int G) {
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int kl = lane % LPR, kr = lane / LPR;  // K: slice and row within an instruction
     const int slot = lane & 7, dg = lane >> 3;   // V: position slot and dim group
-    int64_t L64 = a.len.of(b);
-    if (L64 > a.lmax) L64 = a.lmax;
-    const uint32_t L = (uint32_t)L64;  // lmax * D < 2^31 (attention_qh_supported): 32-bit offsets
     const int hq = a.hkv * G;
-    // gridDim.z > 1: this workgroup covers positions [p0, p1), a share of whole rounds (the
-    // first share is never empty), and leaves an unnormalised partial record
-    const uint32_t ns = gridDim.z;
-    uint32_t p0 = 0, p1 = L;
-    if (ns > 1) {
-        const uint32_t per = ((L + ns - 1) / ns + C - 1) / C * C;
-        p0 = blockIdx.z * per < L ? blockIdx.z * per : L;
-        p1 = p0 + per < L ? p0 + per : L;
-    }
-    const KVT* kb = reinterpret_cast<const KVT*>(a.k) + (int64_t)b * a.kv_bstride + (int64_t)h * a.lmax * D;
-    const KVT* vb = reinterpret_cast<const KVT*>(a.v) + (int64_t)b * a.kv_bstride + (int64_t)h * a.lmax * D;
     const float* qp = a.q + ((int64_t)b * hq + qh) * D;
-    const float sl2 = a.scale * 1.44269504088896341f;  // scores in log2 units: exp(x) = exp2(x log2 e)
-
-    float qv[EPC];  // this lane's slice of q
+    float qv[EPC];  // this lane's slice of q, requested before the cached length is known
 #pragma unroll
     for (int e = 0; e < EPC; e += 4) {
         const float4 t = *reinterpret_cast<const float4*>(qp + kl * EPC + e);
@@ -597,6 +598,20 @@ __global__ __launch_bounds__(64 * W) void k_attn_qh(AttnArgs a, int G) {
         qv[e + 2] = t.z;
         qv[e + 3] = t.w;
     }
+    int64_t L64 = a.len.of(b);
+    if (L64 > a.lmax) L64 = a.lmax;
+    const uint32_t L = (uint32_t)L64;  // lmax * D < 2^31 (attention_qh_supported): 32-bit offsets
+    // gridDim.z > 1: this workgroup covers positions [p0, p1), a share of whole rounds (the
+    // first share is never empty), and leaves an unnormalised partial record
+    uint32_t p0 = 0, p1 = L;
+    if (ns > 1) {
+        const uint32_t per = ((L + ns - 1) / ns + C - 1) / C * C;
+        p0 = blockIdx.z * per < L ? blockIdx.z * per : L;
+        p1 = p0 + per < L ? p0 + per : L;
+    }
+    const KVT* kb = reinterpret_cast<const KVT*>(a.k) + (int64_t)b * a.kv_bstride + (int64_t)h * a.lmax * D;
+    const KVT* vb = reinterpret_cast<const KVT*>(a.v) + (int64_t)b * a.kv_bstride + (int64_t)h * a.lmax * D;
+    const float sl2 = a.scale * 1.44269504088896341f;  // scores in log2 units: exp(x) = exp2(x log2 e)
     float m = -INFINITY, l = 0.f, o[DL];
 #pragma unroll
     for (int i = 0; i < DL; i++) o[i] = 0.f;
@@ -935,22 +950,31 @@ int launch_attention_qh(const float* q, const void* k, const void* v, int kv_dty
     AttnArgs a{q, k, v, out, part, hkv, lmax, kv_bstride, AttnLen{L, len_dev, len_add, len_step}, 64, nsplit,
                scale};
     const int G = hq / hkv;
+    if (hkv < 1 || hkv > 0xffff || G < 1 || G > 0xff || lmax > INT32_MAX) {
+        set_error(TL_HIP_ERR_ARG, "ArgumentError: short-cache attention: %d KV heads, %d query heads each, %lld cached "
+                  "positions", hkv, G, (long long)lmax);
+        return TL_HIP_ERR_ARG;
+    }
     dim3 grid(hq, B, nsplit);
     // a workgroup with a share of the positions has fewer rounds for its wavefronts: 4 of them
     const bool w4 = nsplit > 1;
+    const uint32_t hkv_g = (uint32_t)hkv | (uint32_t)G << 16 | (uint32_t)nsplit << 24;
+#define TLH_QH(DD, T, WW)                                                                                     \
+    k_attn_qh<DD, T, WW><<<grid, 64 * WW, 0, s>>>(q, k, v, len_dev, kv_bstride, (int)lmax, hkv_g, len_add, len_step, a)
     if (D == 64 && kv_dtype == TL_HIP_F16) {
-        if (w4) k_attn_qh<64, __half, 4><<<grid, 64 * 4, 0, s>>>(a, G);
-        else k_attn_qh<64, __half, 8><<<grid, 64 * 8, 0, s>>>(a, G);
+        if (w4) TLH_QH(64, __half, 4);
+        else TLH_QH(64, __half, 8);
     } else if (D == 128 && kv_dtype == TL_HIP_F16) {
-        if (w4) k_attn_qh<128, __half, 4><<<grid, 64 * 4, 0, s>>>(a, G);
-        else k_attn_qh<128, __half, 8><<<grid, 64 * 8, 0, s>>>(a, G);
+        if (w4) TLH_QH(128, __half, 4);
+        else TLH_QH(128, __half, 8);
     } else if (D == 64 && kv_dtype == TL_HIP_F32) {
-        if (w4) k_attn_qh<64, float, 4><<<grid, 64 * 4, 0, s>>>(a, G);
-        else k_attn_qh<64, float, 8><<<grid, 64 * 8, 0, s>>>(a, G);
+        if (w4) TLH_QH(64, float, 4);
+        else TLH_QH(64, float, 8);
     } else {
         set_error(TL_HIP_ERR_ARG, "ArgumentError: short-cache attention covers head_dim 64 / 128 (f16 cache) and 64 (f32)");
         return TL_HIP_ERR_ARG;
     }
+#undef TLH_QH
     hipError_t e = hipGetLastError();
     return e == hipSuccess ? TL_HIP_OK : hip_fail(e, "attention launch");
 }

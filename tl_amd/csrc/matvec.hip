@@ -167,6 +167,11 @@ constexpr int XR = 8, XR_NORM = 4, XR_NORM8 = 2;
 // when S > 1, a power of two 1 << tc_shift).
 struct MvShape {
     int tc, tc_shift, s_shift;
+    // one dword for the kernel argument list: tc (<= 256) | tc_shift << 16 | s_shift << 24
+    __host__ __device__ uint32_t pack() const { return (uint32_t)tc | (uint32_t)tc_shift << 16 | (uint32_t)s_shift << 24; }
+    __host__ __device__ static MvShape unpack(uint32_t v) {
+        return MvShape{(int)(v & 0xffffu), (int)((v >> 16) & 0xffu), (int)(v >> 24)};
+    }
 };
 
 // Thread (sub, tcol) owns block columns tcol + tc * (i + BT * pass) of rows
@@ -206,26 +211,42 @@ __device__ __forceinline__ float4 merge_shares(const float4 (&o)[ATTN_SHARES], c
     return float4{num.x * inv, num.y * inv, num.z * inv, num.w * inv};
 }
 
+// The arguments the first loads need come first, as scalars and pointers, so that they are
+// preloaded into SGPRs at dispatch (kernel-argument preloading covers leading non-aggregate
+// arguments, up to 14 dwords: 16 user SGPRs less the argument-buffer pointer): the weight stream (qs, the scale array w1 -- d, the Q4_K headers
+// or the Q6_K high bits), the activations x, the auxiliary input of the prologue (aux: the
+// RMSNorm weight, or the attention records that form x; aux2: the token id of EMBED or the
+// position of EPI_ROPE_KV; aux_i: the records' head dimension), and the shape.  The rest
+// travels in MvArgs; the compiler's scalar loads of those fields then overlap the weight
+// stream instead of holding back its first loads.
 template <int QT, int BT, int RWT, int M, int EPI, bool NORM, bool EMBED, bool MERGE = false>
-__global__ __launch_bounds__(256) void k_mv(MvArgs a, MvShape sh) {
+__global__ __launch_bounds__(256) void k_mv(const uint8_t* __restrict__ qs_p, const void* __restrict__ w1_p,
+                                            const float* __restrict__ x_p, const float* __restrict__ aux_p,
+                                            const int32_t* __restrict__ aux2_p, uint32_t n_p, uint32_t nb_p,
+                                            uint32_t shape_p, int aux_i, MvArgs a) {
     constexpr int QB = QB_<QT>::v, QW = QB / 16;  // 16-byte loads per block
     constexpr int N = M * RWT;
     constexpr int RWT_SHIFT = RWT == 1 ? 0 : RWT == 2 ? 1 : RWT == 4 ? 2 : RWT == 8 ? 3 : 4;
     static_assert(N <= 64 && (N & (N - 1)) == 0 && (1 << RWT_SHIFT) == RWT, "RWT, M * RWT: powers of two");
-    // Every kernel argument the prologue needs, fetched from the argument buffer in one round
-    // of scalar loads: left to the compiler, loads placed after the prologue's branches wait
-    // for the first round to return (two or three dependent rounds before the first weight
-    // load, each one a memory round trip).
-    asm volatile("" : : "s"(a.qs), "s"(a.d), "s"(a.n), "s"(a.k), "s"(a.nb), "s"(a.x), "s"(sh.tc), "s"(sh.tc_shift),
-                 "s"(sh.s_shift));
-    if constexpr (QT == TL_HIP_GGML_Q4_K) asm volatile("" : : "s"(a.hdr));
-    if constexpr (QT == TL_HIP_GGML_Q6_K) asm volatile("" : : "s"(a.qh), "s"(a.sc));
-    if constexpr (NORM) asm volatile("" : : "s"(a.norm_w));
-    if constexpr (EMBED) asm volatile("" : : "s"(a.embed_id), "s"(a.x_out));
-    if constexpr (MERGE) asm volatile("" : : "s"(a.attn_rec), "s"(a.attn_hd));
-    if constexpr (EPI == EPI_RES) asm volatile("" : : "s"(a.res));
-    if constexpr (EPI == EPI_ROPE_KV) asm volatile("" : : "s"(a.pos), "s"(a.cos_t), "s"(a.sin_t), "s"(a.row_off));
-    if constexpr (EPI == EPI_ARGMAX) asm volatile("" : : "s"(a.seen));
+    a.qs = qs_p;
+    a.x = x_p;
+    a.n = n_p;
+    a.nb = nb_p;
+    a.k = (int64_t)nb_p * 32;
+    if constexpr (QT == TL_HIP_GGML_Q4_K) a.hdr = static_cast<const uint8_t*>(w1_p);
+    else if constexpr (QT == TL_HIP_GGML_Q6_K) a.qh = static_cast<const uint8_t*>(w1_p);
+    else a.d = static_cast<const __half*>(w1_p);
+    if constexpr (NORM) a.norm_w = aux_p;
+    if constexpr (MERGE) {
+        a.attn_rec = aux_p;
+        a.attn_hd = aux_i;
+    }
+    if constexpr (EMBED) a.embed_id = aux2_p;
+    else if constexpr (EPI == EPI_ROPE_KV) a.pos = aux2_p;
+    const MvShape sh = MvShape::unpack(shape_p);
+    // Q6_K's scale arrays are read with the first weight loads: fetched in one round of scalar
+    // loads (left to the compiler, each would wait for the round before it)
+    if constexpr (QT == TL_HIP_GGML_Q6_K) asm volatile("" : : "s"(a.sc), "s"(a.d));
     extern __shared__ float xs[];  // [M][nb][XPAD] staged activations (x * norm weight with NORM)
     __shared__ float red[4][N];
     __shared__ float ys[M][MV_MAX_RW];
@@ -422,7 +443,7 @@ __global__ __launch_bounds__(256) void k_mv(MvArgs a, MvShape sh) {
     set_cols(0);
     {
         const float* xsrc = EMBED ? a.x + (size_t)(*a.embed_id) * k : a.x;
-        const uint32_t k4 = k >> 2, nthr = blockDim.x;
+        const uint32_t k4 = k >> 2, nthr = (uint32_t)sh.tc << sh.s_shift;  // the workgroup size
         float s2[M];
         constexpr int XRK = MERGE ? 2 : NORM ? (RWT >= 8 ? XR_NORM8 : XR_NORM) : XR;
         float4 xr[M][XRK], gr[NORM ? XRK : 1];
@@ -539,7 +560,7 @@ __global__ __launch_bounds__(256) void k_mv(MvArgs a, MvShape sh) {
             for (int q = s * wps; q < (s + 1) * wps; q++) acc_s += red[q][m * RWT + j];
             if constexpr (NORM) {
                 float ss = 0.f;
-                for (int q = 0; q < (int)(blockDim.x >> 6); q++) ss += ssq[q][m];
+                for (int q = 0; q < ((sh.tc << sh.s_shift) >> 6); q++) ss += ssq[q][m];
                 acc_s = acc_s / sqrtf(ss / (float)k + a.eps);
             }
             if constexpr (EPI == EPI_PLAIN || EPI == EPI_RES) {
@@ -650,18 +671,18 @@ __global__ __launch_bounds__(256) void k_mv(MvArgs a, MvShape sh) {
 // larger index) reduction equals the left fold of tensor.rs:1633-1637, otherwise thread 0
 // replays that fold over the penalised logits.  Then the decode-step bookkeeping: token
 // recorded, penalty mask updated, position advanced.
-__global__ __launch_bounds__(256) void k_argmax_finish(MvArgs a, int nwg) {
-    // the arguments read below, fetched from the kernel-argument buffer in one round
-    asm volatile("" : : "s"(a.part_v), "s"(a.part_i), "s"(a.part_nan), "s"(a.out_ids), "s"(a.step), "s"(a.pos_inc),
-                 "s"(a.tok_out), "s"(a.seen_out), "s"(a.max_out), "s"(a.n), "s"(a.plogits), "s"(nwg));
+__global__ __launch_bounds__(256) void k_argmax_finish(float* part_v, int32_t* part_i, int32_t* part_nan,
+                                                       int32_t* step, int32_t* pos_inc, int32_t* out_ids, int nwg,
+                                                       MvArgs a) {
+    // what the first loads need comes first (preloaded into SGPRs at dispatch); the fields the
+    // stores at the end use are loaded from the argument buffer meanwhile
+    a.part_v = part_v;
+    a.part_i = part_i;
+    a.part_nan = part_nan;
+    a.step = step;
+    a.pos_inc = pos_inc;
+    a.out_ids = out_ids;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    // the step counter and the position are read with the candidates, one memory round trip
-    // (read after the stores below they would each cost another)
-    int step0 = 0, pos0 = 0;
-    if (tid == 0) {
-        if (a.out_ids) step0 = *a.step;
-        if (a.pos_inc) pos0 = *a.pos_inc;
-    }
     float bv = -INFINITY;
     int bi = -1, nan = 0;
     for (int i = tid; i < nwg; i += 256) {
@@ -672,6 +693,13 @@ __global__ __launch_bounds__(256) void k_argmax_finish(MvArgs a, int nwg) {
             bv = v;
             bi = ix;
         }
+    }
+    // the step counter and the position are read with the candidates, one memory round trip
+    // (read after the stores below they would each cost another)
+    int step0 = 0, pos0 = 0;
+    if (tid == 0) {
+        if (a.out_ids) step0 = *a.step;
+        if (a.pos_inc) pos0 = *a.pos_inc;
     }
 #pragma unroll
     for (int off = 32; off >= 1; off >>= 1) {
@@ -756,8 +784,15 @@ static int run(const MvArgs& a, const MvPlan& p, hipStream_t s) {
         hipError_t e = hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
         if (e != hipSuccess) return hip_fail(e, "hipFuncSetAttribute(LDS)");
     }
-    kern<<<(unsigned)p.grid, p.S * p.TC, lds, s>>>(a, p.shape());
-    if constexpr (EPI == EPI_ARGMAX) k_argmax_finish<<<1, 256, 0, s>>>(a, (int)p.grid);
+    const MvShape sh = p.shape();
+    const void* w1 = QT == TL_HIP_GGML_Q4_K ? (const void*)a.hdr : QT == TL_HIP_GGML_Q6_K ? (const void*)a.qh
+                                                                                       : (const void*)a.d;
+    kern<<<(unsigned)p.grid, p.S * p.TC, lds, s>>>(a.qs, w1, a.x, NORM ? a.norm_w : MERGE ? a.attn_rec : nullptr,
+                                                  EMBED ? a.embed_id : EPI == EPI_ROPE_KV ? a.pos : nullptr,
+                                                  (uint32_t)a.n, (uint32_t)a.nb, sh.pack(), MERGE ? a.attn_hd : 0, a);
+    if constexpr (EPI == EPI_ARGMAX)
+        k_argmax_finish<<<1, 256, 0, s>>>(a.part_v, a.part_i, a.part_nan, a.step, a.pos_inc, a.out_ids,
+                                          (int)p.grid, a);
     hipError_t e = hipGetLastError();
     return e == hipSuccess ? TL_HIP_OK : hip_fail(e, "matvec launch");
 }
@@ -867,11 +902,19 @@ bool matvec_fits(const QWeight* w, int64_t m) {
 // the loads (and the wait for them) without a store.  The time of a launch that only moves
 // the weight stream the way the matvec moves it.
 template <int QT, int BT, int RWT>
-__global__ __launch_bounds__(256) void k_read_floor(MvArgs a, MvShape sh) {
+__global__ __launch_bounds__(256) void k_read_floor(const uint8_t* __restrict__ qs, const void* __restrict__ w1,
+                                                    const int8_t* __restrict__ sc, const __half* __restrict__ d6,
+                                                    uint32_t n_p, uint32_t nb_p, uint32_t shape_p) {
     constexpr int QB = QB_<QT>::v, QW = QB / 16;
-    // the kernel arguments the loads need, fetched from the argument buffer in one round
-    asm volatile("" : : "s"(a.qs), "s"(a.d), "s"(a.hdr), "s"(a.qh), "s"(a.sc), "s"(a.n), "s"(a.nb), "s"(sh.tc),
-                 "s"(sh.tc_shift), "s"(sh.s_shift));
+    MvArgs a = {};
+    a.qs = qs;
+    a.n = n_p;
+    a.nb = nb_p;
+    a.d = QT == TL_HIP_GGML_Q6_K ? d6 : static_cast<const __half*>(w1);
+    a.hdr = static_cast<const uint8_t*>(w1);
+    a.qh = static_cast<const uint8_t*>(w1);
+    a.sc = sc;
+    const MvShape sh = MvShape::unpack(shape_p);
     const int tid = threadIdx.x;
     const int TC = sh.tc, S = 1 << sh.s_shift;
     const int tcol = sh.s_shift ? (tid & (TC - 1)) : tid;
@@ -920,15 +963,21 @@ __global__ __launch_bounds__(256) void k_read_floor(MvArgs a, MvShape sh) {
 template <int QT>
 static int run_floor(const MvArgs& a, const MvPlan& p, hipStream_t s) {
     const dim3 grid((unsigned)p.grid), block((unsigned)(p.S * p.TC));
+    const MvShape sh = p.shape();
+    const void* w1 = QT == TL_HIP_GGML_Q4_K ? (const void*)a.hdr : QT == TL_HIP_GGML_Q6_K ? (const void*)a.qh
+                                                                                       : (const void*)a.d;
+    const uint32_t n = (uint32_t)a.n, nb = (uint32_t)a.nb;
+#define TLH_FLOOR(B, R) k_read_floor<QT, B, R><<<grid, block, 0, s>>>(a.qs, w1, a.sc, a.d, n, nb, sh.pack())
     if (p.BT == 1) {
-        if (p.RWT == 8) k_read_floor<QT, 1, 8><<<grid, block, 0, s>>>(a, p.shape());
-        else if (p.RWT == 4) k_read_floor<QT, 1, 4><<<grid, block, 0, s>>>(a, p.shape());
-        else k_read_floor<QT, 1, 2><<<grid, block, 0, s>>>(a, p.shape());
+        if (p.RWT == 8) TLH_FLOOR(1, 8);
+        else if (p.RWT == 4) TLH_FLOOR(1, 4);
+        else TLH_FLOOR(1, 2);
     } else {
-        if (p.RWT == 8) k_read_floor<QT, 2, 8><<<grid, block, 0, s>>>(a, p.shape());
-        else if (p.RWT == 4) k_read_floor<QT, 2, 4><<<grid, block, 0, s>>>(a, p.shape());
-        else k_read_floor<QT, 2, 2><<<grid, block, 0, s>>>(a, p.shape());
+        if (p.RWT == 8) TLH_FLOOR(2, 8);
+        else if (p.RWT == 4) TLH_FLOOR(2, 4);
+        else TLH_FLOOR(2, 2);
     }
+#undef TLH_FLOOR
     hipError_t e = hipGetLastError();
     return e == hipSuccess ? TL_HIP_OK : hip_fail(e, "read floor launch");
 }
