@@ -595,15 +595,16 @@ struct F16qPlan {
 }  // namespace
 
 static F16qPlan plan_f16q(const QWeight* w, int64_t m, const GemmEpi& ep, const float* y) {
-    // 128 x 64 tiles when that gives at least two workgroups per CU, else 128 x 32 (twice
-    // the workgroups; measured at M = 512: 2048 x 2048 18.7 -> 15.5 us, 4096 x 4096
-    // 41.0 -> 37.3 us, while 11008 x 4096 is faster with the wide tile, 84.5 vs 101.7 us).
+    // 128 x 64 tiles when that gives at least one workgroup per CU, else 128 x 32 (twice the
+    // workgroups; measured at M = 512: 2048 x 2048 18.7 -> 15.5 us).  At 256 wide tiles the
+    // narrow tile gains nothing (Q4_0 4096 x 4096: 35.7 us wide, 36.4 narrow) and loses at long
+    // K (4096 x 11008: Q4_0 85.2 vs 91.3 us, Q8_0 99.1 vs 111.7 us); 11008 x 4096: 84.5 vs 101.7 us.
     // f16 weights (K-quants) move 3.5x the bytes per tile: 128 x 32 only when 128 x 64 would
     // leave half the CUs idle (2560 x 2048: 16.8 us wide vs 24.8 narrow; 2048 x 2048: 16.6 vs 13.5)
     constexpr int BM = 128;
     const bool f16w = (w->ggml_type == TL_HIP_GGML_Q4_K && !w->us) || w->ggml_type == TL_HIP_GGML_Q6_K;
     const int64_t wide_tiles = cdiv(m, BM) * cdiv(w->n, 64);
-    const bool wide = f16w ? wide_tiles > 128 : wide_tiles >= 512;
+    const bool wide = f16w ? wide_tiles > 128 : wide_tiles >= 256;
     // Short inputs: 32- or 64-row tiles when M fits them, and with at most one tile per CU
     // (512 tiles for M <= 32, where the K loop's latency dominates) the K range split over up
     // to 16 workgroup rows until about 512 workgroups run (the 512-token prefill's 256-tile
