@@ -8,10 +8,12 @@ the whole decoder + LM head + argmax); weights, KV cache and activations are res
 Roofline object: the dominant kernel of decode, the Q4_0 matvec, at the 4096 x 4096 shape of
 algorithmic bytes per launch (9,437,184 B of blocks + 16 KiB x + 16 KiB y) over
 the average launch duration, timed with HIP events on the launch stream while rotating over
-34 distinct weight copies (321 MB > the 256 MB Infinity Cache).
+36 distinct weight copies (341 MB > the 256 MB Infinity Cache), beside the one-launch read
+floor of the same loads (tl_hip_read_floor).
 
-CPU baseline: the oracle's restatement of the tl_cpu loops (matmul_impl order, one thread)
-for one decoder layer + the LM head at the same shapes, extrapolated to 22 layers.
+CPU baseline: the oracle's restatement of the tl_cpu loops (matmul_impl order) on one pinned
+host core: one decoder layer + the LM head at the same shapes, times 22 layers, plus the
+configs[0]-[3] legs (cold / steady matvec, row ops, a sampled GEMM, the attention op chain).
 
 Prints one JSON line on stdout; progress goes to stderr.
 """
@@ -31,10 +33,10 @@ MATVEC_N = MATVEC_K = 4096
 MATVEC_BYTES = MATVEC_N * MATVEC_K // 32 * 18 + MATVEC_K * 4 + MATVEC_N * 4  # 9,469,952 (Q4_0)
 HBM_PEAK_GBS = 8000.0
 # HBM bytes per 4096 x 4096 matvec launch from the two counter runs of
-# `bench.py --matvec-only` (FETCH_SIZE 4,710.04 KiB x 1.99820 + WRITE_SIZE 16.0 KiB x 0.99976,
-# the scale factors read off a 64 MiB device copy in the same runs): 1.019 x the
+# `bench.py --matvec-only` (FETCH_SIZE 4,711.55 KiB x 1.99893 + WRITE_SIZE 16.0 KiB x 1.0,
+# the scale factors read off a 64 MiB device copy in the same runs): 1.020 x the
 # algorithmic bytes
-MATVEC_TRAFFIC = 9_653_848
+MATVEC_TRAFFIC = 9_660_478
 
 
 def log(*a):
