@@ -145,17 +145,40 @@ def test_quant_gemm_f16_split_k(dev, t, m, nk):
 
 
 @pytest.mark.parametrize("t", [GGML_Q4_0, GGML_Q8_0])
-@pytest.mark.parametrize("m,n", [(512, 8192), (512, 8160), (300, 8192)])
+@pytest.mark.parametrize("m,n", [(512, 8192), (300, 8160), (300, 4096)])
 def test_quant_gemm_f16_tile_widths(dev, t, m, n):
-    """The f16 MFMA GEMM's two tile widths: 128 x 64 tiles when they give >= 512 workgroups
-    (512 x 8192 and a row count off the tile), 128 x 32 below that (300 rows: 3 x 128 row
-    tiles); short K keeps the oracle fast."""
+    """The f16 MFMA GEMM's two tile widths: 128 x 64 tiles when they give >= 256 workgroups
+    (512 x 8192, and 300 x 8160 with row and column counts off the tile), 128 x 32 below
+    that (300 x 4096: 3 x 64 wide tiles); short K keeps the oracle fast."""
     k = 256
     rng = np.random.default_rng(0x71530000 + m + n + t)
     raw = blocks(t, rng, n, k)
     x = rng.standard_normal((m, k)).astype(np.float32)
     ref = oracle.qtensor_matmul(x, raw, t, n)
     assert_rel(dev.tl_qtensor_matmul_f16(dev.tensor_new(x), QTensor(t, raw, (n, k))).to_numpy(), ref, F16_TOL)
+    assert _gemm_plan()[:2] == ((128, 32) if n == 4096 else (128, 64))
+
+
+@pytest.mark.parametrize("t", [GGML_Q4_0, GGML_Q8_0])
+@pytest.mark.parametrize("m", [5, 16, 32, 33, 64])
+def test_quant_gemm_f16_short_tiles_split_k(dev, t, m):
+    """Op calls with 32- or 64-row tiles and K split over workgroup rows (17 iterations of 128:
+    an uneven last range): the row tile that ran, the oracle within the f16 tolerance, and
+    the same bits from the allocation-free entry on the same inputs."""
+    n, k = 2048, 2176
+    rng = np.random.default_rng(0x71570000 + m + t)
+    raw = blocks(t, rng, n, k)
+    x = rng.standard_normal((m, k)).astype(np.float32)
+    q = QTensor(t, raw, (n, k))
+    y16 = dev.tl_qtensor_matmul_f16(dev.tensor_new(x), q).to_numpy()
+    plan = _gemm_plan()
+    assert plan[0] == (32 if m <= 32 else 64) and plan[2] > 1
+    assert_rel(y16, oracle.qtensor_matmul(x, raw, t, n), F16_TOL)
+    lib = _lib.load()
+    hw = q.upload(lib)
+    xt, yt = dev.tensor_new(x), dev.tensor_zeros((m, n))
+    assert lib.tl_hip_launch_quant_gemm_noalloc(hw, C.c_void_p(xt.data_ptr), C.c_void_p(yt.data_ptr), m, 1, None) == 0
+    assert np.array_equal(yt.to_numpy(), y16)
 
 
 def test_qtensor_matmul_shapes_and_errors(dev):

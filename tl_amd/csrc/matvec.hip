@@ -155,7 +155,6 @@ __device__ __forceinline__ float xreduce(float (&v)[N], int lane) {
     }
 }
 
-constexpr int MV_MAX_RW = 32;  // rows per workgroup
 constexpr int XPAD = 36;       // floats per staged 32-float block: lane-per-block LDS reads hit distinct banks
 // float4 per thread staged ahead of the weight loads: k <= 8192 at 256 threads in one pass;
 // with the RMSNorm prologue (norm weights staged too) k <= 4096, and k <= 2048 when a thread
@@ -249,7 +248,6 @@ __global__ __launch_bounds__(256) void k_mv(const uint8_t* __restrict__ qs_p, co
     if constexpr (QT == TL_HIP_GGML_Q6_K) asm volatile("" : : "s"(a.sc), "s"(a.d));
     extern __shared__ float xs[];  // [M][nb][XPAD] staged activations (x * norm weight with NORM)
     __shared__ float red[4][N];
-    __shared__ float ys[M][MV_MAX_RW];
     __shared__ float ssq[4][M];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int TC = sh.tc, S = 1 << sh.s_shift, RW = RWT << sh.s_shift, rw_shift = RWT_SHIFT + sh.s_shift;
@@ -524,8 +522,9 @@ __global__ __launch_bounds__(256) void k_mv(const uint8_t* __restrict__ qs_p, co
         if (tid < M * RW && row0 + (tid & (RW - 1)) < n)
             pre_res = a.res[(tid >> rw_shift) * n + row0 + (tid & (RW - 1))];
     } else if constexpr (EPI == EPI_ROPE_KV) {
-        const uint32_t r0 = row0 + 2 * tid + (uint32_t)a.row_off;
-        if (tid < RW / 2 && row0 + 2 * tid < n && r0 < (uint32_t)(a.q_rows + a.kv_rows)) {
+        // pair (row tid, row tid + 1) is rotated by the thread that forms row tid's sum
+        const uint32_t r0 = row0 + tid + (uint32_t)a.row_off;
+        if (tid < RW && (tid & 1) == 0 && row0 + tid < n && r0 < (uint32_t)(a.q_rows + a.kv_rows)) {
             const uint32_t i = (r0 < (uint32_t)a.q_rows ? r0 : r0 - a.q_rows) % (uint32_t)a.hd;
             pre_c = a.cos_t[pre_pos * a.hd + i];
             pre_s = a.sin_t[pre_pos * a.hd + i];
@@ -574,63 +573,57 @@ __global__ __launch_bounds__(256) void k_mv(const uint8_t* __restrict__ qs_p, co
                 }
             } else if constexpr (EPI == EPI_ARGMAX) {
                 row_v = acc_s;  // row tid (m = 0, RW <= 64: wavefront 0)
-            } else {
-                ys[m][rl] = acc_s;
-            }
-        }
-        if constexpr (EPI == EPI_GLU || EPI == EPI_ROPE_KV) __syncthreads();
-    }
-
-    // (5) epilogue
-    if constexpr (EPI == EPI_GLU) {
-        const uint32_t half_n = n / 2;
-        if (tid < M * (RW / 2)) {
-            const int m = tid >> (rw_shift - 1), p = tid & (RW / 2 - 1);
-            const uint32_t i = row0 / 2 + p;
-            if (i < half_n) {
-                const float g = ys[m][2 * p], u = ys[m][2 * p + 1];
-                a.y[m * half_n + i] = (g * (1.0f / (1.0f + expf(-g)))) * u;
-            }
-        }
-    } else if constexpr (EPI == EPI_ROPE_KV) {
-        const int64_t pos = pre_pos;
-        if (tid < RW / 2) {
-            const int64_t r0 = row0 + 2 * tid + a.row_off;  // row of the q | k | v projection
-            if (row0 + 2 * tid < n) {
-                const float v0 = ys[0][2 * tid], v1 = ys[0][2 * tid + 1];
-                if (r0 < a.q_rows + a.kv_rows) {
-                    const bool isq = r0 < a.q_rows;
-                    const int64_t rr = isq ? r0 : r0 - a.q_rows;
-                    const int64_t i = rr % a.hd;
-                    const float c = pre_c, s = pre_s;
-                    const float o0 = v0 * c - v1 * s, o1 = v0 * s + v1 * c;
-                    if (isq) {
-                        a.q_out[r0] = o0;
-                        a.q_out[r0 + 1] = o1;
+            } else if constexpr (EPI == EPI_GLU) {
+                // rows (2i, 2i + 1) = (gate_i, up_i) are formed in lanes tid, tid ^ 1: the gate
+                // lane takes the up value with one lane exchange (no LDS round trip, no barrier)
+                const float u = __shfl_xor(acc_s, 1, 64);
+                const uint32_t half_n = n / 2, i = row0 / 2 + (rl >> 1);
+                if ((rl & 1) == 0 && i < half_n) a.y[m * half_n + i] = (acc_s * (1.0f / (1.0f + expf(-acc_s)))) * u;
+            } else if constexpr (EPI == EPI_ROPE_KV) {
+                // dims (2j, 2j + 1) of a head are rows rl, rl + 1 (M = 1): the even lane rotates
+                // the pair and writes q or the KV cache; v rows are appended as they are
+                const float v1 = __shfl_xor(acc_s, 1, 64);
+                if ((rl & 1) == 0 && row0 + rl < n) {
+                    const float v0 = acc_s;
+                    const int64_t pos = pre_pos;
+                    const int64_t r0 = row0 + rl + a.row_off;  // row of the q | k | v projection
+                    if (r0 < a.q_rows + a.kv_rows) {
+                        const bool isq = r0 < a.q_rows;
+                        const int64_t rr = isq ? r0 : r0 - a.q_rows;
+                        const int64_t i = rr % a.hd;
+                        const float c = pre_c, sn = pre_s;
+                        const float o0 = v0 * c - v1 * sn, o1 = v0 * sn + v1 * c;
+                        if (isq) {
+                            a.q_out[r0] = o0;
+                            a.q_out[r0 + 1] = o1;
+                        } else {
+                            const int64_t off = ((rr / a.hd) * a.max_seq + pos) * a.hd + i;
+                            if (a.kv_f16) {
+                                reinterpret_cast<__half*>(a.kc)[off] = __float2half(o0);
+                                reinterpret_cast<__half*>(a.kc)[off + 1] = __float2half(o1);
+                            } else {
+                                reinterpret_cast<float*>(a.kc)[off] = o0;
+                                reinterpret_cast<float*>(a.kc)[off + 1] = o1;
+                            }
+                        }
                     } else {
+                        const int64_t rr = r0 - a.q_rows - a.kv_rows, i = rr % a.hd;
                         const int64_t off = ((rr / a.hd) * a.max_seq + pos) * a.hd + i;
                         if (a.kv_f16) {
-                            reinterpret_cast<__half*>(a.kc)[off] = __float2half(o0);
-                            reinterpret_cast<__half*>(a.kc)[off + 1] = __float2half(o1);
+                            reinterpret_cast<__half*>(a.vc)[off] = __float2half(v0);
+                            reinterpret_cast<__half*>(a.vc)[off + 1] = __float2half(v1);
                         } else {
-                            reinterpret_cast<float*>(a.kc)[off] = o0;
-                            reinterpret_cast<float*>(a.kc)[off + 1] = o1;
+                            reinterpret_cast<float*>(a.vc)[off] = v0;
+                            reinterpret_cast<float*>(a.vc)[off + 1] = v1;
                         }
-                    }
-                } else {
-                    const int64_t rr = r0 - a.q_rows - a.kv_rows, i = rr % a.hd;
-                    const int64_t off = ((rr / a.hd) * a.max_seq + pos) * a.hd + i;
-                    if (a.kv_f16) {
-                        reinterpret_cast<__half*>(a.vc)[off] = __float2half(v0);
-                        reinterpret_cast<__half*>(a.vc)[off + 1] = __float2half(v1);
-                    } else {
-                        reinterpret_cast<float*>(a.vc)[off] = v0;
-                        reinterpret_cast<float*>(a.vc)[off + 1] = v1;
                     }
                 }
             }
         }
-    } else if constexpr (EPI == EPI_ARGMAX) {
+    }
+
+    // (5) epilogue
+    if constexpr (EPI == EPI_ARGMAX) {
         // logits, penalised logits, then this workgroup's greedy candidate (the left fold of
         // tensor.rs:1633-1637 over its rows: keep the best only when strictly greater)
         // Rows 0 .. RW - 1 sit in lanes 0 .. RW - 1 of wavefront 0 (RW <= 64).  Without NaNs the
