@@ -189,8 +189,8 @@ struct QWords;
 template <>
 struct QWords<TL_HIP_GGML_Q4_0> {
     static constexpr int BYTES = 16;
-    // f16 operand of MFMA t from the block's 16 bytes: word t = bytes 4t .. 4t+3, i.e.
-    // elements 4t..4t+3 (low nibbles) and 16+4t..16+4t+3 (high nibbles), in that order.
+    // f16 operand of MFMA t from word t of raw (the block's word t = bytes 4t .. 4t+3, i.e.
+    // elements 4t..4t+3 (low nibbles) and 16+4t..16+4t+3 (high nibbles), in that order).
     // A byte holding one nibble q is, read as an OCP fp8 E4M3 value, exactly q * 2^-9, so
     // v_cvt_scalef32_pk_f16_fp8 with scale 2^9 turns two such bytes into the f16 pair (q, q')
     // (the instruction applies only the exponent of its scale, hence the separate d); then
@@ -403,10 +403,12 @@ __global__ __launch_bounds__(512) void k_qgemm_mfma(const uint8_t* __restrict__ 
     // This wavefront's half of the iteration: k-steps t = 2 kh, 2 kh + 1.  Every LDS read
     // (W quants, scale words, A fragments) is issued before the first use.
     auto compute = [&](const Stage& st) {
-        // quant data of the wavefront's rows: the whole block (4-bit types), the 16 bytes of
-        // its k half (Q8_0: words 4 kh .. 4 kh + 3), or the two operand words of its k-steps
-        // (f16 weights) -- chunks picked by the wavefront's k half at the read, so the
-        // operand build indexes its words with compile-time values only
+        // quant data of the wavefront's rows: the 8 bytes of its k half (4-bit types: words
+        // 2 kh, 2 kh + 1), the 16 bytes of its k half (Q8_0: words 4 kh .. 4 kh + 3), or the
+        // two operand words of its k-steps (f16 weights) -- picked by the wavefront's k half
+        // at the read, so the operand build indexes its words with compile-time values only
+        // (a word index computed from kh became divergent branches and selects: the compiler
+        // cannot see that kh is uniform; Q4_0 11008 x 4096 at M = 512 78.5 -> 74.8 us)
         constexpr bool Q8 = QT == TL_HIP_GGML_Q8_0;
         constexpr int NW = Q8 ? 1 : SCALED ? QC : 2;
         uint4 wr[TN][NW];
@@ -418,7 +420,12 @@ __global__ __launch_bounds__(512) void k_qgemm_mfma(const uint8_t* __restrict__ 
             for (int h = 0; h < NW; h++) {
                 const int c = Q8 ? g * QC + kh : SCALED ? g * QC + h : g * QC + 2 * kh + h;
                 const int pos = CPR == 16 ? r * 16 + (c ^ xsw(r & 15)) : (r >> 4) * 16 * CPR + c * 16 + (r & 15);
-                wr[j][h] = *reinterpret_cast<const uint4*>(&st.Wq[pos * 16]);
+                if constexpr (SCALED && !Q8) {
+                    const uint2 h2 = *reinterpret_cast<const uint2*>(&st.Wq[pos * 16 + 8 * kh]);
+                    wr[j][h] = uint4{h2.x, h2.y, 0u, 0u};
+                } else {
+                    wr[j][h] = *reinterpret_cast<const uint4*>(&st.Wq[pos * 16]);
+                }
             }
             if constexpr (SCALED) dw[j] = st.Wd[r * Q_KR + g];
         }
@@ -444,12 +451,11 @@ __global__ __launch_bounds__(512) void k_qgemm_mfma(const uint8_t* __restrict__ 
             }
         }
 #pragma unroll
-        for (int tt = 0; tt < 2; tt++) {
-            const int t = 2 * kh + tt;
+        for (int tt = 0; tt < 2; tt++) {  // k-step 2 kh + tt
 #pragma unroll
             for (int j = 0; j < TN; j++) {
                 half8 bop;
-                if constexpr (QT == TL_HIP_GGML_Q4_0 || K4) bop = QWords<QT>::operand(wr[j][0], t, d2[j], m8d2[j]);
+                if constexpr (QT == TL_HIP_GGML_Q4_0 || K4) bop = QWords<QT>::operand(wr[j][0], tt, d2[j], m8d2[j]);
                 else if constexpr (QT == TL_HIP_GGML_Q8_0) bop = QWords<QT>::operand(wr[j][0], tt, d2[j]);
                 else bop = __builtin_bit_cast(half8, wr[j][tt]);
 #pragma unroll
