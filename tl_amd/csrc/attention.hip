@@ -101,7 +101,7 @@ __global__ __launch_bounds__(256) void k_attn(AttnArgs a) {
     __shared__ float stat[G][2];
     __shared__ float part[4][G][D];
     const int split = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform: SGPR
     const int grp = lane >> 3, sub = lane & 7;
     int64_t L = a.len.of(b);
     if (L > a.lmax) L = a.lmax;
@@ -393,7 +393,7 @@ __global__ __launch_bounds__(256) void k_attn_gq(AttnArgs a) {
     __shared__ float stat[G][2];
     __shared__ float part[4][G][D];
     const int split = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform: SGPR
     const int kl = lane % LPR, kr = lane / LPR;
     int64_t L = a.len.of(b);
     if (L > a.lmax) L = a.lmax;
@@ -584,7 +584,7 @@ __global__ __launch_bounds__(64 * W) void k_attn_qh(const float* __restrict__ q_
     __shared__ float wo[W][D];
     const int qh = blockIdx.x, b = blockIdx.y;
     const int h = qh / G;
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform: SGPR
     const int kl = lane % LPR, kr = lane / LPR;  // K: slice and row within an instruction
     const int slot = lane & 7, dg = lane >> 3;   // V: position slot and dim group
     const int hq = a.hkv * G;
@@ -734,7 +734,7 @@ __global__ __launch_bounds__(256) void k_attn_prefill(const float* __restrict__ 
     constexpr int CPR = D / 8;    // 16-byte chunks per K row
     __shared__ __attribute__((aligned(16))) _Float16 Ks[KT * D];  // row-major, chunk c of row r at c ^ (r & (CPR - 1))
     __shared__ __attribute__((aligned(16))) _Float16 Vt[D * KT];  // [dim][pos], 8-byte run j of dim d at j ^ (d & 15)
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform: SGPR
     const int col = lane & 15, g = lane >> 4;
     const int qb = blockIdx.x, h = blockIdx.y;
     const int hq = hkv * G;
@@ -1324,7 +1324,7 @@ __global__ __launch_bounds__(256) void k_sdpa(const float* __restrict__ q, const
     __shared__ float red[4];
     const int64_t row = blockIdx.x;  // slice * sq + i
     const int64_t slice = row / sq, i = row - slice * sq;
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform: SGPR
     const float* kb = k + slice * sk * dk;
     const float* vb = v + slice * sk * dv;
     float* s = sc + row * sk;

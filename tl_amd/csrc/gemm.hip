@@ -344,7 +344,10 @@ __global__ __launch_bounds__(512) void k_qgemm_mfma(const uint8_t* __restrict__ 
         uint32_t Wd[SCALED ? BN * Q_KR : 1];  // aligned word holding the scale
     };
     __shared__ __attribute__((aligned(16))) Stage S0, S1;
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    // the wavefront index in a scalar register: the compiler cannot see that tid >> 6 is
+    // uniform, and every quantity derived from it (k half, sub-tile, DMA slots, LDS
+    // addresses) would otherwise sit in vector registers behind divergent branches
+    const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int sub = wave & 3, kh = wave >> 2;  // output sub-tile, k half
     const int wm = sub >> 1, wn = sub & 1, col = lane & 15, g = lane >> 4;
     const int64_t nt = (n + BN - 1) / BN;

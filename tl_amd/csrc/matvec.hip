@@ -249,7 +249,7 @@ __global__ __launch_bounds__(256) void k_mv(const uint8_t* __restrict__ qs_p, co
     extern __shared__ float xs[];  // [M][nb][XPAD] staged activations (x * norm weight with NORM)
     __shared__ float red[4][N];
     __shared__ float ssq[4][M];
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform: SGPR
     const int TC = sh.tc, S = 1 << sh.s_shift, RW = RWT << sh.s_shift, rw_shift = RWT_SHIFT + sh.s_shift;
     const int tcol = sh.s_shift ? (tid & (TC - 1)) : tid;
     const int sub = sh.s_shift ? (tid >> sh.tc_shift) : 0;
@@ -675,7 +675,7 @@ __global__ __launch_bounds__(256) void k_argmax_finish(float* part_v, int32_t* p
     a.step = step;
     a.pos_inc = pos_inc;
     a.out_ids = out_ids;
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform: SGPR
     float bv = -INFINITY;
     int bi = -1, nan = 0;
     for (int i = tid; i < nwg; i += 256) {
