@@ -252,7 +252,7 @@ __global__ __launch_bounds__(256) void k_mv(const uint8_t* __restrict__ qs_p, co
     const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform: SGPR
     const int TC = sh.tc, S = 1 << sh.s_shift, RW = RWT << sh.s_shift, rw_shift = RWT_SHIFT + sh.s_shift;
     const int tcol = sh.s_shift ? (tid & (TC - 1)) : tid;
-    const int sub = sh.s_shift ? (tid >> sh.tc_shift) : 0;
+    const int sub = sh.s_shift ? __builtin_amdgcn_readfirstlane(tid >> sh.tc_shift) : 0;  // TC >= 64: uniform
     const int wps = TC >> 6;  // wavefronts per row subset
     const uint32_t nb = (uint32_t)a.nb, k = (uint32_t)a.k, n = (uint32_t)a.n;
     const uint32_t row0 = blockIdx.x * (uint32_t)RW;
@@ -911,7 +911,7 @@ __global__ __launch_bounds__(256) void k_read_floor(const uint8_t* __restrict__ 
     const int tid = threadIdx.x;
     const int TC = sh.tc, S = 1 << sh.s_shift;
     const int tcol = sh.s_shift ? (tid & (TC - 1)) : tid;
-    const int sub = sh.s_shift ? (tid >> sh.tc_shift) : 0;
+    const int sub = sh.s_shift ? __builtin_amdgcn_readfirstlane(tid >> sh.tc_shift) : 0;  // TC >= 64: uniform
     const uint32_t nb = (uint32_t)a.nb, n = (uint32_t)a.n;
     const uint32_t my_row0 = blockIdx.x * (uint32_t)(RWT << sh.s_shift) + sub;
     uint32_t acc = 0;
