@@ -638,8 +638,12 @@ static F16qPlan plan_f16q(const QWeight* w, int64_t m, const GemmEpi& ep, const 
 // part_ws / noalloc: the split-K partials go to the caller's workspace and nothing is
 // allocated (weights that need an f16 copy are then rejected); otherwise the allocator
 // provides the workspace.
+// defer_part: a split-K launch leaves its nsp partial tiles (m x n floats each, in K order) in
+// a buffer handed to the caller (*defer_part, *defer_nsp; the caller adds them -- plus ep.res
+// for the residual epilogue -- and frees the buffer with dev_free_on on s); an unsplit launch
+// applies the epilogue as usual and returns *defer_part = nullptr, *defer_nsp = 1.
 int launch_gemm_f16q(const QWeight* w, const _Float16* x16, float* y, int64_t m, const GemmEpi& ep,
-                     hipStream_t s, bool noalloc, float* part_ws) {
+                     hipStream_t s, bool noalloc, float* part_ws, float** defer_part, int* defer_nsp) {
     if (m < 1) return TL_HIP_OK;
     if (w->nb % Q_KR != 0 || (ep.mode == GEMM_GLU16 && (w->n % 64 != 0))) {
         set_error(TL_HIP_ERR_ARG, "ArgumentError: the f16 GEMM takes K in steps of 128 (SwiGLU output: N in steps "
@@ -657,6 +661,11 @@ int launch_gemm_f16q(const QWeight* w, const _Float16* x16, float* y, int64_t m,
     const int bm = plan.bm;
     const bool wide = plan.wide;
     const int64_t tiles = plan.tiles, nsp = plan.nsp;
+    const bool defer = defer_part && nsp > 1 && !noalloc;
+    if (defer_part) {
+        *defer_part = nullptr;
+        *defer_nsp = 1;
+    }
     tls_plan[0] = bm;
     tls_plan[1] = wide ? 64 : 32;
     tls_plan[2] = (int)nsp;
@@ -677,7 +686,7 @@ int launch_gemm_f16q(const QWeight* w, const _Float16* x16, float* y, int64_t m,
         else if (bm == 32) k_qgemm_mfma<QT, 32, 32><<<grid, 512, 0, s>>>(q, d, x16, out, m, w->n, w->k, w->nb, pe);
         else if (bm == 64) k_qgemm_mfma<QT, 64, 32><<<grid, 512, 0, s>>>(q, d, x16, out, m, w->n, w->k, w->nb, pe);
         else k_qgemm_mfma<QT, BM, 32><<<grid, 512, 0, s>>>(q, d, x16, out, m, w->n, w->k, w->nb, pe);
-        if (nsp > 1) {
+        if (nsp > 1 && !defer) {
             const int64_t mn = m * w->n;
             k_splitk_sum<<<(unsigned)cdiv(cdiv(mn, 4), 256), 256, 0, s>>>(
                 part, y, ep.mode == GEMM_RES ? ep.res : nullptr, mn, (int)nsp);
@@ -703,9 +712,23 @@ int launch_gemm_f16q(const QWeight* w, const _Float16* x16, float* y, int64_t m,
     } else {
         gemm(std::integral_constant<int, TL_HIP_GGML_Q8_0>{}, w->qs, w->d);
     }
-    if (part && !noalloc) dev_free_on(part, s);  // freed on s: reused at once only by later work on s
+    if (defer) {
+        *defer_part = part;
+        *defer_nsp = (int)nsp;
+    } else if (part && !noalloc) {
+        dev_free_on(part, s);  // freed on s: reused at once only by later work on s
+    }
     hipError_t e = hipGetLastError();
     return e == hipSuccess ? TL_HIP_OK : hip_fail(e, "quant gemm launch");
+}
+
+// y = res + sum of the nsp partial slices (m n floats each) in slice order: the sum a
+// deferred split-K GEMM leaves to its caller.
+int launch_splitk_sum(const float* part, float* y, const float* res, int64_t mn, int nsp, hipStream_t s) {
+    if (mn <= 0) return TL_HIP_OK;
+    k_splitk_sum<<<(unsigned)cdiv(cdiv(mn, 4), 256), 256, 0, s>>>(part, y, res, mn, nsp);
+    hipError_t e = hipGetLastError();
+    return e == hipSuccess ? TL_HIP_OK : hip_fail(e, "split-K sum launch");
 }
 
 int launch_quant_gemm(const QWeight* w, const float* x, float* y, int64_t m, hipStream_t s,

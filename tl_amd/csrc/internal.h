@@ -184,8 +184,12 @@ int f16q_order(int ggml_type);  // the operand order the f16 GEMM of this weight
 int launch_x_to_f16q(const float* x, _Float16* x16, int64_t m, int64_t k, int order, hipStream_t s);
 // K a multiple of 128 (TL_HIP_ERR_ARG otherwise); GLU16 also needs N a multiple of 64.
 // noalloc: split-K partials in part_ws (sized by the caller), nothing allocated.
+// defer_part: a split-K launch hands its partial slices to the caller instead of summing
+// them (see gemm.hip); launch_splitk_sum or launch_rmsnorm_f16q's summing form adds them.
 int launch_gemm_f16q(const QWeight* w, const _Float16* x16, float* y, int64_t m, const GemmEpi& ep,
-                     hipStream_t s, bool noalloc = false, float* part_ws = nullptr);
+                     hipStream_t s, bool noalloc = false, float* part_ws = nullptr, float** defer_part = nullptr,
+                     int* defer_nsp = nullptr);
+int launch_splitk_sum(const float* part, float* y, const float* res, int64_t mn, int nsp, hipStream_t s);
 // Q4_K weights: builds w->us (4 bytes per 32 weights) on stream s, after which the f16 GEMM
 // dequantizes them in registers like Q4_0 instead of through an f16 copy per call.
 int q4k_build_unit_scales(QWeight* w, hipStream_t s);
@@ -196,9 +200,11 @@ int launch_matmul_f32(const float* a, const float* b, float* c, int64_t batch, i
 int launch_rmsnorm(const float* x, const float* r, const float* w, float* out, int64_t rows,
                    int64_t n, float eps, int mode, hipStream_t s);
 // mode-0 RMSNorm of [rows, n] written as f16 in GEMM operand order `order` (n % 32 == 0,
-// n <= 8192): the value launch_rmsnorm produces, rounded once.
-int launch_rmsnorm_f16q(const float* x, const float* w, _Float16* out16, int64_t rows, int64_t n, float eps,
-                        int order, hipStream_t s);
+// n <= 8192): the value launch_rmsnorm produces, rounded once.  With part (nsp slices of
+// rows * n floats from a deferred split-K GEMM), x first becomes x + the slices in order --
+// written back, as launch_splitk_sum would -- and that row is normalised.
+int launch_rmsnorm_f16q(float* x, const float* w, _Float16* out16, int64_t rows, int64_t n, float eps, int order,
+                        hipStream_t s, const float* part = nullptr, int nsp = 0);
 int launch_swiglu(const float* g, const float* u, float* o, int64_t n, int mode, hipStream_t s);
 int launch_softmax(const float* x, float* out, int64_t outer, int64_t as, int64_t inner,
                    hipStream_t s);

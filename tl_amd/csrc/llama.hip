@@ -370,18 +370,43 @@ static bool fused_layer_ok(const Llama* m, int l) {
     return m->wo[l]->nb % 4 == 0 && wgu->nb % 4 == 0 && m->wdown[l]->nb % 4 == 0;
 }
 
-// the f16 GEMM of a prefill; a Q4_K weight gets its unit scales on first use
-static int gemm16(QWeight* w, const _Float16* x16, float* y, int n, const GemmEpi& ep, hipStream_t s) {
+// the f16 GEMM of a prefill; a Q4_K weight gets its unit scales on first use.  With pend, a
+// split-K launch leaves its partial slices there instead of summing them into y.
+struct Pending {
+    float* part = nullptr;  // nsp slices of [n, D] still to be added (with the residual) into x
+    int nsp = 0;
+};
+static int gemm16(QWeight* w, const _Float16* x16, float* y, int n, const GemmEpi& ep, hipStream_t s,
+                  Pending* pend = nullptr) {
     const int rc = q4k_build_unit_scales(w, s);
-    return rc ? rc : launch_gemm_f16q(w, x16, y, n, ep, s);
+    if (rc) return rc;
+    return pend ? launch_gemm_f16q(w, x16, y, n, ep, s, false, nullptr, &pend->part, &pend->nsp)
+                : launch_gemm_f16q(w, x16, y, n, ep, s);
 }
 
-static int prefill_layer_fused(Llama* m, int l, int n, hipStream_t s) {
+// x += pending partial slices (the residual GEMM's deferred split-K sum), then free them
+static int flush_pending(Pending& p, float* x, int64_t mn, hipStream_t s) {
+    if (!p.part) return TL_HIP_OK;
+    const int rc = launch_splitk_sum(p.part, x, x, mn, p.nsp, s);
+    dev_free_on(p.part, s);
+    p = Pending{};
+    return rc;
+}
+
+// A residual GEMM that splits K (the o-projection and down projection at short prompts, and
+// at 512 tokens, where they have one tile per CU) leaves its partial slices to the RMSNorm
+// that reads the residual next: that kernel adds them into x in slice order -- the split-K
+// sum's own additions -- and normalises the row, one launch instead of two.  The down
+// projection's slices are carried to the next layer's first RMSNorm (pend).
+static int prefill_layer_fused(Llama* m, int l, int n, hipStream_t s, Pending& pend) {
     const int64_t D = m->D, qkv_w = D + 2 * (int64_t)m->KV * m->hd;
     const GemmEpi plain{GEMM_PLAIN, nullptr, nullptr, 0}, res{GEMM_RES, m->x, nullptr, 0};
     int rc;
     const int oq = f16q_order(m->qkv_segs[l][0].w->ggml_type);
-    if ((rc = launch_rmsnorm_f16q(m->x, m->attn_norm[l], m->xa16, n, D, m->eps, oq, s))) return rc;
+    rc = launch_rmsnorm_f16q(m->x, m->attn_norm[l], m->xa16, n, D, m->eps, oq, s, pend.part, pend.nsp);
+    if (pend.part) dev_free_on(pend.part, s);
+    pend = Pending{};
+    if (rc) return rc;
     if (m->qkv_segs[l].size() == 1) {
         if ((rc = gemm16(m->qkv_segs[l][0].w, m->xa16, m->qkv, n, plain, s))) return rc;
     } else {
@@ -393,12 +418,15 @@ static int prefill_layer_fused(Llama* m, int l, int n, hipStream_t s) {
     }
     prefill_rope_kv(m, l, n, s);
     if ((rc = prefill_attention(m, l, n, 1, m->xa16, f16q_order(m->wo[l]->ggml_type), s))) return rc;
-    if ((rc = gemm16(m->wo[l], m->xa16, m->x, n, res, s))) return rc;
-    if ((rc = launch_rmsnorm_f16q(m->x, m->ffn_norm[l], m->xa16, n, D, m->eps, f16q_order(m->wgu[l]->ggml_type), s)))
-        return rc;
+    Pending op;
+    if ((rc = gemm16(m->wo[l], m->xa16, m->x, n, res, s, &op))) return rc;
+    rc = launch_rmsnorm_f16q(m->x, m->ffn_norm[l], m->xa16, n, D, m->eps, f16q_order(m->wgu[l]->ggml_type), s, op.part,
+                             op.nsp);
+    if (op.part) dev_free_on(op.part, s);
+    if (rc) return rc;
     const GemmEpi glu{GEMM_GLU16, nullptr, m->xb16, f16q_order(m->wdown[l]->ggml_type)};
     if ((rc = gemm16(m->wgu[l], m->xa16, nullptr, n, glu, s))) return rc;
-    return gemm16(m->wdown[l], m->xb16, m->x, n, res, s);
+    return gemm16(m->wdown[l], m->xb16, m->x, n, res, s, &pend);
 }
 
 // Enqueues one forward over n tokens whose ids are already in m->ids (device); leaves the
@@ -408,11 +436,18 @@ static int enqueue_forward(Llama* m, int n, int f16, hipStream_t s) {
     const int64_t qkv_w = D + 2 * (int64_t)m->KV * m->hd;
     int rc;
     k_embed<<<cdiv(n * D, 256), 256, 0, s>>>(m->emb, m->ids, m->x, n, D);
+    Pending pend;  // a fused layer's deferred down-projection sum
+    struct Guard {  // frees undelivered partial slices on an error return
+        Pending& p;
+        hipStream_t s;
+        ~Guard() { if (p.part) dev_free_on(p.part, s); }
+    } guard{pend, s};
     for (int l = 0; l < m->nl; l++) {
         if (f16 && n > 4 && fused_layer_ok(m, l)) {
-            if ((rc = prefill_layer_fused(m, l, n, s))) return rc;
+            if ((rc = prefill_layer_fused(m, l, n, s, pend))) return rc;
             continue;
         }
+        if ((rc = flush_pending(pend, m->x, (int64_t)n * D, s))) return rc;
         if ((rc = launch_rmsnorm(m->x, nullptr, m->attn_norm[l], m->h, n, D, m->eps, 0, s))) return rc;
         if (m->qkv_segs[l].size() == 1) {
             if ((rc = linear(m->qkv_segs[l][0].w, m->h, m->qkv, n, nullptr, nullptr, f16, s))) return rc;
@@ -439,6 +474,7 @@ static int enqueue_forward(Llama* m, int n, int f16, hipStream_t s) {
         }
         if ((rc = linear(m->wdown[l], m->act, m->x, n, m->x, m->t, f16, s))) return rc;
     }
+    if ((rc = flush_pending(pend, m->x, (int64_t)n * D, s))) return rc;
     k_advance<<<1, 64, 0, s>>>(m->pos, n);
     if ((rc = launch_rmsnorm(m->x + (int64_t)(n - 1) * D, nullptr, m->out_norm, m->h, 1, D, m->eps, 0, s))) return rc;
     if ((rc = launch_quant_matvec(m->lm, m->h, m->logits, 1, s, nullptr))) return rc;

@@ -133,24 +133,43 @@ __global__ __launch_bounds__(256) void k_rmsnorm_generic(const float* __restrict
 // RMSNorm mode 0 whose output goes straight to the f16 operand order of the GEMM that reads
 // it (the same f32 value as k_rmsnorm, rounded once to f16): the sum of squares in k_rmsnorm's
 // order (thread j's float4 j, j + 256, ...), then one 8-half word per (block, t) unit.
-template <int V>
-__global__ __launch_bounds__(256) void k_rmsnorm_f16q(const float* __restrict__ x, const float* __restrict__ w,
+// SUM: the row is first completed from a deferred split-K GEMM -- x = x + part_0 + ... +
+// part_{nsp-1} in slice order, the additions of k_splitk_sum -- written back to x (the new
+// residual) and kept in LDS for the normalisation: one launch instead of the sum's and this.
+template <int V, bool SUM = false>
+__global__ __launch_bounds__(256) void k_rmsnorm_f16q(float* __restrict__ x, const float* __restrict__ w,
                                                       _Float16* __restrict__ out16, int64_t n, float eps,
-                                                      int order) {
+                                                      int order, const float* __restrict__ part, int nsp,
+                                                      int64_t mn) {
     asm volatile("" : : "s"(x), "s"(w), "s"(out16), "s"(n), "s"(eps), "s"(order));  // arguments in one round
     __shared__ float red[4];
+    __shared__ float4 rowbuf[SUM ? V * 256 : 1];
     const int64_t row = blockIdx.x;
-    const float* xr = x + row * n;
-    const float4* x4 = reinterpret_cast<const float4*>(xr);
+    float* xr = x + row * n;
+    float4* x4 = reinterpret_cast<float4*>(xr);
     const int64_t n4 = n >> 2;
     float ss = 0.f;
 #pragma unroll
     for (int i = 0; i < V; i++) {
         const int64_t j = threadIdx.x + (int64_t)i * 256;
-        const float4 v = j < n4 ? x4[j] : make_float4(0.f, 0.f, 0.f, 0.f);
+        float4 v = j < n4 ? x4[j] : make_float4(0.f, 0.f, 0.f, 0.f);
+        if constexpr (SUM) {
+            if (j < n4) {
+                const float4* p4 = reinterpret_cast<const float4*>(part + row * n) + j;
+                for (int p = 0; p < nsp; p++) {
+                    const float4 t = p4[p * (mn >> 2)];
+                    v.x += t.x;
+                    v.y += t.y;
+                    v.z += t.z;
+                    v.w += t.w;
+                }
+                x4[j] = v;
+                rowbuf[j] = v;
+            }
+        }
         ss += v.x * v.x + v.y * v.y + v.z * v.z + v.w * v.w;
     }
-    ss = block_sum(ss, red);
+    ss = block_sum(ss, red);  // its barriers also publish rowbuf
     const float rms = sqrtf(ss / (float)n + eps);
     const int64_t units = (n >> 5) * 4;
     const float4* w4 = reinterpret_cast<const float4*>(w);
@@ -159,7 +178,7 @@ __global__ __launch_bounds__(256) void k_rmsnorm_f16q(const float* __restrict__ 
         const int64_t b = u >> 2;
         const int t = (int)(u & 3);
         const int64_t i0 = order == F16Q_Q8 ? 8 * b + 2 * t : 8 * b + t, i1 = order == F16Q_Q8 ? i0 + 1 : i0 + 4;
-        const float4 e = x4[i0], f = x4[i1], we = w4[i0], wf = w4[i1];
+        const float4 e = SUM ? rowbuf[i0] : x4[i0], f = SUM ? rowbuf[i1] : x4[i1], we = w4[i0], wf = w4[i1];
         const float v[8] = {(e.x / rms) * we.x, (e.y / rms) * we.y, (e.z / rms) * we.z, (e.w / rms) * we.w,
                             (f.x / rms) * wf.x, (f.y / rms) * wf.y, (f.z / rms) * wf.z, (f.w / rms) * wf.w};
         half8 h;
@@ -174,18 +193,24 @@ __global__ __launch_bounds__(256) void k_rmsnorm_f16q(const float* __restrict__ 
     }
 }
 
-int launch_rmsnorm_f16q(const float* x, const float* w, _Float16* out16, int64_t rows, int64_t n, float eps,
-                        int order, hipStream_t s) {
+int launch_rmsnorm_f16q(float* x, const float* w, _Float16* out16, int64_t rows, int64_t n, float eps, int order,
+                        hipStream_t s, const float* part, int nsp) {
     if (rows <= 0) return TL_HIP_OK;
     const int64_t per = cdiv(n / 4, 256);
-    if (n % 32 != 0 || per > 8 || (uintptr_t)x % 16 != 0 || !w || (uintptr_t)w % 16 != 0) {
+    if (n % 32 != 0 || per > 8 || (uintptr_t)x % 16 != 0 || !w || (uintptr_t)w % 16 != 0 ||
+        (part && ((uintptr_t)part % 16 != 0 || nsp < 1))) {
         set_error(TL_HIP_ERR_ARG, "ArgumentError: f16 operand-order RMSNorm takes rows of 32k <= 8192 floats");
         return TL_HIP_ERR_ARG;
     }
-    if (per <= 1) k_rmsnorm_f16q<1><<<rows, 256, 0, s>>>(x, w, out16, n, eps, order);
-    else if (per <= 2) k_rmsnorm_f16q<2><<<rows, 256, 0, s>>>(x, w, out16, n, eps, order);
-    else if (per <= 4) k_rmsnorm_f16q<4><<<rows, 256, 0, s>>>(x, w, out16, n, eps, order);
-    else k_rmsnorm_f16q<8><<<rows, 256, 0, s>>>(x, w, out16, n, eps, order);
+    const int64_t mn = rows * n;
+#define TLH_RN(VV)                                                                                      \
+    if (part) k_rmsnorm_f16q<VV, true><<<rows, 256, 0, s>>>(x, w, out16, n, eps, order, part, nsp, mn); \
+    else k_rmsnorm_f16q<VV><<<rows, 256, 0, s>>>(x, w, out16, n, eps, order, nullptr, 0, mn)
+    if (per <= 1) TLH_RN(1);
+    else if (per <= 2) TLH_RN(2);
+    else if (per <= 4) TLH_RN(4);
+    else TLH_RN(8);
+#undef TLH_RN
     hipError_t e = hipGetLastError();
     return e == hipSuccess ? TL_HIP_OK : hip_fail(e, "rmsnorm launch");
 }
