@@ -691,15 +691,20 @@ __global__ __launch_bounds__(64 * W) void k_attn_qh(const float* __restrict__ q_
         const float f = act ? __builtin_amdgcn_exp2f(mw - M) : 0.f;
         const float den = wave_sum64(act ? f * wl[lane] : 0.f);
         if (lane < W) wf[lane] = rec ? f : f / den;
-        if (rec && lane == 0) *reinterpret_cast<float4*>(rec + D) = float4{M, den, 0.f, 0.f};
+        if (rec && lane == 0) {
+            st_wt(rec + D, M);
+            st_wt(rec + D + 1, den);
+            st_wt(rec + D + 2, 0.f);
+            st_wt(rec + D + 3, 0.f);
+        }
     }
     __syncthreads();
     for (int d = tid; d < D; d += 64 * W) {
         float num = 0.f;
 #pragma unroll
         for (int w = 0; w < W; w++) num = fmaf(wo[w][d], wf[w], num);
-        if (rec) rec[d] = num;
-        else a.out[((int64_t)b * hq + qh) * D + d] = num;
+        if (rec) st_wt(rec + d, num);
+        else st_wt(a.out + ((int64_t)b * hq + qh) * D + d, num);
     }
 }
 

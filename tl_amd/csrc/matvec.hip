@@ -297,7 +297,7 @@ __global__ __launch_bounds__(256) void k_mv(const uint8_t* __restrict__ qs_p, co
                 const uint32_t blk = __umul24(row, nb) + bc[i];
                 const uint4* p = reinterpret_cast<const uint4*>(a.qs + (size_t)blk * QB);
 #pragma unroll
-                for (int c = 0; c < QW; c++) w[i][r][c] = p[c];
+                for (int c = 0; c < QW; c++) w[i][r][c] = ld_stream(p + c);
                 if constexpr (K4) {
                     kh[i][r] = reinterpret_cast<const uint4*>(a.hdr)[blk >> 3];
                 } else if constexpr (K6) {
@@ -569,7 +569,7 @@ __global__ __launch_bounds__(256) void k_mv(const uint8_t* __restrict__ qs_p, co
                 if (row < n) {
                     float v = acc_s;
                     if constexpr (EPI == EPI_RES) v = pre_res + v;
-                    a.y[m * n + row] = v;
+                    st_wt(a.y + m * n + row, v);
                 }
             } else if constexpr (EPI == EPI_ARGMAX) {
                 row_v = acc_s;  // row tid (m = 0, RW <= 64: wavefront 0)
@@ -578,7 +578,7 @@ __global__ __launch_bounds__(256) void k_mv(const uint8_t* __restrict__ qs_p, co
                 // lane takes the up value with one lane exchange (no LDS round trip, no barrier)
                 const float u = __shfl_xor(acc_s, 1, 64);
                 const uint32_t half_n = n / 2, i = row0 / 2 + (rl >> 1);
-                if ((rl & 1) == 0 && i < half_n) a.y[m * half_n + i] = (acc_s * (1.0f / (1.0f + expf(-acc_s)))) * u;
+                if ((rl & 1) == 0 && i < half_n) st_wt(a.y + m * half_n + i, (acc_s * (1.0f / (1.0f + expf(-acc_s)))) * u);
             } else if constexpr (EPI == EPI_ROPE_KV) {
                 // dims (2j, 2j + 1) of a head are rows rl, rl + 1 (M = 1): the even lane rotates
                 // the pair and writes q or the KV cache; v rows are appended as they are
@@ -594,27 +594,27 @@ __global__ __launch_bounds__(256) void k_mv(const uint8_t* __restrict__ qs_p, co
                         const float c = pre_c, sn = pre_s;
                         const float o0 = v0 * c - v1 * sn, o1 = v0 * sn + v1 * c;
                         if (isq) {
-                            a.q_out[r0] = o0;
-                            a.q_out[r0 + 1] = o1;
+                            st_wt(a.q_out + r0, o0);
+                            st_wt(a.q_out + r0 + 1, o1);
                         } else {
                             const int64_t off = ((rr / a.hd) * a.max_seq + pos) * a.hd + i;
                             if (a.kv_f16) {
-                                reinterpret_cast<__half*>(a.kc)[off] = __float2half(o0);
-                                reinterpret_cast<__half*>(a.kc)[off + 1] = __float2half(o1);
+                                st_wt(reinterpret_cast<__half*>(a.kc) + off, __float2half(o0));
+                                st_wt(reinterpret_cast<__half*>(a.kc) + off + 1, __float2half(o1));
                             } else {
-                                reinterpret_cast<float*>(a.kc)[off] = o0;
-                                reinterpret_cast<float*>(a.kc)[off + 1] = o1;
+                                st_wt(reinterpret_cast<float*>(a.kc) + off, o0);
+                                st_wt(reinterpret_cast<float*>(a.kc) + off + 1, o1);
                             }
                         }
                     } else {
                         const int64_t rr = r0 - a.q_rows - a.kv_rows, i = rr % a.hd;
                         const int64_t off = ((rr / a.hd) * a.max_seq + pos) * a.hd + i;
                         if (a.kv_f16) {
-                            reinterpret_cast<__half*>(a.vc)[off] = __float2half(v0);
-                            reinterpret_cast<__half*>(a.vc)[off + 1] = __float2half(v1);
+                            st_wt(reinterpret_cast<__half*>(a.vc) + off, __float2half(v0));
+                            st_wt(reinterpret_cast<__half*>(a.vc) + off + 1, __float2half(v1));
                         } else {
-                            reinterpret_cast<float*>(a.vc)[off] = v0;
-                            reinterpret_cast<float*>(a.vc)[off + 1] = v1;
+                            st_wt(reinterpret_cast<float*>(a.vc) + off, v0);
+                            st_wt(reinterpret_cast<float*>(a.vc) + off + 1, v1);
                         }
                     }
                 }
@@ -634,9 +634,9 @@ __global__ __launch_bounds__(256) void k_mv(const uint8_t* __restrict__ qs_p, co
             const bool live = lane < RW && row < n;
             float v = row_v;
             if (live) {
-                a.y[row] = v;
+                st_wt(a.y + row, v);
                 if (pre_seen) v = v > 0.0f ? v / a.penalty : v * a.penalty;
-                a.plogits[row] = v;
+                st_wt(a.plogits + row, v);
             }
             float bv = live ? v : -INFINITY;
             int bi = live ? lane : -1, nan = live && v != v;
@@ -651,9 +651,9 @@ __global__ __launch_bounds__(256) void k_mv(const uint8_t* __restrict__ qs_p, co
                 nan |= __shfl_xor(nan, off, 64);
             }
             if (lane == 0) {
-                a.part_v[blockIdx.x] = bv;
-                a.part_i[blockIdx.x] = (int32_t)(row0 + bi);
-                a.part_nan[blockIdx.x] = nan;
+                st_wt(a.part_v + blockIdx.x, bv);
+                st_wt(a.part_i + blockIdx.x, (int32_t)(row0 + bi));
+                st_wt(a.part_nan + blockIdx.x, (int32_t)nan);
             }
         }
     }
@@ -725,13 +725,13 @@ __global__ __launch_bounds__(256) void k_argmax_finish(float* part_v, int32_t* p
             for (int64_t i = 1; i < a.n; i++)
                 if (!(a.plogits[bi] > a.plogits[i])) bi = (int)i;
         }
-        *a.tok_out = bi;
+        st_wt(a.tok_out, (int32_t)bi);
         if (a.out_ids) {
-            if (step0 < a.max_out) a.out_ids[step0] = bi;
-            *a.step = step0 + 1;
+            if (step0 < a.max_out) st_wt(a.out_ids + step0, (int32_t)bi);
+            st_wt(a.step, (int32_t)(step0 + 1));
         }
-        if (a.seen_out) a.seen_out[bi] = 1;
-        if (a.pos_inc) *a.pos_inc = pos0 + 1;
+        if (a.seen_out) st_wt(a.seen_out + bi, (uint8_t)1);
+        if (a.pos_inc) st_wt(a.pos_inc, (int32_t)(pos0 + 1));
     }
 }
 
@@ -929,7 +929,7 @@ __global__ __launch_bounds__(256) void k_read_floor(const uint8_t* __restrict__ 
                 const uint32_t blk = __umul24(row, nb) + b;
                 const uint4* p = reinterpret_cast<const uint4*>(a.qs + (size_t)blk * QB);
 #pragma unroll
-                for (int c = 0; c < QW; c++) w[i][r][c] = p[c];
+                for (int c = 0; c < QW; c++) w[i][r][c] = ld_stream(p + c);
                 if constexpr (QT == TL_HIP_GGML_Q4_K) {
                     extra[i][r] = reinterpret_cast<const uint4*>(a.hdr)[blk >> 3];
                 } else if constexpr (QT == TL_HIP_GGML_Q6_K) {
