@@ -2,8 +2,9 @@
 
 Headline (BASELINE.json metric, configs[4]): greedy decode tokens/s at batch 1 of a
 random-init TinyLlama-shape Q4_0 decoder (22 layers, d_model 2048, 32/4 heads, FFN 5632,
-vocab 32000) after a 512-token prompt.  A step is one decoded token (one hipGraph replay of
-the whole decoder + LM head + argmax); weights, KV cache and activations are resident in HBM.
+vocab 32000) after a 512-token prompt.  A step is one decoded token (the whole decoder + LM
+head + argmax, replayed from hipGraphs that hold eight steps each); weights, KV cache and
+activations are resident in HBM.
 
 Roofline object: the dominant kernel of decode, the Q4_0 matvec, at the 4096 x 4096 shape of
 algorithmic bytes per launch (9,437,184 B of blocks + 16 KiB x + 16 KiB y) over

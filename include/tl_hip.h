@@ -337,9 +337,10 @@ int tl_hip_llama_configure(tl_hip_llama* m, int kv_f16, int rope_per_token);
 int tl_hip_llama_reset(tl_hip_llama* m);
 /* Number of cached positions (the chatbot's start_pos for the next call). */
 int64_t tl_hip_llama_position(const tl_hip_llama* m);
-/* Number of times the decode step has been captured as a hipGraph so far (instrumentation:
- * a capture happens on the first graph decode and after a change of weights, configuration or
- * penalty value; no reference counterpart). */
+/* Number of hipGraph captures of the decode step so far (instrumentation; no reference
+ * counterpart).  Two graphs are kept, one step and eight consecutive steps, each captured
+ * the first time a graph decode needs it and again after a change of weights, configuration
+ * or penalty value. */
 int64_t tl_hip_llama_graph_builds(const tl_hip_llama* m);
 /* One pass of the decode-loop body (chatbot.tl:174-187) over n new token ids at the
  * current cache position; writes the last row's logits [vocab] to logits_out (host,
@@ -354,7 +355,8 @@ int32_t tl_hip_llama_sample_greedy(tl_hip_llama* m, double repetition_penalty,
 /* Greedy decode of n_steps tokens after the cached context (chatbot.tl:188-222 with
  * sample(temp <= 0) = argmax): first token id `first`, generated ids to out_ids (host).
  * repetition_penalty 1.0 disables the penalty; history holds the prior ids (host). With
- * use_graph != 0 each step is a captured hipGraph replay. */
+ * use_graph != 0 the steps are captured hipGraph replays: one launch per eight steps, then
+ * one per remaining step. */
 int tl_hip_llama_generate(tl_hip_llama* m, int32_t first, int n_steps, int32_t* out_ids,
                           double repetition_penalty, const int32_t* history, int n_history,
                           int use_graph);

@@ -194,8 +194,10 @@ def test_graph_follows_the_penalty_value(small):
     builds = lambda: int(gpu.lib.tl_hip_llama_graph_builds(gpu.h))
     for pen in (1.1, 0.5, 1.1):
         b0 = builds()
+        # 23 decode steps after the prefill's token: two launches of the 8-step graph and seven
+        # of the 1-step graph, both captured for the new penalty
         assert list(greedy_generate(gpu, prompt, 24, penalty=pen, use_graph=True)) == wants[pen]
-        assert builds() == b0 + 1
+        assert builds() == b0 + 2
         assert list(greedy_generate(gpu, prompt, 24, penalty=pen, use_graph=False)) == wants[pen]
     b0 = builds()
     for n in (8, 30):   # same settings, fewer and more steps: replays only

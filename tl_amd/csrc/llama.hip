@@ -15,7 +15,8 @@
 //    repeat_interleave copy);
 //  * the LM head runs on the last row only (the chatbot narrows to it, chatbot.tl:189);
 //  * the cache position lives in device memory, so a decode step has no host
-//    dependency and is captured once as a hipGraph and replayed.
+//    dependency: it is captured as hipGraphs of one and of eight consecutive steps and
+//    replayed.
 #include "internal.h"
 
 #include <algorithm>
@@ -137,8 +138,10 @@ struct Llama {
     int32_t *am_i = nullptr, *am_nan = nullptr;
     int max_out = 0;
     int64_t host_pos = 0;
-    hipGraphExec_t graph = nullptr;
-    // what the captured step was built for: penalty bits (the value is a kernel argument),
+    // the decode step captured as hipGraphs: graph[0] holds one step, graph[1] GRAPH_STEPS
+    // consecutive steps (one graph launch per GRAPH_STEPS tokens); built on first use
+    hipGraphExec_t graph[2] = {nullptr, nullptr};
+    // what the captured steps were built for: penalty bits (the value is a kernel argument),
     // kv_f16, rope_per_token
     uint32_t graph_key[3] = {0xffffffffu, 0xffffffffu, 0xffffffffu};
     int64_t graph_builds = 0;
@@ -147,11 +150,18 @@ struct Llama {
 static Llama* L_(tl_hip_llama* h) { return reinterpret_cast<Llama*>(h); }
 
 static void free_graph(Llama* m) {
-    if (m->graph) {
-        (void)hipGraphExecDestroy(m->graph);
-        m->graph = nullptr;
+    for (hipGraphExec_t& g : m->graph) {
+        if (g) {
+            (void)hipGraphExecDestroy(g);
+            g = nullptr;
+        }
     }
 }
+
+// Steps per multi-step decode graph.  Every step reads its position, input token and output
+// slot from device memory, so consecutive copies of the step replay correctly; one graph
+// launch then carries the launch overhead of GRAPH_STEPS tokens.
+constexpr int GRAPH_STEPS = 8;
 
 static int alloc_kv(Llama* m) {
     for (void* p : m->kc) dev_free(p);
@@ -1002,27 +1012,32 @@ int tl_hip_llama_generate(tl_hip_llama* h, int32_t first, int n_steps, int32_t* 
     if (use_graph) {
         uint32_t key[3] = {0, (uint32_t)m->kv_f16, (uint32_t)m->rope_per_token};
         std::memcpy(&key[0], &pen, 4);
-        if (m->graph && std::memcmp(key, m->graph_key, sizeof(key)) != 0) free_graph(m);
-        if (!m->graph) {
+        if (std::memcmp(key, m->graph_key, sizeof(key)) != 0) {
+            free_graph(m);
+            std::memcpy(m->graph_key, key, sizeof(key));
+        }
+        const int n_multi = n_steps / GRAPH_STEPS, n_single = n_steps % GRAPH_STEPS;
+        for (int gi = 0; gi < 2; gi++) {
+            if (m->graph[gi] || (gi == 0 ? n_single : n_multi) == 0) continue;
             hipGraph_t g;
             TLH_CHECK_HIP(hipStreamBeginCapture(s, hipStreamCaptureModeThreadLocal));
-            rc = enqueue_step(m, pen, s);
+            for (int i = 0; i < (gi == 0 ? 1 : GRAPH_STEPS) && rc == 0; i++) rc = enqueue_step(m, pen, s);
             hipError_t e = hipStreamEndCapture(s, &g);
             if (rc) {
                 if (e == hipSuccess) (void)hipGraphDestroy(g);
                 return rc;
             }
             if (e != hipSuccess) return hip_fail(e, "hipStreamEndCapture");
-            e = hipGraphInstantiate(&m->graph, g, nullptr, nullptr, 0);
+            e = hipGraphInstantiate(&m->graph[gi], g, nullptr, nullptr, 0);
             (void)hipGraphDestroy(g);
             if (e != hipSuccess) {
-                m->graph = nullptr;
+                m->graph[gi] = nullptr;
                 return hip_fail(e, "hipGraphInstantiate");
             }
-            std::memcpy(m->graph_key, key, sizeof(key));
             m->graph_builds++;
         }
-        for (int i = 0; i < n_steps; i++) TLH_CHECK_HIP(hipGraphLaunch(m->graph, s));
+        for (int i = 0; i < n_multi; i++) TLH_CHECK_HIP(hipGraphLaunch(m->graph[1], s));
+        for (int i = 0; i < n_single; i++) TLH_CHECK_HIP(hipGraphLaunch(m->graph[0], s));
     } else {
         for (int i = 0; i < n_steps; i++)
             if ((rc = enqueue_step(m, pen, s))) return rc;
