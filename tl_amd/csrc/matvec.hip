@@ -219,7 +219,7 @@ __device__ __forceinline__ float4 merge_shares(const float4 (&o)[ATTN_SHARES], c
 // travels in MvArgs; the compiler's scalar loads of those fields then overlap the weight
 // stream instead of holding back its first loads.
 template <int QT, int BT, int RWT, int M, int EPI, bool NORM, bool EMBED, bool MERGE = false>
-__global__ __launch_bounds__(256) void k_mv(const uint8_t* __restrict__ qs_p, const void* __restrict__ w1_p,
+__global__ __launch_bounds__(512) void k_mv(const uint8_t* __restrict__ qs_p, const void* __restrict__ w1_p,
                                             const float* __restrict__ x_p, const float* __restrict__ aux_p,
                                             const int32_t* __restrict__ aux2_p, uint32_t n_p, uint32_t nb_p,
                                             uint32_t shape_p, int aux_i, MvArgs a) {
@@ -247,8 +247,8 @@ __global__ __launch_bounds__(256) void k_mv(const uint8_t* __restrict__ qs_p, co
     // loads (left to the compiler, each would wait for the round before it)
     if constexpr (QT == TL_HIP_GGML_Q6_K) asm volatile("" : : "s"(a.sc), "s"(a.d));
     extern __shared__ float xs[];  // [M][nb][XPAD] staged activations (x * norm weight with NORM)
-    __shared__ float red[4][N];
-    __shared__ float ssq[4][M];
+    __shared__ float red[8][N];
+    __shared__ float ssq[8][M];
     const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform: SGPR
     const int TC = sh.tc, S = 1 << sh.s_shift, RW = RWT << sh.s_shift, rw_shift = RWT_SHIFT + sh.s_shift;
     const int tcol = sh.s_shift ? (tid & (TC - 1)) : tid;
@@ -738,8 +738,9 @@ __global__ __launch_bounds__(256) void k_argmax_finish(float* part_v, int32_t* p
 // ---------------------------------------------------------------- dispatch --------------
 // TC = nb rounded up to wavefronts (at most 256) threads per row subset, BT block columns
 // per thread and pass (2 once nb > 256), S row subsets (four wavefronts per workgroup when
-// TC is one or two wavefronts), RWT rows per thread: the smallest of 2, 4, 8 that keeps the
-// grid at <= 720 workgroups (about three per CU), with at most 64 quant VGPRs per thread.
+// TC is one or two wavefronts; twice that when the grid stays a multiple of 256), RWT rows
+// per thread: the smallest of 2, 4, 8 that keeps the grid at <= 720 workgroups (about three
+// per CU), with at most 64 quant VGPRs per thread.
 // (Measured on MI355X over the decode shapes: fewer, fuller workgroups lose to this because
 // the per-thread block math then serialises on fewer SIMDs; many more lose to the repeated
 // activation loads.)
@@ -765,6 +766,13 @@ static MvPlan mv_plan(int64_t n, int64_t nb, int qt) {
     while (rwt < 8 && cdiv(n, (int64_t)p.S * rwt) > 720) rwt *= 2;
     while (rwt > 2 && rwt * p.BT * qw > 16) rwt /= 2;
     p.RWT = rwt;
+    // 512-thread workgroups (twice the row subsets, the activations staged once for twice the
+    // rows) when the grid stays a whole number of workgroups per CU -- a multiple of 256.
+    // Measured on MI355X: Q4_0 / Q4_K 4096^2 4.19 -> 4.07 / 4.72 -> 4.61 us, 4096 x 11008 Q4_0
+    // 10.69 -> 10.17, Q8_0 15.2 -> 12.2 us (Q8_0 / Q6_K 4096^2 +1 %); at 344 workgroups
+    // (11008 x 4096) the doubled form loses 19 %, and the decode shapes keep 256 threads.
+    const int64_t g2 = cdiv(n, (int64_t)p.S * 2 * rwt);
+    if ((p.TC & (p.TC - 1)) == 0 && p.S * p.TC == 256 && g2 >= 256 && g2 % 256 == 0) p.S *= 2;
     p.grid = cdiv(n, (int64_t)p.S * rwt);
     return p;
 }
@@ -895,7 +903,7 @@ bool matvec_fits(const QWeight* w, int64_t m) {
 // the loads (and the wait for them) without a store.  The time of a launch that only moves
 // the weight stream the way the matvec moves it.
 template <int QT, int BT, int RWT>
-__global__ __launch_bounds__(256) void k_read_floor(const uint8_t* __restrict__ qs, const void* __restrict__ w1,
+__global__ __launch_bounds__(512) void k_read_floor(const uint8_t* __restrict__ qs, const void* __restrict__ w1,
                                                     const int8_t* __restrict__ sc, const __half* __restrict__ d6,
                                                     uint32_t n_p, uint32_t nb_p, uint32_t shape_p) {
     constexpr int QB = QB_<QT>::v, QW = QB / 16;
