@@ -289,17 +289,19 @@ __global__ __launch_bounds__(256) void k_dequant_f16q(QView qv, _Float16* __rest
     }
 }
 
-// global_load_lds: each lane's SIZE bytes from src land at lds + lane * SIZE (one 64-lane
-// instruction writes 64 consecutive elements).  The builtin exists only in the device pass.
-__device__ __forceinline__ void lds_dma16(const void* src, void* lds) {
-#if defined(__HIP_DEVICE_COMPILE__)
-    __builtin_amdgcn_global_load_lds(src, lds, 16, 0, 0);
-#endif
+// Operand DMA: buffer loads straight into LDS through a raw (stride 0) buffer resource over
+// [p, p + bytes).  A lane's SIZE bytes at voff + soff land at lds + lane * SIZE (one 64-lane
+// instruction writes 64 consecutive elements).  The per-lane offset is fixed for the whole K
+// loop and the iteration's advance is a scalar, so the loop spends no vector instruction on
+// addresses (with flat global_load_lds each load cost two 64-bit vector adds).
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t buf_rsrc(const void* p, uint32_t bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), (short)0, (int)bytes, 0x00020000);
 }
-__device__ __forceinline__ void lds_dma4(const void* src, void* lds) {
-#if defined(__HIP_DEVICE_COMPILE__)
-    __builtin_amdgcn_global_load_lds(src, lds, 4, 0, 0);
-#endif
+__device__ __forceinline__ void buf_dma16(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff, void* lds) {
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void*)lds, 16, voff, soff, 0, 0);
+}
+__device__ __forceinline__ void buf_dma4(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff, void* lds) {
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void*)lds, 4, voff, soff, 0, 0);
 }
 
 // X-tile chunk swizzle of row r (mod 16): a bijection of the 16 chunks for every row
@@ -384,17 +386,20 @@ __global__ __launch_bounds__(512) void k_qgemm_mfma(const uint8_t* __restrict__ 
         // Q4_0 / Q8_0: the word holding the f16 d of (row, block); Q4_K: its (d sc, -dmin m) word
         doff = (uint32_t)(K4 ? (row * nb + (slot & 3)) * 4 : ((row * nb + (slot & 3)) >> 1) * 4);
     }
+    // buffer extents (the launch keeps every one below 2^31 bytes); a Q4_0 / Q8_0 scale array
+    // carries 4 bytes of padding, so its last aligned word is whole
+    const __amdgpu_buffer_rsrc_t rx = buf_rsrc(x16, (uint32_t)(m * k * 2));
+    const __amdgpu_buffer_rsrc_t rq = buf_rsrc(qs, (uint32_t)(n * nb * QB));
+    const __amdgpu_buffer_rsrc_t rd = buf_rsrc(dsc, (uint32_t)(SCALED ? n * nb * (K4 ? 4 : 2) + (K4 ? 0 : 4) : 0));
     auto issue = [&](int64_t kb, Stage& st) {
-        const char* src = reinterpret_cast<const char*>(x16) + kb * 64;  // 32 halves per block
 #pragma unroll
-        for (int u = 0; u < XI; u++) lds_dma16(src + xoff[u], &st.X[(wave * XI + u) * 64 * 8]);
+        for (int u = 0; u < XI; u++) buf_dma16(rx, xoff[u], (uint32_t)(kb * 64), &st.X[(wave * XI + u) * 64 * 8]);
         if (wave < WW) {
 #pragma unroll
-            for (int u = 0; u < WPT; u++)
-                lds_dma16(reinterpret_cast<const char*>(qs) + kb * QB + woff[u], &st.Wq[(wave * WPT + u) * 64 * 16]);
+            for (int u = 0; u < WPT; u++) buf_dma16(rq, woff[u], (uint32_t)(kb * QB), &st.Wq[(wave * WPT + u) * 64 * 16]);
         }
         if (DW > 0 && wave >= 8 - DW)  // kb even: whole words
-            lds_dma4(reinterpret_cast<const char*>(dsc) + kb * (K4 ? 4 : 2) + doff, &st.Wd[(wave - (8 - DW)) * 64]);
+            buf_dma4(rd, doff, (uint32_t)(kb * (K4 ? 4 : 2)), &st.Wd[(wave - (8 - DW)) * 64]);
     };
     uint32_t dpar[TN];  // which half of its word holds this lane's scale (kb is even)
 #pragma unroll
@@ -654,6 +659,13 @@ int launch_gemm_f16q(const QWeight* w, const _Float16* x16, float* y, int64_t m,
     if (noalloc && needs_w16) {
         set_error(TL_HIP_ERR_ARG, "ArgumentError: a %s weight needs an f16 copy for the MFMA GEMM, which the "
                   "allocation-free entry cannot make", ggml_type_name(w->ggml_type));
+        return TL_HIP_ERR_ARG;
+    }
+    // the kernel addresses X, the weight stream and its scales through 32-bit buffer offsets
+    // (quant bytes: k / 2 per row for the 4-bit types, k for Q8_0; an f16 copy 2 k)
+    const int64_t wbytes = needs_w16 ? w->n * w->k * 2 : w->ggml_type == TL_HIP_GGML_Q8_0 ? w->n * w->k : w->n * w->k / 2;
+    if (m * w->k * 2 >= (int64_t(1) << 31) || wbytes >= (int64_t(1) << 31)) {
+        set_error(TL_HIP_ERR_ARG, "ArgumentError: the f16 GEMM takes X and weights below 2 GiB");
         return TL_HIP_ERR_ARG;
     }
     constexpr int BM = 128;
