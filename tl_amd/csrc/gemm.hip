@@ -449,9 +449,10 @@ __global__ __launch_bounds__(512) void k_qgemm_mfma(const uint8_t* __restrict__ 
 #pragma unroll
         for (int j = 0; j < TN; j++) {
             if constexpr (K4) {
-                const uint32_t a = dw[j] & 0xFFFFu, b = dw[j] >> 16;
-                d2[j] = __builtin_bit_cast(half2v, a | (a << 16));
-                m8d2[j] = __builtin_bit_cast(half2v, b | (b << 16));
+                // both halves broadcast by the packed FMA's operand selects (no instruction)
+                const half2v u = __builtin_bit_cast(half2v, dw[j]);
+                d2[j] = __builtin_shufflevector(u, u, 0, 0);
+                m8d2[j] = __builtin_shufflevector(u, u, 1, 1);
             } else if constexpr (SCALED) {
                 const uint32_t b = (dw[j] >> dpar[j]) & 0xFFFFu;
                 d2[j] = __builtin_bit_cast(half2v, b | (b << 16));
