@@ -212,7 +212,8 @@ struct QWords<TL_HIP_GGML_Q8_0> {
     static constexpr int BYTES = 32;
     // words 2t, 2t+1 = elements 8t .. 8t+7 as pairs (8t, 8t+2) (8t+1, 8t+3) (8t+4, 8t+6)
     // (8t+5, 8t+7); (q ^ 0x80) | 0x6400 is 1024 + q + 128.  raw = the block's 16 bytes that
-    // hold k-steps 2 kh and 2 kh + 1; tt selects the step (words 2 tt, 2 tt + 1).
+    // hold k-steps 2 kh and 2 kh + 1; tt selects the step (words 2 tt, 2 tt + 1).  One
+    // v_perm_b32 per pair puts bytes 0 and 2 (or 1 and 3) of the word under 0x64 bytes.
     __device__ static half8 operand(const uint4& raw, int tt, half2v d2) {
         const uint32_t src[4] = {raw.x, raw.y, raw.z, raw.w};
         const half2v off = {(_Float16)-1152.0f, (_Float16)-1152.0f};
@@ -222,7 +223,8 @@ struct QWords<TL_HIP_GGML_Q8_0> {
             const uint32_t w = src[2 * tt + h] ^ 0x80808080u;
 #pragma unroll
             for (int p = 0; p < 2; p++) {
-                const uint32_t bits = ((w >> (8 * p)) & 0x00FF00FFu) | 0x64006400u;
+                // selector bytes 0-3 take w's bytes, 4 the constant's 0x64
+                const uint32_t bits = __builtin_amdgcn_perm(0x64646464u, w, p ? 0x04030401u : 0x04020400u);
                 const half2v v = (__builtin_bit_cast(half2v, bits) + off) * d2;
                 r[4 * h + 2 * p] = v.x;
                 r[4 * h + 2 * p + 1] = v.y;
