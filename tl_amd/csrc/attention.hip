@@ -306,8 +306,8 @@ __device__ __forceinline__ float wave_max64(float v) {
     v = fmaxf(v, dpp_f<0x4E>(v));
     v = fmaxf(v, dpp_f<0x141>(v));
     v = fmaxf(v, dpp_f<0x140>(v));
-    v = fmaxf(v, __shfl_xor(v, 16, 64));
-    v = fmaxf(v, __shfl_xor(v, 32, 64));
+    v = lane_pair_max<16>(v);  // permlane swaps: no LDS round trip
+    v = lane_pair_max<32>(v);
     return v;
 }
 __device__ __forceinline__ float wave_sum64(float v) {
@@ -315,8 +315,8 @@ __device__ __forceinline__ float wave_sum64(float v) {
     v += dpp_f<0x4E>(v);
     v += dpp_f<0x141>(v);
     v += dpp_f<0x140>(v);
-    v += __shfl_xor(v, 16, 64);
-    v += __shfl_xor(v, 32, 64);
+    v = lane_pair_sum<16>(v);
+    v = lane_pair_sum<32>(v);
     return v;
 }
 
@@ -355,7 +355,7 @@ __device__ __forceinline__ float xchg_lo(float v) {  // partner across lane bit 
 template <int OFF>
 __device__ __forceinline__ float xchg_hi(float v) {  // exact xor of lane bit OFF (OFF >= 8)
     if constexpr (OFF == 8) return dpp_f<0x128>(v);  // row_ror:8 = xor 8 within 16 lanes
-    else return __shfl_xor(v, OFF, 64);
+    else return lane_xor_f32<OFF>(v);                // permlane swaps
 }
 
 // Transpose-reduce of N values over the lanes that differ in lane bits LO .. OFF (powers of
@@ -533,7 +533,7 @@ __device__ __forceinline__ float row_sum(float v) {  // over aligned groups of L
     v += dpp_f<0x4E>(v);   // xor 2
     v += dpp_f<0x141>(v);  // half-row mirror: the other four of the eight
     if constexpr (LPR >= 16) v += dpp_f<0x140>(v);  // row mirror: the other eight of sixteen
-    if constexpr (LPR >= 32) v += __shfl_xor(v, 16, 64);
+    if constexpr (LPR >= 32) v = lane_pair_sum<16>(v);
     return v;
 }
 
@@ -849,8 +849,8 @@ __global__ __launch_bounds__(256) void k_attn_prefill(const float* __restrict__ 
                     if (p > prow[rt]) st[pt][rt][i] = -INFINITY;
                     mx = fmaxf(mx, st[pt][rt][i]);
                 }
-            mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
-            mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+            mx = lane_pair_max<16>(mx);
+            mx = lane_pair_max<32>(mx);
             const float mn = fmaxf(mrow[rt], mx);  // finite: position 0 is in every row's range
             const float alpha = __builtin_amdgcn_exp2f(mrow[rt] - mn);  // 0 on the first tile
             float sum = 0.f;
@@ -862,8 +862,8 @@ __global__ __launch_bounds__(256) void k_attn_prefill(const float* __restrict__ 
                     st[pt][rt][i] = e;
                     sum += e;
                 }
-            sum += __shfl_xor(sum, 16, 64);
-            sum += __shfl_xor(sum, 32, 64);
+            sum = lane_pair_sum<16>(sum);
+            sum = lane_pair_sum<32>(sum);
             lrow[rt] = lrow[rt] * alpha + sum;
             mrow[rt] = mn;
 #pragma unroll

@@ -182,6 +182,58 @@ int launch_quant_gemm(const QWeight* w, const float* x, float* y, int64_t m, hip
 // F16Q_Q8 (word t = 8t, 8t+2, 8t+1, 8t+3, 8t+4, 8t+6, 8t+5, 8t+7; Q8_0).
 typedef _Float16 half8 __attribute__((ext_vector_type(8)));  // one operand word
 typedef float floatx4 __attribute__((ext_vector_type(4)));
+
+// ---- lane exchanges across 16 / 32 lanes without LDS (gfx950) ----------------------------
+// v_permlane32_swap(a, b) (v_permlane16_swap) exchanges the upper 32 lanes (the odd 16-lane
+// rows) of a with the lower 32 lanes (the even rows) of b: a lane l with bit OFF clear ends
+// with (a_l, a_{l+OFF}), a lane with it set with (b_{l-OFF}, b_l).  VALU instructions: no LDS
+// round trip as with ds_bpermute (__shfl_xor).
+template <int OFF>
+__device__ __forceinline__ void lane_swap(uint32_t& a, uint32_t& b) {
+    static_assert(OFF == 16 || OFF == 32, "row-crossing swaps only");
+    if constexpr (OFF == 32) {
+        const auto r = __builtin_amdgcn_permlane32_swap(a, b, false, false);
+        a = r[0];
+        b = r[1];
+    } else {
+        const auto r = __builtin_amdgcn_permlane16_swap(a, b, false, false);
+        a = r[0];
+        b = r[1];
+    }
+}
+// a_l + a_{l^OFF}: the sum of a lane's value and its partner's (every lane gets it)
+template <int OFF>
+__device__ __forceinline__ float lane_pair_sum(float v) {
+    uint32_t a = __builtin_bit_cast(uint32_t, v), b = a;
+    lane_swap<OFF>(a, b);
+    return __builtin_bit_cast(float, a) + __builtin_bit_cast(float, b);
+}
+template <int OFF>
+__device__ __forceinline__ float lane_pair_max(float v) {
+    uint32_t a = __builtin_bit_cast(uint32_t, v), b = a;
+    lane_swap<OFF>(a, b);
+    return fmaxf(__builtin_bit_cast(float, a), __builtin_bit_cast(float, b));
+}
+// the value of lane l ^ OFF
+template <int OFF>
+__device__ __forceinline__ uint32_t lane_xor_u32(uint32_t v) {
+    uint32_t a = v, b = v;
+    lane_swap<OFF>(a, b);
+    return (__lane_id() & OFF) ? a : b;
+}
+template <int OFF>
+__device__ __forceinline__ float lane_xor_f32(float v) {
+    return __builtin_bit_cast(float, lane_xor_u32<OFF>(__builtin_bit_cast(uint32_t, v)));
+}
+// The same within 16 lanes by DPP, for all-reduce steps (any involution that pairs the two
+// halves of each group of 2 OFF lanes): quad_perm [1,0,3,2] (OFF 1), [2,3,0,1] (2), half-row
+// mirror (4), row mirror (8).
+template <int OFF>
+__device__ __forceinline__ uint32_t lane_pair_dpp(uint32_t v) {
+    constexpr int CTRL = OFF == 1 ? 0xB1 : OFF == 2 ? 0x4E : OFF == 4 ? 0x141 : 0x140;
+    return (uint32_t)__builtin_amdgcn_mov_dpp((int)v, CTRL, 0xF, 0xF, true);
+}
+
 enum { F16Q_Q4 = 0, F16Q_Q8 = 1 };
 enum { GEMM_PLAIN = 0, GEMM_RES = 1, GEMM_GLU16 = 2 };
 // Epilogue: PLAIN y = v; RES y = res + v (res may be y); GLU16 columns (2i, 2i + 1) are
