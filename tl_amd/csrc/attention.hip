@@ -142,9 +142,7 @@ __global__ __launch_bounds__(256) void k_attn(AttnArgs a) {
                 float s = 0.f;
 #pragma unroll
                 for (int i = 0; i < DL; i++) s = fmaf(qv[g][i], kv[i], s);
-                s += __shfl_xor(s, 1, 64);
-                s += __shfl_xor(s, 2, 64);
-                s += __shfl_xor(s, 4, 64);
+                s = sum8_dpp(s);
                 if (sub == 0 && p < p1) sc[g][p - p0] = s * a.scale;
             }
         };
@@ -164,16 +162,14 @@ __global__ __launch_bounds__(256) void k_attn(AttnArgs a) {
         for (int g = wave; g < G; g += 4) {
             float mx = -INFINITY;
             for (int i = lane; i < cn; i += 64) mx = fmaxf(mx, sc[g][i]);
-#pragma unroll
-            for (int off = 32; off >= 1; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off, 64));
+            mx = wave_allmax(mx);
             float sum = 0.f;
             for (int i = lane; i < cn; i += 64) {
                 float e = expf(sc[g][i] - mx);
                 sc[g][i] = e;
                 sum += e;
             }
-#pragma unroll
-            for (int off = 32; off >= 1; off >>= 1) sum += __shfl_xor(sum, off, 64);
+            sum = wave_allsum(sum);
             if (lane == 0) {
                 stat[g][0] = mx;
                 stat[g][1] = sum;
@@ -212,9 +208,9 @@ __global__ __launch_bounds__(256) void k_attn(AttnArgs a) {
 #pragma unroll
             for (int i = 0; i < DL; i++) {
                 float v = o[g][i];
-                v += __shfl_xor(v, 8, 64);
-                v += __shfl_xor(v, 16, 64);
-                v += __shfl_xor(v, 32, 64);
+                v += dpp_f<0x128>(v);  // row_ror:8 = xor 8 within 16 lanes
+                v = lane_pair_sum<16>(v);
+                v = lane_pair_sum<32>(v);
                 o[g][i] = v;
             }
         if (grp == 0) {
@@ -266,16 +262,14 @@ __global__ __launch_bounds__(256) void k_attn_merge(AttnArgs a) {
     for (int g = wave; g < G; g += 4) {
         float M = -INFINITY;
         for (int s = lane; s < nact; s += 64) M = fmaxf(M, sm[g][s]);
-#pragma unroll
-        for (int off = 32; off >= 1; off >>= 1) M = fmaxf(M, __shfl_xor(M, off, 64));
+        M = wave_allmax(M);
         float den = 0.f;
         for (int s = lane; s < nact; s += 64) {
             const float f = expf(sm[g][s] - M);
             den = fmaf(sf[g][s], f, den);
             sm[g][s] = f;
         }
-#pragma unroll
-        for (int off = 32; off >= 1; off >>= 1) den += __shfl_xor(den, off, 64);
+        den = wave_allsum(den);
         if (lane == 0) sden[g] = den;
     }
     __syncthreads();
@@ -291,16 +285,6 @@ __global__ __launch_bounds__(256) void k_attn_merge(AttnArgs a) {
 }
 
 // ---- shared helpers ---------------------------------------------------------------------
-template <int CTRL>
-__device__ __forceinline__ float dpp_f(float v) {
-    return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), CTRL, 0xF, 0xF, true));
-}
-__device__ __forceinline__ float sum8_dpp(float v) {  // over aligned groups of 8 lanes
-    v += dpp_f<0xB1>(v);   // quad_perm [1,0,3,2]
-    v += dpp_f<0x4E>(v);   // quad_perm [2,3,0,1]
-    v += dpp_f<0x141>(v);  // row_half_mirror
-    return v;
-}
 __device__ __forceinline__ float wave_max64(float v) {
     v = fmaxf(v, dpp_f<0xB1>(v));
     v = fmaxf(v, dpp_f<0x4E>(v));
@@ -1309,18 +1293,6 @@ extern "C" tl_hip_tensor* tl_hip_attention_prefill(const tl_hip_tensor* qh, cons
 // the q row sits in LDS, one wavefront forms each score (lanes over d, DPP reduction) into the
 // row's slice of a score workspace, the workgroup reduces max and sum, normalises in place,
 // and each thread accumulates output columns over the keys in key order.
-__device__ __forceinline__ float sdpa_wmax(float v) {
-#pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, 64));
-    return v;
-}
-
-__device__ __forceinline__ float sdpa_wsum(float v) {
-#pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off, 64);
-    return v;
-}
-
 __global__ __launch_bounds__(256) void k_sdpa(const float* __restrict__ q, const float* __restrict__ k,
                                               const float* __restrict__ v, const float* __restrict__ mask,
                                               int64_t mask_len, float* __restrict__ out, float* __restrict__ sc,
@@ -1339,7 +1311,7 @@ __global__ __launch_bounds__(256) void k_sdpa(const float* __restrict__ q, const
         const float* kr = kb + j * dk;
         float p = 0.f;
         for (int d = lane; d < dk; d += 64) p = fmaf(qs[d], kr[d], p);
-        p = sdpa_wsum(p);
+        p = wave_allsum(p);
         if (lane == 0) {
             float x = p * scale;
             const int64_t mi = i * sk + j;
@@ -1350,7 +1322,7 @@ __global__ __launch_bounds__(256) void k_sdpa(const float* __restrict__ q, const
     __syncthreads();
     float mx = -INFINITY;
     for (int64_t j = tid; j < sk; j += 256) mx = fmaxf(mx, s[j]);
-    mx = sdpa_wmax(mx);
+    mx = wave_allmax(mx);
     if (lane == 0) red[wave] = mx;
     __syncthreads();
     mx = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
@@ -1361,7 +1333,7 @@ __global__ __launch_bounds__(256) void k_sdpa(const float* __restrict__ q, const
         s[j] = e;
         sum += e;
     }
-    sum = sdpa_wsum(sum);
+    sum = wave_allsum(sum);
     if (lane == 0) red[wave] = sum;
     __syncthreads();
     sum = (red[0] + red[1]) + (red[2] + red[3]);

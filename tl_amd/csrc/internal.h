@@ -233,6 +233,79 @@ __device__ __forceinline__ uint32_t lane_pair_dpp(uint32_t v) {
     constexpr int CTRL = OFF == 1 ? 0xB1 : OFF == 2 ? 0x4E : OFF == 4 ? 0x141 : 0x140;
     return (uint32_t)__builtin_amdgcn_mov_dpp((int)v, CTRL, 0xF, 0xF, true);
 }
+// DPP move within 16-lane rows (all rows and banks, bound_ctrl): quad_perm [1,0,3,2] 0xB1,
+// [2,3,0,1] 0x4E, half-row mirror 0x141, row mirror 0x140, row_ror:k 0x120 + k (lane i reads
+// lane (i + k) mod 16 of its row).
+template <int CTRL>
+__device__ __forceinline__ float dpp_f(float v) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), CTRL, 0xF, 0xF, true));
+}
+// sum over aligned groups of 8 lanes in the order xor 1, xor 2, xor 4: after the first two
+// steps a lane's value equals its quad's, so the half-row mirror (lane 7 - i) reads the value
+// of lane i ^ 4
+__device__ __forceinline__ float sum8_dpp(float v) {
+    v += dpp_f<0xB1>(v);
+    v += dpp_f<0x4E>(v);
+    v += dpp_f<0x141>(v);
+    return v;
+}
+// Wavefront all-reduce over the xor butterfly 32, 16, 8, 4, 2, 1 -- the pairing and order of
+// `for (off = 32; off >= 1; off >>= 1) v = op(v, __shfl_xor(v, off))`, hence bitwise equal
+// results.  32 and 16 are permlane swaps.  After the steps above bit k every lane holds the
+// value of each lane that differs from it only in bits above k, so row_ror:k (lane
+// (i + k) mod 16, which differs from i ^ k only in those bits) reads the xor partner's value.
+__device__ __forceinline__ float wave_allsum(float v) {
+    v = lane_pair_sum<32>(v);
+    v = lane_pair_sum<16>(v);
+    v += dpp_f<0x128>(v);
+    v += dpp_f<0x124>(v);
+    v += dpp_f<0x122>(v);
+    v += dpp_f<0x121>(v);
+    return v;
+}
+__device__ __forceinline__ float wave_allmax(float v) {
+    v = lane_pair_max<32>(v);
+    v = lane_pair_max<16>(v);
+    v = fmaxf(v, dpp_f<0x128>(v));
+    v = fmaxf(v, dpp_f<0x124>(v));
+    v = fmaxf(v, dpp_f<0x122>(v));
+    v = fmaxf(v, dpp_f<0x121>(v));
+    return v;
+}
+
+// (greater value, then larger index) over the 64 lanes, empty lanes bi < 0, NaN flags or-ed:
+// every lane ends with the wavefront's best.  The steps pair lanes by DPP within 16 lanes and
+// by the permlane swaps across rows; the order of the steps does not matter for this
+// commutative, associative selection (with a NaN the caller replays a sequential fold).
+__device__ __forceinline__ void argmax_step(float& bv, int& bi, int& nan, float ov, int oi, int on) {
+    if (oi >= 0 && (bi < 0 || ov > bv || (ov == bv && oi > bi))) {
+        bv = ov;
+        bi = oi;
+    }
+    nan |= on;
+}
+template <int OFF>
+__device__ __forceinline__ void argmax_round(float& bv, int& bi, int& nan) {
+    uint32_t v, i, f;
+    if constexpr (OFF >= 16) {
+        v = lane_xor_u32<OFF>(__builtin_bit_cast(uint32_t, bv));
+        i = lane_xor_u32<OFF>((uint32_t)bi);
+        f = lane_xor_u32<OFF>((uint32_t)nan);
+    } else {
+        v = lane_pair_dpp<OFF>(__builtin_bit_cast(uint32_t, bv));
+        i = lane_pair_dpp<OFF>((uint32_t)bi);
+        f = lane_pair_dpp<OFF>((uint32_t)nan);
+    }
+    argmax_step(bv, bi, nan, __builtin_bit_cast(float, v), (int)i, (int)f);
+}
+__device__ __forceinline__ void argmax_allreduce(float& bv, int& bi, int& nan) {
+    argmax_round<1>(bv, bi, nan);
+    argmax_round<2>(bv, bi, nan);
+    argmax_round<4>(bv, bi, nan);
+    argmax_round<8>(bv, bi, nan);
+    argmax_round<16>(bv, bi, nan);
+    argmax_round<32>(bv, bi, nan);
+}
 
 enum { F16Q_Q4 = 0, F16Q_Q8 = 1 };
 enum { GEMM_PLAIN = 0, GEMM_RES = 1, GEMM_GLU16 = 2 };

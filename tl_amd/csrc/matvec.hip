@@ -100,11 +100,6 @@ __device__ __forceinline__ float fma4b(uint32_t q, const float* x, float acc) {
     return acc;
 }
 
-template <int CTRL>
-__device__ __forceinline__ float dpp_mov(float v) {
-    return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), CTRL, 0xF, 0xF, true));
-}
-
 // Lane exchange used by the reductions.  Each form is an involution that flips lane bit OFF
 // within the group of lanes agreeing on the higher bits: the permlane swaps for 32 and 16,
 // the DPP row mirror (xor 15), half-row mirror (xor 7) and quad permutations (xor 2, xor 1)
@@ -112,10 +107,10 @@ __device__ __forceinline__ float dpp_mov(float v) {
 template <int OFF>
 __device__ __forceinline__ float xchg(float v) {
     if constexpr (OFF >= 16) return lane_xor_f32<OFF>(v);
-    else if constexpr (OFF == 8) return dpp_mov<0x140>(v);
-    else if constexpr (OFF == 4) return dpp_mov<0x141>(v);
-    else if constexpr (OFF == 2) return dpp_mov<0x4E>(v);
-    else return dpp_mov<0xB1>(v);
+    else if constexpr (OFF == 8) return dpp_f<0x140>(v);
+    else if constexpr (OFF == 4) return dpp_f<0x141>(v);
+    else if constexpr (OFF == 2) return dpp_f<0x4E>(v);
+    else return dpp_f<0xB1>(v);
 }
 
 template <int OFF>
@@ -165,40 +160,6 @@ __device__ __forceinline__ float xreduce(float (&v)[N], int lane) {
         if constexpr (G > 1) return fold<G / 2>(v[0]);
         else return v[0];
     }
-}
-
-// (greater value, then larger index) over the 64 lanes, empty lanes bi < 0, NaN flags or-ed:
-// every lane ends with the wavefront's best.  The steps pair lanes by DPP within 16 lanes and
-// by the permlane swaps across rows; the order of the steps does not matter for this
-// commutative, associative selection (with a NaN the caller replays a sequential fold).
-__device__ __forceinline__ void argmax_step(float& bv, int& bi, int& nan, float ov, int oi, int on) {
-    if (oi >= 0 && (bi < 0 || ov > bv || (ov == bv && oi > bi))) {
-        bv = ov;
-        bi = oi;
-    }
-    nan |= on;
-}
-template <int OFF>
-__device__ __forceinline__ void argmax_round(float& bv, int& bi, int& nan) {
-    uint32_t v, i, f;
-    if constexpr (OFF >= 16) {
-        v = lane_xor_u32<OFF>(__builtin_bit_cast(uint32_t, bv));
-        i = lane_xor_u32<OFF>((uint32_t)bi);
-        f = lane_xor_u32<OFF>((uint32_t)nan);
-    } else {
-        v = lane_pair_dpp<OFF>(__builtin_bit_cast(uint32_t, bv));
-        i = lane_pair_dpp<OFF>((uint32_t)bi);
-        f = lane_pair_dpp<OFF>((uint32_t)nan);
-    }
-    argmax_step(bv, bi, nan, __builtin_bit_cast(float, v), (int)i, (int)f);
-}
-__device__ __forceinline__ void argmax_allreduce(float& bv, int& bi, int& nan) {
-    argmax_round<1>(bv, bi, nan);
-    argmax_round<2>(bv, bi, nan);
-    argmax_round<4>(bv, bi, nan);
-    argmax_round<8>(bv, bi, nan);
-    argmax_round<16>(bv, bi, nan);
-    argmax_round<32>(bv, bi, nan);
 }
 
 constexpr int XPAD = 36;       // floats per staged 32-float block: lane-per-block LDS reads hit distinct banks
@@ -622,13 +583,13 @@ __global__ __launch_bounds__(512) void k_mv(const uint8_t* __restrict__ qs_p, co
             } else if constexpr (EPI == EPI_GLU) {
                 // rows (2i, 2i + 1) = (gate_i, up_i) are formed in lanes tid, tid ^ 1: the gate
                 // lane takes the up value with one lane exchange (no LDS round trip, no barrier)
-                const float u = dpp_mov<0xB1>(acc_s);  // lane tid ^ 1 (both lanes of a pair are active)
+                const float u = dpp_f<0xB1>(acc_s);  // lane tid ^ 1 (both lanes of a pair are active)
                 const uint32_t half_n = n / 2, i = row0 / 2 + (rl >> 1);
                 if ((rl & 1) == 0 && i < half_n) st_wt(a.y + m * half_n + i, (acc_s * (1.0f / (1.0f + expf(-acc_s)))) * u);
             } else if constexpr (EPI == EPI_ROPE_KV) {
                 // dims (2j, 2j + 1) of a head are rows rl, rl + 1 (M = 1): the even lane rotates
                 // the pair and writes q or the KV cache; v rows are appended as they are
-                const float v1 = dpp_mov<0xB1>(acc_s);  // lane tid ^ 1 (both lanes of a pair are active)
+                const float v1 = dpp_f<0xB1>(acc_s);  // lane tid ^ 1 (both lanes of a pair are active)
                 if ((rl & 1) == 0 && row0 + rl < n) {
                     const float v0 = acc_s;
                     const int64_t pos = pre_pos;

@@ -11,21 +11,10 @@
 
 namespace tlhip {
 
-__device__ __forceinline__ float warp_sum(float v) {
-#pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off, 64);
-    return v;
-}
-__device__ __forceinline__ float warp_max(float v) {
-#pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, 64));
-    return v;
-}
-
 // block-wide sum; every thread receives the result.  `red` holds >= blockDim/64 floats.
 __device__ __forceinline__ float block_sum(float v, float* red) {
     const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, nw = blockDim.x >> 6;
-    v = warp_sum(v);
+    v = wave_allsum(v);
     __syncthreads();
     if (lane == 0) red[w] = v;
     __syncthreads();
@@ -35,7 +24,7 @@ __device__ __forceinline__ float block_sum(float v, float* red) {
 }
 __device__ __forceinline__ float block_max(float v, float* red) {
     const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, nw = blockDim.x >> 6;
-    v = warp_max(v);
+    v = wave_allmax(v);
     __syncthreads();
     if (lane == 0) red[w] = v;
     __syncthreads();
@@ -550,34 +539,26 @@ __global__ void k_embedding(const float* __restrict__ table, const int32_t* __re
 __global__ __launch_bounds__(1024) void k_argmax(const float* __restrict__ x, int64_t n,
                                                  int32_t* __restrict__ out_idx) {
     __shared__ float sv[16];
-    __shared__ int64_t si[16];
+    __shared__ int si[16];
     __shared__ int has_nan;
     if (threadIdx.x == 0) has_nan = 0;
     __syncthreads();
     float bv = -INFINITY;
-    int64_t bi = -1;
+    int bi = -1;  // n <= INT32_MAX (checked by the launcher)
     int nan_seen = 0;
     for (int64_t i = threadIdx.x; i < n; i += blockDim.x) {
         float v = x[i];
         if (v != v) nan_seen = 1;
         if (bi < 0 || !(bv > v)) {  // later index wins ties (i increases per thread)
             bv = v;
-            bi = i;
+            bi = (int)i;
         }
     }
     if (nan_seen) has_nan = 1;
     const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
-#pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) {
-        float ov = __shfl_xor(bv, off, 64);
-        int64_t oi = __shfl_xor(bi, off, 64);
-        // keep the pair a fold would keep: larger value, ties -> larger index
-        bool take = oi >= 0 && (bi < 0 || ov > bv || (ov == bv && oi > bi));
-        if (take) {
-            bv = ov;
-            bi = oi;
-        }
-    }
+    // keep the pair a fold would keep: larger value, ties -> larger index
+    int nan_any = 0;
+    argmax_allreduce(bv, bi, nan_any);
     if (lane == 0) {
         sv[w] = bv;
         si[w] = bi;
@@ -602,6 +583,10 @@ __global__ __launch_bounds__(1024) void k_argmax(const float* __restrict__ x, in
 }
 
 int launch_argmax(const float* x, int64_t n, int32_t* out_idx, hipStream_t s) {
+    if (n > INT32_MAX) {
+        set_error(TL_HIP_ERR_ARG, "ArgumentError: argmax returns an int32 index: n <= 2^31 - 1");
+        return TL_HIP_ERR_ARG;
+    }
     k_argmax<<<1, 1024, 0, s>>>(x, n, out_idx);
     hipError_t e = hipGetLastError();
     return e == hipSuccess ? TL_HIP_OK : hip_fail(e, "argmax launch");
