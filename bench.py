@@ -149,7 +149,7 @@ def _timed(dev, launch, reps):
     return ms.value / 1e3 / reps
 
 
-def bench_gemm(dev, ms=(512, 128, 16), reps=20):
+def bench_gemm(dev, ms=(512, 128, 16), reps=20, shapes=None):
     """Quantized prefill GEMM on the f16 MFMA path (tl_hip_launch_quant_gemm, mode 1: the
     f32 -> f16 operand conversion + the MFMA kernel) at the configs[2] shapes and M values
     (M = 1 is the matvec leg).  GB/s counts the quant weights + X + Y once."""
@@ -161,7 +161,7 @@ def bench_gemm(dev, ms=(512, 128, 16), reps=20):
     lib = dev.lib
     rows = []
     types = ((GGML_Q4_0, random_q4_0_blocks, "Q4_0"), (GGML_Q8_0, random_q8_0_blocks, "Q8_0"))
-    for m, (t, gen, name), (n, k) in itertools.product(ms, types, GEMM_SHAPES):
+    for m, (t, gen, name), (n, k) in itertools.product(ms, types, shapes or GEMM_SHAPES):
         rng = np.random.default_rng(0x71520000 + n + k)
         raw = gen(rng, n, k)
         # below M = 512 the weight stream bounds the call: rotate copies past the Infinity Cache
@@ -186,6 +186,43 @@ def bench_gemm(dev, ms=(512, 128, 16), reps=20):
             f"({100 * tflops / MFMA_F16_PEAK_TFLOPS:.1f}% of dense f16 MFMA peak), {gbs:.0f} GB/s")
         for q in qs:
             q.release()
+    return rows
+
+
+PREFILL_SHAPES = [(2560, 2048), (2048, 2048), (11264, 2048), (2048, 5632)]  # TinyLlama qkv, o, gate/up, down
+
+
+def bench_vendor_gemm(dev, shapes, m=512, reps=30):
+    """Reference point for the prefill GEMM: the vendor library's plain f16 GEMM
+    (torch.nn.functional.linear -> hipBLASLt) on f16 weights already resident (4 x the Q4_0
+    bytes, no dequantization) at the same M and shapes, timed back to back behind a stall
+    kernel on torch's stream.  Not a product path: nothing in the library calls it."""
+    import ctypes as C
+
+    import torch
+
+    lib = dev.lib
+    # a stream of torch's own (default priority): torch's default stream is the null stream,
+    # and a null handle would send the library's stall and events to the library stream
+    ts = torch.cuda.Stream()
+    lib.tl_hip_set_stream(C.c_void_p(ts.cuda_stream))
+    rows = []
+    try:
+        for n, k in shapes:
+            g = torch.Generator(device="cuda").manual_seed(n * 131 + k)
+            x = torch.randn(m, k, device="cuda", dtype=torch.float16, generator=g)
+            w = torch.randn(n, k, device="cuda", dtype=torch.float16, generator=g) * 0.02
+            torch.cuda.synchronize()
+            with torch.cuda.stream(ts):
+                sec = _timed(dev, lambda i: torch.nn.functional.linear(x, w), reps)
+            tflops = 2.0 * m * n * k / sec / 1e12
+            rows.append({"m": m, "n": n, "k": k, "us": round(sec * 1e6, 2), "tflops": round(tflops, 1),
+                         "frac": round(tflops / MFMA_F16_PEAK_TFLOPS, 4)})
+            log(f"[bench] vendor f16 GEMM (hipBLASLt via torch) M={m} N={n} K={k}: {sec * 1e6:.1f} us, "
+                f"{tflops:.0f} TFLOP/s ({100 * tflops / MFMA_F16_PEAK_TFLOPS:.1f}% of dense f16 MFMA peak)")
+    finally:
+        torch.cuda.synchronize()
+        lib.tl_hip_set_stream(None)
     return rows
 
 
@@ -486,6 +523,9 @@ def main():
     ap.add_argument("--no-extra", action="store_true", help="skip the prefill GEMM and attention legs")
     ap.add_argument("--gemm-only", action="store_true", help="only the prefill GEMM leg (counter runs)")
     ap.add_argument("--gemm-m", type=int, default=0, help="with --gemm-only: this M only (default 512, 128, 16)")
+    ap.add_argument("--vendor-gemm", action="store_true",
+                    help="only the M = 512 prefill GEMM at the configs[2] and TinyLlama shapes beside the vendor "
+                         "library's plain f16 GEMM on f16 weights (a reference point, not a product path)")
     ap.add_argument("--kquant-only", action="store_true", help="only the per-type matvec and Q4_K_M decode legs")
     ap.add_argument("--attention-only", action="store_true", help="only the decode attention leg (counter runs)")
     ap.add_argument("--read-floor", action="store_true",
@@ -498,6 +538,12 @@ def main():
               "run with --gpus 1", file=sys.stderr)
         sys.exit(2)
 
+    if args.vendor_gemm:
+        # torch brings its own HIP runtime: it finds the GPU only when it initialises before
+        # the library does
+        import torch
+        torch.cuda.init()
+
     from tl_amd import HipDevice
     from tl_amd.llama import LlamaConfig
 
@@ -506,6 +552,11 @@ def main():
     if args.prompt + args.warmup + args.steps > cfg.max_seq:
         sys.exit("prompt + warmup + steps exceed the 2048-position cache")
 
+    if args.vendor_gemm:
+        shapes = GEMM_SHAPES + PREFILL_SHAPES
+        print(json.dumps({"prefill_gemm": bench_gemm(dev, ms=(512,), shapes=shapes),
+                          "vendor_f16_gemm": bench_vendor_gemm(dev, shapes)}), flush=True)
+        return
     if args.gemm_only:
         print(json.dumps({"prefill_gemm": bench_gemm(dev, ms=(args.gemm_m,) if args.gemm_m else (512, 128, 16))}),
               flush=True)

@@ -104,14 +104,15 @@ def test_quant_gemm_f16_full_size_m512(dev, t, nk):
     """The prefill GEMMs bench.py times, at their full configs[2] size (M = 512, every row of
     W): the f16 MFMA path against the oracle's threaded f32 product (bit-identical to the
     faithful loop) within the f16 tolerance, and the launch plan that ran: unsplit 128 x 64
-    tiles (at least 256 of them in each shape)."""
+    tiles (at least 256 of them in each shape), 128 x 96 for Q4_0 at N = 11008 (688 tiles of
+    64 would overflow the 512 two-per-CU slots, 460 of 96 do not)."""
     n, k = nk
     m = 512
     rng = np.random.default_rng(0x71550000 + n + t)
     raw = blocks(t, rng, n, k)
     x = rng.standard_normal((m, k)).astype(np.float32)
     y16 = dev.tl_qtensor_matmul_f16(dev.tensor_new(x), QTensor(t, raw, (n, k))).to_numpy()
-    assert _gemm_plan() == (128, 64, 1)
+    assert _gemm_plan() == (128, 96 if t == GGML_Q4_0 and n == 11008 else 64, 1)
     ref = oracle.qtensor_matmul(x, raw, t, n, fast=True)
     assert_rel(y16, ref, F16_TOL)
 
@@ -145,18 +146,21 @@ def test_quant_gemm_f16_split_k(dev, t, m, nk):
 
 
 @pytest.mark.parametrize("t", [GGML_Q4_0, GGML_Q8_0])
-@pytest.mark.parametrize("m,n", [(512, 8192), (300, 8160), (300, 4096)])
+@pytest.mark.parametrize("m,n", [(512, 8192), (300, 8160), (300, 4096), (512, 11264), (300, 12008)])
 def test_quant_gemm_f16_tile_widths(dev, t, m, n):
-    """The f16 MFMA GEMM's two tile widths: 128 x 64 tiles when they give >= 256 workgroups
+    """The f16 MFMA GEMM's tile widths: 128 x 64 tiles when they give >= 256 workgroups
     (512 x 8192, and 300 x 8160 with row and column counts off the tile), 128 x 32 below
-    that (300 x 4096: 3 x 64 wide tiles); short K keeps the oracle fast."""
+    that (300 x 4096: 3 x 64 wide tiles), and for Q4_0 128 x 96 when more than 512 tiles of
+    64 but at most 512 of 96 (512 x 11264; 300 x 12008 with a last tile of 8 columns and a
+    last row tile of 44 rows); short K keeps the oracle fast."""
     k = 256
     rng = np.random.default_rng(0x71530000 + m + n + t)
     raw = blocks(t, rng, n, k)
     x = rng.standard_normal((m, k)).astype(np.float32)
     ref = oracle.qtensor_matmul(x, raw, t, n)
     assert_rel(dev.tl_qtensor_matmul_f16(dev.tensor_new(x), QTensor(t, raw, (n, k))).to_numpy(), ref, F16_TOL)
-    assert _gemm_plan()[:2] == ((128, 32) if n == 4096 else (128, 64))
+    want = 32 if n == 4096 else 96 if t == GGML_Q4_0 and n > 8192 else 64
+    assert _gemm_plan()[:2] == (128, want)
 
 
 @pytest.mark.parametrize("t", [GGML_Q4_0, GGML_Q8_0])

@@ -4,6 +4,7 @@ linear against the CPU oracle (quantized.rs:268-415 restated in oracle/), throug
 max-rel-err = max_i |a_i - b_i| / max(max_j |b_j|, 1e-30); dequant bit-exact, the quantized
 linear 1e-4 on the f32 paths and 1e-2 on the f16-MFMA prefill path (weights dequantized to
 f16 operand order, X rounded to f16)."""
+import ctypes as C
 import json
 import os
 
@@ -11,7 +12,7 @@ import numpy as np
 import pytest
 
 import oracle
-from tl_amd import GGML_Q4_K, GGML_Q6_K, BackendError, QTensor
+from tl_amd import GGML_Q4_K, GGML_Q6_K, BackendError, QTensor, _lib
 from tl_amd.quant import random_q4_k_blocks, random_q6_k_blocks
 
 pytestmark = pytest.mark.gpu
@@ -86,15 +87,21 @@ def test_kquant_gemm(dev, t, m, nk):
 
 
 @pytest.mark.parametrize("t", [GGML_Q4_K, GGML_Q6_K])
-def test_kquant_gemm_f16_wide_tiles(dev, t):
-    """512 x 8192 outputs: the f16 GEMM on the dequantized weights with 128 x 64 tiles (the
-    shapes above all take the 128 x 32 tiles); short K keeps the oracle fast."""
-    m, n, k = 512, 8192, 256
-    rng = np.random.default_rng(0x71570000 + t)
+@pytest.mark.parametrize("n", [8192, 11264])
+def test_kquant_gemm_f16_wide_tiles(dev, t, n):
+    """512 x 8192 and 512 x 11264 outputs on the wide tiles (the shapes above all take the
+    128 x 32 tiles): Q4_K straight from its blocks with per-unit scale words, 128 x 64 tiles
+    and, at 11264 (704 tiles of 64 > 512 two-per-CU slots), 128 x 96; Q6_K through its f16
+    copy on 128 x 64 tiles.  Short K keeps the oracle fast."""
+    m, k = 512, 256
+    rng = np.random.default_rng(0x71570000 + t + n)
     raw = blocks(t, rng, n, k)
     x = rng.standard_normal((m, k)).astype(np.float32)
     ref = oracle.qtensor_matmul(x, raw, t, n)
     assert_rel(dev.tl_qtensor_matmul_f16(dev.tensor_new(x), QTensor(t, raw, (n, k))).to_numpy(), ref, F16_TOL)
+    v = [C.c_int32() for _ in range(3)]
+    assert _lib.load().tl_hip_debug_last_gemm_plan(*[C.byref(x) for x in v]) == 0
+    assert (v[0].value, v[1].value) == (128, 96 if t == GGML_Q4_K and n == 11264 else 64)
 
 
 def test_kquant_upload_errors(dev):

@@ -498,16 +498,17 @@ __global__ __launch_bounds__(512) void k_qgemm_mfma(const uint8_t* __restrict__ 
         if (it + 1 < it1) step(it + 1, S1, S0);
     }
     float* const yb = y + (int64_t)blockIdx.y * m * n;
-    // the k half kh = 1 hands its sums to kh = 0 through the (now free) X tile of S0
-    static_assert(4 * TM * TN * 256 * 4 <= BM * 128 * 2, "reduction space");
+    // the k half kh = 1 hands its sums to kh = 0 through the (now free) X tiles: sub-tiles
+    // 0, 1 in S0's, 2, 3 in S1's
+    static_assert(2 * TM * TN * 256 * 4 <= BM * 128 * 2, "reduction space");
     __syncthreads();
-    float* red = reinterpret_cast<float*>(S0.X);
+    float* red = reinterpret_cast<float*>(sub < 2 ? S0.X : S1.X) + (sub & 1) * TM * TN * 256;
     if (kh == 1) {
 #pragma unroll
         for (int i = 0; i < TM; i++)
 #pragma unroll
             for (int j = 0; j < TN; j++)
-                *reinterpret_cast<floatx4*>(red + ((sub * TM + i) * TN + j) * 256 + lane * 4) = acc[i][j];
+                *reinterpret_cast<floatx4*>(red + (i * TN + j) * 256 + lane * 4) = acc[i][j];
     }
     __syncthreads();
     if (kh == 0) {
@@ -515,7 +516,7 @@ __global__ __launch_bounds__(512) void k_qgemm_mfma(const uint8_t* __restrict__ 
         for (int i = 0; i < TM; i++)
 #pragma unroll
             for (int j = 0; j < TN; j++) {
-                const floatx4 o = *reinterpret_cast<const floatx4*>(red + ((sub * TM + i) * TN + j) * 256 + lane * 4);
+                const floatx4 o = *reinterpret_cast<const floatx4*>(red + (i * TN + j) * 256 + lane * 4);
                 const int64_t c = n0 + wn * (BN / 2) + 16 * j + col;
 #pragma unroll
                 for (int e = 0; e < 4; e++) {
@@ -602,11 +603,10 @@ __global__ __launch_bounds__(256) void k_splitk_sum(const float* __restrict__ pa
 static thread_local int tls_plan[3] = {0, 0, 0};
 
 namespace {
-// Launch plan of one f16 GEMM: row tile bm, wide (128 x 64) or narrow (x 32) tiles, tile count
-// and K splits.
+// Launch plan of one f16 GEMM: row tile bm, column tile bn (128 x 96 or 128 x 64 wide tiles,
+// x 32 narrow ones), tile count and K splits.
 struct F16qPlan {
-    int bm;
-    bool wide;
+    int bm, bn;
     int64_t tiles, nsp;
 };
 }  // namespace
@@ -622,6 +622,12 @@ static F16qPlan plan_f16q(const QWeight* w, int64_t m, const GemmEpi& ep, const 
     const bool f16w = (w->ggml_type == TL_HIP_GGML_Q4_K && !w->us) || w->ggml_type == TL_HIP_GGML_Q6_K;
     const int64_t wide_tiles = cdiv(m, BM) * cdiv(w->n, 64);
     const bool wide = f16w ? wide_tiles > 128 : wide_tiles >= 256;
+    // 128 x 96 tiles (4-bit types with 16-byte blocks: 79 KB of LDS, still two workgroups per
+    // CU) when the 128 x 64 tiles overflow the 512 two-per-CU slots and 96-wide ones do not:
+    // one wave of workgroups instead of a full one and a partial second
+    const bool nib16 = w->ggml_type == TL_HIP_GGML_Q4_0 || (w->ggml_type == TL_HIP_GGML_Q4_K && w->us);
+    const int64_t t96 = cdiv(m, BM) * cdiv(w->n, 96);
+    const int bn = !wide ? 32 : nib16 && wide_tiles > 512 && t96 <= 512 ? 96 : 64;
     // Short inputs: 32- or 64-row tiles when M fits them, and with at most one tile per CU
     // (512 tiles for M <= 32, where the K loop's latency dominates) the K range split over up
     // to 16 workgroup rows until about 512 workgroups run (the 512-token prefill's 256-tile
@@ -632,7 +638,7 @@ static F16qPlan plan_f16q(const QWeight* w, int64_t m, const GemmEpi& ep, const 
     // including the X conversion; splitting the 344 tiles of 11008 x 4096 in two at M = 128
     // was slower, 37.0 -> 44.7 us, and faster at M = 16, 23.6 -> 20.5 us.)
     const int bm = wide ? BM : m <= 32 ? 32 : m <= 64 ? 64 : BM;
-    const int64_t tiles = cdiv(m, bm) * cdiv(w->n, wide ? 64 : 32);
+    const int64_t tiles = cdiv(m, bm) * cdiv(w->n, bn);
     const int64_t iters = w->nb / Q_KR;
     int64_t nsp = 1;
     const bool vec_ok = ((reinterpret_cast<uintptr_t>(y) | reinterpret_cast<uintptr_t>(ep.res)) & 15) == 0;
@@ -640,7 +646,7 @@ static F16qPlan plan_f16q(const QWeight* w, int64_t m, const GemmEpi& ep, const 
         nsp = std::min<int64_t>(std::min<int64_t>(cdiv(512, tiles), iters), 16);
         nsp = cdiv(iters, cdiv(iters, nsp));  // every split non-empty
     }
-    return F16qPlan{bm, wide, tiles, nsp};
+    return F16qPlan{bm, bn, tiles, nsp};
 }
 
 // part_ws / noalloc: the split-K partials go to the caller's workspace and nothing is
@@ -673,8 +679,7 @@ int launch_gemm_f16q(const QWeight* w, const _Float16* x16, float* y, int64_t m,
     }
     constexpr int BM = 128;
     const F16qPlan plan = plan_f16q(w, m, ep, y);
-    const int bm = plan.bm;
-    const bool wide = plan.wide;
+    const int bm = plan.bm, bn = plan.bn;
     const int64_t tiles = plan.tiles, nsp = plan.nsp;
     const bool defer = defer_part && nsp > 1 && !noalloc;
     if (defer_part) {
@@ -682,7 +687,7 @@ int launch_gemm_f16q(const QWeight* w, const _Float16* x16, float* y, int64_t m,
         *defer_nsp = 1;
     }
     tls_plan[0] = bm;
-    tls_plan[1] = wide ? 64 : 32;
+    tls_plan[1] = bn;
     tls_plan[2] = (int)nsp;
     float* part = nullptr;
     if (nsp > 1) {
@@ -697,7 +702,10 @@ int launch_gemm_f16q(const QWeight* w, const _Float16* x16, float* y, int64_t m,
     const dim3 grid((unsigned)tiles, (unsigned)nsp);
     auto gemm = [&](auto qt, const uint8_t* q, const __half* d) {
         constexpr int QT = decltype(qt)::value;
-        if (wide) k_qgemm_mfma<QT, BM, 64><<<grid, 512, 0, s>>>(q, d, x16, out, m, w->n, w->k, w->nb, pe);
+        constexpr bool NIB16 = QT == TL_HIP_GGML_Q4_0 || QT == TL_HIP_GGML_Q4_K;
+        if (NIB16 && bn == 96) {
+            if constexpr (NIB16) k_qgemm_mfma<QT, BM, 96><<<grid, 512, 0, s>>>(q, d, x16, out, m, w->n, w->k, w->nb, pe);
+        } else if (bn == 64) k_qgemm_mfma<QT, BM, 64><<<grid, 512, 0, s>>>(q, d, x16, out, m, w->n, w->k, w->nb, pe);
         else if (bm == 32) k_qgemm_mfma<QT, 32, 32><<<grid, 512, 0, s>>>(q, d, x16, out, m, w->n, w->k, w->nb, pe);
         else if (bm == 64) k_qgemm_mfma<QT, 64, 32><<<grid, 512, 0, s>>>(q, d, x16, out, m, w->n, w->k, w->nb, pe);
         else k_qgemm_mfma<QT, BM, 32><<<grid, 512, 0, s>>>(q, d, x16, out, m, w->n, w->k, w->nb, pe);
