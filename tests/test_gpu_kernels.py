@@ -103,16 +103,18 @@ def _gemm_plan():
 def test_quant_gemm_f16_full_size_m512(dev, t, nk):
     """The prefill GEMMs bench.py times, at their full configs[2] size (M = 512, every row of
     W): the f16 MFMA path against the oracle's threaded f32 product (bit-identical to the
-    faithful loop) within the f16 tolerance, and the launch plan that ran: unsplit 128 x 64
-    tiles (at least 256 of them in each shape), 128 x 96 for Q4_0 at N = 11008 (688 tiles of
-    64 would overflow the 512 two-per-CU slots, 460 of 96 do not)."""
+    faithful loop) within the f16 tolerance, and the launch plan that ran: 128 x 64 tiles (at
+    least 256 of them in each shape), 128 x 96 for Q4_0 at N = 11008 (688 tiles of 64 would
+    overflow the 512 two-per-CU slots, 460 of 96 do not), and for Q4_0 at K = 11008 the K
+    range split in two (256 tiles, two workgroups per CU) with the partial sums added after."""
     n, k = nk
     m = 512
     rng = np.random.default_rng(0x71550000 + n + t)
     raw = blocks(t, rng, n, k)
     x = rng.standard_normal((m, k)).astype(np.float32)
     y16 = dev.tl_qtensor_matmul_f16(dev.tensor_new(x), QTensor(t, raw, (n, k))).to_numpy()
-    assert _gemm_plan() == (128, 96 if t == GGML_Q4_0 and n == 11008 else 64, 1)
+    q4 = t == GGML_Q4_0
+    assert _gemm_plan() == (128, 96 if q4 and n == 11008 else 64, 2 if q4 and k == 11008 else 1)
     ref = oracle.qtensor_matmul(x, raw, t, n, fast=True)
     assert_rel(y16, ref, F16_TOL)
 

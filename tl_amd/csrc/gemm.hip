@@ -645,6 +645,12 @@ static F16qPlan plan_f16q(const QWeight* w, int64_t m, const GemmEpi& ep, const 
     if (!wide && ep.mode != GEMM_GLU16 && vec_ok && tiles <= (m <= 32 ? 512 : 256)) {
         nsp = std::min<int64_t>(std::min<int64_t>(cdiv(512, tiles), iters), 16);
         nsp = cdiv(iters, cdiv(iters, nsp));  // every split non-empty
+    } else if (nib16 && bn == 64 && ep.mode != GEMM_GLU16 && vec_ok && tiles <= 256 && iters >= 64) {
+        // at most one 128 x 64 tile per CU over a long K: two K halves fill the second
+        // workgroup slot of each CU (Q4_0 4096 x 11008, M = 512: 81.0 -> 75.9 us with the
+        // partial sums; 4096 x 4096 unchanged; Q8_0 and f16 weights run one workgroup per
+        // CU and lose: Q8_0 89.9 -> 99.1 us)
+        nsp = 2;
     }
     return F16qPlan{bm, bn, tiles, nsp};
 }
