@@ -692,9 +692,10 @@ __global__ __launch_bounds__(64 * W) void k_attn_qh(const float* __restrict__ q_
     }
 }
 
-// ---- causal prefill form (f16 cache, f16 MFMA): one workgroup per (block of queries, KV head)
-// The workgroup's 128 rows are (query, head) pairs of its QB = 128 / G queries and the G heads
-// of the KV head; wavefront w owns rows 32 w .. 32 w + 31 (two 16-row tiles).  Per 64-position
+// ---- causal prefill form (f16 cache, f16 MFMA): one workgroup per (block of queries, KV head,
+// head half).  The workgroup's 128 / HS rows are (query, head) pairs of its QB = 128 / G
+// queries and G / HS of the KV head's G heads; wavefront w owns RT = 2 / HS 16-row tiles
+// (HS = 2: twice the workgroups, each KV tile staged by both halves).  Per 64-position
 // KV tile (K row-major, V transposed, both in LDS):
 //   S^T = K Q^T   (v_mfma_f32_16x16x32_f16: A = K rows from LDS, B = q from registers), so a
 //                 lane holds row l % 16's scores for positions 4 (l / 16) .. +3 of each
@@ -708,7 +709,7 @@ __global__ __launch_bounds__(64 * W) void k_attn_qh(const float* __restrict__ q_
 typedef _Float16 half8v __attribute__((ext_vector_type(8)));
 typedef float floatx4v __attribute__((ext_vector_type(4)));
 
-template <int D, int G>
+template <int D, int G, int HS>
 __global__ __launch_bounds__(256) void k_attn_prefill(const float* __restrict__ q, const __half* __restrict__ kc,
                                                       const __half* __restrict__ vc, float* __restrict__ out,
                                                       int n, int hkv, int64_t lmax, const int32_t* __restrict__ pos_dev,
@@ -718,6 +719,8 @@ __global__ __launch_bounds__(256) void k_attn_prefill(const float* __restrict__ 
     asm volatile("" : : "s"(q), "s"(kc), "s"(vc), "s"(out), "s"(n), "s"(hkv), "s"(lmax), "s"(pos_dev), "s"(pos_host),
                  "s"(scale), "s"(out16), "s"(order));
     constexpr int QB = 128 / G;   // queries per workgroup
+    constexpr int GH = G / HS;    // heads per workgroup
+    constexpr int RT = 2 / HS;    // 16-row tiles per wavefront
     constexpr int KT = 64;        // positions per KV tile
     constexpr int KS = D / 32;    // MFMA k-steps over the head dim
     constexpr int CPR = D / 8;    // 16-byte chunks per K row
@@ -725,28 +728,28 @@ __global__ __launch_bounds__(256) void k_attn_prefill(const float* __restrict__ 
     __shared__ __attribute__((aligned(16))) _Float16 Vt[D * KT];  // [dim][pos], 8-byte run j of dim d at j ^ (d & 15)
     const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform: SGPR
     const int col = lane & 15, g = lane >> 4;
-    const int qb = blockIdx.x, h = blockIdx.y;
+    const int qb = blockIdx.x, h = blockIdx.y / HS, hs = blockIdx.y % HS;
     const int hq = hkv * G;
     const int64_t pos0 = pos_dev ? (int64_t)*pos_dev : pos_host;
     const __half* kb = kc + (int64_t)h * lmax * D;
     const __half* vb = vc + (int64_t)h * lmax * D;
 
-    // this lane's two rows (one per 16-row tile): query qi, head hh
-    int qi[2], hh[2];
-    int64_t prow[2];
+    // this lane's rows (one per 16-row tile): query qi, head hh
+    int qi[RT], hh[RT];
+    int64_t prow[RT];
 #pragma unroll
-    for (int rt = 0; rt < 2; rt++) {
-        const int r = 32 * wave + 16 * rt + col;
-        qi[rt] = qb * QB + r / G;
-        hh[rt] = h * G + r % G;
+    for (int rt = 0; rt < RT; rt++) {
+        const int r = 16 * RT * wave + 16 * rt + col;
+        qi[rt] = qb * QB + r / GH;
+        hh[rt] = h * G + hs * GH + r % GH;
         prow[rt] = pos0 + (qi[rt] < n ? qi[rt] : n - 1);
     }
     // B operand of S^T: q[row][32 ks + 8 g .. +7] * scale * log2(e), in f16: scores in log2
     // units, so the softmax exponentials are single hardware exp2 instructions
     const float sl2 = scale * 1.44269504088896341f;
-    half8v qop[2][KS];
+    half8v qop[RT][KS];
 #pragma unroll
-    for (int rt = 0; rt < 2; rt++) {
+    for (int rt = 0; rt < RT; rt++) {
         const int qq = qi[rt] < n ? qi[rt] : n - 1;
         const float* qp = q + ((int64_t)qq * hq + hh[rt]) * D;
 #pragma unroll
@@ -758,12 +761,15 @@ __global__ __launch_bounds__(256) void k_attn_prefill(const float* __restrict__ 
                                  (_Float16)(b.z * sl2), (_Float16)(b.w * sl2)};
         }
     }
-    floatx4v o[2][D / 16];  // O^T tiles: [row tile][dim tile], lane: dims 4 g .. +3 of row col
+    floatx4v o[RT][D / 16];  // O^T tiles: [row tile][dim tile], lane: dims 4 g .. +3 of row col
+    float mrow[RT], lrow[RT];
 #pragma unroll
-    for (int rt = 0; rt < 2; rt++)
+    for (int rt = 0; rt < RT; rt++) {
 #pragma unroll
         for (int dt = 0; dt < D / 16; dt++) o[rt][dt] = floatx4v{0.f, 0.f, 0.f, 0.f};
-    float mrow[2] = {-INFINITY, -INFINITY}, lrow[2] = {0.f, 0.f};
+        mrow[rt] = -INFINITY;
+        lrow[rt] = 0.f;
+    }
 
     const int64_t last = pos0 + (int64_t)((qb + 1) * QB < n ? (qb + 1) * QB : n);  // positions needed
     const int ntiles = (int)((last + KT - 1) / KT);
@@ -803,11 +809,11 @@ __global__ __launch_bounds__(256) void k_attn_prefill(const float* __restrict__ 
         if (tile + 1 < ntiles) fetch(tile + 1);
         __syncthreads();
         // S^T = K Q^T over the tile: [pos tile pt][row tile rt]
-        floatx4v st[4][2];
+        floatx4v st[4][RT];
 #pragma unroll
         for (int pt = 0; pt < 4; pt++)
 #pragma unroll
-            for (int rt = 0; rt < 2; rt++) st[pt][rt] = floatx4v{0.f, 0.f, 0.f, 0.f};
+            for (int rt = 0; rt < RT; rt++) st[pt][rt] = floatx4v{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
         for (int pt = 0; pt < 4; pt++) {
             const int r = 16 * pt + col;
@@ -816,14 +822,14 @@ __global__ __launch_bounds__(256) void k_attn_prefill(const float* __restrict__ 
                 const int c = 4 * ks + g;
                 const half8v a = *reinterpret_cast<const half8v*>(&Ks[r * D + 8 * (c ^ (r & (CPR - 1)))]);
 #pragma unroll
-                for (int rt = 0; rt < 2; rt++)
+                for (int rt = 0; rt < RT; rt++)
                     st[pt][rt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, qop[rt][ks], st[pt][rt], 0, 0, 0);
             }
         }
         // causal mask, online softmax per row (row col's scores: this lane and lanes col + 16 g)
-        half8v pop[2][2];  // B operand of O^T: [k-step][row tile]
+        half8v pop[2][RT];  // B operand of O^T: [k-step][row tile]
 #pragma unroll
-        for (int rt = 0; rt < 2; rt++) {
+        for (int rt = 0; rt < RT; rt++) {
             float mx = -INFINITY;
 #pragma unroll
             for (int pt = 0; pt < 4; pt++)
@@ -868,7 +874,7 @@ __global__ __launch_bounds__(256) void k_attn_prefill(const float* __restrict__ 
                 const uint2 hi = *reinterpret_cast<const uint2*>(&Vt[d * KT + 4 * j1]);
                 const half8v a = __builtin_bit_cast(half8v, make_uint4(lo.x, lo.y, hi.x, hi.y));
 #pragma unroll
-                for (int rt = 0; rt < 2; rt++)
+                for (int rt = 0; rt < RT; rt++)
                     o[rt][dt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, pop[ks][rt], o[rt][dt], 0, 0, 0);
             }
         }
@@ -876,16 +882,22 @@ __global__ __launch_bounds__(256) void k_attn_prefill(const float* __restrict__ 
     // out[query][head][dims 16 dt + 4 g .. +3] = O / l, f32 or (out16) f16 in the operand order
     // of the GEMM that reads the [n, hq D] rows
 #pragma unroll
-    for (int rt = 0; rt < 2; rt++) {
+    for (int rt = 0; rt < RT; rt++) {
         if (qi[rt] >= n) continue;
         const float rl = 1.0f / lrow[rt];
         if (out16) {
+            // o / l rounded to f32 and then to f16 for every element: the product is pinned in a
+            // register first -- left alone, the compiler fuses some of these conversions into
+            // one-rounding mixed FMAs (v_fma_mix) and not others, depending on the instantiation
 #pragma unroll
             for (int dt = 0; dt < D / 16; dt++)
 #pragma unroll
-                for (int i = 0; i < 4; i++)
+                for (int i = 0; i < 4; i++) {
+                    float v = o[rt][dt][i] * rl;
+                    asm volatile("" : "+v"(v));
                     out16[f16q_index(qi[rt], (int64_t)hh[rt] * D + 16 * dt + 4 * g + i, (int64_t)hq * D, order)] =
-                        (_Float16)(o[rt][dt][i] * rl);
+                        (_Float16)v;
+                }
         } else {
             float* op = out + ((int64_t)qi[rt] * hq + hh[rt]) * D;
 #pragma unroll
@@ -906,13 +918,18 @@ int launch_attention_prefill(const float* q, const void* k, const void* v, float
                              hipStream_t s, _Float16* out16, int order) {
     const int G = hq / hkv;
     if (n < 1) return TL_HIP_OK;
-    dim3 grid((unsigned)cdiv(n, 128 / G), hkv);
+    constexpr int HS = 2;  // head halves per KV head: one 16-row tile per wavefront
+    if (hkv > 65535 / HS) {
+        set_error(TL_HIP_ERR_ARG, "ArgumentError: prefill attention takes at most %d KV heads", 65535 / HS);
+        return TL_HIP_ERR_ARG;
+    }
+    dim3 grid((unsigned)cdiv(n, 128 / G), hkv * HS);
     const __half* kh = static_cast<const __half*>(k);
     const __half* vh = static_cast<const __half*>(v);
-    if (D == 64 && G == 8) k_attn_prefill<64, 8><<<grid, 256, 0, s>>>(q, kh, vh, out, n, hkv, lmax, pos_dev, pos_host, scale, out16, order);
-    else if (D == 64 && G == 4) k_attn_prefill<64, 4><<<grid, 256, 0, s>>>(q, kh, vh, out, n, hkv, lmax, pos_dev, pos_host, scale, out16, order);
-    else if (D == 128 && G == 8) k_attn_prefill<128, 8><<<grid, 256, 0, s>>>(q, kh, vh, out, n, hkv, lmax, pos_dev, pos_host, scale, out16, order);
-    else if (D == 128 && G == 4) k_attn_prefill<128, 4><<<grid, 256, 0, s>>>(q, kh, vh, out, n, hkv, lmax, pos_dev, pos_host, scale, out16, order);
+    if (D == 64 && G == 8) k_attn_prefill<64, 8, HS><<<grid, 256, 0, s>>>(q, kh, vh, out, n, hkv, lmax, pos_dev, pos_host, scale, out16, order);
+    else if (D == 64 && G == 4) k_attn_prefill<64, 4, HS><<<grid, 256, 0, s>>>(q, kh, vh, out, n, hkv, lmax, pos_dev, pos_host, scale, out16, order);
+    else if (D == 128 && G == 8) k_attn_prefill<128, 8, HS><<<grid, 256, 0, s>>>(q, kh, vh, out, n, hkv, lmax, pos_dev, pos_host, scale, out16, order);
+    else if (D == 128 && G == 4) k_attn_prefill<128, 4, HS><<<grid, 256, 0, s>>>(q, kh, vh, out, n, hkv, lmax, pos_dev, pos_host, scale, out16, order);
     else {
         set_error(TL_HIP_ERR_ARG, "ArgumentError: prefill attention covers f16 caches, head_dim 64 / 128, 4 or 8 query "
                   "heads per KV head");
@@ -1262,7 +1279,7 @@ extern "C" tl_hip_tensor* tl_hip_attention_prefill(const tl_hip_tensor* qh, cons
                   (long long)hq, (long long)D, (long long)hkv, (long long)lmax, (long long)k->shape[2]);
         return nullptr;
     }
-    if (!attention_prefill_supported(TL_HIP_F16, (int)hq, (int)hkv, (int)D) || hkv > 65535) {
+    if (!attention_prefill_supported(TL_HIP_F16, (int)hq, (int)hkv, (int)D) || hkv > 32767) {
         set_error(TL_HIP_ERR_ARG, "ArgumentError: prefill attention covers head_dim 64 / 128 with 4 or 8 query heads "
                   "per KV head");
         return nullptr;
