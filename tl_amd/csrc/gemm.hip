@@ -498,24 +498,27 @@ __global__ __launch_bounds__(512) void k_qgemm_mfma(const uint8_t* __restrict__ 
         if (it + 1 < it1) step(it + 1, S1, S0);
     }
     float* const yb = y + (int64_t)blockIdx.y * m * n;
-    // the k half kh = 1 hands its sums to kh = 0 through the (now free) X tiles: sub-tiles
-    // 0, 1 in S0's, 2, 3 in S1's
+    // The two k halves add their sums through the (now free) X tiles (sub-tiles 0, 1 in S0's,
+    // 2, 3 in S1's) and share the epilogue: a wavefront finishes the 16 x 16 tiles it owns
+    // (tile index i TN + j of parity kh; all of them for kh = 0 when there is one tile) and
+    // hands its partial sums of the others to the wavefront that owns them.
     static_assert(2 * TM * TN * 256 * 4 <= BM * 128 * 2, "reduction space");
+    constexpr bool SHARE = TM * TN >= 2;
+    auto owns = [&](int i, int j) { return SHARE ? ((i * TN + j) & 1) == kh : kh == 0; };
     __syncthreads();
     float* red = reinterpret_cast<float*>(sub < 2 ? S0.X : S1.X) + (sub & 1) * TM * TN * 256;
-    if (kh == 1) {
 #pragma unroll
-        for (int i = 0; i < TM; i++)
+    for (int i = 0; i < TM; i++)
 #pragma unroll
-            for (int j = 0; j < TN; j++)
-                *reinterpret_cast<floatx4*>(red + (i * TN + j) * 256 + lane * 4) = acc[i][j];
-    }
+        for (int j = 0; j < TN; j++)
+            if (!owns(i, j)) *reinterpret_cast<floatx4*>(red + (i * TN + j) * 256 + lane * 4) = acc[i][j];
     __syncthreads();
-    if (kh == 0) {
+    {
 #pragma unroll
         for (int i = 0; i < TM; i++)
 #pragma unroll
             for (int j = 0; j < TN; j++) {
+                if (!owns(i, j)) continue;
                 const floatx4 o = *reinterpret_cast<const floatx4*>(red + (i * TN + j) * 256 + lane * 4);
                 const int64_t c = n0 + wn * (BN / 2) + 16 * j + col;
 #pragma unroll
