@@ -193,7 +193,10 @@ int tl_hip_read_floor(const tl_hip_qtensor* w, void* stream);
  * the process ends; calls needing more are ArgumentError, as are weights that need an f16 copy
  * for the MFMA path (Q6_K, and Q4_K before its first f16 GEMM through an allocating entry).
  * The f32 path (use_f16_mfma = 0) needs no workspace.  Every call on a GPU shares that array:
- * calls on one stream are ordered, calls that overlap on different streams race. */
+ * calls on one stream are ordered, calls that overlap on different streams race.  Under
+ * hipGraph capture: the array's address is looked up at library initialisation, and the
+ * first library call on a caller stream (which synchronises the library stream once) must
+ * precede the capture -- captured first, it is ArgumentError. */
 int tl_hip_launch_quant_gemm_noalloc(const tl_hip_qtensor* w, const float* x, float* y, int64_t m,
                                      int use_f16_mfma, void* stream);
 /* Tile plan of the calling thread's last f16-MFMA GEMM launch: rows and columns of one
@@ -356,7 +359,9 @@ int32_t tl_hip_llama_sample_greedy(tl_hip_llama* m, double repetition_penalty,
  * sample(temp <= 0) = argmax): first token id `first`, generated ids to out_ids (host).
  * repetition_penalty 1.0 disables the penalty; history holds the prior ids (host). With
  * use_graph != 0 the steps are captured hipGraph replays: one launch per eight steps, then
- * one per remaining step. */
+ * one per remaining step.  Both graph shapes (one step, eight steps) are captured on the
+ * first graph-mode call after a change of penalty value, KV type or RoPE mode, whatever its
+ * n_steps, so later calls only replay. */
 int tl_hip_llama_generate(tl_hip_llama* m, int32_t first, int n_steps, int32_t* out_ids,
                           double repetition_penalty, const int32_t* history, int n_history,
                           int use_graph);

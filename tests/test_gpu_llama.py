@@ -206,6 +206,32 @@ def test_graph_follows_the_penalty_value(small):
     assert builds() == b0
 
 
+@pytest.mark.parametrize("warm,timed", [(5, 20), (8, 3), (1, 9), (16, 7)])
+def test_no_capture_after_the_first_graph_call(small, warm, timed):
+    """bench.py's decode legs: a warm-up generate of `warm` steps, then a timed generate of
+    `timed` steps must only replay, whatever the two lengths are (both graph shapes are
+    captured by the first graph-mode call of a key); also for a changed penalty and KV type.
+    The tokens of the two calls continue the oracle's greedy sequence."""
+    gpu, cpu = small
+    prompt = synthetic_prompt(SMALL, 16, 11)
+    builds = lambda: int(gpu.lib.tl_hip_llama_graph_builds(gpu.h))
+    for kv_f16, pen in ((False, 1.0), (False, 1.1), (True, 1.0)):
+        gpu.configure(kv_f16=kv_f16)
+        gpu.reset()
+        gpu.forward(prompt, want_logits=False)
+        first = gpu.sample_greedy(pen, prompt)
+        hist = np.concatenate([prompt, [first]]).astype(np.int32)
+        b0 = builds()
+        w = gpu.generate(first, warm, pen, hist, use_graph=True)
+        assert builds() == b0 + 2, "the first graph-mode call captures both graph shapes"
+        hist = np.concatenate([hist, w[:-1]]).astype(np.int32)
+        t = gpu.generate(int(w[-1]), timed, pen, hist, use_graph=True)
+        assert builds() == b0 + 2, f"warm-up {warm} then {timed} steps captured inside the second call"
+        if not kv_f16:
+            want = list(cpu.greedy(prompt, 1 + warm + timed, penalty=pen))
+            assert [first] + list(w) + list(t) == want
+
+
 def test_failed_activation_grow_leaves_the_model_usable():
     """An allocation failure while the activation buffers grow for a longer call returns
     AllocationError and leaves no stale buffer or captured step behind: the next short call

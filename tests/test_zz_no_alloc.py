@@ -26,7 +26,15 @@ def _run(dev, lib, entry, hw, x, n):
     m = x.shape[0]
     xt = dev.tensor_new(x)
     yt = dev.tensor_new(np.full((m, n), np.nan, np.float32))
-    rc = entry(hw, C.c_void_p(xt.data_ptr), C.c_void_p(yt.data_ptr), m, 1, None)
+    noalloc = entry.__name__ == "tl_hip_launch_quant_gemm_noalloc"
+    if noalloc:   # any allocation inside the call fails it (AllocationError)
+        dev.synchronize()
+        lib.tl_hip_debug_fail_alloc(0)
+    try:
+        rc = entry(hw, C.c_void_p(xt.data_ptr), C.c_void_p(yt.data_ptr), m, 1, None)
+    finally:
+        if noalloc:
+            lib.tl_hip_debug_fail_alloc(-1)
     assert rc == 0, lib.tl_hip_last_error()
     return yt.to_numpy(), _plan(lib)
 
@@ -86,3 +94,58 @@ def test_noalloc_gemm_limits(dev):
     assert lib.tl_hip_launch_quant_gemm_noalloc(h4, C.c_void_p(xt.data_ptr), C.c_void_p(yt2.data_ptr), 8, 1,
                                                 None) == 0
     assert np.array_equal(yt2.to_numpy(), want)
+
+
+def test_noalloc_gemm_under_graph_capture(dev):
+    """The allocation-free entry captured on a caller stream (hipStreamBeginCapture / EndCapture /
+    Instantiate / Launch): every replay -- with eager library work and a fresh NaN fill of y
+    between replays -- gives the allocating entry's bits, at M = 16 (split-K partials in the
+    scratch) and M = 256.  Allocation is made to fail while the call is captured."""
+    lib = _lib.load()
+    hip = C.CDLL("libamdhip64.so.7")
+    rng = np.random.default_rng(0x71580200)
+    n, k = 2048, 4096
+    raw = random_q4_0_blocks(rng, n, k)
+    w = QTensor(GGML_Q4_0, raw, (n, k))   # kept alive: the handle below belongs to it
+    hw = w.upload(lib)
+    stream = C.c_void_p()
+    assert hip.hipStreamCreateWithFlags(C.byref(stream), 1) == 0
+    try:
+        for m in (16, 256):
+            x = rng.standard_normal((m, k)).astype(np.float32)
+            want, _ = _run(dev, lib, lib.tl_hip_launch_quant_gemm, hw, x, n)
+            xt = dev.tensor_new(x)
+            yt = dev.tensor_new(np.zeros((m, n), np.float32))
+            args = (hw, C.c_void_p(xt.data_ptr), C.c_void_p(yt.data_ptr), m, 1, stream)
+            # one call on the stream before capturing it (the library's first use of a stream)
+            assert lib.tl_hip_launch_quant_gemm_noalloc(*args) == 0, lib.tl_hip_last_error()
+            assert hip.hipStreamSynchronize(stream) == 0
+            graph, gexec = C.c_void_p(), C.c_void_p()
+            lib.tl_hip_debug_fail_alloc(0)
+            try:
+                assert hip.hipStreamBeginCapture(stream, 1) == 0   # thread-local mode
+                rc = lib.tl_hip_launch_quant_gemm_noalloc(*args)
+                assert hip.hipStreamEndCapture(stream, C.byref(graph)) == 0
+            finally:
+                lib.tl_hip_debug_fail_alloc(-1)
+            assert rc == 0, lib.tl_hip_last_error()
+            assert hip.hipGraphInstantiate(C.byref(gexec), graph, None, None, C.c_size_t(0)) == 0
+            try:
+                nan = np.full((m, n), np.nan, np.float32)
+                for rep in range(3):
+                    assert lib.tl_hip_memcpy_h2d(C.c_void_p(yt.data_ptr), nan.ctypes.data_as(C.c_void_p),
+                                                 nan.nbytes) == 0
+                    dev.synchronize()
+                    assert hip.hipGraphLaunch(gexec, stream) == 0
+                    assert hip.hipStreamSynchronize(stream) == 0
+                    got = yt.to_numpy()
+                    assert np.array_equal(got.view(np.uint32), want.view(np.uint32)), f"m={m}: replay {rep} differs"
+                    # eager work on the library stream between replays
+                    again, _ = _run(dev, lib, lib.tl_hip_launch_quant_gemm, hw, x, n)
+                    assert np.array_equal(again.view(np.uint32), want.view(np.uint32))
+            finally:
+                hip.hipGraphExecDestroy(gexec)
+                hip.hipGraphDestroy(graph)
+    finally:
+        hip.hipStreamSynchronize(stream)
+        hip.hipStreamDestroy(stream)

@@ -730,7 +730,10 @@ int launch_gemm_f16q(const QWeight* w, const _Float16* x16, float* y, int64_t m,
         // K-quants: dequantize once into f16 operand order (n * k halves), then the same
         // MFMA pipeline with the weights read as stored
         _Float16* w16 = static_cast<_Float16*>(dev_alloc_on((size_t)w->n * w->k * sizeof(_Float16), s));
-        if (!w16) return TL_HIP_ERR_ALLOC;
+        if (!w16) {
+            if (part && !noalloc) dev_free_on(part, s);
+            return TL_HIP_ERR_ALLOC;
+        }
         const QView qv{w->qs, w->d, w->hdr, w->qh, w->sc};
         const int64_t wunits = w->n * w->nb;
         if (w->ggml_type == TL_HIP_GGML_Q4_K)
@@ -744,13 +747,13 @@ int launch_gemm_f16q(const QWeight* w, const _Float16* x16, float* y, int64_t m,
     } else {
         gemm(std::integral_constant<int, TL_HIP_GGML_Q8_0>{}, w->qs, w->d);
     }
-    if (defer) {
+    hipError_t e = hipGetLastError();
+    if (defer && e == hipSuccess) {  // the partials are the caller's only on success
         *defer_part = part;
         *defer_nsp = (int)nsp;
     } else if (part && !noalloc) {
         dev_free_on(part, s);  // freed on s: reused at once only by later work on s
     }
-    hipError_t e = hipGetLastError();
     return e == hipSuccess ? TL_HIP_OK : hip_fail(e, "quant gemm launch");
 }
 
@@ -910,6 +913,8 @@ static uint8_t* scratch_on(int dev) {
     return g_scratch_ptr[dev];
 }
 
+int noalloc_scratch_init(int device) { return scratch_on(device) ? TL_HIP_OK : tl_hip_last_status(); }
+
 extern "C" int tl_hip_launch_quant_gemm_noalloc(const tl_hip_qtensor* h, const float* x, float* y, int64_t m,
                                                 int use_f16_mfma, void* stream) {
     if (!h || !x || !y) {
@@ -945,6 +950,17 @@ extern "C" int tl_hip_launch_quant_gemm_noalloc(const tl_hip_qtensor* h, const f
                   "allocation-free entry cannot make (use_f16_mfma = 0 takes the f32 path)",
                   ggml_type_name(w->ggml_type));
         return TL_HIP_ERR_ARG;
+    }
+    if (note_stream_syncs(s)) {
+        // the first call on a caller stream synchronises the library stream once (allocator
+        // bookkeeping), which a stream under capture must not see
+        hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+        if (hipStreamIsCapturing(s, &cs) == hipSuccess && cs != hipStreamCaptureStatusNone) {
+            set_error(TL_HIP_ERR_ARG, "ArgumentError: the first library call on a caller stream cannot be captured; "
+                      "make one call on that stream before capturing it");
+            return TL_HIP_ERR_ARG;
+        }
+        (void)hipGetLastError();
     }
     note_stream(s);
     uint8_t* base = scratch_on(st->device);

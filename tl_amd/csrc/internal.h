@@ -69,6 +69,11 @@ void dev_free_on(void* p, hipStream_t s);
 // Marks that work runs on stream s; the first stream other than the library stream switches
 // the allocator to event-tagged frees.
 void note_stream(hipStream_t s);
+// True when note_stream(s) would synchronise the library stream (the first caller stream).
+bool note_stream_syncs(hipStream_t s);
+// Looks up the device address of the allocation-free GEMM's scratch array on `device` (the
+// current device during library initialisation); status code.
+int noalloc_scratch_init(int device);
 
 // ---- tensors ---------------------------------------------------------------------
 struct Tensor {

@@ -139,7 +139,8 @@ struct Llama {
     int max_out = 0;
     int64_t host_pos = 0;
     // the decode step captured as hipGraphs: graph[0] holds one step, graph[1] GRAPH_STEPS
-    // consecutive steps (one graph launch per GRAPH_STEPS tokens); built on first use
+    // consecutive steps (one graph launch per GRAPH_STEPS tokens); both built on the first
+    // graph-mode call for a key
     hipGraphExec_t graph[2] = {nullptr, nullptr};
     // what the captured steps were built for: penalty bits (the value is a kernel argument),
     // kv_f16, rope_per_token
@@ -1016,9 +1017,12 @@ int tl_hip_llama_generate(tl_hip_llama* h, int32_t first, int n_steps, int32_t* 
             free_graph(m);
             std::memcpy(m->graph_key, key, sizeof(key));
         }
+        // both graph shapes are captured on the first graph-mode call for a key, whatever its
+        // n_steps: a later call of any length then only replays (a capture is ~10 ms of host
+        // work, which must not land inside a caller's timed or latency-bound call)
         const int n_multi = n_steps / GRAPH_STEPS, n_single = n_steps % GRAPH_STEPS;
         for (int gi = 0; gi < 2; gi++) {
-            if (m->graph[gi] || (gi == 0 ? n_single : n_multi) == 0) continue;
+            if (m->graph[gi]) continue;
             hipGraph_t g;
             TLH_CHECK_HIP(hipStreamBeginCapture(s, hipStreamCaptureModeThreadLocal));
             for (int i = 0; i < (gi == 0 ? 1 : GRAPH_STEPS) && rc == 0; i++) rc = enqueue_step(m, pen, s);

@@ -68,6 +68,9 @@ static int init_locked(int device) {
     TLH_CHECK_HIP(hipStreamCreateWithFlags(&g_state.stream, hipStreamNonBlocking));
     g_state.device = device;
     g_state.num_cus = prop.multiProcessorCount;
+    // the allocation-free GEMM's fixed scratch: its address is looked up here, once, so that
+    // entry never does it inside a caller's graph capture
+    if (int rc = noalloc_scratch_init(device)) return rc;
     g_ready = true;
     return TL_HIP_OK;
 }
@@ -99,6 +102,10 @@ static std::map<void*, size_t> g_live;           // block -> class size
 static std::vector<hipEvent_t> g_ev_pool;
 static std::atomic<bool> g_multi{false};
 static std::atomic<int64_t> g_fail_after{-1};    // fault injection: allocations until a failure
+
+bool note_stream_syncs(hipStream_t s) {
+    return s && !g_multi.load(std::memory_order_acquire) && state() && s != g_state.stream;
+}
 
 void note_stream(hipStream_t s) {
     if (!s || g_multi.load(std::memory_order_acquire) || !state() || s == g_state.stream) return;
