@@ -189,7 +189,8 @@ int tl_hip_read_floor(const tl_hip_qtensor* w, void* stream);
  * callers that cannot allocate device memory -- code under hipGraph capture, serving loops
  * that forbid hipMalloc.  Same arguments and results; calls no hipMalloc / hipFree.  The f16
  * MFMA path keeps its workspace (X converted to f16: m * k * 2 bytes rounded up to 256, then
- * the split-K partial tiles of short inputs) in a fixed 32 MiB device array per GPU, held until
+ * the split-K partial tiles of 17-64-row inputs; inputs of up to 16 rows need none) in a
+ * fixed 32 MiB device array per GPU, held until
  * the process ends; calls needing more are ArgumentError, as are weights that need an f16 copy
  * for the MFMA path (Q6_K, and Q4_K before its first f16 GEMM through an allocating entry).
  * The f32 path (use_f16_mfma = 0) needs no workspace.  Every call on a GPU shares that array:

@@ -169,8 +169,9 @@ def test_quant_gemm_f16_tile_widths(dev, t, m, n):
 @pytest.mark.parametrize("m", [5, 16, 32, 33, 64])
 def test_quant_gemm_f16_short_tiles_split_k(dev, t, m):
     """Op calls with 32- or 64-row tiles and K split over workgroup rows (17 iterations of 128:
-    an uneven last range): the row tile that ran, the oracle within the f16 tolerance, and
-    the same bits from the allocation-free entry on the same inputs."""
+    an uneven last range) -- or, up to 16 rows, the one-launch short-input kernel: the row
+    tile that ran, the oracle within the f16 tolerance, and the same bits from the
+    allocation-free entry on the same inputs."""
     n, k = 2048, 2176
     rng = np.random.default_rng(0x71570000 + m + t)
     raw = blocks(t, rng, n, k)
@@ -178,7 +179,10 @@ def test_quant_gemm_f16_short_tiles_split_k(dev, t, m):
     q = QTensor(t, raw, (n, k))
     y16 = dev.tl_qtensor_matmul_f16(dev.tensor_new(x), q).to_numpy()
     plan = _gemm_plan()
-    assert plan[0] == (32 if m <= 32 else 64) and plan[2] > 1
+    if m <= 16:
+        assert plan[0] == (8 if m <= 8 else 16)
+    else:
+        assert plan[0] == (32 if m <= 32 else 64) and plan[2] > 1
     assert_rel(y16, oracle.qtensor_matmul(x, raw, t, n), F16_TOL)
     lib = _lib.load()
     hw = q.upload(lib)

@@ -301,10 +301,31 @@ def test_tinyllama_greedy_golden():
     # the performance configuration (f16 KV cache, f16-MFMA prefill) on the same model
     m.configure(kv_f16=True)
     got16 = greedy_generate(m, prompt, len(gold["tokens"]), prefill_f16=True)
+    # its top-2 logit margins, teacher-forced along the golden tokens (eager forward calls of
+    # the same precision class), beside the oracle's: a flip whose margin on either side is
+    # within f16 rounding of the logits is a precision event, not a wiring fault
+    m.reset()
+    lg = m.forward(prompt, prefill_f16=True)
+    rows = []
+    for i, t in enumerate(gold["tokens"]):
+        a, b = (int(v) for v in np.argsort(lg, kind="stable")[::-1][:2])
+        rows.append((i, a, b, float(lg[a] - lg[b]), float(lg[a] - lg[t]), gold["top2_margins"][i]))
+        lg = m.forward([t], prefill_f16=True)
     m.close()
+    print("step  f16 top-1  top-2  f16 margin  f16 top-1 - golden  oracle margin")
+    for r in rows:
+        print(f"{r[0]:4d} {r[1]:9d} {r[2]:6d} {r[3]:11.3e} {r[4]:19.3e} {r[5]:14.3e}")
+    print(f"smallest f16 margin {min(r[3] for r in rows):.3e}, smallest oracle margin "
+          f"{min(r[5] for r in rows):.3e}")
     agree = int(np.argmax(np.array(list(got16) + [-1]) != np.array(gold["tokens"] + [-2])))
     print(f"f16 KV / f16 prefill: first {agree} of {len(gold['tokens'])} tokens agree")
-    assert list(got16) == gold["tokens"]
+    if agree < len(gold["tokens"]):
+        i = agree
+        r = rows[i]
+        pytest.fail(f"f16 path: step {i} chose {int(got16[i])}, the oracle {gold['tokens'][i]}; teacher-forced f16 "
+                    f"logits there: top-1 {r[1]}, top-2 {r[2]}, margin {r[3]:.3e}, top-1 minus the golden token "
+                    f"{r[4]:.3e}; the oracle's top-2 margin {r[5]:.3e} (an f16 rounding flip has both margins "
+                    f"near the f16 logit error, ~1e-3)")
 
 
 def _q8_handoff_plan(cfg, layer, which):

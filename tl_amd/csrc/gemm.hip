@@ -15,6 +15,9 @@
 
 namespace tlhip {
 
+// tile plan of the calling thread's last f16 GEMM launch (tl_hip_debug_last_gemm_plan)
+static thread_local int tls_plan[3] = {0, 0, 0};
+
 // Residency buffers of a quantized weight (layout at struct QWeight).
 struct QView {
     const uint8_t* qs;
@@ -542,6 +545,330 @@ __global__ __launch_bounds__(512) void k_qgemm_mfma(const uint8_t* __restrict__ 
 }
 
 
+// ------------------------------------------------------ short-input quantized GEMM ----
+// Y[m, n] = sum_k X[m, k] W[n, k] for short inputs (m <= 16 rows: chat prompts, the M = 16
+// case of a prefill GEMM), reading X in f32 (no X conversion launch).  A workgroup of
+// SG_WAVES wavefronts owns a tile of SG_WAVES x 16 NR weight rows (16 NR per wavefront) and
+// one range of the 128-k groups of K (grid.y = the K splits).  Per group the wavefronts stage
+// X once, shared: each loads its rows' part (coalesced, two rows' 512 bytes per
+// instruction), rounds it to f16 and writes it to the LDS tile in the A-operand order of the
+// weight type; after a barrier every wavefront reads its four 16-byte A fragments and runs
+// 4 NR MFMAs (v_mfma_f32_16x16x32_f16) over its own rows.  Weights are the B operand as in
+// k_qgemm_mfma: lane (col, g) holds row col's block g of the group, word t feeding MFMA t
+// (QWords operand builders, one f16 rounding of the dequantized value), loaded non-temporal.
+// Loads run one group ahead.  With more than one split each workgroup stores its partial
+// tile in a workspace slice and k_splitk_sum_short adds the slices in K order, so the result
+// does not depend on scheduling.
+// Measured on MI355X (rocprofv3, M = 16): a CU's L1 takes ~64 misses in flight, each ~350-460
+// cycles to L2 and back, so the number of L2 requests per CU sets the pace.  X is most of
+// them when every wavefront fetches its own copy (64 bytes per k at m = 16, against 0.56
+// (Q4_0) or 1.06 (Q8_0) per k and weight row), hence one shared copy per workgroup and a
+// wide tile; splitting K spreads the tiles over every CU.
+__global__ void k_splitk_sum(const float* __restrict__ part, float* y, const float* res, int64_t mn, int nsp);
+
+constexpr int SG_WAVES = 4;   // wavefronts per workgroup (they split the tile's rows)
+constexpr int SG_PITCH = 68;  // LDS words per X row of one 128-k group (64 + 4)
+
+template <int QT, int MT, int NR>
+__global__ __launch_bounds__(64 * SG_WAVES) void k_qgemm_short(const uint8_t* __restrict__ qs,
+                                                               const void* __restrict__ dsc,
+                                                               const float* __restrict__ x, float* __restrict__ y,
+                                                               int m, int64_t n, int64_t k, int64_t nb) {
+    asm volatile("" : : "s"(qs), "s"(dsc), "s"(x), "s"(y), "s"(m), "s"(n), "s"(k), "s"(nb));
+    constexpr bool Q8 = QT == TL_HIP_GGML_Q8_0, K4 = QT == TL_HIP_GGML_Q4_K;
+    constexpr int QB = Q8 ? 32 : 16, WV = QB / 16;
+    constexpr int XI = MT / (2 * SG_WAVES);  // X load instructions per wavefront and group (two rows each)
+    static_assert(XI >= 1, "tile");
+    __shared__ __attribute__((aligned(16))) uint32_t xs[4][16 * SG_PITCH];
+    const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int col = lane & 15, g = lane >> 4;
+    const int64_t n0 = ((int64_t)blockIdx.x * SG_WAVES + wave) * 16 * NR;
+    const int64_t ng = nb >> 2;  // 128-k groups (K is a multiple of 128)
+    const int64_t gb = ng * blockIdx.y / gridDim.y;
+    const int G = (int)(ng * (blockIdx.y + 1) / gridDim.y - gb);  // >= 1: the launch keeps splits <= groups
+
+    // unit index of (row, block g of group gb) for this lane's rows; rows past n read row
+    // n - 1, whose outputs are not stored
+    int64_t wu[NR];
+#pragma unroll
+    for (int j = 0; j < NR; j++) {
+        const int64_t r = n0 + 16 * j + col;
+        wu[j] = (r < n ? r : n - 1) * nb + gb * 4 + g;
+    }
+    // X: this lane loads float4 unit xj of rows xr + 2 i (i < XI) of every group
+    const int xj = lane & 31, xr = 2 * XI * wave + (lane >> 5);
+    const float* xp = x + (int64_t)xr * k + gb * 128 + xj * 4;
+    // LDS word pair of unit xj within its row: Q8_0 keeps the k order (elements 8t .. 8t+7 of a
+    // block feed MFMA t); Q4_0 / Q4_K interleave units 8g + t and 8g + 4 + t (elements 4t..4t+3
+    // and 16+4t..16+4t+3, MFMA t's nibble slots)
+    const int p = Q8 ? xj : (xj & ~7) | ((xj & 3) << 1) | ((xj >> 2) & 1);
+
+    // two slots of one stage = two 128-k groups each (both halves of every 128-byte line of a
+    // weight row; loads of a stage go out back to back)
+    // Scales: per four groups, lane (col, g) loads group g's four scales of its row (one 8-byte
+    // load, 16 bytes of unit pairs for Q4_K) and parks them in the wavefront's LDS table;
+    // a group's MFMAs read their lane's scale back (2-byte loads of 16 rows per instruction
+    // were measured 1-4.5 us slower per call)
+    constexpr int SCW = K4 ? 4 : 2;  // scale words per (row, group)
+    __shared__ __attribute__((aligned(16))) uint32_t scs[SG_WAVES][NR][16][4][SCW];
+    // A stage is two 128-k groups (both halves of every 128-byte line of a weight row).  Its
+    // X, weights and scales are loaded one stage ahead of their use, in the order of use (a
+    // wait for one load is a wait for every load issued before it).  Deeper rings (weights
+    // four stages ahead, X with them) measured slower.
+    constexpr int SG_WR = 2;
+    uint4 wr[SG_WR][2][NR][WV];
+    uint32_t sc[SG_WR][NR][SCW];
+    float4 xv[SG_WR][2][XI];
+    floatx4 acc[NR];
+#pragma unroll
+    for (int j = 0; j < NR; j++) acc[j] = floatx4{0.f, 0.f, 0.f, 0.f};
+
+    // Every load below is unconditional, with clamped indices (no branch between a load and
+    // its use, so the compiler's waits count loads instead of draining all of them): X rows
+    // past m read row m - 1 and feed only output rows that are not stored; groups past the
+    // range read its last group and feed no MFMA.
+    auto load_x = [&](int st, int sl) {
+#pragma unroll
+        for (int c = 0; c < 2; c++) {
+            const int q = min(2 * st + c, G - 1);
+#pragma unroll
+            for (int i = 0; i < XI; i++) {
+                const int r = min(xr + 2 * i, m - 1);
+                xv[sl][c][i] = *reinterpret_cast<const float4*>(xp + (int64_t)(r - xr) * k + 128 * (int64_t)q);
+            }
+        }
+    };
+    auto load_w = [&](int st, int sl) {
+#pragma unroll
+        for (int j = 0; j < NR; j++)
+#pragma unroll
+            for (int c = 0; c < 2; c++) {
+                const int64_t u = wu[j] + 4 * (int64_t)min(2 * st + c, G - 1);
+#pragma unroll
+                for (int v = 0; v < WV; v++) wr[sl][c][j][v] = ld_stream(reinterpret_cast<const uint4*>(qs + u * QB) + v);
+            }
+        if ((st & 1) == 0) {  // scales of groups 2 st .. 2 st + 3: lane g takes group 2 st + g
+#pragma unroll
+            for (int j = 0; j < NR; j++) {
+                const int64_t u0 = wu[j] - g + 4 * (int64_t)min(2 * st + g, G - 1);  // unit of (row, block 0 of that group)
+                if constexpr (K4) {
+                    const uint4 v = *reinterpret_cast<const uint4*>(reinterpret_cast<const uint32_t*>(dsc) + u0);
+                    sc[sl][j][0] = v.x, sc[sl][j][1] = v.y, sc[sl][j][2] = v.z, sc[sl][j][3] = v.w;
+                } else {
+                    const uint2 v = *reinterpret_cast<const uint2*>(reinterpret_cast<const uint16_t*>(dsc) + u0);
+                    sc[sl][j][0] = v.x, sc[sl][j][1] = v.y;
+                }
+            }
+        }
+    };
+    // this wavefront's X rows of stage st (X slot xsl) -> f16 -> LDS tiles 2 xsl, 2 xsl + 1,
+    // and on even stages the scales (weight slot wsl) -> the wavefront's scale table
+    auto stage = [&](int st, int wsl, int xsl) {
+        if ((st & 1) == 0) {
+#pragma unroll
+            for (int j = 0; j < NR; j++)
+#pragma unroll
+                for (int w = 0; w < SCW; w++) scs[wave][j][col][g][w] = sc[wsl][j][w];
+        }
+#pragma unroll
+        for (int c = 0; c < 2; c++) {
+#pragma unroll
+            for (int i = 0; i < XI; i++) {
+                const float4 v = xv[xsl][c][i];
+                const half2v lo = Q8 ? half2v{(_Float16)v.x, (_Float16)v.z} : half2v{(_Float16)v.x, (_Float16)v.y};
+                const half2v hi = Q8 ? half2v{(_Float16)v.y, (_Float16)v.w} : half2v{(_Float16)v.z, (_Float16)v.w};
+                *reinterpret_cast<uint2*>(&xs[2 * (xsl & 1) + c][(xr + 2 * i) * SG_PITCH + 2 * p]) =
+                    uint2{__builtin_bit_cast(uint32_t, lo), __builtin_bit_cast(uint32_t, hi)};
+            }
+        }
+    };
+    auto compute = [&](int st, int wsl, int xsl, bool two) {
+#pragma unroll
+        for (int c = 0; c < 2; c++) {
+            if (c == 1 && !two) break;
+            const int gq = 2 * (st & 1) + c;  // the group's entry in the scale table
+            half8 a[4];
+#pragma unroll
+            for (int t = 0; t < 4; t++) {
+                a[t] = *reinterpret_cast<const half8*>(&xs[2 * (xsl & 1) + c][col * SG_PITCH + 16 * g + 4 * t]);
+                if (MT < 16 && col >= MT) a[t] = half8{};
+            }
+#pragma unroll
+            for (int j = 0; j < NR; j++) {
+                half2v d2, m8d2;
+                if constexpr (K4) {
+                    const half2v u = __builtin_bit_cast(half2v, scs[wave][j][col][gq][g]);
+                    d2 = __builtin_shufflevector(u, u, 0, 0);
+                    m8d2 = __builtin_shufflevector(u, u, 1, 1);
+                } else {
+                    const uint32_t b = reinterpret_cast<const uint16_t*>(&scs[wave][j][col][gq][0])[g];
+                    d2 = __builtin_bit_cast(half2v, b | (b << 16));
+                    m8d2 = d2 * half2v{(_Float16)-8.0f, (_Float16)-8.0f};
+                }
+#pragma unroll
+                for (int t = 0; t < 4; t++) {
+                    half8 bop;
+                    if constexpr (Q8) bop = QWords<QT>::operand(wr[wsl][c][j][t >> 1], t & 1, d2);
+                    else bop = QWords<QT>::operand(wr[wsl][c][j][0], t, d2, m8d2);
+                    acc[j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[t], bop, acc[j], 0, 0, 0);
+                }
+            }
+        }
+    };
+
+    // stage st: its loads in slot st % 2, one stage ahead; staged (X into the LDS tiles of
+    // slot st % 2), then after the barrier (which also frees those tiles' previous stage) read
+    // by every wavefront.  Loads are issued only for stages that exist: clamped loads of
+    // absent stages (no branch between a load and its use, exact waits) measured slower --
+    // a workgroup of one stage then loads it twice.
+    const int S = (G + 1) / 2;
+    auto two = [&](int st) { return 2 * st + 1 < G; };
+    load_x(0, 0);
+    load_w(0, 0);
+    for (int s0 = 0; s0 < S; s0 += 2) {
+        if (s0 + 1 < S) {
+            load_x(s0 + 1, 1);
+            load_w(s0 + 1, 1);
+        }
+        stage(s0, 0, 0);
+        __syncthreads();
+        compute(s0, 0, 0, two(s0));
+        if (s0 + 1 < S) {
+            if (s0 + 2 < S) {
+                load_x(s0 + 2, 0);
+                load_w(s0 + 2, 0);
+            }
+            stage(s0 + 1, 1, 1);
+            __syncthreads();
+            compute(s0 + 1, 1, 1, two(s0 + 1));
+        }
+    }
+
+    // lane (col, g) holds rows 4g .. 4g + 3 of column col of each sub-tile; a split stores
+    // into its slice of the workspace y (m x n floats per split)
+    float* const yb = y + (int64_t)blockIdx.y * m * n;
+#pragma unroll
+    for (int j = 0; j < NR; j++) {
+        const int64_t cn = n0 + 16 * j + col;
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+            const int r = 4 * g + e;
+            if (r < m && cn < n) yb[(int64_t)r * n + cn] = acc[j][e];
+        }
+    }
+}
+
+// y = sum of the nsp partial slices (m n floats each, 16-byte aligned) in slice order, with
+// every slice's load in flight at once (NSP a power of two >= nsp)
+template <int NSP>
+__global__ __launch_bounds__(64) void k_splitk_sum_short(const float* __restrict__ part, float* __restrict__ y,
+                                                         int64_t mn, int nsp) {
+    asm volatile("" : : "s"(part), "s"(y), "s"(mn), "s"(nsp));
+    const int64_t i = ((int64_t)blockIdx.x * 64 + threadIdx.x) * 4;
+    if (i >= mn) return;
+    float4 t[NSP];
+#pragma unroll
+    for (int p = 0; p < NSP; p++)
+        if (p < nsp) t[p] = *reinterpret_cast<const float4*>(part + p * mn + i);
+    float4 v = t[0];
+#pragma unroll
+    for (int p = 1; p < NSP; p++)
+        if (p < nsp) {
+            v.x += t[p].x;
+            v.y += t[p].y;
+            v.z += t[p].z;
+            v.w += t[p].w;
+        }
+    *reinterpret_cast<float4*>(y + i) = v;
+}
+
+// Whether the short-input GEMM takes this product: 1 <= m <= 16, K in steps of 128, and a
+// weight type with an in-register operand builder (Q4_K once its unit scales exist).
+bool gemm_short_ok(const QWeight* w, int64_t m) {
+    return m >= 1 && m <= 16 && w->nb % Q_KR == 0 &&
+           (w->ggml_type == TL_HIP_GGML_Q4_0 || w->ggml_type == TL_HIP_GGML_Q8_0 ||
+            (w->ggml_type == TL_HIP_GGML_Q4_K && w->us));
+}
+
+namespace {
+struct ShortPlan {
+    int nr;
+    int64_t tiles, nsp;
+};
+}  // namespace
+
+// Tile = SG_WAVES x 16 NR rows: NR = 2 (128 rows) for the 4-bit types at N >= 8192 (fewer
+// tiles re-reading X), else 1 (64 rows); K split until about two workgroups per CU run (at
+// most one split per 128-k group, at most 16; the partial slices need m n % 4 == 0 and a
+// 16-byte aligned y).  Measured at M = 16 (us per call, Q4_0 / Q8_0): 4096^2 NR 1 8.8 / 10.2
+// against NR 2 9.7 / 10.6; 11008 x 4096 NR 2 16.2 / 23.5, NR 1 17.3 / 22.8.
+static ShortPlan plan_short(const QWeight* w, int64_t m, const float* y) {
+    const int64_t ng = w->nb / Q_KR;
+    const int cus = state() ? state()->num_cus : 256;
+    const int nr = w->ggml_type != TL_HIP_GGML_Q8_0 && w->n >= 8192 ? 2 : 1;
+    const int64_t tiles = cdiv(w->n, 16 * SG_WAVES * nr);
+    int64_t nsp = 1;
+    const bool split_ok = (m * w->n) % 4 == 0 && (reinterpret_cast<uintptr_t>(y) & 15) == 0;
+    if (split_ok && tiles < 2 * cus) nsp = std::min<int64_t>(std::min<int64_t>(cdiv(2 * cus, tiles), ng), 16);
+    return ShortPlan{nr, tiles, nsp};
+}
+
+// part_ws: workspace of nsp * m * n floats when the plan splits K and noalloc is set (else
+// allocated on s).
+int launch_gemm_short(const QWeight* w, const float* x, float* y, int64_t m, hipStream_t s, float* part_ws,
+                      bool noalloc) {
+    if (!gemm_short_ok(w, m)) {
+        set_error(TL_HIP_ERR_ARG, "ArgumentError: the short-input GEMM takes 1 <= m <= 16, K in steps of 128 and "
+                  "Q4_0 / Q8_0 / Q4_K weights");
+        return TL_HIP_ERR_ARG;
+    }
+    const ShortPlan pl = plan_short(w, m, y);
+    float* part = nullptr;
+    if (pl.nsp > 1) {
+        part = noalloc ? part_ws : static_cast<float*>(dev_alloc_on((size_t)pl.nsp * m * w->n * sizeof(float), s));
+        if (!part) {
+            if (noalloc) set_error(TL_HIP_ERR_ARG, "ArgumentError: no workspace for the split-K partials");
+            return noalloc ? TL_HIP_ERR_ARG : TL_HIP_ERR_ALLOC;
+        }
+    }
+    float* const out = pl.nsp > 1 ? part : y;
+    const dim3 grid((unsigned)pl.tiles, (unsigned)pl.nsp);
+    const void* dsc = w->ggml_type == TL_HIP_GGML_Q4_K ? static_cast<const void*>(w->us) : static_cast<const void*>(w->d);
+    tls_plan[0] = m <= 8 ? 8 : 16;
+    tls_plan[1] = 16 * SG_WAVES * pl.nr;
+    tls_plan[2] = (int)pl.nsp;
+    const int mi = (int)m;
+    auto go = [&](auto qt) {
+        constexpr int QT = decltype(qt)::value;
+        auto run = [&](auto mt) {
+            constexpr int MT = decltype(mt)::value;
+            if (pl.nr == 1) k_qgemm_short<QT, MT, 1><<<grid, 64 * SG_WAVES, 0, s>>>(w->qs, dsc, x, out, mi, w->n, w->k, w->nb);
+            else k_qgemm_short<QT, MT, 2><<<grid, 64 * SG_WAVES, 0, s>>>(w->qs, dsc, x, out, mi, w->n, w->k, w->nb);
+        };
+        if (m <= 8) run(std::integral_constant<int, 8>{});
+        else run(std::integral_constant<int, 16>{});
+    };
+    if (w->ggml_type == TL_HIP_GGML_Q4_0) go(std::integral_constant<int, TL_HIP_GGML_Q4_0>{});
+    else if (w->ggml_type == TL_HIP_GGML_Q8_0) go(std::integral_constant<int, TL_HIP_GGML_Q8_0>{});
+    else go(std::integral_constant<int, TL_HIP_GGML_Q4_K>{});
+    if (pl.nsp > 1) {
+        const int64_t mn = m * w->n;
+        const unsigned sg = (unsigned)cdiv(cdiv(mn, 4), 64);
+        if (pl.nsp <= 4) k_splitk_sum_short<4><<<sg, 64, 0, s>>>(part, y, mn, (int)pl.nsp);
+        else if (pl.nsp <= 8) k_splitk_sum_short<8><<<sg, 64, 0, s>>>(part, y, mn, (int)pl.nsp);
+        else k_splitk_sum_short<16><<<sg, 64, 0, s>>>(part, y, mn, (int)pl.nsp);
+        if (!noalloc) dev_free_on(part, s);  // freed on s: reused at once only by later work on s
+    }
+    hipError_t e = hipGetLastError();
+    return e == hipSuccess ? TL_HIP_OK : hip_fail(e, "short-input gemm launch");
+}
+
+// workspace bytes of a short-input GEMM call (split-K partial slices; 0 when unsplit)
+size_t gemm_short_workspace(const QWeight* w, int64_t m, const float* y) {
+    const ShortPlan pl = plan_short(w, m, y);
+    return pl.nsp > 1 ? (size_t)pl.nsp * m * w->n * sizeof(float) : 0;
+}
+
 // one word per Q4_K unit: f16 d * scale (low half) and f16 -(dmin * min) (high half)
 __global__ __launch_bounds__(256) void k_q4k_unit_scales(const uint8_t* __restrict__ hdr, uint32_t* __restrict__ us,
                                                          int64_t units) {
@@ -602,8 +929,6 @@ __global__ __launch_bounds__(256) void k_splitk_sum(const float* __restrict__ pa
     }
 }
 
-// tile plan of the calling thread's last f16 GEMM launch (tl_hip_debug_last_gemm_plan)
-static thread_local int tls_plan[3] = {0, 0, 0};
 
 namespace {
 // Launch plan of one f16 GEMM: row tile bm, column tile bn (128 x 96 or 128 x 64 wide tiles,
@@ -785,12 +1110,14 @@ int launch_quant_gemm(const QWeight* w, const float* x, float* y, int64_t m, hip
             default: k_qgemm_f32<TL_HIP_GGML_Q6_K><<<grid, 256, 0, s>>>(qv, x, y, m, w->n, w->k, w->nb); break;
         }
     } else {
+        // a Q4_K tensor gets its unit scales on its first f16 GEMM (kept with the tensor)
+        if (int rc = q4k_build_unit_scales(const_cast<QWeight*>(w), s)) return rc;
+        // short inputs: one launch over f32 X (no conversion, no split-K partial sums)
+        if (m <= 16 && gemm_short_ok(w, m)) return launch_gemm_short(w, x, y, m, s, nullptr, false);
         // X -> f16 in the operand k order (a workspace of m * k halves), then the MFMA GEMM
         _Float16* x16 = static_cast<_Float16*>(dev_alloc_on((size_t)m * w->k * sizeof(_Float16), s));
         if (!x16) return TL_HIP_ERR_ALLOC;
-        // a Q4_K tensor gets its unit scales on its first f16 GEMM (kept with the tensor)
-        int rc = q4k_build_unit_scales(const_cast<QWeight*>(w), s);
-        if (rc == TL_HIP_OK) rc = launch_x_to_f16q(x, x16, m, w->k, f16q_order(w->ggml_type), s);
+        int rc = launch_x_to_f16q(x, x16, m, w->k, f16q_order(w->ggml_type), s);
         if (rc == TL_HIP_OK) rc = launch_gemm_f16q(w, x16, y, m, GemmEpi{GEMM_PLAIN, nullptr, nullptr, 0}, s);
         dev_free_on(x16, s);  // freed on s: reused at once only by later work on s
         if (rc) return rc;
@@ -932,7 +1259,14 @@ extern "C" int tl_hip_launch_quant_gemm_noalloc(const tl_hip_qtensor* h, const f
         return TL_HIP_ERR_ARG;
     }
     const GemmEpi plain{GEMM_PLAIN, nullptr, nullptr, 0};
-    if (m > (int64_t)(NOALLOC_SCRATCH_BYTES / 2 / (size_t)w->k)) {
+    // short inputs read X in f32; the scratch holds only their split-K partial slices
+    const bool short_in = m <= 16 && gemm_short_ok(w, m);
+    if (short_in && gemm_short_workspace(w, m, y) > NOALLOC_SCRATCH_BYTES) {
+        set_error(TL_HIP_ERR_ARG, "ArgumentError: the call needs %zu bytes of scratch (split-K partials), the "
+                  "allocation-free GEMM has %zu MiB", gemm_short_workspace(w, m, y), NOALLOC_SCRATCH_BYTES >> 20);
+        return TL_HIP_ERR_ARG;
+    }
+    if (!short_in && m > (int64_t)(NOALLOC_SCRATCH_BYTES / 2 / (size_t)w->k)) {
         set_error(TL_HIP_ERR_ARG, "ArgumentError: %lld x %lld input exceeds the %zu MiB scratch of the allocation-free "
                   "GEMM", (long long)m, (long long)w->k, NOALLOC_SCRATCH_BYTES >> 20);
         return TL_HIP_ERR_ARG;
@@ -940,7 +1274,7 @@ extern "C" int tl_hip_launch_quant_gemm_noalloc(const tl_hip_qtensor* h, const f
     const size_t x16_bytes = ((size_t)m * w->k * 2 + 255) & ~size_t(255);
     const F16qPlan plan = plan_f16q(w, m, plain, y);
     const size_t part_bytes = plan.nsp > 1 ? (size_t)plan.nsp * m * w->n * 4 : 0;
-    if (x16_bytes + part_bytes > NOALLOC_SCRATCH_BYTES) {
+    if (!short_in && x16_bytes + part_bytes > NOALLOC_SCRATCH_BYTES) {
         set_error(TL_HIP_ERR_ARG, "ArgumentError: the call needs %zu bytes of scratch (X in f16 + split-K partials), "
                   "the allocation-free GEMM has %zu MiB", x16_bytes + part_bytes, NOALLOC_SCRATCH_BYTES >> 20);
         return TL_HIP_ERR_ARG;
@@ -965,6 +1299,7 @@ extern "C" int tl_hip_launch_quant_gemm_noalloc(const tl_hip_qtensor* h, const f
     note_stream(s);
     uint8_t* base = scratch_on(st->device);
     if (!base) return tl_hip_last_status();
+    if (short_in) return launch_gemm_short(w, x, y, m, s, reinterpret_cast<float*>(base), true);
     _Float16* x16 = reinterpret_cast<_Float16*>(base);
     int rc = launch_x_to_f16q(x, x16, m, w->k, f16q_order(w->ggml_type), s);
     if (rc == TL_HIP_OK)
