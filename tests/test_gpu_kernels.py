@@ -272,6 +272,39 @@ def test_rope(dev):
     assert_rel(got, ref, F32_TOL)
 
 
+def test_row_ops_kernel_shapes(dev):
+    """The one-wavefront-per-row RMSNorm (widths up to 4096, multiple of 4) and the float4 RoPE
+    (head sizes 4 .. 1024 floats with hd / 4 a power of two) next to their general kernels:
+    widths 100, 2048, 4096 and 8192 with and without a weight or a residual; RoPE head sizes 4,
+    64 and 96 (general kernel), tl_cpu's fixed row and per-token rows from pos0 = 5, and a table
+    shorter than the positions (identity past its end, as tl_cpu's row bounds give)."""
+    rng = np.random.default_rng(0x71510003)
+    for rows, n in ((7, 100), (33, 2048), (5, 4096), (3, 8192)):
+        x = rng.standard_normal((rows, n)).astype(np.float32)
+        w = rng.uniform(0.5, 1.5, n).astype(np.float32)
+        r = rng.standard_normal((rows, n)).astype(np.float32)
+        xt, wt, rt = dev.tensor_new(x), dev.tensor_new(w), dev.tensor_new(r)
+        assert_rel(dev.tensor_rms_norm(xt, wt, 1e-5).to_numpy(), oracle.rms_norm(x, w, 1e-5), F32_TOL)
+        assert_rel(dev.tensor_rms_norm(xt, None, 1e-5).to_numpy(), oracle.rms_norm(x, None, 1e-5), F32_TOL)
+        assert_rel(dev.fused_add_rms_norm(xt, rt, wt, 1e-5).to_numpy(), oracle.fused_add_rms_norm(x, r, w, 1e-5),
+                   F32_TOL)
+    for tokens, heads, hd in ((9, 4, 64), (6, 3, 96), (11, 8, 4), (4, 2, 1024)):
+        x = rng.standard_normal((tokens, heads, hd)).astype(np.float32)
+        cos_d, sin_d = dev.tensor_rope_new_cos(hd, 12, 10000.0), dev.tensor_rope_new_sin(hd, 12, 10000.0)
+        cos_h, sin_h = oracle.rope_table(12, hd, 10000.0), oracle.rope_table(12, hd, 10000.0, sin=True)
+        xt = dev.tensor_new(x)
+        got = dev.tensor_apply_rope(xt, dev.tensor_narrow(cos_d, 0, 3, 2), dev.tensor_narrow(sin_d, 0, 3, 2))
+        assert_rel(got.to_numpy(), oracle.apply_rope(x, cos_h[3:5], sin_h[3:5]), F32_TOL)
+        got = dev.tensor_apply_rope_pos(xt, cos_d, sin_d, 5, heads).to_numpy()
+        for t in range(tokens):
+            p = 5 + t
+            if p < 12:
+                want = oracle.apply_rope(x[t], cos_h[p:p + 1], sin_h[p:p + 1])
+            else:  # past the table: cos 1, sin 0
+                want = x[t]
+            assert_rel(got[t], want, F32_TOL)
+
+
 def test_swiglu(dev):
     rng = np.random.default_rng(0x71510001)
     g = rng.standard_normal((512, 11008)).astype(np.float32)
