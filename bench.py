@@ -511,6 +511,17 @@ def bench_decode(dev, cfg, ggml_type, args, steps=None, variants=()):
     return tok_s, decode_s, prefill_s, short_s, rows
 
 
+def copy_reference(dev, nbytes=64 << 20):
+    """Reference dispatch for the FETCH_SIZE / WRITE_SIZE scale of counter runs: one device
+    copy of a known size."""
+    import ctypes as C
+    src, dst = dev.lib.tl_hip_malloc(nbytes), dev.lib.tl_hip_malloc(nbytes)
+    dev.lib.tl_hip_memcpy_d2d(C.c_void_p(dst), C.c_void_p(src), nbytes)
+    dev.synchronize()
+    dev.lib.tl_hip_free(C.c_void_p(src))
+    dev.lib.tl_hip_free(C.c_void_p(dst))
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -532,6 +543,8 @@ def main():
                     help="only the 4096x4096 matvec and its one-launch read floor (same shape and copies)")
     ap.add_argument("--matvec-only", action="store_true",
                     help="only the 4096x4096 matvec timing plus a 64 MiB device copy (counter runs)")
+    ap.add_argument("--row-ops-only", action="store_true",
+                    help="only the configs[1] row-op leg plus a 64 MiB device copy (counter runs)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU: this build has no multi-GPU path (every box has one GPU); "
@@ -564,6 +577,11 @@ def main():
     if args.attention_only:
         print(json.dumps({"decode_attention": bench_attention(dev)}), flush=True)
         return
+    if args.row_ops_only:
+        rows = bench_row_ops(dev)
+        copy_reference(dev)
+        print(json.dumps({"row_ops": rows, "copy_bytes": 64 << 20}), flush=True)
+        return
     if args.kquant_only:
         print(json.dumps({"quant_matvec": bench_quant_matvec(dev)}), flush=True)
         tok_s, decode_s, prefill_s, _, _ = bench_decode(dev, cfg, "Q4_K_M", args, steps=64)
@@ -582,16 +600,9 @@ def main():
         print(json.dumps({"matvec_avg_us": round(avg_s * 1e6, 3), "floor_us": round(floor_s * 1e6, 3)}), flush=True)
         return
     if args.matvec_only:
-        # reference dispatch for the FETCH_SIZE / WRITE_SIZE scale: a device copy of 64 MiB
-        import ctypes as C
-        nbytes = 64 << 20
-        src, dst = dev.lib.tl_hip_malloc(nbytes), dev.lib.tl_hip_malloc(nbytes)
-        dev.lib.tl_hip_memcpy_d2d(C.c_void_p(dst), C.c_void_p(src), nbytes)
-        dev.synchronize()
-        dev.lib.tl_hip_free(C.c_void_p(src))
-        dev.lib.tl_hip_free(C.c_void_p(dst))
+        copy_reference(dev)
         print(json.dumps({"matvec_avg_us": round(avg_s * 1e6, 3), "matvec_gbs": round(achieved, 1),
-                          "copy_bytes": nbytes}), flush=True)
+                          "copy_bytes": 64 << 20}), flush=True)
         return
 
     gemm = attn = qmv = qmv2 = rowops = None

@@ -42,7 +42,7 @@ def expected_plan(t, m, n, k, cus=256):
     tiles = -(-n // (64 * nr))
     nsp = 1
     if (m * n) % 4 == 0 and tiles < 2 * cus:
-        nsp = min(-(-2 * cus // tiles), ng, 16)
+        nsp = min(-(-2 * cus // tiles), (ng + 1) // 2, 16)
     return (8 if m <= 8 else 16, 64 * nr, nsp)
 
 

@@ -573,8 +573,16 @@ template <int QT, int MT, int NR>
 __global__ __launch_bounds__(64 * SG_WAVES) void k_qgemm_short(const uint8_t* __restrict__ qs,
                                                                const void* __restrict__ dsc,
                                                                const float* __restrict__ x, float* __restrict__ y,
-                                                               int m, int64_t n, int64_t k, int64_t nb) {
-    asm volatile("" : : "s"(qs), "s"(dsc), "s"(x), "s"(y), "s"(m), "s"(n), "s"(k), "s"(nb));
+                                                               int m, int64_t n, int64_t k, int64_t nb, int tiles,
+                                                               int nsp) {
+    asm volatile("" : : "s"(qs), "s"(dsc), "s"(x), "s"(y), "s"(m), "s"(n), "s"(k), "s"(nb), "s"(tiles), "s"(nsp));
+    // (tile, split) from the 1-D grid so that every split of a tile runs on the XCD of its
+    // tile (workgroups go to the 8 XCDs round-robin by linear id): a weight row's scale lines
+    // and X then stay in one XCD's L2 (with splits spread over XCDs, 11008 x 4096 Q4_0 read
+    // 1.30x its algorithmic bytes from HBM)
+    const int wg = blockIdx.x, xcd = wg & 7, rest = wg >> 3;
+    const int split = rest % nsp, tile = (rest / nsp) * 8 + xcd;
+    if (tile >= tiles) return;  // padding of the grid to whole groups of 8 tiles (uniform)
     constexpr bool Q8 = QT == TL_HIP_GGML_Q8_0, K4 = QT == TL_HIP_GGML_Q4_K;
     constexpr int QB = Q8 ? 32 : 16, WV = QB / 16;
     constexpr int XI = MT / (2 * SG_WAVES);  // X load instructions per wavefront and group (two rows each)
@@ -582,10 +590,14 @@ __global__ __launch_bounds__(64 * SG_WAVES) void k_qgemm_short(const uint8_t* __
     __shared__ __attribute__((aligned(16))) uint32_t xs[4][16 * SG_PITCH];
     const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int col = lane & 15, g = lane >> 4;
-    const int64_t n0 = ((int64_t)blockIdx.x * SG_WAVES + wave) * 16 * NR;
+    const int64_t n0 = ((int64_t)tile * SG_WAVES + wave) * 16 * NR;
     const int64_t ng = nb >> 2;  // 128-k groups (K is a multiple of 128)
-    const int64_t gb = ng * blockIdx.y / gridDim.y;
-    const int G = (int)(ng * (blockIdx.y + 1) / gridDim.y - gb);  // >= 1: the launch keeps splits <= groups
+    // K splits in whole two-group stages, so that no 128-byte line of a weight row is read by
+    // two workgroups (split boundaries at odd groups measured 1.43x the algorithmic HBM bytes)
+    const int64_t nst = (ng + 1) >> 1;
+    const int64_t gb = 2 * (nst * split / nsp);
+    const int64_t ge = min(2 * (nst * (split + 1) / nsp), ng);
+    const int G = (int)(ge - gb);  // >= 1: the launch keeps splits <= stages
 
     // unit index of (row, block g of group gb) for this lane's rows; rows past n read row
     // n - 1, whose outputs are not stored
@@ -746,7 +758,7 @@ __global__ __launch_bounds__(64 * SG_WAVES) void k_qgemm_short(const uint8_t* __
 
     // lane (col, g) holds rows 4g .. 4g + 3 of column col of each sub-tile; a split stores
     // into its slice of the workspace y (m x n floats per split)
-    float* const yb = y + (int64_t)blockIdx.y * m * n;
+    float* const yb = y + (int64_t)split * m * n;
 #pragma unroll
     for (int j = 0; j < NR; j++) {
         const int64_t cn = n0 + 16 * j + col;
@@ -799,7 +811,7 @@ struct ShortPlan {
 
 // Tile = SG_WAVES x 16 NR rows: NR = 2 (128 rows) for the 4-bit types at N >= 8192 (fewer
 // tiles re-reading X), else 1 (64 rows); K split until about two workgroups per CU run (at
-// most one split per 128-k group, at most 16; the partial slices need m n % 4 == 0 and a
+// most one split per two-group stage, at most 16; the partial slices need m n % 4 == 0 and a
 // 16-byte aligned y).  Measured at M = 16 (us per call, Q4_0 / Q8_0): 4096^2 NR 1 8.8 / 10.2
 // against NR 2 9.7 / 10.6; 11008 x 4096 NR 2 16.2 / 23.5, NR 1 17.3 / 22.8.
 static ShortPlan plan_short(const QWeight* w, int64_t m, const float* y) {
@@ -809,7 +821,8 @@ static ShortPlan plan_short(const QWeight* w, int64_t m, const float* y) {
     const int64_t tiles = cdiv(w->n, 16 * SG_WAVES * nr);
     int64_t nsp = 1;
     const bool split_ok = (m * w->n) % 4 == 0 && (reinterpret_cast<uintptr_t>(y) & 15) == 0;
-    if (split_ok && tiles < 2 * cus) nsp = std::min<int64_t>(std::min<int64_t>(cdiv(2 * cus, tiles), ng), 16);
+    if (split_ok && tiles < 2 * cus)
+        nsp = std::min<int64_t>(std::min<int64_t>(cdiv(2 * cus, tiles), (ng + 1) / 2), 16);
     return ShortPlan{nr, tiles, nsp};
 }
 
@@ -832,7 +845,8 @@ int launch_gemm_short(const QWeight* w, const float* x, float* y, int64_t m, hip
         }
     }
     float* const out = pl.nsp > 1 ? part : y;
-    const dim3 grid((unsigned)pl.tiles, (unsigned)pl.nsp);
+    const unsigned grid = (unsigned)(cdiv(pl.tiles, 8) * 8 * pl.nsp);
+    const int ti = (int)pl.tiles, ns = (int)pl.nsp;
     const void* dsc = w->ggml_type == TL_HIP_GGML_Q4_K ? static_cast<const void*>(w->us) : static_cast<const void*>(w->d);
     tls_plan[0] = m <= 8 ? 8 : 16;
     tls_plan[1] = 16 * SG_WAVES * pl.nr;
@@ -842,8 +856,10 @@ int launch_gemm_short(const QWeight* w, const float* x, float* y, int64_t m, hip
         constexpr int QT = decltype(qt)::value;
         auto run = [&](auto mt) {
             constexpr int MT = decltype(mt)::value;
-            if (pl.nr == 1) k_qgemm_short<QT, MT, 1><<<grid, 64 * SG_WAVES, 0, s>>>(w->qs, dsc, x, out, mi, w->n, w->k, w->nb);
-            else k_qgemm_short<QT, MT, 2><<<grid, 64 * SG_WAVES, 0, s>>>(w->qs, dsc, x, out, mi, w->n, w->k, w->nb);
+            if (pl.nr == 1)
+                k_qgemm_short<QT, MT, 1><<<grid, 64 * SG_WAVES, 0, s>>>(w->qs, dsc, x, out, mi, w->n, w->k, w->nb, ti, ns);
+            else
+                k_qgemm_short<QT, MT, 2><<<grid, 64 * SG_WAVES, 0, s>>>(w->qs, dsc, x, out, mi, w->n, w->k, w->nb, ti, ns);
         };
         if (m <= 8) run(std::integral_constant<int, 8>{});
         else run(std::integral_constant<int, 16>{});
