@@ -367,6 +367,40 @@ def test_attention_grouped_split_lengths(dev, d, hq, hkv, lmax, L, B):
         assert_rel(got[b], ref, F32_TOL)
 
 
+@pytest.mark.parametrize("d,hq,hkv,lmax,L,B", [(128, 32, 8, 512, 512, 1), (128, 32, 8, 512, 512, 8),
+                                               (128, 32, 8, 300, 65, 2), (64, 64, 8, 500, 449, 2),
+                                               (128, 32, 4, 256, 200, 3), (128, 32, 8, 2048, 2048, 1),
+                                               (64, 64, 8, 4096, 4001, 1)])
+def test_attention_one_launch_and_two_launch(dev, d, hq, hkv, lmax, L, B):
+    """The grouped split form with its records merged by the last-arriving workgroup of each
+    (batch item, KV head) -- one launch, taken for up to 8 splits: the first five cases, with
+    lengths ending inside a split -- and with the separate merge kernel: both within the f32
+    tolerance of the oracle, and the one-launch form bitwise equal over repeated calls (its
+    arrival counters return to zero after every call).  The last two cases have more splits
+    and take the merge kernel either way."""
+    rng = np.random.default_rng(0x715B0000 + L + d + B + hkv)
+    q = rng.standard_normal((B, hq, d)).astype(np.float32)
+    k = rng.standard_normal((B, hkv, lmax, d)).astype(np.float16)
+    v = rng.standard_normal((B, hkv, lmax, d)).astype(np.float16)
+    qt, kt, vt = dev.tensor_new(q), dev.tensor_new_f16(k), dev.tensor_new_f16(v)
+    scale = 1.0 / np.sqrt(d)
+    lib = dev.lib
+    prev = lib.tl_hip_debug_attention_one_launch(1)
+    try:
+        one = [dev.attention_decode(qt, kt, vt, L, scale).to_numpy() for _ in range(3)]
+        lib.tl_hip_debug_attention_one_launch(0)
+        two = dev.attention_decode(qt, kt, vt, L, scale).to_numpy()
+    finally:
+        lib.tl_hip_debug_attention_one_launch(prev)
+    for r in one[1:]:
+        assert np.array_equal(r.view(np.uint32), one[0].view(np.uint32))
+    for b in sorted({0, B - 1}):
+        ref = oracle.attention(q[b][None], k[b, :, :L].astype(np.float32), v[b, :, :L].astype(np.float32),
+                               np.float32(scale), False).reshape(hq, d)
+        assert_rel(one[0][b], ref, F32_TOL)
+        assert_rel(two[b], ref, F32_TOL)
+
+
 @pytest.mark.parametrize("d,hq,hkv,lmax,pos0,n", [(64, 32, 4, 600, 0, 512), (64, 16, 2, 300, 0, 37),
                                                   (128, 32, 8, 1100, 0, 1031), (128, 16, 4, 700, 333, 250),
                                                   (64, 8, 1, 200, 45, 1), (128, 16, 2, 256, 100, 100)])

@@ -56,6 +56,14 @@ struct KVLoad<float> {
 
 constexpr int ATT_MAX_CHUNK = 1024;
 constexpr int ATT_MAX_SPLITS = 256;
+// One-launch grouped split form: arrival counters per (batch item, KV head), zero at load and
+// returned to zero by the workgroup that arrives last, which merges the item's split records
+// (at most ATT_FUSE_MAX: one workgroup reading more records costs more than a merge launch).
+constexpr int ATT_ARRIVE_MAX = 4096;
+constexpr int ATT_FUSE_MAX = 8;
+__device__ uint32_t g_attn_arrive[ATT_ARRIVE_MAX];
+static std::atomic<bool> g_attn_fuse{true};
+static bool attn_fuse_enabled() { return g_attn_fuse.load(std::memory_order_relaxed); }
 constexpr int ATT_PF = 2;  // 32-position steps whose K/V rows are requested up front
 
 // Cached length of batch item b: (len_dev ? *len_dev + len_add : L) + b * len_step.
@@ -361,7 +369,27 @@ __device__ __forceinline__ void tr_halve(float (&v)[N], int lane) {
     if constexpr (OFF > LO) tr_halve<OFF / 2, LO, H / 2, N, HIGH>(v, lane);
 }
 
-template <int D, int G, int PW>  // PW positions per wavefront, 4 PW per workgroup (split)
+// Split records of the one-launch form are written and read as agent-scope atomics (stores
+// that write through to the agent's point of coherence, loads that do not hit a stale line
+// of another XCD's L2), so neither side needs a whole-L2 write-back or invalidate.
+template <bool FUSE>
+__device__ __forceinline__ void rec_store(float* p, float v) {
+    if constexpr (FUSE) __hip_atomic_store(reinterpret_cast<uint32_t*>(p), __float_as_uint(v), __ATOMIC_RELAXED,
+                                           __HIP_MEMORY_SCOPE_AGENT);
+    else *p = v;
+}
+template <bool FUSE>
+__device__ __forceinline__ float rec_load(const float* p) {
+    if constexpr (FUSE)
+        return __uint_as_float(__hip_atomic_load(reinterpret_cast<const uint32_t*>(p), __ATOMIC_RELAXED,
+                                                 __HIP_MEMORY_SCOPE_AGENT));
+    else return *p;
+}
+
+// PW positions per wavefront, 4 PW per workgroup (split).  FUSE false: the split records are
+// merged by k_attn_merge_gq; true: the workgroup that completes the last split of a (batch
+// item, KV head) merges them in the same launch.
+template <int D, int G, int PW, bool FUSE>
 __global__ __launch_bounds__(256) void k_attn_gq(AttnArgs a) {
     attn_args_prefetch(a);
     constexpr int GQ_PW = PW, GQ_CH = 4 * PW;
@@ -492,11 +520,63 @@ __global__ __launch_bounds__(256) void k_attn_gq(AttnArgs a) {
     float* wr = a.ws + (((int64_t)b * a.hkv + h) * a.nsplit + split) * G * (D + 2);
     for (int idx = tid; idx < G * D; idx += 256) {
         const int g = idx / D, d = idx % D;
-        wr[g * (D + 2) + d] = (part[0][g][d] + part[1][g][d]) + (part[2][g][d] + part[3][g][d]);
+        rec_store<FUSE>(wr + g * (D + 2) + d, (part[0][g][d] + part[1][g][d]) + (part[2][g][d] + part[3][g][d]));
     }
     if (tid < G) {
-        wr[tid * (D + 2) + D] = stat[tid][0];
-        wr[tid * (D + 2) + D + 1] = stat[tid][1];
+        rec_store<FUSE>(wr + tid * (D + 2) + D, stat[tid][0]);
+        rec_store<FUSE>(wr + tid * (D + 2) + D + 1, stat[tid][1]);
+    }
+    if constexpr (FUSE) {
+        // Arrival.  Every wave waits until its record stores have completed (reached the
+        // agent's point of coherence) before the barrier, so the counter is bumped only once
+        // the whole record is visible to every XCD: the release order of an agent-scope
+        // fence without its L2 write-back, which only plain stores need.  The last arriver
+        // reads the records with agent-scope loads issued after its bump has returned.
+        __shared__ int s_last;
+        __shared__ float wts[ATT_FUSE_MAX][G], lsum[ATT_FUSE_MAX][G], rden[G];
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        __syncthreads();
+        // splits holding positions; the grid has a.nsplit <= ATT_FUSE_MAX of them
+        const int nact = (int)min((L + GQ_CH - 1) / GQ_CH, (int64_t)a.nsplit);
+        if (tid == 0) {
+            uint32_t* c = g_attn_arrive + ((int64_t)b * a.hkv + h);
+            const uint32_t old = __hip_atomic_fetch_add(c, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            const int last = old == (uint32_t)(nact - 1);
+            if (last) __hip_atomic_store(c, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            s_last = last;
+        }
+        __syncthreads();
+        if (!s_last) return;  // uniform per workgroup
+        // Merge of the nact records of every head of the group: out = sum_s o_s w_s / sum_s l_s w_s,
+        // w_s = e^(m_s - max m).
+        const float* rb = a.ws + (((int64_t)b * a.hkv + h) * a.nsplit) * G * (D + 2);
+        for (int i = tid; i < nact * G; i += 256) {
+            const int sp = i / G, g = i % G;
+            wts[sp][g] = rec_load<FUSE>(rb + ((int64_t)sp * G + g) * (D + 2) + D);
+            lsum[sp][g] = rec_load<FUSE>(rb + ((int64_t)sp * G + g) * (D + 2) + D + 1);
+        }
+        __syncthreads();
+        if (tid < G) {
+            float M = -INFINITY;
+            for (int sp = 0; sp < nact; sp++) M = fmaxf(M, wts[sp][tid]);
+            float den = 0.f;
+            for (int sp = 0; sp < nact; sp++) {
+                const float e = expf(wts[sp][tid] - M);  // every split holds a valid position
+                wts[sp][tid] = e;
+                den = fmaf(lsum[sp][tid], e, den);
+            }
+            rden[tid] = 1.0f / den;
+        }
+        __syncthreads();
+        const int hq = a.hkv * G;
+        for (int idx = tid; idx < G * D; idx += 256) {
+            const int g = idx / D, d = idx % D;
+            const float* ro = rb + g * (D + 2) + d;
+            float acc = 0.f;
+#pragma unroll 8
+            for (int sp = 0; sp < nact; sp++) acc = fmaf(rec_load<FUSE>(ro + (int64_t)sp * G * (D + 2)), wts[sp][g], acc);
+            a.out[((int64_t)b * hq + h * G + g) * D + d] = acc * rden[g];
+        }
     }
 }
 
@@ -1133,13 +1213,22 @@ int launch_attention_gq(const float* q, const void* k, const void* v, float* out
     AttnArgs a{q, k, v, out, ws, hkv, lmax, kv_bstride, AttnLen{L, len_dev, len_add, len_step}, 4 * pw, nsplit,
                scale};
     dim3 grid(nsplit, hkv, B);
-#define TLH_GQ(DD, GG)                                                                   \
-    if (D == DD && G == GG) {                                                            \
-        if (pw == 32) k_attn_gq<DD, GG, 32><<<grid, 256, 0, s>>>(a);                     \
-        else k_attn_gq<DD, GG, 16><<<grid, 256, 0, s>>>(a);                              \
-        if (nsplit > 1) k_attn_merge_gq<DD, GG><<<dim3(hkv, B, GG), 256, 0, s>>>(a);     \
-        hipError_t e = hipGetLastError();                                                \
-        return e == hipSuccess ? TL_HIP_OK : hip_fail(e, "attention launch");            \
+    // one launch (the last-arriving split merges) when the records fit one workgroup's merge and
+    // no other stream can run a call that shares the arrival counters
+    const bool fuse = nsplit > 1 && nsplit <= ATT_FUSE_MAX && (int64_t)B * hkv <= ATT_ARRIVE_MAX &&
+                      single_stream() && attn_fuse_enabled();
+#define TLH_GQ(DD, GG)                                                                              \
+    if (D == DD && G == GG) {                                                                       \
+        if (fuse) {                                                                                 \
+            if (pw == 32) k_attn_gq<DD, GG, 32, true><<<grid, 256, 0, s>>>(a);                      \
+            else k_attn_gq<DD, GG, 16, true><<<grid, 256, 0, s>>>(a);                               \
+        } else {                                                                                    \
+            if (pw == 32) k_attn_gq<DD, GG, 32, false><<<grid, 256, 0, s>>>(a);                     \
+            else k_attn_gq<DD, GG, 16, false><<<grid, 256, 0, s>>>(a);                              \
+            if (nsplit > 1) k_attn_merge_gq<DD, GG><<<dim3(hkv, B, GG), 256, 0, s>>>(a);            \
+        }                                                                                           \
+        hipError_t e = hipGetLastError();                                                           \
+        return e == hipSuccess ? TL_HIP_OK : hip_fail(e, "attention launch");                       \
     }
     TLH_GQ(64, 4) TLH_GQ(64, 8) TLH_GQ(128, 4) TLH_GQ(128, 8)
 #undef TLH_GQ
@@ -1178,6 +1267,8 @@ int launch_attention(const float* q, const void* k, const void* v, int kv_dtype,
 }  // namespace tlhip
 
 using namespace tlhip;
+
+extern "C" int tl_hip_debug_attention_one_launch(int on) { return g_attn_fuse.exchange(on != 0) ? 1 : 0; }
 
 extern "C" tl_hip_tensor* tl_hip_attention_decode(const tl_hip_tensor* qh, const tl_hip_tensor* kh,
                                                   const tl_hip_tensor* vh, int64_t L, float scale) {

@@ -71,6 +71,7 @@ void dev_free_on(void* p, hipStream_t s);
 void note_stream(hipStream_t s);
 // True when note_stream(s) would synchronise the library stream (the first caller stream).
 bool note_stream_syncs(hipStream_t s);
+bool single_stream();  // no stream but the library's has run library work (calls cannot overlap)
 // Looks up the device address of the allocation-free GEMM's scratch array on `device` (the
 // current device during library initialisation); status code.
 int noalloc_scratch_init(int device);

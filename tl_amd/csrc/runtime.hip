@@ -107,6 +107,8 @@ bool note_stream_syncs(hipStream_t s) {
     return s && !g_multi.load(std::memory_order_acquire) && state() && s != g_state.stream;
 }
 
+bool single_stream() { return !g_multi.load(std::memory_order_acquire); }
+
 void note_stream(hipStream_t s) {
     if (!s || g_multi.load(std::memory_order_acquire) || !state() || s == g_state.stream) return;
     std::lock_guard<std::mutex> lk(g_alloc_mu);
