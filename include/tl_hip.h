@@ -300,11 +300,12 @@ tl_hip_tensor* tl_hip_tensor_scaled_dot_product_attention(const tl_hip_tensor* q
  *   out [B, Hq, D] f32;  query head h reads KV head h / (Hq / Hkv). */
 tl_hip_tensor* tl_hip_attention_decode(const tl_hip_tensor* q, const tl_hip_tensor* k,
                                        const tl_hip_tensor* v, int64_t L, float scale);
-/* Whether the grouped split form may merge its split records inside the same launch (the
- * workgroup finishing a (batch item, KV head) last merges them; default 1) instead of in a
- * second kernel.  Returns the previous setting.  Instrumentation for the parity tests, which
- * run both forms; no reference counterpart. */
-int tl_hip_debug_attention_one_launch(int on);
+/* Whether split kernels may merge their partial results inside the same launch, the
+ * workgroup that finishes a unit last merging it (default 1): decode attention's split records
+ * per (batch item, KV head), the short-input GEMM's K-split slices per tile.  0 selects the
+ * second merge kernel.  Returns the previous setting.  Instrumentation for the parity tests,
+ * which run both forms; no reference counterpart. */
+int tl_hip_debug_one_launch_merge(int on);
 /* Causal prefill attention over an f16 KV cache: the same chatbot chain for sl > 1 with the
  * causal mask (Tensor::new_causal_mask + add_4d, chatbot.tl:76-87), in one f16-MFMA kernel.
  *   q [n, Hq, D] f32 holds the queries of positions pos0 .. pos0 + n - 1;

@@ -277,7 +277,7 @@ extern "C" {
         L: i64,
         scale: f32,
     ) -> *mut tl_hip_tensor;
-    pub fn tl_hip_debug_attention_one_launch(on: i32) -> i32;
+    pub fn tl_hip_debug_one_launch_merge(on: i32) -> i32;
     pub fn tl_hip_attention_prefill(
         q: *const tl_hip_tensor,
         k: *const tl_hip_tensor,

@@ -385,13 +385,13 @@ def test_attention_one_launch_and_two_launch(dev, d, hq, hkv, lmax, L, B):
     qt, kt, vt = dev.tensor_new(q), dev.tensor_new_f16(k), dev.tensor_new_f16(v)
     scale = 1.0 / np.sqrt(d)
     lib = dev.lib
-    prev = lib.tl_hip_debug_attention_one_launch(1)
+    prev = lib.tl_hip_debug_one_launch_merge(1)
     try:
         one = [dev.attention_decode(qt, kt, vt, L, scale).to_numpy() for _ in range(3)]
-        lib.tl_hip_debug_attention_one_launch(0)
+        lib.tl_hip_debug_one_launch_merge(0)
         two = dev.attention_decode(qt, kt, vt, L, scale).to_numpy()
     finally:
-        lib.tl_hip_debug_attention_one_launch(prev)
+        lib.tl_hip_debug_one_launch_merge(prev)
     for r in one[1:]:
         assert np.array_equal(r.view(np.uint32), one[0].view(np.uint32))
     for b in sorted({0, B - 1}):

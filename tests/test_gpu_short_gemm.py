@@ -4,7 +4,8 @@ launcher).  Tolerance: the f16-path bound 1e-2 (max-rel-err as in test_gpu_kerne
 
 Covers the configs[2] shapes at M = 5, 8, 9 and 16 for Q4_0 and Q8_0, Q4_K (its per-unit
 scale pairs), the launch plan (an M tile of 8 or 16, 16-row sub-tiles per tile, K splits),
-run-to-run bit equality, and shapes whose K leaves some wavefronts of a workgroup no 128-k
+run-to-run bit equality and bit equality of the one-launch slice sum (the tile's last split
+adds the slices) with the two-launch one, and shapes whose K leaves some wavefronts of a workgroup no 128-k
 group (K = 128 .. 896) or whose N is not a multiple of 16."""
 import ctypes as C
 
@@ -61,9 +62,17 @@ def test_short_gemm_configs2(dev, t, nk, m):
     ref = oracle.qtensor_matmul(x, raw, t, n)
     err = max_rel(y, ref)
     assert err <= F16_TOL, f"max-rel-err {err:.3e}"
-    # the same call again: bitwise equal (the wavefronts' partial tiles are added in K order)
+    # the same call again: bitwise equal (the K-split slices are added in slice order) -- and
+    # so is the form that adds them in a second kernel instead of the tile's last-arriving split
     y2 = dev.tl_qtensor_matmul_f16(xt, q).to_numpy()
     assert np.array_equal(y.view(np.uint32), y2.view(np.uint32))
+    lib = _lib.load()
+    prev = lib.tl_hip_debug_one_launch_merge(0)
+    try:
+        y3 = dev.tl_qtensor_matmul_f16(xt, q).to_numpy()
+    finally:
+        lib.tl_hip_debug_one_launch_merge(prev)
+    assert np.array_equal(y.view(np.uint32), y3.view(np.uint32))
 
 
 @pytest.mark.parametrize("nk", [(4096, 4096), (2560, 2048), (32000, 2048)])

@@ -62,8 +62,7 @@ constexpr int ATT_MAX_SPLITS = 256;
 constexpr int ATT_ARRIVE_MAX = 4096;
 constexpr int ATT_FUSE_MAX = 8;
 __device__ uint32_t g_attn_arrive[ATT_ARRIVE_MAX];
-static std::atomic<bool> g_attn_fuse{true};
-static bool attn_fuse_enabled() { return g_attn_fuse.load(std::memory_order_relaxed); }
+
 constexpr int ATT_PF = 2;  // 32-position steps whose K/V rows are requested up front
 
 // Cached length of batch item b: (len_dev ? *len_dev + len_add : L) + b * len_step.
@@ -1216,7 +1215,7 @@ int launch_attention_gq(const float* q, const void* k, const void* v, float* out
     // one launch (the last-arriving split merges) when the records fit one workgroup's merge and
     // no other stream can run a call that shares the arrival counters
     const bool fuse = nsplit > 1 && nsplit <= ATT_FUSE_MAX && (int64_t)B * hkv <= ATT_ARRIVE_MAX &&
-                      single_stream() && attn_fuse_enabled();
+                      single_stream() && one_launch_merge();
 #define TLH_GQ(DD, GG)                                                                              \
     if (D == DD && G == GG) {                                                                       \
         if (fuse) {                                                                                 \
@@ -1267,8 +1266,6 @@ int launch_attention(const float* q, const void* k, const void* v, int kv_dtype,
 }  // namespace tlhip
 
 using namespace tlhip;
-
-extern "C" int tl_hip_debug_attention_one_launch(int on) { return g_attn_fuse.exchange(on != 0) ? 1 : 0; }
 
 extern "C" tl_hip_tensor* tl_hip_attention_decode(const tl_hip_tensor* qh, const tl_hip_tensor* kh,
                                                   const tl_hip_tensor* vh, int64_t L, float scale) {

@@ -568,13 +568,25 @@ __global__ void k_splitk_sum(const float* __restrict__ part, float* y, const flo
 
 constexpr int SG_WAVES = 4;   // wavefronts per workgroup (they split the tile's rows)
 constexpr int SG_PITCH = 68;  // LDS words per X row of one 128-k group (64 + 4)
+// One-launch split form: an arrival counter per tile, zero at load and returned to zero by
+// the tile's last-arriving split, which adds the slices (at most SG_FUSE_NSP of them; the
+// launch splits only below 512 tiles).
+constexpr int SG_ARRIVE_MAX = 512;
+constexpr int SG_FUSE_NSP = 8;
+__device__ uint32_t g_short_arrive[SG_ARRIVE_MAX];
 
-template <int QT, int MT, int NR>
+// FUSE: with K split, the split that finishes a tile last adds its slices (y = the final
+// output, part = the slices; n % 4 == 0) instead of k_splitk_sum_short in a second launch.
+// Slices are then written as agent-scope atomics (stores that write through to the agent's
+// point of coherence) and read with the same cache policy (sc1: no stale line of another
+// XCD's L2), and every wavefront waits for its slice stores to complete before the arrival
+// count is bumped.
+template <int QT, int MT, int NR, bool FUSE>
 __global__ __launch_bounds__(64 * SG_WAVES) void k_qgemm_short(const uint8_t* __restrict__ qs,
                                                                const void* __restrict__ dsc,
                                                                const float* __restrict__ x, float* __restrict__ y,
                                                                int m, int64_t n, int64_t k, int64_t nb, int tiles,
-                                                               int nsp) {
+                                                               int nsp, float* __restrict__ part) {
     asm volatile("" : : "s"(qs), "s"(dsc), "s"(x), "s"(y), "s"(m), "s"(n), "s"(k), "s"(nb), "s"(tiles), "s"(nsp));
     // (tile, split) from the 1-D grid so that every split of a tile runs on the XCD of its
     // tile (workgroups go to the 8 XCDs round-robin by linear id): a weight row's scale lines
@@ -757,15 +769,73 @@ __global__ __launch_bounds__(64 * SG_WAVES) void k_qgemm_short(const uint8_t* __
     }
 
     // lane (col, g) holds rows 4g .. 4g + 3 of column col of each sub-tile; a split stores
-    // into its slice of the workspace y (m x n floats per split)
-    float* const yb = y + (int64_t)split * m * n;
+    // into its slice of the workspace (m x n floats per split: y, or part when FUSE)
+    if constexpr (!FUSE) {
+        float* const yb = y + (int64_t)split * m * n;
 #pragma unroll
-    for (int j = 0; j < NR; j++) {
-        const int64_t cn = n0 + 16 * j + col;
+        for (int j = 0; j < NR; j++) {
+            const int64_t cn = n0 + 16 * j + col;
 #pragma unroll
-        for (int e = 0; e < 4; e++) {
-            const int r = 4 * g + e;
-            if (r < m && cn < n) yb[(int64_t)r * n + cn] = acc[j][e];
+            for (int e = 0; e < 4; e++) {
+                const int r = 4 * g + e;
+                if (r < m && cn < n) yb[(int64_t)r * n + cn] = acc[j][e];
+            }
+        }
+    } else {
+        float* const pb = part + (int64_t)split * m * n;
+#pragma unroll
+        for (int j = 0; j < NR; j++) {
+            const int64_t cn = n0 + 16 * j + col;
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+                const int r = 4 * g + e;
+                if (r < m && cn < n)
+                    __hip_atomic_store(reinterpret_cast<uint32_t*>(pb + (int64_t)r * n + cn), __float_as_uint(acc[j][e]),
+                                       __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            }
+        }
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        __syncthreads();
+        __shared__ int s_last;
+        if (tid == 0) {
+            const uint32_t old = __hip_atomic_fetch_add(g_short_arrive + tile, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            const int last = old == (uint32_t)(nsp - 1);
+            if (last) __hip_atomic_store(g_short_arrive + tile, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            s_last = last;
+        }
+        __syncthreads();
+        if (!s_last) return;  // uniform per workgroup
+        // y = the slices added in slice order, as k_splitk_sum_short adds them: thread t takes
+        // 4-column units t, t + 256, ... of the tile's m x 64 NR outputs and requests every
+        // slice's 16 bytes of a unit at once
+        const int64_t mn = (int64_t)m * n;
+        const __amdgpu_buffer_rsrc_t rp = __builtin_amdgcn_make_buffer_rsrc(part, (short)0, (int)(nsp * mn * 4), 0x00020000);
+        constexpr int UPR = 4 * NR * SG_WAVES;  // 4-column units per tile row
+        const int64_t c0 = (int64_t)tile * SG_WAVES * 16 * NR;
+#pragma unroll
+        for (int u0 = 0; u0 < MT * UPR; u0 += 64 * SG_WAVES) {
+            const int u = u0 + tid, r = u / UPR;
+            const int64_t cn = c0 + 4 * (u % UPR);
+            if (r < m && cn < n) {
+                const uint32_t vo = (uint32_t)(((int64_t)r * n + cn) * 4);
+                // every load issued before the first add (slices p >= nsp lie past the buffer's
+                // range and read 0; the selects keep them out of the sum)
+                u32x4 t[SG_FUSE_NSP];
+#pragma unroll
+                for (int p = 0; p < SG_FUSE_NSP; p++)
+                    t[p] = __builtin_amdgcn_raw_buffer_load_b128(rp, vo, (int)(p * mn * 4), 16);
+                float4 v = make_float4(__uint_as_float(t[0].x), __uint_as_float(t[0].y), __uint_as_float(t[0].z),
+                                       __uint_as_float(t[0].w));
+#pragma unroll
+                for (int p = 1; p < SG_FUSE_NSP; p++) {
+                    const bool on = p < nsp;
+                    v.x = on ? v.x + __uint_as_float(t[p].x) : v.x;
+                    v.y = on ? v.y + __uint_as_float(t[p].y) : v.y;
+                    v.z = on ? v.z + __uint_as_float(t[p].z) : v.z;
+                    v.w = on ? v.w + __uint_as_float(t[p].w) : v.w;
+                }
+                *reinterpret_cast<float4*>(y + (int64_t)r * n + cn) = v;
+            }
         }
     }
 }
@@ -846,6 +916,9 @@ int launch_gemm_short(const QWeight* w, const float* x, float* y, int64_t m, hip
     }
     float* const out = pl.nsp > 1 ? part : y;
     const unsigned grid = (unsigned)(cdiv(pl.tiles, 8) * 8 * pl.nsp);
+    // one launch when no other stream can run a call that shares the arrival counters
+    const bool fuse = pl.nsp > 1 && pl.nsp <= SG_FUSE_NSP && pl.tiles <= SG_ARRIVE_MAX && w->n % 4 == 0 &&
+                      (size_t)pl.nsp * m * w->n * 4 < (1ull << 31) && single_stream() && one_launch_merge();
     const int ti = (int)pl.tiles, ns = (int)pl.nsp;
     const void* dsc = w->ggml_type == TL_HIP_GGML_Q4_K ? static_cast<const void*>(w->us) : static_cast<const void*>(w->d);
     tls_plan[0] = m <= 8 ? 8 : 16;
@@ -856,10 +929,20 @@ int launch_gemm_short(const QWeight* w, const float* x, float* y, int64_t m, hip
         constexpr int QT = decltype(qt)::value;
         auto run = [&](auto mt) {
             constexpr int MT = decltype(mt)::value;
-            if (pl.nr == 1)
-                k_qgemm_short<QT, MT, 1><<<grid, 64 * SG_WAVES, 0, s>>>(w->qs, dsc, x, out, mi, w->n, w->k, w->nb, ti, ns);
-            else
-                k_qgemm_short<QT, MT, 2><<<grid, 64 * SG_WAVES, 0, s>>>(w->qs, dsc, x, out, mi, w->n, w->k, w->nb, ti, ns);
+            if (fuse) {
+                if (pl.nr == 1)
+                    k_qgemm_short<QT, MT, 1, true><<<grid, 64 * SG_WAVES, 0, s>>>(w->qs, dsc, x, y, mi, w->n, w->k, w->nb,
+                                                                                  ti, ns, part);
+                else
+                    k_qgemm_short<QT, MT, 2, true><<<grid, 64 * SG_WAVES, 0, s>>>(w->qs, dsc, x, y, mi, w->n, w->k, w->nb,
+                                                                                  ti, ns, part);
+            } else if (pl.nr == 1) {
+                k_qgemm_short<QT, MT, 1, false><<<grid, 64 * SG_WAVES, 0, s>>>(w->qs, dsc, x, out, mi, w->n, w->k, w->nb,
+                                                                               ti, ns, nullptr);
+            } else {
+                k_qgemm_short<QT, MT, 2, false><<<grid, 64 * SG_WAVES, 0, s>>>(w->qs, dsc, x, out, mi, w->n, w->k, w->nb,
+                                                                               ti, ns, nullptr);
+            }
         };
         if (m <= 8) run(std::integral_constant<int, 8>{});
         else run(std::integral_constant<int, 16>{});
@@ -870,7 +953,8 @@ int launch_gemm_short(const QWeight* w, const float* x, float* y, int64_t m, hip
     if (pl.nsp > 1) {
         const int64_t mn = m * w->n;
         const unsigned sg = (unsigned)cdiv(cdiv(mn, 4), 64);
-        if (pl.nsp <= 4) k_splitk_sum_short<4><<<sg, 64, 0, s>>>(part, y, mn, (int)pl.nsp);
+        if (fuse) {
+        } else if (pl.nsp <= 4) k_splitk_sum_short<4><<<sg, 64, 0, s>>>(part, y, mn, (int)pl.nsp);
         else if (pl.nsp <= 8) k_splitk_sum_short<8><<<sg, 64, 0, s>>>(part, y, mn, (int)pl.nsp);
         else k_splitk_sum_short<16><<<sg, 64, 0, s>>>(part, y, mn, (int)pl.nsp);
         if (!noalloc) dev_free_on(part, s);  // freed on s: reused at once only by later work on s

@@ -72,6 +72,7 @@ void note_stream(hipStream_t s);
 // True when note_stream(s) would synchronise the library stream (the first caller stream).
 bool note_stream_syncs(hipStream_t s);
 bool single_stream();  // no stream but the library's has run library work (calls cannot overlap)
+bool one_launch_merge();  // split kernels may merge their partials in the same launch
 // Looks up the device address of the allocation-free GEMM's scratch array on `device` (the
 // current device during library initialisation); status code.
 int noalloc_scratch_init(int device);

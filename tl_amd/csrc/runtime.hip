@@ -109,6 +109,9 @@ bool note_stream_syncs(hipStream_t s) {
 
 bool single_stream() { return !g_multi.load(std::memory_order_acquire); }
 
+static std::atomic<bool> g_one_launch{true};
+bool one_launch_merge() { return g_one_launch.load(std::memory_order_relaxed); }
+
 void note_stream(hipStream_t s) {
     if (!s || g_multi.load(std::memory_order_acquire) || !state() || s == g_state.stream) return;
     std::lock_guard<std::mutex> lk(g_alloc_mu);
@@ -282,6 +285,8 @@ int tl_hip_debug_fail_alloc(int64_t after) {
     g_fail_after.store(after < 0 ? -1 : after);
     return TL_HIP_OK;
 }
+
+int tl_hip_debug_one_launch_merge(int on) { return g_one_launch.exchange(on != 0) ? 1 : 0; }
 
 int tl_hip_synchronize(void) {
     if (!state()) return tls_status;
