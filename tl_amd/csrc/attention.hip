@@ -368,23 +368,6 @@ __device__ __forceinline__ void tr_halve(float (&v)[N], int lane) {
     if constexpr (OFF > LO) tr_halve<OFF / 2, LO, H / 2, N, HIGH>(v, lane);
 }
 
-// Split records of the one-launch form are written and read as agent-scope atomics (stores
-// that write through to the agent's point of coherence, loads that do not hit a stale line
-// of another XCD's L2), so neither side needs a whole-L2 write-back or invalidate.
-template <bool FUSE>
-__device__ __forceinline__ void rec_store(float* p, float v) {
-    if constexpr (FUSE) __hip_atomic_store(reinterpret_cast<uint32_t*>(p), __float_as_uint(v), __ATOMIC_RELAXED,
-                                           __HIP_MEMORY_SCOPE_AGENT);
-    else *p = v;
-}
-template <bool FUSE>
-__device__ __forceinline__ float rec_load(const float* p) {
-    if constexpr (FUSE)
-        return __uint_as_float(__hip_atomic_load(reinterpret_cast<const uint32_t*>(p), __ATOMIC_RELAXED,
-                                                 __HIP_MEMORY_SCOPE_AGENT));
-    else return *p;
-}
-
 // PW positions per wavefront, 4 PW per workgroup (split).  FUSE false: the split records are
 // merged by k_attn_merge_gq; true: the workgroup that completes the last split of a (batch
 // item, KV head) merges them in the same launch.
@@ -517,22 +500,39 @@ __global__ __launch_bounds__(256) void k_attn_gq(AttnArgs a) {
         return;
     }
     float* wr = a.ws + (((int64_t)b * a.hkv + h) * a.nsplit + split) * G * (D + 2);
-    for (int idx = tid; idx < G * D; idx += 256) {
-        const int g = idx / D, d = idx % D;
-        rec_store<FUSE>(wr + g * (D + 2) + d, (part[0][g][d] + part[1][g][d]) + (part[2][g][d] + part[3][g][d]));
-    }
-    if (tid < G) {
-        rec_store<FUSE>(wr + tid * (D + 2) + D, stat[tid][0]);
-        rec_store<FUSE>(wr + tid * (D + 2) + D + 1, stat[tid][1]);
-    }
-    if constexpr (FUSE) {
+    if constexpr (!FUSE) {  // record [G][D + 2]: o, then max and sum, per head
+        for (int idx = tid; idx < G * D; idx += 256) {
+            const int g = idx / D, d = idx % D;
+            wr[g * (D + 2) + d] = (part[0][g][d] + part[1][g][d]) + (part[2][g][d] + part[3][g][d]);
+        }
+        if (tid < G) {
+            wr[tid * (D + 2) + D] = stat[tid][0];
+            wr[tid * (D + 2) + D + 1] = stat[tid][1];
+        }
+    } else {
+        // Record [G][D] of o, then [G] (max, sum) pairs, 16-byte aligned (G (D + 2) floats per
+        // split), written with the agent-coherent cache policy (through to the agent's point
+        // of coherence) in 16-byte stores.
+        const __amdgpu_buffer_rsrc_t rw = buf_rsrc(wr, G * (D + 2) * 4);
+        for (int u = tid; u < G * D / 4; u += 256) {
+            const int g = 4 * u / D, d = 4 * u % D;
+            u32x4 v;
+            v.x = __float_as_uint((part[0][g][d] + part[1][g][d]) + (part[2][g][d] + part[3][g][d]));
+            v.y = __float_as_uint((part[0][g][d + 1] + part[1][g][d + 1]) + (part[2][g][d + 1] + part[3][g][d + 1]));
+            v.z = __float_as_uint((part[0][g][d + 2] + part[1][g][d + 2]) + (part[2][g][d + 2] + part[3][g][d + 2]));
+            v.w = __float_as_uint((part[0][g][d + 3] + part[1][g][d + 3]) + (part[2][g][d + 3] + part[3][g][d + 3]));
+            __builtin_amdgcn_raw_buffer_store_b128(v, rw, 16 * u, 0, CPOL_SC1);
+        }
+        if (tid < G) {
+            const u32x2 ml = {__float_as_uint(stat[tid][0]), __float_as_uint(stat[tid][1])};
+            __builtin_amdgcn_raw_buffer_store_b64(ml, rw, 4 * (G * D + 2 * tid), 0, CPOL_SC1);
+        }
         // Arrival.  Every wave waits until its record stores have completed (reached the
         // agent's point of coherence) before the barrier, so the counter is bumped only once
         // the whole record is visible to every XCD: the release order of an agent-scope
         // fence without its L2 write-back, which only plain stores need.  The last arriver
-        // reads the records with agent-scope loads issued after its bump has returned.
+        // reads the records with the same cache policy, issued after its bump has returned.
         __shared__ int s_last;
-        __shared__ float wts[ATT_FUSE_MAX][G], lsum[ATT_FUSE_MAX][G], rden[G];
         asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
         __syncthreads();
         // splits holding positions; the grid has a.nsplit <= ATT_FUSE_MAX of them
@@ -546,35 +546,40 @@ __global__ __launch_bounds__(256) void k_attn_gq(AttnArgs a) {
         }
         __syncthreads();
         if (!s_last) return;  // uniform per workgroup
-        // Merge of the nact records of every head of the group: out = sum_s o_s w_s / sum_s l_s w_s,
-        // w_s = e^(m_s - max m).
+        // Merge of the nact records: out = sum_s o_s w_s / sum_s l_s w_s, w_s = e^(m_s - max m).
+        // A thread takes four consecutive outputs of one head and requests their o values and
+        // the head's (max, sum) of every split at once (records past nact lie beyond the
+        // resource's range and read 0; the selects drop them).
+        constexpr int RB = G * (D + 2) * 4;  // bytes per split record
         const float* rb = a.ws + (((int64_t)b * a.hkv + h) * a.nsplit) * G * (D + 2);
-        for (int i = tid; i < nact * G; i += 256) {
-            const int sp = i / G, g = i % G;
-            wts[sp][g] = rec_load<FUSE>(rb + ((int64_t)sp * G + g) * (D + 2) + D);
-            lsum[sp][g] = rec_load<FUSE>(rb + ((int64_t)sp * G + g) * (D + 2) + D + 1);
-        }
-        __syncthreads();
-        if (tid < G) {
-            float M = -INFINITY;
-            for (int sp = 0; sp < nact; sp++) M = fmaxf(M, wts[sp][tid]);
-            float den = 0.f;
-            for (int sp = 0; sp < nact; sp++) {
-                const float e = expf(wts[sp][tid] - M);  // every split holds a valid position
-                wts[sp][tid] = e;
-                den = fmaf(lsum[sp][tid], e, den);
-            }
-            rden[tid] = 1.0f / den;
-        }
-        __syncthreads();
+        const __amdgpu_buffer_rsrc_t rr = buf_rsrc(rb, (uint32_t)(nact * RB));
         const int hq = a.hkv * G;
-        for (int idx = tid; idx < G * D; idx += 256) {
-            const int g = idx / D, d = idx % D;
-            const float* ro = rb + g * (D + 2) + d;
-            float acc = 0.f;
-#pragma unroll 8
-            for (int sp = 0; sp < nact; sp++) acc = fmaf(rec_load<FUSE>(ro + (int64_t)sp * G * (D + 2)), wts[sp][g], acc);
-            a.out[((int64_t)b * hq + h * G + g) * D + d] = acc * rden[g];
+        for (int u = tid; u < G * D / 4; u += 256) {
+            const int g = 4 * u / D, d = 4 * u % D;
+            u32x4 o[ATT_FUSE_MAX];
+            u32x2 ml[ATT_FUSE_MAX];
+#pragma unroll
+            for (int sp = 0; sp < ATT_FUSE_MAX; sp++) {
+                o[sp] = __builtin_amdgcn_raw_buffer_load_b128(rr, 16 * u, sp * RB, CPOL_SC1);
+                ml[sp] = __builtin_amdgcn_raw_buffer_load_b64(rr, 4 * (G * D + 2 * g), sp * RB, CPOL_SC1);
+            }
+            float M = __uint_as_float(ml[0].x);  // split 0 always holds positions
+#pragma unroll
+            for (int sp = 1; sp < ATT_FUSE_MAX; sp++) M = sp < nact ? fmaxf(M, __uint_as_float(ml[sp].x)) : M;
+            float den = 0.f;
+            float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+            for (int sp = 0; sp < ATT_FUSE_MAX; sp++) {
+                const float e = sp < nact ? expf(__uint_as_float(ml[sp].x) - M) : 0.f;
+                den = fmaf(__uint_as_float(ml[sp].y), e, den);
+                acc.x = fmaf(__uint_as_float(o[sp].x), e, acc.x);
+                acc.y = fmaf(__uint_as_float(o[sp].y), e, acc.y);
+                acc.z = fmaf(__uint_as_float(o[sp].z), e, acc.z);
+                acc.w = fmaf(__uint_as_float(o[sp].w), e, acc.w);
+            }
+            const float rd = 1.0f / den;
+            *reinterpret_cast<float4*>(a.out + ((int64_t)b * hq + h * G + g) * D + d) =
+                make_float4(acc.x * rd, acc.y * rd, acc.z * rd, acc.w * rd);
         }
     }
 }

@@ -299,9 +299,6 @@ __global__ __launch_bounds__(256) void k_dequant_f16q(QView qv, _Float16* __rest
 // instruction writes 64 consecutive elements).  The per-lane offset is fixed for the whole K
 // loop and the iteration's advance is a scalar, so the loop spends no vector instruction on
 // addresses (with flat global_load_lds each load cost two 64-bit vector adds).
-__device__ __forceinline__ __amdgpu_buffer_rsrc_t buf_rsrc(const void* p, uint32_t bytes) {
-    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), (short)0, (int)bytes, 0x00020000);
-}
 __device__ __forceinline__ void buf_dma16(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff, void* lds) {
     __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void*)lds, 16, voff, soff, 0, 0);
 }
@@ -809,7 +806,7 @@ __global__ __launch_bounds__(64 * SG_WAVES) void k_qgemm_short(const uint8_t* __
         // 4-column units t, t + 256, ... of the tile's m x 64 NR outputs and requests every
         // slice's 16 bytes of a unit at once
         const int64_t mn = (int64_t)m * n;
-        const __amdgpu_buffer_rsrc_t rp = __builtin_amdgcn_make_buffer_rsrc(part, (short)0, (int)(nsp * mn * 4), 0x00020000);
+        const __amdgpu_buffer_rsrc_t rp = buf_rsrc(part, (uint32_t)(nsp * mn * 4));
         constexpr int UPR = 4 * NR * SG_WAVES;  // 4-column units per tile row
         const int64_t c0 = (int64_t)tile * SG_WAVES * 16 * NR;
 #pragma unroll
@@ -823,7 +820,7 @@ __global__ __launch_bounds__(64 * SG_WAVES) void k_qgemm_short(const uint8_t* __
                 u32x4 t[SG_FUSE_NSP];
 #pragma unroll
                 for (int p = 0; p < SG_FUSE_NSP; p++)
-                    t[p] = __builtin_amdgcn_raw_buffer_load_b128(rp, vo, (int)(p * mn * 4), 16);
+                    t[p] = __builtin_amdgcn_raw_buffer_load_b128(rp, vo, (int)(p * mn * 4), CPOL_SC1);
                 float4 v = make_float4(__uint_as_float(t[0].x), __uint_as_float(t[0].y), __uint_as_float(t[0].z),
                                        __uint_as_float(t[0].w));
 #pragma unroll

@@ -44,6 +44,15 @@ __device__ __forceinline__ void st_wt(__half* p, __half v) {
 // Weight-stream loads: read once per pass and not reused by the launch, loaded non-temporal
 // (global_load ... nt)
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+
+// Raw (stride 0) buffer resource over [p, p + bytes): buffer loads past the range read 0.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t buf_rsrc(const void* p, uint32_t bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), (short)0, (int)bytes, 0x00020000);
+}
+// Cache policy of a buffer access that is coherent at agent scope (the sc1 bit): the policy of
+// agent-scope atomic loads and stores on this target.
+constexpr int CPOL_SC1 = 16;
 __device__ __forceinline__ uint4 ld_stream(const uint4* p) {
     const u32x4 t = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p));
     return uint4{t.x, t.y, t.z, t.w};
