@@ -309,10 +309,22 @@ __device__ __forceinline__ void buf_dma4(__amdgpu_buffer_rsrc_t r, uint32_t voff
 // X-tile chunk swizzle of row r (mod 16): a bijection of the 16 chunks for every row
 __device__ __forceinline__ int xsw(int r) { return ((2 * r) & 15) ^ ((r >> 3) & 1); }
 
-template <int QT, int BM, int BN>
+// One-launch split-K form of k_qgemm_mfma: an arrival counter per tile (split plans have at
+// most 512 tiles), zero at load and returned to zero by the tile's last-arriving split.
+constexpr int GM_ARRIVE_MAX = 512;
+constexpr int GM_FUSE_NSP = 16;
+__device__ uint32_t g_gemm_arrive[GM_ARRIVE_MAX];
+
+// FUSE (split K, 32-wide tiles, n % 4 == 0): every split stores its partial tile into its
+// slice of y as agent-scope atomics (written through to the agent's point of coherence) and
+// the split that finishes the tile last forms fin = res + slice 0 + ... + slice nsp-1 (res
+// for the residual epilogue, else 0) -- k_splitk_sum's additions in its order -- reading the
+// slices with the agent-coherent cache policy, all of a 4-column unit's slices at once.
+template <int QT, int BM, int BN, bool FUSE = false>
 __global__ __launch_bounds__(512) void k_qgemm_mfma(const uint8_t* __restrict__ qs, const __half* __restrict__ dsc,
                                                     const _Float16* __restrict__ x16, float* y, int64_t m,
-                                                    int64_t n, int64_t k, int64_t nb, GemmEpi ep) {
+                                                    int64_t n, int64_t k, int64_t nb, GemmEpi ep,
+                                                    float* __restrict__ fin = nullptr) {
     // every argument, fetched from the kernel-argument buffer in one round of scalar loads
     // (left to the compiler, three dependent rounds precede the first tile load)
     asm volatile("" : : "s"(qs), "s"(dsc), "s"(x16), "s"(y), "s"(m), "s"(n), "s"(k), "s"(nb), "s"(ep.mode),
@@ -534,10 +546,55 @@ __global__ __launch_bounds__(512) void k_qgemm_mfma(const uint8_t* __restrict__ 
                             ep.out16[f16q_index(r, c >> 1, n >> 1, ep.order)] = (_Float16)a;
                         }
                     } else if (r < m && c < n) {
-                        yb[r * n + c] = ep.mode == GEMM_RES ? ep.res[r * n + c] + v : v;
+                        if constexpr (FUSE)
+                            __hip_atomic_store(reinterpret_cast<uint32_t*>(yb + r * n + c), __float_as_uint(v),
+                                               __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                        else yb[r * n + c] = ep.mode == GEMM_RES ? ep.res[r * n + c] + v : v;
                     }
                 }
             }
+    }
+    if constexpr (FUSE) {
+        // arrival: every wavefront's slice stores have completed before the count is bumped
+        __shared__ int s_last;
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        __syncthreads();
+        const int nsp = (int)gridDim.y;
+        if (threadIdx.x == 0) {
+            uint32_t* cnt = g_gemm_arrive + blockIdx.x;
+            const uint32_t old = __hip_atomic_fetch_add(cnt, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            const int last = old == (uint32_t)(nsp - 1);
+            if (last) __hip_atomic_store(cnt, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            s_last = last;
+        }
+        __syncthreads();
+        if (!s_last) return;  // uniform per workgroup
+        const int64_t mn = m * n;
+        const __amdgpu_buffer_rsrc_t rp = buf_rsrc(y, (uint32_t)(nsp * mn * 4));
+        constexpr int UPR = BN / 4;  // 4-column units per tile row
+        for (int u = threadIdx.x; u < BM * UPR; u += 512) {
+            const int64_t r = m0 + u / UPR, c = n0 + 4 * (u % UPR);
+            if (r < m && c < n) {
+                // every slice's 16 bytes requested at once (slices past nsp lie beyond the
+                // resource's range and read 0; the selects keep them out of the sum)
+                const uint32_t vo = (uint32_t)((r * n + c) * 4);
+                u32x4 t[GM_FUSE_NSP];
+#pragma unroll
+                for (int p = 0; p < GM_FUSE_NSP; p++)
+                    t[p] = __builtin_amdgcn_raw_buffer_load_b128(rp, vo, (int)(p * mn * 4), CPOL_SC1);
+                float4 v = ep.mode == GEMM_RES ? *reinterpret_cast<const float4*>(ep.res + r * n + c)
+                                               : make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+                for (int p = 0; p < GM_FUSE_NSP; p++) {
+                    const bool on = p < nsp;
+                    v.x = on ? v.x + __uint_as_float(t[p].x) : v.x;
+                    v.y = on ? v.y + __uint_as_float(t[p].y) : v.y;
+                    v.z = on ? v.z + __uint_as_float(t[p].z) : v.z;
+                    v.w = on ? v.w + __uint_as_float(t[p].w) : v.w;
+                }
+                *reinterpret_cast<float4*>(fin + r * n + c) = v;
+            }
+        }
     }
 }
 
@@ -1086,7 +1143,8 @@ static F16qPlan plan_f16q(const QWeight* w, int64_t m, const GemmEpi& ep, const 
 // defer_part: a split-K launch leaves its nsp partial tiles (m x n floats each, in K order) in
 // a buffer handed to the caller (*defer_part, *defer_nsp; the caller adds them -- plus ep.res
 // for the residual epilogue -- and frees the buffer with dev_free_on on s); an unsplit launch
-// applies the epilogue as usual and returns *defer_part = nullptr, *defer_nsp = 1.
+// applies the epilogue as usual and returns *defer_part = nullptr, *defer_nsp = 1, and so does a
+// split launch whose last-arriving splits add the slices in-kernel (the one-launch form).
 int launch_gemm_f16q(const QWeight* w, const _Float16* x16, float* y, int64_t m, const GemmEpi& ep,
                      hipStream_t s, bool noalloc, float* part_ws, float** defer_part, int* defer_nsp) {
     if (m < 1) return TL_HIP_OK;
@@ -1112,7 +1170,15 @@ int launch_gemm_f16q(const QWeight* w, const _Float16* x16, float* y, int64_t m,
     const F16qPlan plan = plan_f16q(w, m, ep, y);
     const int bm = plan.bm, bn = plan.bn;
     const int64_t tiles = plan.tiles, nsp = plan.nsp;
-    const bool defer = defer_part && nsp > 1 && !noalloc;
+    // one launch (the tile's last split adds the slices) for the split plans of short inputs
+    // (32- and 64-row tiles), when no other stream can run a call that shares the arrival
+    // counters.  At 128-row tiles the deferred sum is cheaper: the RMSNorm that reads the
+    // residual next adds the slices with a workgroup per row (512-token prefill 2.83 ms
+    // against 2.89 ms with the in-kernel sum; 32 tokens 1.30 -> 1.21 ms with it).
+    const bool fuse = nsp > 1 && nsp <= GM_FUSE_NSP && bn == 32 && bm <= 64 && tiles <= GM_ARRIVE_MAX && w->n % 4 == 0 &&
+                      ep.mode != GEMM_GLU16 && (size_t)nsp * m * w->n * 4 < (1ull << 31) && single_stream() &&
+                      one_launch_merge();
+    const bool defer = defer_part && nsp > 1 && !noalloc && !fuse;
     if (defer_part) {
         *defer_part = nullptr;
         *defer_nsp = 1;
@@ -1137,10 +1203,13 @@ int launch_gemm_f16q(const QWeight* w, const _Float16* x16, float* y, int64_t m,
         if (NIB16 && bn == 96) {
             if constexpr (NIB16) k_qgemm_mfma<QT, BM, 96><<<grid, 512, 0, s>>>(q, d, x16, out, m, w->n, w->k, w->nb, pe);
         } else if (bn == 64) k_qgemm_mfma<QT, BM, 64><<<grid, 512, 0, s>>>(q, d, x16, out, m, w->n, w->k, w->nb, pe);
-        else if (bm == 32) k_qgemm_mfma<QT, 32, 32><<<grid, 512, 0, s>>>(q, d, x16, out, m, w->n, w->k, w->nb, pe);
+        else if (fuse) {
+            if (bm == 32) k_qgemm_mfma<QT, 32, 32, true><<<grid, 512, 0, s>>>(q, d, x16, out, m, w->n, w->k, w->nb, ep, y);
+            else k_qgemm_mfma<QT, 64, 32, true><<<grid, 512, 0, s>>>(q, d, x16, out, m, w->n, w->k, w->nb, ep, y);
+        } else if (bm == 32) k_qgemm_mfma<QT, 32, 32><<<grid, 512, 0, s>>>(q, d, x16, out, m, w->n, w->k, w->nb, pe);
         else if (bm == 64) k_qgemm_mfma<QT, 64, 32><<<grid, 512, 0, s>>>(q, d, x16, out, m, w->n, w->k, w->nb, pe);
         else k_qgemm_mfma<QT, BM, 32><<<grid, 512, 0, s>>>(q, d, x16, out, m, w->n, w->k, w->nb, pe);
-        if (nsp > 1 && !defer) {
+        if (nsp > 1 && !defer && !fuse) {
             const int64_t mn = m * w->n;
             k_splitk_sum<<<(unsigned)cdiv(cdiv(mn, 4), 256), 256, 0, s>>>(
                 part, y, ep.mode == GEMM_RES ? ep.res : nullptr, mn, (int)nsp);
