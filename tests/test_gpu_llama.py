@@ -100,6 +100,40 @@ def test_f16_prefill_mfma_attention_chunks():
         cpu.close()
 
 
+@pytest.mark.parametrize("n", [21, 32, 64])
+def test_f16_prefill_one_launch_split_sums(n):
+    """Short prompts (32- and 64-row GEMM tiles with K split): the tiles' last-arriving splits
+    add the partial slices in-kernel (with the residual for o-proj / down), and the form with
+    separate sums -- a split-K sum launch after qkv, the slices added by the next RMSNorm --
+    gives bitwise the same logits; both within the f16 tolerance of the oracle."""
+    cfg = LlamaConfig(2, 512, 8, 1, 512, 1000, max_seq=256)
+    tensors = list(synthetic_weights(cfg, 47))
+    gpu = HipLlama(cfg, kv_f16=True)
+    gpu.load(tensors)
+    cpu = oracle.Llama(cfg)
+    cpu.load(tensors)
+    lib = gpu.lib
+    prev = lib.tl_hip_debug_one_launch_merge(1)
+    try:
+        prompt = synthetic_prompt(cfg, 47, n)
+        cpu.reset()
+        ref = cpu.forward(prompt)
+        gpu.reset()
+        one = gpu.forward(prompt, prefill_f16=True)
+        lib.tl_hip_debug_one_launch_merge(0)
+        gpu.reset()
+        two = gpu.forward(prompt, prefill_f16=True)
+        for got in (one, two):
+            err = max_rel(got, ref)
+            assert err <= 1e-2, f"f16 prefill logits max-rel-err {err:.2e}"
+        # the same additions in the same order: bitwise equal logits
+        assert np.array_equal(one.view(np.uint32), two.view(np.uint32)), f"max-rel-err {max_rel(one, two):.2e}"
+    finally:
+        lib.tl_hip_debug_one_launch_merge(prev)
+        gpu.close()
+        cpu.close()
+
+
 @pytest.mark.parametrize("kv_f16", [True, False])
 def test_long_cache_decode_paths(kv_f16):
     """Caches longer than 4096 positions: decode attention takes the grouped-query split form

@@ -317,7 +317,7 @@ __device__ uint32_t g_gemm_arrive[GM_ARRIVE_MAX];
 
 // FUSE (split K, 32-wide tiles, n % 4 == 0): every split stores its partial tile into its
 // slice of y as agent-scope atomics (written through to the agent's point of coherence) and
-// the split that finishes the tile last forms fin = res + slice 0 + ... + slice nsp-1 (res
+// the split that finishes the tile last forms v = res + slice 0 + ... + slice nsp-1 (res
 // for the residual epilogue, else 0) -- k_splitk_sum's additions in its order -- reading the
 // slices with the agent-coherent cache policy, all of a 4-column unit's slices at once.
 template <int QT, int BM, int BN, bool FUSE = false>
@@ -1093,6 +1093,13 @@ struct F16qPlan {
 };
 }  // namespace
 
+// whether a split plan of these tiles may add its slices in-kernel (the one-launch form)
+static bool f16q_fuse_ok(const QWeight* w, int64_t m, int bm, int bn, int64_t tiles, int64_t nsp,
+                         const GemmEpi& ep) {
+    return ep.mode != GEMM_GLU16 && nsp > 1 && nsp <= GM_FUSE_NSP && bn == 32 && bm <= 64 && tiles <= GM_ARRIVE_MAX && w->n % 4 == 0 &&
+           (size_t)nsp * m * w->n * 4 < (1ull << 31) && single_stream() && one_launch_merge();
+}
+
 static F16qPlan plan_f16q(const QWeight* w, int64_t m, const GemmEpi& ep, const float* y) {
     // 128 x 64 tiles when that gives at least one workgroup per CU, else 128 x 32 (twice the
     // workgroups; measured at M = 512: 2048 x 2048 18.7 -> 15.5 us).  At 256 wide tiles the
@@ -1114,8 +1121,10 @@ static F16qPlan plan_f16q(const QWeight* w, int64_t m, const GemmEpi& ep, const 
     // (512 tiles for M <= 32, where the K loop's latency dominates) the K range split over up
     // to 16 workgroup rows until about 512 workgroups run (the 512-token prefill's 256-tile
     // o-projection and down projection included: 3.66 -> 3.49 ms); partial tiles go to a workspace that
-    // k_splitk_sum adds up (with the residual).  The SwiGLU epilogue is not linear and keeps
-    // one workgroup per tile.  (Measured at M = 16 / 128: 4096 x 4096
+    // k_splitk_sum adds up (with the residual), or the tile's last split in-kernel.  The SwiGLU
+    // epilogue is not linear and keeps one workgroup per tile (split in the one-launch form,
+    // with SwiGLU after the last split's sum, it measured slower: 32-token prefill 1.19 ->
+    // 1.22 ms).  (Measured at M = 16 / 128: 4096 x 4096
     // 27.1 -> 13.1 / 28.9 -> 21.7 us, 4096 x 11008 63.5 -> 22.0 / 70.6 -> 36.7 us per call
     // including the X conversion; splitting the 344 tiles of 11008 x 4096 in two at M = 128
     // was slower, 37.0 -> 44.7 us, and faster at M = 16, 23.6 -> 20.5 us.)
@@ -1175,9 +1184,7 @@ int launch_gemm_f16q(const QWeight* w, const _Float16* x16, float* y, int64_t m,
     // counters.  At 128-row tiles the deferred sum is cheaper: the RMSNorm that reads the
     // residual next adds the slices with a workgroup per row (512-token prefill 2.83 ms
     // against 2.89 ms with the in-kernel sum; 32 tokens 1.30 -> 1.21 ms with it).
-    const bool fuse = nsp > 1 && nsp <= GM_FUSE_NSP && bn == 32 && bm <= 64 && tiles <= GM_ARRIVE_MAX && w->n % 4 == 0 &&
-                      ep.mode != GEMM_GLU16 && (size_t)nsp * m * w->n * 4 < (1ull << 31) && single_stream() &&
-                      one_launch_merge();
+    const bool fuse = f16q_fuse_ok(w, m, bm, bn, tiles, nsp, ep);
     const bool defer = defer_part && nsp > 1 && !noalloc && !fuse;
     if (defer_part) {
         *defer_part = nullptr;
