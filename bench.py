@@ -226,10 +226,29 @@ def bench_vendor_gemm(dev, shapes, m=512, reps=30):
     return rows
 
 
+def _copy_floor(dev, half, reps, min_bytes):
+    """Seconds per device-to-device copy of `half` bytes (read half, write half: the traffic of
+    a row op of 2 half algorithmic bytes), sources and destinations rotated past the Infinity
+    Cache like the row ops' inputs: the one-launch floor of a streaming kernel of that size."""
+    import ctypes as C
+    half = -(-half // 256) * 256
+    n = -(-min_bytes // half)
+    src = [dev.lib.tl_hip_malloc(half) for _ in range(n)]
+    dst = [dev.lib.tl_hip_malloc(half) for _ in range(n)]
+
+    def cp(i):
+        dev.lib.tl_hip_memcpy_d2d(C.c_void_p(dst[i % n]), C.c_void_p(src[i % n]), half)
+    sec = _timed(dev, cp, max(reps, n))
+    dev.synchronize()
+    for b in src + dst:
+        dev.lib.tl_hip_free(C.c_void_p(b))
+    return sec
+
+
 def bench_row_ops(dev, reps=60, min_bytes=320 << 20):
     """configs[1] row ops on f32 activations, each input uploaded in enough copies (>= 320 MB)
     that the Infinity Cache cannot serve it: GB/s of the algorithmic bytes (every input read
-    once, the output written once)."""
+    once, the output written once), beside a device copy that moves the same bytes."""
     rng = np.random.default_rng(0x71510001)
     x = rng.standard_normal((512, 4096)).astype(np.float32)
     w = rng.uniform(0.5, 1.5, 4096).astype(np.float32)
@@ -258,12 +277,15 @@ def bench_row_ops(dev, reps=60, min_bytes=320 << 20):
             call(ins[i % copies]).release()
         sec = _timed(dev, launch, max(reps, copies))
         gbs = nbytes / sec / 1e9
-        rows.append({"op": name, "shape": shape, "bytes": nbytes, "us": round(sec * 1e6, 2), "gbs": round(gbs, 1),
-                     "frac": round(gbs / HBM_PEAK_GBS, 4)})
-        log(f"[bench] {name} {shape}: {sec * 1e6:.1f} us, {gbs:.0f} GB/s ({100 * gbs / HBM_PEAK_GBS:.1f}% of HBM peak)")
         for t in ins:
             for h in t:
                 h.release()
+        csec = _copy_floor(dev, nbytes // 2, reps, min_bytes)
+        rows.append({"op": name, "shape": shape, "bytes": nbytes, "us": round(sec * 1e6, 2), "gbs": round(gbs, 1),
+                     "frac": round(gbs / HBM_PEAK_GBS, 4), "copy_us": round(csec * 1e6, 2),
+                     "of_copy": round(csec / sec, 3)})
+        log(f"[bench] {name} {shape}: {sec * 1e6:.1f} us, {gbs:.0f} GB/s ({100 * gbs / HBM_PEAK_GBS:.1f}% of HBM peak); "
+            f"a device copy of the same bytes {csec * 1e6:.1f} us")
     for t in (wt, cos, sin):
         t.release()
     return rows
@@ -511,6 +533,33 @@ def bench_decode(dev, cfg, ggml_type, args, steps=None, variants=()):
     return tok_s, decode_s, prefill_s, short_s, rows
 
 
+def bench_prefill(dev, cfg, args, lengths=(32, 512), reps=4):
+    """Warm f16 prefills of the synthetic TinyLlama-shape decoder (Q4_0, then the Q4_K_M
+    mixture): the best of `reps` forwards per prompt length, in ms."""
+    from tl_amd.llama import HipLlama, synthetic_prompt, synthetic_weights
+
+    out = []
+    for gt in (2, "Q4_K_M"):
+        model = HipLlama(cfg, kv_f16=True)
+        model.load(synthetic_weights(cfg, 1234, ggml_type=gt), ggml_type=gt)
+        prompt = synthetic_prompt(cfg, 1234, max(lengths))
+        row = {"weights": "Q4_0" if gt == 2 else gt}
+        for n in lengths:
+            best = float("inf")
+            for _ in range(reps + 1):  # the first forward of a length allocates its buffers
+                model.reset()
+                dev.synchronize()
+                t0 = time.perf_counter()
+                model.forward(prompt[:n], prefill_f16=True, want_logits=False)
+                dev.synchronize()
+                best = min(best, time.perf_counter() - t0)
+            row[f"prefill_{n}_ms"] = round(best * 1e3, 3)
+        log(f"[bench] prefill {row}")
+        out.append(row)
+        model.close()
+    return out
+
+
 def copy_reference(dev, nbytes=64 << 20):
     """Reference dispatch for the FETCH_SIZE / WRITE_SIZE scale of counter runs: one device
     copy of a known size."""
@@ -545,6 +594,10 @@ def main():
                     help="only the 4096x4096 matvec timing plus a 64 MiB device copy (counter runs)")
     ap.add_argument("--row-ops-only", action="store_true",
                     help="only the configs[1] row-op leg plus a 64 MiB device copy (counter runs)")
+    ap.add_argument("--prefill-only", action="store_true",
+                    help="only the 32- and 512-token prefills of the Q4_0 and Q4_K_M decoders (kernel traces)")
+    ap.add_argument("--two-launch-merges", action="store_true",
+                    help="split kernels merge their partials in a second kernel, not in-kernel (A/B runs)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU: this build has no multi-GPU path (every box has one GPU); "
@@ -561,6 +614,8 @@ def main():
     from tl_amd.llama import LlamaConfig
 
     dev = HipDevice(0)
+    if args.two_launch_merges:
+        dev.lib.tl_hip_debug_one_launch_merge(0)
     cfg = LlamaConfig.tinyllama(max_seq=2048)
     if args.prompt + args.warmup + args.steps > cfg.max_seq:
         sys.exit("prompt + warmup + steps exceed the 2048-position cache")
@@ -576,6 +631,9 @@ def main():
         return
     if args.attention_only:
         print(json.dumps({"decode_attention": bench_attention(dev)}), flush=True)
+        return
+    if args.prefill_only:
+        print(json.dumps({"prefill": bench_prefill(dev, cfg, args)}), flush=True)
         return
     if args.row_ops_only:
         rows = bench_row_ops(dev)
