@@ -27,20 +27,11 @@ struct QView {
     const int8_t* sc;
 };
 
-// Q4_K sub-block j's d * scale and dmin * min from its super-block header (four words: f16 d |
-// f16 dmin, then the 12 packed 6-bit scale / min bytes), QTensor::get_scale_min_k4
-// (quantized.rs:405-415); both products are exact in f32.
+// Q4_K sub-block j's d * scale and dmin * min from its resident super-block header
+// (q4k_hdr_sm; QTensor::get_scale_min_k4, quantized.rs:405-415); both products are exact in f32.
 __device__ __forceinline__ void q4k_scale_min(const uint4& hd, int j, float* d1, float* m1) {
-    const int sh = 8 * (j & 3);
     uint32_t sc, mn;
-    if (j < 4) {
-        sc = (hd.y >> sh) & 63;
-        mn = (hd.z >> sh) & 63;
-    } else {
-        const uint32_t lo = hd.w >> sh;
-        sc = (lo & 0xF) | (((hd.y >> sh) >> 2) & 0x30);
-        mn = ((lo >> 4) & 0xF) | (((hd.z >> sh) >> 2) & 0x30);
-    }
+    q4k_hdr_sm(hd, j, &sc, &mn);
     *d1 = __half2float(__ushort_as_half((uint16_t)(hd.x & 0xFFFF))) * (float)sc;
     *m1 = __half2float(__ushort_as_half((uint16_t)(hd.x >> 16))) * (float)mn;
 }

@@ -110,14 +110,27 @@ size_t dtype_size(int dtype);
 //         d  [n][nb]      f16 scale
 //   Q8_0  qs [n][nb][32]  int8, d [n][nb] f16
 //   Q4_K  qs [n][nb][16]  the unit's 32 nibbles in Q4_0 order (unit = one sub-block)
-//         hdr[n][nb/8][16] the super-block header as stored: f16 d, f16 dmin, 12 packed
-//                          6-bit (scale, min) pairs
+//         hdr[n][nb/8][16] the super-block header: f16 d, f16 dmin, then the 16 6-bit
+//                          fields re-laid (q4k_hdr_sm): scale j at bit 6j of words 1-2,
+//                          min j at bit 16 + 6j of words 2-3
 //   Q6_K  qs [n][nb][16]  low 4 bits in Q4_0 order
 //         qh [n][nb][8]   high 2 bits: word 0 byte b bits 2t..2t+1 = weight b + 4t,
 //                         word 1 the same for weights 16 + b + 4t
 //         sc [n][nb][2]   the int8 scales of the unit's two 16-weight sub-blocks
 //         d  [n][nb/8]    f16 super-block scale
 // Byte counts equal the GGUF stream's (18 / 34 / 144 / 210 bytes per 32 / 32 / 256 / 256).
+// Q4_K sub-block j's 6-bit scale and min from a resident super-block header (words: f16 d |
+// f16 dmin, then the 96 bits of 16 fields -- scales at bits 6j, mins at bits 48 + 6j): one
+// 64-bit shift and a mask each, with no branch on j.  GGUF packs them in 12 bytes two ways
+// (QTensor::get_scale_min_k4, quantized.rs:405-415: sub-blocks 0-3 in the low 6 bits of
+// bytes j and j + 4, sub-blocks 4-7 split over nibbles of bytes j + 4 and the top 2 bits of
+// bytes j - 4 and j), which cost a lane-divergent branch per unit to unpack.
+__host__ __device__ inline void q4k_hdr_sm(const uint4& hd, int j, uint32_t* sc, uint32_t* mn) {
+    const uint64_t a = ((uint64_t)hd.z << 32) | hd.y, b = ((uint64_t)hd.w << 32) | hd.z;
+    *sc = (uint32_t)(a >> (6 * j)) & 63u;
+    *mn = (uint32_t)(b >> (16 + 6 * j)) & 63u;
+}
+
 struct QWeight {
     int ggml_type = 0;
     int64_t n = 0, k = 0, nb = 0;  // rows, cols, 32-weight units per row

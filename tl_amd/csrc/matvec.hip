@@ -71,19 +71,11 @@ struct QB_<TL_HIP_GGML_Q6_K> {
     static constexpr int v = 16;
 };
 
-// Q4_K (scale, min) of sub-block j from a super-block header held as four words (f16 d |
-// f16 dmin, then the 12 packed bytes), QTensor::get_scale_min_k4 (quantized.rs:405-415).
+// Q4_K d * scale and dmin * min of sub-block j from its resident super-block header
+// (q4k_hdr_sm; QTensor::get_scale_min_k4, quantized.rs:405-415); both products exact in f32.
 __device__ __forceinline__ void k4_sm(const uint4& hd, int j, float* du, float* mu) {
-    const int sh = 8 * (j & 3);
     uint32_t sc, mn;
-    if (j < 4) {
-        sc = (hd.y >> sh) & 63;
-        mn = (hd.z >> sh) & 63;
-    } else {
-        const uint32_t lo = hd.w >> sh;
-        sc = (lo & 0xF) | (((hd.y >> sh) >> 2) & 0x30);
-        mn = ((lo >> 4) & 0xF) | (((hd.z >> sh) >> 2) & 0x30);
-    }
+    q4k_hdr_sm(hd, j, &sc, &mn);
     *du = __half2float(__ushort_as_half((uint16_t)(hd.x & 0xFFFF))) * (float)sc;
     *mu = __half2float(__ushort_as_half((uint16_t)(hd.x >> 16))) * (float)mn;
 }

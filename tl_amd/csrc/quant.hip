@@ -80,7 +80,9 @@ __global__ void k_dequant_q8_0(const uint8_t* __restrict__ qs, const __half* __r
 
 // K-quant repack: one thread per 32-weight unit.  Q4_K (quantized.rs:337-400): unit u of a
 // super-block is sub-block u; its weights are the low (u even) or high (u odd) nibbles of
-// quant bytes 32 (u / 2) .. +31.  Unit thread 0 copies the 16-byte header.
+// quant bytes 32 (u / 2) .. +31.  Unit thread 0 writes the header: d and dmin as stored, the
+// eight (scale, min) pairs unpacked by the get_scale_min_k4 rule (quantized.rs:405-415) and
+// re-laid as q4k_hdr_sm reads them.
 __global__ void k_repack_q4_k(const uint8_t* __restrict__ raw, uint8_t* __restrict__ qs,
                               uint8_t* __restrict__ hdr, int64_t nunits) {
     const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
@@ -101,11 +103,18 @@ __global__ void k_repack_q4_k(const uint8_t* __restrict__ raw, uint8_t* __restri
         w[i] = o[4 * i] | (o[4 * i + 1] << 8) | (o[4 * i + 2] << 16) | ((uint32_t)o[4 * i + 3] << 24);
     reinterpret_cast<uint4*>(qs)[t] = make_uint4(w[0], w[1], w[2], w[3]);
     if (u == 0) {
-        uint32_t h[4];
+        const uint8_t* q = p + 4;  // the 12 packed scale bytes
+        uint64_t sc = 0, mn = 0;
 #pragma unroll
-        for (int i = 0; i < 4; i++)
-            h[i] = p[4 * i] | (p[4 * i + 1] << 8) | (p[4 * i + 2] << 16) | ((uint32_t)p[4 * i + 3] << 24);
-        reinterpret_cast<uint4*>(hdr)[sb] = make_uint4(h[0], h[1], h[2], h[3]);
+        for (int j = 0; j < 8; j++) {
+            const uint32_t s = j < 4 ? q[j] & 63u : (q[j + 4] & 0xFu) | ((uint32_t)(q[j - 4] >> 6) << 4);
+            const uint32_t m = j < 4 ? q[j + 4] & 63u : (uint32_t)(q[j + 4] >> 4) | ((uint32_t)(q[j] >> 6) << 4);
+            sc |= (uint64_t)s << (6 * j);
+            mn |= (uint64_t)m << (6 * j);
+        }
+        const uint32_t x = p[0] | (p[1] << 8) | (p[2] << 16) | ((uint32_t)p[3] << 24);  // f16 d | f16 dmin
+        reinterpret_cast<uint4*>(hdr)[sb] =
+            make_uint4(x, (uint32_t)sc, (uint32_t)(sc >> 32) | (uint32_t)(mn << 16), (uint32_t)(mn >> 16));
     }
 }
 
@@ -150,17 +159,6 @@ __global__ void k_repack_q6_k(const uint8_t* __restrict__ raw, uint8_t* __restri
 
 // Q4_K (scale, min) of sub-block j from the header's 12 packed bytes (words 1..3 of the
 // header), QTensor::get_scale_min_k4 (quantized.rs:405-415).
-__device__ __forceinline__ void k4_scale_min(const uint4& hd, int j, int* sc, int* mn) {
-    const uint32_t s03 = hd.y, s47 = hd.z, s811 = hd.w;
-    if (j < 4) {
-        *sc = (s03 >> (8 * j)) & 63;
-        *mn = (s47 >> (8 * j)) & 63;
-    } else {
-        const uint32_t lo = (s811 >> (8 * (j - 4))) & 0xFF;
-        *sc = (int)((lo & 0xF) | (((s03 >> (8 * (j - 4))) >> 6 & 3) << 4));
-        *mn = (int)((lo >> 4) | (((s47 >> (8 * (j - 4))) >> 6 & 3) << 4));
-    }
-}
 
 // Dequantisation from the residency format, one thread per unit.  Q4_K: (d * sc) * q -
 // dmin * m (quantized.rs:380-390; both products exact, one rounding in the subtraction).
@@ -170,8 +168,8 @@ __global__ void k_dequant_q4_k(const uint8_t* __restrict__ qs, const uint8_t* __
     if (t >= nunits) return;
     const uint4 hd = reinterpret_cast<const uint4*>(hdr)[t >> 3];
     const uint4 w = reinterpret_cast<const uint4*>(qs)[t];
-    int sc, mn;
-    k4_scale_min(hd, (int)(t & 7), &sc, &mn);
+    uint32_t sc, mn;
+    q4k_hdr_sm(hd, (int)(t & 7), &sc, &mn);
     const float d = __half2float(__ushort_as_half((uint16_t)(hd.x & 0xFFFF)));
     const float dmin = __half2float(__ushort_as_half((uint16_t)(hd.x >> 16)));
     const float d1 = d * (float)sc, m1 = dmin * (float)mn;
