@@ -302,9 +302,11 @@ tl_hip_tensor* tl_hip_attention_decode(const tl_hip_tensor* q, const tl_hip_tens
                                        const tl_hip_tensor* v, int64_t L, float scale);
 /* Whether split kernels may merge their partial results inside the same launch, the
  * workgroup that finishes a unit last merging it (default 1): decode attention's split records
- * per (batch item, KV head), the short-input GEMM's K-split slices per tile.  0 selects the
- * second merge kernel.  Returns the previous setting.  Instrumentation for the parity tests,
- * which run both forms; no reference counterpart. */
+ * per (batch item, KV head), the short-input GEMMs' K-split slices per tile.  on = 0 selects
+ * the second merge kernel, 1 the one-launch form; both return the previous setting.  on < 0
+ * changes nothing and returns whether one-launch merges are in effect now (the setting is 1
+ * and no stream but the library's has run library work).  Instrumentation for the parity
+ * tests, which run both forms; no reference counterpart. */
 int tl_hip_debug_one_launch_merge(int on);
 /* Causal prefill attention over an f16 KV cache: the same chatbot chain for sl > 1 with the
  * causal mask (Tensor::new_causal_mask + add_4d, chatbot.tl:76-87), in one f16-MFMA kernel.

@@ -2,7 +2,8 @@
 tl_hip_launch_quant_gemm on the same inputs, called through the C ABI: calls in a row, each
 with a smaller input than the one before (64-row tiles with split-K partials in the scratch,
 then the short-input kernel), the size and type limits of its fixed scratch, and the entry
-under hipGraph capture."""
+under hipGraph capture, on the library stream (one-launch split-K sums) and on a caller
+stream."""
 import ctypes as C
 
 import numpy as np
@@ -98,6 +99,62 @@ def test_noalloc_gemm_limits(dev):
     assert lib.tl_hip_launch_quant_gemm_noalloc(h4, C.c_void_p(xt.data_ptr), C.c_void_p(yt2.data_ptr), 8, 1,
                                                 None) == 0
     assert np.array_equal(yt2.to_numpy(), want)
+
+
+def test_one_launch_gemm_under_capture_on_the_library_stream(dev):
+    """The allocation-free entry captured on the library's own stream, where K-split GEMMs add
+    their slices in the same launch (the tile's last-arriving split) while no other stream has
+    run library work: M = 16 (short-input kernel) and M = 48 (64-row tiles, after the X
+    conversion).  Every replay -- with a NaN fill of y and eager work between replays -- gives
+    the eager call's bits, and the graph holds one kernel node fewer when the one-launch form
+    is in effect than when the sum is a kernel of its own."""
+    lib = _lib.load()
+    hip = C.CDLL("libamdhip64.so.7")
+    rng = np.random.default_rng(0x71580300)
+    n, k = 4096, 4096
+    raw = random_q4_0_blocks(rng, n, k)
+    w = QTensor(GGML_Q4_0, raw, (n, k))   # kept alive: the handle below belongs to it
+    hw = w.upload(lib)
+    stream = C.c_void_p(lib.tl_hip_stream())
+    for m in (16, 48):
+        x = rng.standard_normal((m, k)).astype(np.float32)
+        want, plan = _run(dev, lib, lib.tl_hip_launch_quant_gemm, hw, x, n)
+        # K split 8 / 4 ways: within both kernels' one-launch limits (8 and 16 splits)
+        assert 1 < plan[2] <= 8, plan
+        one = lib.tl_hip_debug_one_launch_merge(-1) == 1
+        xt = dev.tensor_new(x)
+        yt = dev.tensor_new(np.zeros((m, n), np.float32))
+        args = (hw, C.c_void_p(xt.data_ptr), C.c_void_p(yt.data_ptr), m, 1, stream)
+        dev.synchronize()
+        graph, gexec = C.c_void_p(), C.c_void_p()
+        lib.tl_hip_debug_fail_alloc(0)
+        try:
+            assert hip.hipStreamBeginCapture(stream, 1) == 0   # thread-local mode
+            rc = lib.tl_hip_launch_quant_gemm_noalloc(*args)
+            assert hip.hipStreamEndCapture(stream, C.byref(graph)) == 0
+        finally:
+            lib.tl_hip_debug_fail_alloc(-1)
+        assert rc == 0, lib.tl_hip_last_error()
+        try:
+            nodes = C.c_size_t(0)
+            assert hip.hipGraphGetNodes(graph, None, C.byref(nodes)) == 0
+            base = 1 if m <= 16 else 2   # the X conversion precedes the tiled GEMM
+            assert nodes.value == base + (0 if one else 1), (m, one, nodes.value)
+            assert hip.hipGraphInstantiate(C.byref(gexec), graph, None, None, C.c_size_t(0)) == 0
+            nan = np.full((m, n), np.nan, np.float32)
+            for rep in range(3):
+                assert lib.tl_hip_memcpy_h2d(C.c_void_p(yt.data_ptr), nan.ctypes.data_as(C.c_void_p), nan.nbytes) == 0
+                dev.synchronize()
+                assert hip.hipGraphLaunch(gexec, stream) == 0
+                assert hip.hipStreamSynchronize(stream) == 0
+                got = yt.to_numpy()
+                assert np.array_equal(got.view(np.uint32), want.view(np.uint32)), f"m={m}: replay {rep} differs"
+                again, _ = _run(dev, lib, lib.tl_hip_launch_quant_gemm, hw, x, n)
+                assert np.array_equal(again.view(np.uint32), want.view(np.uint32))
+        finally:
+            if gexec.value:
+                hip.hipGraphExecDestroy(gexec)
+            hip.hipGraphDestroy(graph)
 
 
 def test_noalloc_gemm_under_graph_capture(dev):

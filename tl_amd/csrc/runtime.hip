@@ -286,7 +286,10 @@ int tl_hip_debug_fail_alloc(int64_t after) {
     return TL_HIP_OK;
 }
 
-int tl_hip_debug_one_launch_merge(int on) { return g_one_launch.exchange(on != 0) ? 1 : 0; }
+int tl_hip_debug_one_launch_merge(int on) {
+    if (on < 0) return single_stream() && one_launch_merge() ? 1 : 0;
+    return g_one_launch.exchange(on != 0) ? 1 : 0;
+}
 
 int tl_hip_synchronize(void) {
     if (!state()) return tls_status;
