@@ -198,6 +198,9 @@ int launch_mv(const QWeight* w, MvArgs a, int m, int epi, bool norm, bool embed,
 // workgroups (= argmax partial slots) of a matvec over n rows
 int mv_partials(int64_t n);
 bool matvec_fits(const QWeight* w, int64_t m);  // the LDS-staged matvec takes this product
+// One launch for the two weights of a q | k | v projection (RMSNorm prologue, RoPE + KV
+// epilogue): returns -1 without launching when the pair is not covered.
+int launch_mv_pair(const QWeight* w1, const QWeight* w2, MvArgs a, int64_t row_off2, bool embed, hipStream_t s);
 int launch_read_floor(const QWeight* w, hipStream_t s);  // read of w's arrays, matvec launch shape
 
 // kernel entry points shared across translation units (all on the given stream)

@@ -526,10 +526,18 @@ static int enqueue_step(Llama* m, float penalty, hipStream_t s) {
         a.hd = (int)hd;
         a.kv_f16 = m->kv_f16;
         a.max_seq = m->max_seq;
-        for (const Seg& sg : m->qkv_segs[l]) {
-            a.row_off = sg.row_off;
-            if ((rc = launch_mv(sg.w, a, 1, EPI_ROPE_KV, true, l == 0, s))) return rc;
+        // a projection in two weight types (Q4_K q | k with Q6_K v, llama.cpp's Q4_K_M) in one launch
+        rc = -1;
+        if (m->qkv_segs[l].size() == 2) {
+            a.row_off = m->qkv_segs[l][0].row_off;
+            rc = launch_mv_pair(m->qkv_segs[l][0].w, m->qkv_segs[l][1].w, a, m->qkv_segs[l][1].row_off, l == 0, s);
+            if (rc > 0) return rc;
         }
+        if (rc == -1)
+            for (const Seg& sg : m->qkv_segs[l]) {
+                a.row_off = sg.row_off;
+                if ((rc = launch_mv(sg.w, a, 1, EPI_ROPE_KV, true, l == 0, s))) return rc;
+            }
         // caches up to 4096 positions: ATTN_SHARES workgroups per query head (each a share of
         // the positions) in a single launch, their records merged by the o-projection as it
         // stages its input (the split form's merge launch costs more than it saves here)

@@ -217,11 +217,13 @@ __device__ __forceinline__ float4 merge_shares(const float4 (&o)[ATTN_SHARES], c
 // position of EPI_ROPE_KV; aux_i: the records' head dimension), and the shape.  The rest
 // travels in MvArgs; the compiler's scalar loads of those fields then overlap the weight
 // stream instead of holding back its first loads.
-template <int QT, int BT, int RWT, int M, int EPI, bool NORM, bool EMBED, bool MERGE = false>
-__global__ __launch_bounds__(512) void k_mv(const uint8_t* __restrict__ qs_p, const void* __restrict__ w1_p,
-                                            const float* __restrict__ x_p, const float* __restrict__ aux_p,
-                                            const int32_t* __restrict__ aux2_p, uint32_t n_p, uint32_t nb_p,
-                                            uint32_t shape_p, int aux_i, MvArgs a) {
+// The body runs as workgroup `bid` of its weight (k_mv: blockIdx.x; k_mv_pair: the index
+// within its segment).
+template <int QT, int BT, int RWT, int M, int EPI, bool NORM, bool EMBED, bool MERGE>
+__device__ __forceinline__ void mv_body(const uint8_t* __restrict__ qs_p, const void* __restrict__ w1_p,
+                                        const float* __restrict__ x_p, const float* __restrict__ aux_p,
+                                        const int32_t* __restrict__ aux2_p, uint32_t n_p, uint32_t nb_p,
+                                        uint32_t shape_p, int aux_i, MvArgs& a, const uint32_t bid) {
     constexpr int QB = QB_<QT>::v, QW = QB / 16;  // 16-byte loads per block
     constexpr int N = M * RWT;
     constexpr int RWT_SHIFT = RWT == 1 ? 0 : RWT == 2 ? 1 : RWT == 4 ? 2 : RWT == 8 ? 3 : 4;
@@ -254,7 +256,7 @@ __global__ __launch_bounds__(512) void k_mv(const uint8_t* __restrict__ qs_p, co
     const int sub = sh.s_shift ? __builtin_amdgcn_readfirstlane(tid >> sh.tc_shift) : 0;  // TC >= 64: uniform
     const int wps = TC >> 6;  // wavefronts per row subset
     const uint32_t nb = (uint32_t)a.nb, k = (uint32_t)a.k, n = (uint32_t)a.n;
-    const uint32_t row0 = blockIdx.x * (uint32_t)RW;
+    const uint32_t row0 = bid * (uint32_t)RW;
     const uint32_t my_row0 = row0 + sub;
 
     // epilogue operands, requested right after the first loads
@@ -471,7 +473,7 @@ __global__ __launch_bounds__(512) void k_mv(const uint8_t* __restrict__ qs_p, co
         load_w();
         auto stage = [&](int m, uint32_t e, float4 v, float4 g) {
             if constexpr (EMBED) {
-                if (blockIdx.x == 0 && a.x_out) reinterpret_cast<float4*>(a.x_out)[e] = v;
+                if (bid == 0 && a.x_out) reinterpret_cast<float4*>(a.x_out)[e] = v;
             }
             if constexpr (NORM) {
                 s2[m] = fmaf(v.x, v.x, fmaf(v.y, v.y, fmaf(v.z, v.z, fmaf(v.w, v.w, s2[m]))));
@@ -641,12 +643,42 @@ __global__ __launch_bounds__(512) void k_mv(const uint8_t* __restrict__ qs_p, co
             int bi = live ? lane : -1, nan = live && v != v;
             argmax_allreduce(bv, bi, nan);
             if (lane == 0) {
-                st_wt(a.part_v + blockIdx.x, bv);
-                st_wt(a.part_i + blockIdx.x, (int32_t)(row0 + bi));
-                st_wt(a.part_nan + blockIdx.x, (int32_t)nan);
+                st_wt(a.part_v + bid, bv);
+                st_wt(a.part_i + bid, (int32_t)(row0 + bi));
+                st_wt(a.part_nan + bid, (int32_t)nan);
             }
         }
     }
+}
+
+template <int QT, int BT, int RWT, int M, int EPI, bool NORM, bool EMBED, bool MERGE = false>
+__global__ __launch_bounds__(512) void k_mv(const uint8_t* __restrict__ qs_p, const void* __restrict__ w1_p,
+                                            const float* __restrict__ x_p, const float* __restrict__ aux_p,
+                                            const int32_t* __restrict__ aux2_p, uint32_t n_p, uint32_t nb_p,
+                                            uint32_t shape_p, int aux_i, MvArgs a) {
+    mv_body<QT, BT, RWT, M, EPI, NORM, EMBED, MERGE>(qs_p, w1_p, x_p, aux_p, aux2_p, n_p, nb_p, shape_p, aux_i, a,
+                                                     blockIdx.x);
+}
+
+// Two weights of one q | k | v projection in one launch (a layer whose q | k and v rows have
+// different types, as llama.cpp's Q4_K_M mixture gives 11 of 22 TinyLlama layers): workgroups
+// [0, grid1) run segment 1's matvec, the rest segment 2's, on the same staged input row
+// (RMSNorm prologue, RoPE + KV-append epilogue); segment 2's workgroup 0 does not store the
+// embedded row.  Both segments take the same workgroup size and K.
+template <int QT1, int RWT1, int QT2, int RWT2, bool EMBED>
+__global__ __launch_bounds__(512) void k_mv_pair(const uint8_t* __restrict__ qs_p, const void* __restrict__ w1_p,
+                                                 const float* __restrict__ x_p, const float* __restrict__ aux_p,
+                                                 const int32_t* __restrict__ aux2_p, uint32_t n_p, uint32_t nb_p,
+                                                 uint32_t shape_p, uint32_t grid1, MvArgs a, MvArgs a2,
+                                                 uint32_t shape2) {
+    if (blockIdx.x < grid1)
+        mv_body<QT1, 1, RWT1, 1, EPI_ROPE_KV, true, EMBED, false>(qs_p, w1_p, x_p, aux_p, aux2_p, n_p, nb_p, shape_p,
+                                                                  0, a, blockIdx.x);
+    else
+        mv_body<QT2, 1, RWT2, 1, EPI_ROPE_KV, true, EMBED, false>(
+            a2.qs, QT2 == TL_HIP_GGML_Q4_K ? (const void*)a2.hdr : QT2 == TL_HIP_GGML_Q6_K ? (const void*)a2.qh
+                                                                                          : (const void*)a2.d,
+            x_p, aux_p, aux2_p, (uint32_t)a2.n, nb_p, shape2, 0, a2, blockIdx.x - grid1);
 }
 
 // Greedy token from the per-workgroup candidates of an EPI_ARGMAX matvec (one workgroup):
@@ -866,6 +898,67 @@ int launch_mv(const QWeight* w, MvArgs a, int m, int epi, bool norm, bool embed,
         case TL_HIP_GGML_Q4_K: return run_t<TL_HIP_GGML_Q4_K>(a, m, epi, norm, embed, p, s);
         default: return run_t<TL_HIP_GGML_Q6_K>(a, m, epi, norm, embed, p, s);
     }
+}
+
+// One launch for a two-weight q | k | v projection (k_mv_pair): Q4_K rows, then Q6_K rows, or
+// the reverse, with the RMSNorm prologue and the RoPE + KV epilogue; a holds the shared
+// arguments and segment 1's row offset, row_off2 segment 2's.  Returns -1 without launching
+// when the pair is not covered (other types or plans, or the checks of launch_mv fail): the
+// caller then launches each weight on its own.
+int launch_mv_pair(const QWeight* w1, const QWeight* w2, MvArgs a, int64_t row_off2, bool embed, hipStream_t s) {
+    const int t1 = w1->ggml_type, t2 = w2->ggml_type;
+    const bool kq = (t1 == TL_HIP_GGML_Q4_K && t2 == TL_HIP_GGML_Q6_K) || (t1 == TL_HIP_GGML_Q6_K && t2 == TL_HIP_GGML_Q4_K);
+    if (!kq || w1->nb != w2->nb || w1->n % 2 || w2->n % 2 || (reinterpret_cast<uintptr_t>(a.x) & 15) ||
+        (reinterpret_cast<uintptr_t>(a.norm_w) & 15) || !a.norm_w)
+        return -1;
+    for (const QWeight* w : {w1, w2})
+        if ((uint64_t)w->n * w->nb * 16 >= (1ull << 31)) return -1;
+    if ((size_t)w1->nb * XPAD * sizeof(float) > 64 * 1024) return -1;  // default LDS limit: no attribute call
+    const MvPlan p1 = mv_plan(w1->n, w1->nb, t1), p2 = mv_plan(w2->n, w2->nb, t2);
+    if (p1.BT != 1 || p2.BT != 1 || p1.S * p1.TC != p2.S * p2.TC || p1.TC != p2.TC || (p1.RWT != 2 && p1.RWT != 4) ||
+        (p2.RWT != 2 && p2.RWT != 4))
+        return -1;
+    MvArgs a1 = a, b = a;
+    for (auto [ar, w] : {std::pair<MvArgs*, const QWeight*>{&a1, w1}, {&b, w2}}) {
+        ar->qs = w->qs;
+        ar->d = w->d;
+        ar->hdr = w->hdr;
+        ar->qh = w->qh;
+        ar->sc = w->sc;
+        ar->n = w->n;
+        ar->k = w->k;
+        ar->nb = w->nb;
+    }
+    b.row_off = row_off2;
+    b.x_out = nullptr;  // the embedded row is stored once, by segment 1
+    const size_t lds = (size_t)a.nb * XPAD * sizeof(float);
+    const unsigned grid = (unsigned)(p1.grid + p2.grid), threads = (unsigned)(p1.S * p1.TC);
+    const void* x1 = t1 == TL_HIP_GGML_Q4_K ? (const void*)a1.hdr : (const void*)a1.qh;
+    const int32_t* aux2 = embed ? a.embed_id : a.pos;
+    const uint32_t sh1 = p1.shape().pack(), sh2 = p2.shape().pack(), g1 = (uint32_t)p1.grid;
+#define TLH_PAIR(Q1, R1, Q2, R2)                                                                              \
+    if (t1 == Q1 && p1.RWT == R1 && p2.RWT == R2) {                                                            \
+        if (embed)                                                                                             \
+            k_mv_pair<Q1, R1, Q2, R2, true><<<grid, threads, lds, s>>>(a1.qs, x1, a.x, a.norm_w, aux2,           \
+                                                                      (uint32_t)a1.n, (uint32_t)a1.nb, sh1, g1,  \
+                                                                      a1, b, sh2);                               \
+        else                                                                                                   \
+            k_mv_pair<Q1, R1, Q2, R2, false><<<grid, threads, lds, s>>>(a1.qs, x1, a.x, a.norm_w, aux2,          \
+                                                                       (uint32_t)a1.n, (uint32_t)a1.nb, sh1, g1, \
+                                                                       a1, b, sh2);                              \
+        hipError_t e = hipGetLastError();                                                                      \
+        return e == hipSuccess ? TL_HIP_OK : hip_fail(e, "matvec pair launch");                                \
+    }
+    TLH_PAIR(TL_HIP_GGML_Q4_K, 2, TL_HIP_GGML_Q6_K, 2)
+    TLH_PAIR(TL_HIP_GGML_Q4_K, 4, TL_HIP_GGML_Q6_K, 2)
+    TLH_PAIR(TL_HIP_GGML_Q4_K, 2, TL_HIP_GGML_Q6_K, 4)
+    TLH_PAIR(TL_HIP_GGML_Q4_K, 4, TL_HIP_GGML_Q6_K, 4)
+    TLH_PAIR(TL_HIP_GGML_Q6_K, 2, TL_HIP_GGML_Q4_K, 2)
+    TLH_PAIR(TL_HIP_GGML_Q6_K, 4, TL_HIP_GGML_Q4_K, 2)
+    TLH_PAIR(TL_HIP_GGML_Q6_K, 2, TL_HIP_GGML_Q4_K, 4)
+    TLH_PAIR(TL_HIP_GGML_Q6_K, 4, TL_HIP_GGML_Q4_K, 4)
+#undef TLH_PAIR
+    return -1;
 }
 
 // Whether the LDS-staged matvec takes an m-row product with this weight (rows staged two at
