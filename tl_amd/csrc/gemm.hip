@@ -1119,7 +1119,11 @@ static F16qPlan plan_f16q(const QWeight* w, int64_t m, const GemmEpi& ep, const 
     // 27.1 -> 13.1 / 28.9 -> 21.7 us, 4096 x 11008 63.5 -> 22.0 / 70.6 -> 36.7 us per call
     // including the X conversion; splitting the 344 tiles of 11008 x 4096 in two at M = 128
     // was slower, 37.0 -> 44.7 us, and faster at M = 16, 23.6 -> 20.5 us.)
-    const int bm = wide ? BM : m <= 32 ? 32 : m <= 64 ? 64 : BM;
+    int bm = wide ? BM : m <= 32 ? 32 : m <= 64 ? 64 : BM;
+    // f16 weights on narrow tiles: 64-row tiles while 128-row ones would leave workgroup slots
+    // empty (Q4_K_M 512-token prefill -- its Q6_K parts -- 3.23 -> 3.10 ms; the 4-bit types
+    // measured slower that way, Q4_0 prefill 2.79 -> 2.84 ms)
+    if (f16w && !wide && bm == BM && cdiv(m, BM) * cdiv(w->n, 32) < 512) bm = 64;
     const int64_t tiles = cdiv(m, bm) * cdiv(w->n, bn);
     const int64_t iters = w->nb / Q_KR;
     int64_t nsp = 1;
