@@ -661,7 +661,7 @@ __global__ __launch_bounds__(512) void k_mv(const uint8_t* __restrict__ qs_p, co
 }
 
 // Two weights of one q | k | v projection in one launch (a layer whose q | k and v rows have
-// different types, as llama.cpp's Q4_K_M mixture gives 11 of 22 TinyLlama layers): workgroups
+// different types, as llama.cpp's Q4_K_M mixture gives 10 of 22 TinyLlama layers): workgroups
 // [0, grid1) run segment 1's matvec, the rest segment 2's, on the same staged input row
 // (RMSNorm prologue, RoPE + KV-append epilogue); segment 2's workgroup 0 does not store the
 // embedded row.  Both segments take the same workgroup size and K.
