@@ -395,18 +395,25 @@ def test_f16_prefill_weight_mixtures(plan):
         cpu.close()
 
 
+def _q6_qk_plan(cfg, layer, which):
+    # q | k in Q6_K and v in Q4_K: a two-type q | k | v projection with the Q6_K rows first
+    return {"attn_q": 14, "attn_k": 14, "attn_v": 12}.get(which, 12)
+
+
 def _mixed_plan(cfg, layer, which):
     # every grouping case of the loader: q | k | v in three runs, gate and up of different types
     return {"attn_q": 14, "attn_k": 12, "attn_v": 14, "ffn_gate": 14, "ffn_up": 12}.get(which, 12)
 
 
-@pytest.mark.parametrize("plan", ["Q4_K_M", "mixed"])
+@pytest.mark.parametrize("plan", ["Q4_K_M", "mixed", "q6_qk"])
 def test_kquant_model_logits_and_tokens(plan):
     """K-quant weights through the whole decoder: llama.cpp's Q4_K_M mixture (Q4_K with Q6_K
-    attn_v / ffn_down in some layers and the LM head) and a plan with q/k/v and gate/up of
-    different types.  f32 logits within 1e-4 and identical greedy tokens, graph and eager."""
+    attn_v / ffn_down in some layers and the LM head: the decode step's q | k and v rows in
+    one two-type launch), a plan with q/k/v and gate/up of different types (three q | k | v
+    runs: one launch each), and Q6_K q | k with a Q4_K v (the two-type launch the other way
+    round).  f32 logits within 1e-4 and identical greedy tokens, graph and eager."""
     cfg = LlamaConfig(4, 256, 4, 2, 512, 1000, max_seq=128)
-    gt = "Q4_K_M" if plan == "Q4_K_M" else _mixed_plan
+    gt = {"Q4_K_M": "Q4_K_M", "mixed": _mixed_plan, "q6_qk": _q6_qk_plan}[plan]
     tensors = list(synthetic_weights(cfg, 31, ggml_type=gt))
     gpu = HipLlama(cfg)
     gpu.load(tensors, ggml_type=gt)
