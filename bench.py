@@ -50,11 +50,13 @@ def matvec_bytes(t, n=MATVEC_N, k=MATVEC_K):
     return n * k // per[0] * per[1] + k * 4 + n * 4
 
 
-def bench_matvec(dev, t=2, launches=340, min_bytes=320 << 20, n=MATVEC_N, k=MATVEC_K, floor=False):
+def bench_matvec(dev, t=2, launches=340, min_bytes=320 << 20, n=MATVEC_N, k=MATVEC_K, floor=False, blocks=1):
     """Average seconds of one n x k matvec (m = 1, default 4096 x 4096) of GGML type t,
     launched back to back over enough resident weight copies (>= 320 MB) that the 256 MB
     Infinity Cache cannot serve them.  floor=True times tl_hip_read_floor instead: the same
-    launch shape and copies, reading the weight bytes and computing nothing."""
+    launch shape and copies, reading the weight bytes and computing nothing.  blocks > 1:
+    that many timed blocks of `launches` launches, each behind its own stall; returns the
+    list of the blocks' per-launch averages."""
     import ctypes as C
 
     from tl_amd import QTensor
@@ -81,21 +83,23 @@ def bench_matvec(dev, t=2, launches=340, min_bytes=320 << 20, n=MATVEC_N, k=MATV
             raise RuntimeError(lib.tl_hip_last_error())
     dev.synchronize()
     e0, e1 = lib.tl_hip_event_create(), lib.tl_hip_event_create()
-    # the stall keeps the GPU busy while the host enqueues every timed launch, so the events
-    # measure back-to-back GPU execution, not the host's launch rate
-    lib.tl_hip_stall(20000)
-    lib.tl_hip_event_record(e0)
-    for i in range(launches):
-        launch(i)
-    lib.tl_hip_event_record(e1)
-    ms = C.c_float()
-    lib.tl_hip_event_elapsed_ms(e0, e1, C.byref(ms))
+    per = []
+    for _ in range(blocks):
+        # the stall keeps the GPU busy while the host enqueues every timed launch, so the
+        # events measure back-to-back GPU execution, not the host's launch rate
+        lib.tl_hip_stall(20000)
+        lib.tl_hip_event_record(e0)
+        for i in range(launches):
+            launch(i)
+        lib.tl_hip_event_record(e1)
+        ms = C.c_float()
+        lib.tl_hip_event_elapsed_ms(e0, e1, C.byref(ms))
+        per.append(ms.value / 1e3 / launches)
     lib.tl_hip_event_destroy(e0)
     lib.tl_hip_event_destroy(e1)
-    avg_s = ms.value / 1e3 / launches
     for w in ws:
         w.release()
-    return avg_s
+    return per if blocks > 1 else per[0]
 
 
 def bench_quant_matvec(dev):
@@ -124,6 +128,7 @@ def bench_matvec_shapes(dev):
 
 
 MFMA_F16_PEAK_TFLOPS = 2500.0
+ROOFLINE_BLOCKS = 9  # timed blocks of the roofline matvec (their per-launch averages give p10 / median / p90)
 GEMM_SHAPES = [(4096, 4096), (11008, 4096), (4096, 11008)]  # configs[2] (N, K), M = 512
 ATTN_CASES = [(512, 1), (2048, 1), (8192, 1), (512, 8), (2048, 8), (8192, 8)]  # configs[3] (L, B)
 
@@ -648,9 +653,14 @@ def main():
         return
 
     log("[bench] Q4_0 4096x4096 matvec roofline ...")
-    avg_s = bench_matvec(dev)
+    blocks_s = bench_matvec(dev, blocks=ROOFLINE_BLOCKS)
+    avg_s = float(np.mean(blocks_s))  # every block has the same launch count: the mean per launch
+    spread = {"blocks": ROOFLINE_BLOCKS, "launches_per_block": 340,
+              **{f"{name}_us": round(float(np.percentile(blocks_s, q)) * 1e6, 3)
+                 for name, q in (("p10", 10), ("median", 50), ("p90", 90))}}
     achieved = MATVEC_BYTES / avg_s / 1e9
-    log(f"[bench] matvec avg {avg_s * 1e6:.2f} us -> {achieved:.0f} GB/s")
+    log(f"[bench] matvec avg {avg_s * 1e6:.2f} us -> {achieved:.0f} GB/s; per-block p10 / median / p90 "
+        f"{spread['p10_us']:.3f} / {spread['median_us']:.3f} / {spread['p90_us']:.3f} us")
     floor_s = bench_matvec(dev, floor=True)
     log(f"[bench] read floor (the matvec's loads only, same copies) {floor_s * 1e6:.2f} us -> "
         f"{MATVEC_BYTES / floor_s / 1e9:.0f} GB/s")
@@ -734,6 +744,7 @@ def main():
             "traffic_source": "not measured in this run: FETCH_SIZE + WRITE_SIZE counter runs of "
                               "`bench.py --matvec-only` (profiles/q4_0_matvec_4096x4096.md)",
             "avg_launch_us": round(avg_s * 1e6, 3),
+            "launch_spread": spread,
             "floor_us": round(floor_s * 1e6, 3),
             "floor_note": "tl_hip_read_floor: the matvec's own loads (launch plan, access pattern, quant bytes + "
                           "scales) over the same weight copies, with no math, reduction or store",

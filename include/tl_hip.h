@@ -345,6 +345,12 @@ int tl_hip_llama_load_gguf(tl_hip_llama* m, tl_hip_gguf* g);
  * start position, chatbot.tl:56-61 + ffi.rs:2655-2681; 1 = token t at start + t).  Resets the
  * cache. */
 int tl_hip_llama_configure(tl_hip_llama* m, int kv_f16, int rope_per_token);
+/* Whether the decoder's f16 prefill applies RoPE and the KV-cache append in the epilogue of
+ * the [q | k | v] projection GEMM (default 1) or in a separate kernel after a plain GEMM (0);
+ * the same values either way.  Returns the previous setting; on < 0 changes nothing and
+ * returns the current one.  Instrumentation for the parity tests, which run both forms; no
+ * reference counterpart. */
+int tl_hip_debug_prefill_rope_epilogue(int on);
 /* KVCache::new / free (system.rs:387-454): empties the cache. */
 int tl_hip_llama_reset(tl_hip_llama* m);
 /* Number of cached positions (the chatbot's start_pos for the next call). */

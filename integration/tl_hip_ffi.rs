@@ -278,6 +278,7 @@ extern "C" {
         scale: f32,
     ) -> *mut tl_hip_tensor;
     pub fn tl_hip_debug_one_launch_merge(on: i32) -> i32;
+    pub fn tl_hip_debug_prefill_rope_epilogue(on: i32) -> i32;
     pub fn tl_hip_attention_prefill(
         q: *const tl_hip_tensor,
         k: *const tl_hip_tensor,

@@ -362,6 +362,51 @@ def test_tinyllama_greedy_golden():
                     f"near the f16 logit error, ~1e-3)")
 
 
+_ROPE_EPI_SMALL = LlamaConfig(2, 512, 8, 1, 512, 1000, max_seq=256)
+_ROPE_EPI_WIDE = LlamaConfig(1, 2048, 32, 4, 5632, 1000, max_seq=640)
+
+
+@pytest.mark.parametrize("case", ["21-f16", "21-f32-per-token", "77-f16-per-token", "77-f32", "512-wide-f16"])
+def test_f16_prefill_rope_epilogue_matches_rope_kernel(case):
+    """The f16 prefill's RoPE and KV append in the [q | k | v] GEMM's epilogue against the
+    separate RoPE / KV kernel after a plain GEMM: bitwise the same prefill logits and the same
+    logits of a decode step after it (which reads every cache row the prefill wrote).  21
+    tokens: 32-row tiles whose last-arriving K split adds the slices and applies RoPE; 77:
+    128-row tiles with K split, the sum launch applying it; 512 at TinyLlama's width: 320
+    unsplit tiles, the GEMM itself applying it.  f16 and f32 caches, both RoPE position rules."""
+    n, kv = int(case.split("-")[0]), "f16" in case
+    cfg = _ROPE_EPI_WIDE if "wide" in case else _ROPE_EPI_SMALL
+    tensors = list(synthetic_weights(cfg, 53))
+    gpu = HipLlama(cfg, kv_f16=kv)
+    gpu.load(tensors)
+    lib = gpu.lib
+    prev = lib.tl_hip_debug_prefill_rope_epilogue(1)
+    try:
+        gpu.configure(kv_f16=kv, rope_per_token="per-token" in case)
+        prompt = synthetic_prompt(cfg, 53, n)
+        got = {}
+        for on in (1, 0):
+            lib.tl_hip_debug_prefill_rope_epilogue(on)
+            gpu.reset()
+            pre = gpu.forward(prompt, prefill_f16=True)
+            dec = gpu.forward([7])
+            got[on] = (pre, dec)
+        for a, b, what in ((got[1][0], got[0][0], "prefill"), (got[1][1], got[0][1], "decode after the prefill")):
+            assert np.array_equal(a.view(np.uint32), b.view(np.uint32)), f"{what}: max-rel {max_rel(a, b):.2e}"
+        if case == "21-f16":  # and within the f16 tolerance of the oracle (its RoPE position rule)
+            cpu = oracle.Llama(cfg)
+            cpu.load(tensors)
+            try:
+                cpu.reset()
+                err = max_rel(got[1][0], cpu.forward(prompt))
+                assert err <= 1e-2, f"f16 prefill logits max-rel-err {err:.2e}"
+            finally:
+                cpu.close()
+    finally:
+        lib.tl_hip_debug_prefill_rope_epilogue(prev)
+        gpu.close()
+
+
 def _q8_handoff_plan(cfg, layer, which):
     # each f16 GEMM input written in the operand order of its reader: Q8_0 and Q4_0 alternate
     return {"attn_q": 8, "attn_k": 8, "attn_v": 8, "attn_output": 2, "ffn_gate": 8, "ffn_up": 8,

@@ -103,6 +103,7 @@ PROTOS = {
     "tl_hip_tensor_scaled_dot_product_attention": (P, [P, P, P, P]),
     "tl_hip_attention_decode": (P, [P, P, P, i64, f32]),
     "tl_hip_debug_one_launch_merge": (i32, [i32]),
+    "tl_hip_debug_prefill_rope_epilogue": (i32, [i32]),
     "tl_hip_attention_prefill": (P, [P, P, P, i64, f32]),
     "tl_hip_llama_new": (P, [i32, i32, i32, i32, i32, i32, f32, f32, i32]),
     "tl_hip_llama_free": (i32, [P]),

@@ -517,6 +517,7 @@ __global__ __launch_bounds__(512) void k_qgemm_mfma(const uint8_t* __restrict__ 
             if (!owns(i, j)) *reinterpret_cast<floatx4*>(red + (i * TN + j) * 256 + lane * 4) = acc[i][j];
     __syncthreads();
     {
+        const int64_t rpos = !FUSE && ep.mode == GEMM_ROPE_KV ? (int64_t)*ep.rk.pos : 0;
 #pragma unroll
         for (int i = 0; i < TM; i++)
 #pragma unroll
@@ -536,6 +537,11 @@ __global__ __launch_bounds__(512) void k_qgemm_mfma(const uint8_t* __restrict__ 
                             const float a = (v * (1.0f / (1.0f + expf(-v)))) * u;  // silu(gate) * up
                             ep.out16[f16q_index(r, c >> 1, n >> 1, ep.order)] = (_Float16)a;
                         }
+                    } else if (!FUSE && ep.mode == GEMM_ROPE_KV) {
+                        // RoPE pairs (2i, 2i + 1) sit in lanes col, col ^ 1 as above
+                        const float u = __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(
+                                                                      __builtin_bit_cast(int, v), 0xB1, 0xF, 0xF, true));
+                        if (r < m && c < n) rope_kv_store(ep.rk, r, c, rpos, (col & 1) ? u : v, (col & 1) ? v : u, v);
                     } else if (r < m && c < n) {
                         if constexpr (FUSE)
                             __hip_atomic_store(reinterpret_cast<uint32_t*>(yb + r * n + c), __float_as_uint(v),
@@ -562,6 +568,7 @@ __global__ __launch_bounds__(512) void k_qgemm_mfma(const uint8_t* __restrict__ 
         if (!s_last) return;  // uniform per workgroup
         const int64_t mn = m * n;
         const __amdgpu_buffer_rsrc_t rp = buf_rsrc(y, (uint32_t)(nsp * mn * 4));
+        const int64_t rpos = ep.mode == GEMM_ROPE_KV ? (int64_t)*ep.rk.pos : 0;
         constexpr int UPR = BN / 4;  // 4-column units per tile row
         for (int u = threadIdx.x; u < BM * UPR; u += 512) {
             const int64_t r = m0 + u / UPR, c = n0 + 4 * (u % UPR);
@@ -583,7 +590,14 @@ __global__ __launch_bounds__(512) void k_qgemm_mfma(const uint8_t* __restrict__ 
                     v.z = on ? v.z + __uint_as_float(t[p].z) : v.z;
                     v.w = on ? v.w + __uint_as_float(t[p].w) : v.w;
                 }
-                *reinterpret_cast<float4*>(fin + r * n + c) = v;
+                if (ep.mode == GEMM_ROPE_KV) {  // a unit holds two whole pairs
+                    rope_kv_store(ep.rk, r, c, rpos, v.x, v.y, v.x);
+                    rope_kv_store(ep.rk, r, c + 1, rpos, v.x, v.y, v.y);
+                    rope_kv_store(ep.rk, r, c + 2, rpos, v.z, v.w, v.z);
+                    rope_kv_store(ep.rk, r, c + 3, rpos, v.z, v.w, v.w);
+                } else {
+                    *reinterpret_cast<float4*>(fin + r * n + c) = v;
+                }
             }
         }
     }
@@ -1074,6 +1088,27 @@ __global__ __launch_bounds__(256) void k_splitk_sum(const float* __restrict__ pa
     }
 }
 
+// k_splitk_sum's sums (slice order, from 0) of a [q | k | v] projection, then RoPE and the
+// KV append (the GEMM's ROPE_KV epilogue) instead of the store: n % 4 == 0, so a 4-column
+// unit holds two whole pairs of one token row.
+__global__ __launch_bounds__(256) void k_splitk_sum_rope(const float* __restrict__ part, int64_t mn, int64_t n,
+                                                         int nsp, RopeKvEpi rk) {
+    const int64_t i = ((int64_t)blockIdx.x * 256 + threadIdx.x) * 4;
+    if (i >= mn) return;
+    float4 v{0.f, 0.f, 0.f, 0.f};
+    for (int p = 0; p < nsp; p++) {
+        const float4 t = *reinterpret_cast<const float4*>(part + p * mn + i);
+        v.x += t.x;
+        v.y += t.y;
+        v.z += t.z;
+        v.w += t.w;
+    }
+    const int64_t r = i / n, c = i % n, pos = *rk.pos;
+    rope_kv_store(rk, r, c, pos, v.x, v.y, v.x);
+    rope_kv_store(rk, r, c + 1, pos, v.x, v.y, v.y);
+    rope_kv_store(rk, r, c + 2, pos, v.z, v.w, v.z);
+    rope_kv_store(rk, r, c + 3, pos, v.z, v.w, v.w);
+}
 
 namespace {
 // Launch plan of one f16 GEMM: row tile bm, column tile bn (128 x 96 or 128 x 64 wide tiles,
@@ -1157,6 +1192,12 @@ int launch_gemm_f16q(const QWeight* w, const _Float16* x16, float* y, int64_t m,
                   "of 64)");
         return TL_HIP_ERR_ARG;
     }
+    if (ep.mode == GEMM_ROPE_KV && (ep.rk.hd < 4 || ep.rk.hd % 4 || w->n != (int64_t)(ep.rk.H + 2 * ep.rk.KV) * ep.rk.hd ||
+                                   !ep.rk.q || !ep.rk.kc || !ep.rk.vc || !ep.rk.ct || !ep.rk.st || !ep.rk.pos)) {
+        set_error(TL_HIP_ERR_ARG, "ArgumentError: the RoPE / KV epilogue takes [q | k | v] rows of whole heads "
+                  "(head size a multiple of 4) and every output");
+        return TL_HIP_ERR_ARG;
+    }
     const bool needs_w16 = (w->ggml_type == TL_HIP_GGML_Q4_K && !w->us) || w->ggml_type == TL_HIP_GGML_Q6_K;
     if (noalloc && needs_w16) {
         set_error(TL_HIP_ERR_ARG, "ArgumentError: a %s weight needs an f16 copy for the MFMA GEMM, which the "
@@ -1180,7 +1221,9 @@ int launch_gemm_f16q(const QWeight* w, const _Float16* x16, float* y, int64_t m,
     // residual next adds the slices with a workgroup per row (512-token prefill 2.83 ms
     // against 2.89 ms with the in-kernel sum; 32 tokens 1.30 -> 1.21 ms with it).
     const bool fuse = f16q_fuse_ok(w, m, bm, bn, tiles, nsp, ep);
-    const bool defer = defer_part && nsp > 1 && !noalloc && !fuse;
+    // (the RoPE / KV epilogue is applied by the kernel that forms the sums: the GEMM, the
+    // tile's last split, or k_splitk_sum_rope -- never left to the caller)
+    const bool defer = defer_part && nsp > 1 && !noalloc && !fuse && ep.mode != GEMM_ROPE_KV;
     if (defer_part) {
         *defer_part = nullptr;
         *defer_nsp = 1;
@@ -1213,8 +1256,11 @@ int launch_gemm_f16q(const QWeight* w, const _Float16* x16, float* y, int64_t m,
         else k_qgemm_mfma<QT, BM, 32><<<grid, 512, 0, s>>>(q, d, x16, out, m, w->n, w->k, w->nb, pe);
         if (nsp > 1 && !defer && !fuse) {
             const int64_t mn = m * w->n;
-            k_splitk_sum<<<(unsigned)cdiv(cdiv(mn, 4), 256), 256, 0, s>>>(
-                part, y, ep.mode == GEMM_RES ? ep.res : nullptr, mn, (int)nsp);
+            if (ep.mode == GEMM_ROPE_KV)
+                k_splitk_sum_rope<<<(unsigned)cdiv(mn / 4, 256), 256, 0, s>>>(part, mn, w->n, (int)nsp, ep.rk);
+            else
+                k_splitk_sum<<<(unsigned)cdiv(cdiv(mn, 4), 256), 256, 0, s>>>(
+                    part, y, ep.mode == GEMM_RES ? ep.res : nullptr, mn, (int)nsp);
         }
     };
     if (w->ggml_type == TL_HIP_GGML_Q4_K && w->us) {

@@ -340,15 +340,63 @@ __device__ __forceinline__ void argmax_allreduce(float& bv, int& bi, int& nan) {
 }
 
 enum { F16Q_Q4 = 0, F16Q_Q8 = 1 };
-enum { GEMM_PLAIN = 0, GEMM_RES = 1, GEMM_GLU16 = 2 };
+enum { GEMM_PLAIN = 0, GEMM_RES = 1, GEMM_GLU16 = 2, GEMM_ROPE_KV = 3 };
+// RoPE of one interleaved pair (x0, x1) by (c, s): (x0 c - x1 s, x0 s + x1 c) with the
+// contraction spelled out, so the prefill's RoPE kernel and the GEMM epilogue round alike.
+__host__ __device__ inline void rope_pair(float x0, float x1, float c, float s, float* r0, float* r1) {
+    *r0 = fmaf(x0, c, -(x1 * s));
+    *r1 = fmaf(x0, s, x1 * c);
+}
+// Operands of the ROPE_KV epilogue: the GEMM's rows are tokens pos .. pos + m - 1 and its
+// columns [q | k | v] (H + 2 KV heads of hd); q is rotated into q [m, H hd], k rotated and v
+// copied into the caches [KV][max_seq][hd] (f16 when kv_f16, else f32) at slot pos + row.
+// Table row pos + row (per_token) or pos of ct / st [*, hd] (entries 2i, 2i + 1 alike).
+struct RopeKvEpi {
+    float* q = nullptr;
+    void* kc = nullptr;
+    void* vc = nullptr;
+    const float* ct = nullptr;
+    const float* st = nullptr;
+    const int32_t* pos = nullptr;
+    int H = 0, KV = 0, hd = 0, per_token = 0, kv_f16 = 0;
+    int64_t max_seq = 0;
+};
 // Epilogue: PLAIN y = v; RES y = res + v (res may be y); GLU16 columns (2i, 2i + 1) are
-// (gate_i, up_i) and silu(gate_i) * up_i goes to out16 [m, n / 2] in operand order `order`.
+// (gate_i, up_i) and silu(gate_i) * up_i goes to out16 [m, n / 2] in operand order `order`;
+// ROPE_KV: RoPE and the KV-cache append of a [q | k | v] projection (rk), y not written.
 struct GemmEpi {
     int mode;
     const float* res;
     _Float16* out16;
     int order;
+    RopeKvEpi rk{};
 };
+// The ROPE_KV epilogue's store of column c (of n = (H + 2 KV) hd) of token row r: pair
+// values (x0, x1) of the column's interleaved pair, v the column's own value.
+// (Column indices and head sizes are 32-bit: n < 2^31.)
+__device__ inline void rope_kv_store(const RopeKvEpi& rk, int64_t r, int64_t c64, int64_t pos, float x0, float x1,
+                                     float v) {
+    const uint32_t c = (uint32_t)c64, hd = (uint32_t)rk.hd, qw = (uint32_t)rk.H * hd, kw = (uint32_t)rk.KV * hd;
+    if (c < qw + kw) {
+        const uint32_t i = c % hd;
+        const int64_t ti = (rk.per_token ? pos + r : pos) * hd + (i & ~1u);
+        float r0, r1;
+        rope_pair(x0, x1, rk.ct[ti], rk.st[ti], &r0, &r1);
+        const float o = (i & 1) ? r1 : r0;
+        if (c < qw) {
+            rk.q[r * qw + c] = o;
+        } else {
+            const int64_t at = ((int64_t)((c - qw) / hd) * rk.max_seq + pos + r) * hd + i;
+            if (rk.kv_f16) static_cast<__half*>(rk.kc)[at] = __float2half(o);
+            else static_cast<float*>(rk.kc)[at] = o;
+        }
+    } else {
+        const uint32_t vi = c - qw - kw;
+        const int64_t at = ((int64_t)(vi / hd) * rk.max_seq + pos + r) * hd + vi % hd;
+        if (rk.kv_f16) static_cast<__half*>(rk.vc)[at] = __float2half(v);
+        else static_cast<float*>(rk.vc)[at] = v;
+    }
+}
 __host__ __device__ inline int64_t f16q_index(int64_t r, int64_t e, int64_t k, int order) {
     const int64_t b = e >> 5;
     const int e32 = (int)(e & 31);

@@ -64,8 +64,8 @@ __global__ void k_rope_kv(const float* __restrict__ qkv, float* __restrict__ qou
         const int i = idx % hd;  // pair start within the head vector
         float c = ct[trow * hd + i], s = st[trow * hd + i];
         float x0 = src[idx], x1 = src[idx + 1];
-        float r0 = x0 * c - x1 * s;
-        float r1 = x0 * s + x1 * c;
+        float r0, r1;
+        rope_pair(x0, x1, c, s, &r0, &r1);
         if (idx < H * hd) {
             qout[(int64_t)tok * H * hd + idx] = r0;
             qout[(int64_t)tok * H * hd + idx + 1] = r1;
@@ -333,6 +333,10 @@ static int check_ready(Llama* m) {
     return TL_HIP_OK;
 }
 
+// Whether the f16 prefill applies RoPE and the KV append in the qkv GEMM's epilogue (one
+// [q | k | v] weight) rather than in k_rope_kv after a plain GEMM: the same values either way.
+static std::atomic<bool> g_rope_epilogue{true};
+
 // RoPE on the q|k rows of n tokens and the k / v append at the device position (prefill).
 static void prefill_rope_kv(Llama* m, int l, int n, hipStream_t s) {
     const int64_t hd = m->hd;
@@ -418,16 +422,33 @@ static int prefill_layer_fused(Llama* m, int l, int n, hipStream_t s, Pending& p
     if (pend.part) dev_free_on(pend.part, s);
     pend = Pending{};
     if (rc) return rc;
-    if (m->qkv_segs[l].size() == 1) {
+    if (m->qkv_segs[l].size() == 1 && g_rope_epilogue.load(std::memory_order_relaxed)) {
+        // one [q | k | v] weight: RoPE and the KV append ride in the GEMM epilogue
+        GemmEpi rope{GEMM_ROPE_KV, nullptr, nullptr, 0};
+        rope.rk.q = m->q;
+        rope.rk.kc = m->kc[l];
+        rope.rk.vc = m->vc[l];
+        rope.rk.ct = m->cos_t;
+        rope.rk.st = m->sin_t;
+        rope.rk.pos = m->pos;
+        rope.rk.H = m->H;
+        rope.rk.KV = m->KV;
+        rope.rk.hd = (int)m->hd;
+        rope.rk.per_token = m->rope_per_token;
+        rope.rk.kv_f16 = m->kv_f16 ? 1 : 0;
+        rope.rk.max_seq = m->max_seq;
+        if ((rc = gemm16(m->qkv_segs[l][0].w, m->xa16, m->qkv, n, rope, s))) return rc;
+    } else if (m->qkv_segs[l].size() == 1) {
         if ((rc = gemm16(m->qkv_segs[l][0].w, m->xa16, m->qkv, n, plain, s))) return rc;
+        prefill_rope_kv(m, l, n, s);
     } else {
         for (const Seg& sg : m->qkv_segs[l]) {  // each segment's columns of the [n, qkv_w] rows
             if ((rc = gemm16(sg.w, m->xa16, m->gu, n, plain, s))) return rc;
             TLH_CHECK_HIP(hipMemcpy2DAsync(m->qkv + sg.row_off, qkv_w * 4, m->gu, sg.w->n * 4, sg.w->n * 4, n,
                                            hipMemcpyDeviceToDevice, s));
         }
+        prefill_rope_kv(m, l, n, s);
     }
-    prefill_rope_kv(m, l, n, s);
     if ((rc = prefill_attention(m, l, n, 1, m->xa16, f16q_order(m->wo[l]->ggml_type), s))) return rc;
     Pending op;
     if ((rc = gemm16(m->wo[l], m->xa16, m->x, n, res, s, &op))) return rc;
@@ -867,6 +888,11 @@ int tl_hip_llama_load_gguf(tl_hip_llama* h, tl_hip_gguf* g) {
     tl_hip_tensor_release(e);
     if (err != hipSuccess) return hip_fail(err, "embedding copy");
     return TL_HIP_OK;
+}
+
+int tl_hip_debug_prefill_rope_epilogue(int on) {
+    if (on < 0) return g_rope_epilogue.load() ? 1 : 0;
+    return g_rope_epilogue.exchange(on != 0) ? 1 : 0;
 }
 
 int tl_hip_llama_configure(tl_hip_llama* h, int kv_f16, int rope_per_token) {
