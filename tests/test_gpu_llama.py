@@ -366,19 +366,28 @@ _ROPE_EPI_SMALL = LlamaConfig(2, 512, 8, 1, 512, 1000, max_seq=256)
 _ROPE_EPI_WIDE = LlamaConfig(1, 2048, 32, 4, 5632, 1000, max_seq=640)
 
 
-@pytest.mark.parametrize("case", ["21-f16", "21-f32-per-token", "77-f16-per-token", "77-f32", "512-wide-f16"])
+def _three_qkv_plan(cfg, layer, which):
+    # q | k | v in three weights (Q6_K, Q4_K, Q6_K), gate and up alike: a fused prefill layer
+    return {"attn_q": 14, "attn_k": 12, "attn_v": 14}.get(which, 12)
+
+
+@pytest.mark.parametrize("case", ["21-f16", "21-f32-per-token", "77-f16-per-token", "77-f32", "512-wide-f16",
+                                  "21-f16-q6qk", "77-f32-q6qk", "21-f16-three", "77-f16-per-token-three"])
 def test_f16_prefill_rope_epilogue_matches_rope_kernel(case):
     """The f16 prefill's RoPE and KV append in the [q | k | v] GEMM's epilogue against the
     separate RoPE / KV kernel after a plain GEMM: bitwise the same prefill logits and the same
     logits of a decode step after it (which reads every cache row the prefill wrote).  21
     tokens: 32-row tiles whose last-arriving K split adds the slices and applies RoPE; 77:
     128-row tiles with K split, the sum launch applying it; 512 at TinyLlama's width: 320
-    unsplit tiles, the GEMM itself applying it.  f16 and f32 caches, both RoPE position rules."""
+    unsplit tiles, the GEMM itself applying it.  f16 and f32 caches, both RoPE position rules;
+    Q4_0 weights, and K-quant q | k | v projections stored as two weights (Q6_K q | k, Q4_K v)
+    or three, each GEMM rotating and appending its own heads."""
     n, kv = int(case.split("-")[0]), "f16" in case
     cfg = _ROPE_EPI_WIDE if "wide" in case else _ROPE_EPI_SMALL
-    tensors = list(synthetic_weights(cfg, 53))
+    gt = _q6_qk_plan if case.endswith("q6qk") else _three_qkv_plan if case.endswith("three") else 2
+    tensors = list(synthetic_weights(cfg, 53, ggml_type=gt))
     gpu = HipLlama(cfg, kv_f16=kv)
-    gpu.load(tensors)
+    gpu.load(tensors, ggml_type=gt)
     lib = gpu.lib
     prev = lib.tl_hip_debug_prefill_rope_epilogue(1)
     try:

@@ -1192,10 +1192,12 @@ int launch_gemm_f16q(const QWeight* w, const _Float16* x16, float* y, int64_t m,
                   "of 64)");
         return TL_HIP_ERR_ARG;
     }
-    if (ep.mode == GEMM_ROPE_KV && (ep.rk.hd < 4 || ep.rk.hd % 4 || w->n != (int64_t)(ep.rk.H + 2 * ep.rk.KV) * ep.rk.hd ||
-                                   !ep.rk.q || !ep.rk.kc || !ep.rk.vc || !ep.rk.ct || !ep.rk.st || !ep.rk.pos)) {
-        set_error(TL_HIP_ERR_ARG, "ArgumentError: the RoPE / KV epilogue takes [q | k | v] rows of whole heads "
-                  "(head size a multiple of 4) and every output");
+    if (ep.mode == GEMM_ROPE_KV &&
+        (ep.rk.hd < 4 || ep.rk.hd % 4 || ep.rk.col_off < 0 || ep.rk.col_off % ep.rk.hd || w->n % ep.rk.hd ||
+         ep.rk.col_off + w->n > (int64_t)(ep.rk.H + 2 * ep.rk.KV) * ep.rk.hd || !ep.rk.q || !ep.rk.kc || !ep.rk.vc ||
+         !ep.rk.ct || !ep.rk.st || !ep.rk.pos)) {
+        set_error(TL_HIP_ERR_ARG, "ArgumentError: the RoPE / KV epilogue takes whole heads of [q | k | v] (head size "
+                  "a multiple of 4) and every output");
         return TL_HIP_ERR_ARG;
     }
     const bool needs_w16 = (w->ggml_type == TL_HIP_GGML_Q4_K && !w->us) || w->ggml_type == TL_HIP_GGML_Q6_K;

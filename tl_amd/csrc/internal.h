@@ -348,7 +348,8 @@ __host__ __device__ inline void rope_pair(float x0, float x1, float c, float s, 
     *r1 = fmaf(x0, s, x1 * c);
 }
 // Operands of the ROPE_KV epilogue: the GEMM's rows are tokens pos .. pos + m - 1 and its
-// columns [q | k | v] (H + 2 KV heads of hd); q is rotated into q [m, H hd], k rotated and v
+// columns are columns col_off .. of [q | k | v] (H + 2 KV heads of hd; col_off a multiple of
+// hd: a weight holding some of the heads); q is rotated into q [m, H hd], k rotated and v
 // copied into the caches [KV][max_seq][hd] (f16 when kv_f16, else f32) at slot pos + row.
 // Table row pos + row (per_token) or pos of ct / st [*, hd] (entries 2i, 2i + 1 alike).
 struct RopeKvEpi {
@@ -358,7 +359,7 @@ struct RopeKvEpi {
     const float* ct = nullptr;
     const float* st = nullptr;
     const int32_t* pos = nullptr;
-    int H = 0, KV = 0, hd = 0, per_token = 0, kv_f16 = 0;
+    int H = 0, KV = 0, hd = 0, per_token = 0, kv_f16 = 0, col_off = 0;
     int64_t max_seq = 0;
 };
 // Epilogue: PLAIN y = v; RES y = res + v (res may be y); GLU16 columns (2i, 2i + 1) are
@@ -371,12 +372,13 @@ struct GemmEpi {
     int order;
     RopeKvEpi rk{};
 };
-// The ROPE_KV epilogue's store of column c (of n = (H + 2 KV) hd) of token row r: pair
-// values (x0, x1) of the column's interleaved pair, v the column's own value.
+// The ROPE_KV epilogue's store of the GEMM's column c (column col_off + c of [q | k | v]) of
+// token row r: pair values (x0, x1) of the column's interleaved pair, v the column's own value.
 // (Column indices and head sizes are 32-bit: n < 2^31.)
 __device__ inline void rope_kv_store(const RopeKvEpi& rk, int64_t r, int64_t c64, int64_t pos, float x0, float x1,
                                      float v) {
-    const uint32_t c = (uint32_t)c64, hd = (uint32_t)rk.hd, qw = (uint32_t)rk.H * hd, kw = (uint32_t)rk.KV * hd;
+    const uint32_t c = (uint32_t)c64 + (uint32_t)rk.col_off, hd = (uint32_t)rk.hd, qw = (uint32_t)rk.H * hd,
+                   kw = (uint32_t)rk.KV * hd;
     if (c < qw + kw) {
         const uint32_t i = c % hd;
         const int64_t ti = (rk.per_token ? pos + r : pos) * hd + (i & ~1u);

@@ -422,8 +422,8 @@ static int prefill_layer_fused(Llama* m, int l, int n, hipStream_t s, Pending& p
     if (pend.part) dev_free_on(pend.part, s);
     pend = Pending{};
     if (rc) return rc;
-    if (m->qkv_segs[l].size() == 1 && g_rope_epilogue.load(std::memory_order_relaxed)) {
-        // one [q | k | v] weight: RoPE and the KV append ride in the GEMM epilogue
+    if (g_rope_epilogue.load(std::memory_order_relaxed)) {
+        // RoPE and the KV append ride in the epilogue of each [q | k | v] weight's GEMM
         GemmEpi rope{GEMM_ROPE_KV, nullptr, nullptr, 0};
         rope.rk.q = m->q;
         rope.rk.kc = m->kc[l];
@@ -437,7 +437,10 @@ static int prefill_layer_fused(Llama* m, int l, int n, hipStream_t s, Pending& p
         rope.rk.per_token = m->rope_per_token;
         rope.rk.kv_f16 = m->kv_f16 ? 1 : 0;
         rope.rk.max_seq = m->max_seq;
-        if ((rc = gemm16(m->qkv_segs[l][0].w, m->xa16, m->qkv, n, rope, s))) return rc;
+        for (const Seg& sg : m->qkv_segs[l]) {
+            rope.rk.col_off = (int)sg.row_off;
+            if ((rc = gemm16(sg.w, m->xa16, m->qkv, n, rope, s))) return rc;
+        }
     } else if (m->qkv_segs[l].size() == 1) {
         if ((rc = gemm16(m->qkv_segs[l][0].w, m->xa16, m->qkv, n, plain, s))) return rc;
         prefill_rope_kv(m, l, n, s);
