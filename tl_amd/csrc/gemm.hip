@@ -1193,11 +1193,12 @@ int launch_gemm_f16q(const QWeight* w, const _Float16* x16, float* y, int64_t m,
         return TL_HIP_ERR_ARG;
     }
     if (ep.mode == GEMM_ROPE_KV &&
-        (ep.rk.hd < 4 || ep.rk.hd % 4 || ep.rk.col_off < 0 || ep.rk.col_off % ep.rk.hd || w->n % ep.rk.hd ||
+        (ep.rk.hd_shift < 2 || ep.rk.hd_shift > 12 || ep.rk.hd != (1 << ep.rk.hd_shift) || ep.rk.col_off < 0 ||
+         ep.rk.col_off % ep.rk.hd || w->n % ep.rk.hd ||
          ep.rk.col_off + w->n > (int64_t)(ep.rk.H + 2 * ep.rk.KV) * ep.rk.hd || !ep.rk.q || !ep.rk.kc || !ep.rk.vc ||
          !ep.rk.ct || !ep.rk.st || !ep.rk.pos)) {
         set_error(TL_HIP_ERR_ARG, "ArgumentError: the RoPE / KV epilogue takes whole heads of [q | k | v] (head size "
-                  "a multiple of 4) and every output");
+                  "a power of two of 4-4096, hd_shift its log2) and every output");
         return TL_HIP_ERR_ARG;
     }
     const bool needs_w16 = (w->ggml_type == TL_HIP_GGML_Q4_K && !w->us) || w->ggml_type == TL_HIP_GGML_Q6_K;

@@ -360,6 +360,7 @@ struct RopeKvEpi {
     const float* st = nullptr;
     const int32_t* pos = nullptr;
     int H = 0, KV = 0, hd = 0, per_token = 0, kv_f16 = 0, col_off = 0;
+    int hd_shift = 0;  // log2(hd): the head size is a power of two
     int64_t max_seq = 0;
 };
 // Epilogue: PLAIN y = v; RES y = res + v (res may be y); GLU16 columns (2i, 2i + 1) are
@@ -374,13 +375,16 @@ struct GemmEpi {
 };
 // The ROPE_KV epilogue's store of the GEMM's column c (column col_off + c of [q | k | v]) of
 // token row r: pair values (x0, x1) of the column's interleaved pair, v the column's own value.
-// (Column indices and head sizes are 32-bit: n < 2^31.)
+// (Column indices are 32-bit: n < 2^31.)
 __device__ inline void rope_kv_store(const RopeKvEpi& rk, int64_t r, int64_t c64, int64_t pos, float x0, float x1,
                                      float v) {
     const uint32_t c = (uint32_t)c64 + (uint32_t)rk.col_off, hd = (uint32_t)rk.hd, qw = (uint32_t)rk.H * hd,
                    kw = (uint32_t)rk.KV * hd;
+    const int sh = rk.hd_shift;
+    auto head = [&](uint32_t x) { return x >> sh; };
+    auto in_head = [&](uint32_t x) { return x & (hd - 1); };
     if (c < qw + kw) {
-        const uint32_t i = c % hd;
+        const uint32_t i = in_head(c);
         const int64_t ti = (rk.per_token ? pos + r : pos) * hd + (i & ~1u);
         float r0, r1;
         rope_pair(x0, x1, rk.ct[ti], rk.st[ti], &r0, &r1);
@@ -388,13 +392,13 @@ __device__ inline void rope_kv_store(const RopeKvEpi& rk, int64_t r, int64_t c64
         if (c < qw) {
             rk.q[r * qw + c] = o;
         } else {
-            const int64_t at = ((int64_t)((c - qw) / hd) * rk.max_seq + pos + r) * hd + i;
+            const int64_t at = ((int64_t)head(c - qw) * rk.max_seq + pos + r) * hd + i;
             if (rk.kv_f16) static_cast<__half*>(rk.kc)[at] = __float2half(o);
             else static_cast<float*>(rk.kc)[at] = o;
         }
     } else {
         const uint32_t vi = c - qw - kw;
-        const int64_t at = ((int64_t)(vi / hd) * rk.max_seq + pos + r) * hd + vi % hd;
+        const int64_t at = ((int64_t)head(vi) * rk.max_seq + pos + r) * hd + in_head(vi);
         if (rk.kv_f16) static_cast<__half*>(rk.vc)[at] = __float2half(v);
         else static_cast<float*>(rk.vc)[at] = v;
     }

@@ -422,7 +422,7 @@ static int prefill_layer_fused(Llama* m, int l, int n, hipStream_t s, Pending& p
     if (pend.part) dev_free_on(pend.part, s);
     pend = Pending{};
     if (rc) return rc;
-    if (g_rope_epilogue.load(std::memory_order_relaxed)) {
+    if (g_rope_epilogue.load(std::memory_order_relaxed) && m->hd >= 4 && (m->hd & (m->hd - 1)) == 0) {
         // RoPE and the KV append ride in the epilogue of each [q | k | v] weight's GEMM
         GemmEpi rope{GEMM_ROPE_KV, nullptr, nullptr, 0};
         rope.rk.q = m->q;
@@ -437,6 +437,7 @@ static int prefill_layer_fused(Llama* m, int l, int n, hipStream_t s, Pending& p
         rope.rk.per_token = m->rope_per_token;
         rope.rk.kv_f16 = m->kv_f16 ? 1 : 0;
         rope.rk.max_seq = m->max_seq;
+        while ((1 << rope.rk.hd_shift) < m->hd) rope.rk.hd_shift++;
         for (const Seg& sg : m->qkv_segs[l]) {
             rope.rk.col_off = (int)sg.row_off;
             if ((rc = gemm16(sg.w, m->xa16, m->qkv, n, rope, s))) return rc;
