@@ -44,22 +44,22 @@ __device__ __forceinline__ void st_nt(float4* p, const float4& v) {
 }
 
 // ------------------------------------------------------------------ RMSNorm ---------
-// One workgroup per row; the row is held in registers (V float4 per thread) so x is read
-// once.  mode 0: (x / sqrt(ms + eps)) * w     (tl_cpu ffi.rs:2444-2486 + mul_impl)
+// One workgroup of T threads per row; the row is held in registers (V float4 per thread) so
+// x is read once.  mode 0: (x / sqrt(ms + eps)) * w     (tl_cpu ffi.rs:2444-2486 + mul_impl)
 //      mode 1: x * (1 / sqrt(ms + eps)) * w   (fused_rms_norm, fused_ops.rs:37-57)
 // With a residual r the row is x + r first (fused_add_rms_norm, fused_ops.rs:59-85).
 // The row, the residual and the weight are all requested before the reduction (the weight
 // used to follow it: a second memory round trip per row), the row streams are non-temporal.
 // (One wavefront per row, no barrier, measured slower: 8.9 against 5.8 us at [512, 4096] --
 // two wavefronts per CU then issue all the loads.)
-template <int V>
-__global__ __launch_bounds__(256) void k_rmsnorm(const float* __restrict__ x,
+template <int V, int T = 256>
+__global__ __launch_bounds__(T) void k_rmsnorm(const float* __restrict__ x,
                                                  const float* __restrict__ r,
                                                  const float* __restrict__ w,
                                                  float* __restrict__ out, int64_t n, float eps,
                                                  int mode) {
     asm volatile("" : : "s"(x), "s"(r), "s"(w), "s"(out), "s"(n), "s"(eps), "s"(mode));  // one round of loads
-    __shared__ float red[4];
+    __shared__ float red[T / 64];
     const int64_t row = blockIdx.x;
     const float4* xr = reinterpret_cast<const float4*>(x + row * n);
     const float4* rr = r ? reinterpret_cast<const float4*>(r + row * n) : nullptr;
@@ -68,18 +68,18 @@ __global__ __launch_bounds__(256) void k_rmsnorm(const float* __restrict__ x,
     float4 v[V], ww[V];
 #pragma unroll
     for (int i = 0; i < V; i++) {
-        const int64_t j = threadIdx.x + (int64_t)i * 256;
+        const int64_t j = threadIdx.x + (int64_t)i * T;
         v[i] = j < n4 ? ld_nt(xr + j) : make_float4(0.f, 0.f, 0.f, 0.f);
     }
 #pragma unroll
     for (int i = 0; i < V; i++) {
-        const int64_t j = threadIdx.x + (int64_t)i * 256;
+        const int64_t j = threadIdx.x + (int64_t)i * T;
         ww[i] = w4 && j < n4 ? w4[j] : make_float4(1.f, 1.f, 1.f, 1.f);
     }
     float ss = 0.f;
 #pragma unroll
     for (int i = 0; i < V; i++) {
-        const int64_t j = threadIdx.x + (int64_t)i * 256;
+        const int64_t j = threadIdx.x + (int64_t)i * T;
         if (rr && j < n4) {
             const float4 q = ld_nt(rr + j);
             v[i].x = v[i].x + q.x;
@@ -93,14 +93,19 @@ __global__ __launch_bounds__(256) void k_rmsnorm(const float* __restrict__ x,
     ss = wave_allsum(ss);
     if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = ss;
     __syncthreads();
-    ss = red[0] + red[1] + red[2] + red[3];
+    if constexpr (T == 256) ss = red[0] + red[1] + red[2] + red[3];
+    else {
+        ss = 0.f;
+#pragma unroll
+        for (int w = 0; w < T / 64; w++) ss += red[w];
+    }
     const float ms = ss / (float)n;
     const float rms = sqrtf(ms + eps);
     const float rcp = 1.0f / rms;
     float4* o = reinterpret_cast<float4*>(out + row * n);
 #pragma unroll
     for (int i = 0; i < V; i++) {
-        const int64_t j = threadIdx.x + (int64_t)i * 256;
+        const int64_t j = threadIdx.x + (int64_t)i * T;
         if (j >= n4) continue;
         const float4 a = v[i], b = ww[i];
         float4 res;
@@ -240,8 +245,8 @@ int launch_rmsnorm(const float* x, const float* r, const float* w, float* out, i
         k_rmsnorm<1><<<rows, 256, 0, s>>>(x, r, w, out, n, eps, mode);
     else if (vec && per <= 2)
         k_rmsnorm<2><<<rows, 256, 0, s>>>(x, r, w, out, n, eps, mode);
-    else if (vec && per <= 4)
-        k_rmsnorm<4><<<rows, 256, 0, s>>>(x, r, w, out, n, eps, mode);
+    else if (vec && per <= 4)  // 2049-4096 elements: 512 threads x 2 float4 (4.9 -> 4.7 us at [512, 4096])
+        k_rmsnorm<2, 512><<<rows, 512, 0, s>>>(x, r, w, out, n, eps, mode);
     else if (vec && per <= 8)
         k_rmsnorm<8><<<rows, 256, 0, s>>>(x, r, w, out, n, eps, mode);
     else
@@ -294,20 +299,21 @@ __global__ void k_apply_rope(const float* __restrict__ x, const float* __restric
 }
 
 // apply_rope with whole float4s: one workgroup per token (grid.y; every vector of a token
-// uses table row row0 + token, or row0 for all with tl_cpu's rule), 256 threads x 4 float4
-// of the token's vpt * hd floats (grid.x slabs of 1024 float4).  hd / 4 is a power of two
-// dividing 256, so a thread's four float4 sit at the same offset i0 of their head vectors and
-// one float4 each of the cos and sin rows serves all of them (pairs (i0, i0+1), (i0+2, i0+3)
+// uses table row row0 + token, or row0 for all with tl_cpu's rule), T threads x F float4
+// (F T = 1024) of the token's vpt * hd floats (grid.x slabs of 1024 float4).  hd / 4 is a
+// power of two dividing T, so a thread's F float4 sit at the same offset i0 of their head
+// vectors and one float4 each of the cos and sin rows serves all of them (pairs (i0, i0+1), (i0+2, i0+3)
 // take entries i0 and i0 + 2, as k_apply_rope).  No 64-bit division; x read and out written
 // non-temporal.
-__global__ __launch_bounds__(256) void k_apply_rope4(const float* __restrict__ x, const float* __restrict__ ct,
+template <int F = 4, int T = 256>
+__global__ __launch_bounds__(T) void k_apply_rope4(const float* __restrict__ x, const float* __restrict__ ct,
                                                      const float* __restrict__ st, float* __restrict__ out,
                                                      int64_t units, int hd4, int64_t row0, int per_token,
                                                      int64_t cos_len, int64_t sin_len) {
     asm volatile("" : : "s"(x), "s"(ct), "s"(st), "s"(out), "s"(units), "s"(hd4), "s"(row0), "s"(per_token),
                  "s"(cos_len), "s"(sin_len));
     const int64_t tok = blockIdx.y;
-    const int64_t u0 = (int64_t)blockIdx.x * 1024 + threadIdx.x;  // float4 index within the token
+    const int64_t u0 = (int64_t)blockIdx.x * (F * T) + threadIdx.x;  // float4 index within the token
     const int i0 = 4 * (threadIdx.x & (hd4 - 1));                  // offset within the head vector
     const int64_t ti = (per_token ? row0 + tok : row0) * (int64_t)hd4 * 4 + i0;
     float c0, c2, s0, s2;
@@ -322,15 +328,15 @@ __global__ __launch_bounds__(256) void k_apply_rope4(const float* __restrict__ x
     }
     const float4* xt = reinterpret_cast<const float4*>(x) + tok * units;
     float4* ot = reinterpret_cast<float4*>(out) + tok * units;
-    float4 a[4];
+    float4 a[F];
 #pragma unroll
-    for (int k = 0; k < 4; k++) {
-        const int64_t u = u0 + 256 * k;
+    for (int k = 0; k < F; k++) {
+        const int64_t u = u0 + T * k;
         a[k] = u < units ? ld_nt(xt + u) : make_float4(0.f, 0.f, 0.f, 0.f);
     }
 #pragma unroll
-    for (int k = 0; k < 4; k++) {
-        const int64_t u = u0 + 256 * k;
+    for (int k = 0; k < F; k++) {
+        const int64_t u = u0 + T * k;
         if (u >= units) break;
         float4 r;
         r.x = a[k].x * c0 - a[k].y * s0;
@@ -705,7 +711,11 @@ int launch_apply_rope(const float* x, const float* ct, const float* st, float* o
     if (vec4) {
         const int64_t units = tok_floats / 4;
         const dim3 grid((unsigned)cdiv(units, 1024), (unsigned)(total / tok_floats));
-        k_apply_rope4<<<grid, 256, 0, s>>>(x, ct, st, out, units, (int)hd4, row0, vpt > 0, cos_len, sin_len);
+        // head vectors up to 512 elements: 128 threads x 8 float4 ([512, 32, 128]: 4.35 -> 4.3 us)
+        if (hd4 <= 128)
+            k_apply_rope4<8, 128><<<grid, 128, 0, s>>>(x, ct, st, out, units, (int)hd4, row0, vpt > 0, cos_len, sin_len);
+        else
+            k_apply_rope4<4, 256><<<grid, 256, 0, s>>>(x, ct, st, out, units, (int)hd4, row0, vpt > 0, cos_len, sin_len);
     } else {
         int64_t np = total / 2;
         k_apply_rope<<<cdiv(np, 256), 256, 0, s>>>(x, ct, st, out, np, hd, cos_len, sin_len, row0, vpt);
