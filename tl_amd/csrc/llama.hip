@@ -333,8 +333,8 @@ static int check_ready(Llama* m) {
     return TL_HIP_OK;
 }
 
-// Whether the f16 prefill applies RoPE and the KV append in the qkv GEMM's epilogue (one
-// [q | k | v] weight) rather than in k_rope_kv after a plain GEMM: the same values either way.
+// Whether the f16 prefill applies RoPE and the KV append in the epilogues of its [q | k | v]
+// GEMMs rather than in k_rope_kv after plain GEMMs: the same values either way.
 static std::atomic<bool> g_rope_epilogue{true};
 
 // RoPE on the q|k rows of n tokens and the k / v append at the device position (prefill).
@@ -438,7 +438,7 @@ static int prefill_layer_fused(Llama* m, int l, int n, hipStream_t s, Pending& p
         rope.rk.kv_f16 = m->kv_f16 ? 1 : 0;
         rope.rk.max_seq = m->max_seq;
         while ((1 << rope.rk.hd_shift) < m->hd) rope.rk.hd_shift++;
-        for (const Seg& sg : m->qkv_segs[l]) {
+        for (const Seg& sg : m->qkv_segs[l]) {  // y (m->qkv) is not written in this mode
             rope.rk.col_off = (int)sg.row_off;
             if ((rc = gemm16(sg.w, m->xa16, m->qkv, n, rope, s))) return rc;
         }
