@@ -376,7 +376,8 @@ def _three_qkv_plan(cfg, layer, which):
 def test_f16_prefill_rope_epilogue_matches_rope_kernel(case):
     """The f16 prefill's RoPE and KV append in the [q | k | v] GEMM's epilogue against the
     separate RoPE / KV kernel after a plain GEMM: bitwise the same prefill logits and the same
-    logits of a decode step after it (which reads every cache row the prefill wrote).  21
+    logits of a decode step after it (which reads every cache row the prefill wrote), then the
+    same for a second 13-token chunk appended at a later cache position.  21
     tokens: 32-row tiles whose last-arriving K split adds the slices and applies RoPE; 77:
     128-row tiles with K split, the sum launch applying it; 512 at TinyLlama's width: 320
     unsplit tiles, the GEMM itself applying it.  f16 and f32 caches, both RoPE position rules;
@@ -399,8 +400,13 @@ def test_f16_prefill_rope_epilogue_matches_rope_kernel(case):
             gpu.reset()
             pre = gpu.forward(prompt, prefill_f16=True)
             dec = gpu.forward([7])
-            got[on] = (pre, dec)
-        for a, b, what in ((got[1][0], got[0][0], "prefill"), (got[1][1], got[0][1], "decode after the prefill")):
+            # a second prompt chunk at cache positions n + 1 .., then a decode step
+            more = gpu.forward(synthetic_prompt(cfg, 54, 13), prefill_f16=True)
+            dec2 = gpu.forward([9])
+            got[on] = (pre, dec, more, dec2)
+        for i, what in enumerate(("prefill", "decode after the prefill", "second chunk at a later position",
+                                  "decode after it")):
+            a, b = got[1][i], got[0][i]
             assert np.array_equal(a.view(np.uint32), b.view(np.uint32)), f"{what}: max-rel {max_rel(a, b):.2e}"
         if case == "21-f16":  # and within the f16 tolerance of the oracle (its RoPE position rule)
             cpu = oracle.Llama(cfg)
