@@ -34,10 +34,10 @@ MATVEC_N = MATVEC_K = 4096
 MATVEC_BYTES = MATVEC_N * MATVEC_K // 32 * 18 + MATVEC_K * 4 + MATVEC_N * 4  # 9,469,952 (Q4_0)
 HBM_PEAK_GBS = 8000.0
 # HBM bytes per 4096 x 4096 matvec launch from the two counter runs of
-# `bench.py --matvec-only` (FETCH_SIZE 4,713.04 KiB x 1.99897 + WRITE_SIZE 16.0 KiB x 1.0,
-# the scale factors read off a 64 MiB device copy in the same runs): 1.0205 x the
+# `bench.py --matvec-only` (FETCH_SIZE 4,711.01 KiB x 1.99895 + WRITE_SIZE 16.0 KiB x 1.0,
+# the scale factors read off a 64 MiB device copy in the same runs): 1.0200 x the
 # algorithmic bytes
-MATVEC_TRAFFIC = 9_663_700
+MATVEC_TRAFFIC = 9_659_467
 
 
 def log(*a):
