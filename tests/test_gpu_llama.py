@@ -397,6 +397,8 @@ def test_f16_prefill_rope_epilogue_matches_rope_kernel(case):
         got = {}
         for on in (1, 0):
             lib.tl_hip_debug_prefill_rope_epilogue(on)
+            assert lib.tl_hip_debug_prefill_rope_epilogue(-1) == on  # the query changes nothing
+            assert lib.tl_hip_debug_prefill_rope_epilogue(-1) == on
             gpu.reset()
             pre = gpu.forward(prompt, prefill_f16=True)
             dec = gpu.forward([7])
