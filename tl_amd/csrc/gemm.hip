@@ -525,20 +525,37 @@ __global__ __launch_bounds__(512) void k_qgemm_mfma(const uint8_t* __restrict__ 
                 if (!owns(i, j)) continue;
                 const floatx4 o = *reinterpret_cast<const floatx4*>(red + (i * TN + j) * 256 + lane * 4);
                 const int64_t c = n0 + wn * (BN / 2) + 16 * j + col;
+                if (ep.mode == GEMM_GLU16) {
+                    // columns (2i, 2i + 1) = (gate_i, up_i) sit in lanes col, col ^ 1, each with
+                    // the same four rows: after one exchange per row the even lane finishes
+                    // rows 0, 1 and the odd lane rows 2, 3, so no lane idles through the SwiGLU
+                    float v4[4], u4[4];
+#pragma unroll
+                    for (int e = 0; e < 4; e++) {
+                        v4[e] = acc[i][j][e] + o[e];
+                        u4[e] = __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v4[e]), 0xB1,
+                                                                                   0xF, 0xF, true));
+                    }
+                    const bool odd = (col & 1) != 0;
+#pragma unroll
+                    for (int h = 0; h < 2; h++) {
+                        const int e = odd ? 2 + h : h;
+                        const float mine = odd ? v4[2 + h] : v4[h], other = odd ? u4[2 + h] : u4[h];
+                        const float gate = odd ? other : mine, up = odd ? mine : other;
+                        const int64_t r = m0 + wm * (BM / 2) + 16 * i + 4 * g + e;
+                        if (r < m && c < n) {
+                            const float a = (gate * (1.0f / (1.0f + expf(-gate)))) * up;  // silu(gate) * up
+                            ep.out16[f16q_index(r, c >> 1, n >> 1, ep.order)] = (_Float16)a;
+                        }
+                    }
+                    continue;
+                }
 #pragma unroll
                 for (int e = 0; e < 4; e++) {
                     const int64_t r = m0 + wm * (BM / 2) + 16 * i + 4 * g + e;
                     const float v = acc[i][j][e] + o[e];
-                    if (ep.mode == GEMM_GLU16) {
-                        // columns (2i, 2i + 1) = (gate_i, up_i) sit in lanes col, col ^ 1
-                        const float u = __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(
-                                                                      __builtin_bit_cast(int, v), 0xB1, 0xF, 0xF, true));
-                        if ((col & 1) == 0 && r < m && c < n) {
-                            const float a = (v * (1.0f / (1.0f + expf(-v)))) * u;  // silu(gate) * up
-                            ep.out16[f16q_index(r, c >> 1, n >> 1, ep.order)] = (_Float16)a;
-                        }
-                    } else if (!FUSE && ep.mode == GEMM_ROPE_KV) {
-                        // RoPE pairs (2i, 2i + 1) sit in lanes col, col ^ 1 as above
+                    if (!FUSE && ep.mode == GEMM_ROPE_KV) {
+                        // RoPE pairs (2i, 2i + 1) sit in lanes col, col ^ 1 as in SwiGLU
                         const float u = __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(
                                                                       __builtin_bit_cast(int, v), 0xB1, 0xF, 0xF, true));
                         if (r < m && c < n) rope_kv_store(ep.rk, r, c, rpos, (col & 1) ? u : v, (col & 1) ? v : u, v);
