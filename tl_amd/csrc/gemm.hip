@@ -550,16 +550,46 @@ __global__ __launch_bounds__(512) void k_qgemm_mfma(const uint8_t* __restrict__ 
                     }
                     continue;
                 }
+                if (!FUSE && ep.mode == GEMM_ROPE_KV) {
+                    // RoPE pairs (2i, 2i + 1) sit in lanes col, col ^ 1 as in SwiGLU; the column's
+                    // place in [q | k | v] once for the lane's four rows, the table entries once
+                    // when every row reads the same table row
+                    float v4[4], u4[4];
+#pragma unroll
+                    for (int e = 0; e < 4; e++) {
+                        v4[e] = acc[i][j][e] + o[e];
+                        u4[e] = __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v4[e]), 0xB1,
+                                                                                   0xF, 0xF, true));
+                    }
+                    if (c < n) {
+                        const RopeCol cl = rope_col(ep.rk, c);
+                        const bool odd = (col & 1) != 0, rot = cl.kind != 2;
+                        const int64_t rb = m0 + wm * (BM / 2) + 16 * i + 4 * g;
+                        float cs = 0.f, sn = 0.f;
+                        if (rot && !ep.rk.per_token) {
+                            const int64_t ti = rope_tab(ep.rk, cl, 0, rpos);
+                            cs = ep.rk.ct[ti];
+                            sn = ep.rk.st[ti];
+                        }
+#pragma unroll
+                        for (int e = 0; e < 4; e++) {
+                            const int64_t r = rb + e;
+                            if (r >= m) break;
+                            if (rot && ep.rk.per_token) {
+                                const int64_t ti = rope_tab(ep.rk, cl, r, rpos);
+                                cs = ep.rk.ct[ti];
+                                sn = ep.rk.st[ti];
+                            }
+                            rope_kv_put(ep.rk, cl, r, rpos, odd ? u4[e] : v4[e], odd ? v4[e] : u4[e], v4[e], cs, sn);
+                        }
+                    }
+                    continue;
+                }
 #pragma unroll
                 for (int e = 0; e < 4; e++) {
                     const int64_t r = m0 + wm * (BM / 2) + 16 * i + 4 * g + e;
                     const float v = acc[i][j][e] + o[e];
-                    if (!FUSE && ep.mode == GEMM_ROPE_KV) {
-                        // RoPE pairs (2i, 2i + 1) sit in lanes col, col ^ 1 as in SwiGLU
-                        const float u = __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(
-                                                                      __builtin_bit_cast(int, v), 0xB1, 0xF, 0xF, true));
-                        if (r < m && c < n) rope_kv_store(ep.rk, r, c, rpos, (col & 1) ? u : v, (col & 1) ? v : u, v);
-                    } else if (r < m && c < n) {
+                    if (r < m && c < n) {
                         if constexpr (FUSE)
                             __hip_atomic_store(reinterpret_cast<uint32_t*>(yb + r * n + c), __float_as_uint(v),
                                                __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -608,10 +638,7 @@ __global__ __launch_bounds__(512) void k_qgemm_mfma(const uint8_t* __restrict__ 
                     v.w = on ? v.w + __uint_as_float(t[p].w) : v.w;
                 }
                 if (ep.mode == GEMM_ROPE_KV) {  // a unit holds two whole pairs
-                    rope_kv_store(ep.rk, r, c, rpos, v.x, v.y, v.x);
-                    rope_kv_store(ep.rk, r, c + 1, rpos, v.x, v.y, v.y);
-                    rope_kv_store(ep.rk, r, c + 2, rpos, v.z, v.w, v.z);
-                    rope_kv_store(ep.rk, r, c + 3, rpos, v.z, v.w, v.w);
+                    rope_kv_store4(ep.rk, r, c, rpos, v);
                 } else {
                     *reinterpret_cast<float4*>(fin + r * n + c) = v;
                 }
@@ -1121,10 +1148,7 @@ __global__ __launch_bounds__(256) void k_splitk_sum_rope(const float* __restrict
         v.w += t.w;
     }
     const int64_t r = i / n, c = i % n, pos = *rk.pos;
-    rope_kv_store(rk, r, c, pos, v.x, v.y, v.x);
-    rope_kv_store(rk, r, c + 1, pos, v.x, v.y, v.y);
-    rope_kv_store(rk, r, c + 2, pos, v.z, v.w, v.z);
-    rope_kv_store(rk, r, c + 3, pos, v.z, v.w, v.w);
+    rope_kv_store4(rk, r, c, pos, v);
 }
 
 namespace {

@@ -373,34 +373,64 @@ struct GemmEpi {
     int order;
     RopeKvEpi rk{};
 };
-// The ROPE_KV epilogue's store of the GEMM's column c (column col_off + c of [q | k | v]) of
-// token row r: pair values (x0, x1) of the column's interleaved pair, v the column's own value.
-// (Column indices are 32-bit: n < 2^31.)
-__device__ inline void rope_kv_store(const RopeKvEpi& rk, int64_t r, int64_t c64, int64_t pos, float x0, float x1,
-                                     float v) {
-    const uint32_t c = (uint32_t)c64 + (uint32_t)rk.col_off, hd = (uint32_t)rk.hd, qw = (uint32_t)rk.H * hd,
-                   kw = (uint32_t)rk.KV * hd;
-    const int sh = rk.hd_shift;
-    auto head = [&](uint32_t x) { return x >> sh; };
-    auto in_head = [&](uint32_t x) { return x & (hd - 1); };
-    if (c < qw + kw) {
-        const uint32_t i = in_head(c);
-        const int64_t ti = (rk.per_token ? pos + r : pos) * hd + (i & ~1u);
-        float r0, r1;
-        rope_pair(x0, x1, rk.ct[ti], rk.st[ti], &r0, &r1);
-        const float o = (i & 1) ? r1 : r0;
-        if (c < qw) {
-            rk.q[r * qw + c] = o;
-        } else {
-            const int64_t at = ((int64_t)head(c - qw) * rk.max_seq + pos + r) * hd + i;
-            if (rk.kv_f16) static_cast<__half*>(rk.kc)[at] = __float2half(o);
-            else static_cast<float*>(rk.kc)[at] = o;
-        }
-    } else {
-        const uint32_t vi = c - qw - kw;
-        const int64_t at = ((int64_t)head(vi) * rk.max_seq + pos + r) * hd + in_head(vi);
+// The ROPE_KV epilogue, split into what depends on the GEMM's column c only (RopeCol: column
+// col_off + c of [q | k | v]: q, k or v, its head and index within the head) and the store of
+// one token row r (pair values (x0, x1) of the column's interleaved pair, v the column's own
+// value; cs / sn the table entries of the pair, rope_tab).  Column indices are 32-bit
+// (n < 2^31).
+struct RopeCol {
+    uint32_t kind;  // 0 q, 1 k, 2 v
+    uint32_t c;     // column of [q | k | v]
+    uint32_t head;  // KV head (k, v)
+    uint32_t i;     // index within the head vector
+};
+__device__ inline RopeCol rope_col(const RopeKvEpi& rk, int64_t c64) {
+    const uint32_t c = (uint32_t)c64 + (uint32_t)rk.col_off, hd = (uint32_t)rk.hd, sh = (uint32_t)rk.hd_shift;
+    const uint32_t qw = (uint32_t)rk.H * hd, kw = (uint32_t)rk.KV * hd;
+    const uint32_t kind = c < qw ? 0u : c < qw + kw ? 1u : 2u;
+    const uint32_t rel = kind == 0 ? c : kind == 1 ? c - qw : c - qw - kw;
+    return RopeCol{kind, c, rel >> sh, rel & (hd - 1)};
+}
+// the table row of token row r: pos + r (per_token) or pos
+__device__ inline int64_t rope_tab(const RopeKvEpi& rk, const RopeCol& cl, int64_t r, int64_t pos) {
+    return (rk.per_token ? pos + r : pos) * rk.hd + (cl.i & ~1u);
+}
+__device__ inline void rope_kv_put(const RopeKvEpi& rk, const RopeCol& cl, int64_t r, int64_t pos, float x0, float x1,
+                                   float v, float cs, float sn) {
+    if (cl.kind == 2) {
+        const int64_t at = ((int64_t)cl.head * rk.max_seq + pos + r) * rk.hd + cl.i;
         if (rk.kv_f16) static_cast<__half*>(rk.vc)[at] = __float2half(v);
         else static_cast<float*>(rk.vc)[at] = v;
+        return;
+    }
+    float r0, r1;
+    rope_pair(x0, x1, cs, sn, &r0, &r1);
+    const float o = (cl.i & 1) ? r1 : r0;
+    if (cl.kind == 0) {
+        rk.q[r * ((int64_t)rk.H * rk.hd) + cl.c] = o;
+    } else {
+        const int64_t at = ((int64_t)cl.head * rk.max_seq + pos + r) * rk.hd + cl.i;
+        if (rk.kv_f16) static_cast<__half*>(rk.kc)[at] = __float2half(o);
+        else static_cast<float*>(rk.kc)[at] = o;
+    }
+}
+// a 4-column unit (columns c .. c + 3, c a multiple of 4: two whole pairs, one head) of token
+// row r: each pair's place and table entries once
+__device__ inline void rope_kv_store4(const RopeKvEpi& rk, int64_t r, int64_t c, int64_t pos, float4 v) {
+#pragma unroll
+    for (int h = 0; h < 2; h++) {
+        const float x0 = h ? v.z : v.x, x1 = h ? v.w : v.y;
+        RopeCol cl = rope_col(rk, c + 2 * h);
+        float cs = 0.f, sn = 0.f;
+        if (cl.kind != 2) {
+            const int64_t ti = rope_tab(rk, cl, r, pos);
+            cs = rk.ct[ti];
+            sn = rk.st[ti];
+        }
+        rope_kv_put(rk, cl, r, pos, x0, x1, x0, cs, sn);
+        cl.c += 1;
+        cl.i += 1;
+        rope_kv_put(rk, cl, r, pos, x0, x1, x1, cs, sn);
     }
 }
 __host__ __device__ inline int64_t f16q_index(int64_t r, int64_t e, int64_t k, int order) {
