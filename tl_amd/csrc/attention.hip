@@ -972,16 +972,23 @@ __global__ __launch_bounds__(256) void k_attn_prefill(const float* __restrict__ 
         if (out16) {
             // o / l rounded to f32 and then to f16 for every element: the product is pinned in a
             // register first -- left alone, the compiler fuses some of these conversions into
-            // one-rounding mixed FMAs (v_fma_mix) and not others, depending on the instantiation
+            // one-rounding mixed FMAs (v_fma_mix) and not others, depending on the instantiation.
+            // The lane's four dims 4 g .. 4 g + 3 (a 4-aligned run) fill slots s .. s + 3 of one
+            // operand word in either order (Q4: in order; Q8: as e0 e2 e1 e3): one 8-byte store.
 #pragma unroll
-            for (int dt = 0; dt < D / 16; dt++)
+            for (int dt = 0; dt < D / 16; dt++) {
+                _Float16 h[4];
 #pragma unroll
                 for (int i = 0; i < 4; i++) {
                     float v = o[rt][dt][i] * rl;
                     asm volatile("" : "+v"(v));
-                    out16[f16q_index(qi[rt], (int64_t)hh[rt] * D + 16 * dt + 4 * g + i, (int64_t)hq * D, order)] =
-                        (_Float16)v;
+                    h[i] = (_Float16)v;
                 }
+                const int64_t at = f16q_index(qi[rt], (int64_t)hh[rt] * D + 16 * dt + 4 * g, (int64_t)hq * D, order);
+                typedef _Float16 half4v __attribute__((ext_vector_type(4)));
+                *reinterpret_cast<half4v*>(out16 + at) =
+                    order == F16Q_Q8 ? half4v{h[0], h[2], h[1], h[3]} : half4v{h[0], h[1], h[2], h[3]};
+            }
         } else {
             float* op = out + ((int64_t)qi[rt] * hq + hh[rt]) * D;
 #pragma unroll
