@@ -414,23 +414,34 @@ __device__ inline void rope_kv_put(const RopeKvEpi& rk, const RopeCol& cl, int64
         else static_cast<float*>(rk.kc)[at] = o;
     }
 }
-// a 4-column unit (columns c .. c + 3, c a multiple of 4: two whole pairs, one head) of token
-// row r: each pair's place and table entries once
+// a 4-column unit (columns c .. c + 3, c a multiple of 4: two whole pairs of one head) of
+// token row r: its place and each pair's table entries once, and one 16-byte (f32) or 8-byte
+// (f16) store of the four values
 __device__ inline void rope_kv_store4(const RopeKvEpi& rk, int64_t r, int64_t c, int64_t pos, float4 v) {
+    const RopeCol cl = rope_col(rk, c);
+    float o[4] = {v.x, v.y, v.z, v.w};
+    if (cl.kind != 2) {
 #pragma unroll
-    for (int h = 0; h < 2; h++) {
-        const float x0 = h ? v.z : v.x, x1 = h ? v.w : v.y;
-        RopeCol cl = rope_col(rk, c + 2 * h);
-        float cs = 0.f, sn = 0.f;
-        if (cl.kind != 2) {
-            const int64_t ti = rope_tab(rk, cl, r, pos);
-            cs = rk.ct[ti];
-            sn = rk.st[ti];
+        for (int h = 0; h < 2; h++) {
+            RopeCol ch = cl;
+            ch.i += 2 * h;
+            const int64_t ti = rope_tab(rk, ch, r, pos);
+            rope_pair(o[2 * h], o[2 * h + 1], rk.ct[ti], rk.st[ti], &o[2 * h], &o[2 * h + 1]);
         }
-        rope_kv_put(rk, cl, r, pos, x0, x1, x0, cs, sn);
-        cl.c += 1;
-        cl.i += 1;
-        rope_kv_put(rk, cl, r, pos, x0, x1, x1, cs, sn);
+    }
+    if (cl.kind == 0) {
+        *reinterpret_cast<float4*>(rk.q + r * ((int64_t)rk.H * rk.hd) + cl.c) = make_float4(o[0], o[1], o[2], o[3]);
+        return;
+    }
+    void* base = cl.kind == 1 ? rk.kc : rk.vc;
+    const int64_t at = ((int64_t)cl.head * rk.max_seq + pos + r) * rk.hd + cl.i;
+    if (rk.kv_f16) {
+        typedef _Float16 half4v __attribute__((ext_vector_type(4)));
+        // (float -> f16 by round to nearest even, as __float2half in rope_kv_put)
+        *reinterpret_cast<half4v*>(static_cast<__half*>(base) + at) =
+            half4v{(_Float16)o[0], (_Float16)o[1], (_Float16)o[2], (_Float16)o[3]};
+    } else {
+        *reinterpret_cast<float4*>(static_cast<float*>(base) + at) = make_float4(o[0], o[1], o[2], o[3]);
     }
 }
 __host__ __device__ inline int64_t f16q_index(int64_t r, int64_t e, int64_t k, int order) {
