@@ -151,8 +151,10 @@ __global__ __launch_bounds__(256) void k_rmsnorm_generic(const float* __restrict
 }
 
 // RMSNorm mode 0 whose output goes straight to the f16 operand order of the GEMM that reads
-// it (the same f32 value as k_rmsnorm, rounded once to f16): the sum of squares in k_rmsnorm's
-// order (thread j's float4 j, j + 256, ...), then one 8-half word per (block, t) unit.
+// it: the sum of squares in the order of k_rmsnorm's 256-thread form (thread j's float4 j,
+// j + 256, ...; k_rmsnorm takes that form for rows up to 2048 elements, so there the f32 value
+// is k_rmsnorm's, rounded once to f16), then one 8-half word per (block, t) unit.  (The norm
+// weight requested with the row, before the reduction, measured no faster: L2 hits.)
 // SUM: the row is first completed from a deferred split-K GEMM -- x = x + part_0 + ... +
 // part_{nsp-1} in slice order, the additions of k_splitk_sum -- written back to x (the new
 // residual) and kept in LDS for the normalisation: one launch instead of the sum's and this.
