@@ -255,10 +255,26 @@ tl_hip_tensor* tl_hip_tensor_repeat_interleave(const tl_hip_tensor* x, int64_t r
 /* IDevice::tensor_embedding (device.rs:418-425; tensor.rs:1094-1112): ids hold f32 token
  * ids; an id outside [0, vocab) is IndexOutOfBounds. */
 tl_hip_tensor* tl_hip_tensor_embedding(const tl_hip_tensor* weight, const tl_hip_tensor* ids);
-/* IDevice::tensor_sample (device.rs:349; tensor.rs:1626-1680), greedy branch only:
- * temp <= 0 returns [1] holding the argmax (last index among equal maxima); temp > 0 is
- * ArgumentError (stochastic top-p sampling is not provided). */
+/* IDevice::tensor_sample (device.rs:349; tensor.rs:1626-1680) over all elements of logits:
+ * returns [1] holding the chosen index.  temp <= 0: the argmax (last index among equal
+ * maxima).  Otherwise (a NaN temp included) top-p sampling of softmax(logits / temp): the
+ * indices by descending probability (equal probabilities in index order), cut after the
+ * first place where the running sum exceeds top_p, and the first place whose running sum
+ * reaches u * (running sum at the cut) is chosen, u a uniform draw in [0, 1) from this
+ * library's per-thread generator (the reference draws from rand::thread_rng).  A NaN or
+ * infinite logits / temp gives index 0, as in the reference.  Empty logits: InternalError. */
 tl_hip_tensor* tl_hip_tensor_sample(const tl_hip_tensor* logits, float temp, float top_p);
+/* tl_hip_tensor_sample with the uniform draw given (0 <= u < 1, else ArgumentError).  No
+ * counterpart in the reference, whose draw cannot be fixed: for callers and tests that
+ * replay a choice.  Running sums are exact (fixed point), so the choice equals the
+ * reference's wherever r = u * cutoff and top_p are not within the reference's f32 rounding
+ * of a running sum. */
+tl_hip_tensor* tl_hip_tensor_sample_uniform(const tl_hip_tensor* logits, float temp, float top_p,
+                                            double u);
+/* Seeds the calling thread's generator of tl_hip_tensor_sample (splitmix64; a draw is its
+ * top 53 bits times 2^-53).  Unseeded threads start from OS entropy.  No counterpart in the
+ * reference (rand::thread_rng is not seedable): for reproducible sampling runs. */
+void tl_hip_sample_seed(uint64_t seed);
 /* argmax over all elements (tensor.rs:841-846), last index among equal maxima. */
 int64_t tl_hip_tensor_argmax_all(const tl_hip_tensor* x);
 /* IDevice::tensor_repetition_penalty (device.rs:194-199; tl_cpu device_impl.rs:967-1001) */

@@ -140,8 +140,8 @@ impl HipDevice {
     pub fn tensor_softmax(&self, t: *mut c_void, dim: i64) -> BackendResult<*mut c_void> {
         check(unsafe { ffi::tl_hip_tensor_softmax(h(t), dim) })
     }
-    /// device.rs:349 tensor_sample(t, temp, top_p): greedy for temp <= 0; temp > 0 is
-    /// ArgumentError from the C entry (stochastic top-p sampling is not provided).
+    /// device.rs:349 tensor_sample(t, temp, top_p): greedy for temp <= 0, else top-p
+    /// sampling with the library's per-thread uniform draw (tl_hip_sample_seed fixes it).
     pub fn tensor_sample(&self, t: *mut c_void, temp: f32, top_p: f32) -> BackendResult<*mut c_void> {
         check(unsafe { ffi::tl_hip_tensor_sample(h(t), temp, top_p) })
     }

@@ -230,6 +230,13 @@ extern "C" {
         temp: f32,
         top_p: f32,
     ) -> *mut tl_hip_tensor;
+    pub fn tl_hip_tensor_sample_uniform(
+        logits: *const tl_hip_tensor,
+        temp: f32,
+        top_p: f32,
+        u: f64,
+    ) -> *mut tl_hip_tensor;
+    pub fn tl_hip_sample_seed(seed: u64);
     pub fn tl_hip_tensor_argmax_all(x: *const tl_hip_tensor) -> i64;
     pub fn tl_hip_tensor_repetition_penalty(
         logits: *const tl_hip_tensor,

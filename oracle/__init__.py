@@ -50,6 +50,7 @@ _PROTOS = {
     "tlo_narrow": (_int, [_f32p, _i64p, _int, _int, _i64, _i64, _f32p]),
     "tlo_embedding": (_int, [_f32p, _i64, _i64, _f32p, _i64, _f32p]),
     "tlo_argmax_last": (_i64, [_f32p, _i64]),
+    "tlo_sample": (_i64, [_f32p, _i64, _f32, _f32, _f64]),
     "tlo_repetition_penalty": (None, [_f32p, _i64, _i64, _f32p, _i64, _f64, _f32p]),
     "tlo_sdpa": (None, [_f32p, _f32p, _f32p, _f32p, _i64, _i64, _i64, _i64, _i64, _i64, _f32p]),
     "tlo_attention": (_int, [_f32p, _f32p, _f32p, _i64, _i64, _i64, _i64, _i64, _f32, _int, _f32p]),
@@ -310,6 +311,12 @@ def embedding(table, ids):
 def argmax_last(x):
     x = _f(x)
     return int(lib().tlo_argmax_last(_p(x), x.size))
+
+
+def sample(x, temp, top_p, u):
+    """sample_impl over all elements of x with the uniform draw u (-1 for an empty input)."""
+    x = _f(x)
+    return int(lib().tlo_sample(_p(x), x.size, temp, top_p, u))
 
 
 def repetition_penalty(logits, tokens, penalty):

@@ -27,6 +27,10 @@
  *   tlo_apply_rope          pos-0 identity (cuda_shader_test.rs:332-355), rotation norm
  *   tlo_softmax             rows sum to 1, monotone (cpu_tensor_tests.rs:439-449)
  *   tlo_argmax_last         hand-built tie cases (last maximum wins)
+ *   tlo_sample              closed forms of two- and four-element distributions (cutoff and
+ *                           choice by hand), ties in index order, NaN / inf -> 0, and a
+ *                           float64 restatement (numpy stable argsort, cumulative sums) on
+ *                           random inputs wherever top_p and r are clear of every running sum
  *   tlo_fused_add_relu      reference KAT (tl_cuda new_ops_comprehensive_test.rs:624-632)
  *   tlo_fused_bias_gelu     reference KAT gelu(0) = 0 (new_ops_comprehensive_test.rs:687-693),
  *                           signs at +-1.1 (tl_metal fused_ops_test.rs:60-75), limits
@@ -637,6 +641,70 @@ int64_t tlo_argmax_last(const float* x, int64_t n) {
     for (int64_t i = 1; i < n; i++)
         if (!(x[best] > x[i])) best = i;
     return best;
+}
+
+/* sort_by(|&a, &b| probs[b].partial_cmp(&probs[a]).unwrap_or(Equal)) of tensor.rs:1649-1650:
+ * a stable merge sort of the indices by descending prob; an element moves ahead of an
+ * earlier one only when it compares greater (a NaN compares Equal and keeps its place). */
+static void sample_sort(int64_t* idx, int64_t* tmp, int64_t n, const float* pr) {
+    for (int64_t w = 1; w < n; w *= 2) {
+        for (int64_t lo = 0; lo < n; lo += 2 * w) {
+            int64_t mid = lo + w < n ? lo + w : n, hi = lo + 2 * w < n ? lo + 2 * w : n;
+            int64_t a = lo, b = mid, o = lo;
+            while (a < mid && b < hi) tmp[o++] = pr[idx[a]] < pr[idx[b]] ? idx[b++] : idx[a++];
+            while (a < mid) tmp[o++] = idx[a++];
+            while (b < hi) tmp[o++] = idx[b++];
+        }
+        memcpy(idx, tmp, sizeof(int64_t) * (size_t)n);
+    }
+}
+
+/* CpuTensor::sample_impl (crates/tl_cpu/src/tensor.rs:1626-1680) with rng.gen::<f64>() given
+ * as u (tensor.rs:1663-1666):
+ *   temp <= 0: the greedy argmax (1633-1638, tlo_argmax_last; a NaN temp is not <= 0);
+ *   probs = x / temp (1642), max by the fold `if a > b {a} else {b}` from -inf (1644),
+ *   sum_exp a left fold of expf(p - max) (1645), probs = expf(p - max) / sum_exp (1646);
+ *   indices sorted by descending prob, stable (1649-1650);
+ *   cum_prob summed in that order until it exceeds top_p: cutoff (1652-1660), else the last;
+ *   r = (f32)u * cutoff_prob (1662-1666); the first index up to the cutoff whose running sum
+ *   reaches r, indices[0] when none does (1667-1677).
+ * Returns -1 for an empty input (the reference's InternalError). */
+int64_t tlo_sample(const float* x, int64_t n, float temp, float top_p, double u) {
+    if (n <= 0) return -1;
+    if (temp <= 0.0f) return tlo_argmax_last(x, n);
+    float* p = (float*)malloc(sizeof(float) * (size_t)n);
+    int64_t* idx = (int64_t*)malloc(sizeof(int64_t) * (size_t)n);
+    int64_t* tmp = (int64_t*)malloc(sizeof(int64_t) * (size_t)n);
+    float mx = -INFINITY, se = 0.0f;
+    for (int64_t i = 0; i < n; i++) p[i] = x[i] / temp;
+    for (int64_t i = 0; i < n; i++) mx = mx > p[i] ? mx : p[i];
+    for (int64_t i = 0; i < n; i++) se += expf(p[i] - mx);
+    for (int64_t i = 0; i < n; i++) p[i] = expf(p[i] - mx) / se;
+    for (int64_t i = 0; i < n; i++) idx[i] = i;
+    sample_sort(idx, tmp, n, p);
+    float cum = 0.0f;
+    int64_t cutoff = n - 1;
+    for (int64_t i = 0; i < n; i++) {
+        cum += p[idx[i]];
+        if (cum > top_p) {
+            cutoff = i;
+            break;
+        }
+    }
+    const float r = (float)u * cum;
+    float acc = 0.0f;
+    int64_t sel = idx[0];
+    for (int64_t i = 0; i <= cutoff; i++) {
+        acc += p[idx[i]];
+        if (acc >= r) {
+            sel = idx[i];
+            break;
+        }
+    }
+    free(p);
+    free(idx);
+    free(tmp);
+    return sel;
 }
 
 /* CpuDevice::tensor_repetition_penalty (crates/tl_cpu/src/device_impl.rs:967-1001): the

@@ -5,6 +5,7 @@ max-rel-err = max_i |a_i - b_i| / max(max_j |b_j|, 1e-30); bounds from the north
 bit-exact for dequant, 1e-4 for f32 paths, 1e-2 for f16 paths."""
 import ctypes as C
 import json
+import math
 import os
 
 import numpy as np
@@ -518,6 +519,104 @@ def test_embedding_argmax_penalty(dev):
     tok = np.array([3, 3, 499, 17, -1], np.float32)
     got = dev.tensor_repetition_penalty(dev.tensor_new(lg), dev.tensor_new(tok), 1.1).to_numpy()
     assert np.array_equal(got, oracle.repetition_penalty(lg, tok, 1.1))
+
+
+# ------------------------------------------------------------------ top-p sampling
+def _choice(dev, t, temp, top_p, u):
+    out = dev.tensor_sample_uniform(t, temp, top_p, float(u)).to_numpy()
+    assert out.shape == (1,) and out[0] == int(out[0])
+    return int(out[0])
+
+
+@pytest.mark.parametrize("temp", [0.1, 0.7, 1.0, 2.5])
+def test_sample_top_p_matches_oracle(dev, temp):
+    """tl_hip_tensor_sample_uniform against sample_impl (tensor.rs:1641-1679): vocab-sized
+    logits ~ N(0, 3) (32000, a ragged 131075, 7).  Every choice sits where the definition
+    puts it in the float64 order (running sums bracket r within 4e-6); where top_p and r are
+    clear of every summation's rounding the choice equals the oracle's and the float64
+    restatement's.  The chatbot samples at temp 0.1, top_p 0.9 (chatbot.tl:189)."""
+    from sampling_f64 import bracketed, decided, sample_f64
+    rng = np.random.default_rng(0x5A40 + int(temp * 10))
+    checked = total = 0
+    for n in (32000, 131075, 7):
+        x = (rng.standard_normal(n) * 3).astype(np.float32)
+        t = dev.tensor_new(x)
+        for top_p in (0.9, 0.5, 0.0, 0.75):
+            for u in rng.random(6):
+                got = _choice(dev, t, temp, top_p, u)
+                assert bracketed(x, temp, top_p, u, got), (n, top_p, u, got)
+                sel, margin, drift = sample_f64(x, temp, top_p, u)
+                total += 1
+                if decided(margin, drift):
+                    checked += 1
+                    assert got == sel == oracle.sample(x, temp, top_p, u), (n, top_p, u, got, sel)
+    assert checked >= 0.5 * total, (checked, total)
+
+
+def test_sample_top_p_ties_and_specials(dev):
+    """Equal probabilities in index order, the cut and the choice by exact running sums;
+    NaN / infinite inputs, temp <= 0, [1, V] logits, sizes 1 and 2, errors."""
+    n = 32000
+    t = dev.tensor_new(np.full(n, 0.5, np.float32))
+    # every prob q = f32(1 / n); the running sum after j elements is j * v, v = q in 2^-48 units
+    q = np.float32(1.0) / np.float32(n)
+    v = int(float(q) * 2.0 ** 48)
+    for top_p in (0.9, 0.3, 1.0):
+        for u in (0.0, 0.25, 0.5, 0.999):
+            tt = int(math.floor(float(np.float32(top_p)) * 2.0 ** 48))
+            j_cut = min(tt // v + 1, n)  # n: the sum never exceeds top_p
+            cutoff = np.float32(j_cut * v * 2.0 ** -48)
+            r = np.float32(u) * cutoff
+            j = max(1, -(-int(math.ceil(float(r) * 2.0 ** 48)) // v))
+            want = j - 1 if j <= j_cut else 0  # past the cut: order[0]
+            got = _choice(dev, t, 1.0, top_p, u)
+            assert got == want, (top_p, u, got, want)
+            # the reference's f32 running sums drift from j * q by a few places at most
+            assert abs(oracle.sample(np.full(n, 0.5, np.float32), 1.0, top_p, u) - got) <= 64
+    # two levels of ties: the four 3.0s first (indices 5, 9, 100, 999), then the rest in order
+    x = np.zeros(1000, np.float32)
+    x[[5, 9, 100, 999]] = 3.0
+    for u in (0.0, 0.3, 0.6, 0.95):
+        got = _choice(dev, dev.tensor_new(x), 1.0, 0.9, u)
+        assert got == oracle.sample(x, 1.0, 0.9, u)
+    # NaN / infinite logits or temp: index 0; temp <= 0: the greedy choice
+    for arr, temp in (([1.0, np.nan, 3.0], 1.0), ([1.0, np.inf, 3.0], 1.0), ([-np.inf] * 5, 1.0),
+                      ([1.0, 2.0, 3.0], float("nan"))):
+        assert _choice(dev, dev.tensor_new(np.array(arr, np.float32)), temp, 0.9, 0.5) == 0
+    g = np.array([1, 7, 3, 7, 2], np.float32)
+    assert _choice(dev, dev.tensor_new(g), 0.0, 0.9, 0.5) == 3
+    assert _choice(dev, dev.tensor_new(g), -2.0, 0.9, 0.5) == 3
+    # [1, V] logits (the chatbot's narrowed row) are taken whole; n = 1 and n = 2
+    rng = np.random.default_rng(99)
+    row = (rng.standard_normal((1, 32000)) * 3).astype(np.float32)
+    assert _choice(dev, dev.tensor_new(row), 0.1, 0.9, 0.3) == oracle.sample(row, 0.1, 0.9, 0.3)
+    assert _choice(dev, dev.tensor_new(np.array([4.0], np.float32)), 1.0, 0.9, 0.7) == 0
+    ln3 = np.float32(math.log(3.0))
+    two = dev.tensor_new(np.array([0.0, ln3], np.float32))
+    assert [_choice(dev, two, 1.0, 0.9, u) for u in (0.0, 0.5, 0.8)] == [1, 1, 0]
+    assert _choice(dev, two, 1.0, 0.5, 0.99) == 1
+    with pytest.raises(BackendError) as e:
+        dev.tensor_sample_uniform(dev.tensor_new(np.zeros(0, np.float32)), 1.0, 0.9, 0.5)
+    assert e.value.variant == "InternalError"
+    for bad_u in (-0.1, 1.0, float("nan")):
+        with pytest.raises(BackendError) as e:
+            dev.tensor_sample_uniform(two, 1.0, 0.9, bad_u)
+        assert e.value.variant == "ArgumentError"
+
+
+def test_sample_seeded_draws(dev):
+    """tl_hip_tensor_sample draws u from the calling thread's splitmix64 generator: after
+    tl_hip_sample_seed its choices equal sample_uniform at the replayed draws."""
+    from sampling_f64 import splitmix64_uniforms
+    rng = np.random.default_rng(5)
+    x = (rng.standard_normal(32000) * 3).astype(np.float32)
+    t = dev.tensor_new(x)
+    for temp, top_p in ((0.1, 0.9), (1.0, 0.95)):
+        dev.sample_seed(1234)
+        got = [int(dev.tensor_sample(t, temp, top_p).to_numpy()[0]) for _ in range(12)]
+        want = [_choice(dev, t, temp, top_p, u) for u in splitmix64_uniforms(1234, 12)]
+        assert got == want
+    assert len(set(got)) > 1  # temp 1: the draws spread over several tokens
 
 
 # ------------------------------------------------------ scaled dot-product attention

@@ -210,6 +210,55 @@ def test_argmax_last_among_ties_and_nan():
     assert oracle.argmax_last(np.array([1, 9, np.nan], np.float32)) == 2
 
 
+def test_sample_top_p_closed_forms():
+    """sample_impl (tensor.rs:1626-1680) on distributions whose cutoff and choice follow by
+    hand."""
+    ln3 = math.log(3.0)
+    # probs (1/4, 3/4): order [1, 0], running sums 3/4, 1
+    assert oracle.sample([0.0, ln3], 1.0, 0.9, 0.5) == 1   # cut after both; r = 0.5 <= 3/4
+    assert oracle.sample([0.0, ln3], 1.0, 0.9, 0.8) == 0   # r = 0.8 > 3/4: the second place
+    assert oracle.sample([0.0, ln3], 1.0, 0.9, 0.0) == 1   # r = 0: the first place
+    assert oracle.sample([0.0, ln3], 1.0, 0.5, 0.99) == 1  # 3/4 > 0.5: cut after the first
+    assert oracle.sample([0.0, ln3], 2.0, 0.9, 0.8) == 0   # probs (0.366, 0.634): r = 0.8
+    # four equal probs stay in index order: sums 0.25, 0.5, 0.75 > 0.6 -> cutoff 0.75
+    assert oracle.sample([1.0, 1.0, 1.0, 1.0], 1.0, 0.6, 0.5) == 1    # r = 0.375
+    assert oracle.sample([1.0, 1.0, 1.0, 1.0], 1.0, 0.6, 0.9) == 2    # r = 0.675
+    assert oracle.sample([1.0, 1.0, 1.0, 1.0], 1.0, 0.6, 0.0) == 0
+    assert oracle.sample([1.0, 1.0, 1.0, 1.0], 1.0, 1.5, 0.99) == 3   # never exceeds: all four
+    assert oracle.sample([1.0, 1.0, 1.0, 1.0], 1.0, -1.0, 0.99) == 0  # cut after the first
+    # the top-probability element first, then ties in index order: [3, 1, 1, 3] -> 0, 3, 1, 2
+    assert oracle.sample([3.0, 1.0, 1.0, 3.0], 1.0, 1.5, 0.6) == 3
+    # a NaN or infinite logit, or a NaN temp, makes every prob NaN: index 0
+    for x, t in (([1.0, np.nan, 3.0], 1.0), ([1.0, np.inf, 3.0], 1.0), ([-np.inf, -np.inf], 1.0),
+                 ([1.0, 2.0, 3.0], np.nan)):
+        assert oracle.sample(x, t, 0.6, 0.5) == 0
+    # temp <= 0: the greedy choice, last index among equal maxima
+    assert oracle.sample([1.0, 3.0, 3.0], 0.0, 0.6, 0.5) == 2
+    assert oracle.sample([1.0, 3.0, 3.0], -1.0, 0.6, 0.5) == 2
+    assert oracle.sample([], 1.0, 0.9, 0.5) == -1
+
+
+@pytest.mark.parametrize("temp", [0.1, 0.7, 1.0, 2.5])
+def test_sample_top_p_against_float64(temp):
+    """The oracle's choice equals the float64 restatement (numpy stable argsort, cumulative
+    sums) wherever top_p and r are clear of the f32 rounding of every running sum."""
+    from sampling_f64 import bracketed, decided, sample_f64
+    rng = np.random.default_rng(int(temp * 1000))
+    checked = total = 0
+    for n in (2, 17, 300, 4000):
+        x = (rng.standard_normal(n) * 3).astype(np.float32)
+        for top_p in (0.9, 0.5, 0.99, 0.0, 0.75):  # (top_p 1.0 sits on the last running sums)
+            for u in rng.random(6):
+                sel, margin, drift = sample_f64(x, temp, top_p, u)
+                got = oracle.sample(x, temp, top_p, u)
+                assert bracketed(x, temp, top_p, u, got, tol=4e-6 + 4 * drift), (n, top_p, u)
+                total += 1
+                if decided(margin, drift):
+                    checked += 1
+                    assert got == sel, (n, top_p, u)
+    assert checked >= 0.9 * total
+
+
 def test_glue_ops_match_numpy():
     rng = np.random.default_rng(8)
     x = rng.standard_normal((2, 3, 4, 5)).astype(np.float32)

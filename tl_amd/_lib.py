@@ -92,6 +92,8 @@ PROTOS = {
     "tl_hip_tensor_repeat_interleave": (P, [P, i64, i64]),
     "tl_hip_tensor_embedding": (P, [P, P]),
     "tl_hip_tensor_sample": (P, [P, f32, f32]),
+    "tl_hip_tensor_sample_uniform": (P, [P, f32, f32, f64]),
+    "tl_hip_sample_seed": (None, [C.c_uint64]),
     "tl_hip_tensor_argmax_all": (i64, [P]),
     "tl_hip_tensor_repetition_penalty": (P, [P, P, f64]),
     "tl_hip_fused_silu_mul": (P, [P, P]),

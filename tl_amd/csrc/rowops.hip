@@ -7,6 +7,7 @@
 
 #include <cmath>
 #include <cstring>
+#include <random>
 #include <vector>
 
 namespace tlhip {
@@ -692,6 +693,267 @@ int launch_rep_penalty(const float* x, const uint8_t* seen, float* o, int64_t ro
     return e == hipSuccess ? TL_HIP_OK : hip_fail(e, "repetition penalty launch");
 }
 
+// ------------------------------------------------------------- top-p sampling ---------
+// The stochastic branch of sample_impl (tensor.rs:1641-1679) for a given uniform draw u:
+//   p_i = x_i / temp, m = max p, prob_i = expf(p_i - m) / sum_j expf(p_j - m);
+//   order = the indices by descending prob, equal probs in index order (a stable sort);
+//   the cutoff is the first place in that order where the running sum of probs exceeds top_p
+//   (else the last place), cutoff_prob the running sum there;
+//   r = (f32) u * cutoff_prob, and the first place up to the cutoff where the running sum
+//   reaches r is chosen (order[0] when there is none).
+// A NaN among the p, or a max that is not finite, makes every prob NaN in the reference:
+// nothing compares, the order stays the index order and index 0 is chosen.
+// The order is never built.  "The first place where the running sum crosses T" is found by
+// a radix descent over the prob bits (non-negative floats order as their bit patterns):
+// four 8-bit digits from the top, each a histogram of (count, sum) over the elements that
+// share the digits found so far; the bin where everything above it plus the bin crosses T
+// holds the place.  After the last digit the prob value v there is known exactly and every
+// larger prob is summed; the place is the j-th element of value v in index order, j the
+// rank at which the sum crosses.  Sums are fixed point (prob * 2^48, integers, independent of
+// the order they are added in), so the choice is deterministic; they are the exact sums the
+// reference's f32 running sums round, and the two choices agree wherever T is not within that
+// rounding of a running sum.  Elements of prob 0 never move a running sum across T and are
+// skipped.
+constexpr int SMP_T = 1024;                      // one workgroup
+constexpr int SMP_E = 16;                        // elements per thread and round, loads issued together
+constexpr int64_t SMP_ROUND = (int64_t)SMP_T * SMP_E;
+constexpr double SMP_SCALE = 281474976710656.0;  // 2^48
+
+__device__ __forceinline__ unsigned long long smp_fx(uint32_t key) {
+    return (unsigned long long)((double)__uint_as_float(key) * SMP_SCALE);  // prob <= 1
+}
+
+struct SmpCross {
+    uint32_t key;              // prob bits of the place
+    uint32_t rank;             // 1-based rank among the elements of that prob, in index order
+    unsigned long long sum;    // running sum before the place's bin / at the place (fixed point)
+    int found;
+};
+
+struct SmpShared {
+    uint32_t cnt[256];
+    unsigned long long sum[256];
+    uint32_t wtot[SMP_T / 64];
+    SmpCross res;
+    int64_t pick;
+    float red[SMP_T / 64];
+};
+
+// f(i, x[i]) for every element, thread tid taking i = round base + e * SMP_T + tid: the
+// SMP_E loads of a round are in flight together.
+template <typename F>
+__device__ __forceinline__ void smp_each(const float* __restrict__ x, int64_t n, F f) {
+    for (int64_t base = 0; base < n; base += SMP_ROUND) {
+        float v[SMP_E];
+#pragma unroll
+        for (int e = 0; e < SMP_E; e++) {
+            const int64_t i = base + (int64_t)e * SMP_T + threadIdx.x;
+            v[e] = i < n ? x[i] : 0.0f;
+        }
+#pragma unroll
+        for (int e = 0; e < SMP_E; e++) {
+            const int64_t i = base + (int64_t)e * SMP_T + threadIdx.x;
+            if (i < n) f(i, v[e]);
+        }
+    }
+}
+
+// First place in the order where the running sum is > t (strict) or >= t.  Every thread
+// calls it and gets the result.
+__device__ SmpCross smp_cross(const uint32_t* __restrict__ key, int64_t n, unsigned long long t, bool strict,
+                              SmpShared& sh) {
+    const int tid = threadIdx.x, lane = tid & 63;
+    uint32_t prefix = 0, mask = 0;
+    unsigned long long above = 0;
+    for (int d = 3; d >= 0; d--) {
+        const int s = 8 * d;
+        for (int b = tid; b < 256; b += SMP_T) {
+            sh.cnt[b] = 0;
+            sh.sum[b] = 0;
+        }
+        __syncthreads();
+        for (int64_t base = 0; base < n; base += SMP_ROUND) {  // the same trip counts in every lane
+            uint32_t kv[SMP_E];
+#pragma unroll
+            for (int e = 0; e < SMP_E; e++) {
+                const int64_t i = base + (int64_t)e * SMP_T + tid;
+                kv[e] = i < n ? key[i] : 0u;
+            }
+#pragma unroll
+            for (int e = 0; e < SMP_E; e++) {
+                const uint32_t k = kv[e];
+                const bool in = k != 0u && (k & mask) == prefix;
+                const uint32_t dig = (k >> s) & 255u;
+                const unsigned long long pb = __ballot(in);
+                if (pb == 0) continue;
+                const int first = __builtin_amdgcn_readfirstlane(__ffsll(pb) - 1);
+                const uint32_t d0 = __builtin_amdgcn_readlane(dig, first);
+                if (__ballot(in && dig == d0) == pb) {  // the wavefront's share falls in one bin
+                    unsigned long long v = in ? smp_fx(k) : 0ull;
+                    for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off);
+                    if (lane == first) {
+                        atomicAdd(&sh.cnt[d0], (uint32_t)__popcll(pb));
+                        atomicAdd(&sh.sum[d0], v);
+                    }
+                } else if (in) {
+                    atomicAdd(&sh.cnt[dig], 1u);
+                    atomicAdd(&sh.sum[dig], smp_fx(k));
+                }
+            }
+        }
+        __syncthreads();
+        if (tid < 64) {
+            // lane l holds bins 255 - 4 l - q, q = 0..3 (the running sum goes from the top
+            // bin down): an exclusive scan over the lanes gives each lane its starting sum
+            uint32_t c[4];
+            unsigned long long sm[4], loc = 0;
+#pragma unroll
+            for (int q = 0; q < 4; q++) {
+                c[q] = sh.cnt[255 - 4 * lane - q];
+                sm[q] = sh.sum[255 - 4 * lane - q];
+                loc += sm[q];
+            }
+            unsigned long long inc = loc;
+            for (int off = 1; off < 64; off <<= 1) {
+                const unsigned long long y = __shfl_up(inc, off);
+                if (lane >= off) inc += y;
+            }
+            unsigned long long run = above + inc - loc, hit_run = 0;
+            int hit = -1;
+#pragma unroll
+            for (int q = 0; q < 4; q++) {
+                if (!c[q]) continue;
+                const unsigned long long nx = run + sm[q];
+                if (hit < 0 && (strict ? nx > t : nx >= t)) {
+                    hit = q;
+                    hit_run = run;
+                }
+                run = nx;
+            }
+            const unsigned long long hb = __ballot(hit >= 0);
+            if (hb == 0) {
+                if (lane == 0) sh.res = SmpCross{0u, 0u, 0ull, 0};
+            } else if (lane == __ffsll(hb) - 1) {
+                sh.res = SmpCross{(uint32_t)(255 - 4 * lane - hit), c[hit], hit_run, 1};
+            }
+        }
+        __syncthreads();
+        const SmpCross r = sh.res;
+        __syncthreads();  // sh is rewritten by the next level
+        if (!r.found) return r;
+        prefix |= r.key << s;
+        mask |= 255u << s;
+        above = r.sum;
+        if (d == 0) {
+            // r.rank elements of value v, in index order: the j-th moves the sum across t
+            // (above <= t when strict, above < t otherwise: the place was not passed yet)
+            const unsigned long long v = smp_fx(prefix);  // > 0: a bin of zero sum never crosses t
+            unsigned long long j = v == 0 ? 1 : strict ? (t - above) / v + 1 : (t - above + v - 1) / v;
+            if (j < 1) j = 1;
+            if (j > r.rank) j = r.rank;
+            return SmpCross{prefix, (uint32_t)j, above + j * v, 1};
+        }
+    }
+    return SmpCross{0u, 0u, 0ull, 0};
+}
+
+// Index of the j-th element (1-based, index order) whose key is kv: thread t counts its
+// contiguous chunk, a workgroup scan places the chunk, and its owner walks it.
+__device__ int64_t smp_nth(const uint32_t* __restrict__ key, int64_t n, uint32_t kv, uint32_t j, SmpShared& sh) {
+    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+    const int64_t c_len = (n + SMP_T - 1) / SMP_T, lo = tid * c_len, hi = lo + c_len < n ? lo + c_len : n;
+    uint32_t c = 0;
+    for (int64_t b = lo; b < hi; b += SMP_E) {
+        uint32_t kk[SMP_E];
+#pragma unroll
+        for (int e = 0; e < SMP_E; e++) kk[e] = b + e < hi ? key[b + e] : ~kv;
+#pragma unroll
+        for (int e = 0; e < SMP_E; e++) c += kk[e] == kv;
+    }
+    uint32_t inc = c;  // inclusive scan over the wavefront
+    for (int off = 1; off < 64; off <<= 1) {
+        const uint32_t y = __shfl_up(inc, off);
+        if (lane >= off) inc += y;
+    }
+    if (lane == 63) sh.wtot[w] = inc;
+    if (tid == 0) sh.pick = 0;
+    __syncthreads();
+    uint32_t woff = 0;
+    for (int q = 0; q < w; q++) woff += sh.wtot[q];
+    const uint32_t ex = woff + inc - c;
+    if (c && ex < j && j <= ex + c) {
+        uint32_t need = j - ex;
+        for (int64_t i = lo; i < hi; i++)
+            if (key[i] == kv && --need == 0) {
+                sh.pick = i;
+                break;
+            }
+    }
+    __syncthreads();
+    return sh.pick;
+}
+
+__global__ __launch_bounds__(SMP_T) void k_sample_top_p(const float* __restrict__ x, int64_t n, float temp,
+                                                        float top_p, float u, uint32_t* __restrict__ key,
+                                                        float* __restrict__ out) {
+    __shared__ SmpShared sh;
+    const int tid = threadIdx.x;
+    // p = x / temp and its max (the fold `if a > b { a } else { b }`: the max value when no
+    // p is NaN)
+    float mx = -INFINITY;
+    int bad = 0;
+    smp_each(x, n, [&](int64_t, float xv) {
+        const float p = xv / temp;
+        bad |= p != p;
+        mx = mx > p ? mx : p;
+    });
+    bad = __syncthreads_or(bad);
+    mx = block_max(mx, sh.red);
+    if (bad || !(fabsf(mx) <= 3.402823466e38f)) {
+        if (tid == 0) *out = 0.0f;
+        return;
+    }
+    float se = 0.f;
+    smp_each(x, n, [&](int64_t, float xv) { se += expf(xv / temp - mx); });
+    se = block_sum(se, sh.red);
+    unsigned long long tot = 0;  // exact sum of every prob
+    smp_each(x, n, [&](int64_t i, float xv) {
+        const uint32_t k = __float_as_uint(expf(xv / temp - mx) / se);
+        key[i] = k;
+        tot += smp_fx(k);
+    });
+    for (int off = 32; off >= 1; off >>= 1) tot += __shfl_xor(tot, off);
+    __syncthreads();  // key[] complete for the workgroup
+    if ((tid & 63) == 0) sh.sum[tid >> 6] = tot;
+    __syncthreads();
+    tot = 0;
+    for (int q = 0; q < SMP_T / 64; q++) tot += sh.sum[q];
+    __syncthreads();
+    // cutoff: first running sum > top_p (a NaN top_p compares false: no cutoff; the sum of
+    // all probs is about 1, so no top_p >= 2^16 is exceeded either)
+    SmpCross cut{0u, 0u, 0ull, 0};
+    if (top_p == top_p && top_p < 65536.0f)
+        cut = smp_cross(key, n, top_p < 0.0f ? 0ull : (unsigned long long)floor((double)top_p * SMP_SCALE), true, sh);
+    const float cutoff_prob = (float)((double)(cut.found ? cut.sum : tot) / SMP_SCALE);
+    const float r = u * cutoff_prob;
+    SmpCross pick = smp_cross(key, n, (unsigned long long)ceil((double)r * SMP_SCALE), false, sh);
+    if (!pick.found || (cut.found && (pick.key < cut.key || (pick.key == cut.key && pick.rank > cut.rank))))
+        pick = smp_cross(key, n, 0ull, false, sh);  // order[0]: the largest prob, lowest index
+    const int64_t idx = smp_nth(key, n, pick.key, pick.rank, sh);
+    if (tid == 0) *out = (float)idx;
+}
+
+static int launch_sample_top_p(const float* x, int64_t n, float temp, float top_p, float u, uint32_t* key,
+                               float* out, hipStream_t s) {
+    if (n < 1 || n > INT32_MAX) {
+        set_error(TL_HIP_ERR_ARG, "ArgumentError: top-p sampling takes 1 .. 2^31 - 1 logits");
+        return TL_HIP_ERR_ARG;
+    }
+    k_sample_top_p<<<1, SMP_T, 0, s>>>(x, n, temp, top_p, u, key, out);
+    hipError_t e = hipGetLastError();
+    return e == hipSuccess ? TL_HIP_OK : hip_fail(e, "top-p sampling launch");
+}
+
 int launch_embedding(const float* table, const int32_t* ids, float* o, int64_t n, int64_t dim,
                      hipStream_t s) {
     if (n * dim == 0) return TL_HIP_OK;
@@ -1314,22 +1576,69 @@ int64_t tl_hip_tensor_argmax_all(const tl_hip_tensor* x) {
     return rc == TL_HIP_OK ? (int64_t)h : -1;
 }
 
-tl_hip_tensor* tl_hip_tensor_sample(const tl_hip_tensor* x, float temp, float top_p) {
-    (void)top_p;
+// The uniform draws of tl_hip_tensor_sample: splitmix64 per calling thread (the reference
+// draws from rand's thread-local generator, tensor.rs:1663-1666), seeded from the OS until
+// tl_hip_sample_seed fixes it; a draw is the top 53 bits scaled by 2^-53, in [0, 1), the
+// construction of rand's `gen::<f64>()`.
+static thread_local uint64_t g_smp_state = 0;
+static thread_local bool g_smp_seeded = false;
+
+static double smp_uniform() {
+    if (!g_smp_seeded) {
+        std::random_device rd;
+        g_smp_state = ((uint64_t)rd() << 32) ^ (uint64_t)rd();
+        g_smp_seeded = true;
+    }
+    uint64_t z = (g_smp_state += 0x9E3779B97F4A7C15ull);
+    z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
+    z = (z ^ (z >> 27)) * 0x94D049BB133111EBull;
+    z ^= z >> 31;
+    return (double)(z >> 11) * 0x1.0p-53;
+}
+
+static tl_hip_tensor* sample(const tl_hip_tensor* x, float temp, float top_p, const double* u) {
     if (!need(x, "logits")) return nullptr;
-    if (CT(x)->numel == 0) {
+    const Tensor* t = CT(x);
+    if (t->numel == 0) {
         set_error(TL_HIP_ERR_INTERNAL, "InternalError: Empty tensor for sampling");
         return nullptr;
     }
-    if (temp > 0.0f) {
-        set_error(TL_HIP_ERR_ARG, "ArgumentError: only greedy sampling (temp <= 0) is provided");
+    int64_t one = 1;
+    if (temp <= 0.0f) {  // greedy (a NaN temp takes the stochastic branch, as in the reference)
+        int64_t idx = tl_hip_tensor_argmax_all(x);
+        if (idx < 0) return nullptr;
+        float v = (float)idx;
+        return tl_hip_tensor_new(&v, &one, 1);
+    }
+    const double draw = u ? *u : smp_uniform();
+    Tensor* o = tensor_alloc(&one, 1);
+    if (!o) return nullptr;
+    uint32_t* key = (uint32_t*)dev_alloc((size_t)t->numel * sizeof(uint32_t));
+    if (!key) {
+        tensor_drop(o);
         return nullptr;
     }
-    int64_t idx = tl_hip_tensor_argmax_all(x);
-    if (idx < 0) return nullptr;
-    float v = (float)idx;
-    int64_t one = 1;
-    return tl_hip_tensor_new(&v, &one, 1);
+    // T::from_f64(u): the draw rounded to f32 (tensor.rs:1666)
+    int rc = launch_sample_top_p(t->f32(), t->numel, temp, top_p, (float)draw, key, o->f32(), cur_stream());
+    dev_free(key);
+    return finish(o, rc);
+}
+
+tl_hip_tensor* tl_hip_tensor_sample(const tl_hip_tensor* x, float temp, float top_p) {
+    return sample(x, temp, top_p, nullptr);
+}
+
+tl_hip_tensor* tl_hip_tensor_sample_uniform(const tl_hip_tensor* x, float temp, float top_p, double u) {
+    if (!(u >= 0.0 && u < 1.0)) {
+        set_error(TL_HIP_ERR_ARG, "ArgumentError: the uniform draw must lie in [0, 1), got %g", u);
+        return nullptr;
+    }
+    return sample(x, temp, top_p, &u);
+}
+
+void tl_hip_sample_seed(uint64_t seed) {
+    g_smp_state = seed;
+    g_smp_seeded = true;
 }
 
 tl_hip_tensor* tl_hip_tensor_repetition_penalty(const tl_hip_tensor* lh, const tl_hip_tensor* th,

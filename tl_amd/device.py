@@ -233,6 +233,12 @@ class HipDevice:
     def tensor_sample(self, logits, temp, top_p):
         return self._wrap(self.lib.tl_hip_tensor_sample(logits.handle, temp, top_p))
 
+    def tensor_sample_uniform(self, logits, temp, top_p, u):
+        return self._wrap(self.lib.tl_hip_tensor_sample_uniform(logits.handle, temp, top_p, u))
+
+    def sample_seed(self, seed):
+        self.lib.tl_hip_sample_seed(seed)
+
     def tensor_argmax_all(self, x):
         r = self.lib.tl_hip_tensor_argmax_all(x.handle)
         if r < 0:
