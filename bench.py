@@ -154,6 +154,20 @@ def _timed(dev, launch, reps):
     return ms.value / 1e3 / reps
 
 
+def bench_sample(dev, reps=100):
+    """Top-p sampling (tl_hip_tensor_sample_uniform, the chatbot's sample(temp, top_p) with
+    the draw given) over vocab-sized logits [32000] ~ N(0, 3): us per call back to back."""
+    rng = np.random.default_rng(0x5A41)
+    t = dev.tensor_new((rng.standard_normal(32000) * 3).astype(np.float32))
+    us = rng.random(reps)
+    rows = []
+    for temp, top_p in ((0.1, 0.9), (1.0, 0.9), (2.5, 0.95)):
+        sec = _timed(dev, lambda i: dev.tensor_sample_uniform(t, temp, top_p, float(us[i % reps])), reps)
+        rows.append({"n": 32000, "temp": temp, "top_p": top_p, "us": round(sec * 1e6, 2)})
+        log(f"[bench] sample top-p n=32000 temp={temp} top_p={top_p}: {sec * 1e6:.1f} us")
+    return rows
+
+
 def bench_gemm(dev, ms=(512, 128, 16), reps=20, shapes=None):
     """Quantized prefill GEMM on the f16 MFMA path (tl_hip_launch_quant_gemm, mode 1: the
     f32 -> f16 operand conversion + the MFMA kernel) at the configs[2] shapes and M values
@@ -601,6 +615,7 @@ def main():
                     help="only the configs[1] row-op leg plus a 64 MiB device copy (counter runs)")
     ap.add_argument("--prefill-only", action="store_true",
                     help="only the 32- and 512-token prefills of the Q4_0 and Q4_K_M decoders (kernel traces)")
+    ap.add_argument("--sample-only", action="store_true", help="only the top-p sampling leg (kernel traces)")
     ap.add_argument("--two-launch-merges", action="store_true",
                     help="split kernels merge their partials in a second kernel, not in-kernel (A/B runs)")
     args = ap.parse_args()
@@ -640,6 +655,9 @@ def main():
     if args.prefill_only:
         print(json.dumps({"prefill": bench_prefill(dev, cfg, args)}), flush=True)
         return
+    if args.sample_only:
+        print(json.dumps({"sample_top_p": bench_sample(dev)}), flush=True)
+        return
     if args.row_ops_only:
         rows = bench_row_ops(dev)
         copy_reference(dev)
@@ -673,11 +691,12 @@ def main():
                           "copy_bytes": 64 << 20}), flush=True)
         return
 
-    gemm = attn = qmv = qmv2 = rowops = None
+    gemm = attn = qmv = qmv2 = rowops = smp = None
     if not args.no_extra:
         qmv = bench_quant_matvec(dev)
         qmv2 = bench_matvec_shapes(dev)
         rowops = bench_row_ops(dev)
+        smp = bench_sample(dev)
         gemm = bench_gemm(dev)
         attn = bench_attention(dev)
 
@@ -757,6 +776,7 @@ def main():
         "quant_matvec": {"shape": "4096x4096, m=1", "unit": "GB/s", "peak": HBM_PEAK_GBS, "types": qmv,
                          "configs2_m1": qmv2},
         "row_ops": {"config": "configs[1]", "unit": "GB/s", "peak": HBM_PEAK_GBS, "ops": rowops},
+        "sample_top_p": {"unit": "us per call", "cases": smp},
         "q4_k_m_decode": kq,
     }
     print(json.dumps(out), flush=True)

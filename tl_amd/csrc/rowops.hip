@@ -707,9 +707,10 @@ int launch_rep_penalty(const float* x, const uint8_t* seen, float* o, int64_t ro
 // a radix descent over the prob bits (non-negative floats order as their bit patterns):
 // four 8-bit digits from the top, each a histogram of (count, sum) over the elements that
 // share the digits found so far; the bin where everything above it plus the bin crosses T
-// holds the place.  After the last digit the prob value v there is known exactly and every
-// larger prob is summed; the place is the j-th element of value v in index order, j the
-// rank at which the sum crosses.  Sums are fixed point (prob * 2^48, integers, independent of
+// holds the place, and a bin holding one element is the place itself (the descent stops
+// there).  After the last digit the prob value v there is known exactly and every larger
+// prob is summed; the place is the j-th element of value v in index order, j the rank at
+// which the sum crosses.  Sums are fixed point (prob * 2^48, integers, independent of
 // the order they are added in), so the choice is deterministic; they are the exact sums the
 // reference's f32 running sums round, and the two choices agree wherever T is not within that
 // rounding of a running sum.  Elements of prob 0 never move a running sum across T and are
@@ -724,16 +725,22 @@ __device__ __forceinline__ unsigned long long smp_fx(uint32_t key) {
 }
 
 struct SmpCross {
-    uint32_t key;              // prob bits of the place
+    uint32_t key;              // prob bits of the place (the bits under `mask`)
     uint32_t rank;             // 1-based rank among the elements of that prob, in index order
     unsigned long long sum;    // running sum before the place's bin / at the place (fixed point)
     int found;
+    uint32_t mask;             // bits of key that are known: all, or the leading digits of the
+                               // place's bin when that bin holds the place alone
+    unsigned long long bin;    // the bin's sum (fixed point)
 };
+
+constexpr int SMP_RE = 32;  // elements per thread kept in registers: n <= SMP_T * SMP_RE (vocab sizes)
 
 struct SmpShared {
     uint32_t cnt[256];
     unsigned long long sum[256];
     uint32_t wtot[SMP_T / 64];
+    uint32_t rc[SMP_RE * (SMP_T / 64)];  // (row, wavefront) match counts of smp_nth_reg
     SmpCross res;
     int64_t pick;
     float red[SMP_T / 64];
@@ -758,10 +765,70 @@ __device__ __forceinline__ void smp_each(const float* __restrict__ x, int64_t n,
     }
 }
 
-// First place in the order where the running sum is > t (strict) or >= t.  Every thread
-// calls it and gets the result.
-__device__ SmpCross smp_cross(const uint32_t* __restrict__ key, int64_t n, unsigned long long t, bool strict,
-                              SmpShared& sh) {
+// Wavefront sum of fixed-point values held as doubles: every partial sum is an integer below
+// 2^53 (all probs add up to about 2^48), so double additions are exact in any order.  Lane
+// exchanges by permlane swaps across rows and DPP row rotations within them, as wave_allsum.
+__device__ __forceinline__ double smp_bits_d(uint32_t lo, uint32_t hi) {
+    return __builtin_bit_cast(double, (unsigned long long)hi << 32 | lo);
+}
+template <int OFF>
+__device__ __forceinline__ double smp_xor_d(double v) {
+    const unsigned long long b = __builtin_bit_cast(unsigned long long, v);
+    return smp_bits_d(lane_xor_u32<OFF>((uint32_t)b), lane_xor_u32<OFF>((uint32_t)(b >> 32)));
+}
+template <int CTRL>
+__device__ __forceinline__ double smp_dpp_d(double v) {
+    const unsigned long long b = __builtin_bit_cast(unsigned long long, v);
+    return smp_bits_d((uint32_t)__builtin_amdgcn_mov_dpp((int)(uint32_t)b, CTRL, 0xF, 0xF, true),
+                      (uint32_t)__builtin_amdgcn_mov_dpp((int)(uint32_t)(b >> 32), CTRL, 0xF, 0xF, true));
+}
+__device__ __forceinline__ unsigned long long smp_wave_sum(unsigned long long x) {
+    double v = (double)x;
+    v += smp_xor_d<32>(v);
+    v += smp_xor_d<16>(v);
+    v += smp_dpp_d<0x128>(v);
+    v += smp_dpp_d<0x124>(v);
+    v += smp_dpp_d<0x122>(v);
+    v += smp_dpp_d<0x121>(v);
+    return (unsigned long long)v;
+}
+
+// One element into the level's histogram (every lane of the wavefront calls it; `in` says
+// whether this lane's key takes part).  A wavefront whose 16 or more takers share the first
+// taker's bin adds them with one reduction and one atomic pair; the rest add their own.
+__device__ __forceinline__ void smp_add(uint32_t k, bool in, uint32_t dig, SmpShared& sh) {
+    // (k is opaque here so the compiler does not hoist every key's 64-bit fixed-point value out
+    // of the level loop: 32 of them would not fit in the registers beside the keys)
+    asm volatile("" : "+v"(k));
+    unsigned long long pb = __ballot(in);
+    if (pb == 0) return;
+    const int lane = threadIdx.x & 63;
+    bool own = in;
+    for (int peel = 0; peel < 4 && __popcll(pb) >= 16; peel++) {
+        const int first = __builtin_amdgcn_readfirstlane(__ffsll(pb) - 1);
+        const uint32_t d0 = __builtin_amdgcn_readlane(dig, first);
+        const bool grp = own && dig == d0;
+        const unsigned long long gb = __ballot(grp);
+        if (__popcll(gb) < 16) break;
+        const unsigned long long v = smp_wave_sum(grp ? smp_fx(k) : 0ull);
+        if (lane == first) {
+            atomicAdd(&sh.cnt[d0], (uint32_t)__popcll(gb));
+            atomicAdd(&sh.sum[d0], v);
+        }
+        own = own && !grp;
+        pb &= ~gb;
+    }
+    if (own) {
+        atomicAdd(&sh.cnt[dig], 1u);
+        atomicAdd(&sh.sum[dig], smp_fx(k));
+    }
+}
+
+// First place in the order where the running sum is > t (strict) or >= t.  each(f) calls
+// f(key) for every element with the same trip count in every lane (keys past n are 0).
+// Every thread calls it and gets the result.
+template <typename EachKey>
+__device__ __forceinline__ SmpCross smp_cross(EachKey each, unsigned long long t, bool strict, SmpShared& sh) {
     const int tid = threadIdx.x, lane = tid & 63;
     uint32_t prefix = 0, mask = 0;
     unsigned long long above = 0;
@@ -772,35 +839,7 @@ __device__ SmpCross smp_cross(const uint32_t* __restrict__ key, int64_t n, unsig
             sh.sum[b] = 0;
         }
         __syncthreads();
-        for (int64_t base = 0; base < n; base += SMP_ROUND) {  // the same trip counts in every lane
-            uint32_t kv[SMP_E];
-#pragma unroll
-            for (int e = 0; e < SMP_E; e++) {
-                const int64_t i = base + (int64_t)e * SMP_T + tid;
-                kv[e] = i < n ? key[i] : 0u;
-            }
-#pragma unroll
-            for (int e = 0; e < SMP_E; e++) {
-                const uint32_t k = kv[e];
-                const bool in = k != 0u && (k & mask) == prefix;
-                const uint32_t dig = (k >> s) & 255u;
-                const unsigned long long pb = __ballot(in);
-                if (pb == 0) continue;
-                const int first = __builtin_amdgcn_readfirstlane(__ffsll(pb) - 1);
-                const uint32_t d0 = __builtin_amdgcn_readlane(dig, first);
-                if (__ballot(in && dig == d0) == pb) {  // the wavefront's share falls in one bin
-                    unsigned long long v = in ? smp_fx(k) : 0ull;
-                    for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off);
-                    if (lane == first) {
-                        atomicAdd(&sh.cnt[d0], (uint32_t)__popcll(pb));
-                        atomicAdd(&sh.sum[d0], v);
-                    }
-                } else if (in) {
-                    atomicAdd(&sh.cnt[dig], 1u);
-                    atomicAdd(&sh.sum[dig], smp_fx(k));
-                }
-            }
-        }
+        each([&](uint32_t k) { smp_add(k, k != 0u && (k & mask) == prefix, (k >> s) & 255u, sh); });
         __syncthreads();
         if (tid < 64) {
             // lane l holds bins 255 - 4 l - q, q = 0..3 (the running sum goes from the top
@@ -832,9 +871,9 @@ __device__ SmpCross smp_cross(const uint32_t* __restrict__ key, int64_t n, unsig
             }
             const unsigned long long hb = __ballot(hit >= 0);
             if (hb == 0) {
-                if (lane == 0) sh.res = SmpCross{0u, 0u, 0ull, 0};
+                if (lane == 0) sh.res = SmpCross{0u, 0u, 0ull, 0, 0u, 0ull};
             } else if (lane == __ffsll(hb) - 1) {
-                sh.res = SmpCross{(uint32_t)(255 - 4 * lane - hit), c[hit], hit_run, 1};
+                sh.res = SmpCross{(uint32_t)(255 - 4 * lane - hit), c[hit], hit_run, 1, 0u, sm[hit]};
             }
         }
         __syncthreads();
@@ -844,6 +883,8 @@ __device__ SmpCross smp_cross(const uint32_t* __restrict__ key, int64_t n, unsig
         prefix |= r.key << s;
         mask |= 255u << s;
         above = r.sum;
+        if (r.rank == 1)  // the bin holds one element: it is the place
+            return SmpCross{prefix, 1u, above + r.bin, 1, mask, r.bin};
         if (d == 0) {
             // r.rank elements of value v, in index order: the j-th moves the sum across t
             // (above <= t when strict, above < t otherwise: the place was not passed yet)
@@ -851,24 +892,35 @@ __device__ SmpCross smp_cross(const uint32_t* __restrict__ key, int64_t n, unsig
             unsigned long long j = v == 0 ? 1 : strict ? (t - above) / v + 1 : (t - above + v - 1) / v;
             if (j < 1) j = 1;
             if (j > r.rank) j = r.rank;
-            return SmpCross{prefix, (uint32_t)j, above + j * v, 1};
+            return SmpCross{prefix, (uint32_t)j, above + j * v, 1, ~0u, v};
         }
     }
-    return SmpCross{0u, 0u, 0ull, 0};
+    return SmpCross{0u, 0u, 0ull, 0, 0u, 0ull};
 }
 
-// Index of the j-th element (1-based, index order) whose key is kv: thread t counts its
-// contiguous chunk, a workgroup scan places the chunk, and its owner walks it.
-__device__ int64_t smp_nth(const uint32_t* __restrict__ key, int64_t n, uint32_t kv, uint32_t j, SmpShared& sh) {
+// Whether place a comes after place b in the order.  Compared on the bits both know: a
+// partial key is the only element of its bin, so a place that matches it there is the same
+// element.
+__device__ __forceinline__ bool smp_after(const SmpCross& a, const SmpCross& b) {
+    const uint32_t m = a.mask & b.mask;
+    if ((a.key & m) != (b.key & m)) return (a.key & m) < (b.key & m);
+    return a.mask == ~0u && b.mask == ~0u && a.rank > b.rank;
+}
+
+// Index of the j-th element (1-based, index order) whose key is kv, keys in global memory:
+// thread t counts its contiguous chunk, a workgroup scan places the chunk, and its owner
+// walks it.
+__device__ int64_t smp_nth(const uint32_t* __restrict__ key, int64_t n, uint32_t kv, uint32_t km, uint32_t j,
+                           SmpShared& sh) {
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
     const int64_t c_len = (n + SMP_T - 1) / SMP_T, lo = tid * c_len, hi = lo + c_len < n ? lo + c_len : n;
     uint32_t c = 0;
     for (int64_t b = lo; b < hi; b += SMP_E) {
         uint32_t kk[SMP_E];
 #pragma unroll
-        for (int e = 0; e < SMP_E; e++) kk[e] = b + e < hi ? key[b + e] : ~kv;
+        for (int e = 0; e < SMP_E; e++) kk[e] = b + e < hi ? key[b + e] : 0u;
 #pragma unroll
-        for (int e = 0; e < SMP_E; e++) c += kk[e] == kv;
+        for (int e = 0; e < SMP_E; e++) c += kk[e] != 0u && (kk[e] & km) == kv;
     }
     uint32_t inc = c;  // inclusive scan over the wavefront
     for (int off = 1; off < 64; off <<= 1) {
@@ -884,7 +936,7 @@ __device__ int64_t smp_nth(const uint32_t* __restrict__ key, int64_t n, uint32_t
     if (c && ex < j && j <= ex + c) {
         uint32_t need = j - ex;
         for (int64_t i = lo; i < hi; i++)
-            if (key[i] == kv && --need == 0) {
+            if (key[i] != 0u && (key[i] & km) == kv && --need == 0) {
                 sh.pick = i;
                 break;
             }
@@ -893,6 +945,63 @@ __device__ int64_t smp_nth(const uint32_t* __restrict__ key, int64_t n, uint32_t
     return sh.pick;
 }
 
+// The same for keys in registers, element (e, tid) = index e * SMP_T + tid: index order is row
+// e, then wavefront, then lane.  Per (row, wavefront) counts go to LDS; wavefront 0 scans the
+// SMP_RE * 16 counts (eight per lane) and the chosen wavefront finds its lane in one ballot.
+__device__ __forceinline__ int64_t smp_nth_reg(const uint32_t (&kv)[SMP_RE], uint32_t target, uint32_t km, uint32_t j,
+                               SmpShared& sh) {
+    constexpr int NW = SMP_T / 64, PER = SMP_RE * NW / 64;
+    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+#pragma unroll
+    for (int e = 0; e < SMP_RE; e++) {
+        const unsigned long long b = __ballot(kv[e] != 0u && (kv[e] & km) == target);
+        if (lane == 0) sh.rc[e * NW + w] = (uint32_t)__popcll(b);
+    }
+    if (tid == 0) sh.pick = 0;
+    __syncthreads();
+    if (tid < 64) {
+        uint32_t c[PER], loc = 0;
+#pragma unroll
+        for (int q = 0; q < PER; q++) {
+            c[q] = sh.rc[lane * PER + q];
+            loc += c[q];
+        }
+        uint32_t inc = loc;
+        for (int off = 1; off < 64; off <<= 1) {
+            const uint32_t y = __shfl_up(inc, off);
+            if (lane >= off) inc += y;
+        }
+        uint32_t run = inc - loc;
+        if (run < j && j <= inc) {  // this lane's counts hold the j-th
+#pragma unroll
+            for (int q = 0; q < PER; q++) {
+                if (run < j && j <= run + c[q]) {
+                    sh.res = SmpCross{(uint32_t)(lane * PER + q), j - run, 0ull, 1, 0u, 0ull};  // (row, wavefront), rank there
+                }
+                run += c[q];
+            }
+        }
+    }
+    __syncthreads();
+    const uint32_t rw = sh.res.key, need = sh.res.rank;
+    const int e_pick = (int)(rw / NW), w_pick = (int)(rw % NW);
+    if (w == w_pick) {
+        unsigned long long b = 0;
+#pragma unroll
+        for (int e = 0; e < SMP_RE; e++) {
+            const unsigned long long be = __ballot(kv[e] != 0u && (kv[e] & km) == target);
+            if (e == e_pick) b = be;
+        }
+        const unsigned long long below = lane ? b & ((1ull << lane) - 1ull) : 0ull;
+        if (((b >> lane) & 1ull) && (uint32_t)__popcll(below) + 1 == need) sh.pick = (int64_t)e_pick * SMP_T + tid;
+    }
+    __syncthreads();
+    return sh.pick;
+}
+
+// RES: n <= SMP_T * SMP_RE, every logit and key held in registers (one load pass, no scratch);
+// otherwise the keys go to `key` (n words) and every pass reads them back.
+template <bool RES>
 __global__ __launch_bounds__(SMP_T) void k_sample_top_p(const float* __restrict__ x, int64_t n, float temp,
                                                         float top_p, float u, uint32_t* __restrict__ key,
                                                         float* __restrict__ out) {
@@ -900,28 +1009,62 @@ __global__ __launch_bounds__(SMP_T) void k_sample_top_p(const float* __restrict_
     const int tid = threadIdx.x;
     // p = x / temp and its max (the fold `if a > b { a } else { b }`: the max value when no
     // p is NaN)
-    float mx = -INFINITY;
+    float mx = -INFINITY, se = 0.f;
     int bad = 0;
-    smp_each(x, n, [&](int64_t, float xv) {
-        const float p = xv / temp;
-        bad |= p != p;
-        mx = mx > p ? mx : p;
-    });
-    bad = __syncthreads_or(bad);
-    mx = block_max(mx, sh.red);
-    if (bad || !(fabsf(mx) <= 3.402823466e38f)) {
-        if (tid == 0) *out = 0.0f;
-        return;
-    }
-    float se = 0.f;
-    smp_each(x, n, [&](int64_t, float xv) { se += expf(xv / temp - mx); });
-    se = block_sum(se, sh.red);
     unsigned long long tot = 0;  // exact sum of every prob
-    smp_each(x, n, [&](int64_t i, float xv) {
-        const uint32_t k = __float_as_uint(expf(xv / temp - mx) / se);
-        key[i] = k;
-        tot += smp_fx(k);
-    });
+    uint32_t kv[RES ? SMP_RE : 1];
+    if constexpr (RES) {
+        float pv[SMP_RE];
+#pragma unroll
+        for (int e = 0; e < SMP_RE; e++) {
+            const int64_t i = (int64_t)e * SMP_T + tid;
+            pv[e] = i < n ? x[i] : 0.0f;
+        }
+#pragma unroll
+        for (int e = 0; e < SMP_RE; e++) {
+            if ((int64_t)e * SMP_T + tid >= n) continue;
+            pv[e] = pv[e] / temp;
+            bad |= pv[e] != pv[e];
+            mx = mx > pv[e] ? mx : pv[e];
+        }
+        bad = __syncthreads_or(bad);
+        mx = block_max(mx, sh.red);
+        if (bad || !(fabsf(mx) <= 3.402823466e38f)) {
+            if (tid == 0) *out = 0.0f;
+            return;
+        }
+#pragma unroll
+        for (int e = 0; e < SMP_RE; e++) {
+            if ((int64_t)e * SMP_T + tid >= n) continue;
+            pv[e] = expf(pv[e] - mx);
+            se += pv[e];
+        }
+        se = block_sum(se, sh.red);
+#pragma unroll
+        for (int e = 0; e < SMP_RE; e++) {
+            kv[e] = (int64_t)e * SMP_T + tid < n ? __float_as_uint(pv[e] / se) : 0u;
+            tot += smp_fx(kv[e]);
+        }
+    } else {
+        smp_each(x, n, [&](int64_t, float xv) {
+            const float p = xv / temp;
+            bad |= p != p;
+            mx = mx > p ? mx : p;
+        });
+        bad = __syncthreads_or(bad);
+        mx = block_max(mx, sh.red);
+        if (bad || !(fabsf(mx) <= 3.402823466e38f)) {
+            if (tid == 0) *out = 0.0f;
+            return;
+        }
+        smp_each(x, n, [&](int64_t, float xv) { se += expf(xv / temp - mx); });
+        se = block_sum(se, sh.red);
+        smp_each(x, n, [&](int64_t i, float xv) {
+            const uint32_t k = __float_as_uint(expf(xv / temp - mx) / se);
+            key[i] = k;
+            tot += smp_fx(k);
+        });
+    }
     for (int off = 32; off >= 1; off >>= 1) tot += __shfl_xor(tot, off);
     __syncthreads();  // key[] complete for the workgroup
     if ((tid & 63) == 0) sh.sum[tid >> 6] = tot;
@@ -929,17 +1072,36 @@ __global__ __launch_bounds__(SMP_T) void k_sample_top_p(const float* __restrict_
     tot = 0;
     for (int q = 0; q < SMP_T / 64; q++) tot += sh.sum[q];
     __syncthreads();
+    auto each = [&](auto f) {
+        if constexpr (RES) {
+#pragma unroll
+            for (int e = 0; e < SMP_RE; e++) f(kv[e]);
+        } else {
+            for (int64_t base = 0; base < n; base += SMP_ROUND) {  // the same trip counts in every lane
+                uint32_t kk[SMP_E];
+#pragma unroll
+                for (int e = 0; e < SMP_E; e++) {
+                    const int64_t i = base + (int64_t)e * SMP_T + tid;
+                    kk[e] = i < n ? key[i] : 0u;
+                }
+#pragma unroll
+                for (int e = 0; e < SMP_E; e++) f(kk[e]);
+            }
+        }
+    };
     // cutoff: first running sum > top_p (a NaN top_p compares false: no cutoff; the sum of
     // all probs is about 1, so no top_p >= 2^16 is exceeded either)
-    SmpCross cut{0u, 0u, 0ull, 0};
+    SmpCross cut{0u, 0u, 0ull, 0, 0u, 0ull};
     if (top_p == top_p && top_p < 65536.0f)
-        cut = smp_cross(key, n, top_p < 0.0f ? 0ull : (unsigned long long)floor((double)top_p * SMP_SCALE), true, sh);
+        cut = smp_cross(each, top_p < 0.0f ? 0ull : (unsigned long long)floor((double)top_p * SMP_SCALE), true, sh);
     const float cutoff_prob = (float)((double)(cut.found ? cut.sum : tot) / SMP_SCALE);
     const float r = u * cutoff_prob;
-    SmpCross pick = smp_cross(key, n, (unsigned long long)ceil((double)r * SMP_SCALE), false, sh);
-    if (!pick.found || (cut.found && (pick.key < cut.key || (pick.key == cut.key && pick.rank > cut.rank))))
-        pick = smp_cross(key, n, 0ull, false, sh);  // order[0]: the largest prob, lowest index
-    const int64_t idx = smp_nth(key, n, pick.key, pick.rank, sh);
+    SmpCross pick = smp_cross(each, (unsigned long long)ceil((double)r * SMP_SCALE), false, sh);
+    if (!pick.found || (cut.found && smp_after(pick, cut)))
+        pick = smp_cross(each, 0ull, false, sh);  // order[0]: the largest prob, lowest index
+    int64_t idx;
+    if constexpr (RES) idx = smp_nth_reg(kv, pick.key, pick.mask, pick.rank, sh);
+    else idx = smp_nth(key, n, pick.key, pick.mask, pick.rank, sh);
     if (tid == 0) *out = (float)idx;
 }
 
@@ -949,7 +1111,8 @@ static int launch_sample_top_p(const float* x, int64_t n, float temp, float top_
         set_error(TL_HIP_ERR_ARG, "ArgumentError: top-p sampling takes 1 .. 2^31 - 1 logits");
         return TL_HIP_ERR_ARG;
     }
-    k_sample_top_p<<<1, SMP_T, 0, s>>>(x, n, temp, top_p, u, key, out);
+    if (n <= (int64_t)SMP_T * SMP_RE) k_sample_top_p<true><<<1, SMP_T, 0, s>>>(x, n, temp, top_p, u, nullptr, out);
+    else k_sample_top_p<false><<<1, SMP_T, 0, s>>>(x, n, temp, top_p, u, key, out);
     hipError_t e = hipGetLastError();
     return e == hipSuccess ? TL_HIP_OK : hip_fail(e, "top-p sampling launch");
 }
@@ -1613,14 +1776,15 @@ static tl_hip_tensor* sample(const tl_hip_tensor* x, float temp, float top_p, co
     const double draw = u ? *u : smp_uniform();
     Tensor* o = tensor_alloc(&one, 1);
     if (!o) return nullptr;
-    uint32_t* key = (uint32_t*)dev_alloc((size_t)t->numel * sizeof(uint32_t));
-    if (!key) {
+    // the key scratch: only for inputs past what the kernel holds in registers
+    uint32_t* key = nullptr;
+    if (t->numel > (int64_t)SMP_T * SMP_RE && !(key = (uint32_t*)dev_alloc((size_t)t->numel * sizeof(uint32_t)))) {
         tensor_drop(o);
         return nullptr;
     }
     // T::from_f64(u): the draw rounded to f32 (tensor.rs:1666)
     int rc = launch_sample_top_p(t->f32(), t->numel, temp, top_p, (float)draw, key, o->f32(), cur_stream());
-    dev_free(key);
+    if (key) dev_free(key);
     return finish(o, rc);
 }
 
