@@ -484,7 +484,9 @@ def bench_decode(dev, cfg, ggml_type, args, steps=None, variants=()):
     unless --no-graph); returns (tok/s, decode seconds, prefill seconds, 32-token prefill
     seconds, variant rows).  The warm-up generate captures the decode step; the timed one
     must replay it without a new capture (checked with the library's capture counter).
-    `variants` are further (kv, penalty) settings timed the same way on the same weights."""
+    `variants` are further (kv, penalty[, temp, top_p]) settings timed the same way on the same
+    weights; with temp > 0 every token is sampled (sample(temp, top_p), seeded draws), as the
+    chatbot does with (0.1, 0.9)."""
     from tl_amd.llama import HipLlama, synthetic_prompt, synthetic_weights
 
     steps = steps or args.steps
@@ -518,10 +520,12 @@ def bench_decode(dev, cfg, ggml_type, args, steps=None, variants=()):
         short_s = time.perf_counter() - t0
     log(f"[bench] prefill 32 tokens: {short_s * 1e3:.2f} ms")
 
-    def timed_decode(penalty):
+    def timed_decode(penalty, temp=0.0, top_p=1.0):
         model.reset()
         model.forward(prompt, prefill_f16=True, want_logits=False)
-        first = model.sample_greedy(penalty, prompt)
+        model.lib.tl_hip_sample_seed(1234)
+        first = model.sample(temp, top_p, penalty, prompt)
+        model.set_sampling(temp, top_p)
         hist = np.concatenate([prompt, [first]]).astype(np.int32)
         warm = model.generate(first, args.warmup, penalty, hist, use_graph=not args.no_graph) \
             if args.warmup else np.array([first], np.int32)
@@ -533,6 +537,7 @@ def bench_decode(dev, cfg, ggml_type, args, steps=None, variants=()):
         model.generate(nxt, steps, penalty, hist, use_graph=not args.no_graph)  # ends with a stream synchronize
         dev.synchronize()
         dt = time.perf_counter() - t0
+        model.set_sampling(0.0)
         if args.warmup and not args.no_graph and model.lib.tl_hip_llama_graph_builds(model.h) != builds:
             raise RuntimeError("the timed decode captured a new graph")
         return dt
@@ -541,13 +546,17 @@ def bench_decode(dev, cfg, ggml_type, args, steps=None, variants=()):
     tok_s = steps / decode_s
     log(f"[bench] decode {steps} tokens: {decode_s * 1e3:.1f} ms -> {tok_s:.1f} tok/s")
     rows = []
-    for kv, pen in variants:
+    for kv, pen, *smp in variants:
+        temp, top_p = smp if smp else (0.0, 1.0)
         model.configure(kv_f16=(kv == "f16"))
-        dt = timed_decode(pen)
-        rows.append({"kv_cache": kv, "repetition_penalty": pen, "value": round(steps / dt, 2), "unit": "tok/s",
-                     "ms_per_step": round(dt * 1e3 / steps, 4)})
-        log(f"[bench] decode {steps} tokens, {kv} KV cache, penalty {pen}: {dt * 1e3:.1f} ms -> "
-            f"{steps / dt:.1f} tok/s")
+        dt = timed_decode(pen, temp, top_p)
+        row = {"kv_cache": kv, "repetition_penalty": pen, "value": round(steps / dt, 2), "unit": "tok/s",
+               "ms_per_step": round(dt * 1e3 / steps, 4)}
+        if temp > 0:
+            row["sample"] = {"temp": temp, "top_p": top_p}
+        rows.append(row)
+        log(f"[bench] decode {steps} tokens, {kv} KV cache, penalty {pen}"
+            + (f", sample({temp}, {top_p})" if temp > 0 else "") + f": {dt * 1e3:.1f} ms -> {steps / dt:.1f} tok/s")
     model.close()
     return tok_s, decode_s, prefill_s, short_s, rows
 
@@ -702,7 +711,7 @@ def main():
 
     other_kv = "f32" if args.kv == "f16" else "f16"
     tok_s, decode_s, prefill_s, short_s, variants = bench_decode(
-        dev, cfg, 2, args, variants=[(args.kv, 1.1), (other_kv, 1.0)])
+        dev, cfg, 2, args, variants=[(args.kv, 1.1), (other_kv, 1.0), (args.kv, 1.1, 0.1, 0.9)])
     kq = None
     if not args.no_extra:
         kq_tok_s, kq_decode_s, kq_prefill_s, kq_short_s, _ = bench_decode(dev, cfg, "Q4_K_M", args, steps=64)
@@ -751,7 +760,9 @@ def main():
             "prefill_32_ms": round(short_s * 1e3, 3),
         },
         "decode_variants": {"note": "the same model and prompt: the chatbot's repetition penalty 1.1 "
-                                    "(chatbot.tl:188) and the other KV-cache element type", "runs": variants},
+                                    "(chatbot.tl:188), the other KV-cache element type, and the chatbot's "
+                                    "loop as it runs: penalty 1.1 then sample(0.1, 0.9) every token "
+                                    "(chatbot.tl:189; seeded draws)", "runs": variants},
         "roofline": {
             "bound": "hbm",
             "kernel": "k_mv<Q4_0> 4096x4096 (m=1)",

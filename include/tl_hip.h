@@ -386,13 +386,24 @@ int tl_hip_llama_forward(tl_hip_llama* m, const int32_t* ids, int n, float* logi
  * (tensor.rs:1633-1637); returns the token id or -1 on error. */
 int32_t tl_hip_llama_sample_greedy(tl_hip_llama* m, double repetition_penalty,
                                    const int32_t* history, int n_history);
-/* Greedy decode of n_steps tokens after the cached context (chatbot.tl:188-222 with
- * sample(temp <= 0) = argmax): first token id `first`, generated ids to out_ids (host).
- * repetition_penalty 1.0 disables the penalty; history holds the prior ids (host). With
- * use_graph != 0 the steps are captured hipGraph replays: one launch per eight steps, then
- * one per remaining step.  Both graph shapes (one step, eight steps) are captured on the
- * first graph-mode call after a change of penalty value, KV type or RoPE mode, whatever its
- * n_steps, so later calls only replay. */
+/* The next token from the logits of the last forward call as chatbot.tl:188-189 takes it:
+ * repetition_penalty(history, p), then sample(temp, top_p) (tensor.rs:1626-1680) with this
+ * library's per-thread uniform draw (tl_hip_sample_seed).  temp <= 0: as
+ * tl_hip_llama_sample_greedy.  Returns the token id or -1 on error. */
+int32_t tl_hip_llama_sample(tl_hip_llama* m, float temp, float top_p, double repetition_penalty,
+                            const int32_t* history, int n_history);
+/* How tl_hip_llama_generate chooses each token: temp <= 0 (the default) greedy; otherwise
+ * sample(temp, top_p) of the penalised logits, one uniform draw per step from the calling
+ * thread's generator, drawn in step order before the steps run.  NaN values are
+ * ArgumentError. */
+int tl_hip_llama_set_sampling(tl_hip_llama* m, float temp, float top_p);
+/* Decode of n_steps tokens after the cached context (chatbot.tl:174-222), each token chosen
+ * as tl_hip_llama_set_sampling says (greedy by default): first token id `first`, generated
+ * ids to out_ids (host).  repetition_penalty 1.0 disables the penalty; history holds the
+ * prior ids (host). With use_graph != 0 the steps are captured hipGraph replays: one launch
+ * per eight steps, then one per remaining step.  Both graph shapes (one step, eight steps)
+ * are captured on the first graph-mode call after a change of penalty value, KV type, RoPE
+ * mode or sampling settings, whatever its n_steps, so later calls only replay. */
 int tl_hip_llama_generate(tl_hip_llama* m, int32_t first, int n_steps, int32_t* out_ids,
                           double repetition_penalty, const int32_t* history, int n_history,
                           int use_graph);

@@ -338,6 +338,15 @@ extern "C" {
         history: *const i32,
         n_history: i32,
     ) -> i32;
+    pub fn tl_hip_llama_sample(
+        m: *mut tl_hip_llama,
+        temp: f32,
+        top_p: f32,
+        repetition_penalty: f64,
+        history: *const i32,
+        n_history: i32,
+    ) -> i32;
+    pub fn tl_hip_llama_set_sampling(m: *mut tl_hip_llama, temp: f32, top_p: f32) -> i32;
     pub fn tl_hip_llama_generate(
         m: *mut tl_hip_llama,
         first: i32,

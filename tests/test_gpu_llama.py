@@ -7,7 +7,8 @@ import numpy as np
 import pytest
 
 import oracle
-from tl_amd.llama import HipLlama, LlamaConfig, greedy_generate, synthetic_prompt, synthetic_weights
+from tl_amd import BackendError
+from tl_amd.llama import HipLlama, LlamaConfig, greedy_generate, sampled_generate, synthetic_prompt, synthetic_weights
 
 pytestmark = pytest.mark.gpu
 HERE = os.path.dirname(os.path.abspath(__file__))
@@ -238,6 +239,68 @@ def test_graph_follows_the_penalty_value(small):
         assert list(greedy_generate(gpu, prompt, n, penalty=1.1, use_graph=True)) == \
             list(cpu.greedy(prompt, n, penalty=1.1))
     assert builds() == b0
+
+
+def _oracle_sampled(cpu, prompt, n, temp, top_p, penalty, draws):
+    """chatbot.tl:174-222 on the oracle: penalty, then sample_impl at the given draws.  Yields
+    (token, logits) per step."""
+    cpu.reset()
+    toks, cur = [int(t) for t in prompt], [int(t) for t in prompt]
+    for i in range(n):
+        logits = cpu.forward(cur)
+        if penalty != 1.0:
+            logits = oracle.repetition_penalty(logits[None, :], np.array(toks, np.float32), penalty)[0]
+        nxt = oracle.sample(logits, temp, top_p, draws[i])
+        yield nxt, logits
+        toks.append(nxt)
+        cur = [nxt]
+
+
+@pytest.mark.parametrize("use_graph", [True, False])
+@pytest.mark.parametrize("temp,top_p,penalty", [(0.7, 0.9, 1.1), (0.1, 0.9, 1.1), (1.5, 0.95, 1.0)])
+def test_sampled_tokens_f32(small, use_graph, temp, top_p, penalty):
+    """The chatbot's decode as it runs (chatbot.tl:188-189: repetition_penalty(1.1), then
+    sample(0.1, 0.9) every token, the first from the prompt's logits) with seeded draws: the
+    device's tokens against the oracle's sample_impl at the same draws, step by step.  A step
+    may differ only where the f32 logits' rounding could move the choice -- the float64
+    margin of top_p / r from a running sum below 1e-3 -- and the comparison stops there."""
+    from sampling_f64 import sample_f64, splitmix64_uniforms
+    gpu, cpu = small
+    gpu.configure(kv_f16=False)
+    prompt = synthetic_prompt(SMALL, 13, 17)
+    n, seed = 24, 77
+    got = sampled_generate(gpu, prompt, n, temp, top_p, penalty=penalty, seed=seed, use_graph=use_graph)
+    draws = splitmix64_uniforms(seed, n)
+    for i, (want, logits) in enumerate(_oracle_sampled(cpu, prompt, n, temp, top_p, penalty, draws)):
+        if got[i] != want:
+            margin = sample_f64(logits, temp, top_p, draws[i])[1]
+            assert margin < 1e-3 and i >= 4, (i, int(got[i]), want, margin)
+            break
+    # the same seed replays the same tokens, graph or eager
+    again = sampled_generate(gpu, prompt, n, temp, top_p, penalty=penalty, seed=seed, use_graph=not use_graph)
+    assert list(again) == list(got)
+    if temp >= 0.7:
+        other = sampled_generate(gpu, prompt, n, temp, top_p, penalty=penalty, seed=seed + 1, use_graph=use_graph)
+        assert list(other) != list(got), "another seed drew the same 24 tokens"
+
+
+def test_sampling_settings_reach_the_graph(small):
+    """temp and top_p reach the captured step as kernel arguments: changing either captures
+    again, the same settings replay, and greedy decoding after sampling is unchanged."""
+    gpu, cpu = small
+    gpu.configure(kv_f16=False)
+    prompt = synthetic_prompt(SMALL, 14, 9)
+    builds = lambda: int(gpu.lib.tl_hip_llama_graph_builds(gpu.h))
+    greedy = list(cpu.greedy(prompt, 12, penalty=1.1))
+    for temp, top_p, new in ((0.8, 0.9, True), (0.8, 0.9, False), (0.8, 0.5, True), (1.2, 0.5, True)):
+        b0 = builds()
+        got = sampled_generate(gpu, prompt, 12, temp, top_p, penalty=1.1, seed=5, use_graph=True)
+        assert builds() == b0 + (2 if new else 0)
+        assert list(got) == list(sampled_generate(gpu, prompt, 12, temp, top_p, penalty=1.1, seed=5,
+                                                  use_graph=False))
+    assert list(greedy_generate(gpu, prompt, 12, penalty=1.1, use_graph=True)) == greedy
+    with pytest.raises(BackendError):
+        gpu.set_sampling(float("nan"), 0.9)
 
 
 @pytest.mark.parametrize("warm,timed", [(5, 20), (8, 3), (1, 9), (16, 7)])

@@ -118,6 +118,8 @@ PROTOS = {
     "tl_hip_llama_graph_builds": (i64, [P]),
     "tl_hip_llama_forward": (i32, [P, i32p, i32, f32p, i32]),
     "tl_hip_llama_sample_greedy": (C.c_int32, [P, f64, i32p, i32]),
+    "tl_hip_llama_sample": (C.c_int32, [P, f32, f32, f64, i32p, i32]),
+    "tl_hip_llama_set_sampling": (i32, [P, f32, f32]),
     "tl_hip_llama_generate": (i32, [P, C.c_int32, i32, i32p, f64, i32p, i32, i32]),
 }
 

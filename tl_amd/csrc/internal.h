@@ -190,6 +190,10 @@ struct MvArgs {
     int32_t* step;
     int32_t* pos_inc;     // position advanced by one (decode step end)
     int max_out;
+    // top-p sampling instead of the greedy finish when smp_temp > 0 (decode steps)
+    float smp_temp, smp_top_p;
+    const float* smp_draws;  // one uniform draw per step
+    uint32_t* smp_key;       // key scratch for vocabularies past 32768
 };
 struct QWeight;
 // One fused matvec launch over weight w (m = 1 or 2 activation rows); weight fields of `a`
@@ -487,6 +491,24 @@ int launch_swiglu(const float* g, const float* u, float* o, int64_t n, int mode,
 int launch_softmax(const float* x, float* out, int64_t outer, int64_t as, int64_t inner,
                    hipStream_t s);
 int launch_argmax(const float* x, int64_t n, int32_t* out_idx, hipStream_t s);
+// Top-p sampling (sample_impl's temp > 0 branch) of x [n] with the uniform draw u.  fin ==
+// nullptr: the index goes to out[0] as a float.  fin: the decode step's form -- u is
+// fin->draws[*fin->step] and the choice is recorded as the greedy finish records it.
+// Inputs of more than 32768 logits need a key scratch of sample_key_words(n) words.
+struct SmpFin {
+    const float* draws;
+    int32_t* tok_out;
+    int32_t* out_ids;
+    int32_t* step;
+    uint8_t* seen_out;
+    int32_t* pos_inc;
+    int max_out;
+};
+int launch_sample_top_p(const float* x, int64_t n, float temp, float top_p, float u, uint32_t* key, float* out,
+                        const SmpFin* fin, hipStream_t s);
+int sample_key_words(int64_t n);
+double sample_draw();            // the calling thread's next uniform draw in [0, 1)
+void sample_seed(uint64_t seed);
 int launch_rep_penalty(const float* x, const uint8_t* seen, float* o, int64_t rows,
                        int64_t vocab, float p, hipStream_t s);
 int launch_embedding(const float* table, const int32_t* ids, float* o, int64_t n, int64_t dim,

@@ -137,14 +137,20 @@ struct Llama {
     float* am_v = nullptr;
     int32_t *am_i = nullptr, *am_nan = nullptr;
     int max_out = 0;
+    // top-p sampling in generate (temp <= 0: greedy): one uniform draw per step, uploaded
+    // before the steps run; a key scratch for vocabularies past what the kernel holds in
+    // registers
+    float smp_temp = 0.0f, smp_top_p = 1.0f;
+    float* draws = nullptr;
+    uint32_t* smp_key = nullptr;
     int64_t host_pos = 0;
     // the decode step captured as hipGraphs: graph[0] holds one step, graph[1] GRAPH_STEPS
     // consecutive steps (one graph launch per GRAPH_STEPS tokens); both built on the first
     // graph-mode call for a key
     hipGraphExec_t graph[2] = {nullptr, nullptr};
     // what the captured steps were built for: penalty bits (the value is a kernel argument),
-    // kv_f16, rope_per_token
-    uint32_t graph_key[3] = {0xffffffffu, 0xffffffffu, 0xffffffffu};
+    // kv_f16, rope_per_token, sampling temp and top_p bits
+    uint32_t graph_key[5] = {0xffffffffu, 0xffffffffu, 0xffffffffu, 0xffffffffu, 0xffffffffu};
     int64_t graph_builds = 0;
 };
 
@@ -625,6 +631,10 @@ static int enqueue_step(Llama* m, float penalty, hipStream_t s) {
     h.step = m->step;
     h.pos_inc = m->pos;
     h.max_out = m->max_out;
+    h.smp_temp = m->smp_temp;
+    h.smp_top_p = m->smp_top_p;
+    h.smp_draws = m->draws;
+    h.smp_key = m->smp_key;
     return launch_mv(m->lm, h, 1, EPI_ARGMAX, true, false, s);
 }
 
@@ -682,8 +692,11 @@ tl_hip_llama* tl_hip_llama_new(int n_layers, int d_model, int n_heads, int n_kv_
     // captured step never has to be rebuilt for a longer call
     m->out_ids = (int32_t*)dev_alloc((size_t)max_seq * 4);
     m->max_out = max_seq;
+    m->draws = (float*)dev_alloc((size_t)max_seq * 4);
+    const int kw = sample_key_words(vocab);
+    if (kw) m->smp_key = (uint32_t*)dev_alloc((size_t)kw * 4);
     int rc = (m->cos_t && m->sin_t && m->logits && m->plogits && m->pos && m->tok && m->step && m->seen &&
-              m->am_v && m->am_i && m->am_nan && m->out_ids)
+              m->am_v && m->am_i && m->am_nan && m->out_ids && m->draws && (!kw || m->smp_key))
                  ? TL_HIP_OK : TL_HIP_ERR_ALLOC;
     if (rc == TL_HIP_OK) rc = launch_rope_table(m->cos_t, max_seq, m->hd, rope_theta, 0, s);
     if (rc == TL_HIP_OK) rc = launch_rope_table(m->sin_t, max_seq, m->hd, rope_theta, 1, s);
@@ -720,7 +733,7 @@ int tl_hip_llama_free(tl_hip_llama* h) {
     for (void* p : m->vc) dev_free(p);
     void* bufs[] = {m->out_norm, m->emb, m->cos_t, m->sin_t, m->x, m->h, m->qkv, m->q, m->ao, m->t, m->gu,
                     m->act, m->logits, m->plogits, m->ws, m->ids, m->pos, m->tok, m->step, m->out_ids, m->seen,
-                    m->am_v, m->am_i, m->am_nan, m->xa16, m->xb16};
+                    m->am_v, m->am_i, m->am_nan, m->xa16, m->xb16, m->draws, m->smp_key};
     for (void* p : bufs) dev_free(p);
     delete m;
     return TL_HIP_OK;
@@ -1009,6 +1022,60 @@ int32_t tl_hip_llama_sample_greedy(tl_hip_llama* h, double repetition_penalty, c
     return id;
 }
 
+int32_t tl_hip_llama_sample(tl_hip_llama* h, float temp, float top_p, double repetition_penalty,
+                            const int32_t* history, int n_history) {
+    if (!h) {
+        set_error(TL_HIP_ERR_NULL, "NullPointerError: model");
+        return -1;
+    }
+    if (temp <= 0.0f) return tl_hip_llama_sample_greedy(h, repetition_penalty, history, n_history);
+    Llama* m = L_(h);
+    if (repetition_penalty <= 0.0) {
+        set_error(TL_HIP_ERR_ARG, "ArgumentError: repetition penalty must be positive");
+        return -1;
+    }
+    hipStream_t s = cur_stream();
+    const float pen = (float)repetition_penalty;
+    const float* lg = m->logits;
+    if (pen != 1.0f) {
+        std::vector<uint8_t> seen(m->V, 0);
+        for (int i = 0; i < n_history; i++)
+            if (history && history[i] >= 0 && history[i] < m->V) seen[history[i]] = 1;
+        if (hipMemcpyAsync(m->seen, seen.data(), m->V, hipMemcpyHostToDevice, s) != hipSuccess ||
+            launch_rep_penalty(m->logits, m->seen, m->plogits, 1, m->V, pen, s) != TL_HIP_OK) {
+            hip_fail(hipGetLastError(), "repetition penalty");
+            return -1;
+        }
+        lg = m->plogits;
+    }
+    // the chosen index as a float in am_v[0] (a free word between decode steps)
+    if (launch_sample_top_p(lg, m->V, temp, top_p, (float)sample_draw(), m->smp_key, m->am_v, nullptr, s) != TL_HIP_OK)
+        return -1;
+    float id = -1.0f;
+    hipError_t e = hipMemcpyAsync(&id, m->am_v, 4, hipMemcpyDeviceToHost, s);
+    if (e == hipSuccess) e = hipStreamSynchronize(s);
+    if (e != hipSuccess) {
+        hip_fail(e, "sample readback");
+        return -1;
+    }
+    return (int32_t)id;
+}
+
+int tl_hip_llama_set_sampling(tl_hip_llama* h, float temp, float top_p) {
+    if (!h) {
+        set_error(TL_HIP_ERR_NULL, "NullPointerError: model");
+        return TL_HIP_ERR_NULL;
+    }
+    if (temp != temp || top_p != top_p) {
+        set_error(TL_HIP_ERR_ARG, "ArgumentError: sampling temp and top_p must not be NaN");
+        return TL_HIP_ERR_ARG;
+    }
+    Llama* m = L_(h);
+    m->smp_temp = temp > 0.0f ? temp : 0.0f;
+    m->smp_top_p = top_p;
+    return TL_HIP_OK;
+}
+
 int tl_hip_llama_generate(tl_hip_llama* h, int32_t first, int n_steps, int32_t* out_ids,
                           double repetition_penalty, const int32_t* history, int n_history, int use_graph) {
     if (!h || !out_ids) {
@@ -1045,12 +1112,22 @@ int tl_hip_llama_generate(tl_hip_llama* h, int32_t first, int n_steps, int32_t* 
         TLH_CHECK_HIP(hipStreamSynchronize(s));
     }
     int32_t zero = 0;
+    std::vector<float> draws;
+    if (m->smp_temp > 0.0f) {  // one draw per step, in step order (T::from_f64(u): rounded to f32)
+        draws.resize(n_steps);
+        for (float& d : draws) d = (float)sample_draw();
+        TLH_CHECK_HIP(hipMemcpyAsync(m->draws, draws.data(), (size_t)n_steps * 4, hipMemcpyHostToDevice, s));
+    }
     TLH_CHECK_HIP(hipMemcpyAsync(m->tok, &first, 4, hipMemcpyHostToDevice, s));
     TLH_CHECK_HIP(hipMemcpyAsync(m->step, &zero, 4, hipMemcpyHostToDevice, s));
     TLH_CHECK_HIP(hipStreamSynchronize(s));
     if (use_graph) {
-        uint32_t key[3] = {0, (uint32_t)m->kv_f16, (uint32_t)m->rope_per_token};
+        uint32_t key[5] = {0, (uint32_t)m->kv_f16, (uint32_t)m->rope_per_token, 0, 0};
         std::memcpy(&key[0], &pen, 4);
+        if (m->smp_temp > 0.0f) {
+            std::memcpy(&key[3], &m->smp_temp, 4);
+            std::memcpy(&key[4], &m->smp_top_p, 4);
+        }
         if (std::memcmp(key, m->graph_key, sizeof(key)) != 0) {
             free_graph(m);
             std::memcpy(m->graph_key, key, sizeof(key));

@@ -804,9 +804,16 @@ static int run(const MvArgs& a, const MvPlan& p, hipStream_t s) {
     kern<<<(unsigned)p.grid, p.S * p.TC, lds, s>>>(a.qs, w1, a.x, NORM ? a.norm_w : MERGE ? a.attn_rec : nullptr,
                                                   EMBED ? a.embed_id : EPI == EPI_ROPE_KV ? a.pos : nullptr,
                                                   (uint32_t)a.n, (uint32_t)a.nb, sh.pack(), MERGE ? a.attn_hd : 0, a);
-    if constexpr (EPI == EPI_ARGMAX)
-        k_argmax_finish<<<1, 256, 0, s>>>(a.part_v, a.part_i, a.part_nan, a.step, a.pos_inc, a.out_ids,
-                                          (int)p.grid, a);
+    if constexpr (EPI == EPI_ARGMAX) {
+        if (a.smp_temp > 0.0f) {  // top-p sampling of the penalised logits instead of the greedy finish
+            const SmpFin fin{a.smp_draws, a.tok_out, a.out_ids, a.step, a.seen_out, a.pos_inc, a.max_out};
+            const int rc = launch_sample_top_p(a.plogits, a.n, a.smp_temp, a.smp_top_p, 0.0f, a.smp_key, nullptr, &fin, s);
+            if (rc) return rc;
+        } else {
+            k_argmax_finish<<<1, 256, 0, s>>>(a.part_v, a.part_i, a.part_nan, a.step, a.pos_inc, a.out_ids,
+                                              (int)p.grid, a);
+        }
+    }
     hipError_t e = hipGetLastError();
     return e == hipSuccess ? TL_HIP_OK : hip_fail(e, "matvec launch");
 }

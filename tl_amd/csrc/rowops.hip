@@ -1002,10 +1002,8 @@ __device__ __forceinline__ int64_t smp_nth_reg(const uint32_t (&kv)[SMP_RE], uin
 // RES: n <= SMP_T * SMP_RE, every logit and key held in registers (one load pass, no scratch);
 // otherwise the keys go to `key` (n words) and every pass reads them back.
 template <bool RES>
-__global__ __launch_bounds__(SMP_T) void k_sample_top_p(const float* __restrict__ x, int64_t n, float temp,
-                                                        float top_p, float u, uint32_t* __restrict__ key,
-                                                        float* __restrict__ out) {
-    __shared__ SmpShared sh;
+__device__ __forceinline__ int64_t smp_choose(const float* __restrict__ x, int64_t n, float temp, float top_p,
+                                              float u, uint32_t* __restrict__ key, SmpShared& sh) {
     const int tid = threadIdx.x;
     // p = x / temp and its max (the fold `if a > b { a } else { b }`: the max value when no
     // p is NaN)
@@ -1029,10 +1027,7 @@ __global__ __launch_bounds__(SMP_T) void k_sample_top_p(const float* __restrict_
         }
         bad = __syncthreads_or(bad);
         mx = block_max(mx, sh.red);
-        if (bad || !(fabsf(mx) <= 3.402823466e38f)) {
-            if (tid == 0) *out = 0.0f;
-            return;
-        }
+        if (bad || !(fabsf(mx) <= 3.402823466e38f)) return 0;
 #pragma unroll
         for (int e = 0; e < SMP_RE; e++) {
             if ((int64_t)e * SMP_T + tid >= n) continue;
@@ -1053,10 +1048,7 @@ __global__ __launch_bounds__(SMP_T) void k_sample_top_p(const float* __restrict_
         });
         bad = __syncthreads_or(bad);
         mx = block_max(mx, sh.red);
-        if (bad || !(fabsf(mx) <= 3.402823466e38f)) {
-            if (tid == 0) *out = 0.0f;
-            return;
-        }
+        if (bad || !(fabsf(mx) <= 3.402823466e38f)) return 0;
         smp_each(x, n, [&](int64_t, float xv) { se += expf(xv / temp - mx); });
         se = block_sum(se, sh.red);
         smp_each(x, n, [&](int64_t i, float xv) {
@@ -1099,23 +1091,64 @@ __global__ __launch_bounds__(SMP_T) void k_sample_top_p(const float* __restrict_
     SmpCross pick = smp_cross(each, (unsigned long long)ceil((double)r * SMP_SCALE), false, sh);
     if (!pick.found || (cut.found && smp_after(pick, cut)))
         pick = smp_cross(each, 0ull, false, sh);  // order[0]: the largest prob, lowest index
-    int64_t idx;
-    if constexpr (RES) idx = smp_nth_reg(kv, pick.key, pick.mask, pick.rank, sh);
-    else idx = smp_nth(key, n, pick.key, pick.mask, pick.rank, sh);
-    if (tid == 0) *out = (float)idx;
+    if constexpr (RES) return smp_nth_reg(kv, pick.key, pick.mask, pick.rank, sh);
+    else return smp_nth(key, n, pick.key, pick.mask, pick.rank, sh);
 }
 
-static int launch_sample_top_p(const float* x, int64_t n, float temp, float top_p, float u, uint32_t* key,
-                               float* out, hipStream_t s) {
+// FIN: the decode step's form -- u is draws[*step], and the choice is recorded as
+// k_argmax_finish records the greedy one: token, output slot, step counter, penalty mask,
+// position.  Otherwise the index goes to out[0] as a float (the [1] tensor of sample_impl).
+template <bool RES, bool FIN>
+__global__ __launch_bounds__(SMP_T) void k_sample_top_p(const float* __restrict__ x, int64_t n, float temp,
+                                                        float top_p, float u, uint32_t* __restrict__ key,
+                                                        float* __restrict__ out, SmpFin fin) {
+    __shared__ SmpShared sh;
+    int step0 = 0;
+    if constexpr (FIN) {
+        step0 = *fin.step;
+        u = fin.draws[step0 < fin.max_out ? step0 : 0];
+    }
+    const int64_t idx = smp_choose<RES>(x, n, temp, top_p, u, key, sh);
+    if (threadIdx.x == 0) {
+        if constexpr (FIN) {
+            st_wt(fin.tok_out, (int32_t)idx);
+            if (fin.out_ids) {
+                if (step0 < fin.max_out) st_wt(fin.out_ids + step0, (int32_t)idx);
+                st_wt(fin.step, (int32_t)(step0 + 1));
+            }
+            if (fin.seen_out) st_wt(fin.seen_out + idx, (uint8_t)1);
+            if (fin.pos_inc) st_wt(fin.pos_inc, (int32_t)(*fin.pos_inc + 1));
+        } else {
+            *out = (float)idx;
+        }
+    }
+}
+
+int launch_sample_top_p(const float* x, int64_t n, float temp, float top_p, float u, uint32_t* key, float* out,
+                        const SmpFin* fin, hipStream_t s) {
     if (n < 1 || n > INT32_MAX) {
         set_error(TL_HIP_ERR_ARG, "ArgumentError: top-p sampling takes 1 .. 2^31 - 1 logits");
         return TL_HIP_ERR_ARG;
     }
-    if (n <= (int64_t)SMP_T * SMP_RE) k_sample_top_p<true><<<1, SMP_T, 0, s>>>(x, n, temp, top_p, u, nullptr, out);
-    else k_sample_top_p<false><<<1, SMP_T, 0, s>>>(x, n, temp, top_p, u, key, out);
+    const bool res = n <= (int64_t)SMP_T * SMP_RE;
+    if (!res && !key) {
+        set_error(TL_HIP_ERR_ARG, "ArgumentError: top-p sampling over more than %d logits needs a key scratch",
+                  SMP_T * SMP_RE);
+        return TL_HIP_ERR_ARG;
+    }
+    const SmpFin f = fin ? *fin : SmpFin{};
+    if (fin) {
+        if (res) k_sample_top_p<true, true><<<1, SMP_T, 0, s>>>(x, n, temp, top_p, u, nullptr, out, f);
+        else k_sample_top_p<false, true><<<1, SMP_T, 0, s>>>(x, n, temp, top_p, u, key, out, f);
+    } else {
+        if (res) k_sample_top_p<true, false><<<1, SMP_T, 0, s>>>(x, n, temp, top_p, u, nullptr, out, f);
+        else k_sample_top_p<false, false><<<1, SMP_T, 0, s>>>(x, n, temp, top_p, u, key, out, f);
+    }
     hipError_t e = hipGetLastError();
     return e == hipSuccess ? TL_HIP_OK : hip_fail(e, "top-p sampling launch");
 }
+
+int sample_key_words(int64_t n) { return n <= (int64_t)SMP_T * SMP_RE ? 0 : (int)n; }
 
 int launch_embedding(const float* table, const int32_t* ids, float* o, int64_t n, int64_t dim,
                      hipStream_t s) {
@@ -1158,6 +1191,31 @@ int launch_rope_table(float* out, int64_t seq_len, int64_t dim, float base, int 
     k_rope_table<<<cdiv(n, 256), 256, 0, s>>>(out, seq_len, dim, base, is_sin);
     hipError_t e = hipGetLastError();
     return e == hipSuccess ? TL_HIP_OK : hip_fail(e, "rope table launch");
+}
+
+// The uniform draws of tl_hip_tensor_sample: splitmix64 per calling thread (the reference
+// draws from rand's thread-local generator, tensor.rs:1663-1666), seeded from the OS until
+// tl_hip_sample_seed fixes it; a draw is the top 53 bits scaled by 2^-53, in [0, 1), the
+// construction of rand's `gen::<f64>()`.
+static thread_local uint64_t g_smp_state = 0;
+static thread_local bool g_smp_seeded = false;
+
+void sample_seed(uint64_t seed) {
+    g_smp_state = seed;
+    g_smp_seeded = true;
+}
+
+double sample_draw() {
+    if (!g_smp_seeded) {
+        std::random_device rd;
+        g_smp_state = ((uint64_t)rd() << 32) ^ (uint64_t)rd();
+        g_smp_seeded = true;
+    }
+    uint64_t z = (g_smp_state += 0x9E3779B97F4A7C15ull);
+    z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
+    z = (z ^ (z >> 27)) * 0x94D049BB133111EBull;
+    z ^= z >> 31;
+    return (double)(z >> 11) * 0x1.0p-53;
 }
 
 }  // namespace tlhip
@@ -1739,26 +1797,6 @@ int64_t tl_hip_tensor_argmax_all(const tl_hip_tensor* x) {
     return rc == TL_HIP_OK ? (int64_t)h : -1;
 }
 
-// The uniform draws of tl_hip_tensor_sample: splitmix64 per calling thread (the reference
-// draws from rand's thread-local generator, tensor.rs:1663-1666), seeded from the OS until
-// tl_hip_sample_seed fixes it; a draw is the top 53 bits scaled by 2^-53, in [0, 1), the
-// construction of rand's `gen::<f64>()`.
-static thread_local uint64_t g_smp_state = 0;
-static thread_local bool g_smp_seeded = false;
-
-static double smp_uniform() {
-    if (!g_smp_seeded) {
-        std::random_device rd;
-        g_smp_state = ((uint64_t)rd() << 32) ^ (uint64_t)rd();
-        g_smp_seeded = true;
-    }
-    uint64_t z = (g_smp_state += 0x9E3779B97F4A7C15ull);
-    z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
-    z = (z ^ (z >> 27)) * 0x94D049BB133111EBull;
-    z ^= z >> 31;
-    return (double)(z >> 11) * 0x1.0p-53;
-}
-
 static tl_hip_tensor* sample(const tl_hip_tensor* x, float temp, float top_p, const double* u) {
     if (!need(x, "logits")) return nullptr;
     const Tensor* t = CT(x);
@@ -1773,7 +1811,7 @@ static tl_hip_tensor* sample(const tl_hip_tensor* x, float temp, float top_p, co
         float v = (float)idx;
         return tl_hip_tensor_new(&v, &one, 1);
     }
-    const double draw = u ? *u : smp_uniform();
+    const double draw = u ? *u : sample_draw();
     Tensor* o = tensor_alloc(&one, 1);
     if (!o) return nullptr;
     // the key scratch: only for inputs past what the kernel holds in registers
@@ -1783,7 +1821,7 @@ static tl_hip_tensor* sample(const tl_hip_tensor* x, float temp, float top_p, co
         return nullptr;
     }
     // T::from_f64(u): the draw rounded to f32 (tensor.rs:1666)
-    int rc = launch_sample_top_p(t->f32(), t->numel, temp, top_p, (float)draw, key, o->f32(), cur_stream());
+    int rc = launch_sample_top_p(t->f32(), t->numel, temp, top_p, (float)draw, key, o->f32(), nullptr, cur_stream());
     if (key) dev_free(key);
     return finish(o, rc);
 }
@@ -1800,10 +1838,7 @@ tl_hip_tensor* tl_hip_tensor_sample_uniform(const tl_hip_tensor* x, float temp, 
     return sample(x, temp, top_p, &u);
 }
 
-void tl_hip_sample_seed(uint64_t seed) {
-    g_smp_state = seed;
-    g_smp_seeded = true;
-}
+void tl_hip_sample_seed(uint64_t seed) { sample_seed(seed); }
 
 tl_hip_tensor* tl_hip_tensor_repetition_penalty(const tl_hip_tensor* lh, const tl_hip_tensor* th,
                                                 double penalty) {
