@@ -945,16 +945,21 @@ __device__ int64_t smp_nth(const uint32_t* __restrict__ key, int64_t n, uint32_t
     return sh.pick;
 }
 
-// The same for keys in registers, element (e, tid) = index e * SMP_T + tid: index order is row
-// e, then wavefront, then lane.  Per (row, wavefront) counts go to LDS; wavefront 0 scans the
-// SMP_RE * 16 counts (eight per lane) and the chosen wavefront finds its lane in one ballot.
-__device__ __forceinline__ int64_t smp_nth_reg(const uint32_t (&kv)[SMP_RE], uint32_t target, uint32_t km, uint32_t j,
-                               SmpShared& sh) {
+// The same for keys in LDS, element i = e * SMP_T + tid at lk[i] (rows e < re): index order
+// is row e, then wavefront, then lane.  Per (row, wavefront) counts go to LDS; wavefront 0
+// scans the SMP_RE * 16 counts (eight per lane) and the chosen wavefront finds its lane in
+// one ballot.
+__device__ __forceinline__ int64_t smp_nth_lds(const uint32_t* lk, int re, uint32_t target, uint32_t km, uint32_t j,
+                                               SmpShared& sh) {
     constexpr int NW = SMP_T / 64, PER = SMP_RE * NW / 64;
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
-#pragma unroll
+    auto hit = [&](int e) {
+        const uint32_t k = e < re ? lk[e * SMP_T + tid] : 0u;
+        return k != 0u && (k & km) == target;
+    };
+#pragma unroll 4
     for (int e = 0; e < SMP_RE; e++) {
-        const unsigned long long b = __ballot(kv[e] != 0u && (kv[e] & km) == target);
+        const unsigned long long b = __ballot(hit(e));
         if (lane == 0) sh.rc[e * NW + w] = (uint32_t)__popcll(b);
     }
     if (tid == 0) sh.pick = 0;
@@ -986,12 +991,7 @@ __device__ __forceinline__ int64_t smp_nth_reg(const uint32_t (&kv)[SMP_RE], uin
     const uint32_t rw = sh.res.key, need = sh.res.rank;
     const int e_pick = (int)(rw / NW), w_pick = (int)(rw % NW);
     if (w == w_pick) {
-        unsigned long long b = 0;
-#pragma unroll
-        for (int e = 0; e < SMP_RE; e++) {
-            const unsigned long long be = __ballot(kv[e] != 0u && (kv[e] & km) == target);
-            if (e == e_pick) b = be;
-        }
+        const unsigned long long b = __ballot(hit(e_pick));
         const unsigned long long below = lane ? b & ((1ull << lane) - 1ull) : 0ull;
         if (((b >> lane) & 1ull) && (uint32_t)__popcll(below) + 1 == need) sh.pick = (int64_t)e_pick * SMP_T + tid;
     }
@@ -1010,7 +1010,12 @@ __device__ __forceinline__ int64_t smp_choose(const float* __restrict__ x, int64
     float mx = -INFINITY, se = 0.f;
     int bad = 0;
     unsigned long long tot = 0;  // exact sum of every prob
-    uint32_t kv[RES ? SMP_RE : 1];
+    uint32_t bk = 0u;            // the largest key and its lowest index (order[0])
+    int bi = 0x7fffffff;
+    // RES: the keys in dynamic LDS (element i at lk[i]), re rows of SMP_T
+    extern __shared__ uint32_t smp_lds_keys[];
+    uint32_t* const lk = smp_lds_keys;
+    const int re = (int)((n + SMP_T - 1) / SMP_T);
     if constexpr (RES) {
         float pv[SMP_RE];
 #pragma unroll
@@ -1037,8 +1042,13 @@ __device__ __forceinline__ int64_t smp_choose(const float* __restrict__ x, int64
         se = block_sum(se, sh.red);
 #pragma unroll
         for (int e = 0; e < SMP_RE; e++) {
-            kv[e] = (int64_t)e * SMP_T + tid < n ? __float_as_uint(pv[e] / se) : 0u;
-            tot += smp_fx(kv[e]);
+            const uint32_t k = (int64_t)e * SMP_T + tid < n ? __float_as_uint(pv[e] / se) : 0u;
+            if (e < re) lk[e * SMP_T + tid] = k;
+            tot += smp_fx(k);
+            if (k > bk) {  // rows in index order: the first of equal keys stays
+                bk = k;
+                bi = e * SMP_T + tid;
+            }
         }
     } else {
         smp_each(x, n, [&](int64_t, float xv) {
@@ -1055,19 +1065,52 @@ __device__ __forceinline__ int64_t smp_choose(const float* __restrict__ x, int64
             const uint32_t k = __float_as_uint(expf(xv / temp - mx) / se);
             key[i] = k;
             tot += smp_fx(k);
+            if (k > bk) {
+                bk = k;
+                bi = (int)i;
+            }
         });
+    }
+    // order[0]: the largest key, lowest index among equal ones
+    for (int off = 32; off >= 1; off >>= 1) {
+        const uint32_t ok = __shfl_xor(bk, off);
+        const int oi = __shfl_xor(bi, off);
+        if (ok > bk || (ok == bk && oi < bi)) {
+            bk = ok;
+            bi = oi;
+        }
     }
     for (int off = 32; off >= 1; off >>= 1) tot += __shfl_xor(tot, off);
     __syncthreads();  // key[] complete for the workgroup
-    if ((tid & 63) == 0) sh.sum[tid >> 6] = tot;
+    if ((tid & 63) == 0) {
+        sh.sum[tid >> 6] = tot;
+        sh.wtot[tid >> 6] = bk;
+        sh.rc[tid >> 6] = (uint32_t)bi;
+    }
     __syncthreads();
     tot = 0;
-    for (int q = 0; q < SMP_T / 64; q++) tot += sh.sum[q];
+    for (int q = 0; q < SMP_T / 64; q++) {
+        tot += sh.sum[q];
+        const uint32_t ok = sh.wtot[q];
+        const int oi = (int)sh.rc[q];
+        if (ok > bk || (ok == bk && oi < bi)) {
+            bk = ok;
+            bi = oi;
+        }
+    }
     __syncthreads();
+    // cutoff: first running sum > top_p (a NaN top_p compares false: no cutoff; the sum of
+    // all probs is about 1, so no top_p >= 2^16 is exceeded either).  When order[0] alone
+    // exceeds top_p it is the cut, r <= its prob, and it is the choice: no descent.
+    const bool has_cut = top_p == top_p && top_p < 65536.0f;
+    const unsigned long long tcut = top_p < 0.0f ? 0ull : (unsigned long long)floor((double)top_p * SMP_SCALE);
+    if (has_cut && smp_fx(bk) > tcut) return bi;
     auto each = [&](auto f) {
         if constexpr (RES) {
-#pragma unroll
-            for (int e = 0; e < SMP_RE; e++) f(kv[e]);
+            // not unrolled: three descents inline this loop, and unrolled copies of its body
+            // overflowed the instruction cache (108 KB of code, 7.5 us per radix level)
+#pragma unroll 1
+            for (int e = 0; e < re; e++) f(lk[e * SMP_T + tid]);
         } else {
             for (int64_t base = 0; base < n; base += SMP_ROUND) {  // the same trip counts in every lane
                 uint32_t kk[SMP_E];
@@ -1081,17 +1124,13 @@ __device__ __forceinline__ int64_t smp_choose(const float* __restrict__ x, int64
             }
         }
     };
-    // cutoff: first running sum > top_p (a NaN top_p compares false: no cutoff; the sum of
-    // all probs is about 1, so no top_p >= 2^16 is exceeded either)
     SmpCross cut{0u, 0u, 0ull, 0, 0u, 0ull};
-    if (top_p == top_p && top_p < 65536.0f)
-        cut = smp_cross(each, top_p < 0.0f ? 0ull : (unsigned long long)floor((double)top_p * SMP_SCALE), true, sh);
+    if (has_cut) cut = smp_cross(each, tcut, true, sh);
     const float cutoff_prob = (float)((double)(cut.found ? cut.sum : tot) / SMP_SCALE);
     const float r = u * cutoff_prob;
     SmpCross pick = smp_cross(each, (unsigned long long)ceil((double)r * SMP_SCALE), false, sh);
-    if (!pick.found || (cut.found && smp_after(pick, cut)))
-        pick = smp_cross(each, 0ull, false, sh);  // order[0]: the largest prob, lowest index
-    if constexpr (RES) return smp_nth_reg(kv, pick.key, pick.mask, pick.rank, sh);
+    if (!pick.found || (cut.found && smp_after(pick, cut))) return bi;  // no running sum up to the cut reaches r
+    if constexpr (RES) return smp_nth_lds(lk, re, pick.key, pick.mask, pick.rank, sh);
     else return smp_nth(key, n, pick.key, pick.mask, pick.rank, sh);
 }
 
@@ -1137,11 +1176,22 @@ int launch_sample_top_p(const float* x, int64_t n, float temp, float top_p, floa
         return TL_HIP_ERR_ARG;
     }
     const SmpFin f = fin ? *fin : SmpFin{};
+    // the RES form keeps every key in LDS: 128 KB beside the static state (one workgroup per CU)
+    constexpr size_t lds = (size_t)SMP_T * SMP_RE * sizeof(uint32_t);
+    static const hipError_t attr = [] {
+        hipError_t e = hipFuncSetAttribute((const void*)k_sample_top_p<true, true>,
+                                           hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+        if (e == hipSuccess)
+            e = hipFuncSetAttribute((const void*)k_sample_top_p<true, false>,
+                                    hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+        return e;
+    }();
+    if (res && attr != hipSuccess) return hip_fail(attr, "hipFuncSetAttribute(sampling LDS)");
     if (fin) {
-        if (res) k_sample_top_p<true, true><<<1, SMP_T, 0, s>>>(x, n, temp, top_p, u, nullptr, out, f);
+        if (res) k_sample_top_p<true, true><<<1, SMP_T, lds, s>>>(x, n, temp, top_p, u, nullptr, out, f);
         else k_sample_top_p<false, true><<<1, SMP_T, 0, s>>>(x, n, temp, top_p, u, key, out, f);
     } else {
-        if (res) k_sample_top_p<true, false><<<1, SMP_T, 0, s>>>(x, n, temp, top_p, u, nullptr, out, f);
+        if (res) k_sample_top_p<true, false><<<1, SMP_T, lds, s>>>(x, n, temp, top_p, u, nullptr, out, f);
         else k_sample_top_p<false, false><<<1, SMP_T, 0, s>>>(x, n, temp, top_p, u, key, out, f);
     }
     hipError_t e = hipGetLastError();
