@@ -558,16 +558,16 @@ def test_sample_top_p_ties_and_specials(dev):
     NaN / infinite inputs, temp <= 0, [1, V] logits, sizes 1 and 2, errors."""
     n = 32000
     t = dev.tensor_new(np.full(n, 0.5, np.float32))
-    # every prob q = f32(1 / n); the running sum after j elements is j * v, v = q in 2^-48 units
+    # every prob q = f32(1 / n); the running sum after j elements is j * v, v = q in 2^-47 units
     q = np.float32(1.0) / np.float32(n)
-    v = int(float(q) * 2.0 ** 48)
+    v = int(float(q) * 2.0 ** 47)
     for top_p in (0.9, 0.3, 1.0):
         for u in (0.0, 0.25, 0.5, 0.999):
-            tt = int(math.floor(float(np.float32(top_p)) * 2.0 ** 48))
+            tt = int(math.floor(float(np.float32(top_p)) * 2.0 ** 47))
             j_cut = min(tt // v + 1, n)  # n: the sum never exceeds top_p
-            cutoff = np.float32(j_cut * v * 2.0 ** -48)
+            cutoff = np.float32(j_cut * v * 2.0 ** -47)
             r = np.float32(u) * cutoff
-            j = max(1, -(-int(math.ceil(float(r) * 2.0 ** 48)) // v))
+            j = max(1, -(-int(math.ceil(float(r) * 2.0 ** 47)) // v))
             want = j - 1 if j <= j_cut else 0  # past the cut: order[0]
             got = _choice(dev, t, 1.0, top_p, u)
             assert got == want, (top_p, u, got, want)

@@ -710,7 +710,7 @@ int launch_rep_penalty(const float* x, const uint8_t* seen, float* o, int64_t ro
 // holds the place, and a bin holding one element is the place itself (the descent stops
 // there).  After the last digit the prob value v there is known exactly and every larger
 // prob is summed; the place is the j-th element of value v in index order, j the rank at
-// which the sum crosses.  Sums are fixed point (prob * 2^48, integers, independent of
+// which the sum crosses.  Sums are fixed point (prob * 2^47, integers, independent of
 // the order they are added in), so the choice is deterministic; they are the exact sums the
 // reference's f32 running sums round, and the two choices agree wherever T is not within that
 // rounding of a running sum.  Elements of prob 0 never move a running sum across T and are
@@ -718,7 +718,8 @@ int launch_rep_penalty(const float* x, const uint8_t* seen, float* o, int64_t ro
 constexpr int SMP_T = 1024;                      // one workgroup
 constexpr int SMP_E = 16;                        // elements per thread and round, loads issued together
 constexpr int64_t SMP_ROUND = (int64_t)SMP_T * SMP_E;
-constexpr double SMP_SCALE = 281474976710656.0;  // 2^48
+constexpr double SMP_SCALE = 140737488355328.0;  // 2^47: a bin's sum stays below 2^48
+constexpr unsigned long long SMP_LOW48 = (1ull << 48) - 1ull;
 
 __device__ __forceinline__ unsigned long long smp_fx(uint32_t key) {
     return (unsigned long long)((double)__uint_as_float(key) * SMP_SCALE);  // prob <= 1
@@ -766,7 +767,7 @@ __device__ __forceinline__ void smp_each(const float* __restrict__ x, int64_t n,
 }
 
 // Wavefront sum of fixed-point values held as doubles: every partial sum is an integer below
-// 2^53 (all probs add up to about 2^48), so double additions are exact in any order.  Lane
+// 2^53 (all probs add up to about 2^47), so double additions are exact in any order.  Lane
 // exchanges by permlane swaps across rows and DPP row rotations within them, as wave_allsum.
 __device__ __forceinline__ double smp_bits_d(uint32_t lo, uint32_t hi) {
     return __builtin_bit_cast(double, (unsigned long long)hi << 32 | lo);
@@ -796,6 +797,9 @@ __device__ __forceinline__ unsigned long long smp_wave_sum(unsigned long long x)
 // One element into the level's histogram (every lane of the wavefront calls it; `in` says
 // whether this lane's key takes part).  A wavefront whose 16 or more takers share the first
 // taker's bin adds them with one reduction and one atomic pair; the rest add their own.
+// PACK (at most 65535 elements per bin): count and sum share one 64-bit word, the count in
+// bits 48-63 -- one atomic per element instead of two.
+template <bool PACK>
 __device__ __forceinline__ void smp_add(uint32_t k, bool in, uint32_t dig, SmpShared& sh) {
     // (k is opaque here so the compiler does not hoist every key's 64-bit fixed-point value out
     // of the level loop: 32 of them would not fit in the registers beside the keys)
@@ -812,22 +816,30 @@ __device__ __forceinline__ void smp_add(uint32_t k, bool in, uint32_t dig, SmpSh
         if (__popcll(gb) < 16) break;
         const unsigned long long v = smp_wave_sum(grp ? smp_fx(k) : 0ull);
         if (lane == first) {
-            atomicAdd(&sh.cnt[d0], (uint32_t)__popcll(gb));
-            atomicAdd(&sh.sum[d0], v);
+            if constexpr (PACK) {
+                atomicAdd(&sh.sum[d0], (unsigned long long)__popcll(gb) << 48 | v);
+            } else {
+                atomicAdd(&sh.cnt[d0], (uint32_t)__popcll(gb));
+                atomicAdd(&sh.sum[d0], v);
+            }
         }
         own = own && !grp;
         pb &= ~gb;
     }
     if (own) {
-        atomicAdd(&sh.cnt[dig], 1u);
-        atomicAdd(&sh.sum[dig], smp_fx(k));
+        if constexpr (PACK) {
+            atomicAdd(&sh.sum[dig], 1ull << 48 | smp_fx(k));
+        } else {
+            atomicAdd(&sh.cnt[dig], 1u);
+            atomicAdd(&sh.sum[dig], smp_fx(k));
+        }
     }
 }
 
 // First place in the order where the running sum is > t (strict) or >= t.  each(f) calls
 // f(key) for every element with the same trip count in every lane (keys past n are 0).
 // Every thread calls it and gets the result.
-template <typename EachKey>
+template <bool PACK, typename EachKey>
 __device__ __forceinline__ SmpCross smp_cross(EachKey each, unsigned long long t, bool strict, SmpShared& sh) {
     const int tid = threadIdx.x, lane = tid & 63;
     uint32_t prefix = 0, mask = 0;
@@ -839,7 +851,7 @@ __device__ __forceinline__ SmpCross smp_cross(EachKey each, unsigned long long t
             sh.sum[b] = 0;
         }
         __syncthreads();
-        each([&](uint32_t k) { smp_add(k, k != 0u && (k & mask) == prefix, (k >> s) & 255u, sh); });
+        each([&](uint32_t k) { smp_add<PACK>(k, k != 0u && (k & mask) == prefix, (k >> s) & 255u, sh); });
         __syncthreads();
         if (tid < 64) {
             // lane l holds bins 255 - 4 l - q, q = 0..3 (the running sum goes from the top
@@ -848,8 +860,9 @@ __device__ __forceinline__ SmpCross smp_cross(EachKey each, unsigned long long t
             unsigned long long sm[4], loc = 0;
 #pragma unroll
             for (int q = 0; q < 4; q++) {
-                c[q] = sh.cnt[255 - 4 * lane - q];
-                sm[q] = sh.sum[255 - 4 * lane - q];
+                const unsigned long long w = sh.sum[255 - 4 * lane - q];
+                c[q] = PACK ? (uint32_t)(w >> 48) : sh.cnt[255 - 4 * lane - q];
+                sm[q] = PACK ? w & SMP_LOW48 : w;
                 loc += sm[q];
             }
             unsigned long long inc = loc;
@@ -1107,10 +1120,15 @@ __device__ __forceinline__ int64_t smp_choose(const float* __restrict__ x, int64
     if (has_cut && smp_fx(bk) > tcut) return bi;
     auto each = [&](auto f) {
         if constexpr (RES) {
-            // not unrolled: three descents inline this loop, and unrolled copies of its body
-            // overflowed the instruction cache (108 KB of code, 7.5 us per radix level)
-#pragma unroll 1
-            for (int e = 0; e < re; e++) f(lk[e * SMP_T + tid]);
+            // unrolled by four only: the descents inline this loop, and a fully unrolled body
+            // made the kernel 108 KB of code
+            for (int e0 = 0; e0 < re; e0 += 4) {  // four LDS reads in flight, then their four keys
+                uint32_t kk[4];
+#pragma unroll
+                for (int q = 0; q < 4; q++) kk[q] = e0 + q < re ? lk[(e0 + q) * SMP_T + tid] : 0u;
+#pragma unroll
+                for (int q = 0; q < 4; q++) f(kk[q]);
+            }
         } else {
             for (int64_t base = 0; base < n; base += SMP_ROUND) {  // the same trip counts in every lane
                 uint32_t kk[SMP_E];
@@ -1125,10 +1143,10 @@ __device__ __forceinline__ int64_t smp_choose(const float* __restrict__ x, int64
         }
     };
     SmpCross cut{0u, 0u, 0ull, 0, 0u, 0ull};
-    if (has_cut) cut = smp_cross(each, tcut, true, sh);
+    if (has_cut) cut = smp_cross<RES>(each, tcut, true, sh);
     const float cutoff_prob = (float)((double)(cut.found ? cut.sum : tot) / SMP_SCALE);
     const float r = u * cutoff_prob;
-    SmpCross pick = smp_cross(each, (unsigned long long)ceil((double)r * SMP_SCALE), false, sh);
+    SmpCross pick = smp_cross<RES>(each, (unsigned long long)ceil((double)r * SMP_SCALE), false, sh);
     if (!pick.found || (cut.found && smp_after(pick, cut))) return bi;  // no running sum up to the cut reaches r
     if constexpr (RES) return smp_nth_lds(lk, re, pick.key, pick.mask, pick.rank, sh);
     else return smp_nth(key, n, pick.key, pick.mask, pick.rank, sh);
