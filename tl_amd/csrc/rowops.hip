@@ -740,6 +740,8 @@ constexpr int SMP_RE = 32;  // elements per thread kept in registers: n <= SMP_T
 struct SmpShared {
     uint32_t cnt[256];
     unsigned long long sum[256];
+    uint32_t cnt1[256];           // the first level's histogram, the same for every descent
+    unsigned long long sum1[256];
     uint32_t wtot[SMP_T / 64];
     uint32_t rc[SMP_RE * (SMP_T / 64)];  // (row, wavefront) match counts of smp_nth_reg
     SmpCross res;
@@ -839,20 +841,37 @@ __device__ __forceinline__ void smp_add(uint32_t k, bool in, uint32_t dig, SmpSh
 // First place in the order where the running sum is > t (strict) or >= t.  each(f) calls
 // f(key) for every element with the same trip count in every lane (keys past n are 0).
 // Every thread calls it and gets the result.
+// reuse1: the first level's histogram was kept by an earlier descent (cnt1 / sum1) and is not
+// built again; otherwise it is built and kept.
 template <bool PACK, typename EachKey>
-__device__ __forceinline__ SmpCross smp_cross(EachKey each, unsigned long long t, bool strict, SmpShared& sh) {
+__device__ __forceinline__ SmpCross smp_cross(EachKey each, unsigned long long t, bool strict, SmpShared& sh,
+                                              bool reuse1 = false) {
     const int tid = threadIdx.x, lane = tid & 63;
     uint32_t prefix = 0, mask = 0;
     unsigned long long above = 0;
     for (int d = 3; d >= 0; d--) {
         const int s = 8 * d;
-        for (int b = tid; b < 256; b += SMP_T) {
-            sh.cnt[b] = 0;
-            sh.sum[b] = 0;
+        if (d == 3 && reuse1) {
+            for (int b = tid; b < 256; b += SMP_T) {
+                sh.cnt[b] = sh.cnt1[b];
+                sh.sum[b] = sh.sum1[b];
+            }
+            __syncthreads();
+        } else {
+            for (int b = tid; b < 256; b += SMP_T) {
+                sh.cnt[b] = 0;
+                sh.sum[b] = 0;
+            }
+            __syncthreads();
+            each([&](uint32_t k) { smp_add<PACK>(k, k != 0u && (k & mask) == prefix, (k >> s) & 255u, sh); });
+            __syncthreads();
+            if (d == 3) {
+                for (int b = tid; b < 256; b += SMP_T) {  // read here, rewritten only after the next barriers
+                    sh.cnt1[b] = sh.cnt[b];
+                    sh.sum1[b] = sh.sum[b];
+                }
+            }
         }
-        __syncthreads();
-        each([&](uint32_t k) { smp_add<PACK>(k, k != 0u && (k & mask) == prefix, (k >> s) & 255u, sh); });
-        __syncthreads();
         if (tid < 64) {
             // lane l holds bins 255 - 4 l - q, q = 0..3 (the running sum goes from the top
             // bin down): an exclusive scan over the lanes gives each lane its starting sum
@@ -1146,7 +1165,7 @@ __device__ __forceinline__ int64_t smp_choose(const float* __restrict__ x, int64
     if (has_cut) cut = smp_cross<RES>(each, tcut, true, sh);
     const float cutoff_prob = (float)((double)(cut.found ? cut.sum : tot) / SMP_SCALE);
     const float r = u * cutoff_prob;
-    SmpCross pick = smp_cross<RES>(each, (unsigned long long)ceil((double)r * SMP_SCALE), false, sh);
+    SmpCross pick = smp_cross<RES>(each, (unsigned long long)ceil((double)r * SMP_SCALE), false, sh, has_cut);
     if (!pick.found || (cut.found && smp_after(pick, cut))) return bi;  // no running sum up to the cut reaches r
     if constexpr (RES) return smp_nth_lds(lk, re, pick.key, pick.mask, pick.rank, sh);
     else return smp_nth(key, n, pick.key, pick.mask, pick.rank, sh);
