@@ -740,8 +740,11 @@ constexpr int SMP_RE = 32;  // elements per thread kept in registers: n <= SMP_T
 struct SmpShared {
     uint32_t cnt[256];
     unsigned long long sum[256];
-    uint32_t cnt1[256];           // the first level's histogram, the same for every descent
-    unsigned long long sum1[256];
+    // each level's histogram as the cut's descent built it, with the digits above it: the
+    // choice's descent reuses a level whose prefix matches
+    uint32_t cntL[4][256];
+    unsigned long long sumL[4][256];
+    uint32_t pfxL[4];
     uint32_t wtot[SMP_T / 64];
     uint32_t rc[SMP_RE * (SMP_T / 64)];  // (row, wavefront) match counts of smp_nth_reg
     SmpCross res;
@@ -841,20 +844,24 @@ __device__ __forceinline__ void smp_add(uint32_t k, bool in, uint32_t dig, SmpSh
 // First place in the order where the running sum is > t (strict) or >= t.  each(f) calls
 // f(key) for every element with the same trip count in every lane (keys past n are 0).
 // Every thread calls it and gets the result.
-// reuse1: the first level's histogram was kept by an earlier descent (cnt1 / sum1) and is not
-// built again; otherwise it is built and kept.
+// keep: every level built is kept with its prefix (cntL / sumL / pfxL; the levels not reached
+// are marked unused); otherwise a level whose prefix matches a kept one is not built again.
 template <bool PACK, typename EachKey>
 __device__ __forceinline__ SmpCross smp_cross(EachKey each, unsigned long long t, bool strict, SmpShared& sh,
-                                              bool reuse1 = false) {
+                                              bool keep) {
     const int tid = threadIdx.x, lane = tid & 63;
     uint32_t prefix = 0, mask = 0;
     unsigned long long above = 0;
     for (int d = 3; d >= 0; d--) {
         const int s = 8 * d;
-        if (d == 3 && reuse1) {
+        if (keep && d == 3) {
+            if (tid < 4) sh.pfxL[tid] = ~0u;  // levels the descent does not reach stay unused
+            // (prefix ~0u never occurs: keys are below 0x3F800001)
+        }
+        if (!keep && sh.pfxL[d] == prefix) {
             for (int b = tid; b < 256; b += SMP_T) {
-                sh.cnt[b] = sh.cnt1[b];
-                sh.sum[b] = sh.sum1[b];
+                sh.cnt[b] = sh.cntL[d][b];
+                sh.sum[b] = sh.sumL[d][b];
             }
             __syncthreads();
         } else {
@@ -865,11 +872,12 @@ __device__ __forceinline__ SmpCross smp_cross(EachKey each, unsigned long long t
             __syncthreads();
             each([&](uint32_t k) { smp_add<PACK>(k, k != 0u && (k & mask) == prefix, (k >> s) & 255u, sh); });
             __syncthreads();
-            if (d == 3) {
+            if (keep) {
                 for (int b = tid; b < 256; b += SMP_T) {  // read here, rewritten only after the next barriers
-                    sh.cnt1[b] = sh.cnt[b];
-                    sh.sum1[b] = sh.sum[b];
+                    sh.cntL[d][b] = sh.cnt[b];
+                    sh.sumL[d][b] = sh.sum[b];
                 }
+                if (tid == 0) sh.pfxL[d] = prefix;
             }
         }
         if (tid < 64) {
@@ -1162,10 +1170,15 @@ __device__ __forceinline__ int64_t smp_choose(const float* __restrict__ x, int64
         }
     };
     SmpCross cut{0u, 0u, 0ull, 0, 0u, 0ull};
-    if (has_cut) cut = smp_cross<RES>(each, tcut, true, sh);
+    if (has_cut) {
+        cut = smp_cross<RES>(each, tcut, true, sh, true);
+    } else if (tid < 4) {
+        sh.pfxL[tid] = ~0u;  // nothing kept
+    }
     const float cutoff_prob = (float)((double)(cut.found ? cut.sum : tot) / SMP_SCALE);
     const float r = u * cutoff_prob;
-    SmpCross pick = smp_cross<RES>(each, (unsigned long long)ceil((double)r * SMP_SCALE), false, sh, has_cut);
+    __syncthreads();  // pfxL as the cut left it
+    SmpCross pick = smp_cross<RES>(each, (unsigned long long)ceil((double)r * SMP_SCALE), false, sh, false);
     if (!pick.found || (cut.found && smp_after(pick, cut))) return bi;  // no running sum up to the cut reaches r
     if constexpr (RES) return smp_nth_lds(lk, re, pick.key, pick.mask, pick.rank, sh);
     else return smp_nth(key, n, pick.key, pick.mask, pick.rank, sh);
