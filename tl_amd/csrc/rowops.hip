@@ -1111,16 +1111,23 @@ __device__ __forceinline__ int64_t smp_choose(const float* __restrict__ x, int64
             }
         });
     }
-    // order[0]: the largest key, lowest index among equal ones
-    for (int off = 32; off >= 1; off >>= 1) {
-        const uint32_t ok = __shfl_xor(bk, off);
-        const int oi = __shfl_xor(bi, off);
-        if (ok > bk || (ok == bk && oi < bi)) {
-            bk = ok;
-            bi = oi;
-        }
+    // order[0]: the largest key, lowest index among equal ones -- the max of key << 32 | ~index
+    {
+        unsigned long long v = (unsigned long long)bk << 32 | (uint32_t)~(uint32_t)bi;
+        auto vmax = [&](double o) {
+            const unsigned long long w = __builtin_bit_cast(unsigned long long, o);
+            v = w > v ? w : v;
+        };
+        vmax(smp_xor_d<32>(__builtin_bit_cast(double, v)));  // (bit moves only: no float arithmetic)
+        vmax(smp_xor_d<16>(__builtin_bit_cast(double, v)));
+        vmax(smp_dpp_d<0x128>(__builtin_bit_cast(double, v)));
+        vmax(smp_dpp_d<0x124>(__builtin_bit_cast(double, v)));
+        vmax(smp_dpp_d<0x122>(__builtin_bit_cast(double, v)));
+        vmax(smp_dpp_d<0x121>(__builtin_bit_cast(double, v)));
+        bk = (uint32_t)(v >> 32);
+        bi = (int)~(uint32_t)v;
     }
-    for (int off = 32; off >= 1; off >>= 1) tot += __shfl_xor(tot, off);
+    tot = smp_wave_sum(tot);
     __syncthreads();  // key[] complete for the workgroup
     if ((tid & 63) == 0) {
         sh.sum[tid >> 6] = tot;
