@@ -1233,17 +1233,14 @@ int launch_sample_top_p(const float* x, int64_t n, float temp, float top_p, floa
         return TL_HIP_ERR_ARG;
     }
     const SmpFin f = fin ? *fin : SmpFin{};
-    // the RES form keeps every key in LDS: 128 KB beside the static state (one workgroup per CU)
+    // the RES form keeps every key in LDS: 128 KB beside the static state (one workgroup per CU);
+    // the attribute is set at each launch, so it holds on whichever device is current
     constexpr size_t lds = (size_t)SMP_T * SMP_RE * sizeof(uint32_t);
-    static const hipError_t attr = [] {
-        hipError_t e = hipFuncSetAttribute((const void*)k_sample_top_p<true, true>,
-                                           hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
-        if (e == hipSuccess)
-            e = hipFuncSetAttribute((const void*)k_sample_top_p<true, false>,
-                                    hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
-        return e;
-    }();
-    if (res && attr != hipSuccess) return hip_fail(attr, "hipFuncSetAttribute(sampling LDS)");
+    if (res) {
+        const void* kern = fin ? (const void*)k_sample_top_p<true, true> : (const void*)k_sample_top_p<true, false>;
+        const hipError_t attr = hipFuncSetAttribute(kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+        if (attr != hipSuccess) return hip_fail(attr, "hipFuncSetAttribute(sampling LDS)");
+    }
     if (fin) {
         if (res) k_sample_top_p<true, true><<<1, SMP_T, lds, s>>>(x, n, temp, top_p, u, nullptr, out, f);
         else k_sample_top_p<false, true><<<1, SMP_T, 0, s>>>(x, n, temp, top_p, u, key, out, f);
