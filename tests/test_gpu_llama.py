@@ -1,5 +1,6 @@
 """GPU parity of the Llama decoder driver (the chatbot.tl composition) against the CPU oracle:
-logits within the f32 tolerance and identical greedy tokens."""
+logits within the f32 tolerance, identical greedy tokens, and sampled tokens equal to the
+oracle's at the same uniform draws wherever rounding cannot move the choice."""
 import json
 import os
 
@@ -262,9 +263,10 @@ def test_sampled_tokens_f32(small, use_graph, temp, top_p, penalty):
     """The chatbot's decode as it runs (chatbot.tl:188-189: repetition_penalty(1.1), then
     sample(0.1, 0.9) every token, the first from the prompt's logits) with seeded draws: the
     device's tokens against the oracle's sample_impl at the same draws, step by step.  A step
-    may differ only where the f32 logits' rounding could move the choice -- the float64
-    margin of top_p / r from a running sum below 1e-3 -- and the comparison stops there."""
-    from sampling_f64 import sample_f64, splitmix64_uniforms
+    may differ only where rounding could move the choice -- top_p or r within 4e-6 plus four
+    times the f32 drift of a running sum (sampling_f64.decided) -- and the comparison stops
+    there."""
+    from sampling_f64 import decided, sample_f64, splitmix64_uniforms
     gpu, cpu = small
     gpu.configure(kv_f16=False)
     prompt = synthetic_prompt(SMALL, 13, 17)
@@ -273,8 +275,8 @@ def test_sampled_tokens_f32(small, use_graph, temp, top_p, penalty):
     draws = splitmix64_uniforms(seed, n)
     for i, (want, logits) in enumerate(_oracle_sampled(cpu, prompt, n, temp, top_p, penalty, draws)):
         if got[i] != want:
-            margin = sample_f64(logits, temp, top_p, draws[i])[1]
-            assert margin < 1e-3 and i >= 4, (i, int(got[i]), want, margin)
+            _, margin, drift = sample_f64(logits, temp, top_p, draws[i])
+            assert not decided(margin, drift), (i, int(got[i]), want, margin, drift)
             break
     # the same seed replays the same tokens, graph or eager
     again = sampled_generate(gpu, prompt, n, temp, top_p, penalty=penalty, seed=seed, use_graph=not use_graph)
@@ -282,6 +284,34 @@ def test_sampled_tokens_f32(small, use_graph, temp, top_p, penalty):
     if temp >= 0.7:
         other = sampled_generate(gpu, prompt, n, temp, top_p, penalty=penalty, seed=seed + 1, use_graph=use_graph)
         assert list(other) != list(got), "another seed drew the same 24 tokens"
+
+
+@pytest.mark.parametrize("temp,top_p", [(0.7, 0.9), (1.5, 0.95)])
+def test_sampled_tokens_large_vocab(temp, top_p):
+    """A vocabulary past 32768 logits: the decode step's sampling keeps its keys in the
+    model's global scratch instead of LDS.  Tokens against the oracle at the same draws, graph
+    and eager (the same rule on a mismatch as test_sampled_tokens_f32; over 33000 flat
+    probabilities the running sums lie ~3e-5 apart, so such steps occur)."""
+    from sampling_f64 import decided, sample_f64, splitmix64_uniforms
+    cfg = LlamaConfig(1, 128, 2, 1, 256, 33000, max_seq=64)
+    tensors = list(synthetic_weights(cfg, 21))
+    gpu, cpu = HipLlama(cfg), oracle.Llama(cfg)
+    try:
+        gpu.load(tensors)
+        cpu.load(tensors)
+        prompt = synthetic_prompt(cfg, 21, 9)
+        n, seed = 12, 31
+        draws = splitmix64_uniforms(seed, n)
+        runs = [sampled_generate(gpu, prompt, n, temp, top_p, penalty=1.1, seed=seed, use_graph=g) for g in (True, False)]
+        assert list(runs[0]) == list(runs[1])
+        for i, (want, logits) in enumerate(_oracle_sampled(cpu, prompt, n, temp, top_p, 1.1, draws)):
+            if runs[0][i] != want:
+                _, margin, drift = sample_f64(logits, temp, top_p, draws[i])
+                assert not decided(margin, drift), (i, int(runs[0][i]), want, margin, drift)
+                break
+    finally:
+        gpu.close()
+        cpu.close()
 
 
 def test_sampling_settings_reach_the_graph(small):
