@@ -736,15 +736,18 @@ struct SmpCross {
 };
 
 constexpr int SMP_RE = 32;  // elements per thread kept in registers: n <= SMP_T * SMP_RE (vocab sizes)
+// Radix digits of the descents: keys of probs <= 1 are below 2^30 (0x3F800000 at most), three
+// levels of 10 bits, 1024 bins each
+constexpr int SMP_DB = 10, SMP_NB = 1 << SMP_DB, SMP_LEVELS = 3;
 
 struct SmpShared {
-    uint32_t cnt[256];
-    unsigned long long sum[256];
-    // each level's histogram as the cut's descent built it, with the digits above it: the
-    // choice's descent reuses a level whose prefix matches
-    uint32_t cntL[4][256];
-    unsigned long long sumL[4][256];
-    uint32_t pfxL[4];
+    uint32_t cnt[SMP_NB];
+    unsigned long long sum[SMP_NB];
+    // the top level's histogram as the cut's descent built it: the choice's descent has no
+    // digits yet at that level either, so it reuses it (top_kept)
+    uint32_t cnt0[SMP_NB];
+    unsigned long long sum0[SMP_NB];
+    int top_kept;
     uint32_t wtot[SMP_T / 64];
     uint32_t rc[SMP_RE * (SMP_T / 64)];  // (row, wavefront) match counts of smp_nth_reg
     SmpCross res;
@@ -844,68 +847,73 @@ __device__ __forceinline__ void smp_add(uint32_t k, bool in, uint32_t dig, SmpSh
 // First place in the order where the running sum is > t (strict) or >= t.  each(f) calls
 // f(key) for every element with the same trip count in every lane (keys past n are 0).
 // Every thread calls it and gets the result.
-// keep: every level built is kept with its prefix (cntL / sumL / pfxL; the levels not reached
-// are marked unused); otherwise a level whose prefix matches a kept one is not built again.
+// keep: the top level's histogram is kept for a later descent (cnt0 / sum0, top_kept);
+// otherwise a kept top level is reused instead of built again.
 template <bool PACK, typename EachKey>
 __device__ __forceinline__ SmpCross smp_cross(EachKey each, unsigned long long t, bool strict, SmpShared& sh,
                                               bool keep) {
+    constexpr int PERL = SMP_NB / 64;  // bins per lane in the scan
     const int tid = threadIdx.x, lane = tid & 63;
     uint32_t prefix = 0, mask = 0;
     unsigned long long above = 0;
-    for (int d = 3; d >= 0; d--) {
-        const int s = 8 * d;
-        if (keep && d == 3) {
-            if (tid < 4) sh.pfxL[tid] = ~0u;  // levels the descent does not reach stay unused
-            // (prefix ~0u never occurs: keys are below 0x3F800001)
-        }
-        if (!keep && sh.pfxL[d] == prefix) {
-            for (int b = tid; b < 256; b += SMP_T) {
-                sh.cnt[b] = sh.cntL[d][b];
-                sh.sum[b] = sh.sumL[d][b];
+    for (int d = SMP_LEVELS - 1; d >= 0; d--) {
+        const int s = SMP_DB * d;
+        if (d == SMP_LEVELS - 1 && !keep && sh.top_kept) {
+            for (int b = tid; b < SMP_NB; b += SMP_T) {
+                sh.cnt[b] = sh.cnt0[b];
+                sh.sum[b] = sh.sum0[b];
             }
             __syncthreads();
         } else {
-            for (int b = tid; b < 256; b += SMP_T) {
+            for (int b = tid; b < SMP_NB; b += SMP_T) {
                 sh.cnt[b] = 0;
                 sh.sum[b] = 0;
             }
             __syncthreads();
-            each([&](uint32_t k) { smp_add<PACK>(k, k != 0u && (k & mask) == prefix, (k >> s) & 255u, sh); });
+            each([&](uint32_t k) {
+                smp_add<PACK>(k, k != 0u && (k & mask) == prefix, (k >> s) & (uint32_t)(SMP_NB - 1), sh);
+            });
             __syncthreads();
-            if (keep) {
-                for (int b = tid; b < 256; b += SMP_T) {  // read here, rewritten only after the next barriers
-                    sh.cntL[d][b] = sh.cnt[b];
-                    sh.sumL[d][b] = sh.sum[b];
+            if (keep && d == SMP_LEVELS - 1) {
+                for (int b = tid; b < SMP_NB; b += SMP_T) {  // read here, rewritten only after the next barriers
+                    sh.cnt0[b] = sh.cnt[b];
+                    sh.sum0[b] = sh.sum[b];
                 }
-                if (tid == 0) sh.pfxL[d] = prefix;
+                if (tid == 0) sh.top_kept = 1;
             }
         }
         if (tid < 64) {
-            // lane l holds bins 255 - 4 l - q, q = 0..3 (the running sum goes from the top
+            // lane l holds bins NB - 1 - PERL l - q, q < PERL (the running sum goes from the top
             // bin down): an exclusive scan over the lanes gives each lane its starting sum
-            uint32_t c[4];
-            unsigned long long sm[4], loc = 0;
-#pragma unroll
-            for (int q = 0; q < 4; q++) {
-                const unsigned long long w = sh.sum[255 - 4 * lane - q];
-                c[q] = PACK ? (uint32_t)(w >> 48) : sh.cnt[255 - 4 * lane - q];
-                sm[q] = PACK ? w & SMP_LOW48 : w;
-                loc += sm[q];
+            // (the bins are read twice, for the lane's total and then for the crossing, rather
+            // than held in registers beside the 32 keys of the descents)
+            unsigned long long loc = 0;
+#pragma unroll 4
+            for (int q = 0; q < PERL; q++) {
+                const unsigned long long w = sh.sum[SMP_NB - 1 - PERL * lane - q];
+                loc += PACK ? w & SMP_LOW48 : w;
             }
             unsigned long long inc = loc;
             for (int off = 1; off < 64; off <<= 1) {
                 const unsigned long long y = __shfl_up(inc, off);
                 if (lane >= off) inc += y;
             }
-            unsigned long long run = above + inc - loc, hit_run = 0;
+            unsigned long long run = above + inc - loc, hit_run = 0, hit_sum = 0;
+            uint32_t hit_cnt = 0;
             int hit = -1;
-#pragma unroll
-            for (int q = 0; q < 4; q++) {
-                if (!c[q]) continue;
-                const unsigned long long nx = run + sm[q];
+#pragma unroll 4
+            for (int q = 0; q < PERL; q++) {
+                const int b = SMP_NB - 1 - PERL * lane - q;
+                const unsigned long long w = sh.sum[b];
+                const uint32_t c = PACK ? (uint32_t)(w >> 48) : sh.cnt[b];
+                const unsigned long long sm = PACK ? w & SMP_LOW48 : w;
+                if (!c) continue;
+                const unsigned long long nx = run + sm;
                 if (hit < 0 && (strict ? nx > t : nx >= t)) {
                     hit = q;
                     hit_run = run;
+                    hit_cnt = c;
+                    hit_sum = sm;
                 }
                 run = nx;
             }
@@ -913,7 +921,7 @@ __device__ __forceinline__ SmpCross smp_cross(EachKey each, unsigned long long t
             if (hb == 0) {
                 if (lane == 0) sh.res = SmpCross{0u, 0u, 0ull, 0, 0u, 0ull};
             } else if (lane == __ffsll(hb) - 1) {
-                sh.res = SmpCross{(uint32_t)(255 - 4 * lane - hit), c[hit], hit_run, 1, 0u, sm[hit]};
+                sh.res = SmpCross{(uint32_t)(SMP_NB - 1 - PERL * lane - hit), hit_cnt, hit_run, 1, 0u, hit_sum};
             }
         }
         __syncthreads();
@@ -921,7 +929,7 @@ __device__ __forceinline__ SmpCross smp_cross(EachKey each, unsigned long long t
         __syncthreads();  // sh is rewritten by the next level
         if (!r.found) return r;
         prefix |= r.key << s;
-        mask |= 255u << s;
+        mask = d == 0 ? ~0u : mask | (uint32_t)(SMP_NB - 1) << s;  // all bits known after the last digit
         above = r.sum;
         if (r.rank == 1)  // the bin holds one element: it is the place
             return SmpCross{prefix, 1u, above + r.bin, 1, mask, r.bin};
@@ -1177,14 +1185,12 @@ __device__ __forceinline__ int64_t smp_choose(const float* __restrict__ x, int64
         }
     };
     SmpCross cut{0u, 0u, 0ull, 0, 0u, 0ull};
-    if (has_cut) {
-        cut = smp_cross<RES>(each, tcut, true, sh, true);
-    } else if (tid < 4) {
-        sh.pfxL[tid] = ~0u;  // nothing kept
-    }
+    if (tid == 0) sh.top_kept = 0;
+    __syncthreads();
+    if (has_cut) cut = smp_cross<RES>(each, tcut, true, sh, true);
     const float cutoff_prob = (float)((double)(cut.found ? cut.sum : tot) / SMP_SCALE);
     const float r = u * cutoff_prob;
-    __syncthreads();  // pfxL as the cut left it
+    __syncthreads();  // top_kept as the cut left it
     SmpCross pick = smp_cross<RES>(each, (unsigned long long)ceil((double)r * SMP_SCALE), false, sh, false);
     if (!pick.found || (cut.found && smp_after(pick, cut))) return bi;  // no running sum up to the cut reaches r
     if constexpr (RES) return smp_nth_lds(lk, re, pick.key, pick.mask, pick.rank, sh);
