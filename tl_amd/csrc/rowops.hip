@@ -705,7 +705,7 @@ int launch_rep_penalty(const float* x, const uint8_t* seen, float* o, int64_t ro
 // nothing compares, the order stays the index order and index 0 is chosen.
 // The order is never built.  "The first place where the running sum crosses T" is found by
 // a radix descent over the prob bits (non-negative floats order as their bit patterns):
-// four 8-bit digits from the top, each a histogram of (count, sum) over the elements that
+// three 10-bit digits from the top, each a histogram of (count, sum) over the elements that
 // share the digits found so far; the bin where everything above it plus the bin crosses T
 // holds the place, and a bin holding one element is the place itself (the descent stops
 // there).  After the last digit the prob value v there is known exactly and every larger
