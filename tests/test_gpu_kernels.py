@@ -595,6 +595,9 @@ def test_sample_top_p_ties_and_specials(dev):
     two = dev.tensor_new(np.array([0.0, ln3], np.float32))
     assert [_choice(dev, two, 1.0, 0.9, u) for u in (0.0, 0.5, 0.8)] == [1, 1, 0]
     assert _choice(dev, two, 1.0, 0.5, 0.99) == 1
+    for tp in (float("nan"), 1e6):  # never exceeded: no cut (the kernel skips the cut's descent)
+        assert [_choice(dev, two, 1.0, tp, u) for u in (0.0, 0.5, 0.8)] == [1, 1, 0]
+        assert _choice(dev, t, 1.0, tp, 0.999) == oracle.sample(np.full(n, 0.5, np.float32), 1.0, tp, 0.999)
     with pytest.raises(BackendError) as e:
         dev.tensor_sample_uniform(dev.tensor_new(np.zeros(0, np.float32)), 1.0, 0.9, 0.5)
     assert e.value.variant == "InternalError"

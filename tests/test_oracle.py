@@ -226,6 +226,9 @@ def test_sample_top_p_closed_forms():
     assert oracle.sample([1.0, 1.0, 1.0, 1.0], 1.0, 0.6, 0.0) == 0
     assert oracle.sample([1.0, 1.0, 1.0, 1.0], 1.0, 1.5, 0.99) == 3   # never exceeds: all four
     assert oracle.sample([1.0, 1.0, 1.0, 1.0], 1.0, -1.0, 0.99) == 0  # cut after the first
+    # a NaN top_p is never exceeded (cum_prob > NaN is false): no cut, as with top_p 1e6
+    for tp in (float("nan"), 1e6):
+        assert [oracle.sample([0.0, ln3], 1.0, tp, u) for u in (0.0, 0.5, 0.8)] == [1, 1, 0]
     # the top-probability element first, then ties in index order: [3, 1, 1, 3] -> 0, 3, 1, 2
     assert oracle.sample([3.0, 1.0, 1.0, 3.0], 1.0, 1.5, 0.6) == 3
     # a NaN or infinite logit, or a NaN temp, makes every prob NaN: index 0
